@@ -1,0 +1,411 @@
+// Device-resident Qwen3 decoder (decoder.rs): int8 weights packed on the GPU
+// at load, an HBM-resident KV cache, and a decode step of 5 fused kernels per
+// layer plus the LM-head argmax, replayed from a captured HIP graph.
+#include "decoder.h"
+
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+using namespace qasr;
+
+template <typename T>
+static int dalloc(qasr_decoder *d, T **p, size_t count) {
+    void *v = nullptr;
+    hipError_t e = hipMalloc(&v, count * sizeof(T) + 256);
+    if (e != hipSuccess)
+        return qasr_fail(QASR_ERR_NOMEM, std::string("decoder: hipMalloc of ") +
+                                             std::to_string(count * sizeof(T)) + " bytes failed");
+    d->allocs.push_back(v);
+    *p = reinterpret_cast<T *>(v);
+    return QASR_OK;
+}
+
+#define TRY(x)                  \
+    do {                        \
+        int rc_ = (x);          \
+        if (rc_ != QASR_OK) {   \
+            return rc_;         \
+        }                       \
+    } while (0)
+
+static int upload(qasr_decoder *d, void *dst, const void *src, size_t bytes) {
+    HIPCHK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, d->h->stream));
+    return QASR_OK;
+}
+
+// upload bf16 [n, k] and pack it to int8 + scales on the device
+static int upload_pack(qasr_decoder *d, const uint16_t *host, int64_t n, int64_t k, uint16_t **bf,
+                       int8_t **q, float **s, bool keep_bf16) {
+    uint16_t *tmp = nullptr;
+    if (keep_bf16) {
+        TRY(dalloc(d, bf, n * k));
+        tmp = *bf;
+    } else {
+        tmp = d->stage;
+    }
+    TRY(upload(d, tmp, host, sizeof(uint16_t) * n * k));
+    TRY(dalloc(d, q, n * k));
+    TRY(dalloc(d, s, n));
+    LAUNCHCHK(launch_pack_int8(tmp, n, (int)k, d->round_mode, *q, *s, d->h->stream), "decoder pack");
+    if (!keep_bf16) HIPCHK(hipStreamSynchronize(d->h->stream));   // the stage buffer is reused
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
+                                     int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
+    CHECK_H(h);
+    if (!cfg || !w || !out || !w->embed || !w->norm || !w->layers)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_load: null argument");
+    *out = nullptr;
+    const qasr_dec_config c = *cfg;
+    if (c.n_layers <= 0 || c.head_dim != 128 || c.n_kv_heads <= 0 || c.n_heads != 2 * c.n_kv_heads ||
+        c.hidden <= 0 || c.hidden % 64 != 0 || c.hidden > 4096 || c.intermediate <= 0 ||
+        (c.intermediate % 64) != 0 || c.intermediate > 6144 || c.vocab <= 0 ||
+        (int64_t)c.n_heads * c.head_dim > 6144 || max_seq <= 0 || max_seq > (1 << 20))
+        return qasr_fail(QASR_ERR_INVALID,
+                         "decoder_load: unsupported config (head_dim 128, n_heads == 2 * n_kv_heads, "
+                         "hidden/intermediate multiples of 64)");
+    if (round_mode != QASR_ROUND_HALF_AWAY && round_mode != QASR_TRUNC)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_load: unknown round_mode");
+    for (int l = 0; l < c.n_layers; l++) {
+        const qasr_dec_layer &L = w->layers[l];
+        if (!L.wq || !L.wk || !L.wv || !L.wo || !L.gate || !L.up || !L.down || !L.q_norm || !L.k_norm ||
+            !L.input_norm || !L.post_attn_norm)
+            return qasr_fail(QASR_ERR_INVALID, "decoder_load: null weight in layer " + std::to_string(l));
+    }
+    qasr_decoder *d = new qasr_decoder();
+    d->h = h;
+    d->c = c;
+    d->round_mode = round_mode;
+    d->kv_bf16 = kv_bf16 ? 1 : 0;
+    d->max_seq = max_seq;
+    d->n_split = attn_splits_for(max_seq);
+    int rc = decoder_build(d, w);
+    if (rc != QASR_OK) {
+        qasr_hip_decoder_free(d);
+        return rc;
+    }
+    *out = d;
+    return QASR_OK;
+}
+
+int decoder_build(qasr_decoder *d, const qasr_dec_weights *w) {
+    const qasr_dec_config &c = d->c;
+    const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd;
+    const int64_t kvd = (int64_t)c.n_kv_heads * hd, I = c.intermediate, V = c.vocab;
+    const int64_t nqkv = qd + 2 * kvd;
+    size_t stage = std::max<size_t>({(size_t)nqkv * H, (size_t)2 * I * H, (size_t)H * qd, (size_t)H * I});
+    TRY(dalloc(d, &d->stage, stage));
+    std::vector<uint16_t> host((size_t)std::max<int64_t>(nqkv * H, 2 * I * H));
+    d->L.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        const qasr_dec_layer &S = w->layers[l];
+        DecLayerDev &D = d->L[l];
+        // q | k | v concatenated by rows (one fused projection)
+        std::memcpy(host.data(), S.wq, sizeof(uint16_t) * qd * H);
+        std::memcpy(host.data() + qd * H, S.wk, sizeof(uint16_t) * kvd * H);
+        std::memcpy(host.data() + (qd + kvd) * H, S.wv, sizeof(uint16_t) * kvd * H);
+        TRY(upload_pack(d, host.data(), nqkv, H, &D.bqkv, &D.wqkv, &D.sqkv, true));
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        TRY(upload_pack(d, S.wo, H, qd, &D.bo, &D.wo, &D.so, true));
+        // gate/up interleaved by rows (decoder.rs:91-104)
+        for (int64_t r = 0; r < I; r++) {
+            std::memcpy(host.data() + 2 * r * H, S.gate + r * H, sizeof(uint16_t) * H);
+            std::memcpy(host.data() + (2 * r + 1) * H, S.up + r * H, sizeof(uint16_t) * H);
+        }
+        TRY(upload_pack(d, host.data(), 2 * I, H, &D.bgu, &D.wgu, &D.sgu, true));
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        TRY(upload_pack(d, S.down, H, I, &D.bdown, &D.wdown, &D.sdown, true));
+        TRY(dalloc(d, &D.q_norm, hd));
+        TRY(dalloc(d, &D.k_norm, hd));
+        TRY(dalloc(d, &D.in_norm, H));
+        TRY(dalloc(d, &D.post_norm, H));
+        TRY(upload(d, D.q_norm, S.q_norm, sizeof(float) * hd));
+        TRY(upload(d, D.k_norm, S.k_norm, sizeof(float) * hd));
+        TRY(upload(d, D.in_norm, S.input_norm, sizeof(float) * H));
+        TRY(upload(d, D.post_norm, S.post_attn_norm, sizeof(float) * H));
+    }
+    // embedding table (bf16, kept for lookups) and the int8 LM head packed from it
+    TRY(dalloc(d, &d->embed, V * H));
+    TRY(upload(d, d->embed, w->embed, sizeof(uint16_t) * V * H));
+    TRY(dalloc(d, &d->lm, V * H));
+    TRY(dalloc(d, &d->lm_s, V));
+    LAUNCHCHK(launch_pack_int8(d->embed, V, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream), "lm pack");
+    TRY(dalloc(d, &d->norm, H));
+    TRY(upload(d, d->norm, w->norm, sizeof(float) * H));
+    // KV cache [layer][kv_head][max_seq][hd]
+    const size_t kv_elems = (size_t)c.n_layers * c.n_kv_heads * d->max_seq * hd;
+    const size_t esz = d->kv_bf16 ? 2 : 4;
+    {
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, kv_elems * esz);
+        if (e != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "decoder: KV cache allocation failed");
+        d->allocs.push_back(p);
+        d->kc = p;
+        e = hipMalloc(&p, kv_elems * esz);
+        if (e != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "decoder: KV cache allocation failed");
+        d->allocs.push_back(p);
+        d->vc = p;
+        HIPCHK(hipMemsetAsync(d->kc, 0, kv_elems * esz, d->h->stream));
+        HIPCHK(hipMemsetAsync(d->vc, 0, kv_elems * esz, d->h->stream));
+    }
+    // RoPE table (RopeCache::ensure, decoder.rs:301-338) with the host libm
+    {
+        std::vector<float> cs((size_t)d->max_seq * hd), sn((size_t)d->max_seq * hd), inv(hd / 2);
+        for (int64_t i = 0; i < hd / 2; i++) inv[i] = 1.0f / powf(c.theta, (float)(2 * i) / (float)hd);
+        for (int64_t p = 0; p < d->max_seq; p++)
+            for (int64_t i = 0; i < hd / 2; i++) {
+                const float a = (float)p * inv[i];
+                const float cv = cosf(a), sv = sinf(a);
+                cs[p * hd + i] = cv; cs[p * hd + hd / 2 + i] = cv;
+                sn[p * hd + i] = sv; sn[p * hd + hd / 2 + i] = sv;
+            }
+        TRY(dalloc(d, &d->rc, cs.size()));
+        TRY(dalloc(d, &d->rs, sn.size()));
+        TRY(upload(d, d->rc, cs.data(), sizeof(float) * cs.size()));
+        TRY(upload(d, d->rs, sn.data(), sizeof(float) * sn.size()));
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+    }
+    TRY(dalloc(d, &d->x, H));
+    TRY(dalloc(d, &d->qkv, nqkv));
+    TRY(dalloc(d, &d->att, qd));
+    TRY(dalloc(d, &d->ffn, I));
+    TRY(dalloc(d, &d->state, 4));
+    TRY(dalloc(d, &d->token_log, d->max_seq));
+    TRY(dalloc(d, &d->out_idx, 4));
+    TRY(dalloc(d, &d->counters, QASR_COUNTERS));
+    HIPCHK(hipMemsetAsync(d->counters, 0, QASR_COUNTERS * sizeof(unsigned), d->h->stream));
+    TRY(dalloc(d, &d->am_val, QASR_ARGMAX_MAX_BLOCKS));
+    TRY(dalloc(d, &d->am_idx, QASR_ARGMAX_MAX_BLOCKS));
+    const int max_split = attn_splits_for(d->max_seq) > 64 ? attn_splits_for(d->max_seq) : 64;
+    TRY(dalloc(d, &d->part, (size_t)c.n_kv_heads * max_split * 2 * (hd + 2)));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    return QASR_OK;
+}
+
+extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
+    if (!d) return;
+    (void)hipSetDevice(d->h->device);
+    (void)hipStreamSynchronize(d->h->stream);
+    if (d->graph_exec) (void)hipGraphExecDestroy(d->graph_exec);
+    decoder_free_prefill(d);
+    for (void *p : d->allocs) (void)hipFree(p);
+    delete d;
+}
+
+// ---------------------------------------------------------------------------
+// one decode step: per layer [norm+qkv] [qk-norm+rope+kv-write+attention]
+// [o-proj += ] [norm+gate_up+swiglu] [down += ], then [norm+LM-head argmax]
+// ---------------------------------------------------------------------------
+int decoder_enqueue_step(qasr_decoder *d, bool embed_mode) {
+    const qasr_dec_config &c = d->c;
+    const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    const int I = c.intermediate;
+    hipStream_t st = d->h->stream;
+    const size_t esz = d->kv_bf16 ? 2 : 4;
+    const int64_t layer_elems = (int64_t)c.n_kv_heads * d->max_seq * hd;
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int l = 0; l < c.n_layers; l++) {
+        const DecLayerDev &L = d->L[l];
+        MvArgs a{};
+        a.x = d->x; a.embed = d->embed; a.state = d->state; a.norm_w = L.in_norm; a.eps = c.eps; a.K = H;
+        a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
+        a.n_total = qd + 2 * kvd;
+        a.resid_out = d->x;
+        LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, 4, st), "step qkv");
+
+        AttnDecodeArgs t{};
+        t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
+        t.rope_cos = d->rc; t.rope_sin = d->rs; t.state = d->state;
+        t.kcache = (char *)d->kc + (size_t)l * layer_elems * esz;
+        t.vcache = (char *)d->vc + (size_t)l * layer_elems * esz;
+        t.head_stride = (int64_t)d->max_seq * hd;
+        t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
+        t.n_split = d->n_split; t.eps = c.eps; t.scale = scale;
+        LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st), "step attention");
+
+        MvArgs o{};
+        o.x = d->att; o.K = qd;
+        o.seg[0] = {L.wo, L.so, d->x, H};
+        o.n_total = H;
+        LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+
+        MvArgs g{};
+        g.x = d->x; g.norm_w = L.post_norm; g.eps = c.eps; g.K = H;
+        g.seg[0] = {L.wgu, L.sgu, d->ffn, 2 * I};
+        g.n_total = 2 * I;
+        LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, 4, st), "step gate_up");
+
+        MvArgs dn{};
+        dn.x = d->ffn; dn.K = I;
+        dn.seg[0] = {L.wdown, L.sdown, d->x, H};
+        dn.n_total = H;
+        LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, 1, st), "step down");
+    }
+    ArgmaxArgs am{};
+    am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = c.vocab;
+    am.w = d->lm; am.ws = d->lm_s;
+    am.part_val = d->am_val; am.part_idx = d->am_idx; am.counter = d->counters + QASR_CTR_ARGMAX;
+    am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
+    LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st), "step argmax");
+    return QASR_OK;
+}
+
+static int set_state(qasr_decoder *d, int32_t token) {
+    d->host_state[0] = token;
+    d->host_state[1] = (int32_t)d->len;
+    d->host_state[2] = 0;
+    d->host_state[3] = 0;
+    HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, d->h->stream));
+    return QASR_OK;
+}
+
+static int run_embed_step(qasr_decoder *d) {
+    if (!d->use_graph) return decoder_enqueue_step(d, true);
+    if (!d->graph_exec) {
+        hipGraph_t g = nullptr;
+        HIPCHK(hipStreamBeginCapture(d->h->stream, hipStreamCaptureModeThreadLocal));
+        int rc = decoder_enqueue_step(d, true);
+        hipError_t e = hipStreamEndCapture(d->h->stream, &g);
+        if (rc != QASR_OK) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        HIPCHK(e);
+        e = hipGraphInstantiate(&d->graph_exec, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        HIPCHK(e);
+    }
+    HIPCHK(hipGraphLaunch(d->graph_exec, d->h->stream));
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int32_t token_in,
+                                        int32_t *token_out) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (!token_out) return qasr_fail(QASR_ERR_INVALID, "token_out is null");
+    if (d->len + 1 > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_forward: KV cache capacity exceeded");
+    if (!embed && (token_in < 0 || token_in >= d->c.vocab))
+        return qasr_fail(QASR_ERR_INVALID, "decoder_forward: token id out of range");
+    TRY(set_state(d, token_in));
+    if (embed) {
+        HIPCHK(hipMemcpyAsync(d->x, embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice, d->h->stream));
+        TRY(decoder_enqueue_step(d, false));
+    } else {
+        TRY(run_embed_step(d));
+    }
+    HIPCHK(hipMemcpyAsync(d->host_state, d->state, sizeof(d->host_state), hipMemcpyDeviceToHost, d->h->stream));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    *token_out = d->host_state[0];
+    d->len += 1;
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_embed, int32_t first_token,
+                                         int32_t n_steps, int32_t *tokens_out) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (n_steps <= 0 || !tokens_out) return qasr_fail(QASR_ERR_INVALID, "decoder_generate: bad arguments");
+    if (d->len + n_steps > d->max_seq)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_generate: KV cache capacity exceeded");
+    if (!first_embed && (first_token < 0 || first_token >= d->c.vocab))
+        return qasr_fail(QASR_ERR_INVALID, "decoder_generate: token id out of range");
+    TRY(set_state(d, first_token));
+    if (first_embed) {
+        HIPCHK(hipMemcpyAsync(d->x, first_embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice,
+                              d->h->stream));
+        TRY(decoder_enqueue_step(d, false));
+    } else {
+        TRY(run_embed_step(d));
+    }
+    for (int32_t s = 1; s < n_steps; s++) TRY(run_embed_step(d));
+    HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost,
+                          d->h->stream));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    d->len += n_steps;
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_set_len(qasr_decoder *d, int64_t len) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    if (len < 0 || len > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_set_len: out of range");
+    d->len = len;
+    return QASR_OK;
+}
+
+extern "C" int64_t qasr_hip_decoder_len(const qasr_decoder *d) { return d ? d->len : -1; }
+
+extern "C" int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (attn_splits > 0) {
+        if (attn_splits < attn_splits_for(d->max_seq) || attn_splits > 64)
+            return qasr_fail(QASR_ERR_INVALID, "decoder_set_options: attn_splits must cover max_seq with "
+                                               "<= 256 positions per split and be <= 64");
+        d->n_split = attn_splits;
+    }
+    d->use_graph = use_graph ? 1 : 0;
+    if (d->graph_exec) {
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        HIPCHK(hipGraphExecDestroy(d->graph_exec));
+        d->graph_exec = nullptr;
+    }
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, int8_t *q_host,
+                                       float *scales_host) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    const qasr_dec_config &c = d->c;
+    const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd;
+    const int64_t kvd = (int64_t)c.n_kv_heads * hd, I = c.intermediate;
+    const int8_t *q = nullptr;
+    const float *s = nullptr;
+    int64_t rows = 0, cols = H;
+    if (layer == -1) {
+        q = d->lm; s = d->lm_s; rows = c.vocab;
+    } else if (layer >= 0 && layer < c.n_layers && which >= 0 && which <= 5) {
+        const DecLayerDev &L = d->L[layer];
+        switch (which) {
+            case 0: q = L.wqkv; s = L.sqkv; rows = qd; break;
+            case 1: q = L.wqkv + qd * H; s = L.sqkv + qd; rows = kvd; break;
+            case 2: q = L.wqkv + (qd + kvd) * H; s = L.sqkv + qd + kvd; rows = kvd; break;
+            case 3: q = L.wo; s = L.so; rows = H; cols = qd; break;
+            case 4: q = L.wgu; s = L.sgu; rows = 2 * I; break;
+            default: q = L.wdown; s = L.sdown; rows = H; cols = I; break;
+        }
+    } else {
+        return qasr_fail(QASR_ERR_INVALID, "decoder_packed: bad layer / which");
+    }
+    if (q_host) HIPCHK(hipMemcpyAsync(q_host, q, rows * cols, hipMemcpyDeviceToHost, d->h->stream));
+    if (scales_host) HIPCHK(hipMemcpyAsync(scales_host, s, sizeof(float) * rows, hipMemcpyDeviceToHost, d->h->stream));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    return QASR_OK;
+}
+
+static int kv_copy(qasr_decoder *d, float *kh, float *vh, bool up) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (d->kv_bf16) return qasr_fail(QASR_ERR_INVALID, "kv copy: only for f32 caches");
+    const size_t n = (size_t)d->c.n_layers * d->c.n_kv_heads * d->max_seq * d->c.head_dim;
+    if (up) {
+        if (kh) HIPCHK(hipMemcpyAsync(d->kc, kh, n * 4, hipMemcpyHostToDevice, d->h->stream));
+        if (vh) HIPCHK(hipMemcpyAsync(d->vc, vh, n * 4, hipMemcpyHostToDevice, d->h->stream));
+    } else {
+        if (kh) HIPCHK(hipMemcpyAsync(kh, d->kc, n * 4, hipMemcpyDeviceToHost, d->h->stream));
+        if (vh) HIPCHK(hipMemcpyAsync(vh, d->vc, n * 4, hipMemcpyDeviceToHost, d->h->stream));
+    }
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_kv_upload(qasr_decoder *d, const float *k, const float *v) {
+    return kv_copy(d, const_cast<float *>(k), const_cast<float *>(v), true);
+}
+
+extern "C" int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k, float *v) {
+    return kv_copy(d, k, v, false);
+}

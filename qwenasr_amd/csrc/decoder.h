@@ -1,0 +1,46 @@
+// Internal layout of the device-resident decoder.
+#pragma once
+#include <vector>
+#include "kernels.h"
+#include "model.h"
+
+struct DecLayerDev {
+    // int8 packed (decode) and bf16 (prefill) weights, row-major [out, in]
+    int8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdown = nullptr;
+    float *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sdown = nullptr;
+    uint16_t *bqkv = nullptr, *bo = nullptr, *bgu = nullptr, *bdown = nullptr;
+    float *q_norm = nullptr, *k_norm = nullptr, *in_norm = nullptr, *post_norm = nullptr;
+};
+
+struct PrefillBufs {
+    int64_t cap = 0;
+    float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *g = nullptr;
+};
+
+struct qasr_decoder {
+    qasr_hip *h = nullptr;
+    qasr_dec_config c{};
+    int round_mode = 0, kv_bf16 = 0;
+    int64_t max_seq = 0, len = 0;
+    std::vector<DecLayerDev> L;
+    uint16_t *embed = nullptr, *stage = nullptr;
+    int8_t *lm = nullptr;
+    float *lm_s = nullptr, *norm = nullptr;
+    void *kc = nullptr, *vc = nullptr;          // [layer][kv_head][max_seq][hd]
+    float *rc = nullptr, *rs = nullptr;         // RoPE [max_seq][hd]
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr;
+    int32_t *state = nullptr;                   // {token, pos, step, flag}
+    int32_t *token_log = nullptr, *out_idx = nullptr;
+    unsigned *counters = nullptr;
+    float *am_val = nullptr, *part = nullptr;
+    int32_t *am_idx = nullptr;
+    int n_split = 16, use_graph = 1;
+    hipGraphExec_t graph_exec = nullptr;
+    int32_t host_state[4] = {0, 0, 0, 0};
+    PrefillBufs pf;
+    std::vector<void *> allocs;
+};
+
+int decoder_build(qasr_decoder *d, const qasr_dec_weights *w);
+int decoder_enqueue_step(qasr_decoder *d, bool embed_mode);
+void decoder_free_prefill(qasr_decoder *d);

@@ -1,0 +1,58 @@
+// Internal host-side definitions shared by the C-ABI translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <algorithm>
+#include <string>
+#include "qasr_hip.h"
+
+// scratch area of a handle: argmax partials, attention partials
+#define QASR_SCRATCH_BYTES (8u << 20)
+#define QASR_ARGMAX_MAX_BLOCKS 4096
+#define QASR_COUNTERS 1024
+#define QASR_CTR_ARGMAX 0
+#define QASR_CTR_ATTN 64
+#define QASR_CTR_ATTN_N 256
+
+struct qasr_hip {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    void *scratch = nullptr;       // QASR_SCRATCH_BYTES
+    unsigned *counters = nullptr;  // QASR_COUNTERS, zero between kernels
+};
+
+int qasr_fail(int code, const std::string &msg);
+
+#define CHECK_H(h)                                                                   \
+    do {                                                                             \
+        if (!(h)) return qasr_fail(QASR_ERR_INVALID, "handle is null");              \
+        hipError_t e_ = hipSetDevice((h)->device);                                   \
+        if (e_ != hipSuccess) return qasr_fail(QASR_ERR_HIP, hipGetErrorString(e_)); \
+    } while (0)
+
+#define HIPCHK(x)                                                                                    \
+    do {                                                                                             \
+        hipError_t e_ = (x);                                                                         \
+        if (e_ != hipSuccess) return qasr_fail(QASR_ERR_HIP, std::string(#x) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define LAUNCHCHK(x, what)                                                                          \
+    do {                                                                                             \
+        hipError_t e_ = (x);                                                                         \
+        if (e_ == hipErrorInvalidValue) return qasr_fail(QASR_ERR_INVALID, std::string(what) + ": unsupported shape"); \
+        if (e_ != hipSuccess) return qasr_fail(QASR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+// number of context splits of the decode attention for a context of `len`
+// positions: at most 256 positions per split, at least min(16, len) splits
+static inline int attn_splits_for(int64_t len) {
+    int64_t s = std::max<int64_t>((len + 255) / 256, std::min<int64_t>(16, len));
+    return (int)std::max<int64_t>(1, s);
+}
+
+// blocks of the LM-head argmax grid
+static inline int argmax_blocks(int64_t rows) {
+    int64_t groups = (rows + 3) / 4;
+    int64_t b = (groups + 3) / 4;
+    return (int)std::max<int64_t>(1, std::min<int64_t>(b, 1024));
+}

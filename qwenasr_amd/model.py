@@ -1,0 +1,105 @@
+"""Model-level mirror of the reference's decoder API (decoder.rs) on the GPU."""
+import ctypes as C
+
+import numpy as np
+
+from ._lib import (QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, I32, P, check, lib)
+
+
+class Decoder:
+    """Device-resident Qwen3 decoder: Decoder::load + KvCache + decoder_prefill/forward.
+
+    ``weights`` is a :class:`qwenasr_amd.synth.SynthDecoder` (or any object with
+    the same numpy attributes).  The bf16 host arrays are uploaded once; the
+    int8 packing happens on the GPU.
+    """
+
+    def __init__(self, dev, weights, max_seq=2048, round_mode=QASR_ROUND_HALF_AWAY, kv_bf16=False):
+        self.dev = dev
+        self.cfg = dict(weights.cfg)
+        cfg, w = weights.structs(DecConfig, DecLayer, DecWeights)
+        d = P()
+        check(lib().qasr_hip_decoder_load(dev.h, C.byref(cfg), C.byref(w), round_mode, max_seq,
+                                          1 if kv_bf16 else 0, C.byref(d)))
+        self.d = d
+        self.max_seq = max_seq
+        self.kv_bf16 = kv_bf16
+
+    def close(self):
+        if self.d:
+            lib().qasr_hip_decoder_free(self.d)
+            self.d = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def kv_len(self):
+        return int(lib().qasr_hip_decoder_len(self.d))
+
+    @kv_len.setter
+    def kv_len(self, n):
+        check(lib().qasr_hip_decoder_set_len(self.d, int(n)))
+
+    def prefill(self, embeds):
+        """decoder_prefill (decoder.rs:455): embeds f32 [seq, hidden]."""
+        e = np.ascontiguousarray(embeds, np.float32)
+        check(lib().qasr_hip_decoder_prefill(self.d, e.ctypes.data_as(P), e.shape[0]))
+
+    def forward(self, embed=None, token=0):
+        """decoder_forward (decoder.rs:550): returns the greedy token id."""
+        out = I32()
+        if embed is None:
+            check(lib().qasr_hip_decoder_forward(self.d, None, int(token), C.byref(out)))
+        else:
+            e = np.ascontiguousarray(embed, np.float32)
+            check(lib().qasr_hip_decoder_forward(self.d, e.ctypes.data_as(P), 0, C.byref(out)))
+        return int(out.value)
+
+    def generate(self, n_steps, first_embed=None, first_token=0):
+        """n_steps forced greedy steps with no host round trip between steps."""
+        toks = np.empty(n_steps, np.int32)
+        if first_embed is None:
+            check(lib().qasr_hip_decoder_generate(self.d, None, int(first_token), n_steps,
+                                                  toks.ctypes.data_as(P)))
+        else:
+            e = np.ascontiguousarray(first_embed, np.float32)
+            check(lib().qasr_hip_decoder_generate(self.d, e.ctypes.data_as(P), 0, n_steps,
+                                                  toks.ctypes.data_as(P)))
+        return toks
+
+    def packed(self, layer, which):
+        """(int8 rows, scales) as packed on the GPU; layer -1 is the LM head."""
+        c = self.cfg
+        H, hd, I = c["hidden"], c["head_dim"], c["intermediate"]
+        qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+        if layer == -1:
+            shape = (c["vocab"], H)
+        else:
+            shape = [(qd, H), (kvd, H), (kvd, H), (H, qd), (2 * I, H), (H, I)][which]
+        q = np.empty(shape, np.int8)
+        s = np.empty(shape[0], np.float32)
+        check(lib().qasr_hip_decoder_packed(self.d, layer, which, q.ctypes.data_as(P),
+                                            s.ctypes.data_as(P)))
+        return q, s
+
+    def kv_shape(self):
+        c = self.cfg
+        return (c["n_layers"], c["n_kv_heads"], self.max_seq, c["head_dim"])
+
+    def kv_upload(self, k, v):
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        check(lib().qasr_hip_decoder_kv_upload(self.d, k.ctypes.data_as(P), v.ctypes.data_as(P)))
+
+    def kv_download(self):
+        k = np.empty(self.kv_shape(), np.float32)
+        v = np.empty(self.kv_shape(), np.float32)
+        check(lib().qasr_hip_decoder_kv_download(self.d, k.ctypes.data_as(P), v.ctypes.data_as(P)))
+        return k, v
+
+    def set_options(self, attn_splits=0, use_graph=True):
+        check(lib().qasr_hip_decoder_set_options(self.d, int(attn_splits), 1 if use_graph else 0))

@@ -1,0 +1,48 @@
+"""CPU checks of the drop-in boundary: the built libraries load and
+libqasr_hip.so exports exactly the entry points include/qasr_hip.h declares
+(no compute calls — there is no GPU in the CPU suite)."""
+import ctypes
+import os
+import re
+
+from conftest import ROOT
+
+
+def declared():
+    src = open(os.path.join(ROOT, "include", "qasr_hip.h")).read()
+    return sorted(set(re.findall(r"\b(qasr_hip_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol():
+    from qwenasr_amd import _lib
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    names = declared()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+    # the Python binding covers every declared entry point
+    assert set(names) <= set(_lib.declared_symbols()), set(names) - set(_lib.declared_symbols())
+
+
+def test_no_cpu_fallback_in_product():
+    """The product package never imports the oracle."""
+    pkg = os.path.join(ROOT, "qwenasr_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h", ".c")):
+                txt = open(os.path.join(dirpath, f)).read()
+                assert "oracle" not in txt.replace("Oracle", ""), f
+
+
+def test_synth_and_oracle_load():
+    from oracle import oracle
+    from qwenasr_amd import synth
+    oracle.lib()
+    a = synth.normal_f32(1000, 1, "x")
+    b = synth.normal_f32(1000, 1, "x")
+    assert (a == b).all() and abs(float(a.std()) - 1.0) < 0.1
+    c = synth.normal_bf16((4, 1 << 21), 2, "big")
+    synth._synth().qs_set_threads(1)
+    d = synth.normal_bf16((4, 1 << 21), 2, "big")
+    synth._synth().qs_set_threads(8)
+    assert (c == d).all()                      # block streams: thread count does not matter

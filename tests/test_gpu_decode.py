@@ -1,0 +1,119 @@
+"""GPU parity of the decode step (decoder_forward, decoder.rs:550-645) and its
+float kernels against the oracle.
+
+Per-head norm, RoPE and attention are f32 kernels compared within 1e-5
+relative; token ids must be identical under teacher forcing (the oracle's
+token is fed back to both sides at every step).
+"""
+import numpy as np
+import pytest
+
+from conftest import rng
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(n_layers=2, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=3072,
+            vocab=8192, eps=1e-6, theta=1e6)
+
+
+def test_head_norm_and_rope(dev, orc):
+    from qwenasr_amd import kernels as K
+    r = rng(21)
+    seq, heads, hd = 7, 16, 128
+    x = r.normal(0, 1, (seq, heads, hd)).astype(np.float32)
+    w = r.uniform(0.5, 1.5, hd).astype(np.float32)
+    cos, sin = orc.rope_table(64, hd, 1e6)
+    dx = dev.upload(x)
+    K.rms_norm_per_head(dx, dev.upload(w), seq, heads, hd, 1e-6)
+    ref = orc.rms_norm_per_head(x, w, heads, 1e-6)
+    np.testing.assert_allclose(dx.numpy(), ref.reshape(x.shape), rtol=1e-5, atol=1e-6)
+    dx.copy_from(x)
+    K.apply_rope_neox(dx, dev.upload(cos[40:40 + seq]), dev.upload(sin[40:40 + seq]), seq, heads, hd)
+    ref = orc.apply_rope(x, cos[40:40 + seq], sin[40:40 + seq], heads)
+    np.testing.assert_allclose(dx.numpy(), ref.reshape(x.shape), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("L", [1, 17, 604, 2048, 4096])
+def test_decode_attention(dev, orc, L):
+    from qwenasr_amd import kernels as K
+    print(f"attention L={L}", flush=True)
+    r = rng(L)
+    hq, hkv, hd, max_seq = 16, 8, 128, 4096
+    kc = r.normal(0, 1, (hkv, max_seq, hd)).astype(np.float32)
+    vc = r.normal(0, 1, (hkv, max_seq, hd)).astype(np.float32)
+    q = r.normal(0, 1, hq * hd).astype(np.float32)
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    out = dev.empty(hq * hd, np.float32)
+    K.causal_attention(out, dev.upload(q), dev.upload(kc), dev.upload(vc), max_seq * hd, 1, L, hq, hkv,
+                       hd, float(scale), L - 1)
+    ref = orc.causal_attention(q, kc, vc, max_seq * hd, 1, L, hq, hkv, hd, float(scale), L - 1)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-5, atol=2e-6)
+
+
+@pytest.fixture(scope="module")
+def tiny_models(dev, orc):
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    w = SynthDecoder(TINY, seed=1002)
+    gpu = Decoder(dev, w, max_seq=512)
+    cpu = orc.OracleDecoder(w, max_seq=512)
+    yield w, gpu, cpu
+    gpu.close()
+    cpu.close()
+
+
+def test_decoder_packing_bitexact(tiny_models):
+    _, gpu, cpu = tiny_models
+    for layer in (0, 1):
+        for which in range(6):
+            qg, sg = gpu.packed(layer, which)
+            qc, sc = cpu.packed(layer, which)
+            assert (qg == qc).all() and (sg == sc).all(), (layer, which)
+    qg, sg = gpu.packed(-1, 0)
+    qc, sc = cpu.packed(-1, 0)
+    assert (qg == qc).all() and (sg == sc).all()
+
+
+def test_decoder_teacher_forced(tiny_models):
+    w, gpu, cpu = tiny_models
+    gpu.kv_len = 0
+    cpu.kv_len = 0
+    n = 48
+    tok = 151644 % TINY["vocab"]
+    mism = []
+    for s in range(n):
+        e = cpu.embed(tok)
+        t_c, margin = cpu.forward(e)
+        t_g = gpu.forward(token=tok) if s else gpu.forward(embed=e)
+        if t_c != t_g:
+            mism.append((s, t_c, t_g, margin))
+        tok = t_c
+    assert not mism, mism
+    kg, vg = gpu.kv_download()
+    kc, vc = cpu.kv()
+    np.testing.assert_allclose(kg[:, :, :n], kc[:, :, :n], rtol=1e-4, atol=1e-4)
+    np.testing.assert_allclose(vg[:, :, :n], vc[:, :, :n], rtol=1e-4, atol=1e-4)
+
+
+def test_generate_matches_forward(tiny_models):
+    w, gpu, cpu = tiny_models
+    e = cpu.embed(42)
+    gpu.kv_len = 0
+    toks_fwd = [gpu.forward(embed=e)]
+    for _ in range(23):
+        toks_fwd.append(gpu.forward(token=toks_fwd[-1]))
+    for graph in (True, False):
+        gpu.set_options(use_graph=graph)
+        gpu.kv_len = 0
+        toks = gpu.generate(24, first_embed=e)
+        assert list(toks) == toks_fwd, graph
+    gpu.set_options(use_graph=True)
+
+
+def test_kv_capacity_error(tiny_models):
+    from qwenasr_amd import QasrError
+    _, gpu, _ = tiny_models
+    gpu.kv_len = 512
+    with pytest.raises(QasrError):
+        gpu.forward(token=1)
+    gpu.kv_len = 0
