@@ -31,6 +31,23 @@ __device__ __forceinline__ float group_sum_f32(float v) {
     return v;
 }
 
+// IEEE round-to-nearest sqrt (what glibc sqrtf returns).  v_sqrt_f32 alone is
+// only ~1 ulp accurate; the estimate s is corrected by comparing x against the
+// products with its two neighbours, computed exactly with fma.
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const bool tiny = x < 0x1.0p-96f;
+    const float xs = tiny ? x * 0x1.0p+32f : x;
+    float s = __builtin_amdgcn_sqrtf(xs);
+    const float dn = __uint_as_float(__float_as_uint(s) - 1u);
+    const float up = __uint_as_float(__float_as_uint(s) + 1u);
+    const float r_dn = fmaf(-dn, s, xs);
+    const float r_up = fmaf(-up, s, xs);
+    s = r_dn <= 0.0f ? dn : s;
+    s = r_up > 0.0f ? up : s;
+    s = tiny ? s * 0x1.0p-16f : s;
+    return (xs == 0.0f || xs == __builtin_inff() || xs != xs) ? __builtin_amdgcn_sqrtf(xs) * (tiny ? 0x1.0p-16f : 1.0f) : s;
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
 }

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
         float v = a.qkv[(kvh * G + gi) * D + d];
         if (prep) {
             const float ss = head_sum128(__fmul_rn(v, v), red);
-            const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
+            const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
             v = __fmul_rn(__fmul_rn(v, r), a.q_norm[d]);
             qs[gi][d] = v;
             __syncthreads();
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
         float kv = a.qkv[Hq * D + kvh * D + d];
         const float ss = head_sum128(t < D ? __fmul_rn(kv, kv) : 0.0f, red);
         if (t < D) {
-            const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
+            const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
             kv = __fmul_rn(__fmul_rn(kv, r), a.k_norm[d]);
             knew[d] = kv;
         }
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void k_rms_norm_rows(float *__restrict__ out, 
         for (int i = 0; i < nslot; i++) acc = fmaf(tr[i], tr[i], acc);
     }
     const float ss = avx16_tree(acc);
-    const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
+    const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
     for (int i = lane; i < H; i += 64) o[i] = __fmul_rn(__fmul_rn(xr[i], rinv), w[i]);
 }
 
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(float *__restrict__ x, c
     float x1 = v[lane], x2 = v[lane + 64];
     if (do_norm) {
         const float ss = wave_sum_f32(__fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2)));
-        const float r = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
         x1 = __fmul_rn(__fmul_rn(x1, r), w[lane]);
         x2 = __fmul_rn(__fmul_rn(x2, r), w[lane + 64]);
     }

@@ -117,7 +117,7 @@ __device__ __forceinline__ void act_prologue(const float *__restrict__ x, const 
         }
         __builtin_amdgcn_wave_barrier();
         const float ss = avx16_tree(acc);
-        const float rinv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
+        const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
 #pragma unroll
         for (int c = 0; c < NS; c++) {
             const int s = lane + 64 * c;
