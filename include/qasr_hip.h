@@ -115,11 +115,34 @@ int qasr_hip_apply_rope_neox(qasr_hip *h, float *x, const float *cos_vals, const
                              int64_t seq, int64_t n_heads, int64_t head_dim);
 /* causal_attention (kernels/mod.rs:1663-1698); K/V layout [kv_head][pos][head_dim]
  * with head_stride elements between heads, as KvCache (decoder.rs:174-271).
- * seq_q == 1 only in this build; head_dim == 128, n_heads == 2 * n_kv_heads. */
+ * head_dim == 128, n_heads == 2 * n_kv_heads; seq_q > 1 uses the multi-row kernel. */
 int qasr_hip_causal_attention(qasr_hip *h, float *out, const float *q, const float *k_base,
                               const float *v_base, int64_t head_stride, int64_t seq_q,
                               int64_t seq_k, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                               float scale, int64_t q_offset);
+
+/* ---- A15/A16: dense GEMMs (MFMA) ----------------------------------------
+ * linear (kernels/mod.rs:550-584) / linear_accumulate (mod.rs:591-628) on
+ * bf16-valued weights, as the reference runs them through cblas_sgemm after
+ * bf16->f32 conversion: y[seq, out] = x W^T (+ bias), or with accumulate != 0
+ * y = (y + bias) + x W^T.  x f32 is split into three bf16 terms so every
+ * product is exact and accumulation is f32 (f32-class accuracy). */
+int qasr_hip_linear_bf16w(qasr_hip *h, float *y, const float *x, const uint16_t *w_bf16,
+                          const float *bias, int64_t seq, int64_t in_dim, int64_t out_dim,
+                          int accumulate);
+/* int8 weights x bf16 activations (the prefill / encoder GEMM of the int8 path):
+ * y[M, N] = (sum_k a[m, k] * q[n, k]) * scales[n]; q and scales as packed by
+ * qasr_hip_pack_int8_rows.  MFMA bf16 with exact int8->bf16 dequantisation. */
+int qasr_hip_gemm_w8_bf16(qasr_hip *h, float *y, const uint16_t *a_bf16, const int8_t *w,
+                          const float *scales, int64_t M, int64_t N, int64_t K);
+/* layer_norm (kernels/mod.rs:1160-1189, AVX order); hidden % 16 == 0, <= 4096 */
+int qasr_hip_layer_norm(qasr_hip *h, float *out, const float *x, const float *w, const float *b,
+                        int64_t seq, int64_t hidden, float eps);
+/* bidirectional_attention (kernels/mod.rs:1386-1471) over windows of window_tokens
+ * (every window full except the last); q/k/v/out [seq][n_heads * head_dim], head_dim 64 or 128 */
+int qasr_hip_bidirectional_attention(qasr_hip *h, float *out, const float *q, const float *k,
+                                     const float *v, int64_t seq, int64_t n_heads, int64_t head_dim,
+                                     float scale, int64_t window_tokens);
 
 /* ---- model level: the Qwen3 decoder (decoder.rs) ------------------------ */
 typedef struct {
@@ -173,6 +196,49 @@ int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
 /* decode-step tuning: attention context splits (default chosen from max_seq)
  * and whether steps replay a captured HIP graph (default 1) */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
+
+/* ---- model level: audio front end (audio.rs:273-372, encoder.rs) ---------- */
+typedef struct {
+    int32_t d_model, n_layers, n_heads, head_dim, ffn_dim, output_dim;
+    int32_t chunk_size, n_window_infer, conv_hidden;        /* QwenConfig enc_*, config.rs:29-39 */
+} qasr_enc_config;
+
+typedef struct {                                        /* EncLayer, encoder.rs:7-24 */
+    const uint16_t *wq, *wk, *wv, *wo, *fc1, *fc2;      /* host bf16 [out, in] */
+    const float *bq, *bk, *bv, *bo, *b1, *b2;
+    const float *ln1_w, *ln1_b, *ln2_w, *ln2_b;
+} qasr_enc_layer;
+
+typedef struct {                                        /* Encoder, encoder.rs:78-93 */
+    const uint16_t *conv1_w, *conv2_w, *conv3_w, *conv_out_w;   /* bf16 [out, in*3*3] / [d, 480*16] */
+    const float *conv1_b, *conv2_b, *conv3_b;
+    const qasr_enc_layer *layers;
+    const float *ln_post_w, *ln_post_b;
+    const uint16_t *proj1_w, *proj2_w;
+    const float *proj1_b, *proj2_b;
+} qasr_enc_weights;
+
+typedef struct qasr_encoder qasr_encoder;
+
+/* Encoder::load (encoder.rs:123-182) plus the mel tables (audio.rs:225-330) */
+int qasr_hip_encoder_load(qasr_hip *h, const qasr_enc_config *cfg, const qasr_enc_weights *w,
+                          qasr_encoder **out);
+void qasr_hip_encoder_free(qasr_encoder *e);
+int64_t qasr_hip_encoder_tokens(const qasr_encoder *e, int64_t mel_frames);
+/* mel_spectrogram (audio.rs:273): host samples -> host mel [128][frames]
+ * (mel_out NULL: only report *frames) */
+int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n_samples, float *mel_out,
+                 int64_t *frames);
+/* Encoder::forward (encoder.rs:186): host mel [128][frames] -> host [tokens][output_dim] */
+int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64_t frames, float *out,
+                             int64_t *n_tokens);
+/* transcribe_segment (transcribe.rs:63-247) with a forced decode length and no
+ * text prompt: mel -> encoder -> prompt -> prefill(total - 1) -> n_steps greedy
+ * forwards, all device-resident.  times_ms (optional, 4 entries): mel, encoder,
+ * prefill + first forward, remaining decode. */
+int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *samples,
+                               int64_t n_samples, int32_t n_steps, int32_t *tokens_out,
+                               double *times_ms);
 
 #ifdef __cplusplus
 }

@@ -108,6 +108,16 @@ _SIGS = {
     "qasr_hip_decoder_kv_upload": (C.c_int, [P, P, P]),
     "qasr_hip_decoder_kv_download": (C.c_int, [P, P, P]),
     "qasr_hip_decoder_set_options": (C.c_int, [P, C.c_int, C.c_int]),
+    "qasr_hip_linear_bf16w": (C.c_int, [P, P, P, P, P, I64, I64, I64, C.c_int]),
+    "qasr_hip_gemm_w8_bf16": (C.c_int, [P, P, P, P, P, I64, I64, I64]),
+    "qasr_hip_layer_norm": (C.c_int, [P, P, P, P, P, I64, I64, F32]),
+    "qasr_hip_bidirectional_attention": (C.c_int, [P, P, P, P, P, I64, I64, I64, F32, I64]),
+    "qasr_hip_encoder_load": (C.c_int, [P, C.POINTER(EncConfig), C.POINTER(EncWeights), C.POINTER(P)]),
+    "qasr_hip_encoder_free": (None, [P]),
+    "qasr_hip_encoder_tokens": (I64, [P, I64]),
+    "qasr_hip_mel": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),
+    "qasr_hip_encoder_forward": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),
+    "qasr_hip_transcribe_forced": (C.c_int, [P, P, P, I64, I32, P, P]),
 }
 
 _lib = None

@@ -327,10 +327,20 @@ extern "C" int qasr_hip_causal_attention(qasr_hip *h, float *out, const float *q
                                          int64_t seq_k, int64_t n_heads, int64_t n_kv_heads,
                                          int64_t hd, float scale, int64_t q_offset) {
     CHECK_H(h);
-    if (!out || !q || !k_base || !v_base || seq_q != 1 || hd != 128 || n_kv_heads <= 0 ||
-        n_heads != 2 * n_kv_heads || seq_k < 0 || q_offset < 0 || head_stride < hd)
+    if (!out || !q || !k_base || !v_base || seq_q <= 0 || hd != 128 || n_kv_heads <= 0 ||
+        n_heads != 2 * n_kv_heads || seq_k < 0 || q_offset < 0 || head_stride < hd || seq_k > (1 << 24))
         return qasr_fail(QASR_ERR_INVALID,
-                         "causal_attention: supported shape is seq_q == 1, head_dim 128, n_heads == 2 * n_kv_heads");
+                         "causal_attention: supported shape is head_dim 128, n_heads == 2 * n_kv_heads");
+    if (seq_q > 1) {
+        AttnRowsArgs a{};
+        a.q = q; a.q_rs = n_heads * hd;
+        a.k = k_base; a.v = v_base; a.k_hs = head_stride; a.k_rs = hd;
+        a.out = out; a.o_rs = n_heads * hd;
+        a.n_q = (int)seq_q; a.n_k = (int)seq_k; a.G = (int)(n_heads / n_kv_heads);
+        a.q_offset = (int)q_offset; a.window = 0; a.scale = scale;
+        LAUNCHCHK(launch_attn_rows(a, (int)n_kv_heads, (int)hd, h->stream), "causal_attention");
+        return QASR_OK;
+    }
     const int64_t k_end = std::min(q_offset + 1, seq_k);
     if (k_end == 0) {
         HIPCHK(hipMemsetAsync(out, 0, sizeof(float) * n_heads * hd, h->stream));
@@ -344,12 +354,65 @@ extern "C" int qasr_hip_causal_attention(qasr_hip *h, float *out, const float *q
     a.head_stride = head_stride;
     a.n_split = attn_splits_for(k_end);
     const size_t need = (size_t)n_kv_heads * a.n_split * 2 * (hd + 2) * sizeof(float);
-    if (need > QASR_SCRATCH_BYTES || n_kv_heads > QASR_CTR_ATTN_N)
+    if (need > QASR_SCRATCH_BYTES || n_kv_heads > QASR_CTR_ATTN_N || a.n_split > 64)
         return qasr_fail(QASR_ERR_INVALID, "causal_attention: context too long for the scratch area");
     a.part = reinterpret_cast<float *>(h->scratch);
     a.counters = h->counters + QASR_CTR_ATTN;
     a.out = out;
     a.scale = scale;
     LAUNCHCHK(launch_attn_decode(a, (int)n_heads, (int)n_kv_heads, (int)hd, 0, h->stream), "causal_attention");
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_bidirectional_attention(qasr_hip *h, float *out, const float *q, const float *k,
+                                                const float *v, int64_t seq, int64_t n_heads, int64_t hd,
+                                                float scale, int64_t window) {
+    CHECK_H(h);
+    if (!out || !q || !k || !v || seq <= 0 || n_heads <= 0 || (hd != 64 && hd != 128) || window <= 0 ||
+        seq > (1 << 24))
+        return qasr_fail(QASR_ERR_INVALID, "bidirectional_attention: bad arguments (head_dim 64 or 128)");
+    AttnRowsArgs a{};
+    a.q = q; a.q_rs = n_heads * hd;
+    a.k = k; a.v = v; a.k_hs = hd; a.k_rs = n_heads * hd;
+    a.out = out; a.o_rs = n_heads * hd;
+    a.n_q = (int)seq; a.n_k = (int)seq; a.G = 1; a.q_offset = 0; a.window = (int)window; a.scale = scale;
+    LAUNCHCHK(launch_attn_rows(a, (int)n_heads, (int)hd, h->stream), "bidirectional_attention");
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_linear_bf16w(qasr_hip *h, float *y, const float *x, const uint16_t *w,
+                                     const float *bias, int64_t seq, int64_t in_dim, int64_t out_dim,
+                                     int accumulate) {
+    CHECK_H(h);
+    if (!y || !x || !w || seq <= 0 || in_dim <= 0 || out_dim <= 0 || seq > (1 << 28) || in_dim > (1 << 24) ||
+        out_dim > (1 << 28))
+        return qasr_fail(QASR_ERR_INVALID, "linear_bf16w: bad arguments");
+    GemmArgs g{};
+    g.M = (int)seq; g.N = (int)out_dim; g.K = (int)in_dim;
+    g.A = x; g.lda = in_dim; g.B = w; g.ldb = in_dim; g.C = y; g.ldc = out_dim; g.bias = bias;
+    LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, accumulate ? EPI_ACCUM : EPI_NONE, h->stream), "linear_bf16w");
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_gemm_w8_bf16(qasr_hip *h, float *y, const uint16_t *a, const int8_t *w,
+                                     const float *scales, int64_t M, int64_t N, int64_t K) {
+    CHECK_H(h);
+    if (!y || !a || !w || !scales || M <= 0 || N <= 0 || K <= 0 || M > (1 << 28) || N > (1 << 28) ||
+        K > (1 << 24))
+        return qasr_fail(QASR_ERR_INVALID, "gemm_w8_bf16: bad arguments");
+    GemmArgs g{};
+    g.M = (int)M; g.N = (int)N; g.K = (int)K;
+    g.A = a; g.lda = K; g.B = w; g.ldb = K; g.C = y; g.ldc = N; g.scale = scales;
+    LAUNCHCHK(launch_gemm(g, A_BF16, B_I8, EPI_SCALE, h->stream), "gemm_w8_bf16");
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_layer_norm(qasr_hip *h, float *out, const float *x, const float *w, const float *b,
+                                   int64_t seq, int64_t hidden, float eps) {
+    CHECK_H(h);
+    if (!out || !x || !w || !b || seq < 0 || hidden <= 0 || hidden % 16 != 0 || hidden > 4096)
+        return qasr_fail(QASR_ERR_INVALID, "layer_norm: hidden must be a positive multiple of 16 and <= 4096");
+    if (seq == 0) return QASR_OK;
+    LAUNCHCHK(launch_layer_norm_rows(out, x, w, b, seq, (int)hidden, eps, h->stream), "layer_norm");
     return QASR_OK;
 }

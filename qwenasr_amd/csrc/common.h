@@ -48,6 +48,40 @@ __device__ __forceinline__ float sqrt_rn(float x) {
     return (xs == 0.0f || xs == __builtin_inff() || xs != xs) ? __builtin_amdgcn_sqrtf(xs) * (tiny ? 0x1.0p-16f : 1.0f) : s;
 }
 
+// ---- cross-block hand-off ------------------------------------------------
+// MI355X's L2 is private to each XCD, so a block that publishes data for a
+// block on another XCD must get it past its own L2.  Instead of a release fence
+// (which writes back the whole L2) the producer stores with agent-scope relaxed
+// atomics (write-through), waits for their acknowledgement, and only then bumps
+// the counter; the consumer reads with agent-scope atomic loads (which miss the
+// local L2).  Nothing else in the kernel needs to be made visible.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int *p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_agent(const int *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait until every memory operation this thread issued has completed
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
+// counter bump after the block's stores completed; true in the last block to arrive
+__device__ __forceinline__ bool arrive_last(unsigned *ctr, unsigned n_blocks, int *flag_lds) {
+    wait_all_mem();
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *flag_lds = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_blocks - 1;
+    __syncthreads();
+    return *flag_lds != 0;
+}
+__device__ __forceinline__ void reset_counter(unsigned *ctr) {
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float((uint32_t)h << 16);
 }
@@ -85,6 +119,48 @@ __device__ __forceinline__ float avx16_tree(float a) {
     float v = __fadd_rn(u, __shfl_down(u, 1, QASR_WAVE));
     float r = __fadd_rn(v, __shfl_down(v, 2, QASR_WAVE));
     return __shfl(r, 0, QASR_WAVE);
+}
+
+// gelu of the reference (avx.rs:536-563) for element `idx` of a buffer of n
+// elements that gelu() splits into 16 per-thread chunks (mod.rs:1250-1289):
+// the last n_chunk % 8 elements of each chunk take the scalar libm-tanh path.
+// avx::fast_exp_avx (avx.rs:487-514); cvtps_epi32 rounds to nearest even
+__device__ __forceinline__ float fast_exp_ref(float x) {
+    float val = __fmul_rn(x, 1.442695041f);
+    val = fminf(val, 126.0f);
+    val = fmaxf(val, -126.0f);
+    const int ip = (int)rintf(val);
+    const float fp = __fsub_rn(val, (float)ip);
+    const float ei = __uint_as_float((uint32_t)(ip + 127) << 23);
+    const float f = __fmul_rn(fp, 0.6931471806f);
+    float p = fmaf(1.0f / 120.0f, f, 1.0f / 24.0f);
+    p = fmaf(p, f, 1.0f / 6.0f);
+    p = fmaf(p, f, 0.5f);
+    p = fmaf(p, f, 1.0f);
+    p = fmaf(p, f, 1.0f);
+    return __fmul_rn(ei, p);
+}
+
+__device__ __forceinline__ float gelu_ref(float v, int64_t idx, int64_t n) {
+    bool vec = true;
+    if (n > 4096) {
+        const int64_t chunk = (n + 15) / 16;
+        const int64_t c = idx / chunk, start = c * chunk;
+        const int64_t len = min(chunk, n - start);
+        vec = (idx - start) < len - (len % 8);
+    } else {
+        vec = idx < n - (n % 8);
+    }
+    if (vec) {
+        const float v3 = __fmul_rn(__fmul_rn(v, v), v);
+        const float inner = __fmul_rn(0.7978845608028654f, fmaf(0.044715f, v3, v));
+        const float e2 = fast_exp_ref(__fmul_rn(2.0f, inner));
+        const float t = __fsub_rn(1.0f, __fdiv_rn(2.0f, __fadd_rn(e2, 1.0f)));
+        return __fmul_rn(0.5f, __fmul_rn(v, __fadd_rn(1.0f, t)));
+    }
+    const float x3 = __fmul_rn(__fmul_rn(v, v), v);
+    const float inner = __fmul_rn(0.7978845608028654f, __fadd_rn(v, __fmul_rn(0.044715f, x3)));
+    return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, tanhf(inner)));
 }
 
 }  // namespace qasr

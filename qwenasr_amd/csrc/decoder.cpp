@@ -261,7 +261,7 @@ static int set_state(qasr_decoder *d, int32_t token) {
     return QASR_OK;
 }
 
-static int run_embed_step(qasr_decoder *d) {
+int decoder_run_embed_step(qasr_decoder *d) {
     if (!d->use_graph) return decoder_enqueue_step(d, true);
     if (!d->graph_exec) {
         hipGraph_t g = nullptr;
@@ -294,7 +294,7 @@ extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int
         HIPCHK(hipMemcpyAsync(d->x, embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice, d->h->stream));
         TRY(decoder_enqueue_step(d, false));
     } else {
-        TRY(run_embed_step(d));
+        TRY(decoder_run_embed_step(d));
     }
     HIPCHK(hipMemcpyAsync(d->host_state, d->state, sizeof(d->host_state), hipMemcpyDeviceToHost, d->h->stream));
     HIPCHK(hipStreamSynchronize(d->h->stream));
@@ -318,9 +318,9 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
                               d->h->stream));
         TRY(decoder_enqueue_step(d, false));
     } else {
-        TRY(run_embed_step(d));
+        TRY(decoder_run_embed_step(d));
     }
-    for (int32_t s = 1; s < n_steps; s++) TRY(run_embed_step(d));
+    for (int32_t s = 1; s < n_steps; s++) TRY(decoder_run_embed_step(d));
     HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost,
                           d->h->stream));
     HIPCHK(hipStreamSynchronize(d->h->stream));

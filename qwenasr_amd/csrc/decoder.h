@@ -44,3 +44,5 @@ struct qasr_decoder {
 int decoder_build(qasr_decoder *d, const qasr_dec_weights *w);
 int decoder_enqueue_step(qasr_decoder *d, bool embed_mode);
 void decoder_free_prefill(qasr_decoder *d);
+int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S);
+int decoder_run_embed_step(qasr_decoder *d);

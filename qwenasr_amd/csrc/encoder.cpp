@@ -1,1 +1,500 @@
+// Audio front end on the device: mel spectrogram (audio.rs:273-372), the audio
+// encoder (encoder.rs:186-358) and the offline driver with a forced decode
+// length (transcribe.rs:63-247).
+#include <cmath>
+#include <cstring>
+#include <vector>
+
 #include "decoder.h"
+
+using namespace qasr;
+
+#define TRY(x)                  \
+    do {                        \
+        int rc_ = (x);          \
+        if (rc_ != QASR_OK) {   \
+            return rc_;         \
+        }                       \
+    } while (0)
+
+struct EncLayerDev {
+    uint16_t *wqkv = nullptr, *wo = nullptr, *fc1 = nullptr, *fc2 = nullptr;
+    float *bqkv = nullptr, *bo = nullptr, *b1 = nullptr, *b2 = nullptr;
+    float *ln1_w = nullptr, *ln1_b = nullptr, *ln2_w = nullptr, *ln2_b = nullptr;
+};
+
+struct qasr_encoder {
+    qasr_hip *h = nullptr;
+    qasr_enc_config c{};
+    uint16_t *conv1_w = nullptr, *conv2_w = nullptr, *conv3_w = nullptr, *conv_out_w = nullptr;
+    float *conv1_b = nullptr, *conv2_b = nullptr, *conv3_b = nullptr;
+    std::vector<EncLayerDev> L;
+    float *ln_post_w = nullptr, *ln_post_b = nullptr;
+    uint16_t *proj1_w = nullptr, *proj2_w = nullptr;
+    float *proj1_b = nullptr, *proj2_b = nullptr;
+    float *pe = nullptr;                        // sinusoidal PE [tokens_per_chunk][d_model]
+    int tokens_per_chunk = 0;
+    // mel tables
+    float *window = nullptr, *dft_cos = nullptr, *dft_sin = nullptr, *filters = nullptr;
+    // scratch (grown on demand)
+    size_t scratch_bytes = 0;
+    char *scratch = nullptr;
+    std::vector<void *> allocs;
+};
+
+template <typename T>
+static int ealloc(qasr_encoder *e, T **p, size_t count) {
+    void *v = nullptr;
+    if (hipMalloc(&v, count * sizeof(T) + 256) != hipSuccess)
+        return qasr_fail(QASR_ERR_NOMEM, "encoder: device allocation failed");
+    e->allocs.push_back(v);
+    *p = reinterpret_cast<T *>(v);
+    return QASR_OK;
+}
+
+template <typename T>
+static int eupload(qasr_encoder *e, T **p, const T *host, size_t count) {
+    TRY(ealloc(e, p, count));
+    HIPCHK(hipMemcpyAsync(*p, host, count * sizeof(T), hipMemcpyHostToDevice, e->h->stream));
+    return QASR_OK;
+}
+
+static int conv_len(int n) { return (n + 2 - 3) / 2 + 1; }
+
+// ---- mel tables with the reference's f32 formulas and the host libm ---------
+static float hz_to_mel(float f) {                       // audio.rs:202-212
+    const float logstep = 27.0f / logf(6.4f);
+    const float mels = 3.0f * f / 200.0f;
+    return f >= 1000.0f ? 15.0f + logf(f / 1000.0f) * logstep : mels;
+}
+static float mel_to_hz(float m) {                       // audio.rs:214-223
+    const float logstep = logf(6.4f) / 27.0f;
+    return m >= 15.0f ? 1000.0f * expf(logstep * (m - 15.0f)) : 200.0f * m / 3.0f;
+}
+
+static void mel_tables(std::vector<float> &win, std::vector<float> &ct, std::vector<float> &sn,
+                       std::vector<float> &filt) {
+    const float PI = 3.14159265358979323846264338327950288f;
+    win.resize(400);
+    for (int i = 0; i < 400; i++) win[i] = 0.5f * (1.0f - cosf(2.0f * PI * (float)i / 400.0f));
+    ct.resize(201 * 400);
+    sn.resize(201 * 400);
+    for (int k = 0; k < 201; k++)
+        for (int n = 0; n < 400; n++) {
+            const float a = 2.0f * PI * (float)k * (float)n / 400.0f;
+            ct[k * 400 + n] = cosf(a);
+            sn[k * 400 + n] = sinf(a);
+        }
+    float fft[201], ff[130], fd[129];                    // audio.rs:225-262
+    for (int i = 0; i < 201; i++) fft[i] = (float)i * (16000.0f / 2.0f) / 200.0f;
+    const float mmin = hz_to_mel(0.0f), mmax = hz_to_mel(8000.0f);
+    for (int i = 0; i < 130; i++) ff[i] = mel_to_hz(mmin + (mmax - mmin) * (float)i / 129.0f);
+    for (int i = 0; i < 129; i++) {
+        fd[i] = ff[i + 1] - ff[i];
+        if (fd[i] == 0.0f) fd[i] = 1e-6f;
+    }
+    filt.assign(128 * 201, 0.0f);
+    for (int m = 0; m < 128; m++) {
+        const float enorm = 2.0f / (ff[m + 2] - ff[m]);
+        for (int f = 0; f < 201; f++) {
+            const float down = (fft[f] - ff[m]) / fd[m];
+            const float up = (ff[m + 2] - fft[f]) / fd[m + 1];
+            filt[m * 201 + f] = fmaxf(fminf(down, up), 0.0f) * enorm;
+        }
+    }
+}
+
+static std::vector<uint16_t> concat3(const uint16_t *a, const uint16_t *b, const uint16_t *c, size_t n) {
+    std::vector<uint16_t> v(3 * n);
+    std::memcpy(v.data(), a, n * 2);
+    std::memcpy(v.data() + n, b, n * 2);
+    std::memcpy(v.data() + 2 * n, c, n * 2);
+    return v;
+}
+
+static int encoder_build(qasr_encoder *e, const qasr_enc_weights *w) {
+    const qasr_enc_config &c = e->c;
+    const int64_t D = c.d_model, F = c.ffn_dim, C = c.conv_hidden, O = c.output_dim;
+    const int h3 = conv_len(conv_len(conv_len(128)));
+    TRY(eupload(e, &e->conv1_w, w->conv1_w, C * 9));
+    TRY(eupload(e, &e->conv2_w, w->conv2_w, C * C * 9));
+    TRY(eupload(e, &e->conv3_w, w->conv3_w, C * C * 9));
+    TRY(eupload(e, &e->conv1_b, w->conv1_b, C));
+    TRY(eupload(e, &e->conv2_b, w->conv2_b, C));
+    TRY(eupload(e, &e->conv3_b, w->conv3_b, C));
+    TRY(eupload(e, &e->conv_out_w, w->conv_out_w, D * C * h3));
+    e->L.resize(c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        const qasr_enc_layer &s = w->layers[l];
+        EncLayerDev &L = e->L[l];
+        std::vector<uint16_t> qkv = concat3(s.wq, s.wk, s.wv, D * D);
+        std::vector<float> bqkv(3 * D);
+        std::memcpy(bqkv.data(), s.bq, D * 4);
+        std::memcpy(bqkv.data() + D, s.bk, D * 4);
+        std::memcpy(bqkv.data() + 2 * D, s.bv, D * 4);
+        TRY(eupload(e, &L.wqkv, qkv.data(), 3 * D * D));
+        TRY(eupload(e, &L.bqkv, bqkv.data(), 3 * D));
+        HIPCHK(hipStreamSynchronize(e->h->stream));     // host staging vectors go out of scope
+        TRY(eupload(e, &L.wo, s.wo, D * D));
+        TRY(eupload(e, &L.bo, s.bo, D));
+        TRY(eupload(e, &L.fc1, s.fc1, F * D));
+        TRY(eupload(e, &L.b1, s.b1, F));
+        TRY(eupload(e, &L.fc2, s.fc2, D * F));
+        TRY(eupload(e, &L.b2, s.b2, D));
+        TRY(eupload(e, &L.ln1_w, s.ln1_w, D));
+        TRY(eupload(e, &L.ln1_b, s.ln1_b, D));
+        TRY(eupload(e, &L.ln2_w, s.ln2_w, D));
+        TRY(eupload(e, &L.ln2_b, s.ln2_b, D));
+    }
+    TRY(eupload(e, &e->ln_post_w, w->ln_post_w, D));
+    TRY(eupload(e, &e->ln_post_b, w->ln_post_b, D));
+    TRY(eupload(e, &e->proj1_w, w->proj1_w, D * D));
+    TRY(eupload(e, &e->proj1_b, w->proj1_b, D));
+    TRY(eupload(e, &e->proj2_w, w->proj2_w, O * D));
+    TRY(eupload(e, &e->proj2_b, w->proj2_b, O));
+    // per-chunk sinusoidal PE (sinusoidal_pe, kernels/mod.rs:1704-1717)
+    e->tokens_per_chunk = conv_len(conv_len(conv_len(c.chunk_size)));
+    {
+        const int64_t n_pos = e->tokens_per_chunk, half = D / 2;
+        std::vector<float> pe(n_pos * D);
+        const float lt = logf(10000.0f) / (float)(half - 1);
+        for (int64_t p = 0; p < n_pos; p++)
+            for (int64_t d = 0; d < half; d++) {
+                const float inv_ts = expf(-(float)d * lt);
+                const float a = (float)p * inv_ts;
+                pe[p * D + d] = sinf(a);
+                pe[p * D + half + d] = cosf(a);
+            }
+        TRY(eupload(e, &e->pe, pe.data(), pe.size()));
+        std::vector<float> win, ct, sn, filt;
+        mel_tables(win, ct, sn, filt);
+        TRY(eupload(e, &e->window, win.data(), win.size()));
+        TRY(eupload(e, &e->dft_cos, ct.data(), ct.size()));
+        TRY(eupload(e, &e->dft_sin, sn.data(), sn.size()));
+        TRY(eupload(e, &e->filters, filt.data(), filt.size()));
+        HIPCHK(hipStreamSynchronize(e->h->stream));
+    }
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_encoder_load(qasr_hip *h, const qasr_enc_config *cfg, const qasr_enc_weights *w,
+                                     qasr_encoder **out) {
+    CHECK_H(h);
+    if (!cfg || !w || !out || !w->layers) return qasr_fail(QASR_ERR_INVALID, "encoder_load: null argument");
+    *out = nullptr;
+    const qasr_enc_config c = *cfg;
+    if (c.n_layers <= 0 || c.d_model <= 0 || c.d_model % 16 != 0 || c.d_model > 4096 || c.head_dim != 64 ||
+        c.n_heads * c.head_dim != c.d_model || c.ffn_dim <= 0 || c.output_dim <= 0 || c.chunk_size <= 0 ||
+        c.n_window_infer < c.chunk_size || c.conv_hidden <= 0)
+        return qasr_fail(QASR_ERR_INVALID, "encoder_load: unsupported config (head_dim 64, d_model % 16 == 0)");
+    qasr_encoder *e = new qasr_encoder();
+    e->h = h;
+    e->c = c;
+    int rc = encoder_build(e, w);
+    if (rc != QASR_OK) {
+        qasr_hip_encoder_free(e);
+        return rc;
+    }
+    *out = e;
+    return QASR_OK;
+}
+
+extern "C" void qasr_hip_encoder_free(qasr_encoder *e) {
+    if (!e) return;
+    (void)hipSetDevice(e->h->device);
+    (void)hipStreamSynchronize(e->h->stream);
+    if (e->scratch) (void)hipFree(e->scratch);
+    for (void *p : e->allocs) (void)hipFree(p);
+    delete e;
+}
+
+static int ensure_scratch(qasr_encoder *e, size_t bytes) {
+    if (bytes <= e->scratch_bytes) return QASR_OK;
+    HIPCHK(hipStreamSynchronize(e->h->stream));
+    if (e->scratch) (void)hipFree(e->scratch);
+    e->scratch = nullptr;
+    e->scratch_bytes = 0;
+    if (hipMalloc((void **)&e->scratch, bytes) != hipSuccess)
+        return qasr_fail(QASR_ERR_NOMEM, "encoder: scratch allocation failed");
+    e->scratch_bytes = bytes;
+    return QASR_OK;
+}
+
+int64_t encoder_tokens(const qasr_encoder *e, int64_t frames) {
+    int64_t tot = 0;
+    for (int64_t s = 0; s < frames; s += e->c.chunk_size) {
+        const int w = (int)std::min<int64_t>(e->c.chunk_size, frames - s);
+        tot += conv_len(conv_len(conv_len(w)));
+    }
+    return tot;
+}
+
+static int egemm(qasr_encoder *e, const float *A, int64_t lda, const uint16_t *B, int64_t ldb, float *C,
+                 int64_t ldc, int M, int N, int K, const float *bias, int epi, int64_t gelu_n = 0,
+                 int gelu_rows = 0) {
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.bias = bias;
+    g.gelu_n = gelu_n; g.gelu_rows = gelu_rows;
+    LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, epi, e->h->stream), "encoder gemm");
+    return QASR_OK;
+}
+
+// conv stem for n_chunks chunks of cw frames starting at frame f0; writes the
+// projected + PE rows to x (encoder.rs:226-287)
+static int conv_stem(qasr_encoder *e, const float *mel, int64_t frames, int64_t f0, int n_chunks, int cw,
+                     float *x, char *buf) {
+    hipStream_t st = e->h->stream;
+    const int C = e->c.conv_hidden, D = e->c.d_model;
+    const int h1 = conv_len(128), w1 = conv_len(cw), h2 = conv_len(h1), w2 = conv_len(w1);
+    const int h3 = conv_len(h2), w3 = conv_len(w2);
+    float *cols = reinterpret_cast<float *>(buf);
+    float *a1 = cols + (int64_t)n_chunks * h2 * w2 * C * 9 + (int64_t)n_chunks * h1 * w1 * 9;
+    float *a2 = a1 + (int64_t)n_chunks * C * h1 * w1;
+    float *a3 = a2 + (int64_t)n_chunks * C * h2 * w2;
+    float *rsh = a3 + (int64_t)n_chunks * C * h3 * w3;
+    // conv1: input (chunk c, ic 0, ih, iw) = mel[ih * frames + f0 + c * chunk + iw]
+    LAUNCHCHK(launch_im2col3x3s2(cols, mel + f0, n_chunks, 1, 128, cw, e->c.chunk_size, 0, frames, h1, w1, st),
+              "im2col1");
+    TRY(egemm(e, cols, 9, e->conv1_w, 9, a1, 0, n_chunks * h1 * w1, C, 9, e->conv1_b, EPI_TRANS | EPI_GELU,
+              (int64_t)C * h1 * w1, h1 * w1));
+    LAUNCHCHK(launch_im2col3x3s2(cols, a1, n_chunks, C, h1, w1, (int64_t)C * h1 * w1, (int64_t)h1 * w1, w1, h2, w2,
+                                 st),
+              "im2col2");
+    TRY(egemm(e, cols, (int64_t)C * 9, e->conv2_w, (int64_t)C * 9, a2, 0, n_chunks * h2 * w2, C, C * 9, e->conv2_b,
+              EPI_TRANS | EPI_GELU, (int64_t)C * h2 * w2, h2 * w2));
+    LAUNCHCHK(launch_im2col3x3s2(cols, a2, n_chunks, C, h2, w2, (int64_t)C * h2 * w2, (int64_t)h2 * w2, w2, h3, w3,
+                                 st),
+              "im2col3");
+    TRY(egemm(e, cols, (int64_t)C * 9, e->conv3_w, (int64_t)C * 9, a3, 0, n_chunks * h3 * w3, C, C * 9, e->conv3_b,
+              EPI_TRANS | EPI_GELU, (int64_t)C * h3 * w3, h3 * w3));
+    LAUNCHCHK(launch_conv_reshape(rsh, a3, n_chunks, C, h3, w3, st), "conv reshape");
+    TRY(egemm(e, rsh, (int64_t)C * h3, e->conv_out_w, (int64_t)C * h3, x, D, n_chunks * w3, D, C * h3, nullptr,
+              EPI_NONE));
+    LAUNCHCHK(launch_add_periodic(x, e->pe, (int64_t)n_chunks * w3, D, w3, st), "pe add");
+    return QASR_OK;
+}
+
+static size_t stem_bytes(const qasr_encoder *e, int n_chunks, int cw) {
+    const int C = e->c.conv_hidden;
+    const int h1 = conv_len(128), w1 = conv_len(cw), h2 = conv_len(h1), w2 = conv_len(w1);
+    const int h3 = conv_len(h2), w3 = conv_len(w2);
+    const int64_t f = (int64_t)n_chunks * h2 * w2 * C * 9 + (int64_t)n_chunks * h1 * w1 * 9 +
+                      (int64_t)n_chunks * C * (h1 * w1 + h2 * w2 + h3 * w3) + (int64_t)n_chunks * w3 * C * h3;
+    return sizeof(float) * f + 1024;
+}
+
+// Encoder::forward on a device mel [128][frames]; out [tokens][output_dim]
+int encoder_forward_dev(qasr_encoder *e, const float *mel, int64_t frames, float *out, int64_t *n_tok) {
+    const qasr_enc_config &c = e->c;
+    hipStream_t st = e->h->stream;
+    const int64_t T = encoder_tokens(e, frames);
+    const int D = c.d_model, F = c.ffn_dim, O = c.output_dim;
+    const int64_t n_full = frames / c.chunk_size;
+    const int tail = (int)(frames % c.chunk_size);
+    size_t stem = std::max(stem_bytes(e, (int)std::max<int64_t>(n_full, 1), c.chunk_size),
+                           tail ? stem_bytes(e, 1, tail) : (size_t)0);
+    const size_t tf = sizeof(float) * (size_t)T;
+    const size_t layer_bytes = tf * (D + 3 * D + D + F) + 4096;
+    const size_t x_bytes = (tf * D + 255) / 256 * 256;
+    TRY(ensure_scratch(e, x_bytes + std::max(stem, layer_bytes)));
+    float *x = reinterpret_cast<float *>(e->scratch);     // residual stream [T][D]
+    char *buf = e->scratch + x_bytes;
+    if (n_full > 0) TRY(conv_stem(e, mel, frames, 0, (int)n_full, c.chunk_size, x, buf));
+    if (tail) TRY(conv_stem(e, mel, frames, n_full * c.chunk_size, 1, tail, x + n_full * e->tokens_per_chunk * D, buf));
+    float *xn = reinterpret_cast<float *>(buf);
+    float *qkv = xn + T * D;
+    float *att = qkv + T * 3 * D;
+    float *mid = att + T * D;
+    const int wsz = e->tokens_per_chunk * (c.n_window_infer / c.chunk_size);
+    const int M = (int)T;
+    for (int l = 0; l < c.n_layers; l++) {
+        const EncLayerDev &L = e->L[l];
+        LAUNCHCHK(launch_layer_norm_rows(xn, x, L.ln1_w, L.ln1_b, T, D, 1e-5f, st), "enc ln1");
+        TRY(egemm(e, xn, D, L.wqkv, D, qkv, 3 * D, M, 3 * D, D, L.bqkv, EPI_NONE));
+        AttnRowsArgs a{};
+        a.q = qkv; a.q_rs = 3 * D;
+        a.k = qkv + D; a.v = qkv + 2 * D; a.k_hs = c.head_dim; a.k_rs = 3 * D;
+        a.out = att; a.o_rs = D;
+        a.n_q = M; a.n_k = M; a.G = 1; a.q_offset = 0; a.window = wsz;
+        a.scale = 1.0f / sqrtf((float)c.head_dim);
+        LAUNCHCHK(launch_attn_rows(a, c.n_heads, c.head_dim, st), "enc attention");
+        TRY(egemm(e, att, D, L.wo, D, x, D, M, D, D, L.bo, EPI_ACCUM));
+        LAUNCHCHK(launch_layer_norm_rows(xn, x, L.ln2_w, L.ln2_b, T, D, 1e-5f, st), "enc ln2");
+        TRY(egemm(e, xn, D, L.fc1, D, mid, F, M, F, D, L.b1, EPI_GELU, (int64_t)T * F));
+        TRY(egemm(e, mid, F, L.fc2, F, x, D, M, D, F, L.b2, EPI_ACCUM));
+    }
+    LAUNCHCHK(launch_layer_norm_rows(xn, x, e->ln_post_w, e->ln_post_b, T, D, 1e-5f, st), "enc ln_post");
+    TRY(egemm(e, xn, D, e->proj1_w, D, att, D, M, D, D, e->proj1_b, EPI_GELU, (int64_t)T * D));
+    TRY(egemm(e, att, D, e->proj2_w, D, out, O, M, O, D, e->proj2_b, EPI_NONE));
+    if (n_tok) *n_tok = T;
+    return QASR_OK;
+}
+
+int64_t mel_frames_for(int64_t n) {
+    const int64_t padded = n + 400;
+    if (padded < 400) return 0;
+    return (padded - 400) / 160;
+}
+
+// mel_spectrogram on device samples; mel [128][frames]
+int mel_dev(qasr_encoder *e, const float *x, int64_t ns, float *mel, float *scratch) {
+    hipStream_t st = e->h->stream;
+    const int nf = (int)mel_frames_for(ns);
+    float *fr = scratch, *re = fr + (int64_t)nf * 400, *im = re + (int64_t)nf * 201;
+    float *pT = im + (int64_t)nf * 201, *bmax = pT + (int64_t)nf * 201;
+    LAUNCHCHK(launch_mel_frames(fr, x, ns, e->window, nf, st), "mel frames");
+    GemmArgs g{};
+    g.M = 201; g.N = nf; g.K = 400;
+    g.A = e->dft_cos; g.lda = 400; g.B = fr; g.ldb = 400; g.C = re; g.ldc = nf;
+    LAUNCHCHK(launch_gemm_f32(g, st), "mel dft");
+    g.A = e->dft_sin; g.C = im;
+    LAUNCHCHK(launch_gemm_f32(g, st), "mel dft");
+    LAUNCHCHK(launch_mel_power(pT, re, im, nf, st), "mel power");
+    g.M = 128; g.N = nf; g.K = 201;
+    g.A = e->filters; g.lda = 201; g.B = pT; g.ldb = 201; g.C = mel; g.ldc = nf;
+    LAUNCHCHK(launch_gemm_f32(g, st), "mel filterbank");
+    LAUNCHCHK(launch_mel_log_norm(mel, (int64_t)128 * nf, bmax, st), "mel log");
+    return QASR_OK;
+}
+
+static size_t mel_scratch_floats(int64_t nf) { return (size_t)nf * (400 + 3 * 201) + (size_t)(128 * nf / 256 + 2); }
+
+extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, float *mel_out, int64_t *frames) {
+    if (!e) return qasr_fail(QASR_ERR_INVALID, "encoder is null");
+    CHECK_H(e->h);
+    if (!samples || n <= 0 || !frames) return qasr_fail(QASR_ERR_INVALID, "mel: bad arguments");
+    const int64_t nf = mel_frames_for(n);
+    if (nf <= 0) return qasr_fail(QASR_ERR_INVALID, "mel: audio too short");
+    *frames = nf;
+    if (!mel_out) return QASR_OK;
+    float *dx = nullptr, *dm = nullptr, *sc = nullptr;
+    HIPCHK(hipMalloc(&dx, sizeof(float) * n));
+    HIPCHK(hipMalloc(&dm, sizeof(float) * 128 * nf));
+    HIPCHK(hipMalloc(&sc, sizeof(float) * mel_scratch_floats(nf)));
+    int rc = QASR_OK;
+    if (hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
+        rc = qasr_fail(QASR_ERR_HIP, "mel: upload failed");
+    if (rc == QASR_OK) rc = mel_dev(e, dx, n, dm, sc);
+    if (rc == QASR_OK &&
+        hipMemcpyAsync(mel_out, dm, sizeof(float) * 128 * nf, hipMemcpyDeviceToHost, e->h->stream) != hipSuccess)
+        rc = qasr_fail(QASR_ERR_HIP, "mel: download failed");
+    (void)hipStreamSynchronize(e->h->stream);
+    (void)hipFree(dx);
+    (void)hipFree(dm);
+    (void)hipFree(sc);
+    return rc;
+}
+
+extern "C" int64_t qasr_hip_encoder_tokens(const qasr_encoder *e, int64_t frames) {
+    return e ? encoder_tokens(e, frames) : -1;
+}
+
+extern "C" int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64_t frames, float *out,
+                                        int64_t *n_tokens) {
+    if (!e) return qasr_fail(QASR_ERR_INVALID, "encoder is null");
+    CHECK_H(e->h);
+    if (!mel || frames <= 0 || !out) return qasr_fail(QASR_ERR_INVALID, "encoder_forward: bad arguments");
+    const int64_t T = encoder_tokens(e, frames);
+    float *dm = nullptr, *dout = nullptr;
+    HIPCHK(hipMalloc(&dm, sizeof(float) * 128 * frames));
+    HIPCHK(hipMalloc(&dout, sizeof(float) * T * e->c.output_dim));
+    int rc = QASR_OK;
+    if (hipMemcpyAsync(dm, mel, sizeof(float) * 128 * frames, hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
+        rc = qasr_fail(QASR_ERR_HIP, "encoder_forward: upload failed");
+    if (rc == QASR_OK) rc = encoder_forward_dev(e, dm, frames, dout, n_tokens);
+    if (rc == QASR_OK && hipMemcpyAsync(out, dout, sizeof(float) * T * e->c.output_dim, hipMemcpyDeviceToHost,
+                                        e->h->stream) != hipSuccess)
+        rc = qasr_fail(QASR_ERR_HIP, "encoder_forward: download failed");
+    (void)hipStreamSynchronize(e->h->stream);
+    (void)hipFree(dm);
+    (void)hipFree(dout);
+    return rc;
+}
+
+// ---------------------------------------------------------------------------
+// offline transcription with a forced number of decode steps
+// ---------------------------------------------------------------------------
+static const int PREFIX_HEAD[] = {151644, 8948, 198};
+static const int PREFIX_TAIL[] = {151645, 198, 151644, 872, 198, 151669};
+static const int SUFFIX_BASE[] = {151670, 151645, 198, 151644, 77091, 198};
+
+extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
+                                          int32_t n_steps, int32_t *tokens_out, double *times_ms) {
+    if (!d || !e) return qasr_fail(QASR_ERR_INVALID, "transcribe: null model");
+    CHECK_H(d->h);
+    if (d->h != e->h) return qasr_fail(QASR_ERR_INVALID, "transcribe: models on different handles");
+    if (!samples || n <= 0 || n_steps <= 0 || !tokens_out) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
+    if (e->c.output_dim != d->c.hidden) return qasr_fail(QASR_ERR_INVALID, "transcribe: encoder/decoder width mismatch");
+    hipStream_t st = d->h->stream;
+    const int64_t nf = mel_frames_for(n);
+    if (nf <= 0) return qasr_fail(QASR_ERR_INVALID, "transcribe: audio too short");
+    const int64_t T = encoder_tokens(e, nf);
+    const int H = d->c.hidden;
+    const int n_head = 9, n_tail = 6;
+    const int64_t total = n_head + T + n_tail;
+    if (total - 1 + n_steps > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "transcribe: KV cache capacity exceeded");
+    for (int t : PREFIX_HEAD) if (t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "transcribe: vocab too small for the prompt");
+    // device buffers for this call
+    float *dx = nullptr, *dmel = nullptr, *msc = nullptr, *enc = nullptr, *emb = nullptr;
+    int *dtok = nullptr;
+    HIPCHK(hipMalloc(&dx, sizeof(float) * n));
+    HIPCHK(hipMalloc(&dmel, sizeof(float) * 128 * nf));
+    HIPCHK(hipMalloc(&msc, sizeof(float) * mel_scratch_floats(nf)));
+    HIPCHK(hipMalloc(&enc, sizeof(float) * T * H));
+    HIPCHK(hipMalloc(&emb, sizeof(float) * total * H));
+    HIPCHK(hipMalloc(&dtok, sizeof(int) * (n_head + n_tail)));
+    int toks[15];
+    for (int i = 0; i < 3; i++) toks[i] = PREFIX_HEAD[i];
+    for (int i = 0; i < 6; i++) toks[3 + i] = PREFIX_TAIL[i];
+    for (int i = 0; i < 6; i++) toks[9 + i] = SUFFIX_BASE[i];
+    hipEvent_t ev[5];
+    for (auto &v : ev) HIPCHK(hipEventCreate(&v));
+    int rc = QASR_OK;
+    HIPCHK(hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(dtok, toks, sizeof(toks), hipMemcpyHostToDevice, st));
+    HIPCHK(hipEventRecord(ev[0], st));
+    rc = mel_dev(e, dx, n, dmel, msc);
+    if (rc == QASR_OK) {
+        HIPCHK(hipEventRecord(ev[1], st));
+        int64_t nt = 0;
+        rc = encoder_forward_dev(e, dmel, nf, enc, &nt);
+    }
+    if (rc == QASR_OK) {
+        HIPCHK(hipEventRecord(ev[2], st));
+        LAUNCHCHK(launch_build_prompt(emb, d->embed, dtok, n_head, enc, (int)T, n_tail, H, st), "prompt");
+        d->len = 0;
+        rc = decoder_prefill_dev(d, emb, total - 1);
+    }
+    if (rc == QASR_OK) {
+        // first token from the last prompt row, then n_steps - 1 graph-replayed steps
+        d->host_state[0] = 0;
+        d->host_state[1] = (int32_t)d->len;
+        d->host_state[2] = 0;
+        d->host_state[3] = 0;
+        HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, st));
+        HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
+        rc = decoder_enqueue_step(d, false);
+    }
+    if (rc == QASR_OK) {
+        HIPCHK(hipEventRecord(ev[3], st));
+        for (int32_t s = 1; s < n_steps && rc == QASR_OK; s++) rc = decoder_run_embed_step(d);
+    }
+    if (rc == QASR_OK) {
+        HIPCHK(hipEventRecord(ev[4], st));
+        HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        d->len += n_steps;
+        if (times_ms) {
+            for (int i = 0; i < 4; i++) {
+                float ms = 0.0f;
+                (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+                times_ms[i] = ms;
+            }
+        }
+    }
+    (void)hipStreamSynchronize(st);
+    for (auto &v : ev) (void)hipEventDestroy(v);
+    for (void *p : {(void *)dx, (void *)dmel, (void *)msc, (void *)enc, (void *)emb, (void *)dtok}) (void)hipFree(p);
+    return rc;
+}

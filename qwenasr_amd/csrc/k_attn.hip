@@ -50,6 +50,7 @@ __device__ __forceinline__ float head_sum128(float v, float *red) {
 // to f32 rounding, not bit for bit.
 // ---------------------------------------------------------------------------
 #define ATT_MAXC 256
+#define ATT_MAXS 64
 
 template <int G, typename KVT>
 __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
@@ -60,6 +61,7 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
     __shared__ float red[8];
     __shared__ float sc[G][ATT_MAXC];
     __shared__ float pv[2][G][D];
+    __shared__ float mw[G][ATT_MAXS], lw[G][ATT_MAXS];
     __shared__ int last;
     const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
     const int n_split = a.n_split;
@@ -198,46 +200,55 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
     float *part = a.part + ((int64_t)kvh * n_split + split) * G * (D + 2);
     {
         const int gi = t / D, d = t % D;
-        part[gi * (D + 2) + 2 + d] = __fadd_rn(pv[0][gi][d], pv[1][gi][d]);
+        st_agent(part + gi * (D + 2) + 2 + d, __fadd_rn(pv[0][gi][d], pv[1][gi][d]));
         if (d == 0) {
-            part[gi * (D + 2)] = n > 0 ? mloc[gi] : -INFINITY;
-            part[gi * (D + 2) + 1] = n > 0 ? lsum[gi] : 0.0f;
+            st_agent(part + gi * (D + 2), n > 0 ? mloc[gi] : -INFINITY);
+            st_agent(part + gi * (D + 2) + 1, n > 0 ? lsum[gi] : 0.0f);
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (t == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + kvh, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        last = (prev == (unsigned)n_split - 1);
+    if (!arrive_last(a.counters + kvh, (unsigned)n_split, &last)) return;
+    // ---- last block of this KV head: log-sum-exp merge of the n_split partials
+    const float *pb = a.part + (int64_t)kvh * n_split * G * (D + 2);
+    for (int i = t; i < n_split * G; i += 256) {
+        const int s = i / G, gi = i % G;
+        mw[gi][s] = ld_agent(pb + (s * G + gi) * (D + 2));
+        lw[gi][s] = ld_agent(pb + (s * G + gi) * (D + 2) + 1);
     }
     __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (t < G) {
+        float M = -INFINITY;
+        for (int s = 0; s < n_split; s++) M = fmaxf(M, mw[t][s]);
+        float lt = 0.0f;
+        for (int s = 0; s < n_split; s++) {
+            const float f = mw[t][s] == -INFINITY ? 0.0f : expf(__fsub_rn(mw[t][s], M));
+            mw[t][s] = f;
+            lt = fmaf(lw[t][s], f, lt);
+        }
+        lw[t][0] = lt;
+    }
+    __syncthreads();
     {
         const int gi = t / D, d = t % D;
-        const float *pb = a.part + (int64_t)kvh * n_split * G * (D + 2) + gi * (D + 2);
-        float M = -INFINITY;
-        for (int s = 0; s < n_split; s++)
-            M = fmaxf(M, __hip_atomic_load(pb + s * G * (D + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-        float lt = 0.0f, ot = 0.0f;
-        for (int s = 0; s < n_split; s++) {
-            const float *ps = pb + s * G * (D + 2);
-            const float ms = __hip_atomic_load(ps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (ms == -INFINITY) continue;
-            const float f = expf(__fsub_rn(ms, M));
-            lt = fmaf(__hip_atomic_load(ps + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, lt);
-            ot = fmaf(__hip_atomic_load(ps + 2 + d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, ot);
+        float ot = 0.0f;
+        for (int s0 = 0; s0 < n_split; s0 += 8) {
+            float ov[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                ov[i] = s0 + i < n_split ? ld_agent(pb + ((s0 + i) * G + gi) * (D + 2) + 2 + d) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (s0 + i < n_split) ot = fmaf(ov[i], mw[gi][s0 + i], ot);
         }
+        const float lt = lw[gi][0];
         a.out[(kvh * G + gi) * D + d] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
     }
-    if (t == 0) a.counters[kvh] = 0u;
+    if (t == 0) reset_counter(a.counters + kvh);
 }
 
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
                               int kv_bf16, hipStream_t st) {
     if (head_dim != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads) return hipErrorInvalidValue;
-    if (a.n_split <= 0) return hipErrorInvalidValue;
+    if (a.n_split <= 0 || a.n_split > ATT_MAXS) return hipErrorInvalidValue;
     const dim3 grid(n_kv_heads * a.n_split);
     if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<2, uint16_t>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((k_attn_decode<2, float>), grid, dim3(256), 0, st, a);
@@ -289,13 +300,14 @@ hipError_t launch_rms_norm_rows(float *out, const float *x, const float *w, int6
 __global__ __launch_bounds__(256) void k_head_norm_rope(float *__restrict__ x, const float *__restrict__ w,
                                                         const float *__restrict__ cos_t,
                                                         const float *__restrict__ sin_t, int64_t seq,
-                                                        int heads, float eps, int do_norm, int do_rope) {
+                                                        int heads, int64_t row_stride, float eps, int do_norm,
+                                                        int do_rope) {
     constexpr int D = 128;
     const int lane = threadIdx.x & 63;
     const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (item >= seq * heads) return;
     const int64_t s = item / heads;
-    float *v = x + item * D;
+    float *v = x + s * row_stride + (item % heads) * D;
     float x1 = v[lane], x2 = v[lane + 64];
     if (do_norm) {
         const float ss = wave_sum_f32(__fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2)));
@@ -313,14 +325,21 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(float *__restrict__ x, c
     v[lane + 64] = x2;
 }
 
+hipError_t launch_head_norm_rope_strided(float *x, int64_t row_stride, const float *w, const float *cos_t,
+                                         const float *sin_t, int64_t seq, int heads, float eps, int do_norm,
+                                         int do_rope, hipStream_t st) {
+    const unsigned blocks = (unsigned)((seq * heads + 3) / 4);
+    hipLaunchKernelGGL(k_head_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, cos_t, sin_t, seq, heads, row_stride,
+                       eps, do_norm, do_rope);
+    return hipGetLastError();
+}
+
 hipError_t launch_head_norm_rope(float *x, const float *w, const float *cos_t, const float *sin_t,
                                  int64_t seq, int heads, int hd, float eps, int do_norm, int do_rope,
                                  hipStream_t st) {
     if (hd != 128) return hipErrorInvalidValue;
-    const unsigned blocks = (unsigned)((seq * heads + 3) / 4);
-    hipLaunchKernelGGL(k_head_norm_rope, dim3(blocks), dim3(256), 0, st, x, w, cos_t, sin_t, seq, heads,
-                       eps, do_norm, do_rope);
-    return hipGetLastError();
+    return launch_head_norm_rope_strided(x, (int64_t)heads * hd, w, cos_t, sin_t, seq, heads, eps, do_norm,
+                                         do_rope, st);
 }
 
 }  // namespace qasr

@@ -1,1 +1,267 @@
+// Dense GEMMs of the prefill, the audio encoder and the mel front end.
+//
+//   C[m, n] (op)= sum_k A[m, k] * B[n, k]          ("NT": both operands K-contiguous)
+//
+// k_gemm_mfma: CDNA4 MFMA (v_mfma_f32_16x16x32_bf16), 64x64 block tile, four
+// waves of 32x32, K-step 32, LDS double buffer.  Operand sources:
+//   A f32, split: A = hi + mid + lo with three bf16 terms (each the RNE rounding
+//                 of the remaining residual), so A*B is formed from exact bf16
+//                 products accumulated in f32 — f32-class accuracy against the
+//                 reference's cblas_sgemm on bf16-valued weights (mod.rs:550-628)
+//   A bf16        activations already in bf16 (the int8 x bf16 GEMM)
+//   B bf16        the reference's weights (exact)
+//   B int8        per-row int8 weights, dequantised exactly to bf16 in LDS; the
+//                 per-row scale is applied in the epilogue
+// k_gemm_f32: plain f32 FMA tiles for the small GEMMs whose operands are both
+// f32 tables (mel DFT and filterbank, audio.rs:339-351).
 #include "kernels.h"
+
+namespace qasr {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf16_round(float v) {
+    return __uint_as_float((uint32_t)f32_to_bf16_rne(v) << 16);
+}
+
+template <int ASRC, int BSRC, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
+    constexpr int BM = 64, BN = 64, BK = 32, LDK = BK + 8;
+    constexpr int NA = ASRC == A_F32_SPLIT ? 3 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t As[2][NA][BM][LDK];
+    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN][LDK];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wid >> 1, wn = wid & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int M = g.M, N = g.N, K = g.K;
+    // global -> register staging: thread t covers row t/4, k-offset (t%4)*8 of the tile
+    const int lr = t >> 2, lk = (t & 3) * 8;
+    const int am = m0 + lr, bn = n0 + lr;
+    float ar[8];
+    u16x8 ab;
+    u16x8 br;
+
+    auto load_tile = [&](int k0) {
+        const int kk = k0 + lk;
+        if (ASRC == A_F32_SPLIT) {
+            const float *ap = reinterpret_cast<const float *>(g.A) + (int64_t)am * g.lda + kk;
+            if (am < M && kk + 8 <= K && g.a_vec4) {
+                const float4 x0 = reinterpret_cast<const float4 *>(ap)[0];
+                const float4 x1 = reinterpret_cast<const float4 *>(ap)[1];
+                ar[0] = x0.x; ar[1] = x0.y; ar[2] = x0.z; ar[3] = x0.w;
+                ar[4] = x1.x; ar[5] = x1.y; ar[6] = x1.z; ar[7] = x1.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float *q = reinterpret_cast<const float *>(g.A) + (int64_t)min(am, M - 1) * g.lda + min(kk + i, K - 1);
+                    ar[i] = (am < M && kk + i < K) ? *q : 0.0f;
+                }
+            }
+        } else {
+            const uint16_t *ap = reinterpret_cast<const uint16_t *>(g.A) + (int64_t)am * g.lda + kk;
+            if (am < M && kk + 8 <= K && g.a_vec4) {
+                ab = *reinterpret_cast<const u16x8 *>(ap);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint16_t *q = reinterpret_cast<const uint16_t *>(g.A) + (int64_t)min(am, M - 1) * g.lda + min(kk + i, K - 1);
+                    ab[i] = (am < M && kk + i < K) ? *q : (uint16_t)0;
+                }
+            }
+        }
+        if (BSRC == B_BF16) {
+            const uint16_t *bp = reinterpret_cast<const uint16_t *>(g.B) + (int64_t)bn * g.ldb + kk;
+            if (bn < N && kk + 8 <= K && g.b_vec) {
+                br = *reinterpret_cast<const u16x8 *>(bp);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint16_t *q = reinterpret_cast<const uint16_t *>(g.B) + (int64_t)min(bn, N - 1) * g.ldb + min(kk + i, K - 1);
+                    br[i] = (bn < N && kk + i < K) ? *q : (uint16_t)0;
+                }
+            }
+        } else {
+            const int8_t *bp = reinterpret_cast<const int8_t *>(g.B) + (int64_t)bn * g.ldb + kk;
+            int8_t q[8];
+            if (bn < N && kk + 8 <= K && g.b_vec) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(bp);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    q[i] = (int8_t)(v.x >> (8 * i));
+                    q[4 + i] = (int8_t)(v.y >> (8 * i));
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const int8_t *qp = reinterpret_cast<const int8_t *>(g.B) + (int64_t)min(bn, N - 1) * g.ldb + min(kk + i, K - 1);
+                    q[i] = (bn < N && kk + i < K) ? *qp : (int8_t)0;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) br[i] = f32_to_bf16_rne((float)q[i]);   // exact, |q| <= 128
+        }
+    };
+    auto store_tile = [&](int buf) {
+        if (ASRC == A_F32_SPLIT) {
+            u16x8 hi, mi, lo;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float x = ar[i];
+                const uint16_t h = f32_to_bf16_rne(x);
+                const float r1 = __fsub_rn(x, __uint_as_float((uint32_t)h << 16));
+                const uint16_t m = f32_to_bf16_rne(r1);
+                const float r2 = __fsub_rn(r1, __uint_as_float((uint32_t)m << 16));
+                hi[i] = h; mi[i] = m; lo[i] = f32_to_bf16_rne(r2);
+            }
+            *reinterpret_cast<u16x8 *>(&As[buf][0][lr][lk]) = hi;
+            *reinterpret_cast<u16x8 *>(&As[buf][1][lr][lk]) = mi;
+            *reinterpret_cast<u16x8 *>(&As[buf][2 % NA][lr][lk]) = lo;
+        } else {
+            *reinterpret_cast<u16x8 *>(&As[buf][0][lr][lk]) = ab;
+        }
+        *reinterpret_cast<u16x8 *>(&Bs[buf][lr][lk]) = br;
+    };
+
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int nk = (K + BK - 1) / BK;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    const int fr = lane & 15, fk = (lane >> 4) * 8;
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < nk) load_tile((kt + 1) * BK);
+        bf16x8 bfrag[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            bfrag[j] = *reinterpret_cast<const bf16x8 *>(&Bs[buf][wn * 32 + j * 16 + fr][fk]);
+#pragma unroll
+        for (int s = NA - 1; s >= 0; s--) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const bf16x8 afrag = *reinterpret_cast<const bf16x8 *>(&As[buf][s][wm * 32 + i * 16 + fr][fk]);
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(afrag, bfrag[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (kt + 1 < nk) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 32 + i * 16 + (lane >> 4) * 4 + r;
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (m >= M || n >= N) continue;
+                float v = acc[i][j][r];
+                // EPI_TRANS: rows are (chunk, spatial) of a batched conv and the
+                // output keeps the reference layout [chunk][channel][spatial]
+                int64_t off, gidx;
+                if (EPI & EPI_TRANS) {
+                    const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
+                    gidx = (int64_t)n * g.gelu_rows + sp;
+                    off = (int64_t)c * g.gelu_n + gidx;
+                } else {
+                    gidx = (int64_t)m * g.ldc + n;
+                    off = gidx;
+                }
+                float *cp = g.C + off;
+                if (EPI & EPI_SCALE) v = __fmul_rn(v, g.scale[n]);
+                if (EPI & EPI_ACCUM) {
+                    float c = *cp;
+                    if (g.bias) c = __fadd_rn(c, g.bias[n]);
+                    v = __fadd_rn(c, v);
+                } else if (g.bias) {
+                    v = __fadd_rn(v, g.bias[n]);
+                }
+                if (EPI & EPI_GELU) v = gelu_ref(v, gidx, g.gelu_n);
+                *cp = v;
+            }
+}
+
+// ---------------------------------------------------------------------------
+// f32 SIMT GEMM (NT), 64x64 tile, 4x4 outputs per thread, K-step 16
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_gemm_f32(GemmArgs g) {
+    __shared__ float As[16][65], Bs[16][65];
+    const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const float *A = reinterpret_cast<const float *>(g.A), *B = reinterpret_cast<const float *>(g.B);
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < g.K; k0 += 16) {
+        for (int i = t; i < 64 * 16; i += 256) {
+            const int r = i >> 4, k = i & 15;
+            const int m = m0 + r, n = n0 + r, kk = k0 + k;
+            const float av = A[(int64_t)min(m, g.M - 1) * g.lda + min(kk, g.K - 1)];
+            const float bv = B[(int64_t)min(n, g.N - 1) * g.ldb + min(kk, g.K - 1)];
+            As[k][r] = (m < g.M && kk < g.K) ? av : 0.0f;
+            Bs[k][r] = (n < g.N && kk < g.K) ? bv : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            float a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) { a[i] = As[k][ty * 4 + i]; b[i] = Bs[k][tx * 4 + i]; }
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+            if (m < g.M && n < g.N) g.C[(int64_t)m * g.ldc + n] = acc[i][j];
+        }
+}
+
+template <int ASRC, int BSRC>
+static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
+    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64);
+    switch (epi) {
+#define QE(E) case E: hipLaunchKernelGGL((k_gemm_mfma<ASRC, BSRC, E>), grid, dim3(256), 0, st, g); break;
+        QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+#undef QE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm(const GemmArgs &g0, int asrc, int bsrc, int epi, hipStream_t st) {
+    GemmArgs g = g0;
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0) return hipErrorInvalidValue;
+    g.a_vec4 = (g.lda % 8 == 0) && ((uintptr_t)g.A % 16 == 0);
+    g.b_vec = (g.ldb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
+    if ((epi & (EPI_GELU | EPI_TRANS)) && g.gelu_rows <= 0 && (epi & EPI_TRANS)) return hipErrorInvalidValue;
+    if (asrc == A_F32_SPLIT && bsrc == B_BF16) return go_gemm<A_F32_SPLIT, B_BF16>(g, epi, st);
+    if (asrc == A_BF16 && bsrc == B_I8) return go_gemm<A_BF16, B_I8>(g, epi, st);
+    if (asrc == A_BF16 && bsrc == B_BF16) return go_gemm<A_BF16, B_BF16>(g, epi, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_f32(const GemmArgs &g, hipStream_t st) {
+    if (g.M <= 0 || g.N <= 0 || g.K <= 0) return hipErrorInvalidValue;
+    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64);
+    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, st, g);
+    return hipGetLastError();
+}
+
+}  // namespace qasr

@@ -53,46 +53,76 @@ __global__ __launch_bounds__(256) void k_pack_int8_rows(const uint16_t *__restri
 // the prologue redundantly (x is a few KiB and sits in L2).
 // ---------------------------------------------------------------------------
 template <int NS, bool NORM, bool EMBED>
-__device__ __forceinline__ void act_prologue(const float *__restrict__ x, const uint16_t *__restrict__ xe,
-                                             const float *__restrict__ norm_w, float eps, int K,
-                                             float *lds_t, int xd[NS][4], float *xs,
-                                             float *__restrict__ resid_out) {
+struct ActIn {
+    float xv[NS][16];
+    float wn[NORM ? NS : 1][16];
+};
+
+// Phase 1: issue the loads of the lane's activation slice (and RMSNorm gains).
+// Called before the weight loads: vmcnt retires loads in issue order, so these
+// small L2-resident reads complete while the weight stream is still in flight.
+template <int NS, bool NORM, bool EMBED>
+__device__ __forceinline__ void act_load(const float *__restrict__ x, const uint16_t *__restrict__ xe,
+                                         const float *__restrict__ norm_w, int K, ActIn<NS, NORM, EMBED> &in,
+                                         float *__restrict__ resid_out) {
     const int lane = threadIdx.x & 63;
     const int nslot = K >> 4;
-    float xv[NS][16];
+    // branch-free: out-of-range slots load slot 0 and are zeroed by a select
 #pragma unroll
     for (int c = 0; c < NS; c++) {
         const int s = lane + 64 * c;
-        if (s < nslot) {
-            if (EMBED) {
-                const uint4 *p = reinterpret_cast<const uint4 *>(xe + 16 * s);
-                uint4 a = p[0], b = p[1];
-                uint32_t wds[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        const bool ok = s < nslot;
+        const int se = ok ? s : 0;
+        if (EMBED) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(xe + 16 * se);
+            const uint4 a = p[0], b = p[1];
+            const uint32_t wds[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    xv[c][2 * i] = __uint_as_float(wds[i] << 16);
-                    xv[c][2 * i + 1] = __uint_as_float(wds[i] & 0xFFFF0000u);
-                }
-            } else {
-                const float4 *p = reinterpret_cast<const float4 *>(x + 16 * s);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float4 v = p[i];
-                    xv[c][4 * i] = v.x; xv[c][4 * i + 1] = v.y;
-                    xv[c][4 * i + 2] = v.z; xv[c][4 * i + 3] = v.w;
-                }
-            }
-            if (resid_out) {
-                float4 *o = reinterpret_cast<float4 *>(resid_out + 16 * s);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    o[i] = make_float4(xv[c][4 * i], xv[c][4 * i + 1], xv[c][4 * i + 2], xv[c][4 * i + 3]);
+            for (int i = 0; i < 8; i++) {
+                in.xv[c][2 * i] = ok ? __uint_as_float(wds[i] << 16) : 0.0f;
+                in.xv[c][2 * i + 1] = ok ? __uint_as_float(wds[i] & 0xFFFF0000u) : 0.0f;
             }
         } else {
+            const float4 *p = reinterpret_cast<const float4 *>(x + 16 * se);
 #pragma unroll
-            for (int r = 0; r < 16; r++) xv[c][r] = 0.0f;
+            for (int i = 0; i < 4; i++) {
+                const float4 v = p[i];
+                in.xv[c][4 * i] = ok ? v.x : 0.0f;
+                in.xv[c][4 * i + 1] = ok ? v.y : 0.0f;
+                in.xv[c][4 * i + 2] = ok ? v.z : 0.0f;
+                in.xv[c][4 * i + 3] = ok ? v.w : 0.0f;
+            }
+        }
+        if (NORM) {
+            const float4 *wp = reinterpret_cast<const float4 *>(norm_w + 16 * se);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = wp[i];
+                in.wn[c][4 * i] = v.x; in.wn[c][4 * i + 1] = v.y;
+                in.wn[c][4 * i + 2] = v.z; in.wn[c][4 * i + 3] = v.w;
+            }
+        }
+        if (resid_out && ok) {
+            float4 *o = reinterpret_cast<float4 *>(resid_out + 16 * s);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                o[i] = make_float4(in.xv[c][4 * i], in.xv[c][4 * i + 1], in.xv[c][4 * i + 2], in.xv[c][4 * i + 3]);
         }
     }
+}
+
+// Phase 2: optional RMSNorm with the reference's exact AVX2 summation order
+// (kernels/avx.rs:377-415: 16 lanes of sequential FMAs over 16-element blocks,
+// then the hsum tree), then the absmax int8 quantization of
+// quantize_f32_to_int8 (kernels/mod.rs:1795-1802).  Lane l owns the 16-element
+// slots s = l + 64 c; the result is its int8 dwords plus the activation scale.
+// Each wave computes this redundantly — x is a few KiB and sits in L2 — so no
+// block barrier is needed.
+template <int NS, bool NORM, bool EMBED>
+__device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
+                                           int xd[NS][4], float *xs) {
+    const int lane = threadIdx.x & 63;
+    const int nslot = K >> 4;
     if (NORM) {
         // transpose through LDS: T[r][s] = x[16 s + r]
 #pragma unroll
@@ -100,7 +130,7 @@ __device__ __forceinline__ void act_prologue(const float *__restrict__ x, const 
             const int s = lane + 64 * c;
             if (s < nslot) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) lds_t[r * nslot + s] = xv[c][r];
+                for (int r = 0; r < 16; r++) lds_t[r * nslot + s] = in.xv[c][r];
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -119,26 +149,15 @@ __device__ __forceinline__ void act_prologue(const float *__restrict__ x, const 
         const float ss = avx16_tree(acc);
         const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
 #pragma unroll
-        for (int c = 0; c < NS; c++) {
-            const int s = lane + 64 * c;
-            if (s < nslot) {
-                const float4 *wp = reinterpret_cast<const float4 *>(norm_w + 16 * s);
+        for (int c = 0; c < NS; c++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float4 wv = wp[i];
-                    xv[c][4 * i] = __fmul_rn(__fmul_rn(xv[c][4 * i], rinv), wv.x);
-                    xv[c][4 * i + 1] = __fmul_rn(__fmul_rn(xv[c][4 * i + 1], rinv), wv.y);
-                    xv[c][4 * i + 2] = __fmul_rn(__fmul_rn(xv[c][4 * i + 2], rinv), wv.z);
-                    xv[c][4 * i + 3] = __fmul_rn(__fmul_rn(xv[c][4 * i + 3], rinv), wv.w);
-                }
-            }
-        }
+            for (int r = 0; r < 16; r++) in.xv[c][r] = __fmul_rn(__fmul_rn(in.xv[c][r], rinv), in.wn[c][r]);
     }
     float m = 0.0f;
 #pragma unroll
     for (int c = 0; c < NS; c++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) m = fmaxf(m, fabsf(xv[c][r]));
+        for (int r = 0; r < 16; r++) m = fmaxf(m, fabsf(in.xv[c][r]));
     m = wave_max_f32(m);
     float scale, inv;
     act_scales(m, &scale, &inv);
@@ -147,10 +166,10 @@ __device__ __forceinline__ void act_prologue(const float *__restrict__ x, const 
     for (int c = 0; c < NS; c++)
 #pragma unroll
         for (int d = 0; d < 4; d++)
-            xd[c][d] = pack4_i8(round_clamp_i8(__fmul_rn(xv[c][4 * d], inv)),
-                                round_clamp_i8(__fmul_rn(xv[c][4 * d + 1], inv)),
-                                round_clamp_i8(__fmul_rn(xv[c][4 * d + 2], inv)),
-                                round_clamp_i8(__fmul_rn(xv[c][4 * d + 3], inv)));
+            xd[c][d] = pack4_i8(round_clamp_i8(__fmul_rn(in.xv[c][4 * d], inv)),
+                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 1], inv)),
+                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 2], inv)),
+                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 3], inv)));
 }
 
 __device__ __forceinline__ int dot16(const i32x4 w, const int xd[4], int acc) {
@@ -174,34 +193,38 @@ __device__ __forceinline__ int dot16(const i32x4 w, const int xd[4], int acc) {
 template <int NS, int R, int MODE, bool NORM, bool EMBED>
 __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
     __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = (blockIdx.x * 4 + wid) * R;
     if (row0 >= a.n_total) return;
     const int K = a.K, nslot = K >> 4;
-    // segment of this wave (segments are multiples of R rows)
-    int seg = 0, base = 0;
-    if (row0 >= a.seg[0].n) { seg = 1; base = a.seg[0].n; }
-    if (seg == 1 && row0 >= base + a.seg[1].n) { seg = 2; base += a.seg[1].n; }
-    const MvSeg S = a.seg[seg];
-    const int lrow0 = row0 - base;
+    // segment of this wave (segments are multiples of R rows); scalar selects
+    // keep the segment fields in SGPRs
+    const int n0 = a.seg[0].n, n1 = a.seg[1].n;
+    const bool in0 = row0 < n0, in1 = !in0 && row0 < n0 + n1;
+    MvSeg S;
+    S.w = in0 ? a.seg[0].w : (in1 ? a.seg[1].w : a.seg[2].w);
+    S.ws = in0 ? a.seg[0].ws : (in1 ? a.seg[1].ws : a.seg[2].ws);
+    S.y = in0 ? a.seg[0].y : (in1 ? a.seg[1].y : a.seg[2].y);
+    const int lrow0 = row0 - (in0 ? 0 : (in1 ? n0 : n0 + n1));
+    const uint16_t *xe = nullptr;
+    if (EMBED) xe = a.embed + (int64_t)a.state[0] * K;
+    float *resid = (EMBED && blockIdx.x == 0 && wid == 0) ? a.resid_out : nullptr;
+    ActIn<NS, NORM, EMBED> in;
+    act_load<NS, NORM, EMBED>(a.x, xe, a.norm_w, K, in, resid);
     i32x4 wv[R][NS];
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int c = 0; c < NS; c++) {
             const int s = lane + 64 * c;
-            if (s < nslot)
-                wv[r][c] = __builtin_nontemporal_load(
-                    reinterpret_cast<const i32x4 *>(S.w + (int64_t)(lrow0 + r) * K) + s);
-            else
-                wv[r][c] = i32x4{0, 0, 0, 0};
+            const i32x4 v = __builtin_nontemporal_load(
+                reinterpret_cast<const i32x4 *>(S.w + (int64_t)(lrow0 + r) * K) + (s < nslot ? s : 0));
+            wv[r][c] = s < nslot ? v : i32x4{0, 0, 0, 0};
         }
-    const uint16_t *xe = nullptr;
-    if (EMBED) xe = a.embed + (int64_t)a.state[0] * K;
-    float *resid = (EMBED && blockIdx.x == 0 && wid == 0) ? a.resid_out : nullptr;
     int xd[NS][4];
     float xs;
-    act_prologue<NS, NORM, EMBED>(a.x, xe, a.norm_w, a.eps, K, lds + wid * NS * 1024, xd, &xs, resid);
+    act_finish<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
     int acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -253,7 +276,8 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
     __shared__ float bvals[4];
     __shared__ int bidx[4];
     __shared__ int last;
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslot = K >> 4;
     const int n_groups = (a.N + R - 1) / R;
     const int gw = blockIdx.x * 4 + wid, n_waves = gridDim.x * 4;
@@ -270,17 +294,17 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
 #pragma unroll
             for (int c = 0; c < NS; c++) {
                 const int s = lane + 64 * c;
-                if (row < a.N && s < nslot)
-                    wv[r][c] = __builtin_nontemporal_load(
-                        reinterpret_cast<const i32x4 *>(a.w + (int64_t)row * K) + s);
-                else
-                    wv[r][c] = i32x4{0, 0, 0, 0};
+                const bool ok = row < a.N && s < nslot;
+                const i32x4 v = __builtin_nontemporal_load(
+                    reinterpret_cast<const i32x4 *>(a.w + (int64_t)(row < a.N ? row : 0) * K) + (s < nslot ? s : 0));
+                wv[r][c] = ok ? v : i32x4{0, 0, 0, 0};
             }
         }
     };
+    ActIn<NS, NORM, false> in;
+    act_load<NS, NORM, false>(a.x, nullptr, a.norm_w, K, in, nullptr);
     if (g < n_groups) load_group(g);
-    act_prologue<NS, NORM, false>(a.x, nullptr, a.norm_w, a.eps, K, lds + wid * NS * 1024, xd, &xs,
-                                  nullptr);
+    act_finish<NS, NORM, false>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
     for (; g < n_groups; g += n_waves) {
         int acc[R];
 #pragma unroll
@@ -309,23 +333,17 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
         int bi = bidx[0];
         for (int w = 1; w < 4; w++)
             if (better(bvals[w], bidx[w], bv, bi)) { bv = bvals[w]; bi = bidx[w]; }
-        a.part_val[blockIdx.x] = bv;
-        a.part_idx[blockIdx.x] = bi;
-        __threadfence();
-        const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-        last = (prev == gridDim.x - 1);
+        st_agent(a.part_val + blockIdx.x, bv);
+        st_agent(a.part_idx + blockIdx.x, bi);
     }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
+    if (!arrive_last(a.counter, gridDim.x, &last)) return;
     // final merge by one wave
     if (wid == 0) {
         float bv = -1e30f;
         int bi = -1;
         for (int b = lane; b < (int)gridDim.x; b += 64) {
-            const float v = __hip_atomic_load(a.part_val + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const int i = __hip_atomic_load(a.part_idx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const float v = ld_agent(a.part_val + b);
+            const int i = ld_agent(a.part_idx + b);
             if (better(v, i, bv, bi)) { bv = v; bi = i; }
         }
 #pragma unroll
@@ -343,7 +361,7 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
                 if (a.token_log) a.token_log[a.state[2]] = tok;
                 a.state[2] += 1;
             }
-            *a.counter = 0u;
+            reset_counter(a.counter);
         }
     }
 }

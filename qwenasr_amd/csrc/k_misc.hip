@@ -1,1 +1,409 @@
+// Row-wise and element-wise kernels of the prefill, the audio encoder and the
+// mel front end, plus the multi-row (prefill / encoder-window) attention.
 #include "kernels.h"
+
+namespace qasr {
+
+// ---------------------------------------------------------------------------
+// LayerNorm rows: avx::layer_norm_row (avx.rs:420-481) in its exact order —
+// mean over 2x8 lane accumulators, variance with FMA accumulators, both
+// through the hsum tree, then fma((x - mean) * inv, w, b).  One wave per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_layer_norm_rows(float *__restrict__ out, const float *__restrict__ x,
+                                                         const float *__restrict__ w, const float *__restrict__ b,
+                                                         int64_t seq, int H, float eps) {
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row = (int64_t)blockIdx.x * 4 + wid;
+    if (row >= seq) return;
+    const float *xr = x + row * H;
+    float *o = out + row * H;
+    const int nslot = H >> 4;
+    float *T = lds + wid * H;
+    for (int s = lane; s < nslot; s += 64)
+        for (int r = 0; r < 16; r++) T[r * nslot + s] = xr[16 * s + r];
+    __builtin_amdgcn_wave_barrier();
+    float acc = 0.0f;
+    if (lane < 16)
+        for (int i = 0; i < nslot; i++) acc = __fadd_rn(acc, T[lane * nslot + i]);
+    const float mean = __fdiv_rn(avx16_tree(acc), (float)H);
+    acc = 0.0f;
+    if (lane < 16)
+        for (int i = 0; i < nslot; i++) {
+            const float d = __fsub_rn(T[lane * nslot + i], mean);
+            acc = fmaf(d, d, acc);
+        }
+    const float var = avx16_tree(acc);
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(var, (float)H), eps)));
+    const int nv = H - H % 8;
+    for (int i = lane; i < H; i += 64)
+        o[i] = i < nv ? fmaf(__fmul_rn(__fsub_rn(xr[i], mean), inv), w[i], b[i])
+                      : __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xr[i], mean), inv), w[i]), b[i]);
+}
+
+hipError_t launch_layer_norm_rows(float *out, const float *x, const float *w, const float *b, int64_t seq,
+                                  int hidden, float eps, hipStream_t st) {
+    if (hidden % 16 != 0 || hidden > 4096 || seq <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_layer_norm_rows, dim3((unsigned)((seq + 3) / 4)), dim3(256), 4 * hidden * sizeof(float), st,
+                       out, x, w, b, seq, hidden, eps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU over rows of interleaved gate/up (swiglu_multiply, mod.rs:1291-1341 ->
+// avx::swiglu_interleaved, avx.rs:568-599): fast_exp on 8-wide blocks, libm
+// expf on the tail.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_swiglu_rows(float *__restrict__ out, const float *__restrict__ gu,
+                                                     int64_t seq, int inter) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= seq * inter) return;
+    const int64_t s = i / inter;
+    const int j = (int)(i % inter);
+    const float g = gu[s * 2 * inter + 2 * j], u = gu[s * 2 * inter + 2 * j + 1];
+    const int nv = inter - inter % 8;
+    const float e = j < nv ? fast_exp_ref(__fsub_rn(0.0f, g)) : expf(-g);
+    out[i] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, e)), u);
+}
+
+hipError_t launch_swiglu_rows(float *out, const float *gu, int64_t seq, int inter, hipStream_t st) {
+    const int64_t n = seq * inter;
+    hipLaunchKernelGGL(k_swiglu_rows, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, gu, seq, inter);
+    return hipGetLastError();
+}
+
+// gelu in place over a buffer of n elements (gelu, mod.rs:1250-1289)
+__global__ __launch_bounds__(256) void k_gelu(float *__restrict__ x, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) x[i] = gelu_ref(x[i], i, n);
+}
+
+hipError_t launch_gelu(float *x, int64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_gelu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n);
+    return hipGetLastError();
+}
+
+// y[r][c] += table[r % period][c]  (add_inplace of the per-chunk sinusoidal PE)
+__global__ __launch_bounds__(256) void k_add_periodic(float *__restrict__ y, const float *__restrict__ table,
+                                                      int64_t rows, int cols, int period) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * cols) return;
+    const int64_t r = i / cols;
+    const int c = (int)(i % cols);
+    y[i] = __fadd_rn(y[i], table[(r % period) * cols + c]);
+}
+
+hipError_t launch_add_periodic(float *y, const float *table, int64_t rows, int cols, int period, hipStream_t st) {
+    const int64_t n = rows * cols;
+    hipLaunchKernelGGL(k_add_periodic, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, y, table, rows, cols, period);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// im2col for a batch of independent 3x3 / stride-2 / pad-1 convolutions
+// (conv2d, mod.rs:1077-1154), transposed: cols[(c * Ho + oh) * Wo + ow][p] with
+// p = (ic * 3 + ki) * 3 + kj.  Input element (c, ic, ih, iw) lives at
+//   in + c * cs + ic * chs + ih * rs + iw.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_im2col3x3s2(float *__restrict__ cols, const float *__restrict__ in,
+                                                     int n_chunks, int C, int H, int W, int64_t cs, int64_t chs,
+                                                     int64_t rs, int Ho, int Wo) {
+    const int P = C * 9;
+    const int64_t total = (int64_t)n_chunks * Ho * Wo * P;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int p = (int)(i % P);
+        const int64_t row = i / P;
+        const int ow = (int)(row % Wo);
+        const int oh = (int)((row / Wo) % Ho);
+        const int c = (int)(row / ((int64_t)Wo * Ho));
+        const int ic = p / 9, ki = (p % 9) / 3, kj = p % 3;
+        const int ih = oh * 2 + ki - 1, iw = ow * 2 + kj - 1;
+        float v = 0.0f;
+        if (ih >= 0 && ih < H && iw >= 0 && iw < W) v = in[c * cs + ic * chs + (int64_t)ih * rs + iw];
+        cols[i] = v;
+    }
+}
+
+hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C, int H, int W, int64_t cs,
+                              int64_t chs, int64_t rs, int Ho, int Wo, hipStream_t st) {
+    const int64_t total = (int64_t)n_chunks * Ho * Wo * C * 9;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_im2col3x3s2, dim3(blocks), dim3(256), 0, st, cols, in, n_chunks, C, H, W, cs, chs, rs,
+                       Ho, Wo);
+    return hipGetLastError();
+}
+
+// [chunk][C][F][T] -> [chunk * T][C * F] with column ch * F + f (encoder.rs:265-277)
+__global__ __launch_bounds__(256) void k_conv_reshape(float *__restrict__ out, const float *__restrict__ in,
+                                                      int n_chunks, int C, int F, int T) {
+    const int64_t total = (int64_t)n_chunks * C * F * T;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int col = (int)(i % (C * F));
+        const int64_t row = i / (C * F);
+        const int t = (int)(row % T);
+        const int c = (int)(row / T);
+        const int ch = col / F, f = col % F;
+        out[i] = in[(((int64_t)c * C + ch) * F + f) * T + t];
+    }
+}
+
+hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C, int F, int T, hipStream_t st) {
+    const int64_t total = (int64_t)n_chunks * C * F * T;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_conv_reshape, dim3(blocks), dim3(256), 0, st, out, in, n_chunks, C, F, T);
+    return hipGetLastError();
+}
+
+// copy K (after norm + RoPE) and V rows of a prefill into the cache (decoder.rs:511-514)
+__global__ __launch_bounds__(256) void k_kv_scatter(const float *__restrict__ qkv, int64_t qkv_rs, int k_off,
+                                                    int v_off, float *__restrict__ kc, float *__restrict__ vc,
+                                                    int64_t head_stride, int start, int64_t S, int Hkv) {
+    const int64_t total = S * Hkv * 128;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int d = (int)(i % 128);
+    const int h = (int)((i / 128) % Hkv);
+    const int64_t s = i / (128 * Hkv);
+    const int64_t dst = h * head_stride + (start + s) * 128 + d;
+    kc[dst] = qkv[s * qkv_rs + k_off + h * 128 + d];
+    vc[dst] = qkv[s * qkv_rs + v_off + h * 128 + d];
+}
+
+hipError_t launch_kv_scatter(const float *qkv, int64_t qkv_rs, int k_off, int v_off, float *kc, float *vc,
+                             int64_t head_stride, int start, int64_t S, int Hkv, hipStream_t st) {
+    const int64_t n = S * Hkv * 128;
+    hipLaunchKernelGGL(k_kv_scatter, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, qkv, qkv_rs, k_off, v_off,
+                       kc, vc, head_stride, start, S, Hkv);
+    return hipGetLastError();
+}
+
+// prompt rows: row r < n_tok_head: embed[tok[r]]; then n_mid rows copied from
+// mid; then the remaining token rows (transcribe.rs:106-169)
+__global__ __launch_bounds__(256) void k_build_prompt(float *__restrict__ out, const uint16_t *__restrict__ embed,
+                                                      const int *__restrict__ toks, int n_head, const float *mid,
+                                                      int n_mid, int n_tail, int H) {
+    const int r = blockIdx.x;
+    float *o = out + (int64_t)r * H;
+    if (r < n_head || r >= n_head + n_mid) {
+        const int ti = r < n_head ? r : r - n_mid;
+        const uint16_t *e = embed + (int64_t)toks[ti] * H;
+        for (int i = threadIdx.x; i < H; i += 256) o[i] = bf16_to_f32(e[i]);
+    } else {
+        const float *m = mid + (int64_t)(r - n_head) * H;
+        for (int i = threadIdx.x; i < H; i += 256) o[i] = m[i];
+    }
+    (void)n_tail;
+}
+
+hipError_t launch_build_prompt(float *out, const uint16_t *embed, const int *toks, int n_head, const float *mid,
+                               int n_mid, int n_tail, int H, hipStream_t st) {
+    hipLaunchKernelGGL(k_build_prompt, dim3(n_head + n_mid + n_tail), dim3(256), 0, st, out, embed, toks, n_head,
+                       mid, n_mid, n_tail, H);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Multi-row attention (flash-style online softmax, f32):
+//   decoder prefill: causal over the KV cache, GQA (causal_attention with
+//                    seq_q > 1, mod.rs:1539-1607)
+//   encoder:         full attention inside fixed windows (bidirectional_attention,
+//                    mod.rs:1386-1471)
+// A block owns 32 query rows (QT queries x G heads of one KV head) and walks key
+// tiles of 32; 8 threads per row.
+// ---------------------------------------------------------------------------
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
+    constexpr int R = 32, KT = 32, DP = HD / 8;
+    __shared__ float Qs[R][HD + 4];
+    __shared__ float Ks[KT][HD + 4];
+    __shared__ float Vs[KT][HD + 4];
+    __shared__ float Ps[R][KT + 1];
+    const int t = threadIdx.x, r = t >> 3, sub = t & 7;
+    const int G = a.G, QT = R / G;
+    const int kvh = blockIdx.x, q0 = blockIdx.y * QT;
+    const int qi = q0 + r / G, h = kvh * G + r % G;
+    const bool row_ok = qi < a.n_q;
+    // key range of this row
+    int lo = 0, hi;
+    if (a.window > 0) {
+        lo = (qi / a.window) * a.window;
+        hi = min(lo + a.window, a.n_k);
+    } else {
+        hi = min(a.q_offset + qi + 1, a.n_k);
+    }
+    if (!row_ok) { lo = 0; hi = 0; }
+    // key range of the block
+    const int qlast = min(q0 + QT, a.n_q) - 1;
+    int blo, bhi;
+    if (a.window > 0) {
+        blo = (q0 / a.window) * a.window;
+        bhi = min((qlast / a.window) * a.window + a.window, a.n_k);
+    } else {
+        blo = 0;
+        bhi = min(a.q_offset + qlast + 1, a.n_k);
+    }
+    for (int i = t; i < R * HD; i += 256) {
+        const int rr = i / HD, d = i % HD;
+        const int qq = q0 + rr / G, hh = kvh * G + rr % G;
+        Qs[rr][d] = qq < a.n_q ? a.q[(int64_t)qq * a.q_rs + hh * HD + d] : 0.0f;
+    }
+    float m = -INFINITY, l = 0.0f, o[DP];
+#pragma unroll
+    for (int i = 0; i < DP; i++) o[i] = 0.0f;
+    const float *kb = a.k + (int64_t)kvh * a.k_hs, *vb = a.v + (int64_t)kvh * a.k_hs;
+    for (int j0 = blo; j0 < bhi; j0 += KT) {
+        __syncthreads();
+        for (int i = t; i < KT * HD; i += 256) {
+            const int kk = i / HD, d = i % HD;
+            const int j = j0 + kk;
+            const bool ok = j < bhi;
+            const int64_t off = (int64_t)(ok ? j : j0) * a.k_rs + d;
+            const float kv = kb[off], vv = vb[off];
+            Ks[kk][d] = ok ? kv : 0.0f;
+            Vs[kk][d] = ok ? vv : 0.0f;
+        }
+        __syncthreads();
+        float s[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int kk = sub * 4 + c;
+            float acc = 0.0f;
+#pragma unroll 8
+            for (int d = 0; d < HD; d++) acc = fmaf(Qs[r][d], Ks[kk][d], acc);
+            const int j = j0 + kk;
+            s[c] = (j >= lo && j < hi) ? __fmul_rn(acc, a.scale) : -INFINITY;
+        }
+        float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        tm = fmaxf(tm, __shfl_xor(tm, 1, 64));
+        tm = fmaxf(tm, __shfl_xor(tm, 2, 64));
+        tm = fmaxf(tm, __shfl_xor(tm, 4, 64));
+        const float mn = fmaxf(m, tm);
+        float corr = 1.0f, ps = 0.0f;
+        if (mn != -INFINITY) {
+            corr = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, mn));
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                s[c] = s[c] == -INFINITY ? 0.0f : expf(__fsub_rn(s[c], mn));
+                ps = __fadd_rn(ps, s[c]);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; c++) s[c] = 0.0f;
+        }
+        ps = __fadd_rn(ps, __shfl_xor(ps, 1, 64));
+        ps = __fadd_rn(ps, __shfl_xor(ps, 2, 64));
+        ps = __fadd_rn(ps, __shfl_xor(ps, 4, 64));
+        l = fmaf(l, corr, ps);
+        m = mn;
+#pragma unroll
+        for (int c = 0; c < 4; c++) Ps[r][sub * 4 + c] = s[c];
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < DP; i++) o[i] = __fmul_rn(o[i], corr);
+        for (int kk = 0; kk < KT; kk++) {
+            const float p = Ps[r][kk];
+#pragma unroll
+            for (int i = 0; i < DP; i++) o[i] = fmaf(p, Vs[kk][sub * DP + i], o[i]);
+        }
+    }
+    if (row_ok) {
+        float *op = a.out + (int64_t)qi * a.o_rs + h * HD + sub * DP;
+        const float inv = l > 0.0f ? __fdiv_rn(1.0f, l) : 0.0f;
+#pragma unroll
+        for (int i = 0; i < DP; i++) op[i] = __fmul_rn(o[i], inv);
+    }
+}
+
+hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st) {
+    if (a.G <= 0 || 32 % a.G != 0 || a.n_q <= 0) return hipErrorInvalidValue;
+    const dim3 grid(n_kv_heads, (a.n_q + 32 / a.G - 1) / (32 / a.G));
+    if (head_dim == 128) hipLaunchKernelGGL(k_attn_rows<128>, grid, dim3(256), 0, st, a);
+    else if (head_dim == 64) hipLaunchKernelGGL(k_attn_rows<64>, grid, dim3(256), 0, st, a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// mel pieces (audio.rs:273-372)
+// ---------------------------------------------------------------------------
+// frames[t][n] = padded[t * 160 + n] * window[n], reflect padding of 200
+__global__ __launch_bounds__(256) void k_mel_frames(float *__restrict__ fr, const float *__restrict__ x, int64_t ns,
+                                                    const float *__restrict__ window, int nf) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)nf * 400) return;
+    const int n = (int)(i % 400);
+    const int64_t t = i / 400;
+    const int64_t p = t * 160 + n;          // index into the padded signal
+    float v;
+    if (p < 200) {
+        const int64_t s = 200 - p;
+        v = s < ns ? x[s] : 0.0f;
+    } else if (p < 200 + ns) {
+        v = x[p - 200];
+    } else {
+        const int64_t s = ns - 2 - (p - 200 - ns);
+        v = s >= 0 ? x[s] : 0.0f;
+    }
+    fr[i] = __fmul_rn(v, window[n]);
+}
+
+// powT[t][k] = re^2 + im^2 from re/im [k][t]
+__global__ __launch_bounds__(256) void k_mel_power(float *__restrict__ pT, const float *__restrict__ re,
+                                                   const float *__restrict__ im, int nf) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)nf * 201) return;
+    const int k = (int)(i % 201);
+    const int64_t t = i / 201;
+    const float r = re[k * (int64_t)nf + t], m = im[k * (int64_t)nf + t];
+    pT[i] = __fadd_rn(__fmul_rn(r, r), __fmul_rn(m, m));
+}
+
+// log10(max(v, 1e-10)) in place and per-block maxima
+__global__ __launch_bounds__(256) void k_mel_log(float *__restrict__ mel, int64_t n, float *__restrict__ bmax) {
+    __shared__ float red[4];
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    float v = -1e30f;
+    if (i < n) {
+        v = log10f(fmaxf(mel[i], 1e-10f));
+        mel[i] = v;
+    }
+    v = wave_max_f32(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) bmax[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__global__ __launch_bounds__(256) void k_mel_norm(float *__restrict__ mel, int64_t n, const float *__restrict__ bmax,
+                                                  int nb) {
+    __shared__ float gm;
+    if (threadIdx.x < 64) {
+        float v = -1e30f;
+        for (int b = threadIdx.x; b < nb; b += 64) v = fmaxf(v, bmax[b]);
+        v = wave_max_f32(v);
+        if (threadIdx.x == 0) gm = v;
+    }
+    __syncthreads();
+    const float mn = __fsub_rn(gm, 8.0f);
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        mel[i] = __fdiv_rn(__fadd_rn(fmaxf(mel[i], mn), 4.0f), 4.0f);
+}
+
+hipError_t launch_mel_frames(float *fr, const float *x, int64_t ns, const float *window, int nf, hipStream_t st) {
+    const int64_t n = (int64_t)nf * 400;
+    hipLaunchKernelGGL(k_mel_frames, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, fr, x, ns, window, nf);
+    return hipGetLastError();
+}
+hipError_t launch_mel_power(float *pT, const float *re, const float *im, int nf, hipStream_t st) {
+    const int64_t n = (int64_t)nf * 201;
+    hipLaunchKernelGGL(k_mel_power, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, pT, re, im, nf);
+    return hipGetLastError();
+}
+hipError_t launch_mel_log_norm(float *mel, int64_t n, float *bmax, hipStream_t st) {
+    const int nb = (int)((n + 255) / 256);
+    hipLaunchKernelGGL(k_mel_log, dim3(nb), dim3(256), 0, st, mel, n, bmax);
+    hipLaunchKernelGGL(k_mel_norm, dim3(std::min(nb, 1024)), dim3(256), 0, st, mel, n, bmax, nb);
+    return hipGetLastError();
+}
+
+}  // namespace qasr

@@ -82,3 +82,64 @@ hipError_t launch_head_norm_rope(float *x, const float *w, const float *cos_t, c
                                  int do_rope, hipStream_t st);
 
 }  // namespace qasr
+
+namespace qasr {
+// ---- GEMM ----------------------------------------------------------------
+enum { A_F32_SPLIT = 0, A_BF16 = 1 };
+enum { B_BF16 = 0, B_I8 = 1 };
+enum { EPI_NONE = 0, EPI_ACCUM = 1, EPI_SCALE = 2, EPI_GELU = 4, EPI_TRANS = 8 };
+
+struct GemmArgs {
+    int M, N, K;
+    const void *A;            // [M, lda]  f32 or bf16
+    int64_t lda;
+    const void *B;            // [N, ldb]  bf16 or int8
+    int64_t ldb;
+    float *C;                 // [M, ldc]  (EPI_TRANS: [M / gelu_rows][N][gelu_rows])
+    int64_t ldc;
+    const float *bias;        // [N] or null: C = acc + bias (EPI_ACCUM: C = (C + bias) + acc)
+    const float *scale;       // [N] (EPI_SCALE)
+    int64_t gelu_n;           // elements of the buffer gelu() sees (EPI_GELU / EPI_TRANS: per chunk)
+    int gelu_rows;            // EPI_TRANS: spatial positions per chunk
+    int a_vec4, b_vec;        // set by the launcher
+};
+
+hipError_t launch_gemm(const GemmArgs &g, int asrc, int bsrc, int epi, hipStream_t st);
+hipError_t launch_gemm_f32(const GemmArgs &g, hipStream_t st);
+}  // namespace qasr
+
+namespace qasr {
+// ---- prefill / encoder / mel ------------------------------------------------
+struct AttnRowsArgs {
+    const float *q;           // row i, head h at q + i * q_rs + h * hd
+    int64_t q_rs;
+    const float *k, *v;       // kv head g, position j at k + g * k_hs + j * k_rs
+    int64_t k_hs, k_rs;
+    float *out;               // row i, head h at out + i * o_rs + h * hd
+    int64_t o_rs;
+    int n_q, n_k;             // query rows; key positions available
+    int G;                    // query heads per KV head (32 % G == 0)
+    int q_offset;             // causal: query i sees keys [0, q_offset + i]
+    int window;               // > 0: query i sees its window [w*window, min((w+1)*window, n_k))
+    float scale;
+};
+hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st);
+hipError_t launch_layer_norm_rows(float *out, const float *x, const float *w, const float *b, int64_t seq,
+                                  int hidden, float eps, hipStream_t st);
+hipError_t launch_swiglu_rows(float *out, const float *gu, int64_t seq, int inter, hipStream_t st);
+hipError_t launch_gelu(float *x, int64_t n, hipStream_t st);
+hipError_t launch_add_periodic(float *y, const float *table, int64_t rows, int cols, int period, hipStream_t st);
+hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C, int H, int W, int64_t cs,
+                              int64_t chs, int64_t rs, int Ho, int Wo, hipStream_t st);
+hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C, int F, int T, hipStream_t st);
+hipError_t launch_kv_scatter(const float *qkv, int64_t qkv_rs, int k_off, int v_off, float *kc, float *vc,
+                             int64_t head_stride, int start, int64_t S, int Hkv, hipStream_t st);
+hipError_t launch_build_prompt(float *out, const uint16_t *embed, const int *toks, int n_head, const float *mid,
+                               int n_mid, int n_tail, int H, hipStream_t st);
+hipError_t launch_mel_frames(float *fr, const float *x, int64_t ns, const float *window, int nf, hipStream_t st);
+hipError_t launch_mel_power(float *pT, const float *re, const float *im, int nf, hipStream_t st);
+hipError_t launch_mel_log_norm(float *mel, int64_t n, float *bmax, hipStream_t st);
+hipError_t launch_head_norm_rope_strided(float *x, int64_t row_stride, const float *w, const float *cos_t,
+                                         const float *sin_t, int64_t seq, int heads, float eps, int do_norm,
+                                         int do_rope, hipStream_t st);
+}  // namespace qasr

@@ -1,5 +1,12 @@
-// decoder_prefill (decoder.rs:455-547) on the device.
+// decoder_prefill (decoder.rs:455-547) on the device: f32-class MFMA GEMMs on
+// the bf16 weights (as the reference's cblas_sgemm on bf16->f32 weights),
+// exact-order RMSNorm rows, per-head norm + RoPE, KV scatter, causal GQA
+// attention and the AVX-order SwiGLU.
+#include <cmath>
+
 #include "decoder.h"
+
+using namespace qasr;
 
 void decoder_free_prefill(qasr_decoder *d) {
     PrefillBufs &p = d->pf;
@@ -8,9 +15,108 @@ void decoder_free_prefill(qasr_decoder *d) {
     p = PrefillBufs{};
 }
 
+static int ensure_prefill(qasr_decoder *d, int64_t S) {
+    if (S <= d->pf.cap) return QASR_OK;
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    decoder_free_prefill(d);
+    const qasr_dec_config &c = d->c;
+    const int64_t H = c.hidden, qd = (int64_t)c.n_heads * c.head_dim, kvd = (int64_t)c.n_kv_heads * c.head_dim;
+    const int64_t I = c.intermediate, cap = std::max<int64_t>(64, S);
+    PrefillBufs &p = d->pf;
+    struct { float **ptr; int64_t n; } bufs[] = {
+        {&p.x, cap * H}, {&p.xn, cap * H}, {&p.qkv, cap * (qd + 2 * kvd)}, {&p.att, cap * qd},
+        {&p.gu, cap * 2 * I}, {&p.g, cap * I}};
+    for (auto &b : bufs) {
+        hipError_t e = hipMalloc(b.ptr, sizeof(float) * b.n);
+        if (e != hipSuccess) {
+            decoder_free_prefill(d);
+            return qasr_fail(QASR_ERR_NOMEM, "decoder_prefill: buffer allocation failed");
+        }
+    }
+    p.cap = cap;
+    return QASR_OK;
+}
+
+static int gemm(qasr_decoder *d, const float *A, int64_t lda, const uint16_t *B, int64_t ldb, float *C,
+                int64_t ldc, int M, int N, int K, int epi) {
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
+    LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, epi, d->h->stream), "prefill gemm");
+    return QASR_OK;
+}
+
+#define TRY(x)                  \
+    do {                        \
+        int rc_ = (x);          \
+        if (rc_ != QASR_OK) {   \
+            return rc_;         \
+        }                       \
+    } while (0)
+
+int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S) {
+    const qasr_dec_config &c = d->c;
+    if (S <= 0) return QASR_OK;
+    if (d->kv_bf16) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: needs an f32 KV cache");
+    const int64_t start = d->len;
+    if (start + S > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: KV cache capacity exceeded");
+    TRY(ensure_prefill(d, S));
+    hipStream_t st = d->h->stream;
+    PrefillBufs &p = d->pf;
+    const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    const int I = c.intermediate, nqkv = qd + 2 * kvd;
+    const int M = (int)S;
+    const int64_t layer_elems = (int64_t)c.n_kv_heads * d->max_seq * hd;
+    const float scale = 1.0f / sqrtf((float)hd);
+    HIPCHK(hipMemcpyAsync(p.x, emb_dev, sizeof(float) * S * H, hipMemcpyDeviceToDevice, st));
+    const float *rc = d->rc + start * hd, *rs = d->rs + start * hd;
+    for (int l = 0; l < c.n_layers; l++) {
+        const DecLayerDev &L = d->L[l];
+        float *kc = reinterpret_cast<float *>(d->kc) + l * layer_elems;
+        float *vc = reinterpret_cast<float *>(d->vc) + l * layer_elems;
+        LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.in_norm, S, H, c.eps, st), "prefill rms_norm");
+        TRY(gemm(d, p.xn, H, L.bqkv, H, p.qkv, nqkv, M, nqkv, H, EPI_NONE));
+        LAUNCHCHK(launch_head_norm_rope_strided(p.qkv, nqkv, L.q_norm, rc, rs, S, c.n_heads, c.eps, 1, 1, st),
+                  "prefill q norm/rope");
+        LAUNCHCHK(launch_head_norm_rope_strided(p.qkv + qd, nqkv, L.k_norm, rc, rs, S, c.n_kv_heads, c.eps, 1, 1, st),
+                  "prefill k norm/rope");
+        LAUNCHCHK(launch_kv_scatter(p.qkv, nqkv, qd, qd + kvd, kc, vc, d->max_seq * hd, (int)start, S, c.n_kv_heads,
+                                    st),
+                  "prefill kv write");
+        AttnRowsArgs a{};
+        a.q = p.qkv; a.q_rs = nqkv;
+        a.k = kc; a.v = vc; a.k_hs = d->max_seq * hd; a.k_rs = hd;
+        a.out = p.att; a.o_rs = qd;
+        a.n_q = M; a.n_k = (int)(start + S);
+        a.G = c.n_heads / c.n_kv_heads; a.q_offset = (int)start; a.window = 0; a.scale = scale;
+        LAUNCHCHK(launch_attn_rows(a, c.n_kv_heads, hd, st), "prefill attention");
+        TRY(gemm(d, p.att, qd, L.bo, qd, p.x, H, M, H, qd, EPI_ACCUM));
+        LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.post_norm, S, H, c.eps, st), "prefill rms_norm");
+        TRY(gemm(d, p.xn, H, L.bgu, H, p.gu, 2 * I, M, 2 * I, H, EPI_NONE));
+        LAUNCHCHK(launch_swiglu_rows(p.g, p.gu, S, I, st), "prefill swiglu");
+        TRY(gemm(d, p.g, I, L.bdown, I, p.x, H, M, H, I, EPI_ACCUM));
+    }
+    d->len = start + S;
+    return QASR_OK;
+}
+
 extern "C" int qasr_hip_decoder_prefill(qasr_decoder *d, const float *embeds, int64_t seq_len) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
-    (void)embeds;
-    (void)seq_len;
-    return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: not available in this build");
+    CHECK_H(d->h);
+    if (seq_len < 0 || (seq_len > 0 && !embeds)) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: bad arguments");
+    if (seq_len == 0) return QASR_OK;
+    TRY(ensure_prefill(d, seq_len));
+    // stage the host rows in the layer-norm buffer, then run from device memory
+    HIPCHK(hipMemcpyAsync(d->pf.xn, embeds, sizeof(float) * seq_len * d->c.hidden, hipMemcpyHostToDevice,
+                          d->h->stream));
+    TRY(decoder_prefill_dev(d, d->pf.xn, seq_len));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    return QASR_OK;
+}
+
+int decoder_prefill_hidden(qasr_decoder *d, float *host_out, int64_t seq_len) {
+    HIPCHK(hipMemcpyAsync(host_out, d->pf.x, sizeof(float) * seq_len * d->c.hidden, hipMemcpyDeviceToHost,
+                          d->h->stream));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    return QASR_OK;
 }

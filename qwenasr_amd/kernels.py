@@ -91,3 +91,25 @@ def causal_attention(out, q, k_base, v_base, head_stride, seq_q, seq_k, n_heads,
     vp = v_base.ptr if hasattr(v_base, "ptr") else v_base
     check(lib().qasr_hip_causal_attention(_h(q), out.ptr, q.ptr, kp, vp, head_stride, seq_q, seq_k,
                                           n_heads, n_kv_heads, head_dim, scale, q_offset))
+
+
+def linear(y, x, w_bf16, bias, seq_len, in_dim, out_dim, accumulate=False):
+    """linear / linear_accumulate (kernels/mod.rs:550, 591) on bf16-valued weights."""
+    check(lib().qasr_hip_linear_bf16w(_h(x), y.ptr, x.ptr, w_bf16.ptr, bias.ptr if bias is not None else None,
+                                      seq_len, in_dim, out_dim, 1 if accumulate else 0))
+
+
+def gemm_w8_bf16(y, a_bf16, w_int8, scales, M, N, K):
+    """y[M, N] = (a_bf16 [M, K] . w_int8[N, K]^T) * scales[N] on MFMA."""
+    check(lib().qasr_hip_gemm_w8_bf16(_h(a_bf16), y.ptr, a_bf16.ptr, w_int8.ptr, scales.ptr, M, N, K))
+
+
+def layer_norm(out, x, weight, bias, seq_len, hidden, eps):
+    """kernels/mod.rs:1160."""
+    check(lib().qasr_hip_layer_norm(_h(x), out.ptr, x.ptr, weight.ptr, bias.ptr, seq_len, hidden, eps))
+
+
+def bidirectional_attention(out, q, k, v, seq, n_heads, head_dim, scale, window_tokens):
+    """kernels/mod.rs:1386 with windows of window_tokens positions."""
+    check(lib().qasr_hip_bidirectional_attention(_h(q), out.ptr, q.ptr, k.ptr, v.ptr, seq, n_heads, head_dim,
+                                                 scale, window_tokens))

@@ -3,7 +3,8 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import (QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, I32, P, check, lib)
+from ._lib import (I64, QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, EncConfig, EncLayer,
+                   EncWeights, I32, P, check, lib)
 
 
 class Decoder:
@@ -103,3 +104,59 @@ class Decoder:
 
     def set_options(self, attn_splits=0, use_graph=True):
         check(lib().qasr_hip_decoder_set_options(self.d, int(attn_splits), 1 if use_graph else 0))
+
+
+class Encoder:
+    """Audio front end on the GPU: mel_spectrogram (audio.rs:273) + Encoder::forward (encoder.rs:186)."""
+
+    def __init__(self, dev, weights):
+        self.dev = dev
+        self.cfg = dict(weights.cfg)
+        cfg, w = weights.structs(EncConfig, EncLayer, EncWeights)
+        e = P()
+        check(lib().qasr_hip_encoder_load(dev.h, C.byref(cfg), C.byref(w), C.byref(e)))
+        self.e = e
+
+    def close(self):
+        if self.e:
+            lib().qasr_hip_encoder_free(self.e)
+            self.e = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tokens(self, frames):
+        return int(lib().qasr_hip_encoder_tokens(self.e, int(frames)))
+
+    def mel(self, samples):
+        s = np.ascontiguousarray(samples, np.float32)
+        nf = I64()
+        check(lib().qasr_hip_mel(self.e, s.ctypes.data_as(P), s.size, None, C.byref(nf)))
+        out = np.empty((128, nf.value), np.float32)
+        check(lib().qasr_hip_mel(self.e, s.ctypes.data_as(P), s.size, out.ctypes.data_as(P), C.byref(nf)))
+        return out
+
+    def forward(self, mel):
+        m = np.ascontiguousarray(mel, np.float32)
+        frames = m.shape[1]
+        out = np.empty((self.tokens(frames), self.cfg["output_dim"]), np.float32)
+        nt = I64()
+        check(lib().qasr_hip_encoder_forward(self.e, m.ctypes.data_as(P), frames, out.ctypes.data_as(P),
+                                             C.byref(nt)))
+        return out
+
+
+def transcribe_forced(decoder, encoder, samples, n_steps):
+    """transcribe_segment (transcribe.rs:63-247) with a forced decode length.
+
+    Returns (token ids, stage times in ms: mel, encoder, prefill + first forward, decode).
+    """
+    s = np.ascontiguousarray(samples, np.float32)
+    toks = np.empty(n_steps, np.int32)
+    times = np.empty(4, np.float64)
+    check(lib().qasr_hip_transcribe_forced(decoder.d, encoder.e, s.ctypes.data_as(P), s.size, int(n_steps),
+                                           toks.ctypes.data_as(P), times.ctypes.data_as(P)))
+    return toks, times

@@ -1,0 +1,186 @@
+"""GPU parity of the prefill / audio-encoder / mel path and the offline driver.
+
+Tolerances: f32-class GEMMs (bf16x3 split on MFMA) vs the oracle's f32 GEMM
+within 2e-5 norm-wise; int8 x bf16 GEMM within 1e-2 norm-wise of the f32 GEMM
+on the bf16 weights and 1e-5 of its own exact int8
+restatement; LayerNorm bit-exact; attention 1e-5; encoder / mel 2e-4;
+transcription token ids identical.
+"""
+import numpy as np
+import pytest
+
+from conftest import bf16, bf16f, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def nrel(a, b):
+    return float(np.linalg.norm(np.asarray(a, np.float64) - b) / np.linalg.norm(np.asarray(b, np.float64)))
+
+
+@pytest.mark.parametrize("M,N,K", [(404, 4096, 1024), (375, 1024, 3072), (390, 2688, 896), (100, 480, 9),
+                                   (33, 70, 100)])
+def test_linear_bf16w(dev, orc, M, N, K):
+    from qwenasr_amd import kernels as Kr
+    print(f"linear_bf16w M={M} N={N} K={K}", flush=True)
+    r = rng(M + N + K)
+    x = r.normal(0, 1, (M, K)).astype(np.float32)
+    w = bf16(r.normal(0, 0.02, (N, K)))
+    b = r.normal(0, 1, N).astype(np.float32)
+    y = dev.empty((M, N), np.float32)
+    dx, dw, db = dev.upload(x), dev.upload(w), dev.upload(b)
+    Kr.linear(y, dx, dw, db, M, K, N)
+    ref = orc.linear(x, bf16f(w), b)
+    exact = x.astype(np.float64) @ bf16f(w).astype(np.float64).T + b
+    assert nrel(y.numpy(), exact) < 2e-6
+    assert nrel(y.numpy(), ref) < 2e-5
+    # linear_accumulate: y = (y + b) + x W^T
+    y0 = r.normal(0, 1, (M, N)).astype(np.float32)
+    y.copy_from(y0)
+    Kr.linear(y, dx, dw, db, M, K, N, accumulate=True)
+    assert nrel(y.numpy(), exact + y0) < 2e-6
+
+
+@pytest.mark.parametrize("N,K", [(2048, 1024), (1024, 3072), (6144, 1024), (151936, 1024)])
+def test_gemm_w8_bf16_config1(dev, orc, N, K):
+    """Config 1: M = 375 rows of bf16 activations x int8 per-row weights."""
+    from qwenasr_amd import kernels as Kr
+    M = 375
+    print(f"gemm_w8_bf16 M={M} N={N} K={K}", flush=True)
+    r = rng(N + K)
+    wb = bf16(r.normal(0, 0.02, (N, K)))
+    a = bf16(r.normal(0, 1, (M, K)))
+    q, s = orc.quantize_bf16_rows(wb, 0)
+    y = dev.empty((M, N), np.float32)
+    Kr.gemm_w8_bf16(y, dev.upload(a), dev.upload(q), dev.upload(s), M, N, K)
+    got = y.numpy()
+    af = bf16f(a).astype(np.float64)
+    exact_int8 = (af @ q.astype(np.float64).T) * s
+    assert nrel(got, exact_int8) < 1e-5
+    if N <= 8192:
+        ref = orc.sgemm_nt(bf16f(a), bf16f(wb))     # the reference's f32 GEMM on bf16 weights
+        assert nrel(got, ref) < 1e-2
+
+
+def test_layer_norm_bitexact(dev, orc):
+    from qwenasr_amd import kernels as Kr
+    r = rng(5)
+    for seq, hidden in ((390, 896), (3, 1024), (1, 16)):
+        x = (r.normal(0, 1, (seq, hidden)) * r.uniform(0.1, 10, (seq, 1)) + r.normal(0, 3, (seq, 1))).astype(np.float32)
+        w = r.uniform(0.5, 1.5, hidden).astype(np.float32)
+        b = r.normal(0, 0.1, hidden).astype(np.float32)
+        out = dev.empty((seq, hidden), np.float32)
+        Kr.layer_norm(out, dev.upload(x), dev.upload(w), dev.upload(b), seq, hidden, 1e-5)
+        assert (out.numpy() == orc.layer_norm(x, w, b, 1e-5)).all()
+
+
+@pytest.mark.parametrize("S,start", [(404, 0), (37, 100), (1, 0)])
+def test_prefill_attention(dev, orc, S, start):
+    from qwenasr_amd import kernels as Kr
+    r = rng(S + start)
+    hq, hkv, hd, max_seq = 16, 8, 128, 1024
+    kc = r.normal(0, 1, (hkv, max_seq, hd)).astype(np.float32)
+    vc = r.normal(0, 1, (hkv, max_seq, hd)).astype(np.float32)
+    q = r.normal(0, 1, (S, hq * hd)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    out = dev.empty((S, hq * hd), np.float32)
+    Kr.causal_attention(out, dev.upload(q), dev.upload(kc), dev.upload(vc), max_seq * hd, S, start + S, hq, hkv,
+                        hd, scale, start)
+    ref = orc.causal_attention(q, kc, vc, max_seq * hd, S, start + S, hq, hkv, hd, scale, start)
+    np.testing.assert_allclose(out.numpy().reshape(-1), ref, rtol=1e-4, atol=2e-5)
+    assert nrel(out.numpy().reshape(-1), ref) < 1e-5
+
+
+def test_bidirectional_attention(dev, orc):
+    from qwenasr_amd import kernels as Kr
+    r = rng(77)
+    T, H, hd, win = 390, 14, 64, 104
+    q, k, v = (r.normal(0, 1, (T, H * hd)).astype(np.float32) for _ in range(3))
+    out = dev.empty((T, H * hd), np.float32)
+    Kr.bidirectional_attention(out, dev.upload(q), dev.upload(k), dev.upload(v), T, H, hd, 0.125, win)
+    ws = list(range(0, T, win)) + [T]
+    ref = orc.bidir_attention(q, k, v, T, H, hd, 0.125, ws)
+    assert nrel(out.numpy().reshape(-1), ref) < 1e-5
+
+
+TINY_DEC = dict(n_layers=2, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=3072,
+                vocab=8192, eps=1e-6, theta=1e6)
+
+
+def test_decoder_prefill_then_decode(dev, orc):
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    w = SynthDecoder(TINY_DEC, seed=1002)
+    gpu = Decoder(dev, w, max_seq=512)
+    cpu = orc.OracleDecoder(w, max_seq=512)
+    r = rng(4)
+    S = 100
+    emb = (r.normal(0, 0.02, (S, 1024))).astype(np.float32)
+    gpu.prefill(emb)
+    cpu.prefill(emb)
+    assert gpu.kv_len == cpu.kv_len == S
+    kg, vg = gpu.kv_download()
+    kc, vc = cpu.kv()
+    assert nrel(kg[:, :, :S], kc[:, :, :S]) < 1e-4 and nrel(vg[:, :, :S], vc[:, :, :S]) < 1e-4
+    # layer 0 only sees f32-class GEMMs + per-head norm + RoPE
+    assert nrel(kg[0, :, :S], kc[0, :, :S]) < 1e-5
+    tok = 11
+    for step in range(16):
+        e = cpu.embed(tok)
+        t_c, margin = cpu.forward(e)
+        t_g = gpu.forward(token=tok)
+        assert t_c == t_g, (step, t_c, t_g, margin)
+        tok = t_c
+    gpu.close()
+    cpu.close()
+
+
+def test_mel(dev, orc):
+    from qwenasr_amd.model import Encoder
+    from qwenasr_amd.synth import ENC_0_6B, SynthEncoder, audio
+    cfg = dict(ENC_0_6B, n_layers=1)
+    enc = Encoder(dev, SynthEncoder(cfg, seed=1002))
+    for n in (48000, 480000, 16123):
+        x = audio(n, 1002)
+        m_g = enc.mel(x)
+        m_c = orc.mel(x)
+        assert m_g.shape == m_c.shape == (128, orc.lib().or_mel_frames(n))
+        np.testing.assert_allclose(m_g, m_c, atol=2e-4, rtol=0)
+    enc.close()
+
+
+def test_encoder(dev, orc):
+    from qwenasr_amd.model import Encoder
+    from qwenasr_amd.synth import ENC_0_6B, SynthEncoder, audio
+    cfg = dict(ENC_0_6B, n_layers=2)
+    w = SynthEncoder(cfg, seed=1002)
+    enc = Encoder(dev, w)
+    ore = orc.OracleEncoder(w)
+    for n in (64000, 50000):                    # 400 frames (4 full chunks); 312 frames (a tail chunk)
+        mel = orc.mel(audio(n, 7))
+        out_g = enc.forward(mel)
+        out_c = ore.forward(mel)
+        assert out_g.shape == out_c.shape
+        print(f"encoder frames={mel.shape[1]} tokens={out_g.shape[0]} rel={nrel(out_g, out_c):.2e}", flush=True)
+        assert nrel(out_g, out_c) < 2e-4
+    enc.close()
+    ore.close()
+
+
+def test_transcribe_forced_tokens(dev, orc):
+    """transcribe_segment with a forced decode length: identical token ids."""
+    from qwenasr_amd.model import Decoder, Encoder, transcribe_forced
+    from qwenasr_amd.synth import DEC_0_6B, ENC_0_6B, SynthDecoder, SynthEncoder, audio
+    dcfg = dict(DEC_0_6B, n_layers=2)
+    ecfg = dict(ENC_0_6B, n_layers=2)
+    wd, we = SynthDecoder(dcfg, seed=1002), SynthEncoder(ecfg, seed=1002)
+    x = audio(64000, 1002)
+    gd, ge = Decoder(dev, wd, max_seq=512), Encoder(dev, we)
+    cd, ce = orc.OracleDecoder(wd, max_seq=512), orc.OracleEncoder(we)
+    toks_g, times = transcribe_forced(gd, ge, x, 24)
+    res = orc.transcribe_forced(cd, ce, x, 24)
+    print("gpu", toks_g.tolist(), "times", times.tolist(), flush=True)
+    print("cpu", res["tokens"].tolist(), "margins", np.round(res["margins"], 4).tolist(), flush=True)
+    assert toks_g.tolist() == res["tokens"].tolist()
+    for m in (gd, ge, cd, ce):
+        m.close()
