@@ -4,6 +4,7 @@
 #include "decoder.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -81,6 +82,10 @@ extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, co
     d->kv_bf16 = kv_bf16 ? 1 : 0;
     d->max_seq = max_seq;
     d->n_split = attn_splits_for(max_seq);
+    // QASR_DISABLE_GRAPH=1: launch decode steps kernel by kernel (profilers that
+    // do not follow graph launches)
+    const char *ng = getenv("QASR_DISABLE_GRAPH");
+    if (ng && ng[0] == '1') d->use_graph = 0;
     int rc = decoder_build(d, w);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
@@ -198,7 +203,20 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
 // one decode step: per layer [norm+qkv] [qk-norm+rope+kv-write+attention]
 // [o-proj += ] [norm+gate_up+swiglu] [down += ], then [norm+LM-head argmax]
 // ---------------------------------------------------------------------------
-int decoder_enqueue_step(qasr_decoder *d, bool embed_mode) {
+// optional per-launch timing: events recorded around every kernel of a step
+#define PROF_BEGIN(kind)                                                        \
+    do {                                                                        \
+        if (prof) HIPCHK(hipEventRecord(prof->ev[prof->n][0], st));             \
+    } while (0)
+#define PROF_END(kind)                                                          \
+    do {                                                                        \
+        if (prof) {                                                             \
+            HIPCHK(hipEventRecord(prof->ev[prof->n][1], st));                   \
+            prof->kind_of[prof->n++] = (kind);                                  \
+        }                                                                       \
+    } while (0)
+
+int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, StepProfile *prof) {
     const qasr_dec_config &c = d->c;
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     const int I = c.intermediate;
@@ -213,7 +231,9 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode) {
         a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
         a.n_total = qd + 2 * kvd;
         a.resid_out = d->x;
+        PROF_BEGIN(0);
         LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, 4, st), "step qkv");
+        PROF_END(0);
 
         AttnDecodeArgs t{};
         t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
@@ -223,32 +243,42 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode) {
         t.head_stride = (int64_t)d->max_seq * hd;
         t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
         t.n_split = d->n_split; t.eps = c.eps; t.scale = scale;
+        PROF_BEGIN(1);
         LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st), "step attention");
+        PROF_END(1);
 
         MvArgs o{};
         o.x = d->att; o.K = qd;
         o.seg[0] = {L.wo, L.so, d->x, H};
         o.n_total = H;
+        PROF_BEGIN(2);
         LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+        PROF_END(2);
 
         MvArgs g{};
         g.x = d->x; g.norm_w = L.post_norm; g.eps = c.eps; g.K = H;
         g.seg[0] = {L.wgu, L.sgu, d->ffn, 2 * I};
         g.n_total = 2 * I;
+        PROF_BEGIN(3);
         LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, 4, st), "step gate_up");
+        PROF_END(3);
 
         MvArgs dn{};
         dn.x = d->ffn; dn.K = I;
         dn.seg[0] = {L.wdown, L.sdown, d->x, H};
         dn.n_total = H;
+        PROF_BEGIN(4);
         LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, 1, st), "step down");
+        PROF_END(4);
     }
     ArgmaxArgs am{};
     am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = c.vocab;
     am.w = d->lm; am.ws = d->lm_s;
     am.part_val = d->am_val; am.part_idx = d->am_idx; am.counter = d->counters + QASR_CTR_ARGMAX;
     am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
+    PROF_BEGIN(5);
     LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st), "step argmax");
+    PROF_END(5);
     return QASR_OK;
 }
 
@@ -262,11 +292,11 @@ static int set_state(qasr_decoder *d, int32_t token) {
 }
 
 int decoder_run_embed_step(qasr_decoder *d) {
-    if (!d->use_graph) return decoder_enqueue_step(d, true);
+    if (!d->use_graph) return decoder_enqueue_step(d, true, nullptr);
     if (!d->graph_exec) {
         hipGraph_t g = nullptr;
         HIPCHK(hipStreamBeginCapture(d->h->stream, hipStreamCaptureModeThreadLocal));
-        int rc = decoder_enqueue_step(d, true);
+        int rc = decoder_enqueue_step(d, true, nullptr);
         hipError_t e = hipStreamEndCapture(d->h->stream, &g);
         if (rc != QASR_OK) {
             if (g) (void)hipGraphDestroy(g);
@@ -292,7 +322,7 @@ extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int
     TRY(set_state(d, token_in));
     if (embed) {
         HIPCHK(hipMemcpyAsync(d->x, embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice, d->h->stream));
-        TRY(decoder_enqueue_step(d, false));
+        TRY(decoder_enqueue_step(d, false, nullptr));
     } else {
         TRY(decoder_run_embed_step(d));
     }
@@ -316,7 +346,7 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
     if (first_embed) {
         HIPCHK(hipMemcpyAsync(d->x, first_embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice,
                               d->h->stream));
-        TRY(decoder_enqueue_step(d, false));
+        TRY(decoder_enqueue_step(d, false, nullptr));
     } else {
         TRY(decoder_run_embed_step(d));
     }
@@ -408,4 +438,73 @@ extern "C" int qasr_hip_decoder_kv_upload(qasr_decoder *d, const float *k, const
 
 extern "C" int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k, float *v) {
     return kv_copy(d, k, v, false);
+}
+
+// ---------------------------------------------------------------------------
+// per-kernel timing of real decode steps (no graph): HIP events around every
+// launch on the handle's stream; the KV length is restored afterwards
+// ---------------------------------------------------------------------------
+extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float *us_per_launch,
+                                        double *bytes_per_launch, int32_t *launches_per_step) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (n_steps <= 0 || !us_per_launch) return qasr_fail(QASR_ERR_INVALID, "decoder_profile: bad arguments");
+    if (d->len + n_steps > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_profile: KV cache capacity exceeded");
+    const qasr_dec_config &c = d->c;
+    StepProfile prof;
+    const int per_step = 5 * c.n_layers + 1;
+    prof.ev.resize(per_step);
+    prof.kind_of.resize(per_step);
+    for (auto &e : prof.ev) {
+        HIPCHK(hipEventCreate(&e[0]));
+        HIPCHK(hipEventCreate(&e[1]));
+    }
+    double tot[6] = {0, 0, 0, 0, 0, 0};
+    int cnt[6] = {0, 0, 0, 0, 0, 0};
+    const int64_t len0 = d->len;
+    int rc = QASR_OK;
+    int32_t tok = 0;
+    for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
+        d->host_state[0] = tok;
+        d->host_state[1] = (int32_t)d->len;
+        d->host_state[2] = 0;
+        d->host_state[3] = 0;
+        HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, d->h->stream));
+        prof.n = 0;
+        rc = decoder_enqueue_step(d, true, &prof);
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        for (int i = 0; i < prof.n; i++) {
+            float ms = 0.0f;
+            HIPCHK(hipEventElapsedTime(&ms, prof.ev[i][0], prof.ev[i][1]));
+            tot[prof.kind_of[i]] += ms * 1000.0;
+            cnt[prof.kind_of[i]] += 1;
+        }
+        HIPCHK(hipMemcpy(d->host_state, d->state, sizeof(d->host_state), hipMemcpyDeviceToHost));
+        tok = d->host_state[0];
+        d->len += 1;
+    }
+    const double Lavg = (double)len0 + 0.5 * (n_steps - 1) + 1.0;   // context length seen by the attention
+    d->len = len0;
+    for (auto &e : prof.ev) {
+        (void)hipEventDestroy(e[0]);
+        (void)hipEventDestroy(e[1]);
+    }
+    if (rc != QASR_OK) return rc;
+    const double H = c.hidden, qd = (double)c.n_heads * c.head_dim, kvd = (double)c.n_kv_heads * c.head_dim;
+    const double I = c.intermediate, V = c.vocab, esz = d->kv_bf16 ? 2 : 4;
+    // algorithmic bytes: int8 weights N*K + scales 4N + activation 4K + output 4N (+4N read for += )
+    const double nqkv = qd + 2 * kvd;
+    const double bytes[6] = {
+        nqkv * H + 4 * nqkv + 4 * H + 4 * nqkv,
+        2.0 * kvd * Lavg * esz + 4 * nqkv + 4 * qd + 2 * kvd * esz,
+        H * qd + 4 * H + 4 * qd + 8 * H,
+        2 * I * H + 8 * I + 4 * H + 4 * I,
+        H * I + 4 * H + 4 * I + 8 * H,
+        V * H + 4 * V + 4 * H};
+    for (int k = 0; k < 6; k++) {
+        us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
+        if (bytes_per_launch) bytes_per_launch[k] = bytes[k];
+        if (launches_per_step) launches_per_step[k] = k == 5 ? 1 : c.n_layers;
+    }
+    return QASR_OK;
 }

@@ -1,5 +1,6 @@
 // Internal layout of the device-resident decoder.
 #pragma once
+#include <array>
 #include <vector>
 #include "kernels.h"
 #include "model.h"
@@ -15,6 +16,12 @@ struct DecLayerDev {
 struct PrefillBufs {
     int64_t cap = 0;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *g = nullptr;
+};
+
+struct StepProfile {
+    std::vector<std::array<hipEvent_t, 2>> ev;
+    std::vector<int> kind_of;
+    int n = 0;
 };
 
 struct qasr_decoder {
@@ -42,7 +49,7 @@ struct qasr_decoder {
 };
 
 int decoder_build(qasr_decoder *d, const qasr_dec_weights *w);
-int decoder_enqueue_step(qasr_decoder *d, bool embed_mode);
+int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, StepProfile *prof = nullptr);
 void decoder_free_prefill(qasr_decoder *d);
 int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S);
 int decoder_run_embed_step(qasr_decoder *d);

@@ -160,3 +160,18 @@ def transcribe_forced(decoder, encoder, samples, n_steps):
     check(lib().qasr_hip_transcribe_forced(decoder.d, encoder.e, s.ctypes.data_as(P), s.size, int(n_steps),
                                            toks.ctypes.data_as(P), times.ctypes.data_as(P)))
     return toks, times
+
+
+KERNEL_KINDS = ("norm+qkv", "attention", "o_proj+=", "norm+gate_up+swiglu", "down+=", "norm+lm_head_argmax")
+
+
+def profile_decoder(decoder, n_steps):
+    """Average us per launch, algorithmic bytes per launch and launches per step
+    of each decode-step kernel, timed with HIP events inside real decode steps."""
+    us = np.zeros(6, np.float32)
+    by = np.zeros(6, np.float64)
+    n = np.zeros(6, np.int32)
+    check(lib().qasr_hip_decoder_profile(decoder.d, int(n_steps), us.ctypes.data_as(P), by.ctypes.data_as(P),
+                                         n.ctypes.data_as(P)))
+    return [dict(kernel=k, us=float(us[i]), bytes=float(by[i]), per_step=int(n[i]))
+            for i, k in enumerate(KERNEL_KINDS)]
