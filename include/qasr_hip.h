@@ -193,8 +193,12 @@ int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, int8_t *q_hos
                             float *scales_host);
 int qasr_hip_decoder_kv_upload(qasr_decoder *d, const float *k_host, const float *v_host);
 int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
-/* decode-step tuning: attention context splits (default chosen from max_seq)
- * and whether steps replay a captured HIP graph (default 1) */
+/* decode-step tuning: attention context splits, 1..64 (0 keeps the current
+ * value, -1 restores the default chosen from max_seq: >= 16, about 256
+ * positions per split).  At <= 8 splits with 16 query / 8 KV heads the o_proj
+ * kernel merges the split partials in its prologue; otherwise the attention
+ * kernel's last block per KV head merges them.  use_graph: steps replay a
+ * captured HIP graph (default 1). */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
 /* per-kernel timing of n_steps real decode steps from the current KV length
  * (no graph; HIP events around every launch on the handle's stream; the KV

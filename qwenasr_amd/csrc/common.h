@@ -8,15 +8,38 @@
 namespace qasr {
 
 // ---- wave reductions (all lanes receive the result) ------------------------
+// DPP controls (GFX9 encoding): quad_perm [1,0,3,2] / [2,3,0,1], row_half_mirror,
+// row_mirror, then row_bcast:15 into rows 1,3 and row_bcast:31 into rows 2,3;
+// lane 63 ends with the full reduction.  Integer sums and max are exact in any
+// order, so these need not follow any particular tree.
+#define QASR_DPP_QP_1032 0xB1
+#define QASR_DPP_QP_2301 0x4E
+#define QASR_DPP_ROW_HALF_MIRROR 0x141
+#define QASR_DPP_ROW_MIRROR 0x140
+#define QASR_DPP_ROW_BCAST15 0x142
+#define QASR_DPP_ROW_BCAST31 0x143
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, QASR_WAVE);
-    return v;
+    v += __builtin_amdgcn_update_dpp(0, v, QASR_DPP_QP_1032, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, QASR_DPP_QP_2301, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, QASR_DPP_ROW_HALF_MIRROR, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, QASR_DPP_ROW_MIRROR, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, QASR_DPP_ROW_BCAST15, 0xA, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, QASR_DPP_ROW_BCAST31, 0xC, 0xF, false);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_max_step(float v) {
+    const int o = __builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, ROW_MASK, 0xF, false);
+    return fmaxf(v, __int_as_float(o));
 }
 __device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, QASR_WAVE));
-    return v;
+    v = dpp_max_step<QASR_DPP_QP_1032, 0xF>(v);
+    v = dpp_max_step<QASR_DPP_QP_2301, 0xF>(v);
+    v = dpp_max_step<QASR_DPP_ROW_HALF_MIRROR, 0xF>(v);
+    v = dpp_max_step<QASR_DPP_ROW_MIRROR, 0xF>(v);
+    v = dpp_max_step<QASR_DPP_ROW_BCAST15, 0xA>(v);
+    v = dpp_max_step<QASR_DPP_ROW_BCAST31, 0xC>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ float wave_sum_f32(float v) {
 #pragma unroll

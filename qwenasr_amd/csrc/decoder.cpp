@@ -81,7 +81,7 @@ extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, co
     d->round_mode = round_mode;
     d->kv_bf16 = kv_bf16 ? 1 : 0;
     d->max_seq = max_seq;
-    d->n_split = attn_splits_for(max_seq);
+    d->n_split = default_attn_splits(c, max_seq);
     // QASR_DISABLE_GRAPH=1: launch decode steps kernel by kernel (profilers that
     // do not follow graph launches)
     const char *ng = getenv("QASR_DISABLE_GRAPH");
@@ -183,8 +183,7 @@ int decoder_build(qasr_decoder *d, const qasr_dec_weights *w) {
     HIPCHK(hipMemsetAsync(d->counters, 0, QASR_COUNTERS * sizeof(unsigned), d->h->stream));
     TRY(dalloc(d, &d->am_val, QASR_ARGMAX_MAX_BLOCKS));
     TRY(dalloc(d, &d->am_idx, QASR_ARGMAX_MAX_BLOCKS));
-    const int max_split = attn_splits_for(d->max_seq) > 64 ? attn_splits_for(d->max_seq) : 64;
-    TRY(dalloc(d, &d->part, (size_t)c.n_kv_heads * max_split * 2 * (hd + 2)));
+    TRY(dalloc(d, &d->part, (size_t)c.n_kv_heads * 64 * 2 * (hd + 2)));
     HIPCHK(hipStreamSynchronize(d->h->stream));
     return QASR_OK;
 }
@@ -243,16 +242,25 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, StepProfile *prof) {
         t.head_stride = (int64_t)d->max_seq * hd;
         t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
         t.n_split = d->n_split; t.eps = c.eps; t.scale = scale;
+        // with few splits the o_proj kernel merges the attention partials in
+        // its prologue; otherwise the attention's last block per head merges
+        const bool fused_merge = oproj_merges(c, d->n_split);
         PROF_BEGIN(1);
-        LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st), "step attention");
+        LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, !fused_merge),
+                  "step attention");
         PROF_END(1);
 
-        MvArgs o{};
-        o.x = d->att; o.K = qd;
-        o.seg[0] = {L.wo, L.so, d->x, H};
-        o.n_total = H;
         PROF_BEGIN(2);
-        LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+        if (fused_merge) {
+            OprojMergeArgs om{d->part, d->n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
+            LAUNCHCHK(launch_oproj_merge(om, st), "step o_proj");
+        } else {
+            MvArgs o{};
+            o.x = d->att; o.K = qd;
+            o.seg[0] = {L.wo, L.so, d->x, H};
+            o.n_total = H;
+            LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+        }
         PROF_END(2);
 
         MvArgs g{};
@@ -370,10 +378,10 @@ extern "C" int64_t qasr_hip_decoder_len(const qasr_decoder *d) { return d ? d->l
 extern "C" int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
     CHECK_H(d->h);
+    if (attn_splits < 0) d->n_split = default_attn_splits(d->c, d->max_seq);
     if (attn_splits > 0) {
-        if (attn_splits < attn_splits_for(d->max_seq) || attn_splits > 64)
-            return qasr_fail(QASR_ERR_INVALID, "decoder_set_options: attn_splits must cover max_seq with "
-                                               "<= 256 positions per split and be <= 64");
+        if (attn_splits > 64)
+            return qasr_fail(QASR_ERR_INVALID, "decoder_set_options: attn_splits must be <= 64");
         d->n_split = attn_splits;
     }
     d->use_graph = use_graph ? 1 : 0;

@@ -43,27 +43,94 @@ __device__ __forceinline__ float head_sum128(float v, float *red) {
 // scores dot(q, k_j) * scale over j <= pos, softmax, sum_j p_j v_j, with q/k
 // per-head RMSNorm (mod.rs:1214-1238) and NeoX RoPE (mod.rs:1780-1788) fused
 // in front and the new K/V row written into the cache (decoder.rs:233-253).
-// The context is split into n_split ranges (one block each); every block
-// writes (max, sum, o) partials and the last block of a KV head merges them
-// with the usual log-sum-exp rescaling.  Softmax is therefore evaluated in a
-// different order than the reference's sequential online scan: results agree
-// to f32 rounding, not bit for bit.
+//
+// The context is split into n_split ranges (one block each).  A block streams
+// its range in tiles of 32 positions through LDS: the first tile's loads are
+// issued before the q/k prologue and each next tile is prefetched into
+// registers while the current one is consumed, so the block pays about one
+// memory round trip per tile.  Softmax is online within the block; every
+// block publishes (max, sum, o) and the last block of a KV head merges them
+// with log-sum-exp rescaling.  The order of operations differs from the
+// reference's sequential scan: results agree to f32 rounding, not bit for bit.
 // ---------------------------------------------------------------------------
 #define ATT_MAXC 256
 #define ATT_MAXS 64
+#define ATT_TP 32
 
-template <int G, typename KVT>
+template <typename KVT> struct KvTile;
+template <> struct KvTile<float> {      // 32 x 128 f32 = 1024 float4, 4 per thread
+    static constexpr int N = 4;
+    float4 k[N], v[N];
+};
+template <> struct KvTile<uint16_t> {   // 32 x 128 bf16 = 512 uint4, 2 per thread
+    static constexpr int N = 2;
+    uint4 k[N], v[N];
+};
+
+template <typename KVT>
+__device__ __forceinline__ void tile_load(KvTile<KVT> &r, const KVT *kc, const KVT *vc, int j0, int j1, int skip) {
+    constexpr int PER_ROW = sizeof(KVT) == 4 ? 32 : 16;     // 16-byte vectors per position
+#pragma unroll
+    for (int i = 0; i < KvTile<KVT>::N; i++) {
+        const int idx = threadIdx.x + 256 * i;
+        const int j = j0 + idx / PER_ROW, c = idx % PER_ROW;
+        const bool ok = j < j1 && j != skip;
+        const int jj = ok ? j : j0;
+        if (sizeof(KVT) == 4) {
+            const float4 kv = reinterpret_cast<const float4 *>(kc + (int64_t)jj * 128)[c];
+            const float4 vv = reinterpret_cast<const float4 *>(vc + (int64_t)jj * 128)[c];
+            reinterpret_cast<float4 *>(&r.k[i])[0] = kv;
+            reinterpret_cast<float4 *>(&r.v[i])[0] = vv;
+        } else {
+            const uint4 kv = reinterpret_cast<const uint4 *>(kc + (int64_t)jj * 128)[c];
+            const uint4 vv = reinterpret_cast<const uint4 *>(vc + (int64_t)jj * 128)[c];
+            reinterpret_cast<uint4 *>(&r.k[i])[0] = kv;
+            reinterpret_cast<uint4 *>(&r.v[i])[0] = vv;
+        }
+    }
+}
+
+template <typename KVT>
+__device__ __forceinline__ void tile_store(const KvTile<KVT> &r, float (*Ks)[132], float (*Vs)[128]) {
+    constexpr int PER_ROW = sizeof(KVT) == 4 ? 32 : 16;
+#pragma unroll
+    for (int i = 0; i < KvTile<KVT>::N; i++) {
+        const int idx = threadIdx.x + 256 * i;
+        const int p = idx / PER_ROW, c = idx % PER_ROW;
+        if (sizeof(KVT) == 4) {
+            const float4 kv = reinterpret_cast<const float4 *>(&r.k[i])[0];
+            const float4 vv = reinterpret_cast<const float4 *>(&r.v[i])[0];
+            *reinterpret_cast<float4 *>(&Ks[p][4 * c]) = kv;
+            *reinterpret_cast<float4 *>(&Vs[p][4 * c]) = vv;
+        } else {
+            const uint4 kv = reinterpret_cast<const uint4 *>(&r.k[i])[0];
+            const uint4 vv = reinterpret_cast<const uint4 *>(&r.v[i])[0];
+            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                Ks[p][8 * c + 2 * e] = __uint_as_float(kw[e] << 16);
+                Ks[p][8 * c + 2 * e + 1] = __uint_as_float(kw[e] & 0xFFFF0000u);
+                Vs[p][8 * c + 2 * e] = __uint_as_float(vw[e] << 16);
+                Vs[p][8 * c + 2 * e + 1] = __uint_as_float(vw[e] & 0xFFFF0000u);
+            }
+        }
+    }
+}
+
+template <int G, typename KVT, bool MERGE>
 __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
-    constexpr int D = 128;
+    constexpr int D = 128, TP = ATT_TP;
     static_assert(G * D == 256, "one thread per (query head, dim)");
+    __shared__ float Ks[TP][D + 4];
+    __shared__ float Vs[TP][D];
     __shared__ float qs[G][D];
     __shared__ float knew[D], vnew[D];
     __shared__ float red[8];
-    __shared__ float sc[G][ATT_MAXC];
+    __shared__ float ps[G][TP];
     __shared__ float pv[2][G][D];
     __shared__ float mw[G][ATT_MAXS], lw[G][ATT_MAXS];
     __shared__ int last;
-    const int t = threadIdx.x, lane = t & 63, wid = t >> 6;
+    const int t = threadIdx.x, lane = t & 63;
     const int n_split = a.n_split;
     const int kvh = blockIdx.x / n_split, split = blockIdx.x % n_split;
     const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
@@ -73,146 +140,159 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
     const int j0 = split * chunk, j1 = min(L, j0 + chunk);
     const bool prep = a.q_norm != nullptr;     // raw projections: norm + rope + cache write
     const bool own_pos = prep && j0 <= pos && pos < j1;
+    const int skip = own_pos ? pos : -1;
     KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
     KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
+    const int gi = t / D, d = t % D;
 
-    // ---- query heads of this group ---------------------------------------
-    {
-        const int gi = t / D, d = t % D;
-        float v = a.qkv[(kvh * G + gi) * D + d];
-        if (prep) {
-            const float ss = head_sum128(__fmul_rn(v, v), red);
-            const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
-            v = __fmul_rn(__fmul_rn(v, r), a.q_norm[d]);
-            qs[gi][d] = v;
-            __syncthreads();
-            const float *c = a.rope_cos + (int64_t)pos * D, *s = a.rope_sin + (int64_t)pos * D;
-            const int h = D / 2;
-            float o;
-            if (d < h) o = __fadd_rn(__fmul_rn(v, c[d]), __fmul_rn(-qs[gi][d + h], s[d]));
-            else o = __fadd_rn(__fmul_rn(v, c[d]), __fmul_rn(qs[gi][d - h], s[d]));
-            __syncthreads();
-            qs[gi][d] = o;
-        } else {
-            qs[gi][d] = v;
-        }
+    // ---- issue the small operand loads, then the first tile ---------------
+    float qv = a.qkv[(kvh * G + gi) * D + d];
+    float cv = 0.0f, sv = 0.0f, kraw = 0.0f, vraw = 0.0f;
+    if (prep) {
+        cv = a.rope_cos[(int64_t)pos * D + d];
+        sv = a.rope_sin[(int64_t)pos * D + d];
+    }
+    if (own_pos && t < D) {
+        kraw = a.qkv[Hq * D + kvh * D + d];
+        vraw = a.qkv[Hq * D + Hkv * D + kvh * D + d];
+    }
+    KvTile<KVT> tr;
+    if (j0 < j1) tile_load<KVT>(tr, kc, vc, j0, min(j1, j0 + TP), skip);
+
+    // ---- query heads of this group: per-head RMSNorm + RoPE --------------
+    if (prep) {
+        const float ss = head_sum128(__fmul_rn(qv, qv), red);
+        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
+        qv = __fmul_rn(__fmul_rn(qv, r), a.q_norm[d]);
+        qs[gi][d] = qv;
+        __syncthreads();
+        const int h = D / 2;
+        float o;
+        if (d < h) o = __fadd_rn(__fmul_rn(qv, cv), __fmul_rn(-qs[gi][d + h], sv));
+        else o = __fadd_rn(__fmul_rn(qv, cv), __fmul_rn(qs[gi][d - h], sv));
+        __syncthreads();
+        qs[gi][d] = o;
+    } else {
+        qs[gi][d] = qv;
     }
     // ---- new K/V row (the block whose range holds pos) --------------------
     if (own_pos) {
-        const int d = t % D;
-        float kv = a.qkv[Hq * D + kvh * D + d];
-        const float ss = head_sum128(t < D ? __fmul_rn(kv, kv) : 0.0f, red);
+        const float ss = head_sum128(t < D ? __fmul_rn(kraw, kraw) : 0.0f, red);
+        float kv = 0.0f;
         if (t < D) {
             const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
-            kv = __fmul_rn(__fmul_rn(kv, r), a.k_norm[d]);
+            kv = __fmul_rn(__fmul_rn(kraw, r), a.k_norm[d]);
             knew[d] = kv;
         }
         __syncthreads();
-        float o = 0.0f, vv = 0.0f;
+        float o = 0.0f;
         if (t < D) {
-            const float *c = a.rope_cos + (int64_t)pos * D, *s = a.rope_sin + (int64_t)pos * D;
             const int h = D / 2;
-            if (d < h) o = __fadd_rn(__fmul_rn(kv, c[d]), __fmul_rn(-knew[d + h], s[d]));
-            else o = __fadd_rn(__fmul_rn(kv, c[d]), __fmul_rn(knew[d - h], s[d]));
-            vv = a.qkv[Hq * D + Hkv * D + kvh * D + d];
+            if (d < h) o = __fadd_rn(__fmul_rn(kv, cv), __fmul_rn(-knew[d + h], sv));
+            else o = __fadd_rn(__fmul_rn(kv, cv), __fmul_rn(knew[d - h], sv));
             kc[(int64_t)pos * D + d] = st_kv<KVT>(o);
-            vc[(int64_t)pos * D + d] = st_kv<KVT>(vv);
+            vc[(int64_t)pos * D + d] = st_kv<KVT>(vraw);
         }
         __syncthreads();
         if (t < D) {   // the values the cache now holds (a bf16 cache rounds)
             knew[d] = round_kv<KVT>(o);
-            vnew[d] = round_kv<KVT>(vv);
+            vnew[d] = round_kv<KVT>(vraw);
         }
     }
     __syncthreads();
 
-    // ---- scores: 16 lanes per position, 8 dims per lane --------------------
-    const int sub = lane >> 4, dl = (lane & 15) * 8;
-    float qv[G][8];
+    // ---- stream the range in tiles -----------------------------------------
+    // scores: thread t -> position p = t / 8, dims (t % 8) * 16 .. +16
+    const int sp = t >> 3, sd = (t & 7) * 16;
+    float qreg[G][16];
 #pragma unroll
-    for (int gi = 0; gi < G; gi++)
+    for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) qv[gi][i] = qs[gi][dl + i];
-    for (int base = j0; base < j1; base += 16) {
-        const int j = base + wid * 4 + sub;
-        float kr[8];
-        if (j < j1) {
-            if (own_pos && j == pos) {
+        for (int i = 0; i < 16; i++) qreg[g][i] = qs[g][sd + i];
+    float m_run[G], l_run[G], acc[G];
 #pragma unroll
-                for (int i = 0; i < 8; i++) kr[i] = knew[dl + i];
-            } else {
-                ld8(kc + (int64_t)j * D + dl, kr);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) kr[i] = 0.0f;
+    for (int g = 0; g < G; g++) { m_run[g] = -INFINITY; l_run[g] = 0.0f; acc[g] = 0.0f; }
+    const int hh = t / D;                    // PV: thread (hh, d) takes positions p = hh, hh + 2, ...
+    for (int b = j0; b < j1; b += TP) {
+        const int n = min(TP, j1 - b);
+        tile_store<KVT>(tr, Ks, Vs);
+        __syncthreads();
+        if (own_pos && pos >= b && pos < b + n) {          // the new row comes from LDS
+            if (t < D) { Ks[pos - b][t] = knew[t]; Vs[pos - b][t] = vnew[t]; }
+            __syncthreads();
         }
+        if (b + TP < j1) tile_load<KVT>(tr, kc, vc, b + TP, min(j1, b + 2 * TP), skip);   // prefetch
+        float sc[G];
 #pragma unroll
-        for (int gi = 0; gi < G; gi++) {
+        for (int g = 0; g < G; g++) {
             float p = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) p = fmaf(qv[gi][i], kr[i], p);
-            p = group_sum_f32<16>(p);
-            if ((lane & 15) == 0 && j < j1) sc[gi][j - j0] = __fmul_rn(p, a.scale);
+            for (int i = 0; i < 16; i++) p = fmaf(qreg[g][i], Ks[sp][sd + i], p);
+            p = group_sum_f32<8>(p);
+            sc[g] = p;
         }
-    }
-    __syncthreads();
-    // ---- softmax over this block's range ------------------------------------
-    const int n = j1 > j0 ? j1 - j0 : 0;
-    float mloc[G], lsum[G];
+        if ((t & 7) == 0) {
 #pragma unroll
-    for (int gi = 0; gi < G; gi++) {
-        float m = -INFINITY;
-        for (int j = t; j < n; j += 256) m = fmaxf(m, sc[gi][j]);
-        m = wave_max_f32(m);
-        __syncthreads();
-        if (lane == 0) red[wid] = m;
-        __syncthreads();
-        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        float s = 0.0f;
-        for (int j = t; j < n; j += 256) {
-            const float p = expf(__fsub_rn(sc[gi][j], m));
-            sc[gi][j] = p;
-            s = __fadd_rn(s, p);
+            for (int g = 0; g < G; g++) ps[g][sp] = sp < n ? __fmul_rn(sc[g], a.scale) : -INFINITY;
         }
-        s = wave_sum_f32(s);
         __syncthreads();
-        if (lane == 0) red[4 + wid] = s;
-        __syncthreads();
-        mloc[gi] = m;
-        lsum[gi] = __fadd_rn(__fadd_rn(red[4], red[5]), __fadd_rn(red[6], red[7]));
-    }
-    // ---- o = sum_j p_j v_j: thread (half, d) covers j = j0 + half + 2i ------
-    {
-        const int d = t % D, half = t / D;
-        float acc[G];
+        // online softmax update (every thread keeps the block-wide state of each head)
+        float corr[G];
 #pragma unroll
-        for (int gi = 0; gi < G; gi++) acc[gi] = 0.0f;
-        for (int j = j0 + half; j < j1; j += 2) {
-            const float vv = (own_pos && j == pos) ? vnew[d] : ld_kv<KVT>(vc + (int64_t)j * D + d);
-#pragma unroll
-            for (int gi = 0; gi < G; gi++) acc[gi] = fmaf(sc[gi][j - j0], vv, acc[gi]);
+        for (int g = 0; g < G; g++) {
+            float tm = -INFINITY;
+            for (int p = 0; p < n; p++) tm = fmaxf(tm, ps[g][p]);
+            const float mn = fmaxf(m_run[g], tm);
+            corr[g] = m_run[g] == -INFINITY ? 0.0f : expf(__fsub_rn(m_run[g], mn));
+            m_run[g] = mn;
         }
+        __syncthreads();
+        if (t < G * TP) {
+            const int g = t / TP, p = t % TP;
+            ps[g][p] = p < n ? expf(__fsub_rn(ps[g][p], m_run[g])) : 0.0f;
+        }
+        __syncthreads();
 #pragma unroll
-        for (int gi = 0; gi < G; gi++) pv[half][gi][d] = acc[gi];
+        for (int g = 0; g < G; g++) {
+            float s = 0.0f;
+            for (int p = 0; p < n; p++) s = __fadd_rn(s, ps[g][p]);
+            l_run[g] = fmaf(l_run[g], corr[g], s);
+            acc[g] = __fmul_rn(acc[g], corr[g]);
+        }
+        for (int p = hh; p < n; p += 2) {
+            const float vv = Vs[p][d];
+#pragma unroll
+            for (int g = 0; g < G; g++) acc[g] = fmaf(ps[g][p], vv, acc[g]);
+        }
+        __syncthreads();
     }
+#pragma unroll
+    for (int g = 0; g < G; g++) pv[hh][g][d] = acc[g];
     __syncthreads();
     float *part = a.part + ((int64_t)kvh * n_split + split) * G * (D + 2);
-    {
-        const int gi = t / D, d = t % D;
-        st_agent(part + gi * (D + 2) + 2 + d, __fadd_rn(pv[0][gi][d], pv[1][gi][d]));
+    const float o_part = __fadd_rn(pv[0][gi][d], pv[1][gi][d]);
+    const float m_part = j1 > j0 ? m_run[gi] : -INFINITY, l_part = j1 > j0 ? l_run[gi] : 0.0f;
+    if (!MERGE) {
+        // the consumer (the o_proj kernel) merges; the kernel boundary publishes these
+        part[gi * (D + 2) + 2 + d] = o_part;
         if (d == 0) {
-            st_agent(part + gi * (D + 2), n > 0 ? mloc[gi] : -INFINITY);
-            st_agent(part + gi * (D + 2) + 1, n > 0 ? lsum[gi] : 0.0f);
+            part[gi * (D + 2)] = m_part;
+            part[gi * (D + 2) + 1] = l_part;
         }
+        return;
+    }
+    st_agent(part + gi * (D + 2) + 2 + d, o_part);
+    if (d == 0) {
+        st_agent(part + gi * (D + 2), m_part);
+        st_agent(part + gi * (D + 2) + 1, l_part);
     }
     if (!arrive_last(a.counters + kvh, (unsigned)n_split, &last)) return;
     // ---- last block of this KV head: log-sum-exp merge of the n_split partials
     const float *pb = a.part + (int64_t)kvh * n_split * G * (D + 2);
     for (int i = t; i < n_split * G; i += 256) {
-        const int s = i / G, gi = i % G;
-        mw[gi][s] = ld_agent(pb + (s * G + gi) * (D + 2));
-        lw[gi][s] = ld_agent(pb + (s * G + gi) * (D + 2) + 1);
+        const int s = i / G, g = i % G;
+        mw[g][s] = ld_agent(pb + (s * G + g) * (D + 2));
+        lw[g][s] = ld_agent(pb + (s * G + g) * (D + 2) + 1);
     }
     __syncthreads();
     if (t < G) {
@@ -228,7 +308,6 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
     }
     __syncthreads();
     {
-        const int gi = t / D, d = t % D;
         float ot = 0.0f;
         for (int s0 = 0; s0 < n_split; s0 += 8) {
             float ov[8];
@@ -246,12 +325,17 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
 }
 
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
-                              int kv_bf16, hipStream_t st) {
+                              int kv_bf16, hipStream_t st, bool merge) {
     if (head_dim != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads) return hipErrorInvalidValue;
     if (a.n_split <= 0 || a.n_split > ATT_MAXS) return hipErrorInvalidValue;
     const dim3 grid(n_kv_heads * a.n_split);
-    if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<2, uint16_t>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_attn_decode<2, float>), grid, dim3(256), 0, st, a);
+    if (merge) {
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<2, uint16_t, true>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_attn_decode<2, float, true>), grid, dim3(256), 0, st, a);
+    } else {
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<2, uint16_t, false>), grid, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL((k_attn_decode<2, float, false>), grid, dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 

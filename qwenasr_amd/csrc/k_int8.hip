@@ -259,6 +259,125 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// o_proj of the decode step with the split-attention merge in front
+// (causal_attention's result, mod.rs:1527-1535, then linear_nobias_int8_addto,
+// decoder.rs:616-617).  The attention kernel leaves n_split partials
+// (max, sum, o[128]) per query head; every block loads them (L2/MALL), merges
+// with log-sum-exp weights into LDS, and its waves quantize the merged vector
+// as the activation of a 4-rows-per-wave W8A8 addto matvec.  The partial loads
+// are issued before the weight loads so the merge overlaps the weight stream.
+// ---------------------------------------------------------------------------
+#define OM_MAXS 8
+__global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
+    constexpr int D = 128, G = 2, NS = 2, R = 4, HQ = 16, K = HQ * D;
+    __shared__ float att[K];
+    __shared__ float ms[HQ][OM_MAXS], ls[HQ][OM_MAXS], wf[HQ][OM_MAXS], lsum[HQ];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int S = a.n_split;
+    const int row0 = (blockIdx.x * 4 + wid) * R;
+    // (1) partial statistics and outputs of this thread
+    float pm = -INFINITY, pl = 0.0f;
+    if (t < HQ * S) {
+        const int h = t / S, sp = t % S, kvh = h / G, g = h % G;
+        const float *b = a.part + ((int64_t)(kvh * S + sp) * G + g) * (D + 2);
+        pm = b[0];
+        pl = b[1];
+    }
+    float ov[K / 256][OM_MAXS];
+#pragma unroll
+    for (int j = 0; j < K / 256; j++) {
+        const int i = t + 256 * j, h = i / D, d = i % D, kvh = h / G, g = h % G;
+#pragma unroll
+        for (int sp = 0; sp < OM_MAXS; sp++) {
+            const int se = sp < S ? sp : 0;
+            const float v = a.part[((int64_t)(kvh * S + se) * G + g) * (D + 2) + 2 + d];
+            ov[j][sp] = sp < S ? v : 0.0f;
+        }
+    }
+    // (2) weights of this wave's rows
+    const int nslot = K >> 4;
+    const bool live = row0 < a.N;
+    const int r0 = live ? row0 : 0;
+    i32x4 wv[R][NS];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int c = 0; c < NS; c++)
+            wv[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(a.w + (int64_t)(r0 + r) * K) +
+                                                  lane + 64 * c);
+    // (3) log-sum-exp weights per head
+    if (t < HQ * S) {
+        ms[t / S][t % S] = pm;
+        ls[t / S][t % S] = pl;
+    }
+    __syncthreads();
+    if (t < HQ) {
+        float M = -INFINITY;
+        for (int sp = 0; sp < S; sp++) M = fmaxf(M, ms[t][sp]);
+        float lt = 0.0f;
+        for (int sp = 0; sp < S; sp++) {
+            const float f = ms[t][sp] == -INFINITY ? 0.0f : expf(__fsub_rn(ms[t][sp], M));
+            wf[t][sp] = f;
+            lt = fmaf(ls[t][sp], f, lt);
+        }
+        lsum[t] = lt;
+    }
+    __syncthreads();
+    // (4) merged attention output
+#pragma unroll
+    for (int j = 0; j < K / 256; j++) {
+        const int i = t + 256 * j, h = i / D;
+        float ot = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < OM_MAXS; sp++)
+            if (sp < S) ot = fmaf(ov[j][sp], wf[h][sp], ot);
+        att[i] = lsum[h] > 0.0f ? __fdiv_rn(ot, lsum[h]) : 0.0f;
+    }
+    __syncthreads();
+    if (!live) return;
+    // (5) quantize (each wave covers the whole vector with its lanes' slots)
+    ActIn<NS, false, false> in;
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const float4 *p = reinterpret_cast<const float4 *>(att + 16 * (lane + 64 * c));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = p[i];
+            in.xv[c][4 * i] = v.x; in.xv[c][4 * i + 1] = v.y; in.xv[c][4 * i + 2] = v.z; in.xv[c][4 * i + 3] = v.w;
+        }
+    }
+    int xd[NS][4];
+    float xs;
+    act_finish<NS, false, false>(in, 0.0f, K, nullptr, xd, &xs);
+    (void)nslot;
+    // (6) dots and the residual-add epilogue
+    int acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        int q = 0;
+#pragma unroll
+        for (int c = 0; c < NS; c++) q = dot16(wv[r][c], xd[c], q);
+        acc[r] = wave_sum_i32(q);
+    }
+    if (lane < R) {
+        int av = 0;
+#pragma unroll
+        for (int r = 0; r < R; r++) if (r == lane) av = acc[r];
+        const int row = row0 + lane;
+        const float v = __fmul_rn(__fmul_rn((float)av, xs), a.ws[row]);
+        a.y[row] = __fadd_rn(v, a.y[row]);
+    }
+}
+
+hipError_t launch_oproj_merge(const OprojMergeArgs &a, hipStream_t st) {
+    if (a.Hkv != 8 || a.n_split <= 0 || a.n_split > OM_MAXS || a.N % 4 != 0) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)((a.N / 4 + 3) / 4);
+    hipLaunchKernelGGL(k_oproj_merge, dim3(blocks), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // LM-head argmax: argmax_matvec_int8 (kernels/mod.rs:1832-1893).  Optional
 // final RMSNorm prologue; grid-stride over row groups; strict > per wave
 // (rows visited in increasing order), then block and grid merges with the

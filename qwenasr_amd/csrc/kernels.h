@@ -72,8 +72,21 @@ struct AttnDecodeArgs {
     float eps, scale;
 };
 
+// merge: the last block of each KV head merges the split partials into out;
+// otherwise the partials are left for k_oproj_merge
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
-                              int kv_bf16, hipStream_t st);
+                              int kv_bf16, hipStream_t st, bool merge = true);
+
+// o_proj += Wo attn with the split-attention merge as its prologue (decode step)
+struct OprojMergeArgs {
+    const float *part;        // [Hkv][n_split][2][130] attention partials (m, l, o[128])
+    int n_split, Hkv;
+    const int8_t *w;          // [N, K = 2 * Hkv * 128] int8
+    const float *ws;          // [N]
+    float *y;                 // [N], y += W attn
+    int N;
+};
+hipError_t launch_oproj_merge(const OprojMergeArgs &a, hipStream_t st);
 
 hipError_t launch_rms_norm_rows(float *out, const float *x, const float *w, int64_t seq, int hidden,
                                 float eps, hipStream_t st);

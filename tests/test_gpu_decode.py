@@ -74,8 +74,14 @@ def test_decoder_packing_bitexact(tiny_models):
     assert (qg == qc).all() and (sg == sc).all()
 
 
-def test_decoder_teacher_forced(tiny_models):
+@pytest.mark.parametrize("splits", [-1, 8, 3, 40])
+def test_decoder_teacher_forced(tiny_models, splits):
+    """splits -1: the default (16 context splits merged by the attention
+    kernel); 8 and 3: partials merged inside the o_proj kernel (3 leaves
+    ragged splits); 40: more splits than positions early on (empty splits)."""
     w, gpu, cpu = tiny_models
+    print(f"teacher forced splits={splits}", flush=True)
+    gpu.set_options(attn_splits=splits)
     gpu.kv_len = 0
     cpu.kv_len = 0
     n = 48
@@ -100,6 +106,7 @@ def test_decoder_teacher_forced(tiny_models):
     for a, b in ((kg, kc), (vg, vc)):
         rel = np.linalg.norm(a[:, :, :n] - b[:, :, :n]) / np.linalg.norm(b[:, :, :n])
         assert rel < 2e-3, rel
+    gpu.set_options(attn_splits=-1)
 
 
 def test_generate_matches_forward(tiny_models):
