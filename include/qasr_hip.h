@@ -200,11 +200,13 @@ int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
  * kernel's last block per KV head merges them.  use_graph: steps replay a
  * captured HIP graph (default 1). */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
-/* per-kernel timing of n_steps real decode steps from the current KV length
- * (no graph; HIP events around every launch on the handle's stream; the KV
- * length is restored).  Kinds: 0 norm+qkv, 1 attention, 2 o_proj, 3
- * norm+gate_up+swiglu, 4 down, 5 norm+LM-head argmax.  Outputs average us per
- * launch, algorithmic bytes per launch and launches per step (6 entries each). */
+/* per-kernel timing over n_steps real decode steps from the current KV length
+ * (no graph).  After each step every kernel kind is launched once per layer
+ * (the LM head n_layers times) back to back between two HIP events on the
+ * handle's stream, from the step's input state.  Kinds: 0 norm+qkv, 1
+ * attention, 2 o_proj, 3 norm+gate_up+swiglu, 4 down, 5 norm+LM-head argmax.
+ * Outputs average us per launch, algorithmic bytes per launch and launches
+ * per step (6 entries each).  The KV length is restored afterwards. */
 int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float *us_per_launch,
                              double *bytes_per_launch, int32_t *launches_per_step);
 

@@ -202,20 +202,7 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
 // one decode step: per layer [norm+qkv] [qk-norm+rope+kv-write+attention]
 // [o-proj += ] [norm+gate_up+swiglu] [down += ], then [norm+LM-head argmax]
 // ---------------------------------------------------------------------------
-// optional per-launch timing: events recorded around every kernel of a step
-#define PROF_BEGIN(kind)                                                        \
-    do {                                                                        \
-        if (prof) HIPCHK(hipEventRecord(prof->ev[prof->n][0], st));             \
-    } while (0)
-#define PROF_END(kind)                                                          \
-    do {                                                                        \
-        if (prof) {                                                             \
-            HIPCHK(hipEventRecord(prof->ev[prof->n][1], st));                   \
-            prof->kind_of[prof->n++] = (kind);                                  \
-        }                                                                       \
-    } while (0)
-
-int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, StepProfile *prof) {
+int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     const qasr_dec_config &c = d->c;
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     const int I = c.intermediate;
@@ -223,70 +210,67 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, StepProfile *prof) {
     const size_t esz = d->kv_bf16 ? 2 : 4;
     const int64_t layer_elems = (int64_t)c.n_kv_heads * d->max_seq * hd;
     const float scale = 1.0f / sqrtf((float)hd);
+    auto want = [only_kind](int kind) { return only_kind < 0 || only_kind == kind; };
+    // with few splits the o_proj kernel merges the attention partials in its
+    // prologue; otherwise the attention's last block per head merges them
+    const bool fused_merge = oproj_merges(c, d->n_split);
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
-        MvArgs a{};
-        a.x = d->x; a.embed = d->embed; a.state = d->state; a.norm_w = L.in_norm; a.eps = c.eps; a.K = H;
-        a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
-        a.n_total = qd + 2 * kvd;
-        a.resid_out = d->x;
-        PROF_BEGIN(0);
-        LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, 4, st), "step qkv");
-        PROF_END(0);
-
-        AttnDecodeArgs t{};
-        t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
-        t.rope_cos = d->rc; t.rope_sin = d->rs; t.state = d->state;
-        t.kcache = (char *)d->kc + (size_t)l * layer_elems * esz;
-        t.vcache = (char *)d->vc + (size_t)l * layer_elems * esz;
-        t.head_stride = (int64_t)d->max_seq * hd;
-        t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
-        t.n_split = d->n_split; t.eps = c.eps; t.scale = scale;
-        // with few splits the o_proj kernel merges the attention partials in
-        // its prologue; otherwise the attention's last block per head merges
-        const bool fused_merge = oproj_merges(c, d->n_split);
-        PROF_BEGIN(1);
-        LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, !fused_merge),
-                  "step attention");
-        PROF_END(1);
-
-        PROF_BEGIN(2);
-        if (fused_merge) {
-            OprojMergeArgs om{d->part, d->n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
-            LAUNCHCHK(launch_oproj_merge(om, st), "step o_proj");
-        } else {
-            MvArgs o{};
-            o.x = d->att; o.K = qd;
-            o.seg[0] = {L.wo, L.so, d->x, H};
-            o.n_total = H;
-            LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+        if (want(0)) {
+            MvArgs a{};
+            a.x = d->x; a.embed = d->embed; a.state = d->state; a.norm_w = L.in_norm; a.eps = c.eps; a.K = H;
+            a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
+            a.n_total = qd + 2 * kvd;
+            a.resid_out = d->x;
+            LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, 4, st), "step qkv");
         }
-        PROF_END(2);
-
-        MvArgs g{};
-        g.x = d->x; g.norm_w = L.post_norm; g.eps = c.eps; g.K = H;
-        g.seg[0] = {L.wgu, L.sgu, d->ffn, 2 * I};
-        g.n_total = 2 * I;
-        PROF_BEGIN(3);
-        LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, 4, st), "step gate_up");
-        PROF_END(3);
-
-        MvArgs dn{};
-        dn.x = d->ffn; dn.K = I;
-        dn.seg[0] = {L.wdown, L.sdown, d->x, H};
-        dn.n_total = H;
-        PROF_BEGIN(4);
-        LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, 1, st), "step down");
-        PROF_END(4);
+        if (want(1)) {
+            AttnDecodeArgs t{};
+            t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
+            t.rope_cos = d->rc; t.rope_sin = d->rs; t.state = d->state;
+            t.kcache = (char *)d->kc + (size_t)l * layer_elems * esz;
+            t.vcache = (char *)d->vc + (size_t)l * layer_elems * esz;
+            t.head_stride = (int64_t)d->max_seq * hd;
+            t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
+            t.n_split = d->n_split; t.eps = c.eps; t.scale = scale;
+            LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, !fused_merge),
+                      "step attention");
+        }
+        if (want(2)) {
+            if (fused_merge) {
+                OprojMergeArgs om{d->part, d->n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
+                LAUNCHCHK(launch_oproj_merge(om, st), "step o_proj");
+            } else {
+                MvArgs o{};
+                o.x = d->att; o.K = qd;
+                o.seg[0] = {L.wo, L.so, d->x, H};
+                o.n_total = H;
+                LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+            }
+        }
+        if (want(3)) {
+            MvArgs g{};
+            g.x = d->x; g.norm_w = L.post_norm; g.eps = c.eps; g.K = H;
+            g.seg[0] = {L.wgu, L.sgu, d->ffn, 2 * I};
+            g.n_total = 2 * I;
+            LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, 4, st), "step gate_up");
+        }
+        if (want(4)) {
+            MvArgs dn{};
+            dn.x = d->ffn; dn.K = I;
+            dn.seg[0] = {L.wdown, L.sdown, d->x, H};
+            dn.n_total = H;
+            LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, 1, st), "step down");
+        }
     }
-    ArgmaxArgs am{};
-    am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = c.vocab;
-    am.w = d->lm; am.ws = d->lm_s;
-    am.part_val = d->am_val; am.part_idx = d->am_idx; am.counter = d->counters + QASR_CTR_ARGMAX;
-    am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
-    PROF_BEGIN(5);
-    LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st), "step argmax");
-    PROF_END(5);
+    if (want(5)) {
+        ArgmaxArgs am{};
+        am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = c.vocab;
+        am.w = d->lm; am.ws = d->lm_s;
+        am.part_val = d->am_val; am.part_idx = d->am_idx; am.counter = d->counters + QASR_CTR_ARGMAX;
+        am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
+        LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st), "step argmax");
+    }
     return QASR_OK;
 }
 
@@ -300,11 +284,11 @@ static int set_state(qasr_decoder *d, int32_t token) {
 }
 
 int decoder_run_embed_step(qasr_decoder *d) {
-    if (!d->use_graph) return decoder_enqueue_step(d, true, nullptr);
+    if (!d->use_graph) return decoder_enqueue_step(d, true);
     if (!d->graph_exec) {
         hipGraph_t g = nullptr;
         HIPCHK(hipStreamBeginCapture(d->h->stream, hipStreamCaptureModeThreadLocal));
-        int rc = decoder_enqueue_step(d, true, nullptr);
+        int rc = decoder_enqueue_step(d, true);
         hipError_t e = hipStreamEndCapture(d->h->stream, &g);
         if (rc != QASR_OK) {
             if (g) (void)hipGraphDestroy(g);
@@ -330,7 +314,7 @@ extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int
     TRY(set_state(d, token_in));
     if (embed) {
         HIPCHK(hipMemcpyAsync(d->x, embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice, d->h->stream));
-        TRY(decoder_enqueue_step(d, false, nullptr));
+        TRY(decoder_enqueue_step(d, false));
     } else {
         TRY(decoder_run_embed_step(d));
     }
@@ -354,7 +338,7 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
     if (first_embed) {
         HIPCHK(hipMemcpyAsync(d->x, first_embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice,
                               d->h->stream));
-        TRY(decoder_enqueue_step(d, false, nullptr));
+        TRY(decoder_enqueue_step(d, false));
     } else {
         TRY(decoder_run_embed_step(d));
     }
@@ -449,8 +433,16 @@ extern "C" int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k, float *v)
 }
 
 // ---------------------------------------------------------------------------
-// per-kernel timing of real decode steps (no graph): HIP events around every
-// launch on the handle's stream; the KV length is restored afterwards
+// per-kernel timing.  Each of n_steps real decode steps runs unbracketed (no
+// graph); then, from the same input state, every kernel kind is launched once
+// per layer back to back (the LM head n_layers times) between two HIP events
+// on the handle's stream, behind a 400 us delay kernel that holds the stream
+// until the host has queued the batch.  The average per launch is then the
+// kernel's duration plus the queue's inter-dispatch gap, neither an event
+// bracket's overhead nor the host's launch rate.  These
+// extra launches rewrite the KV slot of the step's position, the residual and
+// the step buffers; the KV length is restored afterwards and that slot is
+// beyond it, so later decoding is unaffected.
 // ---------------------------------------------------------------------------
 extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float *us_per_launch,
                                         double *bytes_per_launch, int32_t *launches_per_step) {
@@ -459,44 +451,42 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
     if (n_steps <= 0 || !us_per_launch) return qasr_fail(QASR_ERR_INVALID, "decoder_profile: bad arguments");
     if (d->len + n_steps > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_profile: KV cache capacity exceeded");
     const qasr_dec_config &c = d->c;
-    StepProfile prof;
-    const int per_step = 5 * c.n_layers + 1;
-    prof.ev.resize(per_step);
-    prof.kind_of.resize(per_step);
-    for (auto &e : prof.ev) {
-        HIPCHK(hipEventCreate(&e[0]));
-        HIPCHK(hipEventCreate(&e[1]));
-    }
+    hipStream_t st = d->h->stream;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    const int lm_reps = (int)std::min<int64_t>(c.n_layers, d->max_seq);
     double tot[6] = {0, 0, 0, 0, 0, 0};
     int cnt[6] = {0, 0, 0, 0, 0, 0};
     const int64_t len0 = d->len;
     int rc = QASR_OK;
     int32_t tok = 0;
     for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
-        d->host_state[0] = tok;
-        d->host_state[1] = (int32_t)d->len;
-        d->host_state[2] = 0;
-        d->host_state[3] = 0;
-        HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, d->h->stream));
-        prof.n = 0;
-        rc = decoder_enqueue_step(d, true, &prof);
-        HIPCHK(hipStreamSynchronize(d->h->stream));
-        for (int i = 0; i < prof.n; i++) {
+        if ((rc = set_state(d, tok)) != QASR_OK) break;
+        if ((rc = decoder_enqueue_step(d, true)) != QASR_OK) break;
+        HIPCHK(hipStreamSynchronize(st));
+        int32_t next[4];
+        HIPCHK(hipMemcpy(next, d->state, sizeof(next), hipMemcpyDeviceToHost));
+        for (int k = 0; k < 6 && rc == QASR_OK; k++) {
+            if ((rc = set_state(d, tok)) != QASR_OK) break;
+            LAUNCHCHK(launch_delay(400, st), "profile delay");
+            HIPCHK(hipEventRecord(e0, st));
+            const int reps = k == 5 ? lm_reps : 1;
+            for (int r = 0; r < reps && rc == QASR_OK; r++) rc = decoder_enqueue_step(d, true, k);
+            HIPCHK(hipEventRecord(e1, st));
+            HIPCHK(hipEventSynchronize(e1));
             float ms = 0.0f;
-            HIPCHK(hipEventElapsedTime(&ms, prof.ev[i][0], prof.ev[i][1]));
-            tot[prof.kind_of[i]] += ms * 1000.0;
-            cnt[prof.kind_of[i]] += 1;
+            HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+            tot[k] += ms * 1000.0;
+            cnt[k] += k == 5 ? lm_reps : c.n_layers;
         }
-        HIPCHK(hipMemcpy(d->host_state, d->state, sizeof(d->host_state), hipMemcpyDeviceToHost));
-        tok = d->host_state[0];
+        tok = next[0];
         d->len += 1;
     }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     const double Lavg = (double)len0 + 0.5 * (n_steps - 1) + 1.0;   // context length seen by the attention
     d->len = len0;
-    for (auto &e : prof.ev) {
-        (void)hipEventDestroy(e[0]);
-        (void)hipEventDestroy(e[1]);
-    }
     if (rc != QASR_OK) return rc;
     const double H = c.hidden, qd = (double)c.n_heads * c.head_dim, kvd = (double)c.n_kv_heads * c.head_dim;
     const double I = c.intermediate, V = c.vocab, esz = d->kv_bf16 ? 2 : 4;

@@ -18,12 +18,6 @@ struct PrefillBufs {
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *gu = nullptr, *g = nullptr;
 };
 
-struct StepProfile {
-    std::vector<std::array<hipEvent_t, 2>> ev;
-    std::vector<int> kind_of;
-    int n = 0;
-};
-
 struct qasr_decoder {
     qasr_hip *h = nullptr;
     qasr_dec_config c{};
@@ -49,7 +43,9 @@ struct qasr_decoder {
 };
 
 int decoder_build(qasr_decoder *d, const qasr_dec_weights *w);
-int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, StepProfile *prof = nullptr);
+// enqueue one decode step; only_kind >= 0 launches only the kernels of that
+// kind (0 norm+qkv, 1 attention, 2 o_proj, 3 norm+gate_up, 4 down, 5 LM head)
+int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind = -1);
 void decoder_free_prefill(qasr_decoder *d);
 int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S);
 int decoder_run_embed_step(qasr_decoder *d);

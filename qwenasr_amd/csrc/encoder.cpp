@@ -474,7 +474,7 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
         d->host_state[3] = 0;
         HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, st));
         HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
-        rc = decoder_enqueue_step(d, false, nullptr);
+        rc = decoder_enqueue_step(d, false);
     }
     if (rc == QASR_OK) {
         HIPCHK(hipEventRecord(ev[3], st));

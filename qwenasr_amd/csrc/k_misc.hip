@@ -406,4 +406,21 @@ hipError_t launch_mel_log_norm(float *mel, int64_t n, float *bmax, hipStream_t s
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// timing helper: one wave that idles for `ticks` of the 100 MHz constant clock
+// (s_memrealtime).  Queued in front of a timed batch of launches, it holds the
+// stream until the host has enqueued the whole batch, so the batch runs back to
+// back.  The loop always ends: the clock is monotonic.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_delay(int64_t ticks) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while ((int64_t)(__builtin_amdgcn_s_memrealtime() - t0) < ticks) __builtin_amdgcn_s_sleep(64);
+}
+
+hipError_t launch_delay(int us, hipStream_t st) {
+    if (us < 0 || us > 100000) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_delay, dim3(1), dim3(64), 0, st, (int64_t)us * 100);
+    return hipGetLastError();
+}
+
 }  // namespace qasr

@@ -145,6 +145,8 @@ hipError_t launch_add_periodic(float *y, const float *table, int64_t rows, int c
 hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C, int H, int W, int64_t cs,
                               int64_t chs, int64_t rs, int Ho, int Wo, hipStream_t st);
 hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C, int F, int T, hipStream_t st);
+// idle one wave for `us` microseconds (timing helper)
+hipError_t launch_delay(int us, hipStream_t st);
 hipError_t launch_kv_scatter(const float *qkv, int64_t qkv_rs, int k_off, int v_off, float *kc, float *vc,
                              int64_t head_stride, int start, int64_t S, int Hkv, hipStream_t st);
 hipError_t launch_build_prompt(float *out, const uint16_t *embed, const int *toks, int n_head, const float *mid,
