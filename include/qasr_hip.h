@@ -194,11 +194,12 @@ int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, int8_t *q_hos
 int qasr_hip_decoder_kv_upload(qasr_decoder *d, const float *k_host, const float *v_host);
 int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
 /* decode-step tuning: attention context splits, 1..64 (0 keeps the current
- * value, -1 restores the default chosen from max_seq: >= 16, about 256
- * positions per split).  At <= 8 splits with 16 query / 8 KV heads the o_proj
- * kernel merges the split partials in its prologue; otherwise the attention
- * kernel's last block per KV head merges them.  use_graph: steps replay a
- * captured HIP graph (default 1). */
+ * value, -1 restores the automatic choice per context bucket of 256
+ * positions: 8 up to 1024 positions, 16 up to 2048, then about one per 64).
+ * At 1, 2, 4, 8 or 16 splits with 16 query / 8 KV heads the o_proj kernel
+ * merges the split partials in its prologue; otherwise the attention kernel's
+ * last block per KV head merges them.  use_graph: steps replay a captured HIP
+ * graph, one per context bucket (default 1). */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
 /* per-kernel timing over n_steps real decode steps from the current KV length
  * (no graph).  After each step every kernel kind is launched once per layer

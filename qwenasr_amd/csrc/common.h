@@ -46,6 +46,49 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     for (int o = 32; o > 0; o >>= 1) v = __fadd_rn(v, __shfl_xor(v, o, QASR_WAVE));
     return v;
 }
+// ---- 8-lane reductions without LDS -----------------------------------------
+// Lanes are viewed as 8 groups of 8 (group = lane / 8, member = lane % 8).
+// sum8/max8 reduce over the members of a group (quad_perm [1,0,3,2], [2,3,0,1],
+// then row_half_mirror, which pairs each quad with the other quad of its 8);
+// sum_x8/max_x8 reduce over the groups at a fixed member (row_ror:8 pairs
+// lanes i and i ^ 8 within a 16-lane row, v_permlane16_swap pairs rows 0/1 and
+// 2/3, v_permlane32_swap pairs the wave's halves).  Every lane of a reduction
+// set receives the same value.
+#define QASR_DPP_ROW_ROR8 0x128
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xrow16_sum(float v) {     // v[i] + v[i ^ 16]
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xhalf_sum(float v) {      // v[i] + v[i ^ 32]
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __fadd_rn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xrow16_max(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float xhalf_max(float v) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float sum8(float v) {
+    v = __fadd_rn(v, dpp_f32<QASR_DPP_QP_1032>(v));
+    v = __fadd_rn(v, dpp_f32<QASR_DPP_QP_2301>(v));
+    return __fadd_rn(v, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(v));
+}
+__device__ __forceinline__ float sum_x8(float v) {
+    v = __fadd_rn(v, dpp_f32<QASR_DPP_ROW_ROR8>(v));
+    return xhalf_sum(xrow16_sum(v));
+}
+__device__ __forceinline__ float max_x8(float v) {
+    v = fmaxf(v, dpp_f32<QASR_DPP_ROW_ROR8>(v));
+    return xhalf_max(xrow16_max(v));
+}
+
 // reduction over aligned groups of `width` lanes (width a power of two <= 64)
 template <int WIDTH>
 __device__ __forceinline__ float group_sum_f32(float v) {

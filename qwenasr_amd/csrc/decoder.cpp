@@ -81,11 +81,14 @@ extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, co
     d->round_mode = round_mode;
     d->kv_bf16 = kv_bf16 ? 1 : 0;
     d->max_seq = max_seq;
-    d->n_split = default_attn_splits(c, max_seq);
+    d->n_split = 0;   // automatic, per context bucket
     // QASR_DISABLE_GRAPH=1: launch decode steps kernel by kernel (profilers that
     // do not follow graph launches)
     const char *ng = getenv("QASR_DISABLE_GRAPH");
     if (ng && ng[0] == '1') d->use_graph = 0;
+    // QASR_ATTN_WAVES=4|8: waves per decode-attention block (tuning)
+    const char *aw = getenv("QASR_ATTN_WAVES");
+    if (aw && (aw[0] == '4' || aw[0] == '8') && aw[1] == 0) d->attn_waves = aw[0] - '0';
     int rc = decoder_build(d, w);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
@@ -168,6 +171,7 @@ int decoder_build(qasr_decoder *d, const qasr_dec_weights *w) {
             }
         TRY(dalloc(d, &d->rc, cs.size()));
         TRY(dalloc(d, &d->rs, sn.size()));
+        TRY(dalloc(d, &d->rope_cur, 2 * hd));
         TRY(upload(d, d->rc, cs.data(), sizeof(float) * cs.size()));
         TRY(upload(d, d->rs, sn.data(), sizeof(float) * sn.size()));
         HIPCHK(hipStreamSynchronize(d->h->stream));
@@ -192,7 +196,7 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
     if (!d) return;
     (void)hipSetDevice(d->h->device);
     (void)hipStreamSynchronize(d->h->stream);
-    if (d->graph_exec) (void)hipGraphExecDestroy(d->graph_exec);
+    for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
     decoder_free_prefill(d);
     for (void *p : d->allocs) (void)hipFree(p);
     delete d;
@@ -202,6 +206,11 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
 // one decode step: per layer [norm+qkv] [qk-norm+rope+kv-write+attention]
 // [o-proj += ] [norm+gate_up+swiglu] [down += ], then [norm+LM-head argmax]
 // ---------------------------------------------------------------------------
+int64_t decoder_ctx_cap(const qasr_decoder *d, int64_t L) {
+    const int64_t c = ((L + 255) / 256) * 256;
+    return std::min<int64_t>(std::max<int64_t>(c, 256), d->max_seq);
+}
+
 int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     const qasr_dec_config &c = d->c;
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
@@ -213,7 +222,10 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     auto want = [only_kind](int kind) { return only_kind < 0 || only_kind == kind; };
     // with few splits the o_proj kernel merges the attention partials in its
     // prologue; otherwise the attention's last block per head merges them
-    const bool fused_merge = oproj_merges(c, d->n_split);
+    // context bucket of this step: sizes the attention's static partition and its splits
+    const int64_t cap = decoder_ctx_cap(d, d->step_pos + 1);
+    const int n_split = d->n_split > 0 ? d->n_split : attn_splits_auto(c, cap);
+    const bool fused_merge = oproj_merges(c, n_split);
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
         if (want(0)) {
@@ -227,18 +239,20 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         if (want(1)) {
             AttnDecodeArgs t{};
             t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
-            t.rope_cos = d->rc; t.rope_sin = d->rs; t.state = d->state;
+            t.rope_cos = d->rc; t.rope_sin = d->rs; t.rope_cur = d->rope_cur; t.state = d->state;
             t.kcache = (char *)d->kc + (size_t)l * layer_elems * esz;
             t.vcache = (char *)d->vc + (size_t)l * layer_elems * esz;
             t.head_stride = (int64_t)d->max_seq * hd;
             t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
-            t.n_split = d->n_split; t.eps = c.eps; t.scale = scale;
+            t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = scale;
+            // static partition of the step's context bucket: the first KV loads need no device state
+            t.gpb = (int)((((cap + 7) / 8) + n_split - 1) / n_split);
             LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, !fused_merge),
                       "step attention");
         }
         if (want(2)) {
             if (fused_merge) {
-                OprojMergeArgs om{d->part, d->n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
+                OprojMergeArgs om{d->part, n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
                 LAUNCHCHK(launch_oproj_merge(om, st), "step o_proj");
             } else {
                 MvArgs o{};
@@ -269,24 +283,42 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         am.w = d->lm; am.ws = d->lm_s;
         am.part_val = d->am_val; am.part_idx = d->am_idx; am.counter = d->counters + QASR_CTR_ARGMAX;
         am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
+        am.rope_cos = d->rc; am.rope_sin = d->rs; am.rope_cur = d->rope_cur; am.max_pos = (int)d->max_seq;
         LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st), "step argmax");
     }
     return QASR_OK;
 }
 
-static int set_state(qasr_decoder *d, int32_t token) {
+int decoder_set_state(qasr_decoder *d, int32_t token) {
+    const int64_t hd = d->c.head_dim;
     d->host_state[0] = token;
     d->host_state[1] = (int32_t)d->len;
     d->host_state[2] = 0;
     d->host_state[3] = 0;
     HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, d->h->stream));
+    d->step_pos = d->len;
+    if (d->len < d->max_seq) {
+        HIPCHK(hipMemcpyAsync(d->rope_cur, d->rc + d->len * hd, sizeof(float) * hd, hipMemcpyDeviceToDevice,
+                              d->h->stream));
+        HIPCHK(hipMemcpyAsync(d->rope_cur + hd, d->rs + d->len * hd, sizeof(float) * hd, hipMemcpyDeviceToDevice,
+                              d->h->stream));
+    }
     return QASR_OK;
 }
 
+static int set_state(qasr_decoder *d, int32_t token) { return decoder_set_state(d, token); }
+
 int decoder_run_embed_step(qasr_decoder *d) {
-    if (!d->use_graph) return decoder_enqueue_step(d, true);
-    if (!d->graph_exec) {
+    if (!d->use_graph) {
+        TRY(decoder_enqueue_step(d, true));
+        d->step_pos += 1;
+        return QASR_OK;
+    }
+    const int64_t cap = decoder_ctx_cap(d, d->step_pos + 1);
+    auto it = d->graphs.find(cap);
+    if (it == d->graphs.end()) {
         hipGraph_t g = nullptr;
+        hipGraphExec_t ge = nullptr;
         HIPCHK(hipStreamBeginCapture(d->h->stream, hipStreamCaptureModeThreadLocal));
         int rc = decoder_enqueue_step(d, true);
         hipError_t e = hipStreamEndCapture(d->h->stream, &g);
@@ -295,11 +327,13 @@ int decoder_run_embed_step(qasr_decoder *d) {
             return rc;
         }
         HIPCHK(e);
-        e = hipGraphInstantiate(&d->graph_exec, g, nullptr, nullptr, 0);
+        e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         HIPCHK(e);
+        it = d->graphs.emplace(cap, ge).first;
     }
-    HIPCHK(hipGraphLaunch(d->graph_exec, d->h->stream));
+    HIPCHK(hipGraphLaunch(it->second, d->h->stream));
+    d->step_pos += 1;
     return QASR_OK;
 }
 
@@ -315,6 +349,7 @@ extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int
     if (embed) {
         HIPCHK(hipMemcpyAsync(d->x, embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice, d->h->stream));
         TRY(decoder_enqueue_step(d, false));
+        d->step_pos += 1;
     } else {
         TRY(decoder_run_embed_step(d));
     }
@@ -339,6 +374,7 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
         HIPCHK(hipMemcpyAsync(d->x, first_embed, sizeof(float) * d->c.hidden, hipMemcpyHostToDevice,
                               d->h->stream));
         TRY(decoder_enqueue_step(d, false));
+        d->step_pos += 1;
     } else {
         TRY(decoder_run_embed_step(d));
     }
@@ -362,17 +398,17 @@ extern "C" int64_t qasr_hip_decoder_len(const qasr_decoder *d) { return d ? d->l
 extern "C" int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
     CHECK_H(d->h);
-    if (attn_splits < 0) d->n_split = default_attn_splits(d->c, d->max_seq);
+    if (attn_splits < 0) d->n_split = 0;
     if (attn_splits > 0) {
         if (attn_splits > 64)
             return qasr_fail(QASR_ERR_INVALID, "decoder_set_options: attn_splits must be <= 64");
         d->n_split = attn_splits;
     }
     d->use_graph = use_graph ? 1 : 0;
-    if (d->graph_exec) {
+    if (!d->graphs.empty()) {
         HIPCHK(hipStreamSynchronize(d->h->stream));
-        HIPCHK(hipGraphExecDestroy(d->graph_exec));
-        d->graph_exec = nullptr;
+        for (auto &g : d->graphs) HIPCHK(hipGraphExecDestroy(g.second));
+        d->graphs.clear();
     }
     return QASR_OK;
 }

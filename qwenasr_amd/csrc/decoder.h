@@ -1,6 +1,7 @@
 // Internal layout of the device-resident decoder.
 #pragma once
 #include <array>
+#include <map>
 #include <vector>
 #include "kernels.h"
 #include "model.h"
@@ -29,14 +30,19 @@ struct qasr_decoder {
     float *lm_s = nullptr, *norm = nullptr;
     void *kc = nullptr, *vc = nullptr;          // [layer][kv_head][max_seq][hd]
     float *rc = nullptr, *rs = nullptr;         // RoPE [max_seq][hd]
+    float *rope_cur = nullptr;                  // [2][hd]: cos, sin rows of the step's position
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr;
     int32_t *state = nullptr;                   // {token, pos, step, flag}
     int32_t *token_log = nullptr, *out_idx = nullptr;
     unsigned *counters = nullptr;
     float *am_val = nullptr, *part = nullptr;
     int32_t *am_idx = nullptr;
-    int n_split = 16, use_graph = 1;
-    hipGraphExec_t graph_exec = nullptr;
+    int n_split = 0, use_graph = 1;             // attention splits (0: automatic per context bucket)
+    int attn_waves = 4;                         // waves per attention block (4 or 8)
+    // one captured decode step per context bucket (the attention's static
+    // partition is sized for the bucket); keyed by the bucket's capacity
+    std::map<int64_t, hipGraphExec_t> graphs;
+    int64_t step_pos = 0;                       // position of the next step to enqueue
     int32_t host_state[4] = {0, 0, 0, 0};
     PrefillBufs pf;
     std::vector<void *> allocs;
@@ -45,7 +51,12 @@ struct qasr_decoder {
 int decoder_build(qasr_decoder *d, const qasr_dec_weights *w);
 // enqueue one decode step; only_kind >= 0 launches only the kernels of that
 // kind (0 norm+qkv, 1 attention, 2 o_proj, 3 norm+gate_up, 4 down, 5 LM head)
+// The step is enqueued for position d->step_pos (the caller advances it).
 int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind = -1);
+// context capacity of the bucket holding a context of L positions
+int64_t decoder_ctx_cap(const qasr_decoder *d, int64_t L);
 void decoder_free_prefill(qasr_decoder *d);
 int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S);
 int decoder_run_embed_step(qasr_decoder *d);
+// host -> device decode state {token, pos = d->len, 0, 0} and the RoPE rows of pos
+int decoder_set_state(qasr_decoder *d, int32_t token);

@@ -468,13 +468,12 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
     }
     if (rc == QASR_OK) {
         // first token from the last prompt row, then n_steps - 1 graph-replayed steps
-        d->host_state[0] = 0;
-        d->host_state[1] = (int32_t)d->len;
-        d->host_state[2] = 0;
-        d->host_state[3] = 0;
-        HIPCHK(hipMemcpyAsync(d->state, d->host_state, sizeof(d->host_state), hipMemcpyHostToDevice, st));
-        HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
-        rc = decoder_enqueue_step(d, false);
+        rc = decoder_set_state(d, 0);
+        if (rc == QASR_OK) {
+            HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
+            rc = decoder_enqueue_step(d, false);
+            d->step_pos += 1;
+        }
     }
     if (rc == QASR_OK) {
         HIPCHK(hipEventRecord(ev[3], st));

@@ -12,284 +12,318 @@ template <> __device__ __forceinline__ uint16_t st_kv<uint16_t>(float v) { retur
 // the f32 value a cache element of type T holds after storing v
 template <typename T> __device__ __forceinline__ float round_kv(float v) { const T s = st_kv<T>(v); return ld_kv<T>(&s); }
 
-// load 8 consecutive KV elements as f32
-__device__ __forceinline__ void ld8(const float *p, float o[8]) {
-    const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
-    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
-}
-__device__ __forceinline__ void ld8(const uint16_t *p, float o[8]) {
-    const uint4 a = *reinterpret_cast<const uint4 *>(p);
-    const uint32_t w[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        o[2 * i] = __uint_as_float(w[i] << 16);
-        o[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-    }
-}
-
-// Sum over the 128 threads of a head (two waves) through LDS slots red[2h], red[2h+1].
-__device__ __forceinline__ float head_sum128(float v, float *red) {
-    v = wave_sum_f32(v);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    return __fadd_rn(red[w & ~1], red[w | 1]);
-}
-
 // ---------------------------------------------------------------------------
-// GQA decode attention, one layer, D = 128, G = Hq / Hkv query heads per KV
-// head.  Restates causal_attention with seq_q = 1 (kernels/mod.rs:1492-1536):
-// scores dot(q, k_j) * scale over j <= pos, softmax, sum_j p_j v_j, with q/k
+// GQA decode attention, one layer, D = 128, two query heads per KV head.
+// Restates causal_attention with seq_q = 1 (kernels/mod.rs:1492-1536): scores
+// dot(q, k_j) * scale over j <= pos, softmax, sum_j p_j v_j, with the q/k
 // per-head RMSNorm (mod.rs:1214-1238) and NeoX RoPE (mod.rs:1780-1788) fused
 // in front and the new K/V row written into the cache (decoder.rs:233-253).
 //
-// The context is split into n_split ranges (one block each).  A block streams
-// its range in tiles of 32 positions through LDS: the first tile's loads are
-// issued before the q/k prologue and each next tile is prefetched into
-// registers while the current one is consumed, so the block pays about one
-// memory round trip per tile.  Softmax is online within the block; every
-// block publishes (max, sum, o) and the last block of a KV head merges them
-// with log-sum-exp rescaling.  The order of operations differs from the
+// Work split: the context is cut into groups of 8 positions; block (KV head,
+// split) owns a contiguous run of groups and each of its NW waves takes every
+// NW-th group with an online-softmax state of its own, so the main loop has no
+// block barrier.  Lane (pj = lane / 8, ds = lane % 8) holds 16 dimensions of
+// position pj of the wave's current group: dims 32 i + 4 ds + e (i, e < 4) of
+// an f32 cache, 64 i + 8 ds + e (i < 2, e < 8) of a bf16 cache.  Either way
+// each load instruction covers whole 128-byte lines of 8 positions, and dims d
+// and d + 64 (a RoPE pair) sit in the same lane as slots k and k + 8.  A score
+// is a 16-term dot plus three xor shuffles; the softmax max and sum over the 8
+// positions take three more.  Each lane accumulates p_j v_j of its own
+// positions under the wave's running max; after the loop the lanes of a wave
+// are summed, the waves' states merged in LDS (one barrier) and the result
+// published as the block's partial (max, sum, o[128]).  The partials of a KV
+// head are merged by log-sum-exp either by its last block to finish (MERGE) or
+// by the o_proj kernel's prologue.  The order of operations differs from the
 // reference's sequential scan: results agree to f32 rounding, not bit for bit.
 // ---------------------------------------------------------------------------
-#define ATT_MAXC 256
 #define ATT_MAXS 64
-#define ATT_TP 32
 
-template <typename KVT> struct KvTile;
-template <> struct KvTile<float> {      // 32 x 128 f32 = 1024 float4, 4 per thread
-    static constexpr int N = 4;
-    float4 k[N], v[N];
-};
-template <> struct KvTile<uint16_t> {   // 32 x 128 bf16 = 512 uint4, 2 per thread
-    static constexpr int N = 2;
-    uint4 k[N], v[N];
-};
-
-template <typename KVT>
-__device__ __forceinline__ void tile_load(KvTile<KVT> &r, const KVT *kc, const KVT *vc, int j0, int j1, int skip) {
-    constexpr int PER_ROW = sizeof(KVT) == 4 ? 32 : 16;     // 16-byte vectors per position
+// 16 dimensions of one position in the lane layout of cache type T
+template <typename T> struct KvSlice;
+template <> struct KvSlice<float> {
+    float4 v[4];
+    static __device__ __forceinline__ int dim(int k, int ds) { return 32 * (k >> 2) + 4 * ds + (k & 3); }
+    __device__ __forceinline__ void load(const float *row, int ds) {
 #pragma unroll
-    for (int i = 0; i < KvTile<KVT>::N; i++) {
-        const int idx = threadIdx.x + 256 * i;
-        const int j = j0 + idx / PER_ROW, c = idx % PER_ROW;
-        const bool ok = j < j1 && j != skip;
-        const int jj = ok ? j : j0;
-        if (sizeof(KVT) == 4) {
-            const float4 kv = reinterpret_cast<const float4 *>(kc + (int64_t)jj * 128)[c];
-            const float4 vv = reinterpret_cast<const float4 *>(vc + (int64_t)jj * 128)[c];
-            reinterpret_cast<float4 *>(&r.k[i])[0] = kv;
-            reinterpret_cast<float4 *>(&r.v[i])[0] = vv;
-        } else {
-            const uint4 kv = reinterpret_cast<const uint4 *>(kc + (int64_t)jj * 128)[c];
-            const uint4 vv = reinterpret_cast<const uint4 *>(vc + (int64_t)jj * 128)[c];
-            reinterpret_cast<uint4 *>(&r.k[i])[0] = kv;
-            reinterpret_cast<uint4 *>(&r.v[i])[0] = vv;
+        for (int i = 0; i < 4; i++) v[i] = reinterpret_cast<const float4 *>(row + dim(4 * i, ds))[0];
+    }
+    __device__ __forceinline__ void to_f32(float o[16]) const {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[4 * i] = v[i].x; o[4 * i + 1] = v[i].y; o[4 * i + 2] = v[i].z; o[4 * i + 3] = v[i].w;
         }
     }
-}
-
-template <typename KVT>
-__device__ __forceinline__ void tile_store(const KvTile<KVT> &r, float (*Ks)[132], float (*Vs)[128]) {
-    constexpr int PER_ROW = sizeof(KVT) == 4 ? 32 : 16;
+    static __device__ __forceinline__ void store(float *row, int ds, const float o[16]) {
 #pragma unroll
-    for (int i = 0; i < KvTile<KVT>::N; i++) {
-        const int idx = threadIdx.x + 256 * i;
-        const int p = idx / PER_ROW, c = idx % PER_ROW;
-        if (sizeof(KVT) == 4) {
-            const float4 kv = reinterpret_cast<const float4 *>(&r.k[i])[0];
-            const float4 vv = reinterpret_cast<const float4 *>(&r.v[i])[0];
-            *reinterpret_cast<float4 *>(&Ks[p][4 * c]) = kv;
-            *reinterpret_cast<float4 *>(&Vs[p][4 * c]) = vv;
-        } else {
-            const uint4 kv = reinterpret_cast<const uint4 *>(&r.k[i])[0];
-            const uint4 vv = reinterpret_cast<const uint4 *>(&r.v[i])[0];
-            const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        for (int i = 0; i < 4; i++)
+            reinterpret_cast<float4 *>(row + dim(4 * i, ds))[0] =
+                make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    }
+};
+template <> struct KvSlice<uint16_t> {
+    uint4 v[2];
+    static __device__ __forceinline__ int dim(int k, int ds) { return 64 * (k >> 3) + 8 * ds + (k & 7); }
+    __device__ __forceinline__ void load(const uint16_t *row, int ds) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) v[i] = reinterpret_cast<const uint4 *>(row + dim(8 * i, ds))[0];
+    }
+    __device__ __forceinline__ void to_f32(float o[16]) const {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                Ks[p][8 * c + 2 * e] = __uint_as_float(kw[e] << 16);
-                Ks[p][8 * c + 2 * e + 1] = __uint_as_float(kw[e] & 0xFFFF0000u);
-                Vs[p][8 * c + 2 * e] = __uint_as_float(vw[e] << 16);
-                Vs[p][8 * c + 2 * e + 1] = __uint_as_float(vw[e] & 0xFFFF0000u);
+                o[8 * i + 2 * e] = __uint_as_float(w[e] << 16);
+                o[8 * i + 2 * e + 1] = __uint_as_float(w[e] & 0xFFFF0000u);
             }
         }
     }
+    static __device__ __forceinline__ void store(uint16_t *row, int ds, const float o[16]) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            uint32_t w[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                w[e] = (uint32_t)f32_to_bf16_rne(o[8 * i + 2 * e]) |
+                       ((uint32_t)f32_to_bf16_rne(o[8 * i + 2 * e + 1]) << 16);
+            reinterpret_cast<uint4 *>(row + dim(8 * i, ds))[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+    }
+};
+
+// 16 f32 values of a [128] vector in the lane layout of cache type T
+template <typename T>
+__device__ __forceinline__ void ld16(const float *v, int ds, float o[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; k += 4) {
+        const float4 x = reinterpret_cast<const float4 *>(v + KvSlice<T>::dim(k, ds))[0];
+        o[k] = x.x; o[k + 1] = x.y; o[k + 2] = x.z; o[k + 3] = x.w;
+    }
 }
 
-template <int G, typename KVT, bool MERGE>
-__global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
-    constexpr int D = 128, TP = ATT_TP;
-    static_assert(G * D == 256, "one thread per (query head, dim)");
-    __shared__ float Ks[TP][D + 4];
-    __shared__ float Vs[TP][D];
-    __shared__ float qs[G][D];
-    __shared__ float knew[D], vnew[D];
-    __shared__ float red[8];
-    __shared__ float ps[G][TP];
-    __shared__ float pv[2][G][D];
+// per-head RMSNorm then NeoX RoPE of one head's 16 lane slots (slot k + 8 is
+// dim d + 64); the 8 lanes of a position together hold the head's 128 dims
+__device__ __forceinline__ void norm_rope16(float x[16], const float w[16], const float c[16], const float s[16],
+                                            float eps) {
+    constexpr int D = 128;
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) ss = fmaf(x[k], x[k], ss);
+    ss = sum8(ss);
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = __fmul_rn(__fmul_rn(x[k], r), w[k]);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+        const float x1 = x[k], x2 = x[k + 8];
+        x[k] = __fadd_rn(__fmul_rn(x1, c[k]), __fmul_rn(-x2, s[k]));
+        x[k + 8] = __fadd_rn(__fmul_rn(x2, c[k + 8]), __fmul_rn(x1, s[k + 8]));
+    }
+}
+
+template <typename KVT, int NW, bool MERGE, bool DEC>
+__global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
+    constexpr int D = 128, G = 2;
+    using Sl = KvSlice<KVT>;
+    __shared__ float wm[NW][G], wl[NW][G];
+    __shared__ float wacc[NW][G][D];
     __shared__ float mw[G][ATT_MAXS], lw[G][ATT_MAXS];
     __shared__ int last;
     const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int pj = lane >> 3, ds = lane & 7;
     const int n_split = a.n_split;
     const int kvh = blockIdx.x / n_split, split = blockIdx.x % n_split;
     const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
-    const int pos = a.state ? a.state[1] : a.pos;
-    const int L = pos + 1;
-    const int chunk = (L + n_split - 1) / n_split;
-    const int j0 = split * chunk, j1 = min(L, j0 + chunk);
-    const bool prep = a.q_norm != nullptr;     // raw projections: norm + rope + cache write
-    const bool own_pos = prep && j0 <= pos && pos < j1;
-    const int skip = own_pos ? pos : -1;
+    constexpr bool prep = DEC;                           // raw projections: norm + rope + cache write
     KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
     KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
-    const int gi = t / D, d = t % D;
 
-    // ---- issue the small operand loads, then the first tile ---------------
-    float qv = a.qkv[(kvh * G + gi) * D + d];
-    float cv = 0.0f, sv = 0.0f, kraw = 0.0f, vraw = 0.0f;
-    if (prep) {
-        cv = a.rope_cos[(int64_t)pos * D + d];
-        sv = a.rope_sin[(int64_t)pos * D + d];
-    }
-    if (own_pos && t < D) {
-        kraw = a.qkv[Hq * D + kvh * D + d];
-        vraw = a.qkv[Hq * D + Hkv * D + kvh * D + d];
-    }
-    KvTile<KVT> tr;
-    if (j0 < j1) tile_load<KVT>(tr, kc, vc, j0, min(j1, j0 + TP), skip);
-
-    // ---- query heads of this group: per-head RMSNorm + RoPE --------------
-    if (prep) {
-        const float ss = head_sum128(__fmul_rn(qv, qv), red);
-        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
-        qv = __fmul_rn(__fmul_rn(qv, r), a.q_norm[d]);
-        qs[gi][d] = qv;
-        __syncthreads();
-        const int h = D / 2;
-        float o;
-        if (d < h) o = __fadd_rn(__fmul_rn(qv, cv), __fmul_rn(-qs[gi][d + h], sv));
-        else o = __fadd_rn(__fmul_rn(qv, cv), __fmul_rn(qs[gi][d - h], sv));
-        __syncthreads();
-        qs[gi][d] = o;
+    // ---- loads, all issued before the first wait.  Decode-step mode (DEC):
+    // the block owns groups [split gpb, (split + 1) gpb) whatever the
+    // position, so the first two groups of each wave are requested before the
+    // position (device state) arrives; rows past the cache read row 0 and
+    // everything past the context is masked later (the new K/V row's slot is
+    // read too and replaced).  The RoPE rows of the position come from
+    // rope_cur.  Operator mode: the position is an argument and the context is
+    // split evenly.  Every load is unconditional (dummy addresses when unused):
+    // a branch around a load makes the compiler wait for it at the join.
+    Sl ka, va, kb, vb;
+    float q[G][16];
+    float cs[16], sn[16], qn[16], kn[16], vn[16], knw[16];
+    int pos, g0, g1s;
+    if constexpr (DEC) {
+        const int max_rows = (int)(a.head_stride / D);
+        g0 = split * a.gpb;
+        g1s = g0 + a.gpb;
+        const int ja = 8 * (g0 + wid) + pj, jb = ja + 8 * NW;
+        const int ra = ja < max_rows ? ja : 0, rb = jb < max_rows ? jb : 0;
+        ka.load(kc + (int64_t)ra * D, ds);
+        va.load(vc + (int64_t)ra * D, ds);
+        kb.load(kc + (int64_t)rb * D, ds);
+        vb.load(vc + (int64_t)rb * D, ds);
+#pragma unroll
+        for (int g = 0; g < G; g++) ld16<KVT>(a.qkv + (kvh * G + g) * D, ds, q[g]);
+        ld16<KVT>(a.q_norm, ds, qn);
+        ld16<KVT>(a.k_norm, ds, knw);
+        ld16<KVT>(a.qkv + Hq * D + kvh * D, ds, kn);
+        ld16<KVT>(a.qkv + Hq * D + Hkv * D + kvh * D, ds, vn);
+        ld16<KVT>(a.rope_cur, ds, cs);
+        ld16<KVT>(a.rope_cur + D, ds, sn);
+        pos = a.state[1];
     } else {
-        qs[gi][d] = qv;
+        pos = a.pos;
+        const int n_grp = (pos + 8) >> 3;
+        const int gpb = (n_grp + n_split - 1) / n_split;
+        g0 = split * gpb;
+        g1s = g0 + gpb;
+        const int j0 = 8 * g0, j1 = min(pos + 1, 8 * min(n_grp, g1s));
+        const int ja = 8 * (g0 + wid) + pj, jb = ja + 8 * NW;
+        const int ra = ja < j1 ? ja : j0, rb = jb < j1 ? jb : j0;
+        ka.load(kc + (int64_t)ra * D, ds);
+        va.load(vc + (int64_t)ra * D, ds);
+        kb.load(kc + (int64_t)rb * D, ds);
+        vb.load(vc + (int64_t)rb * D, ds);
+#pragma unroll
+        for (int g = 0; g < G; g++) ld16<KVT>(a.qkv + (kvh * G + g) * D, ds, q[g]);
     }
-    // ---- new K/V row (the block whose range holds pos) --------------------
-    if (own_pos) {
-        const float ss = head_sum128(t < D ? __fmul_rn(kraw, kraw) : 0.0f, red);
-        float kv = 0.0f;
-        if (t < D) {
-            const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), a.eps)));
-            kv = __fmul_rn(__fmul_rn(kraw, r), a.k_norm[d]);
-            knew[d] = kv;
-        }
-        __syncthreads();
-        float o = 0.0f;
-        if (t < D) {
-            const int h = D / 2;
-            if (d < h) o = __fadd_rn(__fmul_rn(kv, cv), __fmul_rn(-knew[d + h], sv));
-            else o = __fadd_rn(__fmul_rn(kv, cv), __fmul_rn(knew[d - h], sv));
-            kc[(int64_t)pos * D + d] = st_kv<KVT>(o);
-            vc[(int64_t)pos * D + d] = st_kv<KVT>(vraw);
-        }
-        __syncthreads();
-        if (t < D) {   // the values the cache now holds (a bf16 cache rounds)
-            knew[d] = round_kv<KVT>(o);
-            vnew[d] = round_kv<KVT>(vraw);
-        }
-    }
-    __syncthreads();
+    const int L = pos + 1;
+    const int n_grp = (L + 7) >> 3;
+    const int g1 = min(n_grp, g1s);
+    const int j0 = 8 * g0, j1 = min(L, 8 * g1);
+    const bool own_pos = prep && j0 <= pos && pos < j1;
+    const int skip = own_pos ? pos : -1;
+    // rows of group grp once the context is known: out-of-range and the new
+    // position read row j0 (< j1 whenever the block has a group to stream)
+    auto row_of = [&](int grp) {
+        const int j = 8 * grp + pj;
+        return (j < j1 && j != skip) ? j : j0;
+    };
+    __builtin_amdgcn_sched_barrier(0);
 
-    // ---- stream the range in tiles -----------------------------------------
-    // scores: thread t -> position p = t / 8, dims (t % 8) * 16 .. +16
-    const int sp = t >> 3, sd = (t & 7) * 16;
-    float qreg[G][16];
+    // ---- query heads: per-head RMSNorm + RoPE; the new K/V row -------------
+    if (prep) {
 #pragma unroll
-    for (int g = 0; g < G; g++)
+        for (int g = 0; g < G; g++) norm_rope16(q[g], qn, cs, sn, a.eps);
+    }
+    if (own_pos) {
+        norm_rope16(kn, knw, cs, sn, a.eps);
 #pragma unroll
-        for (int i = 0; i < 16; i++) qreg[g][i] = qs[g][sd + i];
-    float m_run[G], l_run[G], acc[G];
-#pragma unroll
-    for (int g = 0; g < G; g++) { m_run[g] = -INFINITY; l_run[g] = 0.0f; acc[g] = 0.0f; }
-    const int hh = t / D;                    // PV: thread (hh, d) takes positions p = hh, hh + 2, ...
-    for (int b = j0; b < j1; b += TP) {
-        const int n = min(TP, j1 - b);
-        tile_store<KVT>(tr, Ks, Vs);
-        __syncthreads();
-        if (own_pos && pos >= b && pos < b + n) {          // the new row comes from LDS
-            if (t < D) { Ks[pos - b][t] = knew[t]; Vs[pos - b][t] = vnew[t]; }
-            __syncthreads();
+        for (int k = 0; k < 16; k++) {     // the values the cache holds (a bf16 cache rounds)
+            kn[k] = round_kv<KVT>(kn[k]);
+            vn[k] = round_kv<KVT>(vn[k]);
         }
-        if (b + TP < j1) tile_load<KVT>(tr, kc, vc, b + TP, min(j1, b + 2 * TP), skip);   // prefetch
-        float sc[G];
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float p = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; i++) p = fmaf(qreg[g][i], Ks[sp][sd + i], p);
-            p = group_sum_f32<8>(p);
-            sc[g] = p;
+        if (wid == 0 && pj == 0) {
+            Sl::store(kc + (int64_t)pos * D, ds, kn);
+            Sl::store(vc + (int64_t)pos * D, ds, vn);
         }
-        if ((t & 7) == 0) {
+    }
+
+    // ---- stream this wave's groups (two in flight) -------------------------
+    float m[G], l[G], acc[G][16];
 #pragma unroll
-            for (int g = 0; g < G; g++) ps[g][sp] = sp < n ? __fmul_rn(sc[g], a.scale) : -INFINITY;
-        }
-        __syncthreads();
-        // online softmax update (every thread keeps the block-wide state of each head)
-        float corr[G];
+    for (int g = 0; g < G; g++) {
+        m[g] = -INFINITY;
+        l[g] = 0.0f;
 #pragma unroll
-        for (int g = 0; g < G; g++) {
-            float tm = -INFINITY;
-            for (int p = 0; p < n; p++) tm = fmaxf(tm, ps[g][p]);
-            const float mn = fmaxf(m_run[g], tm);
-            corr[g] = m_run[g] == -INFINITY ? 0.0f : expf(__fsub_rn(m_run[g], mn));
-            m_run[g] = mn;
+        for (int k = 0; k < 16; k++) acc[g][k] = 0.0f;
+    }
+    const float scale = a.scale;
+    auto consume = [&](const Sl &kt, const Sl &vt, int grp) {
+        float kf[16], vf[16];
+        kt.to_f32(kf);
+        vt.to_f32(vf);
+        const int j = 8 * grp + pj;
+        const bool valid = j < j1;
+        if (j == skip) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) { kf[k] = kn[k]; vf[k] = vn[k]; }
         }
-        __syncthreads();
-        if (t < G * TP) {
-            const int g = t / TP, p = t % TP;
-            ps[g][p] = p < n ? expf(__fsub_rn(ps[g][p], m_run[g])) : 0.0f;
-        }
-        __syncthreads();
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float s = 0.0f;
-            for (int p = 0; p < n; p++) s = __fadd_rn(s, ps[g][p]);
-            l_run[g] = fmaf(l_run[g], corr[g], s);
-            acc[g] = __fmul_rn(acc[g], corr[g]);
-        }
-        for (int p = hh; p < n; p += 2) {
-            const float vv = Vs[p][d];
 #pragma unroll
-            for (int g = 0; g < G; g++) acc[g] = fmaf(ps[g][p], vv, acc[g]);
+            for (int k = 0; k < 16; k++) s = fmaf(q[g][k], kf[k], s);
+            s = sum8(s);
+            s = valid ? __fmul_rn(s, scale) : -INFINITY;
+            const float mn = fmaxf(m[g], max_x8(s));           // finite: a group has a valid position
+            const float corr = m[g] == -INFINITY ? 0.0f : expf(__fsub_rn(m[g], mn));
+            const float p = valid ? expf(__fsub_rn(s, mn)) : 0.0f;
+            l[g] = fmaf(l[g], corr, sum_x8(p));
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc[g][k] = fmaf(p, vf[k], __fmul_rn(acc[g][k], corr));
+            m[g] = mn;
         }
-        __syncthreads();
+    };
+    auto load = [&](Sl &kt, Sl &vt, int grp) {
+        const int j = row_of(grp);
+        kt.load(kc + (int64_t)j * D, ds);
+        vt.load(vc + (int64_t)j * D, ds);
+    };
+    for (int gi = g0 + wid; gi < g1; gi += 2 * NW) {
+        consume(ka, va, gi);
+        if (gi + 2 * NW < g1) load(ka, va, gi + 2 * NW);
+        const int gb = gi + NW;
+        if (gb < g1) {
+            consume(kb, vb, gb);
+            if (gb + 2 * NW < g1) load(kb, vb, gb + 2 * NW);
+        }
     }
+
+    // ---- merge the lanes of each wave, then the waves of the block ----------
 #pragma unroll
-    for (int g = 0; g < G; g++) pv[hh][g][d] = acc[g];
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc[g][k] = sum_x8(acc[g][k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) { wm[wid][g] = m[g]; wl[wid][g] = l[g]; }
+    }
+    if (pj == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int k = 0; k < 16; k++) wacc[wid][g][Sl::dim(k, ds)] = acc[g][k];
+    }
     __syncthreads();
-    float *part = a.part + ((int64_t)kvh * n_split + split) * G * (D + 2);
-    const float o_part = __fadd_rn(pv[0][gi][d], pv[1][gi][d]);
-    const float m_part = j1 > j0 ? m_run[gi] : -INFINITY, l_part = j1 > j0 ? l_run[gi] : 0.0f;
+    const int gq = (t >> 7) & 1, d = t & 127;    // threads t < 256: (query head, dim)
+    float o_part = 0.0f, m_part = -INFINITY, l_part = 0.0f;
+    if (t < G * D) {
+#pragma unroll
+        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w][gq]);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = wm[w][gq] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w][gq], m_part));
+            o_part = fmaf(wacc[w][gq][d], f, o_part);
+            l_part = fmaf(wl[w][gq], f, l_part);
+        }
+    }
     if (!MERGE) {
-        // the consumer (the o_proj kernel) merges; the kernel boundary publishes these
-        part[gi * (D + 2) + 2 + d] = o_part;
-        if (d == 0) {
-            part[gi * (D + 2)] = m_part;
-            part[gi * (D + 2) + 1] = l_part;
+        // the consumer (the o_proj kernel) merges; the kernel boundary publishes
+        // these.  Layout, split index fastest: (m, l) of head h = G kvh + gq at
+        // [(2 h + {0,1}) S + split], o at [2 Hq S + (D h + d) S + split].
+        if (t < G * D) {
+            const int h = kvh * G + gq;
+            a.part[(int64_t)(2 * Hq + h * D + d) * n_split + split] = o_part;
+            if (d == 0) {
+                a.part[(2 * h) * n_split + split] = m_part;
+                a.part[(2 * h + 1) * n_split + split] = l_part;
+            }
         }
         return;
     }
-    st_agent(part + gi * (D + 2) + 2 + d, o_part);
-    if (d == 0) {
-        st_agent(part + gi * (D + 2), m_part);
-        st_agent(part + gi * (D + 2) + 1, l_part);
+    float *part = a.part + ((int64_t)kvh * n_split + split) * G * (D + 2);
+    if (t < G * D) {
+        st_agent(part + gq * (D + 2) + 2 + d, o_part);
+        if (d == 0) {
+            st_agent(part + gq * (D + 2), m_part);
+            st_agent(part + gq * (D + 2) + 1, l_part);
+        }
     }
     if (!arrive_last(a.counters + kvh, (unsigned)n_split, &last)) return;
     // ---- last block of this KV head: log-sum-exp merge of the n_split partials
     const float *pb = a.part + (int64_t)kvh * n_split * G * (D + 2);
-    for (int i = t; i < n_split * G; i += 256) {
+    for (int i = t; i < n_split * G; i += NW * 64) {
         const int s = i / G, g = i % G;
         mw[g][s] = ld_agent(pb + (s * G + g) * (D + 2));
         lw[g][s] = ld_agent(pb + (s * G + g) * (D + 2) + 1);
@@ -307,19 +341,19 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnDecodeArgs a) {
         lw[t][0] = lt;
     }
     __syncthreads();
-    {
+    if (t < G * D) {
         float ot = 0.0f;
         for (int s0 = 0; s0 < n_split; s0 += 8) {
             float ov[8];
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                ov[i] = s0 + i < n_split ? ld_agent(pb + ((s0 + i) * G + gi) * (D + 2) + 2 + d) : 0.0f;
+                ov[i] = s0 + i < n_split ? ld_agent(pb + ((s0 + i) * G + gq) * (D + 2) + 2 + d) : 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; i++)
-                if (s0 + i < n_split) ot = fmaf(ov[i], mw[gi][s0 + i], ot);
+                if (s0 + i < n_split) ot = fmaf(ov[i], mw[gq][s0 + i], ot);
         }
-        const float lt = lw[gi][0];
-        a.out[(kvh * G + gi) * D + d] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
+        const float lt = lw[gq][0];
+        a.out[(kvh * G + gq) * D + d] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
     }
     if (t == 0) reset_counter(a.counters + kvh);
 }
@@ -328,14 +362,25 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
                               int kv_bf16, hipStream_t st, bool merge) {
     if (head_dim != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads) return hipErrorInvalidValue;
     if (a.n_split <= 0 || a.n_split > ATT_MAXS) return hipErrorInvalidValue;
+    if (a.waves != 0 && a.waves != 4 && a.waves != 8) return hipErrorInvalidValue;
+    // decode-step mode: every pointer of the fused prologue, the state and a static partition
+    const bool dec = a.q_norm != nullptr;
+    if (dec && (!a.k_norm || !a.rope_cur || !a.state || a.gpb <= 0 || a.head_stride < 128)) return hipErrorInvalidValue;
     const dim3 grid(n_kv_heads * a.n_split);
-    if (merge) {
-        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<2, uint16_t, true>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_attn_decode<2, float, true>), grid, dim3(256), 0, st, a);
-    } else {
-        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<2, uint16_t, false>), grid, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((k_attn_decode<2, float, false>), grid, dim3(256), 0, st, a);
+#define QASR_ATT(NW, DEC)                                                                           \
+    if (merge) {                                                                                     \
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, true, DEC>), grid, dim3(NW * 64), 0, st, a); \
+        else hipLaunchKernelGGL((k_attn_decode<float, NW, true, DEC>), grid, dim3(NW * 64), 0, st, a);            \
+    } else {                                                                                         \
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, DEC>), grid, dim3(NW * 64), 0, st, a); \
+        else hipLaunchKernelGGL((k_attn_decode<float, NW, false, DEC>), grid, dim3(NW * 64), 0, st, a);           \
     }
+    if (dec) {
+        if (a.waves == 4) { QASR_ATT(4, true) } else { QASR_ATT(8, true) }
+    } else {
+        QASR_ATT(4, false)
+    }
+#undef QASR_ATT
     return hipGetLastError();
 }
 

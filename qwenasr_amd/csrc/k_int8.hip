@@ -54,39 +54,71 @@ __global__ __launch_bounds__(256) void k_pack_int8_rows(const uint16_t *__restri
 // ---------------------------------------------------------------------------
 template <int NS, bool NORM, bool EMBED>
 struct ActIn {
+    float4 xf[EMBED ? 1 : NS][4];     // raw f32 activation loads
+    uint4 xb[EMBED ? NS : 1][2];      // raw bf16 embedding-row loads
+    float4 wf[NORM ? NS : 1][4];      // raw RMSNorm gain loads
     float xv[NS][16];
     float wn[NORM ? NS : 1][16];
 };
 
-// Phase 1: issue the loads of the lane's activation slice (and RMSNorm gains).
-// Called before the weight loads: vmcnt retires loads in issue order, so these
-// small L2-resident reads complete while the weight stream is still in flight.
+// Phase 1: issue the loads of the lane's activation slice (and RMSNorm gains)
+// into raw registers, nothing else.  Callers issue their weight loads right
+// after and then place a scheduling barrier, so no instruction that consumes
+// these values (and would make the wave wait for them) can be hoisted above
+// the weight loads: the weight stream is in flight before the wave first
+// waits on memory.  vmcnt retires loads in issue order, so these small
+// L2-resident reads are the first to complete.
 template <int NS, bool NORM, bool EMBED>
 __device__ __forceinline__ void act_load(const float *__restrict__ x, const uint16_t *__restrict__ xe,
-                                         const float *__restrict__ norm_w, int K, ActIn<NS, NORM, EMBED> &in,
-                                         float *__restrict__ resid_out) {
+                                         const float *__restrict__ norm_w, int K, ActIn<NS, NORM, EMBED> &in) {
     const int lane = threadIdx.x & 63;
     const int nslot = K >> 4;
-    // branch-free: out-of-range slots load slot 0 and are zeroed by a select
+    // out-of-range slots load slot 0; act_convert zeroes them
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int s = lane + 64 * c;
+        const int se = s < nslot ? s : 0;
+        if (EMBED) {
+            const uint4 *p = reinterpret_cast<const uint4 *>(xe + 16 * se);
+            in.xb[c][0] = p[0];
+            in.xb[c][1] = p[1];
+        } else {
+            const float4 *p = reinterpret_cast<const float4 *>(x + 16 * se);
+#pragma unroll
+            for (int i = 0; i < 4; i++) in.xf[c][i] = p[i];
+        }
+        if (NORM) {
+            const float4 *wp = reinterpret_cast<const float4 *>(norm_w + 16 * se);
+#pragma unroll
+            for (int i = 0; i < 4; i++) in.wf[c][i] = wp[i];
+        }
+    }
+}
+
+// Phase 1b: raw loads -> f32 slots (zero beyond K); optionally stores the f32
+// slice to resid_out (the embedding row becomes the residual stream).
+template <int NS, bool NORM, bool EMBED>
+__device__ __forceinline__ void act_convert(ActIn<NS, NORM, EMBED> &in, int K, float *__restrict__ resid_out) {
+    const int lane = threadIdx.x & 63;
+    const int nslot = K >> 4;
 #pragma unroll
     for (int c = 0; c < NS; c++) {
         const int s = lane + 64 * c;
         const bool ok = s < nslot;
-        const int se = ok ? s : 0;
         if (EMBED) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(xe + 16 * se);
-            const uint4 a = p[0], b = p[1];
-            const uint32_t wds[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                in.xv[c][2 * i] = ok ? __uint_as_float(wds[i] << 16) : 0.0f;
-                in.xv[c][2 * i + 1] = ok ? __uint_as_float(wds[i] & 0xFFFF0000u) : 0.0f;
+            for (int h = 0; h < 2; h++) {
+                const uint32_t wds[4] = {in.xb[c][h].x, in.xb[c][h].y, in.xb[c][h].z, in.xb[c][h].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    in.xv[c][8 * h + 2 * i] = ok ? __uint_as_float(wds[i] << 16) : 0.0f;
+                    in.xv[c][8 * h + 2 * i + 1] = ok ? __uint_as_float(wds[i] & 0xFFFF0000u) : 0.0f;
+                }
             }
         } else {
-            const float4 *p = reinterpret_cast<const float4 *>(x + 16 * se);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 v = p[i];
+                const float4 v = in.xf[c][i];
                 in.xv[c][4 * i] = ok ? v.x : 0.0f;
                 in.xv[c][4 * i + 1] = ok ? v.y : 0.0f;
                 in.xv[c][4 * i + 2] = ok ? v.z : 0.0f;
@@ -94,10 +126,9 @@ __device__ __forceinline__ void act_load(const float *__restrict__ x, const uint
             }
         }
         if (NORM) {
-            const float4 *wp = reinterpret_cast<const float4 *>(norm_w + 16 * se);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 v = wp[i];
+                const float4 v = in.wf[c][i];
                 in.wn[c][4 * i] = v.x; in.wn[c][4 * i + 1] = v.y;
                 in.wn[c][4 * i + 2] = v.z; in.wn[c][4 * i + 3] = v.w;
             }
@@ -211,17 +242,35 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
     if (EMBED) xe = a.embed + (int64_t)a.state[0] * K;
     float *resid = (EMBED && blockIdx.x == 0 && wid == 0) ? a.resid_out : nullptr;
     ActIn<NS, NORM, EMBED> in;
-    act_load<NS, NORM, EMBED>(a.x, xe, a.norm_w, K, in, resid);
+    act_load<NS, NORM, EMBED>(a.x, xe, a.norm_w, K, in);
+    // weight slots beyond K load slot 0; their activation bytes are zero
     i32x4 wv[R][NS];
 #pragma unroll
     for (int r = 0; r < R; r++)
 #pragma unroll
         for (int c = 0; c < NS; c++) {
             const int s = lane + 64 * c;
-            const i32x4 v = __builtin_nontemporal_load(
+            wv[r][c] = __builtin_nontemporal_load(
                 reinterpret_cast<const i32x4 *>(S.w + (int64_t)(lrow0 + r) * K) + (s < nslot ? s : 0));
-            wv[r][c] = s < nslot ? v : i32x4{0, 0, 0, 0};
         }
+    // epilogue operands (row scales, the old y of +=, the bias), loaded with the
+    // weights so that no load is left on the path after the dot products.
+    // SwiGLU: lane j < R/2 owns the gate/up row pair (2j, 2j+1); otherwise lane r < R owns row r.
+    // (Vector loads on purpose: as scalar loads of uniform addresses they get
+    // scheduled after the dot products.)
+    float ws0 = 0.0f, ws1 = 0.0f, yb = 0.0f;
+    if (MODE == MV_SWIGLU) {
+        const int j = lane < R / 2 ? lane : 0;
+        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * j);
+        ws1 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * j + 1);
+    } else {
+        const int r = lane < R ? lane : 0;
+        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + r);
+        if (MODE == MV_ADDTO) yb = __builtin_nontemporal_load(S.y + lrow0 + r);
+        if (MODE == MV_BIAS) yb = __builtin_nontemporal_load(a.bias + lrow0 + r);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    act_convert<NS, NORM, EMBED>(in, K, resid);
     int xd[NS][4];
     float xs;
     act_finish<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
@@ -233,70 +282,102 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
         for (int c = 0; c < NS; c++) t = dot16(wv[r][c], xd[c], t);
         acc[r] = wave_sum_i32(t);
     }
+    // The epilogue runs in every lane with no branch: lanes past the owners
+    // recompute the first owner's value and store it to the same address.  A
+    // predicated store would let the compiler sink the operand loads above
+    // into the branch, after the dot products.
     if (MODE == MV_SWIGLU) {
-        if (lane < R / 2) {
-            float g = 0.0f, u = 0.0f;
+        const int j = lane < R / 2 ? lane : 0;
+        int ag = 0, au = 0;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const float v = __fmul_rn(__fmul_rn((float)acc[r], xs), S.ws[lrow0 + r]);
-                if (r == 2 * lane) g = v;
-                if (r == 2 * lane + 1) u = v;
-            }
-            S.y[(lrow0 >> 1) + lane] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        for (int r = 0; r < R; r++) {
+            if (r == 2 * j) ag = acc[r];
+            if (r == 2 * j + 1) au = acc[r];
         }
+        const float g = __fmul_rn(__fmul_rn((float)ag, xs), ws0);
+        const float u = __fmul_rn(__fmul_rn((float)au, xs), ws1);
+        S.y[(lrow0 >> 1) + j] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
     } else {
-        if (lane < R) {
-            int av = 0;
+        const int rl = lane < R ? lane : 0;
+        int av = 0;
 #pragma unroll
-            for (int r = 0; r < R; r++) if (r == lane) av = acc[r];
-            const int row = lrow0 + lane;
-            float v = __fmul_rn(__fmul_rn((float)av, xs), S.ws[row]);
-            if (MODE == MV_ADDTO) v = __fadd_rn(v, S.y[row]);
-            if (MODE == MV_BIAS) v = __fadd_rn(v, a.bias[row]);
-            S.y[row] = v;
-        }
+        for (int r = 0; r < R; r++) if (r == rl) av = acc[r];
+        float v = __fmul_rn(__fmul_rn((float)av, xs), ws0);
+        if (MODE == MV_ADDTO || MODE == MV_BIAS) v = __fadd_rn(v, yb);
+        S.y[lrow0 + rl] = v;
     }
 }
 
 // ---------------------------------------------------------------------------
 // o_proj of the decode step with the split-attention merge in front
 // (causal_attention's result, mod.rs:1527-1535, then linear_nobias_int8_addto,
-// decoder.rs:616-617).  The attention kernel leaves n_split partials
-// (max, sum, o[128]) per query head; every block loads them (L2/MALL), merges
-// with log-sum-exp weights into LDS, and its waves quantize the merged vector
-// as the activation of a 4-rows-per-wave W8A8 addto matvec.  The partial loads
-// are issued before the weight loads so the merge overlaps the weight stream.
+// decoder.rs:616-617).  The attention kernel leaves S partials per query head
+// h = 2 kvh + g: max m and sum l at part[(2h + {0,1}) S + s], and o[128] at
+// part[32 S + (128 h + d) S + s] (split index fastest).  Every block merges
+// all 16 heads into LDS: thread (g, d) loads its 8 heads' S partials as
+// vectors, threads t < 16 S turn (m, l) into log-sum-exp weights with 8-lane
+// DPP reductions; then each wave quantizes the merged vector (the activation
+// of a W8A8 += matvec, R = 4 rows per wave).  All loads (partials, weights,
+// epilogue operands) are issued before the first wait.
 // ---------------------------------------------------------------------------
-#define OM_MAXS 8
+template <int S>
+__device__ __forceinline__ void ld_split(const float *p, float (&v)[S]) {
+    if constexpr (S >= 8) {
+#pragma unroll
+        for (int i = 0; i < S / 4; i++) {
+            const float4 a = reinterpret_cast<const float4 *>(p)[i];
+            v[4 * i] = a.x; v[4 * i + 1] = a.y; v[4 * i + 2] = a.z; v[4 * i + 3] = a.w;
+        }
+    } else if constexpr (S == 8) {
+        const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else if constexpr (S == 4) {
+        const float4 a = reinterpret_cast<const float4 *>(p)[0];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    } else if constexpr (S == 2) {
+        const float2 a = reinterpret_cast<const float2 *>(p)[0];
+        v[0] = a.x; v[1] = a.y;
+    } else {
+        v[0] = p[0];
+    }
+}
+// max / sum over aligned groups of S lanes (S = 1, 2, 4, 8, 16; row_mirror
+// pairs the two 8-lane halves of a 16-lane row)
+template <int S>
+__device__ __forceinline__ float split_max(float v) {
+    if (S >= 2) v = fmaxf(v, dpp_f32<QASR_DPP_QP_1032>(v));
+    if (S >= 4) v = fmaxf(v, dpp_f32<QASR_DPP_QP_2301>(v));
+    if (S >= 8) v = fmaxf(v, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(v));
+    if (S >= 16) v = fmaxf(v, dpp_f32<QASR_DPP_ROW_MIRROR>(v));
+    return v;
+}
+template <int S>
+__device__ __forceinline__ float split_sum(float v) {
+    if (S >= 2) v = __fadd_rn(v, dpp_f32<QASR_DPP_QP_1032>(v));
+    if (S >= 4) v = __fadd_rn(v, dpp_f32<QASR_DPP_QP_2301>(v));
+    if (S >= 8) v = __fadd_rn(v, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(v));
+    if (S >= 16) v = __fadd_rn(v, dpp_f32<QASR_DPP_ROW_MIRROR>(v));
+    return v;
+}
+
+template <int S>
 __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
-    constexpr int D = 128, G = 2, NS = 2, R = 4, HQ = 16, K = HQ * D;
+    constexpr int D = 128, NS = 2, R = 4, HQ = 16, K = HQ * D;
     __shared__ float att[K];
-    __shared__ float ms[HQ][OM_MAXS], ls[HQ][OM_MAXS], wf[HQ][OM_MAXS], lsum[HQ];
+    __shared__ float fw[HQ][S], lsum[HQ];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int S = a.n_split;
+    const int g = t >> 7, d = t & 127;
+    // (1) this thread's o partials: heads h = 2 j + g, dim d, all splits
+    const float *po = a.part + 2 * HQ * S;
+    float ov[HQ / 2][S];
+#pragma unroll
+    for (int j = 0; j < HQ / 2; j++) ld_split<S>(po + ((2 * j + g) * D + d) * S, ov[j]);
+    // (m, l) of entry e = (head, split) = (e / S, e % S); threads past 16 S reload entry t % (16 S)
+    const int e = t % (HQ * S), eh = e / S, es = e % S;
+    const float pm = a.part[(2 * eh) * S + es], pl = a.part[(2 * eh + 1) * S + es];
+    // (2) weights and epilogue operands of this wave's rows (rows past N read row 0 and are not stored)
     const int row0 = (blockIdx.x * 4 + wid) * R;
-    // (1) partial statistics and outputs of this thread
-    float pm = -INFINITY, pl = 0.0f;
-    if (t < HQ * S) {
-        const int h = t / S, sp = t % S, kvh = h / G, g = h % G;
-        const float *b = a.part + ((int64_t)(kvh * S + sp) * G + g) * (D + 2);
-        pm = b[0];
-        pl = b[1];
-    }
-    float ov[K / 256][OM_MAXS];
-#pragma unroll
-    for (int j = 0; j < K / 256; j++) {
-        const int i = t + 256 * j, h = i / D, d = i % D, kvh = h / G, g = h % G;
-#pragma unroll
-        for (int sp = 0; sp < OM_MAXS; sp++) {
-            const int se = sp < S ? sp : 0;
-            const float v = a.part[((int64_t)(kvh * S + se) * G + g) * (D + 2) + 2 + d];
-            ov[j][sp] = sp < S ? v : 0.0f;
-        }
-    }
-    // (2) weights of this wave's rows
-    const int nslot = K >> 4;
     const bool live = row0 < a.N;
     const int r0 = live ? row0 : 0;
     i32x4 wv[R][NS];
@@ -306,36 +387,32 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
         for (int c = 0; c < NS; c++)
             wv[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(a.w + (int64_t)(r0 + r) * K) +
                                                   lane + 64 * c);
-    // (3) log-sum-exp weights per head
-    if (t < HQ * S) {
-        ms[t / S][t % S] = pm;
-        ls[t / S][t % S] = pl;
-    }
-    __syncthreads();
-    if (t < HQ) {
-        float M = -INFINITY;
-        for (int sp = 0; sp < S; sp++) M = fmaxf(M, ms[t][sp]);
-        float lt = 0.0f;
-        for (int sp = 0; sp < S; sp++) {
-            const float f = ms[t][sp] == -INFINITY ? 0.0f : expf(__fsub_rn(ms[t][sp], M));
-            wf[t][sp] = f;
-            lt = fmaf(ls[t][sp], f, lt);
+    const int rl = lane < R ? lane : 0;
+    const float ws0 = __builtin_nontemporal_load(a.ws + r0 + rl);
+    const float yb = __builtin_nontemporal_load(a.y + r0 + rl);
+    __builtin_amdgcn_sched_barrier(0);
+    // (3) log-sum-exp weights per (head, split)
+    {
+        const float M = split_max<S>(pm);
+        const float f = pm == -INFINITY ? 0.0f : expf(__fsub_rn(pm, M));
+        const float lt = split_sum<S>(__fmul_rn(pl, f));
+        if (t < HQ * S) {
+            fw[eh][es] = f;
+            if (es == 0) lsum[eh] = lt;
         }
-        lsum[t] = lt;
     }
     __syncthreads();
-    // (4) merged attention output
+    // (4) merged attention output of heads 2 j + g, dim d
 #pragma unroll
-    for (int j = 0; j < K / 256; j++) {
-        const int i = t + 256 * j, h = i / D;
+    for (int j = 0; j < HQ / 2; j++) {
+        const int h = 2 * j + g;
         float ot = 0.0f;
 #pragma unroll
-        for (int sp = 0; sp < OM_MAXS; sp++)
-            if (sp < S) ot = fmaf(ov[j][sp], wf[h][sp], ot);
-        att[i] = lsum[h] > 0.0f ? __fdiv_rn(ot, lsum[h]) : 0.0f;
+        for (int s = 0; s < S; s++) ot = fmaf(ov[j][s], fw[h][s], ot);
+        const float lt = lsum[h];
+        att[h * D + d] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
     }
     __syncthreads();
-    if (!live) return;
     // (5) quantize (each wave covers the whole vector with its lanes' slots)
     ActIn<NS, false, false> in;
 #pragma unroll
@@ -350,8 +427,7 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     int xd[NS][4];
     float xs;
     act_finish<NS, false, false>(in, 0.0f, K, nullptr, xd, &xs);
-    (void)nslot;
-    // (6) dots and the residual-add epilogue
+    // (6) dots and the residual-add epilogue (branch-free: extra lanes repeat lane 0's row)
     int acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -360,20 +436,24 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
         for (int c = 0; c < NS; c++) q = dot16(wv[r][c], xd[c], q);
         acc[r] = wave_sum_i32(q);
     }
-    if (lane < R) {
-        int av = 0;
+    int av = 0;
 #pragma unroll
-        for (int r = 0; r < R; r++) if (r == lane) av = acc[r];
-        const int row = row0 + lane;
-        const float v = __fmul_rn(__fmul_rn((float)av, xs), a.ws[row]);
-        a.y[row] = __fadd_rn(v, a.y[row]);
-    }
+    for (int r = 0; r < R; r++) if (r == rl) av = acc[r];
+    const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)av, xs), ws0), yb);
+    if (live) a.y[r0 + rl] = v;
 }
 
 hipError_t launch_oproj_merge(const OprojMergeArgs &a, hipStream_t st) {
-    if (a.Hkv != 8 || a.n_split <= 0 || a.n_split > OM_MAXS || a.N % 4 != 0) return hipErrorInvalidValue;
+    if (a.Hkv != 8 || a.N % 4 != 0) return hipErrorInvalidValue;
     const unsigned blocks = (unsigned)((a.N / 4 + 3) / 4);
-    hipLaunchKernelGGL(k_oproj_merge, dim3(blocks), dim3(256), 0, st, a);
+    switch (a.n_split) {
+        case 1: hipLaunchKernelGGL(k_oproj_merge<1>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(k_oproj_merge<2>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(k_oproj_merge<4>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL(k_oproj_merge<8>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 16: hipLaunchKernelGGL(k_oproj_merge<16>, dim3(blocks), dim3(256), 0, st, a); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -404,45 +484,53 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
     float xs;
     float best_v = -1e30f;
     int best_i = -1;
-    int g = gw;
-    i32x4 wv[R][NS];
-    auto load_group = [&](int grp) {
+    // Two groups in flight per wave: buffer A holds groups gw, gw + 2n, ...,
+    // buffer B groups gw + n, gw + 3n, ... (n = waves in the grid).  Rows past
+    // N load row 0 (discarded by the row < N test); slots past K load slot 0
+    // (their activation bytes are zero).
+    i32x4 wa[R][NS], wb[R][NS];
+    float sa[R], sb[R];
+    auto load_group = [&](i32x4 (&wv)[R][NS], float (&sc)[R], int grp) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const int row = grp * R + r;
+            const int row = grp * R + r < a.N ? grp * R + r : 0;
 #pragma unroll
             for (int c = 0; c < NS; c++) {
                 const int s = lane + 64 * c;
-                const bool ok = row < a.N && s < nslot;
-                const i32x4 v = __builtin_nontemporal_load(
-                    reinterpret_cast<const i32x4 *>(a.w + (int64_t)(row < a.N ? row : 0) * K) + (s < nslot ? s : 0));
-                wv[r][c] = ok ? v : i32x4{0, 0, 0, 0};
+                wv[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(a.w + (int64_t)row * K) +
+                                                      (s < nslot ? s : 0));
             }
+            sc[r] = a.ws[row];
         }
     };
-    ActIn<NS, NORM, false> in;
-    act_load<NS, NORM, false>(a.x, nullptr, a.norm_w, K, in, nullptr);
-    if (g < n_groups) load_group(g);
-    act_finish<NS, NORM, false>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
-    for (; g < n_groups; g += n_waves) {
-        int acc[R];
+    // rows visited in increasing order per wave, strict > (first index wins)
+    auto consume = [&](const i32x4 (&wv)[R][NS], const float (&sc)[R], int grp) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
             int t = 0;
 #pragma unroll
             for (int c = 0; c < NS; c++) t = dot16(wv[r][c], xd[c], t);
-            acc[r] = t;
-        }
-        const int gn = g + n_waves;
-        if (gn < n_groups) load_group(gn);   // prefetch the next group before reducing
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = g * R + r;
-            const int s = wave_sum_i32(acc[r]);
+            const int sum = wave_sum_i32(t);
+            const int row = grp * R + r;
             if (row < a.N) {
-                const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)s, xs), a.ws[row]), 0.0f);
+                const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)sum, xs), sc[r]), 0.0f);
                 if (v > best_v) { best_v = v; best_i = row; }
             }
+        }
+    };
+    ActIn<NS, NORM, false> in;
+    act_load<NS, NORM, false>(a.x, nullptr, a.norm_w, K, in);
+    if (gw < n_groups) load_group(wa, sa, gw);
+    if (gw + n_waves < n_groups) load_group(wb, sb, gw + n_waves);
+    __builtin_amdgcn_sched_barrier(0);
+    act_convert<NS, NORM, false>(in, K, nullptr);
+    act_finish<NS, NORM, false>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
+    for (int g = gw; g < n_groups; g += 2 * n_waves) {
+        consume(wa, sa, g);
+        if (g + 2 * n_waves < n_groups) load_group(wa, sa, g + 2 * n_waves);
+        if (g + n_waves < n_groups) {
+            consume(wb, sb, g + n_waves);
+            if (g + 3 * n_waves < n_groups) load_group(wb, sb, g + 3 * n_waves);
         }
     }
     if (lane == 0) { bvals[wid] = best_v; bidx[wid] = best_i; }
@@ -471,12 +559,21 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
             const int oi = __shfl_xor(bi, o, 64);
             if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
         }
+        // the next position's RoPE rows for the next step's attention kernels
+        // (read by every lane before lane 0 advances the state)
+        const int next_pos = a.state ? a.state[1] + 1 : 0;
+        if (a.state && a.rope_cur && next_pos < a.max_pos) {
+            for (int i = lane; i < 128; i += 64) {
+                a.rope_cur[i] = a.rope_cos[(int64_t)next_pos * 128 + i];
+                a.rope_cur[128 + i] = a.rope_sin[(int64_t)next_pos * 128 + i];
+            }
+        }
         if (lane == 0) {
             const int tok = bi < 0 ? 0 : bi;
             a.out_idx[0] = tok;
             if (a.state) {
                 a.state[0] = tok;
-                a.state[1] += 1;
+                a.state[1] = next_pos;
                 if (a.token_log) a.token_log[a.state[2]] = tok;
                 a.state[2] += 1;
             }

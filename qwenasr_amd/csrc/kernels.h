@@ -47,6 +47,9 @@ struct ArgmaxArgs {
     int *out_idx;             // [1]
     int *state;               // nullable decode-loop state
     int *token_log;           // nullable
+    const float *rope_cos, *rope_sin;   // decode loop: RoPE table [max_pos][128]
+    float *rope_cur;          // nullable: receives the cos, sin rows of the next position
+    int max_pos;
 };
 
 hipError_t launch_pack_int8(const uint16_t *w, int64_t n, int K, int mode, int8_t *q, float *s,
@@ -61,6 +64,7 @@ struct AttnDecodeArgs {
     const float *qkv;         // raw projections: q [Hq*D] | k [Hkv*D] | v [Hkv*D]
     const float *q_norm, *k_norm;   // per-head RMSNorm gains [D] (nullable: skip norm+rope)
     const float *rope_cos, *rope_sin;   // [max_pos][D]
+    const float *rope_cur;    // nullable: [2][D] cos, sin rows of the current position
     const int *state;         // decode state (pos = state[1]); nullable -> use pos
     int pos;
     void *kcache, *vcache;    // layer base, layout [Hkv][max_seq][D]
@@ -69,17 +73,19 @@ struct AttnDecodeArgs {
     unsigned *counters;       // [Hkv], zero-initialised; the merging block resets its counter
     float *out;               // [Hq * D]
     int n_split;
+    int waves;                // waves per block: 4 or 8 (0: 8)
+    int gpb;                  // > 0: static partition, 8-position groups per block (rows < head_stride / D)
     float eps, scale;
 };
 
 // merge: the last block of each KV head merges the split partials into out;
-// otherwise the partials are left for k_oproj_merge
+// otherwise the partials are left for k_oproj_merge (n_split 1, 2, 4 or 8)
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
                               int kv_bf16, hipStream_t st, bool merge = true);
 
 // o_proj += Wo attn with the split-attention merge as its prologue (decode step)
 struct OprojMergeArgs {
-    const float *part;        // [Hkv][n_split][2][130] attention partials (m, l, o[128])
+    const float *part;        // attention partials, split index fastest: (m, l) [2 Hq][S], o [Hq][128][S]
     int n_split, Hkv;
     const int8_t *w;          // [N, K = 2 * Hkv * 128] int8
     const float *ws;          // [N]

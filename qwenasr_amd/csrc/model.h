@@ -52,17 +52,25 @@ static inline int attn_splits_for(int64_t len) {
 }
 
 // o_proj merges the split-attention partials itself for the 16-query-head /
-// 8-KV-head shapes (hidden of attention output 2048) at <= 8 splits
+// 8-KV-head shapes (hidden of attention output 2048) at 1, 2, 4, 8 or 16 splits
 static inline bool oproj_merges(const qasr_dec_config &c, int n_split) {
-    return c.n_kv_heads == 8 && c.n_heads == 16 && c.head_dim == 128 && c.hidden % 4 == 0 && n_split <= 8;
+    return c.n_kv_heads == 8 && c.n_heads == 16 && c.head_dim == 128 && c.hidden % 4 == 0 &&
+           (n_split == 1 || n_split == 2 || n_split == 4 || n_split == 8 || n_split == 16);
 }
 
-// default split count.  Measured at a 405-605 position context (0.6B, graph
-// replay): 16 splits merged by the attention kernel 878.6 us/token, 8 splits
-// merged in o_proj 924.1, 6: 972.3, 24: 903.0, 32: 959.9.
-static inline int default_attn_splits(const qasr_dec_config &c, int64_t max_seq) {
-    (void)c;
-    return attn_splits_for(max_seq);
+// Context splits of the decode attention for a context bucket of `cap`
+// positions.  Measured on the 0.6B decoder (16 query / 8 KV heads, 4 waves
+// per block): 8 splits merged in the o_proj prologue are fastest up to a
+// 1024-position bucket (2-4 groups of 8 positions per wave; 16 splits cost
+// 1.4 us more in the o_proj merge than they save in the attention), 16 up to
+// 2048; longer contexts use about cap / 64 splits (<= 64) merged by the
+// attention kernel's last block per KV head.
+static inline int attn_splits_auto(const qasr_dec_config &c, int64_t cap) {
+    if (oproj_merges(c, 8)) {
+        if (cap <= 1024) return 8;
+        if (cap <= 2048) return 16;
+    }
+    return (int)std::min<int64_t>(64, std::max<int64_t>(1, (cap + 63) / 64));
 }
 
 // blocks of the LM-head argmax grid

@@ -74,11 +74,12 @@ def test_decoder_packing_bitexact(tiny_models):
     assert (qg == qc).all() and (sg == sc).all()
 
 
-@pytest.mark.parametrize("splits", [-1, 8, 3, 40])
+@pytest.mark.parametrize("splits", [-1, 16, 8, 3, 40])
 def test_decoder_teacher_forced(tiny_models, splits):
-    """splits -1: the default (16 context splits merged by the attention
-    kernel); 8 and 3: partials merged inside the o_proj kernel (3 leaves
-    ragged splits); 40: more splits than positions early on (empty splits)."""
+    """splits -1: the automatic choice (8 splits at this context, partials
+    merged inside the o_proj kernel); 16 and 8: o_proj merges, most splits
+    empty early on; 3: merged by the attention kernel's last block with
+    ragged splits; 40: attention-side merge, more splits than positions."""
     w, gpu, cpu = tiny_models
     print(f"teacher forced splits={splits}", flush=True)
     gpu.set_options(attn_splits=splits)
