@@ -52,6 +52,9 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-steps", type=int, default=20)
+    ap.add_argument("--copy-calib-mb", type=int, default=0,
+                    help="after the run, one device copy of this many MiB with the library's copy kernel "
+                         "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the multi-GPU "
@@ -113,7 +116,7 @@ def main():
             "traffic": traffic_from_profiles(dom["kernel"]),
             "us_per_launch": round(dom["us"], 3), "bytes_per_launch": dom["bytes"]}
     lm = [p for p in prof if p["kernel"].endswith("lm_head_argmax")][0]
-    mv = [p for p in prof if p["kernel"] != "attention"]
+    mv = [p for p in prof if p["kernel"] not in ("attention", "argmax_merge")]
     mv_bytes = sum(p["bytes"] * p["per_step"] for p in mv)
     mv_us = sum(p["us_per_token"] for p in mv)
     matvec = {"gbs": round(mv_bytes / (mv_us * 1e3), 1), "frac": round(mv_bytes / (mv_us * 1e3) / HBM_PEAK_GBS, 4),
@@ -146,6 +149,13 @@ def main():
               flush=True)
         od.close()
         oe.close()
+
+    if args.copy_calib_mb > 0:
+        nb = args.copy_calib_mb << 20
+        a_, b_ = dev.empty(nb, np.uint8), dev.empty(nb, np.uint8)
+        dev.copy(b_, a_)
+        dev.sync()
+        print(f"[bench] calibration copy: {args.copy_calib_mb} MiB (k_copy16)", file=sys.stderr, flush=True)
 
     line = {
         "metric": METRIC,

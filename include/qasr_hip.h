@@ -54,6 +54,10 @@ int qasr_hip_free(qasr_hip *h, void *dptr);
 int qasr_hip_upload(qasr_hip *h, void *dst, const void *src, size_t bytes);     /* synchronous */
 int qasr_hip_download(qasr_hip *h, void *dst, const void *src, size_t bytes);   /* synchronous */
 int qasr_hip_memset(qasr_hip *h, void *dst, int value, size_t bytes);
+/* device-to-device copy on the handle's stream with the library's own copy
+ * kernel (asynchronous; also the known-size kernel that calibrates HBM
+ * traffic counters) */
+int qasr_hip_copy(qasr_hip *h, void *dst, const void *src, size_t bytes);
 
 /* ---- timing on the handle's stream (HIP events) ------------------------- */
 int qasr_hip_timer_start(qasr_hip *h);
@@ -205,9 +209,10 @@ int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph
  * (no graph).  After each step every kernel kind is launched once per layer
  * (the LM head n_layers times) back to back between two HIP events on the
  * handle's stream, from the step's input state.  Kinds: 0 norm+qkv, 1
- * attention, 2 o_proj, 3 norm+gate_up+swiglu, 4 down, 5 norm+LM-head argmax.
- * Outputs average us per launch, algorithmic bytes per launch and launches
- * per step (6 entries each).  The KV length is restored afterwards. */
+ * attention, 2 o_proj, 3 norm+gate_up+swiglu, 4 down, 5 norm+LM-head argmax
+ * streaming pass, 6 argmax merge (+ step-state update).  Outputs average us
+ * per launch, algorithmic bytes per launch and launches per step (7 entries
+ * each).  The KV length is restored afterwards. */
 int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float *us_per_launch,
                              double *bytes_per_launch, int32_t *launches_per_step);
 

@@ -78,6 +78,7 @@ _SIGS = {
     "qasr_hip_upload": (C.c_int, [P, P, P, C.c_size_t]),
     "qasr_hip_download": (C.c_int, [P, P, P, C.c_size_t]),
     "qasr_hip_memset": (C.c_int, [P, P, C.c_int, C.c_size_t]),
+    "qasr_hip_copy": (C.c_int, [P, P, P, C.c_size_t]),
     "qasr_hip_timer_start": (C.c_int, [P]),
     "qasr_hip_timer_stop": (C.c_int, [P, C.POINTER(F32)]),
     "qasr_hip_pack_int8_rows": (C.c_int, [P, P, I64, I64, C.c_int, P, P]),

@@ -109,6 +109,13 @@ extern "C" int qasr_hip_memset(qasr_hip *h, void *dst, int value, size_t bytes) 
     return QASR_OK;
 }
 
+extern "C" int qasr_hip_copy(qasr_hip *h, void *dst, const void *src, size_t bytes) {
+    CHECK_H(h);
+    if ((!dst || !src) && bytes) return qasr_fail(QASR_ERR_INVALID, "copy: null pointer");
+    LAUNCHCHK(launch_copy(dst, src, (int64_t)bytes, h->stream), "copy");
+    return QASR_OK;
+}
+
 extern "C" int qasr_hip_timer_start(qasr_hip *h) {
     CHECK_H(h);
     HIPCHK(hipEventRecord(h->ev0, h->stream));
@@ -272,7 +279,6 @@ static int argmax_impl(qasr_hip *h, const float *x, const float *norm_w, float e
     const int blocks = argmax_blocks(out_dim);
     a.part_val = reinterpret_cast<float *>(h->scratch);
     a.part_idx = reinterpret_cast<int *>(reinterpret_cast<char *>(h->scratch) + QASR_ARGMAX_MAX_BLOCKS * 4);
-    a.counter = h->counters + QASR_CTR_ARGMAX;
     a.out_idx = idx;
     LAUNCHCHK(launch_argmax(a, norm, blocks, h->stream), "argmax_int8");
     return QASR_OK;

@@ -277,14 +277,14 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, 1, st), "step down");
         }
     }
-    if (want(5)) {
+    if (want(5) || want(6)) {
         ArgmaxArgs am{};
         am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = c.vocab;
         am.w = d->lm; am.ws = d->lm_s;
-        am.part_val = d->am_val; am.part_idx = d->am_idx; am.counter = d->counters + QASR_CTR_ARGMAX;
+        am.part_val = d->am_val; am.part_idx = d->am_idx;
         am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
         am.rope_cos = d->rc; am.rope_sin = d->rs; am.rope_cur = d->rope_cur; am.max_pos = (int)d->max_seq;
-        LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st), "step argmax");
+        LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st, want(5), want(6)), "step argmax");
     }
     return QASR_OK;
 }
@@ -492,8 +492,8 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
     HIPCHK(hipEventCreate(&e0));
     HIPCHK(hipEventCreate(&e1));
     const int lm_reps = (int)std::min<int64_t>(c.n_layers, d->max_seq);
-    double tot[6] = {0, 0, 0, 0, 0, 0};
-    int cnt[6] = {0, 0, 0, 0, 0, 0};
+    double tot[QASR_PROFILE_KINDS] = {};
+    int cnt[QASR_PROFILE_KINDS] = {};
     const int64_t len0 = d->len;
     int rc = QASR_OK;
     int32_t tok = 0;
@@ -503,18 +503,18 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
         HIPCHK(hipStreamSynchronize(st));
         int32_t next[4];
         HIPCHK(hipMemcpy(next, d->state, sizeof(next), hipMemcpyDeviceToHost));
-        for (int k = 0; k < 6 && rc == QASR_OK; k++) {
+        for (int k = 0; k < QASR_PROFILE_KINDS && rc == QASR_OK; k++) {
             if ((rc = set_state(d, tok)) != QASR_OK) break;
             LAUNCHCHK(launch_delay(400, st), "profile delay");
             HIPCHK(hipEventRecord(e0, st));
-            const int reps = k == 5 ? lm_reps : 1;
+            const int reps = k >= 5 ? lm_reps : 1;
             for (int r = 0; r < reps && rc == QASR_OK; r++) rc = decoder_enqueue_step(d, true, k);
             HIPCHK(hipEventRecord(e1, st));
             HIPCHK(hipEventSynchronize(e1));
             float ms = 0.0f;
             HIPCHK(hipEventElapsedTime(&ms, e0, e1));
             tot[k] += ms * 1000.0;
-            cnt[k] += k == 5 ? lm_reps : c.n_layers;
+            cnt[k] += k >= 5 ? lm_reps : c.n_layers;
         }
         tok = next[0];
         d->len += 1;
@@ -528,17 +528,18 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
     const double I = c.intermediate, V = c.vocab, esz = d->kv_bf16 ? 2 : 4;
     // algorithmic bytes: int8 weights N*K + scales 4N + activation 4K + output 4N (+4N read for += )
     const double nqkv = qd + 2 * kvd;
-    const double bytes[6] = {
+    const double bytes[QASR_PROFILE_KINDS] = {
         nqkv * H + 4 * nqkv + 4 * H + 4 * nqkv,
         2.0 * kvd * Lavg * esz + 4 * nqkv + 4 * qd + 2 * kvd * esz,
         H * qd + 4 * H + 4 * qd + 8 * H,
         2 * I * H + 8 * I + 4 * H + 4 * I,
         H * I + 4 * H + 4 * I + 8 * H,
-        V * H + 4 * V + 4 * H};
-    for (int k = 0; k < 6; k++) {
+        V * H + 4 * V + 4 * H,
+        8.0 * argmax_blocks(c.vocab)};
+    for (int k = 0; k < QASR_PROFILE_KINDS; k++) {
         us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
         if (bytes_per_launch) bytes_per_launch[k] = bytes[k];
-        if (launches_per_step) launches_per_step[k] = k == 5 ? 1 : c.n_layers;
+        if (launches_per_step) launches_per_step[k] = k >= 5 ? 1 : c.n_layers;
     }
     return QASR_OK;
 }

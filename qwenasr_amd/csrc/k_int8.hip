@@ -226,8 +226,9 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
     __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int row0 = (blockIdx.x * 4 + wid) * R;
-    if (row0 >= a.n_total) return;
+    // waves past the last row compute row 0 and store nothing
+    const bool live = (blockIdx.x * 4 + wid) * R < a.n_total;
+    const int row0 = live ? (blockIdx.x * 4 + wid) * R : 0;
     const int K = a.K, nslot = K >> 4;
     // segment of this wave (segments are multiples of R rows); scalar selects
     // keep the segment fields in SGPRs
@@ -296,7 +297,8 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
         }
         const float g = __fmul_rn(__fmul_rn((float)ag, xs), ws0);
         const float u = __fmul_rn(__fmul_rn((float)au, xs), ws1);
-        S.y[(lrow0 >> 1) + j] = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        const float o = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        if (live) S.y[(lrow0 >> 1) + j] = o;
     } else {
         const int rl = lane < R ? lane : 0;
         int av = 0;
@@ -304,7 +306,7 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
         for (int r = 0; r < R; r++) if (r == rl) av = acc[r];
         float v = __fmul_rn(__fmul_rn((float)av, xs), ws0);
         if (MODE == MV_ADDTO || MODE == MV_BIAS) v = __fadd_rn(v, yb);
-        S.y[lrow0 + rl] = v;
+        if (live) S.y[lrow0 + rl] = v;
     }
 }
 
@@ -474,7 +476,6 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
     __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
     __shared__ float bvals[4];
     __shared__ int bidx[4];
-    __shared__ int last;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int K = a.K, nslot = K >> 4;
@@ -540,44 +541,60 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
         int bi = bidx[0];
         for (int w = 1; w < 4; w++)
             if (better(bvals[w], bidx[w], bv, bi)) { bv = bvals[w]; bi = bidx[w]; }
-        st_agent(a.part_val + blockIdx.x, bv);
-        st_agent(a.part_idx + blockIdx.x, bi);
+        a.part_val[blockIdx.x] = bv;   // published by the kernel boundary
+        a.part_idx[blockIdx.x] = bi;
     }
-    if (!arrive_last(a.counter, gridDim.x, &last)) return;
-    // final merge by one wave
-    if (wid == 0) {
-        float bv = -1e30f;
-        int bi = -1;
-        for (int b = lane; b < (int)gridDim.x; b += 64) {
-            const float v = ld_agent(a.part_val + b);
-            const int i = ld_agent(a.part_idx + b);
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
+}
+
+// ---------------------------------------------------------------------------
+// Second pass of the LM-head argmax: one block merges the per-block
+// (value, index) partials with the same rule (larger value, lower index on
+// ties) and, in decode-loop mode, advances the device-side step state: the
+// token, the position, the token log and the next position's RoPE rows for the
+// next step's attention kernels.  A separate launch costs less than merging in
+// the streaming kernel: its last-block hand-off (an agent-scope counter bumped
+// by every block) measured 6-12 us at 512-1024 blocks.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_argmax_finish(ArgmaxArgs a, int n_parts) {
+    __shared__ float bvals[4];
+    __shared__ int bidx[4];
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    float bv = -1e30f;
+    int bi = -1;
+    for (int b = threadIdx.x; b < n_parts; b += 256) {
+        const float v = a.part_val[b];
+        const int i = a.part_idx[b];
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    if (lane == 0) { bvals[wid] = bv; bidx[wid] = bi; }
+    __syncthreads();
+    if (wid != 0) return;
+    bv = bvals[0];
+    bi = bidx[0];
+    for (int w = 1; w < 4; w++)
+        if (better(bvals[w], bidx[w], bv, bi)) { bv = bvals[w]; bi = bidx[w]; }
+    // the next position's RoPE rows (read by every lane before lane 0 advances the state)
+    const int next_pos = a.state ? a.state[1] + 1 : 0;
+    if (a.state && a.rope_cur && next_pos < a.max_pos) {
+        for (int i = lane; i < 128; i += 64) {
+            a.rope_cur[i] = a.rope_cos[(int64_t)next_pos * 128 + i];
+            a.rope_cur[128 + i] = a.rope_sin[(int64_t)next_pos * 128 + i];
         }
-        // the next position's RoPE rows for the next step's attention kernels
-        // (read by every lane before lane 0 advances the state)
-        const int next_pos = a.state ? a.state[1] + 1 : 0;
-        if (a.state && a.rope_cur && next_pos < a.max_pos) {
-            for (int i = lane; i < 128; i += 64) {
-                a.rope_cur[i] = a.rope_cos[(int64_t)next_pos * 128 + i];
-                a.rope_cur[128 + i] = a.rope_sin[(int64_t)next_pos * 128 + i];
-            }
-        }
-        if (lane == 0) {
-            const int tok = bi < 0 ? 0 : bi;
-            a.out_idx[0] = tok;
-            if (a.state) {
-                a.state[0] = tok;
-                a.state[1] = next_pos;
-                if (a.token_log) a.token_log[a.state[2]] = tok;
-                a.state[2] += 1;
-            }
-            reset_counter(a.counter);
+    }
+    if (lane == 0) {
+        const int tok = bi < 0 ? 0 : bi;
+        a.out_idx[0] = tok;
+        if (a.state) {
+            a.state[0] = tok;
+            a.state[1] = next_pos;
+            if (a.token_log) a.token_log[a.state[2]] = tok;
+            a.state[2] += 1;
         }
     }
 }
@@ -598,6 +615,25 @@ __global__ __launch_bounds__(256) void k_quant_act(const float *__restrict__ x, 
     act_scales(m, &scale, &inv);
     if (threadIdx.x == 0) *xs = scale;
     for (int k = threadIdx.x; k < K; k += 256) q[k] = (int8_t)round_clamp_i8(__fmul_rn(x[k], inv));
+}
+
+// ---------------------------------------------------------------------------
+// device-to-device copy (16-byte vectors when both pointers and the size allow)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_copy16(int4 *__restrict__ dst, const int4 *__restrict__ src, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) dst[i] = src[i];
+}
+__global__ __launch_bounds__(256) void k_copy1(uint8_t *__restrict__ dst, const uint8_t *__restrict__ src, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) dst[i] = src[i];
+}
+hipError_t launch_copy(void *dst, const void *src, int64_t bytes, hipStream_t st) {
+    if (bytes <= 0) return hipSuccess;
+    const bool v16 = ((uintptr_t)dst % 16 == 0) && ((uintptr_t)src % 16 == 0) && (bytes % 16 == 0);
+    const int64_t n = v16 ? bytes / 16 : bytes;
+    const unsigned blocks = (unsigned)std::min<int64_t>((n + 255) / 256, 4096);
+    if (v16) hipLaunchKernelGGL(k_copy16, dim3(blocks), dim3(256), 0, st, (int4 *)dst, (const int4 *)src, n);
+    else hipLaunchKernelGGL(k_copy1, dim3(blocks), dim3(256), 0, st, (uint8_t *)dst, (const uint8_t *)src, n);
+    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------
@@ -662,18 +698,19 @@ hipError_t launch_w8a8(const MvArgs &a, int mode, bool norm, bool embed, int row
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_argmax(const ArgmaxArgs &a, bool norm, int blocks, hipStream_t st) {
+hipError_t launch_argmax(const ArgmaxArgs &a, bool norm, int blocks, hipStream_t st, bool stream, bool finish) {
     if (a.K % 64 != 0 || a.K > 4096) return hipErrorInvalidValue;
     const int ns = (a.K + 1023) / 1024;
+    if (ns < 1 || ns > 4) return hipErrorInvalidValue;
 #define QASR_AM(NS)                                                                           \
     if (ns == NS) {                                                                           \
         if (norm) hipLaunchKernelGGL((k_argmax_w8a8<NS, 4, true>), dim3(blocks), dim3(256), 0, st, a); \
         else hipLaunchKernelGGL((k_argmax_w8a8<NS, 4, false>), dim3(blocks), dim3(256), 0, st, a);     \
-        return hipGetLastError();                                                             \
     }
-    QASR_AM(1) QASR_AM(2) QASR_AM(3) QASR_AM(4)
+    if (stream) { QASR_AM(1) QASR_AM(2) QASR_AM(3) QASR_AM(4) }
+    if (finish) hipLaunchKernelGGL(k_argmax_finish, dim3(1), dim3(256), 0, st, a, blocks);
+    return hipGetLastError();
 #undef QASR_AM
-    return hipErrorInvalidValue;
 }
 
 }  // namespace qasr

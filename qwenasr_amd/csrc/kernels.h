@@ -41,9 +41,8 @@ struct ArgmaxArgs {
     int K, N;
     const int8_t *w;
     const float *ws;
-    float *part_val;          // [gridDim.x]
+    float *part_val;          // [gridDim.x] per-block partials, merged by k_argmax_finish
     int *part_idx;            // [gridDim.x]
-    unsigned *counter;        // zero before the first launch; the last block resets it
     int *out_idx;             // [1]
     int *state;               // nullable decode-loop state
     int *token_log;           // nullable
@@ -57,7 +56,10 @@ hipError_t launch_pack_int8(const uint16_t *w, int64_t n, int K, int mode, int8_
 hipError_t launch_quant_act(const float *x, int K, int8_t *q, float *xs, hipStream_t st);
 hipError_t launch_w8a8(const MvArgs &a, int mode, bool norm, bool embed, int rows_per_wave,
                        hipStream_t st);
-hipError_t launch_argmax(const ArgmaxArgs &a, bool norm, int blocks, hipStream_t st);
+// stream: the per-block pass; finish: the one-block merge (and decode-state update)
+hipError_t launch_argmax(const ArgmaxArgs &a, bool norm, int blocks, hipStream_t st, bool stream = true,
+                         bool finish = true);
+hipError_t launch_copy(void *dst, const void *src, int64_t bytes, hipStream_t st);
 
 // ---- attention / norms / rope ---------------------------------------------
 struct AttnDecodeArgs {

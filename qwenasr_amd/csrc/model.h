@@ -12,6 +12,8 @@
 #define QASR_CTR_ARGMAX 0
 #define QASR_CTR_ATTN 64
 #define QASR_CTR_ATTN_N 256
+// kernel kinds of qasr_hip_decoder_profile
+#define QASR_PROFILE_KINDS 7
 
 struct qasr_hip {
     int device = 0;
@@ -73,9 +75,11 @@ static inline int attn_splits_auto(const qasr_dec_config &c, int64_t cap) {
     return (int)std::min<int64_t>(64, std::max<int64_t>(1, (cap + 63) / 64));
 }
 
-// blocks of the LM-head argmax grid
+// blocks of the LM-head argmax grid (4 waves of 4-row groups each; 512
+// blocks stream the 0.6B LM head as fast as 1024 and leave half the partials
+// for the merge pass)
 static inline int argmax_blocks(int64_t rows) {
     int64_t groups = (rows + 3) / 4;
     int64_t b = (groups + 3) / 4;
-    return (int)std::max<int64_t>(1, std::min<int64_t>(b, 1024));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(b, 512));
 }

@@ -43,6 +43,11 @@ class Device:
         check(lib().qasr_hip_memset(self.h, d.ptr, 0, d.nbytes))
         return d
 
+    def copy(self, dst, src, nbytes=None):
+        """Device-to-device copy with the library's copy kernel (asynchronous)."""
+        n = src.nbytes if nbytes is None else int(nbytes)
+        check(lib().qasr_hip_copy(self.h, dst.ptr, src.ptr, n))
+
     def timer_start(self):
         check(lib().qasr_hip_timer_start(self.h))
 

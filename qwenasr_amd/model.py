@@ -162,15 +162,17 @@ def transcribe_forced(decoder, encoder, samples, n_steps):
     return toks, times
 
 
-KERNEL_KINDS = ("norm+qkv", "attention", "o_proj+=", "norm+gate_up+swiglu", "down+=", "norm+lm_head_argmax")
+KERNEL_KINDS = ("norm+qkv", "attention", "o_proj+=", "norm+gate_up+swiglu", "down+=", "norm+lm_head_argmax",
+                "argmax_merge")
 
 
 def profile_decoder(decoder, n_steps):
     """Average us per launch, algorithmic bytes per launch and launches per step
     of each decode-step kernel, timed with HIP events inside real decode steps."""
-    us = np.zeros(6, np.float32)
-    by = np.zeros(6, np.float64)
-    n = np.zeros(6, np.int32)
+    k = len(KERNEL_KINDS)
+    us = np.zeros(k, np.float32)
+    by = np.zeros(k, np.float64)
+    n = np.zeros(k, np.int32)
     check(lib().qasr_hip_decoder_profile(decoder.d, int(n_steps), us.ctypes.data_as(P), by.ctypes.data_as(P),
                                          n.ctypes.data_as(P)))
     return [dict(kernel=k, us=float(us[i]), bytes=float(by[i]), per_step=int(n[i]))

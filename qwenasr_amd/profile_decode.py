@@ -1,0 +1,42 @@
+"""Decode-only driver for hardware-counter runs (``rocprofv3 --pmc``).
+
+    QASR_DISABLE_GRAPH=1 rocprofv3 --pmc FETCH_SIZE --kernel-include-regex 'k_attn_decode|k_w8a8|k_oproj|k_argmax|k_copy' \\
+        --output-format csv -d <dir> -o run -- python3 -m qwenasr_amd.profile_decode [steps] [calib_mib]
+
+Loads the seeded 0.6B decoder of the headline workload (bench.py, seed 1002),
+prefills a 404-row synthetic prompt (the config-2 prompt length), runs `steps`
+greedy decode steps (kernel by kernel when QASR_DISABLE_GRAPH=1, so the
+profiler sees every dispatch) and finally one device copy of `calib_mib` MiB
+with the library's copy kernel, whose counter reading calibrates the others
+(``python -m qwenasr_amd.rocprof_summary --pmc``).
+"""
+import sys
+
+import numpy as np
+
+from . import Device
+from .model import Decoder
+from .synth import DEC_0_6B, SynthDecoder
+
+
+def main(steps=100, calib_mib=256):
+    w = SynthDecoder(DEC_0_6B, seed=1002)
+    dev = Device(0)
+    dec = Decoder(dev, w, max_seq=1024)
+    rng = np.random.default_rng(1002)
+    prompt = (rng.standard_normal((404, DEC_0_6B["hidden"])) * 0.5).astype(np.float32)
+    dec.prefill(prompt)
+    toks = dec.generate(steps, first_embed=prompt[-1])
+    print(f"[profile_decode] {steps} steps at context {404}..{404 + steps}, last token {int(toks[-1])}",
+          flush=True)
+    nb = calib_mib << 20
+    a, b = dev.empty(nb, np.uint8), dev.empty(nb, np.uint8)
+    dev.copy(b, a)
+    dev.sync()
+    print(f"[profile_decode] calibration copy {calib_mib} MiB done", flush=True)
+    dec.close()
+    dev.close()
+
+
+if __name__ == "__main__":
+    main(int(sys.argv[1]) if len(sys.argv) > 1 else 100, int(sys.argv[2]) if len(sys.argv) > 2 else 256)
