@@ -42,7 +42,7 @@ typedef struct qasr_hip qasr_hip;
 
 /* ---- lifecycle ---------------------------------------------------------- */
 int qasr_hip_create(int device, qasr_hip **out);
-void qasr_hip_destroy(qasr_hip *h);
+void qasr_hip_destroy(qasr_hip *h);   /* free every decoder / encoder / allocation made on h first */
 const char *qasr_hip_last_error(void);
 int qasr_hip_device_count(int *n);
 int qasr_hip_synchronize(qasr_hip *h);
@@ -124,6 +124,13 @@ int qasr_hip_causal_attention(qasr_hip *h, float *out, const float *q, const flo
                               const float *v_base, int64_t head_stride, int64_t seq_q,
                               int64_t seq_k, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
                               float scale, int64_t q_offset);
+/* the same single-query (decode) attention over a bf16 KV cache (the config-3
+ * layout; no counterpart in the reference, whose KV cache is f32): seq_q must
+ * be 1; k_base / v_base hold bf16 [kv_head][pos][head_dim] */
+int qasr_hip_causal_attention_bf16kv(qasr_hip *h, float *out, const float *q, const uint16_t *k_base,
+                                     const uint16_t *v_base, int64_t head_stride, int64_t seq_k,
+                                     int64_t n_heads, int64_t n_kv_heads, int64_t hd, float scale,
+                                     int64_t q_offset);
 
 /* ---- A15/A16: dense GEMMs (MFMA) ----------------------------------------
  * linear (kernels/mod.rs:550-584) / linear_accumulate (mod.rs:591-628) on
@@ -192,7 +199,8 @@ int qasr_hip_decoder_set_len(qasr_decoder *d, int64_t len);
 int64_t qasr_hip_decoder_len(const qasr_decoder *d);
 /* test hooks: the packed int8 rows / scales of layer `layer` (-1 = LM head),
  * which = 0 q, 1 k, 2 v, 3 o, 4 gate_up (interleaved), 5 down; and the KV cache
- * in the reference layout [layer][kv_head][max_seq][head_dim] as f32 */
+ * in the reference layout [layer][kv_head][max_seq][head_dim] as f32 (a bf16
+ * cache is rounded to nearest even on upload and widened exactly on download) */
 int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, int8_t *q_host,
                             float *scales_host);
 int qasr_hip_decoder_kv_upload(qasr_decoder *d, const float *k_host, const float *v_host);

@@ -339,6 +339,12 @@ class OracleDecoder:
         e = f32(embeds)
         lib().or_decoder_prefill(self.d, _p(e), e.shape[0])
 
+    def forward_logits(self, embed):
+        """(token, best logit, second-best logit)."""
+        bv, sv = C.c_float(), C.c_float()
+        t = lib().or_decoder_forward(self.d, _p(f32(embed)), C.byref(bv), C.byref(sv), None)
+        return int(t), bv.value, sv.value
+
     def forward(self, embed, return_hidden=False):
         bv, sv = C.c_float(), C.c_float()
         hid = np.empty(self.cfg["hidden"], np.float32) if return_hidden else None
@@ -346,6 +352,13 @@ class OracleDecoder:
         if return_hidden:
             return int(t), bv.value - sv.value, hid
         return int(t), bv.value - sv.value
+
+    def set_kv(self, k, v):
+        """Overwrite the KV cache ([layer][kv_head][max_seq][head_dim] f32)."""
+        for which, a in ((0, k), (1, v)):
+            a = f32(a)
+            assert a.size == self.cfg["n_layers"] * self.cfg["n_kv_heads"] * self.max_seq * self.cfg["head_dim"]
+            C.memmove(lib().or_decoder_kv(self.d, which), a.ctypes.data, a.nbytes)
 
     def kv(self):
         c = self.cfg

@@ -97,6 +97,7 @@ _SIGS = {
     "qasr_hip_apply_rope_neox": (C.c_int, [P, P, P, P, I64, I64, I64]),
     "qasr_hip_causal_attention": (C.c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, I64, F32,
                                             I64]),
+    "qasr_hip_causal_attention_bf16kv": (C.c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F32, I64]),
     "qasr_hip_decoder_load": (C.c_int, [P, C.POINTER(DecConfig), C.POINTER(DecWeights), C.c_int,
                                         I64, C.c_int, C.POINTER(P)]),
     "qasr_hip_decoder_free": (None, [P]),

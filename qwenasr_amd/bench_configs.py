@@ -1,0 +1,131 @@
+"""Measurement harness for the BASELINE configs other than the headline.
+
+    python -m qwenasr_amd.bench_configs config1 [reps]
+    python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
+
+config1: the prefill / audio-encoder int8 x bf16 GEMMs at M = 375 (also 390,
+404), the seven 0.6B projections and the LM head, seeded N(0,0.02) weights
+packed per row on the GPU, bf16 activations N(0,1).  Each shape is timed
+with HIP events over `reps` back-to-back launches; reported as TFLOP/s
+against the 2.5 PFLOP/s dense bf16 MFMA peak (the kernel dequantizes int8 to
+bf16 exactly and runs v_mfma_f32_16x16x32_bf16) and as HBM GB/s.
+
+config3: Qwen3-1.7B-sized decoder (28 layers, hidden 2048, GQA 16/8,
+intermediate 6144, int8 per-row weights), batch 1, bf16 KV cache filled with
+N(0,1) values, at KV lengths 512, 2048 and 4096: decode us/token (graph
+replay, HIP events), per-kernel us and algorithmic GB/s (the same
+back-to-back timing as bench.py), int8 matvec GB/s and GQA attention us per
+token.
+
+Each configuration prints one JSON line (stdout); progress goes to stderr.
+"""
+import json
+import sys
+import time
+
+import numpy as np
+
+from . import Device
+from . import kernels as K
+from .model import Decoder, profile_decoder
+from .synth import DEC_1_7B, SynthDecoder, normal_bf16
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def config1(reps=20):
+    dev = Device(0)
+    shapes = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
+              ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072), ("lm_head", 151936, 1024)]
+    rows = []
+    for M in (375, 390, 404):
+        for name, N, Kd in shapes:
+            wb = dev.upload(normal_bf16((N, Kd), 1001, f"w_{name}"))
+            q = dev.empty((N, Kd), np.int8)
+            s = dev.empty(N, np.float32)
+            K.quantize_bf16_weights_to_int8(wb, N, Kd, q, s)
+            a = dev.upload(normal_bf16((M, Kd), 1001, f"a_{name}_{M}", std=1.0))
+            y = dev.empty((M, N), np.float32)
+            K.gemm_w8_bf16(y, a, q, s, M, N, Kd)          # warm-up
+            dev.sync()
+            dev.timer_start()
+            for _ in range(reps):
+                K.gemm_w8_bf16(y, a, q, s, M, N, Kd)
+            ms = dev.timer_stop() / reps
+            flops = 2.0 * M * N * Kd
+            byts = N * Kd + 4.0 * N + 2.0 * M * Kd + 4.0 * M * N
+            r = dict(M=M, shape=name, N=N, K=Kd, us=round(ms * 1e3, 2), tflops=round(flops / (ms * 1e9), 1),
+                     mfma_frac=round(flops / (ms * 1e9) / BF16_PEAK_TFLOPS, 4), gbs=round(byts / (ms * 1e6), 1))
+            rows.append(r)
+            log(f"[config1] M={M} {name:8s} {N}x{Kd}: {r['us']:9.2f} us  {r['tflops']:7.1f} TFLOP/s "
+                f"({100 * r['mfma_frac']:.1f}% of bf16 MFMA)  {r['gbs']:8.1f} GB/s")
+            for d in (wb, q, s, a, y):
+                d.free()
+    print(json.dumps({"config": "config 1: int8 x bf16 GEMM (prefill / encoder shapes)", "results": rows}))
+    dev.close()
+
+
+def config3(n_layers=28, steps=20):
+    dev = Device(0)
+    cfg = dict(DEC_1_7B, n_layers=n_layers)
+    t0 = time.time()
+    w = SynthDecoder(cfg, seed=1003)
+    log(f"[config3] synthetic 1.7B decoder ({n_layers} layers) in {time.time() - t0:.1f}s")
+    contexts = (512, 2048, 4096)
+    max_seq = contexts[-1] + 2 * steps + 8
+    dec = Decoder(dev, w, max_seq=max_seq, kv_bf16=True)
+    rng = np.random.default_rng(1003)
+    shape = dec.kv_shape()
+    k = rng.standard_normal(shape, dtype=np.float32)
+    v = rng.standard_normal(shape, dtype=np.float32)
+    dec.kv_upload(k, v)
+    del k, v
+    log("[config3] weights packed, bf16 KV filled with N(0,1)")
+    res = []
+    for L in contexts:
+        dec.kv_len = L
+        dec.generate(2, first_token=17)                 # captures the graph of this bucket
+        dec.kv_len = L
+        dev.sync()
+        dev.timer_start()
+        dec.generate(steps, first_token=17)
+        us_tok = dev.timer_stop() * 1e3 / steps
+        dec.kv_len = L
+        prof = profile_decoder(dec, steps)
+        kern = {}
+        for p in prof:
+            kern[p["kernel"]] = dict(us=round(p["us"], 3), bytes=p["bytes"],
+                                     gbs=round(p["bytes"] / (p["us"] * 1e3), 1) if p["us"] > 0 else 0.0,
+                                     per_step=p["per_step"])
+        mv = [p for p in prof if p["kernel"] not in ("attention", "argmax_merge")]
+        mv_bytes = sum(p["bytes"] * p["per_step"] for p in mv)
+        mv_us = sum(p["us"] * p["per_step"] for p in mv)
+        att = [p for p in prof if p["kernel"] == "attention"][0]
+        r = dict(kv_len=L, decode_us_per_token=round(us_tok, 2),
+                 int8_matvec_gbs=round(mv_bytes / (mv_us * 1e3), 1),
+                 int8_matvec_frac=round(mv_bytes / (mv_us * 1e3) / HBM_PEAK_GBS, 4),
+                 attention_us_per_layer=round(att["us"], 3), attention_us_per_token=round(att["us"] * att["per_step"], 2),
+                 attention_gbs=round(att["bytes"] / (att["us"] * 1e3), 1), kernels=kern)
+        res.append(r)
+        log(f"[config3] L={L}: {us_tok:.1f} us/token; matvecs {r['int8_matvec_gbs']} GB/s "
+            f"({100 * r['int8_matvec_frac']:.1f}%); attention {att['us']:.2f} us/layer "
+            f"({r['attention_gbs']} GB/s); " + ", ".join(f"{k_} {v_['us']}" for k_, v_ in kern.items()))
+    print(json.dumps({"config": f"config 3: Qwen3-1.7B-sized decoder, {n_layers} layers, bf16 KV, batch 1",
+                      "results": res}))
+    dec.close()
+    dev.close()
+
+
+if __name__ == "__main__":
+    what = sys.argv[1] if len(sys.argv) > 1 else "config3"
+    if what == "config1":
+        config1(int(sys.argv[2]) if len(sys.argv) > 2 else 20)
+    elif what == "config3":
+        config3(int(sys.argv[2]) if len(sys.argv) > 2 else 28, int(sys.argv[3]) if len(sys.argv) > 3 else 20)
+    else:
+        raise SystemExit(f"unknown configuration {what!r}")

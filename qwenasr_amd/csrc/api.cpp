@@ -370,6 +370,38 @@ extern "C" int qasr_hip_causal_attention(qasr_hip *h, float *out, const float *q
     return QASR_OK;
 }
 
+extern "C" int qasr_hip_causal_attention_bf16kv(qasr_hip *h, float *out, const float *q, const uint16_t *k_base,
+                                                const uint16_t *v_base, int64_t head_stride, int64_t seq_k,
+                                                int64_t n_heads, int64_t n_kv_heads, int64_t hd, float scale,
+                                                int64_t q_offset) {
+    CHECK_H(h);
+    if (!out || !q || !k_base || !v_base || hd != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads ||
+        seq_k < 0 || q_offset < 0 || head_stride < hd || seq_k > (1 << 24))
+        return qasr_fail(QASR_ERR_INVALID,
+                         "causal_attention_bf16kv: supported shape is head_dim 128, n_heads == 2 * n_kv_heads");
+    const int64_t k_end = std::min(q_offset + 1, seq_k);
+    if (k_end == 0) {
+        HIPCHK(hipMemsetAsync(out, 0, sizeof(float) * n_heads * hd, h->stream));
+        return QASR_OK;
+    }
+    AttnDecodeArgs a{};
+    a.qkv = q;
+    a.pos = (int)(k_end - 1);
+    a.kcache = const_cast<uint16_t *>(k_base);
+    a.vcache = const_cast<uint16_t *>(v_base);
+    a.head_stride = head_stride;
+    a.n_split = attn_splits_for(k_end);
+    const size_t need = (size_t)n_kv_heads * a.n_split * 2 * (hd + 2) * sizeof(float);
+    if (need > QASR_SCRATCH_BYTES || n_kv_heads > QASR_CTR_ATTN_N || a.n_split > 64)
+        return qasr_fail(QASR_ERR_INVALID, "causal_attention_bf16kv: context too long for the scratch area");
+    a.part = reinterpret_cast<float *>(h->scratch);
+    a.counters = h->counters + QASR_CTR_ATTN;
+    a.out = out;
+    a.scale = scale;
+    LAUNCHCHK(launch_attn_decode(a, (int)n_heads, (int)n_kv_heads, (int)hd, 1, h->stream), "causal_attention_bf16kv");
+    return QASR_OK;
+}
+
 extern "C" int qasr_hip_bidirectional_attention(qasr_hip *h, float *out, const float *q, const float *k,
                                                 const float *v, int64_t seq, int64_t n_heads, int64_t hd,
                                                 float scale, int64_t window) {

@@ -444,19 +444,51 @@ extern "C" int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, in
     return QASR_OK;
 }
 
+// host f32 <-> device cache.  A bf16 cache is converted on the host (f32 -> bf16
+// round-to-nearest-even on upload; bf16 -> f32 is exact on download), in
+// slices so the staging buffer stays small.
+static uint16_t f32_to_bf16_host(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
 static int kv_copy(qasr_decoder *d, float *kh, float *vh, bool up) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
     CHECK_H(d->h);
-    if (d->kv_bf16) return qasr_fail(QASR_ERR_INVALID, "kv copy: only for f32 caches");
     const size_t n = (size_t)d->c.n_layers * d->c.n_kv_heads * d->max_seq * d->c.head_dim;
-    if (up) {
-        if (kh) HIPCHK(hipMemcpyAsync(d->kc, kh, n * 4, hipMemcpyHostToDevice, d->h->stream));
-        if (vh) HIPCHK(hipMemcpyAsync(d->vc, vh, n * 4, hipMemcpyHostToDevice, d->h->stream));
-    } else {
-        if (kh) HIPCHK(hipMemcpyAsync(kh, d->kc, n * 4, hipMemcpyDeviceToHost, d->h->stream));
-        if (vh) HIPCHK(hipMemcpyAsync(vh, d->vc, n * 4, hipMemcpyDeviceToHost, d->h->stream));
+    if (!d->kv_bf16) {
+        if (up) {
+            if (kh) HIPCHK(hipMemcpyAsync(d->kc, kh, n * 4, hipMemcpyHostToDevice, d->h->stream));
+            if (vh) HIPCHK(hipMemcpyAsync(d->vc, vh, n * 4, hipMemcpyHostToDevice, d->h->stream));
+        } else {
+            if (kh) HIPCHK(hipMemcpyAsync(kh, d->kc, n * 4, hipMemcpyDeviceToHost, d->h->stream));
+            if (vh) HIPCHK(hipMemcpyAsync(vh, d->vc, n * 4, hipMemcpyDeviceToHost, d->h->stream));
+        }
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        return QASR_OK;
     }
-    HIPCHK(hipStreamSynchronize(d->h->stream));
+    const size_t slice = (size_t)1 << 22;
+    std::vector<uint16_t> tmp(std::min(n, slice));
+    for (int which = 0; which < 2; which++) {
+        float *hbuf = which ? vh : kh;
+        uint16_t *dbuf = reinterpret_cast<uint16_t *>(which ? d->vc : d->kc);
+        if (!hbuf) continue;
+        for (size_t o = 0; o < n; o += slice) {
+            const size_t m = std::min(slice, n - o);
+            if (up) {
+                for (size_t i = 0; i < m; i++) tmp[i] = f32_to_bf16_host(hbuf[o + i]);
+                HIPCHK(hipMemcpy(dbuf + o, tmp.data(), m * 2, hipMemcpyHostToDevice));
+            } else {
+                HIPCHK(hipMemcpy(tmp.data(), dbuf + o, m * 2, hipMemcpyDeviceToHost));
+                for (size_t i = 0; i < m; i++) {
+                    const uint32_t u = (uint32_t)tmp[i] << 16;
+                    std::memcpy(hbuf + o + i, &u, 4);
+                }
+            }
+        }
+    }
     return QASR_OK;
 }
 

@@ -1,5 +1,6 @@
 """Device handle and device arrays over the qasr_hip C ABI."""
 import ctypes as C
+import weakref
 
 import numpy as np
 
@@ -14,9 +15,16 @@ class Device:
         check(lib().qasr_hip_create(index, C.byref(h)))
         self.h = h
         self.index = index
+        self._children = weakref.WeakSet()   # decoders / encoders created on this handle
+
+    def adopt(self, obj):
+        """Register an object whose close() must run before the handle is destroyed."""
+        self._children.add(obj)
 
     def close(self):
         if self.h:
+            for c in list(self._children):   # the C ABI requires them freed first
+                c.close()
             lib().qasr_hip_destroy(self.h)
             self.h = None
 

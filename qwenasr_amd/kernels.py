@@ -93,6 +93,15 @@ def causal_attention(out, q, k_base, v_base, head_stride, seq_q, seq_k, n_heads,
                                           n_heads, n_kv_heads, head_dim, scale, q_offset))
 
 
+def causal_attention_bf16kv(out, q, k_base, v_base, head_stride, seq_k, n_heads, n_kv_heads, head_dim,
+                            scale, q_offset):
+    """Single-query attention over a bf16 [kv_head][pos][head_dim] cache (config 3)."""
+    kp = k_base.ptr if hasattr(k_base, "ptr") else k_base
+    vp = v_base.ptr if hasattr(v_base, "ptr") else v_base
+    check(lib().qasr_hip_causal_attention_bf16kv(_h(q), out.ptr, q.ptr, kp, vp, head_stride, seq_k, n_heads,
+                                                 n_kv_heads, head_dim, scale, q_offset))
+
+
 def linear(y, x, w_bf16, bias, seq_len, in_dim, out_dim, accumulate=False):
     """linear / linear_accumulate (kernels/mod.rs:550, 591) on bf16-valued weights."""
     check(lib().qasr_hip_linear_bf16w(_h(x), y.ptr, x.ptr, w_bf16.ptr, bias.ptr if bias is not None else None,

@@ -25,6 +25,7 @@ class Decoder:
         self.d = d
         self.max_seq = max_seq
         self.kv_bf16 = kv_bf16
+        dev.adopt(self)
 
     def close(self):
         if self.d:
@@ -116,6 +117,7 @@ class Encoder:
         e = P()
         check(lib().qasr_hip_encoder_load(dev.h, C.byref(cfg), C.byref(w), C.byref(e)))
         self.e = e
+        dev.adopt(self)
 
     def close(self):
         if self.e:
