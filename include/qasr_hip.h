@@ -267,6 +267,38 @@ int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *sa
                                int64_t n_samples, int32_t n_steps, int32_t *tokens_out,
                                double *times_ms);
 
+/* ---- A20: incremental streaming (stream_push_audio, transcribe.rs:902-1304) ----
+ * A stream borrows a decoder (its KV cache and step state) and an encoder; one
+ * stream per decoder at a time.  Text comes out as token ids (the caller's
+ * tokenizer turns them into bytes).  Defaults are QwenCtx's (context.rs:144-150). */
+typedef struct qasr_stream qasr_stream;
+typedef struct {
+    float chunk_sec;                /* 2.0 */
+    int32_t rollback;               /* 5 */
+    int32_t unfixed_chunks;         /* 2 */
+    int32_t max_new_tokens;         /* 32 */
+    int32_t past_text_conditioning; /* 0 */
+    int32_t stop_tokens[2];         /* TOKEN_ENDOFTEXT 151643, TOKEN_IM_END 151645 */
+} qasr_stream_config;
+#define QASR_STREAM_STATS 8
+void qasr_hip_stream_default_config(qasr_stream_config *cfg);
+int qasr_hip_stream_create(qasr_decoder *d, qasr_encoder *e, const qasr_stream_config *cfg, qasr_stream **out);
+void qasr_hip_stream_free(qasr_stream *s);
+/* StreamState::reset (transcribe.rs:865-883) */
+int qasr_hip_stream_reset(qasr_stream *s);
+/* samples: the whole audio of the stream so far (16 kHz mono f32); processes
+ * every complete chunk past the cursor (and the rest when finalize != 0) and
+ * writes the newly committed text token ids to tokens_out (capacity cap);
+ * n_out = their count */
+int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_t n_samples, int finalize,
+                         int32_t *tokens_out, int64_t cap, int64_t *n_out);
+/* every committed text token so far (up to cap); n = the total count */
+int qasr_hip_stream_tokens(const qasr_stream *s, int32_t *tokens_out, int64_t cap, int64_t *n);
+int64_t qasr_hip_stream_audio_cursor(const qasr_stream *s);
+/* chunks processed, last chunk's reused prefill rows, prefill length, rows
+ * prefilled, forwards, total forwards, encoder windows encoded, raw tokens */
+int qasr_hip_stream_stats(const qasr_stream *s, int64_t *stats);
+
 #ifdef __cplusplus
 }
 #endif

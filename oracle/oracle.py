@@ -92,6 +92,13 @@ _SIGS = {
     "or_encoder_tokens": (I64, [P, I64]),
     "or_encoder_forward": (I64, [P, P, I64, P]),
     "or_transcribe_forced": (I64, [P, P, P, I64, I32, P, P, P]),
+    "or_stream_default_config": (None, [P]),
+    "or_stream_create": (P, [P, P, P, I64]),
+    "or_stream_destroy": (None, [P]),
+    "or_stream_push": (I64, [P, P, I64, C.c_int, P, I64]),
+    "or_stream_tokens": (I64, [P, P, I64]),
+    "or_stream_stats": (None, [P, P]),
+    "or_tail_repeat_blocks": (I64, [P, I64, I64, P]),
     "or_set_threads": (None, [C.c_int]),
     "or_get_threads": (C.c_int, []),
 }
@@ -403,3 +410,60 @@ def transcribe_forced(dec, enc, samples, n_steps):
     total = lib().or_transcribe_forced(dec.d, enc.e, _p(s), s.size, n_steps, _p(toks), _p(margins),
                                        _p(times))
     return dict(tokens=toks, margins=margins, times_ms=times, prompt_len=int(total))
+
+
+class StreamConfig(C.Structure):
+    _fields_ = [("chunk_sec", C.c_float), ("rollback", C.c_int32), ("unfixed_chunks", C.c_int32),
+                ("max_new_tokens", C.c_int32), ("past_text_conditioning", C.c_int32),
+                ("stop_tokens", C.c_int32 * 2)]
+
+
+def stream_config(**kw):
+    c = StreamConfig()
+    lib().or_stream_default_config(C.byref(c))
+    for k, v in kw.items():
+        if k == "stop_tokens":
+            c.stop_tokens[0], c.stop_tokens[1] = v
+        else:
+            setattr(c, k, v)
+    return c
+
+
+def tail_repeat_blocks(tokens, max_period):
+    t = np.ascontiguousarray(tokens, np.int32)
+    period = I64()
+    reps = lib().or_tail_repeat_blocks(_p(t), t.size, max_period, C.byref(period))
+    return int(reps), int(period.value)
+
+
+class OracleStream:
+    """or_stream: stream_push_audio (transcribe.rs:902-1304) on the oracle model."""
+
+    def __init__(self, dec, enc, **cfg):
+        self.cfg = stream_config(**cfg)
+        self.dec, self.enc = dec, enc
+        self.s = lib().or_stream_create(dec.d, enc.e, C.byref(self.cfg), dec.cfg["hidden"])
+
+    def push(self, samples, finalize=False):
+        x = f32(samples)
+        out = np.empty(4096, np.int32)
+        n = lib().or_stream_push(self.s, _p(x), x.size, 1 if finalize else 0, _p(out), out.size)
+        return out[:n].copy()
+
+    def tokens(self):
+        out = np.empty(1 << 16, np.int32)
+        n = lib().or_stream_tokens(self.s, _p(out), out.size)
+        return out[:n].copy()
+
+    def stats(self):
+        st = np.zeros(8, np.int64)
+        lib().or_stream_stats(self.s, _p(st))
+        return st
+
+    def close(self):
+        if self.s:
+            lib().or_stream_destroy(self.s)
+            self.s = None
+
+    def __del__(self):
+        self.close()

@@ -168,6 +168,21 @@ int64_t or_transcribe_forced(or_decoder *d, or_encoder *e, const float *samples,
                              float *margins, double *times_ms);
 
 /* Threads used by the oracle's OpenMP loops; results do not depend on it. */
+/* streaming (stream_push_audio, transcribe.rs:902-1304), oracle_stream.c */
+typedef struct {
+    float chunk_sec;
+    int32_t rollback, unfixed_chunks, max_new_tokens, past_text_conditioning;
+    int32_t stop_tokens[2];
+} or_stream_config;
+typedef struct or_stream or_stream;
+void or_stream_default_config(or_stream_config *c);
+or_stream *or_stream_create(or_decoder *d, or_encoder *e, const or_stream_config *cfg, int64_t hidden);
+void or_stream_destroy(or_stream *s);
+int64_t or_stream_push(or_stream *s, const float *samples, int64_t n, int finalize, int32_t *out, int64_t cap);
+int64_t or_stream_tokens(const or_stream *s, int32_t *out, int64_t cap);
+void or_stream_stats(const or_stream *s, int64_t *stats);
+int64_t or_tail_repeat_blocks(const int32_t *t, int64_t n, int64_t max_period, int64_t *period);
+
 void or_set_threads(int n);
 int or_get_threads(void);
 

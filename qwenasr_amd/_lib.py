@@ -65,6 +65,12 @@ class EncWeights(C.Structure):
                                      "proj1_b", "proj2_b")])
 
 
+class StreamConfig(C.Structure):
+    _fields_ = [("chunk_sec", C.c_float), ("rollback", C.c_int32), ("unfixed_chunks", C.c_int32),
+                ("max_new_tokens", C.c_int32), ("past_text_conditioning", C.c_int32),
+                ("stop_tokens", C.c_int32 * 2)]
+
+
 # name -> (restype, argtypes); every function returning int is status-checked
 _SIGS = {
     "qasr_hip_create": (C.c_int, [C.c_int, C.POINTER(P)]),
@@ -121,6 +127,14 @@ _SIGS = {
     "qasr_hip_mel": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),
     "qasr_hip_encoder_forward": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),
     "qasr_hip_transcribe_forced": (C.c_int, [P, P, P, I64, I32, P, P]),
+    "qasr_hip_stream_default_config": (None, [C.POINTER(StreamConfig)]),
+    "qasr_hip_stream_create": (C.c_int, [P, P, C.POINTER(StreamConfig), C.POINTER(P)]),
+    "qasr_hip_stream_free": (None, [P]),
+    "qasr_hip_stream_reset": (C.c_int, [P]),
+    "qasr_hip_stream_push": (C.c_int, [P, P, I64, C.c_int, P, I64, C.POINTER(I64)]),
+    "qasr_hip_stream_tokens": (C.c_int, [P, P, I64, C.POINTER(I64)]),
+    "qasr_hip_stream_audio_cursor": (I64, [P]),
+    "qasr_hip_stream_stats": (C.c_int, [P, P]),
 }
 
 _lib = None

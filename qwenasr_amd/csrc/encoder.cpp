@@ -6,6 +6,7 @@
 #include <vector>
 
 #include "decoder.h"
+#include "encoder.h"
 
 using namespace qasr;
 
@@ -331,6 +332,9 @@ int encoder_forward_dev(qasr_encoder *e, const float *mel, int64_t frames, float
     return QASR_OK;
 }
 
+int64_t encoder_output_dim(const qasr_encoder *e) { return e->c.output_dim; }
+qasr_hip *encoder_handle(const qasr_encoder *e) { return e->h; }
+
 int64_t mel_frames_for(int64_t n) {
     const int64_t padded = n + 400;
     if (padded < 400) return 0;
@@ -358,7 +362,7 @@ int mel_dev(qasr_encoder *e, const float *x, int64_t ns, float *mel, float *scra
     return QASR_OK;
 }
 
-static size_t mel_scratch_floats(int64_t nf) { return (size_t)nf * (400 + 3 * 201) + (size_t)(128 * nf / 256 + 2); }
+size_t mel_scratch_floats(int64_t nf) { return (size_t)nf * (400 + 3 * 201) + (size_t)(128 * nf / 256 + 2); }
 
 extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, float *mel_out, int64_t *frames) {
     if (!e) return qasr_fail(QASR_ERR_INVALID, "encoder is null");

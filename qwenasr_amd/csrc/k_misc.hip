@@ -196,6 +196,28 @@ __global__ __launch_bounds__(256) void k_build_prompt(float *__restrict__ out, c
     (void)n_tail;
 }
 
+// flags[r] = 1 when rows r of a and b differ in any bit (the row-equality test
+// of the streaming prefill's prefix reuse, transcribe.rs:1095-1104)
+__global__ __launch_bounds__(256) void k_row_diff(const float *__restrict__ a, const float *__restrict__ b,
+                                                  int64_t H, int *__restrict__ flags) {
+    __shared__ int any;
+    const int64_t r = blockIdx.x;
+    if (threadIdx.x == 0) any = 0;
+    __syncthreads();
+    const uint32_t *pa = reinterpret_cast<const uint32_t *>(a + r * H), *pb = reinterpret_cast<const uint32_t *>(b + r * H);
+    int d = 0;
+    for (int64_t i = threadIdx.x; i < H; i += 256) d |= pa[i] != pb[i];
+    if (d) any = 1;
+    __syncthreads();
+    if (threadIdx.x == 0) flags[r] = any;
+}
+
+hipError_t launch_row_diff(const float *a, const float *b, int64_t rows, int64_t H, int *flags, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_row_diff, dim3((unsigned)rows), dim3(256), 0, st, a, b, H, flags);
+    return hipGetLastError();
+}
+
 hipError_t launch_build_prompt(float *out, const uint16_t *embed, const int *toks, int n_head, const float *mid,
                                int n_mid, int n_tail, int H, hipStream_t st) {
     hipLaunchKernelGGL(k_build_prompt, dim3(n_head + n_mid + n_tail), dim3(256), 0, st, out, embed, toks, n_head,

@@ -1,0 +1,470 @@
+// Incremental streaming transcription on the device-resident encoder and
+// decoder: stream_push_audio (transcribe.rs:902-1304) with the defaults of
+// QwenCtx (context.rs:144-150).  Per 2 s chunk:
+//   1. completed 8 s encoder windows are encoded once and kept in HBM
+//      (transcribe.rs:959-965); the partial tail is re-encoded on the first
+//      chunk, every second chunk and when finalizing (:971-1002);
+//   2. the prompt rows (prefix tokens | encoder rows | suffix tokens | rolled-
+//      back text tokens) are assembled in HBM (:1036-1089);
+//   3. the rows equal to the previous chunk's prefill (bitwise, k_row_diff)
+//      keep their KV entries: kv len = that common-prefix length, and only the
+//      remaining rows are prefilled (:1095-1115);
+//   4. up to max_new_tokens greedy steps stop at the first stop token
+//      (:1138-1151) — the steps run as graph replays in bursts, the host reads
+//      the token log between bursts;
+//   5. host bookkeeping on token ids: speech-end commit, rollback, degeneracy
+//      and periodic re-anchoring, emission of the newly stable text tokens
+//      (:1153-1292).
+// Text is returned as token ids; turning them into bytes is the tokenizer's
+// job on the host (tokenizer.rs), outside this library.
+#include "decoder.h"
+#include "encoder.h"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+using namespace qasr;
+
+#define TRY(x)                  \
+    do {                        \
+        int rc_ = (x);          \
+        if (rc_ != QASR_OK) {   \
+            return rc_;         \
+        }                       \
+    } while (0)
+
+namespace {
+constexpr int32_t TOKEN_ASR_TEXT = 151704;
+// PREFIX_HEAD | PREFIX_TAIL and SUFFIX_BASE (transcribe.rs:13-15); no prompt or
+// language tokens (those come from the tokenizer)
+constexpr int32_t PREFIX[9] = {151644, 8948, 198, 151645, 198, 151644, 872, 198, 151669};
+constexpr int32_t SUFFIX[6] = {151670, 151645, 198, 151644, 77091, 198};
+constexpr int DEGEN_MAX_PERIOD = 6, DEGEN_MIN_REPEATS = 4, STALE_CHUNKS = 4;
+constexpr int RESET_INTERVAL_CHUNKS = 45, RESET_CARRY_TOKENS = 24, MAX_ENC_WINDOWS = 4;
+constexpr int64_t SAMPLE_RATE = 16000, HOP = 160, WINDOW_FRAMES = 800;
+constexpr int DECODE_BURST = 4;
+
+// grow-only device buffer
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    template <typename T> T *as() { return reinterpret_cast<T *>(p); }
+};
+int ensure(DevBuf &b, size_t bytes) {
+    if (bytes <= b.cap) return QASR_OK;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t want = std::max<size_t>(bytes, 4096);
+    if (hipMalloc(&b.p, want) != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "stream: device allocation failed");
+    b.cap = want;
+    return QASR_OK;
+}
+void release(DevBuf &b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+}
+
+// stream_tail_repeat_blocks (transcribe.rs:38-56): how many times a block of
+// some period <= max_period repeats at the tail; the best (reps, period)
+std::pair<int64_t, int64_t> tail_repeat_blocks(const std::vector<int32_t> &t, int64_t max_period) {
+    const int64_t n = (int64_t)t.size();
+    if (n < 2) return {1, 0};
+    const int64_t cap = std::min(n / 2, max_period > 0 ? max_period : n / 2);
+    int64_t best_reps = 1, best_period = 0;
+    for (int64_t p = 1; p <= cap; p++) {
+        int64_t reps = 1;
+        while ((reps + 1) * p <= n) {
+            const int32_t *a = t.data() + n - (reps + 1) * p, *b = t.data() + n - reps * p;
+            if (!std::equal(a, a + p, b)) break;
+            reps++;
+        }
+        if (reps > best_reps) { best_reps = reps; best_period = p; }
+    }
+    return {best_reps, best_period};
+}
+}  // namespace
+
+struct EncWindow {
+    DevBuf out;
+    int64_t seq = 0;
+};
+
+struct qasr_stream {
+    qasr_decoder *d = nullptr;
+    qasr_encoder *e = nullptr;
+    qasr_stream_config cfg{};
+    // encoder
+    std::vector<EncWindow> win;
+    int64_t enc_cached_total = 0, enc_base_windows = 0;
+    DevBuf partial;
+    int64_t partial_seq = 0, last_partial_cursor = 0;
+    // tokens
+    std::vector<int32_t> raw, stable, prev_tail;
+    // prefill reuse
+    DevBuf embeds, prev_embeds;
+    int64_t prev_prefill_len = 0;
+    int stale = 0;
+    int64_t cursor = 0;
+    int32_t chunk_idx = 0;
+    // scratch
+    DevBuf audio, mel, melsc, enc_all, toks, flags;
+    std::vector<int32_t> host_tok;
+    // statistics of the last chunk
+    int64_t st_reused = 0, st_prefill_len = 0, st_delta = 0, st_steps_total = 0, st_forwards = 0;
+};
+
+extern "C" void qasr_hip_stream_default_config(qasr_stream_config *c) {
+    if (!c) return;
+    c->chunk_sec = 2.0f;
+    c->rollback = 5;
+    c->unfixed_chunks = 2;
+    c->max_new_tokens = 32;
+    c->past_text_conditioning = 0;
+    c->stop_tokens[0] = 151643;   // TOKEN_ENDOFTEXT
+    c->stop_tokens[1] = 151645;   // TOKEN_IM_END
+}
+
+extern "C" int qasr_hip_stream_create(qasr_decoder *d, qasr_encoder *e, const qasr_stream_config *cfg,
+                                      qasr_stream **out) {
+    if (!d || !e || !out) return qasr_fail(QASR_ERR_INVALID, "stream_create: null argument");
+    *out = nullptr;
+    if (encoder_output_dim(e) != d->c.hidden)
+        return qasr_fail(QASR_ERR_INVALID, "stream_create: encoder output_dim != decoder hidden");
+    for (int32_t t : PREFIX)
+        if (t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream_create: vocab too small for the prompt");
+    qasr_stream *s = new qasr_stream();
+    s->d = d;
+    s->e = e;
+    if (cfg) s->cfg = *cfg;
+    else qasr_hip_stream_default_config(&s->cfg);
+    if (s->cfg.chunk_sec <= 0.0f || s->cfg.rollback < 0 || s->cfg.unfixed_chunks < 0 || s->cfg.max_new_tokens <= 0) {
+        delete s;
+        return qasr_fail(QASR_ERR_INVALID, "stream_create: bad configuration");
+    }
+    *out = s;
+    return QASR_OK;
+}
+
+static void release_windows(qasr_stream *s) {
+    for (auto &w : s->win) release(w.out);
+    s->win.clear();
+}
+
+extern "C" void qasr_hip_stream_free(qasr_stream *s) {
+    if (!s) return;
+    (void)hipSetDevice(s->d->h->device);
+    (void)hipStreamSynchronize(s->d->h->stream);
+    release_windows(s);
+    for (DevBuf *b : {&s->partial, &s->embeds, &s->prev_embeds, &s->audio, &s->mel, &s->melsc, &s->enc_all,
+                      &s->toks, &s->flags})
+        release(*b);
+    delete s;
+}
+
+// StreamState::reset (transcribe.rs:865-883)
+extern "C" int qasr_hip_stream_reset(qasr_stream *s) {
+    if (!s) return qasr_fail(QASR_ERR_INVALID, "stream is null");
+    CHECK_H(s->d->h);
+    HIPCHK(hipStreamSynchronize(s->d->h->stream));
+    release_windows(s);
+    s->enc_cached_total = s->enc_base_windows = 0;
+    s->partial_seq = s->last_partial_cursor = 0;
+    s->raw.clear();
+    s->stable.clear();
+    s->prev_tail.clear();
+    s->prev_prefill_len = 0;
+    s->stale = 0;
+    s->cursor = 0;
+    s->chunk_idx = 0;
+    return QASR_OK;
+}
+
+// mel + encoder of host samples[0, ns) into `out` (grown); seq = 0 when too short
+static int encode_slice(qasr_stream *s, const float *samples, int64_t ns, DevBuf &out, int64_t *seq) {
+    hipStream_t st = s->d->h->stream;
+    *seq = 0;
+    const int64_t nf = mel_frames_for(ns);
+    if (nf <= 0) return QASR_OK;
+    TRY(ensure(s->audio, sizeof(float) * ns));
+    HIPCHK(hipMemcpyAsync(s->audio.p, samples, sizeof(float) * ns, hipMemcpyHostToDevice, st));
+    TRY(ensure(s->mel, sizeof(float) * 128 * nf));
+    TRY(ensure(s->melsc, sizeof(float) * mel_scratch_floats(nf)));
+    TRY(mel_dev(s->e, s->audio.as<float>(), ns, s->mel.as<float>(), s->melsc.as<float>()));
+    const int64_t T = encoder_tokens(s->e, nf);
+    TRY(ensure(out, sizeof(float) * T * s->d->c.hidden));
+    int64_t got = 0;
+    TRY(encoder_forward_dev(s->e, s->mel.as<float>(), nf, out.as<float>(), &got));
+    // the host copy of the audio slice must outlive the upload
+    HIPCHK(hipStreamSynchronize(st));
+    *seq = got;
+    return QASR_OK;
+}
+
+static bool is_stop(const qasr_stream *s, int32_t t) {
+    return t == s->cfg.stop_tokens[0] || t == s->cfg.stop_tokens[1];
+}
+
+// index just past TOKEN_ASR_TEXT in raw (0 when absent): the text region
+static size_t text_start(const std::vector<int32_t> &raw) {
+    const auto it = std::find(raw.begin(), raw.end(), TOKEN_ASR_TEXT);
+    return it == raw.end() ? 0 : (size_t)(it - raw.begin()) + 1;
+}
+
+static void carry_reset(qasr_stream *s) {
+    const size_t carry = std::min<size_t>(s->stable.size(), RESET_CARRY_TOKENS);
+    const size_t carry_start = s->stable.size() - carry;
+    s->raw.clear();
+    if (carry > 0) {
+        s->raw.push_back(TOKEN_ASR_TEXT);
+        s->raw.insert(s->raw.end(), s->stable.begin() + carry_start, s->stable.end());
+    }
+    s->prev_prefill_len = 0;
+    s->stale = 0;
+    s->prev_tail.clear();
+    if ((int)s->win.size() >= MAX_ENC_WINDOWS) {
+        s->enc_base_windows += (int64_t)s->win.size();
+        release_windows(s);
+        s->enc_cached_total = 0;
+    }
+}
+
+// greedy decode of up to max_new tokens after the prefill of prefill_len rows;
+// returns the chunk's tokens (stop token excluded)
+static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t> &chunk) {
+    qasr_decoder *d = s->d;
+    hipStream_t st = d->h->stream;
+    const int64_t H = d->c.hidden;
+    const int max_new = s->cfg.max_new_tokens;
+    chunk.clear();
+    if (prefill_len + max_new + DECODE_BURST > d->max_seq)
+        return qasr_fail(QASR_ERR_INVALID, "stream: decoder max_seq too small for this context");
+    // first forward on the last prompt row
+    d->len = prefill_len;
+    TRY(decoder_set_state(d, 0));
+    HIPCHK(hipMemcpyAsync(d->x, s->embeds.as<float>() + prefill_len * H, sizeof(float) * H, hipMemcpyDeviceToDevice,
+                          st));
+    TRY(decoder_enqueue_step(d, false));
+    d->step_pos += 1;
+    int64_t done = 1, seen = 0;
+    s->host_tok.resize(max_new + DECODE_BURST + 1);
+    // tokens t_0 .. t_{max_new-1}; t_j comes from forward j + 1
+    for (;;) {
+        HIPCHK(hipMemcpyAsync(s->host_tok.data() + seen, d->token_log + seen, sizeof(int32_t) * (done - seen),
+                              hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        bool stop = false;
+        for (; seen < done && (int64_t)chunk.size() < max_new; seen++) {
+            const int32_t t = s->host_tok[seen];
+            if (is_stop(s, t)) { stop = true; break; }
+            chunk.push_back(t);
+        }
+        if (stop || (int64_t)chunk.size() >= max_new) break;
+        const int64_t burst = std::min<int64_t>(DECODE_BURST, max_new - done);
+        for (int64_t i = 0; i < burst; i++) TRY(decoder_run_embed_step(d));
+        done += burst;
+    }
+    d->len = prefill_len + done;
+    s->st_forwards = done;
+    s->st_steps_total += done;
+    return QASR_OK;
+}
+
+// one chunk of stream_push_audio; *speech_ended stops the push loop
+static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool finalize,
+                         std::vector<int32_t> &emitted, bool *speech_ended_out, bool *abort_push) {
+    qasr_decoder *d = s->d;
+    hipStream_t st = d->h->stream;
+    const int64_t H = d->c.hidden;
+    const int64_t chunk_samples = (int64_t)(s->cfg.chunk_sec * (float)SAMPLE_RATE);
+    const int64_t win_samples = WINDOW_FRAMES * HOP;
+    const int rollback = s->cfg.rollback;
+    *speech_ended_out = false;
+    *abort_push = false;
+
+    s->cursor = std::min(s->cursor + chunk_samples, n);
+    const bool is_final = finalize && s->cursor >= n;
+
+    // ---- encoder: new complete windows, then the partial tail ----
+    const int64_t full_end = (s->cursor / win_samples) * win_samples;
+    while ((s->enc_base_windows + (int64_t)s->win.size()) * win_samples < full_end) {
+        const int64_t ws = (s->enc_base_windows + (int64_t)s->win.size()) * win_samples;
+        EncWindow w;
+        TRY(encode_slice(s, samples + ws, win_samples, w.out, &w.seq));
+        s->enc_cached_total += w.seq;
+        s->win.push_back(w);
+    }
+    const int64_t partial_age = s->cursor - s->last_partial_cursor;
+    const bool need_encode = s->last_partial_cursor == 0 || partial_age >= 2 * chunk_samples || is_final;
+    int64_t partial_seq = 0;
+    if (full_end < s->cursor) {
+        partial_seq = s->partial_seq;                       // reuse unless re-encoded below
+        if (need_encode) {
+            DevBuf fresh;
+            int64_t seq = 0;
+            TRY(encode_slice(s, samples + full_end, s->cursor - full_end, fresh, &seq));
+            if (seq > 0) {
+                release(s->partial);
+                s->partial = fresh;
+                s->partial_seq = partial_seq = seq;
+                s->last_partial_cursor = s->cursor;
+            } else {
+                release(fresh);
+            }
+        }
+    }
+    const int64_t enc_len = s->enc_cached_total + partial_seq;
+    if (enc_len == 0) {
+        // nothing to decode: the reference returns from the whole push with an
+        // empty delta here (transcribe.rs:1005-1008)
+        s->chunk_idx += 1;
+        *abort_push = true;
+        return QASR_OK;
+    }
+
+    // ---- prompt rows ----
+    const int64_t n_prefix_tokens =
+        (s->cfg.past_text_conditioning && s->chunk_idx >= s->cfg.unfixed_chunks && !s->raw.empty())
+            ? (int64_t)std::max<int64_t>((int64_t)s->raw.size() - rollback, 0)
+            : 0;
+    const int64_t total_seq = 9 + enc_len + 6 + n_prefix_tokens;
+    const int64_t prefill_len = total_seq - 1;
+    TRY(ensure(s->enc_all, sizeof(float) * enc_len * H));
+    int64_t off = 0;
+    for (auto &w : s->win) {
+        HIPCHK(hipMemcpyAsync(s->enc_all.as<float>() + off * H, w.out.p, sizeof(float) * w.seq * H,
+                              hipMemcpyDeviceToDevice, st));
+        off += w.seq;
+    }
+    if (partial_seq > 0)
+        HIPCHK(hipMemcpyAsync(s->enc_all.as<float>() + off * H, s->partial.p, sizeof(float) * partial_seq * H,
+                              hipMemcpyDeviceToDevice, st));
+    std::vector<int32_t> toks(PREFIX, PREFIX + 9);
+    toks.insert(toks.end(), SUFFIX, SUFFIX + 6);
+    toks.insert(toks.end(), s->raw.begin(), s->raw.begin() + n_prefix_tokens);
+    for (int32_t t : toks)
+        if (t < 0 || t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream: token id out of range");
+    TRY(ensure(s->toks, sizeof(int32_t) * toks.size()));
+    HIPCHK(hipMemcpyAsync(s->toks.p, toks.data(), sizeof(int32_t) * toks.size(), hipMemcpyHostToDevice, st));
+    TRY(ensure(s->embeds, sizeof(float) * total_seq * H));
+    LAUNCHCHK(launch_build_prompt(s->embeds.as<float>(), d->embed, s->toks.as<int>(), 9, s->enc_all.as<float>(),
+                                  (int)enc_len, (int)(6 + n_prefix_tokens), (int)H, st),
+              "stream prompt");
+
+    // ---- prefill with common-prefix reuse ----
+    int64_t reused = 0;
+    if (s->prev_prefill_len > 0) {
+        const int64_t cmp = std::min(prefill_len, s->prev_prefill_len);
+        TRY(ensure(s->flags, sizeof(int) * cmp));
+        LAUNCHCHK(launch_row_diff(s->embeds.as<float>(), s->prev_embeds.as<float>(), cmp, H, s->flags.as<int>(), st),
+                  "stream row diff");
+        std::vector<int> fl(cmp);
+        HIPCHK(hipMemcpyAsync(fl.data(), s->flags.p, sizeof(int) * cmp, hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        while (reused < cmp && !fl[reused]) reused++;
+    }
+    d->len = reused;
+    const int64_t delta = prefill_len - reused;
+    if (prefill_len + 1 > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "stream: decoder max_seq too small");
+    if (delta > 0) TRY(decoder_prefill_dev(d, s->embeds.as<float>() + reused * H, delta));
+    s->st_reused = reused;
+    s->st_prefill_len = prefill_len;
+    s->st_delta = delta;
+
+    // ---- decode ----
+    std::vector<int32_t> chunk;
+    TRY(decode_chunk(s, prefill_len, chunk));
+    // keep this chunk's prefill rows for the next comparison
+    std::swap(s->embeds, s->prev_embeds);
+    s->prev_prefill_len = prefill_len;
+
+    // ---- speech end: commit everything that was held back ----
+    const bool speech_ended = chunk.empty() && !s->raw.empty() && s->chunk_idx >= s->cfg.unfixed_chunks;
+    if (speech_ended) {
+        const size_t ts = text_start(s->raw);
+        for (size_t i = s->stable.size(); i + ts < s->raw.size(); i++) {
+            s->stable.push_back(s->raw[ts + i]);
+            emitted.push_back(s->raw[ts + i]);
+        }
+    }
+    s->raw.resize((size_t)n_prefix_tokens);
+    s->raw.insert(s->raw.end(), chunk.begin(), chunk.end());
+
+    if (!speech_ended) {
+        // ---- degeneracy and periodic re-anchoring ----
+        if (s->raw == s->prev_tail) {
+            s->stale += 1;
+        } else {
+            s->stale = 0;
+            s->prev_tail = s->raw;
+        }
+        const int64_t reps = tail_repeat_blocks(s->raw, DEGEN_MAX_PERIOD).first;
+        if (s->stale >= STALE_CHUNKS || reps >= DEGEN_MIN_REPEATS) carry_reset(s);
+        if (s->chunk_idx > 0 && s->chunk_idx % RESET_INTERVAL_CHUNKS == 0) carry_reset(s);
+        // ---- emit the tokens that are now stable ----
+        const size_t ts = text_start(s->raw);
+        const int64_t n_text = (int64_t)s->raw.size() - (int64_t)std::min(ts, s->raw.size());
+        int64_t cand = 0;
+        if (is_final) cand = n_text;
+        else if (s->chunk_idx >= s->cfg.unfixed_chunks) cand = std::max<int64_t>(n_text - rollback, 0);
+        const int64_t from = (int64_t)s->stable.size();
+        const int64_t to = std::max(cand, from);
+        for (int64_t i = from; i < to; i++) {
+            if (i < n_text) {
+                s->stable.push_back(s->raw[ts + i]);
+                emitted.push_back(s->raw[ts + i]);
+            }
+        }
+    }
+    s->chunk_idx += 1;
+    *speech_ended_out = speech_ended;
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_t n_samples, int finalize,
+                                    int32_t *tokens_out, int64_t cap, int64_t *n_out) {
+    if (!s) return qasr_fail(QASR_ERR_INVALID, "stream is null");
+    CHECK_H(s->d->h);
+    if (n_out) *n_out = 0;
+    if (n_samples < 0 || (n_samples > 0 && !samples) || n_samples < s->cursor)
+        return qasr_fail(QASR_ERR_INVALID, "stream_push: samples must hold the whole stream so far");
+    const int64_t chunk_samples = (int64_t)(s->cfg.chunk_sec * (float)SAMPLE_RATE);
+    std::vector<int32_t> emitted;
+    const int64_t available = n_samples - s->cursor;
+    if ((available < chunk_samples && !finalize) || available == 0) return QASR_OK;
+    while (s->cursor < n_samples) {
+        if (n_samples - s->cursor < chunk_samples && !finalize) break;
+        bool ended = false, abort_push = false;
+        TRY(process_chunk(s, samples, n_samples, finalize != 0, emitted, &ended, &abort_push));
+        if (abort_push) {
+            emitted.clear();
+            break;
+        }
+        if (ended) break;
+    }
+    if (n_out) *n_out = (int64_t)emitted.size();
+    if ((int64_t)emitted.size() > cap && tokens_out)
+        return qasr_fail(QASR_ERR_INVALID, "stream_push: tokens_out too small (n_out holds the count)");
+    if (tokens_out) std::copy(emitted.begin(), emitted.end(), tokens_out);
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_stream_tokens(const qasr_stream *s, int32_t *tokens_out, int64_t cap, int64_t *n) {
+    if (!s || !n) return qasr_fail(QASR_ERR_INVALID, "stream_tokens: null argument");
+    *n = (int64_t)s->stable.size();
+    if (tokens_out) std::copy(s->stable.begin(), s->stable.begin() + std::min<int64_t>(cap, *n), tokens_out);
+    return QASR_OK;
+}
+
+extern "C" int64_t qasr_hip_stream_audio_cursor(const qasr_stream *s) { return s ? s->cursor : -1; }
+
+extern "C" int qasr_hip_stream_stats(const qasr_stream *s, int64_t *stats) {
+    if (!s || !stats) return qasr_fail(QASR_ERR_INVALID, "stream_stats: null argument");
+    const int64_t v[QASR_STREAM_STATS] = {s->chunk_idx,  s->st_reused,        s->st_prefill_len,
+                                          s->st_delta,   s->st_forwards,      s->st_steps_total,
+                                          (int64_t)s->win.size() + s->enc_base_windows, (int64_t)s->raw.size()};
+    std::copy(v, v + QASR_STREAM_STATS, stats);
+    return QASR_OK;
+}

@@ -23,7 +23,8 @@ class Device:
 
     def close(self):
         if self.h:
-            for c in list(self._children):   # the C ABI requires them freed first
+            # the C ABI requires them freed first; streams before the decoders they borrow
+            for c in sorted(self._children, key=lambda o: getattr(o, "_close_first", 1), reverse=True):
                 c.close()
             lib().qasr_hip_destroy(self.h)
             self.h = None

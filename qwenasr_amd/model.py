@@ -4,7 +4,7 @@ import ctypes as C
 import numpy as np
 
 from ._lib import (I64, QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, EncConfig, EncLayer,
-                   EncWeights, I32, P, check, lib)
+                   EncWeights, I32, P, StreamConfig, check, lib)
 
 
 class Decoder:
@@ -179,3 +179,63 @@ def profile_decoder(decoder, n_steps):
                                          n.ctypes.data_as(P)))
     return [dict(kernel=k, us=float(us[i]), bytes=float(by[i]), per_step=int(n[i]))
             for i, k in enumerate(KERNEL_KINDS)]
+
+
+class Stream:
+    """Incremental streaming transcription (StreamState + stream_push_audio,
+    transcribe.rs:902-1304) on a device-resident decoder and encoder.  push()
+    takes the whole audio so far and returns the newly committed token ids."""
+
+    _close_first = 2
+
+    def __init__(self, decoder, encoder, **cfg):
+        c = StreamConfig()
+        lib().qasr_hip_stream_default_config(C.byref(c))
+        for k, v in cfg.items():
+            if k == "stop_tokens":
+                c.stop_tokens[0], c.stop_tokens[1] = v
+            else:
+                setattr(c, k, v)
+        s = P()
+        check(lib().qasr_hip_stream_create(decoder.d, encoder.e, C.byref(c), C.byref(s)))
+        self.s = s
+        self.decoder, self.encoder = decoder, encoder
+        decoder.dev.adopt(self)
+
+    def push(self, samples, finalize=False):
+        x = np.ascontiguousarray(samples, np.float32)
+        out = np.empty(4096, np.int32)
+        n = I64()
+        check(lib().qasr_hip_stream_push(self.s, x.ctypes.data_as(P), x.size, 1 if finalize else 0,
+                                         out.ctypes.data_as(P), out.size, C.byref(n)))
+        return out[:n.value].copy()
+
+    def tokens(self):
+        n = I64()
+        check(lib().qasr_hip_stream_tokens(self.s, None, 0, C.byref(n)))
+        out = np.empty(max(n.value, 1), np.int32)
+        check(lib().qasr_hip_stream_tokens(self.s, out.ctypes.data_as(P), out.size, C.byref(n)))
+        return out[:n.value].copy()
+
+    def reset(self):
+        check(lib().qasr_hip_stream_reset(self.s))
+
+    @property
+    def audio_cursor(self):
+        return int(lib().qasr_hip_stream_audio_cursor(self.s))
+
+    def stats(self):
+        st = np.zeros(8, np.int64)
+        check(lib().qasr_hip_stream_stats(self.s, st.ctypes.data_as(P)))
+        return st
+
+    def close(self):
+        if self.s:
+            lib().qasr_hip_stream_free(self.s)
+            self.s = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
