@@ -267,6 +267,28 @@ int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *sa
                                int64_t n_samples, int32_t n_steps, int32_t *tokens_out,
                                double *times_ms);
 
+/* ---- multi-stream decode (no counterpart in the reference,
+ * whose streaming is batch 1 per QwenCtx) ----
+ * Up to 32 independent streams share a loaded decoder's weights; each owns a
+ * KV region of max_seq positions (<= the decoder's max_seq) and steps together
+ * with the others: M = streams int8 MFMA projections, attention over every
+ * stream's own cache.  Integer dots are exact, so a stream's tokens equal
+ * those of the single-stream decoder run with the same attention split count
+ * (e.g. 1 for both). */
+typedef struct qasr_batch qasr_batch;
+int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t max_seq, int64_t max_steps,
+                          qasr_batch **out);
+void qasr_hip_batch_free(qasr_batch *b);
+/* decoder_prefill of one stream (host f32 [seq_len][hidden]) */
+int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float *embeds, int64_t seq_len);
+int qasr_hip_batch_set_len(qasr_batch *b, int32_t stream, int64_t len);
+int64_t qasr_hip_batch_len(const qasr_batch *b, int32_t stream);
+/* attn_splits: 1, 2, 4, 8, 16 (-1: automatic per context bucket); use_graph as the decoder's */
+int qasr_hip_batch_set_options(qasr_batch *b, int attn_splits, int use_graph);
+/* n_steps greedy steps of every stream; first_tokens [streams] (each stream's
+ * first input token); tokens_out [streams][n_steps] */
+int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_tokens, int32_t n_steps, int32_t *tokens_out);
+
 /* ---- A20: incremental streaming (stream_push_audio, transcribe.rs:902-1304) ----
  * A stream borrows a decoder (its KV cache and step state) and an encoder; one
  * stream per decoder at a time.  Text comes out as token ids (the caller's

@@ -135,6 +135,13 @@ _SIGS = {
     "qasr_hip_stream_tokens": (C.c_int, [P, P, I64, C.POINTER(I64)]),
     "qasr_hip_stream_audio_cursor": (I64, [P]),
     "qasr_hip_stream_stats": (C.c_int, [P, P]),
+    "qasr_hip_batch_create": (C.c_int, [P, I32, I64, I64, C.POINTER(P)]),
+    "qasr_hip_batch_free": (None, [P]),
+    "qasr_hip_batch_prefill": (C.c_int, [P, I32, P, I64]),
+    "qasr_hip_batch_set_len": (C.c_int, [P, I32, I64]),
+    "qasr_hip_batch_len": (I64, [P, I32]),
+    "qasr_hip_batch_set_options": (C.c_int, [P, C.c_int, C.c_int]),
+    "qasr_hip_batch_generate": (C.c_int, [P, P, I32, P]),
 }
 
 _lib = None

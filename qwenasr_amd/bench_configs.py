@@ -2,6 +2,7 @@
 
     python -m qwenasr_amd.bench_configs config1 [reps]
     python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
+    python -m qwenasr_amd.bench_configs config4 [n_streams] [steps]
 
 config1: the prefill / audio-encoder int8 x bf16 GEMMs at M = 375 (also 390,
 404), the seven 0.6B projections and the LM head, seeded N(0,0.02) weights
@@ -17,6 +18,15 @@ replay, HIP events), per-kernel us and algorithmic GB/s (the same
 back-to-back timing as bench.py), int8 matvec GB/s and GQA attention us per
 token.
 
+config4: the 0.6B decoder (28 layers, int8) decoding 32 independent streams
+together, each with a ragged prefix of U[100, 1500] positions (seeded;
+prefilled from N(0,1) embeddings), `steps` greedy steps per stream (a 2 s
+chunk's worth of text).  Reports the batched step time and aggregate
+tokens/s (HIP events, graph replay), the same streams decoded one at a time
+by the single-stream decoder, the token identity of the two, and the
+step's algorithmic bytes (int8 weights once + every stream's KV cache) as
+GB/s.
+
 Each configuration prints one JSON line (stdout); progress goes to stderr.
 """
 import json
@@ -27,8 +37,8 @@ import numpy as np
 
 from . import Device
 from . import kernels as K
-from .model import Decoder, profile_decoder
-from .synth import DEC_1_7B, SynthDecoder, normal_bf16
+from .model import Batch, Decoder, profile_decoder
+from .synth import DEC_0_6B, DEC_1_7B, SynthDecoder, normal_bf16
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -121,11 +131,86 @@ def config3(n_layers=28, steps=20):
     dev.close()
 
 
+def config4(n_streams=32, steps=32):
+    dev = Device(0)
+    cfg = dict(DEC_0_6B)
+    t0 = time.time()
+    w = SynthDecoder(cfg, seed=1004)
+    log(f"[config4] synthetic 0.6B decoder in {time.time() - t0:.1f}s")
+    rng = np.random.default_rng(1004)
+    lens = rng.integers(100, 1501, n_streams)
+    first = rng.integers(0, cfg["vocab"], n_streams)
+    max_seq = 2048
+    dec = Decoder(dev, w, max_seq=max_seq)
+    bat = Batch(dec, n_streams, max_seq, max_steps=steps)
+    H = cfg["hidden"]
+    prefixes = [rng.standard_normal((int(L), H), dtype=np.float32) for L in lens]
+    t0 = time.time()
+    for i, p in enumerate(prefixes):
+        bat.prefill(i, p)
+    dev.sync()
+    log(f"[config4] {n_streams} prefixes prefilled ({int(lens.sum())} positions) in {time.time() - t0:.1f}s")
+    # warm-up: capture the step graphs of every split count the run meets
+    toks = bat.generate(first, steps)
+    for i in range(n_streams):
+        bat.set_len(i, int(lens[i]))
+    reps, times = 3, []
+    for _ in range(reps):
+        dev.sync()
+        dev.timer_start()
+        toks = bat.generate(first, steps)
+        times.append(dev.timer_stop())
+        for i in range(n_streams):
+            bat.set_len(i, int(lens[i]))
+    ms = float(np.median(times))
+    us_step = ms * 1e3 / steps
+    tok_s = n_streams * steps / (ms / 1e3)
+    log(f"[config4] batched: {us_step:.1f} us/step, {tok_s:.0f} tokens/s ({n_streams} streams)")
+    # the same streams one at a time on the single-stream decoder
+    solo_ms, match = 0.0, 0
+    for i in range(n_streams):
+        dec.kv_len = 0
+        dec.prefill(prefixes[i])
+        dec.generate(2, first_token=int(first[i]))          # graph capture of the bucket
+        dec.kv_len = int(lens[i])
+        dev.sync()
+        dev.timer_start()
+        t = dec.generate(steps, first_token=int(first[i]))
+        solo_ms += dev.timer_stop()
+        match += int((t == toks[i]).all())
+    solo_tok_s = n_streams * steps / (solo_ms / 1e3)
+    log(f"[config4] one at a time: {solo_ms * 1e3 / (n_streams * steps):.1f} us/token, {solo_tok_s:.0f} tokens/s; "
+        f"identical streams {match}/{n_streams}")
+    # algorithmic bytes of one batched step: int8 weights (+ scales) once and
+    # every stream's K/V rows (f32) at the mid-run context
+    c = cfg
+    hd, qd, kvd, I = c["head_dim"], c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"], c["intermediate"]
+    per_layer_w = (qd + 2 * kvd) * (H + 4) + H * (qd + 4) + 2 * I * (H + 4) + H * (I + 4)
+    w_bytes = c["n_layers"] * per_layer_w + c["vocab"] * (H + 4)
+    mid = lens + steps // 2
+    kv_bytes = int(c["n_layers"] * 2 * kvd * 4 * mid.sum())
+    gbs = (w_bytes + kv_bytes) / (us_step * 1e3)
+    print(json.dumps({"config": f"config 4: Qwen3-ASR-0.6B decoder, {n_streams} streams, prefixes U[100,1500], "
+                                f"{steps} greedy steps per stream, f32 KV",
+                      "prefix_lens": [int(x) for x in lens],
+                      "batched_us_per_step": round(us_step, 2), "batched_tokens_per_s": round(tok_s, 1),
+                      "solo_us_per_token": round(solo_ms * 1e3 / (n_streams * steps), 2),
+                      "solo_tokens_per_s": round(solo_tok_s, 1), "speedup": round(tok_s / solo_tok_s, 2),
+                      "identical_streams": f"{match}/{n_streams}",
+                      "step_bytes": {"weights": w_bytes, "kv": kv_bytes},
+                      "step_gbs": round(gbs, 1), "step_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}))
+    bat.close()
+    dec.close()
+    dev.close()
+
+
 if __name__ == "__main__":
     what = sys.argv[1] if len(sys.argv) > 1 else "config3"
     if what == "config1":
         config1(int(sys.argv[2]) if len(sys.argv) > 2 else 20)
     elif what == "config3":
         config3(int(sys.argv[2]) if len(sys.argv) > 2 else 28, int(sys.argv[3]) if len(sys.argv) > 3 else 20)
+    elif what == "config4":
+        config4(int(sys.argv[2]) if len(sys.argv) > 2 else 32, int(sys.argv[3]) if len(sys.argv) > 3 else 32)
     else:
         raise SystemExit(f"unknown configuration {what!r}")

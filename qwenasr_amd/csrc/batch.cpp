@@ -1,0 +1,344 @@
+// Multi-stream decode: B <= 32 independent streams share
+// the decoder's int8 weights and step together.  Each stream owns a KV region
+// (layout [layer][stream][kv_head][max_seq][hd], f32) with its own length and
+// device step state {token, pos, step, flag}.  One step per layer: per-row
+// RMSNorm + int8 quantization, an M = B W8A8 projection on int8 MFMA, the
+// decode attention over every stream's ragged cache (grid y = stream), the
+// split merge, and the o_proj / gate_up / down projections; then the LM-head
+// argmax per stream.  Integer dots are exact and every per-row operation is
+// the single-stream one, so each stream's tokens are those it would produce
+// alone.  That includes the attention's split partition: each stream gets
+// the single-stream decoder's partition for its own context bucket (groups per
+// block from a per-position table, kept per stream on the device and advanced
+// by the argmax finisher), inside a launch with the largest stream's split
+// count; the extra splits of a shorter stream are empty and merge as exact
+// zeros.  Steps replay one captured HIP graph per split count.
+#include "decoder.h"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+using namespace qasr;
+
+#define TRY(x)                  \
+    do {                        \
+        int rc_ = (x);          \
+        if (rc_ != QASR_OK) {   \
+            return rc_;         \
+        }                       \
+    } while (0)
+
+namespace {
+constexpr int MAX_STREAMS = 32;
+constexpr int ARGMAX_BLOCKS = 512;
+}
+
+struct qasr_batch {
+    qasr_decoder *d = nullptr;
+    int B = 0;
+    int64_t max_seq = 0, max_steps = 0;
+    void *kc = nullptr, *vc = nullptr;
+    float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *xs = nullptr, *part = nullptr;
+    float *rope_cur = nullptr, *am_val = nullptr;
+    int8_t *xq = nullptr;
+    int32_t *state = nullptr, *token_log = nullptr, *am_idx = nullptr;
+    int32_t *gpb_dev = nullptr, *gpb_table = nullptr;   // per-stream / per-position attention partition
+    std::vector<int32_t> gpb_host;
+    int64_t part_stride = 0;
+    std::vector<int64_t> len;          // host copy of each stream's KV length
+    int64_t steps_done = 0;            // steps since the last set of first tokens
+    int n_split = 0, use_graph = 1;
+    std::map<int, hipGraphExec_t> graphs;                // by split count
+    std::vector<void *> allocs;
+};
+
+template <typename T>
+static int balloc(qasr_batch *b, T **p, size_t count, bool zero = false) {
+    void *v = nullptr;
+    if (hipMalloc(&v, count * sizeof(T) + 256) != hipSuccess)
+        return qasr_fail(QASR_ERR_NOMEM, "batch: device allocation failed");
+    b->allocs.push_back(v);
+    if (zero && hipMemset(v, 0, count * sizeof(T) + 256) != hipSuccess)
+        return qasr_fail(QASR_ERR_HIP, "batch: memset failed");
+    *p = reinterpret_cast<T *>(v);
+    return QASR_OK;
+}
+
+extern "C" void qasr_hip_batch_free(qasr_batch *b) {
+    if (!b) return;
+    (void)hipSetDevice(b->d->h->device);
+    (void)hipStreamSynchronize(b->d->h->stream);
+    for (auto &g : b->graphs) (void)hipGraphExecDestroy(g.second);
+    for (void *p : b->allocs) (void)hipFree(p);
+    delete b;
+}
+
+// context bucket of a step whose new position is pos (the single-stream
+// decoder's rule, decoder_ctx_cap at L = pos + 1, with this batch's capacity)
+static int64_t batch_cap(const qasr_batch *b, int64_t pos) {
+    const int64_t c = ((pos + 1 + 255) / 256) * 256;
+    return std::min<int64_t>(std::max<int64_t>(c, 256), b->max_seq);
+}
+
+// split count of a bucket: the forced count, else the single-stream automatic
+// choice limited to the 16 splits the merge pass takes
+static int batch_splits(const qasr_batch *b, int64_t cap) {
+    if (b->n_split > 0) return b->n_split;
+    return std::min(16, attn_splits_auto(b->d->c, cap));
+}
+
+// groups of 8 positions per attention block for every position (the
+// single-stream decoder's static partition: ceil(ceil(cap / 8) / splits))
+static int batch_partition(qasr_batch *b) {
+    b->gpb_host.resize(b->max_seq);
+    for (int64_t p = 0; p < b->max_seq; p++) {
+        const int64_t cap = batch_cap(b, p);
+        const int S = batch_splits(b, cap);
+        b->gpb_host[p] = (int32_t)((((cap + 7) / 8) + S - 1) / S);
+    }
+    HIPCHK(hipMemcpy(b->gpb_table, b->gpb_host.data(), sizeof(int32_t) * b->max_seq, hipMemcpyHostToDevice));
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t max_seq, int64_t max_steps,
+                                     qasr_batch **out) {
+    if (!d || !out) return qasr_fail(QASR_ERR_INVALID, "batch_create: null argument");
+    CHECK_H(d->h);
+    *out = nullptr;
+    const qasr_dec_config &c = d->c;
+    if (n_streams <= 0 || n_streams > MAX_STREAMS)
+        return qasr_fail(QASR_ERR_INVALID, "batch_create: 1..32 streams");
+    if (max_seq <= 0 || max_seq > d->max_seq || max_steps <= 0)
+        return qasr_fail(QASR_ERR_INVALID, "batch_create: max_seq must be in 1..decoder max_seq, max_steps > 0");
+    if (c.n_heads != 16 || c.n_kv_heads != 8 || c.head_dim != 128 || d->kv_bf16)
+        return qasr_fail(QASR_ERR_INVALID, "batch_create: needs the 16/8-head, head_dim 128 decoder with an f32 KV cache");
+    auto steps_ok = [](int64_t k) { return k % 1024 == 0 && (k == 1024 || k == 2048 || k == 3072 || k == 4096 || k == 6144); };
+    if (!steps_ok(c.hidden) || !steps_ok(c.intermediate) || c.hidden > 4096 || c.vocab % 16)
+        return qasr_fail(QASR_ERR_INVALID, "batch_create: hidden and intermediate must be 1024, 2048, 3072, 4096 or 6144");
+    qasr_batch *b = new qasr_batch();
+    b->d = d;
+    b->B = n_streams;
+    b->max_seq = max_seq;
+    b->max_steps = max_steps;
+    b->len.assign(n_streams, 0);
+    b->use_graph = d->use_graph;         // the decoder's setting (QASR_DISABLE_GRAPH=1 turns both off)
+    const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd, kvd = (int64_t)c.n_kv_heads * hd;
+    const int64_t I = c.intermediate, nqkv = qd + 2 * kvd;
+    const int64_t kmax = std::max({H, qd, I});
+    const size_t kv = (size_t)c.n_layers * n_streams * c.n_kv_heads * max_seq * hd;
+    b->part_stride = (2 * c.n_heads + c.n_heads * hd) * 16;
+    int rc = QASR_OK;
+    float *kcf = nullptr, *vcf = nullptr;
+    if (rc == QASR_OK) rc = balloc(b, &kcf, kv, true);
+    if (rc == QASR_OK) rc = balloc(b, &vcf, kv, true);
+    b->kc = kcf;
+    b->vc = vcf;
+    if (rc == QASR_OK) rc = balloc(b, &b->x, (size_t)n_streams * H);
+    if (rc == QASR_OK) rc = balloc(b, &b->qkv, (size_t)n_streams * nqkv);
+    if (rc == QASR_OK) rc = balloc(b, &b->att, (size_t)n_streams * qd);
+    if (rc == QASR_OK) rc = balloc(b, &b->ffn, (size_t)n_streams * I);
+    if (rc == QASR_OK) rc = balloc(b, &b->xq, (size_t)MAX_STREAMS * kmax, true);   // rows >= B stay zero
+    if (rc == QASR_OK) rc = balloc(b, &b->xs, MAX_STREAMS, true);
+    if (rc == QASR_OK) rc = balloc(b, &b->part, (size_t)n_streams * b->part_stride);
+    if (rc == QASR_OK) rc = balloc(b, &b->rope_cur, (size_t)n_streams * 256);
+    if (rc == QASR_OK) rc = balloc(b, &b->state, (size_t)n_streams * 4, true);
+    if (rc == QASR_OK) rc = balloc(b, &b->token_log, (size_t)n_streams * max_steps, true);
+    if (rc == QASR_OK) rc = balloc(b, &b->am_val, (size_t)ARGMAX_BLOCKS * 32);
+    if (rc == QASR_OK) rc = balloc(b, &b->am_idx, (size_t)ARGMAX_BLOCKS * 32);
+    if (rc == QASR_OK) rc = balloc(b, &b->gpb_dev, (size_t)n_streams, true);
+    if (rc == QASR_OK) rc = balloc(b, &b->gpb_table, (size_t)max_seq);
+    if (rc == QASR_OK) rc = batch_partition(b);
+    if (rc != QASR_OK) {
+        qasr_hip_batch_free(b);
+        return rc;
+    }
+    *out = b;
+    return QASR_OK;
+}
+
+static int64_t stream_layer_elems(const qasr_batch *b) {
+    return (int64_t)b->d->c.n_kv_heads * b->max_seq * b->d->c.head_dim;
+}
+
+// decoder_prefill (decoder.rs:455) of one stream: the decoder's prefill run on
+// the stream's view of the cache
+extern "C" int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float *embeds, int64_t seq_len) {
+    if (!b || !embeds || seq_len <= 0) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: bad arguments");
+    qasr_decoder *d = b->d;
+    CHECK_H(d->h);
+    if (stream < 0 || stream >= b->B) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: stream out of range");
+    if (b->len[stream] + seq_len > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: capacity exceeded");
+    const int64_t H = d->c.hidden, le = stream_layer_elems(b);
+    float *emb = nullptr;
+    HIPCHK(hipMalloc(&emb, sizeof(float) * seq_len * H));
+    hipError_t e = hipMemcpyAsync(emb, embeds, sizeof(float) * seq_len * H, hipMemcpyHostToDevice, d->h->stream);
+    // swap in the stream's view: base, layer stride, capacity, length
+    void *kc0 = d->kc, *vc0 = d->vc;
+    const int64_t ms0 = d->max_seq, len0 = d->len, ls0 = d->kv_layer_stride;
+    d->kc = reinterpret_cast<float *>(b->kc) + stream * le;
+    d->vc = reinterpret_cast<float *>(b->vc) + stream * le;
+    d->kv_layer_stride = (int64_t)b->B * le;
+    d->max_seq = b->max_seq;
+    d->len = b->len[stream];
+    int rc = e == hipSuccess ? decoder_prefill_dev(d, emb, seq_len) : qasr_fail(QASR_ERR_HIP, "batch_prefill: upload");
+    d->kc = kc0;
+    d->vc = vc0;
+    d->kv_layer_stride = ls0;
+    d->max_seq = ms0;
+    d->len = len0;
+    (void)hipStreamSynchronize(d->h->stream);
+    (void)hipFree(emb);
+    if (rc == QASR_OK) b->len[stream] += seq_len;
+    return rc;
+}
+
+extern "C" int qasr_hip_batch_set_len(qasr_batch *b, int32_t stream, int64_t len) {
+    if (!b || stream < 0 || stream >= b->B || len < 0 || len > b->max_seq)
+        return qasr_fail(QASR_ERR_INVALID, "batch_set_len: bad arguments");
+    b->len[stream] = len;
+    return QASR_OK;
+}
+
+extern "C" int64_t qasr_hip_batch_len(const qasr_batch *b, int32_t stream) {
+    return (b && stream >= 0 && stream < b->B) ? b->len[stream] : -1;
+}
+
+extern "C" int qasr_hip_batch_set_options(qasr_batch *b, int attn_splits, int use_graph) {
+    if (!b) return qasr_fail(QASR_ERR_INVALID, "batch is null");
+    CHECK_H(b->d->h);
+    if (attn_splits < 0) b->n_split = 0;
+    if (attn_splits > 0) {
+        if (attn_splits != 1 && attn_splits != 2 && attn_splits != 4 && attn_splits != 8 && attn_splits != 16)
+            return qasr_fail(QASR_ERR_INVALID, "batch_set_options: attn_splits must be 1, 2, 4, 8 or 16");
+        b->n_split = attn_splits;
+    }
+    b->use_graph = use_graph ? 1 : 0;
+    HIPCHK(hipStreamSynchronize(b->d->h->stream));
+    for (auto &g : b->graphs) HIPCHK(hipGraphExecDestroy(g.second));
+    b->graphs.clear();
+    return batch_partition(b);
+}
+
+// one batched step with n_split attention splits
+static int batch_enqueue_step(qasr_batch *b, int n_split) {
+    qasr_decoder *d = b->d;
+    const qasr_dec_config &c = d->c;
+    hipStream_t st = d->h->stream;
+    const int B = b->B, H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    const int I = c.intermediate, nqkv = qd + 2 * kvd;
+    const int64_t le = stream_layer_elems(b);
+    LAUNCHCHK(launch_embed_rows(b->x, d->embed, b->state, B, H, st), "batch embed");
+    auto mv = [&](const int8_t *w, const float *ws, float *y, int64_t ldy, int K, int N, int mode) -> int {
+        BatchMvArgs a{};
+        a.xq = b->xq; a.xs = b->xs; a.w = w; a.ws = ws; a.y = y; a.ldy = ldy; a.K = K; a.N = N; a.B = B;
+        LAUNCHCHK(launch_w8a8_batch(a, mode, st), "batch projection");
+        return QASR_OK;
+    };
+    for (int l = 0; l < c.n_layers; l++) {
+        const DecLayerDev &L = d->L[l];
+        LAUNCHCHK(launch_quant_rows(b->x, L.in_norm, c.eps, H, B, b->xq, b->xs, st), "batch norm+quant");
+        TRY(mv(L.wqkv, L.sqkv, b->qkv, nqkv, H, nqkv, MV_PLAIN));
+        AttnDecodeArgs t{};
+        t.qkv = b->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
+        t.rope_cos = d->rc; t.rope_sin = d->rs; t.rope_cur = b->rope_cur; t.state = b->state;
+        t.kcache = reinterpret_cast<float *>(b->kc) + (int64_t)l * B * le;
+        t.vcache = reinterpret_cast<float *>(b->vc) + (int64_t)l * B * le;
+        t.head_stride = b->max_seq * hd;
+        t.part = b->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = b->att;
+        t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = 1.0f / sqrtf((float)hd);
+        t.gpb = 1;                           // the per-stream gpb_dev rows are used
+        t.gpb_dev = b->gpb_dev;
+        t.batch = B; t.batch_kv_stride = le; t.batch_qkv_stride = nqkv; t.batch_part_stride = b->part_stride;
+        LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
+        LAUNCHCHK(launch_attn_merge_rows(b->part, b->part_stride, n_split, nullptr, qd, b->xq, b->xs, B, st),
+                  "batch merge+quant");
+        TRY(mv(L.wo, L.so, b->x, H, qd, H, MV_ADDTO));
+        LAUNCHCHK(launch_quant_rows(b->x, L.post_norm, c.eps, H, B, b->xq, b->xs, st), "batch norm+quant");
+        TRY(mv(L.wgu, L.sgu, b->ffn, I, H, 2 * I, MV_SWIGLU));
+        LAUNCHCHK(launch_quant_rows(b->ffn, nullptr, 0.0f, I, B, b->xq, b->xs, st), "batch quant");
+        TRY(mv(L.wdown, L.sdown, b->x, H, I, H, MV_ADDTO));
+    }
+    LAUNCHCHK(launch_quant_rows(b->x, d->norm, c.eps, H, B, b->xq, b->xs, st), "batch final norm");
+    BatchMvArgs am{};
+    am.xq = b->xq; am.xs = b->xs; am.w = d->lm; am.ws = d->lm_s; am.K = H; am.N = c.vocab; am.B = B;
+    am.part_val = b->am_val; am.part_idx = b->am_idx;
+    LAUNCHCHK(launch_argmax_batch(am, ARGMAX_BLOCKS, b->state, b->token_log, b->max_steps, d->rc, d->rs,
+                                  b->rope_cur, (int)b->max_seq, b->gpb_table, b->gpb_dev, st),
+              "batch argmax");
+    return QASR_OK;
+}
+
+// set every stream's step state {first token, len, 0, 0} and RoPE rows
+static int batch_set_state(qasr_batch *b, const int32_t *first_tokens) {
+    qasr_decoder *d = b->d;
+    hipStream_t st = d->h->stream;
+    const int64_t hd = d->c.head_dim;
+    std::vector<int32_t> hs((size_t)b->B * 4, 0);
+    for (int i = 0; i < b->B; i++) {
+        if (first_tokens[i] < 0 || first_tokens[i] >= d->c.vocab)
+            return qasr_fail(QASR_ERR_INVALID, "batch: token id out of range");
+        hs[4 * i] = first_tokens[i];
+        hs[4 * i + 1] = (int32_t)b->len[i];
+    }
+    HIPCHK(hipMemcpyAsync(b->state, hs.data(), sizeof(int32_t) * hs.size(), hipMemcpyHostToDevice, st));
+    std::vector<int32_t> gp(b->B);
+    for (int i = 0; i < b->B; i++) gp[i] = b->gpb_host[b->len[i]];
+    HIPCHK(hipMemcpyAsync(b->gpb_dev, gp.data(), sizeof(int32_t) * b->B, hipMemcpyHostToDevice, st));
+    for (int i = 0; i < b->B; i++) {
+        HIPCHK(hipMemcpyAsync(b->rope_cur + 256 * i, d->rc + b->len[i] * hd, sizeof(float) * hd,
+                              hipMemcpyDeviceToDevice, st));
+        HIPCHK(hipMemcpyAsync(b->rope_cur + 256 * i + hd, d->rs + b->len[i] * hd, sizeof(float) * hd,
+                              hipMemcpyDeviceToDevice, st));
+    }
+    HIPCHK(hipStreamSynchronize(st));
+    return QASR_OK;
+}
+
+// n_steps greedy steps of every stream; the first consumes first_tokens[b];
+// tokens_out [B][n_steps]
+extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_tokens, int32_t n_steps,
+                                       int32_t *tokens_out) {
+    if (!b || !first_tokens || !tokens_out || n_steps <= 0) return qasr_fail(QASR_ERR_INVALID, "batch_generate: bad arguments");
+    qasr_decoder *d = b->d;
+    CHECK_H(d->h);
+    if (n_steps > b->max_steps) return qasr_fail(QASR_ERR_INVALID, "batch_generate: more steps than max_steps");
+    const int64_t longest = *std::max_element(b->len.begin(), b->len.end());
+    if (longest + n_steps > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch_generate: KV capacity exceeded");
+    TRY(batch_set_state(b, first_tokens));
+    hipStream_t st = d->h->stream;
+    for (int32_t s = 0; s < n_steps; s++) {
+        // the longest stream's bucket sets the split count (the largest of the streams')
+        const int S = batch_splits(b, batch_cap(b, longest + s));
+        if (!b->use_graph) {
+            TRY(batch_enqueue_step(b, S));
+            continue;
+        }
+        auto it = b->graphs.find(S);
+        if (it == b->graphs.end()) {
+            hipGraph_t g = nullptr;
+            hipGraphExec_t ge = nullptr;
+            HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+            int rc = batch_enqueue_step(b, S);
+            hipError_t e = hipStreamEndCapture(st, &g);
+            if (rc != QASR_OK) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            HIPCHK(e);
+            e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            HIPCHK(e);
+            it = b->graphs.emplace(S, ge).first;
+        }
+        HIPCHK(hipGraphLaunch(it->second, st));
+    }
+    // the whole [streams][max_steps] log in one contiguous copy, then the rows
+    std::vector<int32_t> log((size_t)b->B * b->max_steps);
+    HIPCHK(hipMemcpyAsync(log.data(), b->token_log, sizeof(int32_t) * log.size(), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipStreamSynchronize(st));
+    for (int i = 0; i < b->B; i++)
+        memcpy(tokens_out + (size_t)i * n_steps, log.data() + (size_t)i * b->max_steps, sizeof(int32_t) * n_steps);
+    for (auto &l : b->len) l += n_steps;
+    return QASR_OK;
+}

@@ -29,6 +29,7 @@ struct qasr_decoder {
     int8_t *lm = nullptr;
     float *lm_s = nullptr, *norm = nullptr;
     void *kc = nullptr, *vc = nullptr;          // [layer][kv_head][max_seq][hd]
+    int64_t kv_layer_stride = 0;                // prefill's cache elements between layers (0: kv_heads * max_seq * hd)
     float *rc = nullptr, *rs = nullptr;         // RoPE [max_seq][hd]
     float *rope_cur = nullptr;                  // [2][hd]: cos, sin rows of the step's position
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr;

@@ -121,7 +121,11 @@ __device__ __forceinline__ void norm_rope16(float x[16], const float w[16], cons
     }
 }
 
-template <typename KVT, int NW, bool MERGE, bool DEC>
+// DEC: 0 operator mode (position argument, even split of the context);
+// 1 decode step (device state, static partition, loads before the position
+// arrives); 2 multi-stream decode step (per-stream partition and position read
+// first, so that no row past a stream's context is fetched)
+template <typename KVT, int NW, bool MERGE, int DEC>
 __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     constexpr int D = 128, G = 2;
     using Sl = KvSlice<KVT>;
@@ -135,12 +139,18 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     const int n_split = a.n_split;
     const int kvh = blockIdx.x / n_split, split = blockIdx.x % n_split;
     const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
-    constexpr bool prep = DEC;                           // raw projections: norm + rope + cache write
-    KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
-    KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
+    constexpr bool prep = DEC != 0;                      // raw projections: norm + rope + cache write
+    // stream of a multi-stream step (0 otherwise): its cache, q/k/v row,
+    // position, RoPE rows and partials
+    const int bs = blockIdx.y;
+    KVT *kc = reinterpret_cast<KVT *>(a.kcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
+    KVT *vc = reinterpret_cast<KVT *>(a.vcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
+    const float *qkv = a.qkv + bs * a.batch_qkv_stride;
+    float *partb = a.part + bs * a.batch_part_stride;
 
     // ---- loads, all issued before the first wait.  Decode-step mode (DEC):
-    // the block owns groups [split gpb, (split + 1) gpb) whatever the
+    // the block owns groups [split gpb, (split + 1) gpb) (gpb per stream in a
+    // multi-stream step) whatever the
     // position, so the first two groups of each wave are requested before the
     // position (device state) arrives; rows past the cache read row 0 and
     // everything past the context is masked later (the new K/V row's slot is
@@ -152,10 +162,15 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     float q[G][16];
     float cs[16], sn[16], qn[16], kn[16], vn[16], knw[16];
     int pos, g0, g1s;
-    if constexpr (DEC) {
-        const int max_rows = (int)(a.head_stride / D);
-        g0 = split * a.gpb;
-        g1s = g0 + a.gpb;
+    if constexpr (DEC != 0) {
+        int max_rows = (int)(a.head_stride / D), gpb = a.gpb;
+        if constexpr (DEC == 2) {
+            pos = a.state[4 * bs + 1];
+            gpb = a.gpb_dev[bs];
+            max_rows = min(max_rows, pos + 1);
+        }
+        g0 = split * gpb;
+        g1s = g0 + gpb;
         const int ja = 8 * (g0 + wid) + pj, jb = ja + 8 * NW;
         const int ra = ja < max_rows ? ja : 0, rb = jb < max_rows ? jb : 0;
         ka.load(kc + (int64_t)ra * D, ds);
@@ -163,14 +178,14 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
         kb.load(kc + (int64_t)rb * D, ds);
         vb.load(vc + (int64_t)rb * D, ds);
 #pragma unroll
-        for (int g = 0; g < G; g++) ld16<KVT>(a.qkv + (kvh * G + g) * D, ds, q[g]);
+        for (int g = 0; g < G; g++) ld16<KVT>(qkv + (kvh * G + g) * D, ds, q[g]);
         ld16<KVT>(a.q_norm, ds, qn);
         ld16<KVT>(a.k_norm, ds, knw);
-        ld16<KVT>(a.qkv + Hq * D + kvh * D, ds, kn);
-        ld16<KVT>(a.qkv + Hq * D + Hkv * D + kvh * D, ds, vn);
-        ld16<KVT>(a.rope_cur, ds, cs);
-        ld16<KVT>(a.rope_cur + D, ds, sn);
-        pos = a.state[1];
+        ld16<KVT>(qkv + Hq * D + kvh * D, ds, kn);
+        ld16<KVT>(qkv + Hq * D + Hkv * D + kvh * D, ds, vn);
+        ld16<KVT>(a.rope_cur + 256 * bs, ds, cs);
+        ld16<KVT>(a.rope_cur + 256 * bs + D, ds, sn);
+        if constexpr (DEC == 1) pos = a.state[4 * bs + 1];
     } else {
         pos = a.pos;
         const int n_grp = (pos + 8) >> 3;
@@ -185,7 +200,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
         kb.load(kc + (int64_t)rb * D, ds);
         vb.load(vc + (int64_t)rb * D, ds);
 #pragma unroll
-        for (int g = 0; g < G; g++) ld16<KVT>(a.qkv + (kvh * G + g) * D, ds, q[g]);
+        for (int g = 0; g < G; g++) ld16<KVT>(qkv + (kvh * G + g) * D, ds, q[g]);
     }
     const int L = pos + 1;
     const int n_grp = (L + 7) >> 3;
@@ -304,10 +319,10 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
         // [(2 h + {0,1}) S + split], o at [2 Hq S + (D h + d) S + split].
         if (t < G * D) {
             const int h = kvh * G + gq;
-            a.part[(int64_t)(2 * Hq + h * D + d) * n_split + split] = o_part;
+            partb[(int64_t)(2 * Hq + h * D + d) * n_split + split] = o_part;
             if (d == 0) {
-                a.part[(2 * h) * n_split + split] = m_part;
-                a.part[(2 * h + 1) * n_split + split] = l_part;
+                partb[(2 * h) * n_split + split] = m_part;
+                partb[(2 * h + 1) * n_split + split] = l_part;
             }
         }
         return;
@@ -366,7 +381,10 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
     // decode-step mode: every pointer of the fused prologue, the state and a static partition
     const bool dec = a.q_norm != nullptr;
     if (dec && (!a.k_norm || !a.rope_cur || !a.state || a.gpb <= 0 || a.head_stride < 128)) return hipErrorInvalidValue;
-    const dim3 grid(n_kv_heads * a.n_split);
+    const int nb = a.batch > 1 ? a.batch : 1;
+    if (nb > 1 && (merge || !dec || !a.gpb_dev || nb > 65535)) return hipErrorInvalidValue;   // streams: separate merge
+    if (a.gpb_dev && (merge || !dec)) return hipErrorInvalidValue;
+    const dim3 grid(n_kv_heads * a.n_split, nb);
 #define QASR_ATT(NW, DEC)                                                                           \
     if (merge) {                                                                                     \
         if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, true, DEC>), grid, dim3(NW * 64), 0, st, a); \
@@ -375,11 +393,17 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
         if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, DEC>), grid, dim3(NW * 64), 0, st, a); \
         else hipLaunchKernelGGL((k_attn_decode<float, NW, false, DEC>), grid, dim3(NW * 64), 0, st, a);           \
     }
-    if (dec) {
-        if (a.waves == 4) { QASR_ATT(4, true) } else { QASR_ATT(8, true) }
+#define QASR_ATT_MS(NW)                                                                              \
+    if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, 2>), grid, dim3(NW * 64), 0, st, a); \
+    else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);
+    if (a.gpb_dev) {
+        if (a.waves == 4) { QASR_ATT_MS(4) } else { QASR_ATT_MS(8) }
+    } else if (dec) {
+        if (a.waves == 4) { QASR_ATT(4, 1) } else { QASR_ATT(8, 1) }
     } else {
-        QASR_ATT(4, false)
+        QASR_ATT(4, 0)
     }
+#undef QASR_ATT_MS
 #undef QASR_ATT
     return hipGetLastError();
 }

@@ -713,4 +713,366 @@ hipError_t launch_argmax(const ArgmaxArgs &a, bool norm, int blocks, hipStream_t
 #undef QASR_AM
 }
 
+
+// ===========================================================================
+// Multi-stream decode: B <= 32 independent streams step
+// together.  Every per-row operation is the single-stream one (the same
+// prologue helpers, the same epilogue operation order), and the W8A8 dots run
+// on int8 MFMA (v_mfma_i32_16x16x64_i8) with exact int32 accumulation, so each
+// stream's output is bit-identical to its own M = 1 step.
+// ===========================================================================
+
+// layer-0 input: x[b] = f32(embedding row of stream b's token)
+__global__ __launch_bounds__(256) void k_embed_rows(float *__restrict__ x, const uint16_t *__restrict__ embed,
+                                                    const int *__restrict__ state, int H) {
+    const int b = blockIdx.x;
+    const int tok = state[4 * b];
+    for (int i = threadIdx.x; i < H; i += 256) x[(int64_t)b * H + i] = bf16_to_f32(embed[(int64_t)tok * H + i]);
+}
+
+hipError_t launch_embed_rows(float *x, const uint16_t *embed, const int *state, int B, int H, hipStream_t st) {
+    hipLaunchKernelGGL(k_embed_rows, dim3(B), dim3(256), 0, st, x, embed, state, H);
+    return hipGetLastError();
+}
+
+// per-row activation prologue: optional RMSNorm (AVX order) + absmax int8
+// quantization of x[b][K] -> xq[b][K], xs[b]; one wave per row
+template <int NS, bool NORM>
+__global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, const float *__restrict__ norm_w,
+                                                    float eps, int K, int B, int8_t *__restrict__ xq,
+                                                    float *__restrict__ xs) {
+    __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int b = blockIdx.x * 4 + wid;
+    if (b >= B) return;
+    ActIn<NS, NORM, false> in;
+    act_load<NS, NORM, false>(x + (int64_t)b * K, nullptr, norm_w, K, in);
+    act_convert<NS, NORM, false>(in, K, nullptr);
+    int xd[NS][4];
+    float s;
+    act_finish<NS, NORM, false>(in, eps, K, lds + wid * NS * 1024, xd, &s);
+    const int nslot = K >> 4;
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c;
+        if (sl < nslot)
+            reinterpret_cast<int4 *>(xq + (int64_t)b * K)[sl] = make_int4(xd[c][0], xd[c][1], xd[c][2], xd[c][3]);
+    }
+    if (lane == 0) xs[b] = s;
+}
+
+hipError_t launch_quant_rows(const float *x, const float *norm_w, float eps, int K, int B, int8_t *xq, float *xs,
+                             hipStream_t st) {
+    if (K % 64 != 0 || K > 6144 || B <= 0) return hipErrorInvalidValue;
+    if (norm_w && K > 4096) return hipErrorInvalidValue;
+    const unsigned blocks = (unsigned)((B + 3) / 4);
+    const int ns = (K + 1023) / 1024;
+#define QR(NS)                                                                                                  \
+    if (ns == NS) {                                                                                             \
+        if (norm_w) hipLaunchKernelGGL((k_quant_rows<NS, true>), dim3(blocks), dim3(256), 0, st, x, norm_w, eps, K, B, xq, xs); \
+        else hipLaunchKernelGGL((k_quant_rows<NS, false>), dim3(blocks), dim3(256), 0, st, x, norm_w, eps, K, B, xq, xs);      \
+        return hipGetLastError();                                                                               \
+    }
+    QR(1) QR(2) QR(3) QR(4)
+    if (ns == 6 && !norm_w) {
+        hipLaunchKernelGGL((k_quant_rows<6, false>), dim3(blocks), dim3(256), 0, st, x, norm_w, eps, K, B, xq, xs);
+        return hipGetLastError();
+    }
+#undef QR
+    return hipErrorInvalidValue;
+}
+
+// C[b][n] for 16 weight rows n x 32 stream columns b per wave: two
+// v_mfma_i32_16x16x64_i8 tiles per 64-wide K step.  Lane l supplies 16
+// consecutive K bytes of weight row n0 + l % 16 and of activation rows
+// l % 16 and 16 + l % 16 at K offset 16 (l / 16) (the same lane -> k map on
+// both operands, so the exact int32 sums do not depend on the hardware's k
+// order); it receives C[n0 + 4 (l / 16) + j][l % 16 (+16)], j < 4.
+__device__ __forceinline__ void mfma_rows16(const int8_t *__restrict__ wrow, const int8_t *__restrict__ xa,
+                                            const int8_t *__restrict__ xb, int K, i32x4 &c0, i32x4 &c1) {
+    constexpr int CH = 16;                       // K steps per chunk (1024 bytes of a row)
+    for (int k0 = 0; k0 < K; k0 += 64 * CH) {
+        const int steps = min(CH, (K - k0) / 64);
+        i32x4 wa[CH], xa_[CH], xb_[CH];
+#pragma unroll
+        for (int s = 0; s < CH; s++) {
+            if (s < steps) {
+                wa[s] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wrow + k0 + 64 * s));
+                xa_[s] = *reinterpret_cast<const i32x4 *>(xa + k0 + 64 * s);
+                xb_[s] = *reinterpret_cast<const i32x4 *>(xb + k0 + 64 * s);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < CH; s++) {
+            if (s < steps) {
+                c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[s], xa_[s], c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wa[s], xb_[s], c1, 0, 0, 0);
+            }
+        }
+    }
+}
+
+// Batched W8A8 projection: out = epilogue((sum_k xq[b][k] w[n][k]) * xs[b] * ws[n])
+// with the single-stream epilogues (MV_PLAIN / MV_ADDTO / MV_SWIGLU).  xq has
+// 32 rows; rows >= B hold stale bytes, and since each output column depends
+// only on its own activation row, their columns are computed and dropped.
+//
+// One block per 16-row tile, 16 waves splitting K (ST steps of 64 each, every
+// load issued up front: the weight tile streams in one round trip); the 16
+// int32 partial tiles are summed through LDS (exact, so the order is free) and
+// the block applies the epilogue, threads over (stream, row) so that stores
+// are row-contiguous.
+template <int MODE, int ST>
+__global__ __launch_bounds__(1024) void k_w8a8_batch(BatchMvArgs a) {
+    constexpr int W = 16;
+    __shared__ int red[W][512];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * 16;
+    const int K = a.K, r = lane & 15, kg = lane >> 4;
+    const int kb = wid * ST * 64 + 16 * kg;
+    const int8_t *wr = a.w + (int64_t)(n0 + r) * K + kb;
+    const int8_t *xa = a.xq + (int64_t)r * K + kb, *xb = a.xq + (int64_t)(16 + r) * K + kb;
+    i32x4 wv[ST], av[ST], bv[ST];
+#pragma unroll
+    for (int s = 0; s < ST; s++) {
+        wv[s] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + 64 * s));
+        av[s] = *reinterpret_cast<const i32x4 *>(xa + 64 * s);
+        bv[s] = *reinterpret_cast<const i32x4 *>(xb + 64 * s);
+    }
+    i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < ST; s++) {
+        c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[s], av[s], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[s], bv[s], c1, 0, 0, 0);
+    }
+    // lane holds C[row 4 kg + j][stream r] (c0) and [stream 16 + r] (c1); LDS index stream * 16 + row
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        red[wid][r * 16 + 4 * kg + j] = c0[j];
+        red[wid][(16 + r) * 16 + 4 * kg + j] = c1[j];
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (MODE == MV_SWIGLU) {
+        // 8 outputs per stream: rows (2 p, 2 p + 1) = (gate, up) of output n0 / 2 + p
+        if (t < 256) {
+            const int b = t >> 3, p = t & 7;
+            int g = 0, u = 0;
+#pragma unroll
+            for (int w = 0; w < W; w++) {
+                g += red[w][b * 16 + 2 * p];
+                u += red[w][b * 16 + 2 * p + 1];
+            }
+            if (b < a.B) {
+                const float xs = a.xs[b];
+                const float gf = __fmul_rn(__fmul_rn((float)g, xs), a.ws[n0 + 2 * p]);
+                const float uf = __fmul_rn(__fmul_rn((float)u, xs), a.ws[n0 + 2 * p + 1]);
+                a.y[(int64_t)b * a.ldy + n0 / 2 + p] = __fmul_rn(__fdiv_rn(gf, __fadd_rn(1.0f, expf(-gf))), uf);
+            }
+        }
+    } else if (t < 512) {
+        const int b = t >> 4, rr = t & 15;
+        int acc = 0;
+#pragma unroll
+        for (int w = 0; w < W; w++) acc += red[w][t];
+        if (b < a.B) {
+            float v = __fmul_rn(__fmul_rn((float)acc, a.xs[b]), a.ws[n0 + rr]);
+            float *yp = a.y + (int64_t)b * a.ldy + n0 + rr;
+            if (MODE == MV_ADDTO) v = __fadd_rn(v, *yp);
+            *yp = v;
+        }
+    }
+}
+
+hipError_t launch_w8a8_batch(const BatchMvArgs &a, int mode, hipStream_t st) {
+    // K = 16 waves x ST steps x 64
+    if (a.K % 1024 != 0 || a.N % 16 != 0 || a.B <= 0 || a.B > 32) return hipErrorInvalidValue;
+    const int st_ = a.K / 1024;
+    const unsigned blocks = (unsigned)(a.N / 16);
+#define QB(S)                                                                                              \
+    if (st_ == S) {                                                                                        \
+        switch (mode) {                                                                                    \
+            case MV_PLAIN: hipLaunchKernelGGL((k_w8a8_batch<MV_PLAIN, S>), dim3(blocks), dim3(1024), 0, st, a); break;   \
+            case MV_ADDTO: hipLaunchKernelGGL((k_w8a8_batch<MV_ADDTO, S>), dim3(blocks), dim3(1024), 0, st, a); break;   \
+            case MV_SWIGLU: hipLaunchKernelGGL((k_w8a8_batch<MV_SWIGLU, S>), dim3(blocks), dim3(1024), 0, st, a); break; \
+            default: return hipErrorInvalidValue;                                                          \
+        }                                                                                                  \
+        return hipGetLastError();                                                                          \
+    }
+    QB(1) QB(2) QB(3) QB(4) QB(6)
+#undef QB
+    return hipErrorInvalidValue;
+}
+
+// Batched LM-head argmax: per stream the larger value wins, lower index on
+// ties (argmax_matvec_int8, kernels/mod.rs:1832-1893).  Waves stride over
+// 16-row tiles; each lane keeps the best of its rows for its two stream
+// columns, then the 4 lanes of a column and the block's 4 waves merge; block
+// partials go to part_val / part_idx [blocks][32].
+__global__ __launch_bounds__(256) void k_argmax_batch(BatchMvArgs a) {
+    __shared__ float sv[4][32];
+    __shared__ int si[4][32];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int K = a.K, r = lane & 15, kg = lane >> 4;
+    const int n_tiles = a.N / 16, gw = blockIdx.x * 4 + wid, n_waves = gridDim.x * 4;
+    float bv[2] = {-1e30f, -1e30f};
+    int bi[2] = {-1, -1};
+    for (int tile = gw; tile < n_tiles; tile += n_waves) {
+        const int n0 = tile * 16;
+        i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
+        mfma_rows16(a.w + (int64_t)(n0 + r) * K + 16 * kg, a.xq + (int64_t)r * K + 16 * kg,
+                    a.xq + (int64_t)(16 + r) * K + 16 * kg, K, c0, c1);
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int b = 16 * t + r;
+            const float xs = a.xs[b < a.B ? b : 0];
+            const i32x4 c = t ? c1 : c0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int n = n0 + 4 * kg + j;
+                const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)c[j], xs), a.ws[n]), 0.0f);
+                if (better(v, n, bv[t], bi[t])) { bv[t] = v; bi[t] = n; }
+            }
+        }
+    }
+    // the 4 lanes (kg) of a column hold disjoint rows: merge with xor 16, 32
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+#pragma unroll
+        for (int o = 16; o <= 32; o <<= 1) {
+            const float ov = __shfl_xor(bv[t], o, 64);
+            const int oi = __shfl_xor(bi[t], o, 64);
+            if (better(ov, oi, bv[t], bi[t])) { bv[t] = ov; bi[t] = oi; }
+        }
+        if (kg == 0) { sv[wid][16 * t + r] = bv[t]; si[wid][16 * t + r] = bi[t]; }
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int b = threadIdx.x;
+        float v = sv[0][b];
+        int i = si[0][b];
+        for (int w = 1; w < 4; w++)
+            if (better(sv[w][b], si[w][b], v, i)) { v = sv[w][b]; i = si[w][b]; }
+        a.part_val[blockIdx.x * 32 + b] = v;
+        a.part_idx[blockIdx.x * 32 + b] = i;
+    }
+}
+
+// merge of the block partials per stream and the per-stream step-state update
+// (token, position, token log, the next position's RoPE rows)
+__global__ __launch_bounds__(256) void k_argmax_batch_finish(BatchMvArgs a, int n_parts, int *state, int *token_log,
+                                                             int64_t log_stride, const float *rope_cos,
+                                                             const float *rope_sin, float *rope_cur, int max_pos,
+                                                             const int *gpb_table, int *gpb_dev) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    for (int b = wid; b < a.B; b += 4) {
+        float bv = -1e30f;
+        int bi = -1;
+        for (int p = lane; p < n_parts; p += 64) {
+            const float v = a.part_val[p * 32 + b];
+            const int i = a.part_idx[p * 32 + b];
+            if (better(v, i, bv, bi)) { bv = v; bi = i; }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
+        int *s = state + 4 * b;
+        const int next_pos = s[1] + 1;
+        if (next_pos < max_pos)
+            for (int i = lane; i < 128; i += 64) {
+                rope_cur[b * 256 + i] = rope_cos[(int64_t)next_pos * 128 + i];
+                rope_cur[b * 256 + 128 + i] = rope_sin[(int64_t)next_pos * 128 + i];
+            }
+        if (lane == 0) {
+            const int tok = bi < 0 ? 0 : bi;
+            s[0] = tok;
+            s[1] = next_pos;
+            token_log[b * log_stride + s[2]] = tok;
+            s[2] += 1;
+            if (gpb_table && next_pos < max_pos) gpb_dev[b] = gpb_table[next_pos];
+        }
+    }
+}
+
+hipError_t launch_argmax_batch(const BatchMvArgs &a, int blocks, int *state, int *token_log, int64_t log_stride,
+                               const float *rope_cos, const float *rope_sin, float *rope_cur, int max_pos,
+                               const int *gpb_table, int *gpb_dev, hipStream_t st) {
+    if (a.K % 64 != 0 || a.N % 16 != 0 || a.B <= 0 || a.B > 32 || blocks <= 0) return hipErrorInvalidValue;
+    if (gpb_table && !gpb_dev) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax_batch, dim3(blocks), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_argmax_batch_finish, dim3(1), dim3(256), 0, st, a, blocks, state, token_log, log_stride,
+                       rope_cos, rope_sin, rope_cur, max_pos, gpb_table, gpb_dev);
+    return hipGetLastError();
+}
+
+// attention partial merge per stream (the o_proj prologue's merge as its own
+// pass), split-fastest layout, then the o_proj activation quantization of the
+// merged row (absmax over the 16 heads x 128 dims, act_finish's scale and
+// rounding): xq[b][128 h + d], xs[b]; att (nullable) receives the f32 row
+template <int S>
+__global__ __launch_bounds__(256) void k_attn_merge_rows(const float *__restrict__ part, int64_t part_stride,
+                                                         float *__restrict__ att, int64_t att_stride,
+                                                         int8_t *__restrict__ xq, float *__restrict__ xs) {
+    constexpr int D = 128, HQ = 16, K = HQ * D;
+    __shared__ float fw[HQ][S], lsum[HQ], wmax[4];
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
+    const float *pb = part + (int64_t)b * part_stride;
+    const int g = t >> 7, d = t & 127;
+    float ov[HQ / 2][S];
+#pragma unroll
+    for (int j = 0; j < HQ / 2; j++) ld_split<S>(pb + 2 * HQ * S + ((2 * j + g) * D + d) * S, ov[j]);
+    const int e = t % (HQ * S), eh = e / S, es = e % S;
+    const float pm = pb[(2 * eh) * S + es], pl = pb[(2 * eh + 1) * S + es];
+    {
+        const float M = split_max<S>(pm);
+        const float f = pm == -INFINITY ? 0.0f : expf(__fsub_rn(pm, M));
+        const float lt = split_sum<S>(__fmul_rn(pl, f));
+        if (t < HQ * S) {
+            fw[eh][es] = f;
+            if (es == 0) lsum[eh] = lt;
+        }
+    }
+    __syncthreads();
+    float o[HQ / 2], m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < HQ / 2; j++) {
+        const int h = 2 * j + g;
+        float ot = 0.0f;
+#pragma unroll
+        for (int s = 0; s < S; s++) ot = fmaf(ov[j][s], fw[h][s], ot);
+        const float lt = lsum[h];
+        o[j] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
+        m = fmaxf(m, fabsf(o[j]));
+        if (att) att[(int64_t)b * att_stride + h * D + d] = o[j];
+    }
+    m = wave_max_f32(m);
+    if (lane == 0) wmax[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float scale, inv;
+    act_scales(m, &scale, &inv);
+    if (t == 0) xs[b] = scale;
+#pragma unroll
+    for (int j = 0; j < HQ / 2; j++)
+        xq[(int64_t)b * K + (2 * j + g) * D + d] = (int8_t)round_clamp_i8(__fmul_rn(o[j], inv));
+}
+
+hipError_t launch_attn_merge_rows(const float *part, int64_t part_stride, int n_split, float *att,
+                                  int64_t att_stride, int8_t *xq, float *xs, int B, hipStream_t st) {
+    if (!xq || !xs || B <= 0) return hipErrorInvalidValue;
+    switch (n_split) {
+#define AM(S) case S: hipLaunchKernelGGL(k_attn_merge_rows<S>, dim3(B), dim3(256), 0, st, part, part_stride, att, att_stride, xq, xs); break;
+        AM(1) AM(2) AM(4) AM(8) AM(16)
+#undef AM
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace qasr

@@ -61,6 +61,30 @@ hipError_t launch_argmax(const ArgmaxArgs &a, bool norm, int blocks, hipStream_t
                          bool finish = true);
 hipError_t launch_copy(void *dst, const void *src, int64_t bytes, hipStream_t st);
 
+// ---- multi-stream decode (config 4) -----------------------------------------
+struct BatchMvArgs {
+    const int8_t *xq;         // [32][K] int8 activations (rows >= B zero)
+    const float *xs;          // [B] activation scales
+    const int8_t *w;          // [N][K] int8 weights
+    const float *ws;          // [N] row scales
+    float *y;                 // [B][ldy] outputs (SwiGLU: N / 2 per row)
+    int64_t ldy;
+    int K, N, B;
+    float *part_val;          // argmax partials [blocks][32]
+    int *part_idx;
+};
+hipError_t launch_embed_rows(float *x, const uint16_t *embed, const int *state, int B, int H, hipStream_t st);
+hipError_t launch_quant_rows(const float *x, const float *norm_w, float eps, int K, int B, int8_t *xq, float *xs,
+                             hipStream_t st);
+hipError_t launch_w8a8_batch(const BatchMvArgs &a, int mode, hipStream_t st);
+// gpb_table[pos] (nullable): the attention partition of a step at pos, copied to gpb_dev[stream]
+hipError_t launch_argmax_batch(const BatchMvArgs &a, int blocks, int *state, int *token_log, int64_t log_stride,
+                               const float *rope_cos, const float *rope_sin, float *rope_cur, int max_pos,
+                               const int *gpb_table, int *gpb_dev, hipStream_t st);
+// split merge per stream + int8 quantization of the merged row (xq [B][2048], xs [B]); att nullable
+hipError_t launch_attn_merge_rows(const float *part, int64_t part_stride, int n_split, float *att,
+                                  int64_t att_stride, int8_t *xq, float *xs, int B, hipStream_t st);
+
 // ---- attention / norms / rope ---------------------------------------------
 struct AttnDecodeArgs {
     const float *qkv;         // raw projections: q [Hq*D] | k [Hkv*D] | v [Hkv*D]
@@ -78,6 +102,11 @@ struct AttnDecodeArgs {
     int waves;                // waves per block: 4 or 8 (0: 8)
     int gpb;                  // > 0: static partition, 8-position groups per block (rows < head_stride / D)
     float eps, scale;
+    // multi-stream decode: blockIdx.y = stream; per-stream strides of the cache
+    // (elements), the qkv rows, the partials and the state / rope_cur rows
+    int batch;                // streams (0 or 1: one)
+    int64_t batch_kv_stride, batch_qkv_stride, batch_part_stride;
+    const int *gpb_dev;       // nullable: per-stream groups per block [batch] (overrides gpb)
 };
 
 // merge: the last block of each KV head merges the split partials into out;

@@ -66,7 +66,7 @@ int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S) {
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     const int I = c.intermediate, nqkv = qd + 2 * kvd;
     const int M = (int)S;
-    const int64_t layer_elems = (int64_t)c.n_kv_heads * d->max_seq * hd;
+    const int64_t layer_elems = d->kv_layer_stride ? d->kv_layer_stride : (int64_t)c.n_kv_heads * d->max_seq * hd;
     const float scale = 1.0f / sqrtf((float)hd);
     HIPCHK(hipMemcpyAsync(p.x, emb_dev, sizeof(float) * S * H, hipMemcpyDeviceToDevice, st));
     const float *rc = d->rc + start * hd, *rs = d->rs + start * hd;

@@ -239,3 +239,52 @@ class Stream:
             self.close()
         except Exception:
             pass
+
+
+class Batch:
+    """Multi-stream greedy decode: up to 32 streams with
+    their own KV caches and lengths step together on one decoder's weights.
+    A stream's tokens equal those of the single-stream decoder at the same
+    attention split count."""
+
+    _close_first = 2
+
+    def __init__(self, decoder, n_streams, max_seq, max_steps=256):
+        b = P()
+        check(lib().qasr_hip_batch_create(decoder.d, int(n_streams), int(max_seq), int(max_steps), C.byref(b)))
+        self.b = b
+        self.n_streams = int(n_streams)
+        self.decoder = decoder
+        decoder.dev.adopt(self)
+
+    def prefill(self, stream, embeds):
+        e = np.ascontiguousarray(embeds, np.float32)
+        check(lib().qasr_hip_batch_prefill(self.b, int(stream), e.ctypes.data_as(P), e.shape[0]))
+
+    def set_len(self, stream, n):
+        check(lib().qasr_hip_batch_set_len(self.b, int(stream), int(n)))
+
+    def length(self, stream):
+        return int(lib().qasr_hip_batch_len(self.b, int(stream)))
+
+    def set_options(self, attn_splits=-1, use_graph=True):
+        check(lib().qasr_hip_batch_set_options(self.b, int(attn_splits), 1 if use_graph else 0))
+
+    def generate(self, first_tokens, n_steps):
+        ft = np.ascontiguousarray(first_tokens, np.int32)
+        if ft.size != self.n_streams:
+            raise ValueError("one first token per stream")
+        out = np.empty((self.n_streams, int(n_steps)), np.int32)
+        check(lib().qasr_hip_batch_generate(self.b, ft.ctypes.data_as(P), int(n_steps), out.ctypes.data_as(P)))
+        return out
+
+    def close(self):
+        if self.b:
+            lib().qasr_hip_batch_free(self.b)
+            self.b = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

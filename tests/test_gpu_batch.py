@@ -1,0 +1,108 @@
+"""GPU parity of multi-stream decode: B streams with
+ragged KV lengths step together on one decoder's int8 weights (M = B int8
+MFMA projections, per-stream attention).  Every stream's tokens must equal
+those of the single-stream decoder (itself pinned to the oracle by
+test_gpu_decode.py) run alone from the same prefix with the same split
+option and capacity: the int8 dots are exact, every per-row float operation
+is the single-stream one, and each stream keeps the single-stream attention
+partition of its own context bucket, so the comparison is bit-exact.
+"""
+import numpy as np
+import pytest
+
+from conftest import rng
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=3, hidden=1024, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=3072,
+             vocab=151936, eps=1e-6, theta=1e6)
+
+
+@pytest.fixture(scope="module")
+def small_decoder(dev):
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    w = SynthDecoder(SMALL, seed=1004)
+    gpu = Decoder(dev, w, max_seq=2048)
+    yield w, gpu
+    gpu.close()
+
+
+def solo_tokens(dec, prefix, first, n, splits):
+    dec.set_options(attn_splits=splits)
+    dec.kv_len = 0
+    dec.prefill(prefix)
+    return dec.generate(n, first_token=int(first))
+
+
+def run_case(dec, n_streams, lens, n_steps, splits, max_seq, seed, use_graph=True):
+    from qwenasr_amd.model import Batch
+    r = rng(seed)
+    H = SMALL["hidden"]
+    prefixes = [r.normal(0, 1, (L, H)).astype(np.float32) for L in lens]
+    first = r.integers(0, SMALL["vocab"], n_streams)
+    b = Batch(dec, n_streams, max_seq, max_steps=n_steps)
+    try:
+        b.set_options(attn_splits=splits, use_graph=use_graph)
+        for i, p in enumerate(prefixes):
+            b.prefill(i, p)
+            assert b.length(i) == lens[i]
+        got = b.generate(first, n_steps)
+        for i in range(n_streams):
+            assert b.length(i) == lens[i] + n_steps
+    finally:
+        b.close()
+    for i in range(n_streams):
+        want = solo_tokens(dec, prefixes[i], first[i], n_steps, splits)
+        assert (got[i] == want).all(), (i, lens[i], got[i].tolist(), want.tolist())
+    dec.set_options(attn_splits=-1)
+    return got
+
+
+@pytest.mark.parametrize("n_streams", [1, 5, 16, 32])
+def test_batch_matches_solo_auto(small_decoder, n_streams):
+    """automatic splits (8 up to a 1024 bucket, 16 up to 2048): streams in
+    different buckets each keep their own partition inside the launch"""
+    _, dec = small_decoder
+    print(f"batch vs solo, {n_streams} streams, automatic splits", flush=True)
+    lens = list(rng(40 + n_streams).integers(1, 1900, n_streams))
+    got = run_case(dec, n_streams, lens, 12, -1, 2048, 400 + n_streams)
+    assert len(np.unique(got)) > max(3, n_streams // 2)     # not a degenerate constant output
+
+
+@pytest.mark.parametrize("splits", [1, 8, 16])
+def test_batch_matches_solo_forced_splits(small_decoder, splits):
+    _, dec = small_decoder
+    print(f"batch vs solo, 7 streams, {splits} splits", flush=True)
+    lens = [3, 250, 300, 700, 1100, 1490, 1700]
+    run_case(dec, 7, lens, 16, splits, 2048, 500 + splits)
+
+
+def test_batch_eager_equals_graph(small_decoder):
+    _, dec = small_decoder
+    print("batch eager vs graph", flush=True)
+    lens = [5, 90, 300]
+    a = run_case(dec, 3, lens, 8, 1, 512, 77, use_graph=True)
+    b = run_case(dec, 3, lens, 8, 1, 512, 77, use_graph=False)
+    assert (a == b).all()
+
+
+def test_batch_argument_errors(small_decoder):
+    from qwenasr_amd import QasrError
+    from qwenasr_amd.model import Batch
+    _, dec = small_decoder
+    with pytest.raises(QasrError):
+        Batch(dec, 33, 512)
+    with pytest.raises(QasrError):
+        Batch(dec, 4, 4096)            # more than the decoder's max_seq
+    b = Batch(dec, 2, 64, max_steps=8)
+    try:
+        b.prefill(0, np.zeros((60, SMALL["hidden"]), np.float32))
+        with pytest.raises(QasrError):
+            b.prefill(1, np.zeros((65, SMALL["hidden"]), np.float32))
+        with pytest.raises(QasrError):
+            b.generate([1, 2], 5)      # stream 0 would pass 64 positions
+        with pytest.raises(QasrError):
+            b.set_options(attn_splits=3)
+    finally:
+        b.close()
