@@ -288,6 +288,13 @@ int qasr_hip_batch_set_options(qasr_batch *b, int attn_splits, int use_graph);
 /* n_steps greedy steps of every stream; first_tokens [streams] (each stream's
  * first input token); tokens_out [streams][n_steps] */
 int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_tokens, int32_t n_steps, int32_t *tokens_out);
+/* HIP-event timing per kernel kind of a step, us per launch (QASR_BATCH_PROFILE_KINDS
+ * entries: embed, in-norm+quant, qkv, q/k prep, attention, merge+quant, o_proj,
+ * post-norm+quant, gate_up+swiglu, ffn quant, down, final norm+quant, LM head,
+ * argmax finish); launches_per_step (nullable) likewise.  Lengths are restored. */
+#define QASR_BATCH_PROFILE_KINDS 14
+int qasr_hip_batch_profile(qasr_batch *b, const int32_t *first_tokens, int32_t n_steps, float *us_per_launch,
+                           int32_t *launches_per_step);
 
 /* ---- A20: incremental streaming (stream_push_audio, transcribe.rs:902-1304) ----
  * A stream borrows a decoder (its KV cache and step state) and an encoder; one

@@ -142,6 +142,7 @@ _SIGS = {
     "qasr_hip_batch_len": (I64, [P, I32]),
     "qasr_hip_batch_set_options": (C.c_int, [P, C.c_int, C.c_int]),
     "qasr_hip_batch_generate": (C.c_int, [P, P, I32, P]),
+    "qasr_hip_batch_profile": (C.c_int, [P, P, I32, P, P]),
 }
 
 _lib = None

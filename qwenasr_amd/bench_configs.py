@@ -2,7 +2,7 @@
 
     python -m qwenasr_amd.bench_configs config1 [reps]
     python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
-    python -m qwenasr_amd.bench_configs config4 [n_streams] [steps]
+    python -m qwenasr_amd.bench_configs config4 [n_streams] [steps] [attn_splits]
 
 config1: the prefill / audio-encoder int8 x bf16 GEMMs at M = 375 (also 390,
 404), the seven 0.6B projections and the LM head, seeded N(0,0.02) weights
@@ -131,7 +131,7 @@ def config3(n_layers=28, steps=20):
     dev.close()
 
 
-def config4(n_streams=32, steps=32):
+def config4(n_streams=32, steps=32, splits=-1):
     dev = Device(0)
     cfg = dict(DEC_0_6B)
     t0 = time.time()
@@ -143,6 +143,8 @@ def config4(n_streams=32, steps=32):
     max_seq = 2048
     dec = Decoder(dev, w, max_seq=max_seq)
     bat = Batch(dec, n_streams, max_seq, max_steps=steps)
+    bat.set_options(attn_splits=splits)
+    dec.set_options(attn_splits=splits)
     H = cfg["hidden"]
     prefixes = [rng.standard_normal((int(L), H), dtype=np.float32) for L in lens]
     t0 = time.time()
@@ -166,6 +168,31 @@ def config4(n_streams=32, steps=32):
     us_step = ms * 1e3 / steps
     tok_s = n_streams * steps / (ms / 1e3)
     log(f"[config4] batched: {us_step:.1f} us/step, {tok_s:.0f} tokens/s ({n_streams} streams)")
+    # per-kernel HIP-event timing of the step at the mid-run lengths
+    for i in range(n_streams):
+        bat.set_len(i, int(lens[i]) + steps // 2)
+    prof = bat.profile(first, 4)
+    for i in range(n_streams):
+        bat.set_len(i, int(lens[i]))
+    c_ = cfg
+    H_, hd_, I_ = c_["hidden"], c_["head_dim"], c_["intermediate"]
+    qd_, kvd_ = c_["n_heads"] * hd_, c_["n_kv_heads"] * hd_
+    B_ = n_streams
+    ctx = float((lens + steps // 2 + 1).sum())
+    # algorithmic bytes per launch: int8 weights + scales once, activations per stream
+    kbytes = {"qkv": (qd_ + 2 * kvd_) * (H_ + 4) + B_ * (H_ + 4 * (qd_ + 2 * kvd_)),
+              "attention": 2 * kvd_ * 4 * ctx + B_ * 4 * (qd_ + 2 * kvd_),
+              "o_proj+=": H_ * (qd_ + 4) + B_ * (qd_ + 8 * H_),
+              "gate_up+swiglu": 2 * I_ * (H_ + 4) + B_ * (H_ + 4 * I_),
+              "down+=": H_ * (I_ + 4) + B_ * (I_ + 8 * H_),
+              "lm_head_argmax": c_["vocab"] * (H_ + 4) + B_ * H_}
+    for p in prof:
+        p["bytes"] = kbytes.get(p["kernel"], 0)
+        p["gbs"] = round(p["bytes"] / (p["us"] * 1e3), 1) if p["us"] > 0 and p["bytes"] else None
+        p["us_per_step"] = round(p["us"] * p["per_step"], 2)
+        p["us"] = round(p["us"], 3)
+        log(f"[config4] {p['kernel']:18s} {p['us']:8.2f} us x{p['per_step']:2d} = {p['us_per_step']:8.1f} us/step"
+            + (f"  {p['gbs']} GB/s" if p["gbs"] else ""))
     # the same streams one at a time on the single-stream decoder
     solo_ms, match = 0.0, 0
     for i in range(n_streams):
@@ -192,13 +219,15 @@ def config4(n_streams=32, steps=32):
     gbs = (w_bytes + kv_bytes) / (us_step * 1e3)
     print(json.dumps({"config": f"config 4: Qwen3-ASR-0.6B decoder, {n_streams} streams, prefixes U[100,1500], "
                                 f"{steps} greedy steps per stream, f32 KV",
+                      "attn_splits": "automatic" if splits < 0 else splits,
                       "prefix_lens": [int(x) for x in lens],
                       "batched_us_per_step": round(us_step, 2), "batched_tokens_per_s": round(tok_s, 1),
                       "solo_us_per_token": round(solo_ms * 1e3 / (n_streams * steps), 2),
                       "solo_tokens_per_s": round(solo_tok_s, 1), "speedup": round(tok_s / solo_tok_s, 2),
                       "identical_streams": f"{match}/{n_streams}",
                       "step_bytes": {"weights": w_bytes, "kv": kv_bytes},
-                      "step_gbs": round(gbs, 1), "step_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4)}))
+                      "step_gbs": round(gbs, 1), "step_frac_of_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                      "kernels": prof}))
     bat.close()
     dec.close()
     dev.close()
@@ -211,6 +240,7 @@ if __name__ == "__main__":
     elif what == "config3":
         config3(int(sys.argv[2]) if len(sys.argv) > 2 else 28, int(sys.argv[3]) if len(sys.argv) > 3 else 20)
     elif what == "config4":
-        config4(int(sys.argv[2]) if len(sys.argv) > 2 else 32, int(sys.argv[3]) if len(sys.argv) > 3 else 32)
+        config4(int(sys.argv[2]) if len(sys.argv) > 2 else 32, int(sys.argv[3]) if len(sys.argv) > 3 else 32,
+                int(sys.argv[4]) if len(sys.argv) > 4 else -1)
     else:
         raise SystemExit(f"unknown configuration {what!r}")

@@ -16,6 +16,7 @@
 #include "decoder.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -31,7 +32,7 @@ using namespace qasr;
 
 namespace {
 constexpr int MAX_STREAMS = 32;
-constexpr int ARGMAX_BLOCKS = 512;
+constexpr int ARGMAX_BLOCKS = 608;      // 16 waves each: one 16-row tile per wave and pass (9496 tiles at 0.6B)
 }
 
 struct qasr_batch {
@@ -49,6 +50,9 @@ struct qasr_batch {
     std::vector<int64_t> len;          // host copy of each stream's KV length
     int64_t steps_done = 0;            // steps since the last set of first tokens
     int n_split = 0, use_graph = 1;
+    // groups in flight per attention wave (QASR_BATCH_ATTN_DEPTH=1|2): one
+    // keeps the kernel at 4 waves per SIMD, which measured faster at 32 streams
+    int attn_depth = 1;
     std::map<int, hipGraphExec_t> graphs;                // by split count
     std::vector<void *> allocs;
 };
@@ -123,6 +127,8 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     b->max_steps = max_steps;
     b->len.assign(n_streams, 0);
     b->use_graph = d->use_graph;         // the decoder's setting (QASR_DISABLE_GRAPH=1 turns both off)
+    const char *ad = getenv("QASR_BATCH_ATTN_DEPTH");
+    if (ad && (ad[0] == '1' || ad[0] == '2') && ad[1] == 0) b->attn_depth = ad[0] - '0';
     const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd, kvd = (int64_t)c.n_kv_heads * hd;
     const int64_t I = c.intermediate, nqkv = qd + 2 * kvd;
     const int64_t kmax = std::max({H, qd, I});
@@ -220,15 +226,25 @@ extern "C" int qasr_hip_batch_set_options(qasr_batch *b, int attn_splits, int us
     return batch_partition(b);
 }
 
-// one batched step with n_split attention splits
-static int batch_enqueue_step(qasr_batch *b, int n_split) {
+// kernels of a step (profile kinds); per-layer kinds launch once per layer
+enum {
+    BK_EMBED, BK_IN_QUANT, BK_QKV, BK_PREP, BK_ATTN, BK_MERGE, BK_O, BK_POST_QUANT, BK_GU, BK_FFN_QUANT, BK_DOWN,
+    BK_FINAL_QUANT, BK_LM, BK_LM_FINISH, BK_KINDS
+};
+static_assert(BK_KINDS == QASR_BATCH_PROFILE_KINDS, "profile kinds");
+static bool per_layer_kind(int k) { return k >= BK_IN_QUANT && k <= BK_DOWN; }
+
+// one batched step with n_split attention splits (only kernels of one kind
+// when kind >= 0)
+static int batch_enqueue_step(qasr_batch *b, int n_split, int kind = -1) {
     qasr_decoder *d = b->d;
     const qasr_dec_config &c = d->c;
     hipStream_t st = d->h->stream;
     const int B = b->B, H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     const int I = c.intermediate, nqkv = qd + 2 * kvd;
     const int64_t le = stream_layer_elems(b);
-    LAUNCHCHK(launch_embed_rows(b->x, d->embed, b->state, B, H, st), "batch embed");
+    auto on = [&](int k) { return kind < 0 || kind == k; };
+    if (on(BK_EMBED)) LAUNCHCHK(launch_embed_rows(b->x, d->embed, b->state, B, H, st), "batch embed");
     auto mv = [&](const int8_t *w, const float *ws, float *y, int64_t ldy, int K, int N, int mode) -> int {
         BatchMvArgs a{};
         a.xq = b->xq; a.xs = b->xs; a.w = w; a.ws = ws; a.y = y; a.ldy = ldy; a.K = K; a.N = N; a.B = B;
@@ -237,8 +253,8 @@ static int batch_enqueue_step(qasr_batch *b, int n_split) {
     };
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
-        LAUNCHCHK(launch_quant_rows(b->x, L.in_norm, c.eps, H, B, b->xq, b->xs, st), "batch norm+quant");
-        TRY(mv(L.wqkv, L.sqkv, b->qkv, nqkv, H, nqkv, MV_PLAIN));
+        if (on(BK_IN_QUANT)) LAUNCHCHK(launch_quant_rows(b->x, L.in_norm, c.eps, H, B, b->xq, b->xs, st), "batch norm+quant");
+        if (on(BK_QKV)) TRY(mv(L.wqkv, L.sqkv, b->qkv, nqkv, H, nqkv, MV_PLAIN));
         AttnDecodeArgs t{};
         t.qkv = b->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
         t.rope_cos = d->rc; t.rope_sin = d->rs; t.rope_cur = b->rope_cur; t.state = b->state;
@@ -249,23 +265,31 @@ static int batch_enqueue_step(qasr_batch *b, int n_split) {
         t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = 1.0f / sqrtf((float)hd);
         t.gpb = 1;                           // the per-stream gpb_dev rows are used
         t.gpb_dev = b->gpb_dev;
+        t.depth = b->attn_depth;
         t.batch = B; t.batch_kv_stride = le; t.batch_qkv_stride = nqkv; t.batch_part_stride = b->part_stride;
-        LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
-        LAUNCHCHK(launch_attn_merge_rows(b->part, b->part_stride, n_split, nullptr, qd, b->xq, b->xs, B, st),
-                  "batch merge+quant");
-        TRY(mv(L.wo, L.so, b->x, H, qd, H, MV_ADDTO));
-        LAUNCHCHK(launch_quant_rows(b->x, L.post_norm, c.eps, H, B, b->xq, b->xs, st), "batch norm+quant");
-        TRY(mv(L.wgu, L.sgu, b->ffn, I, H, 2 * I, MV_SWIGLU));
-        LAUNCHCHK(launch_quant_rows(b->ffn, nullptr, 0.0f, I, B, b->xq, b->xs, st), "batch quant");
-        TRY(mv(L.wdown, L.sdown, b->x, H, I, H, MV_ADDTO));
+        if (on(BK_PREP)) LAUNCHCHK(launch_qk_prep_rows(t, c.n_heads, c.n_kv_heads, hd, 0, st), "batch q/k prep");
+        if (on(BK_ATTN)) LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
+        if (on(BK_MERGE))
+            LAUNCHCHK(launch_attn_merge_rows(b->part, b->part_stride, n_split, nullptr, qd, b->xq, b->xs, B, st),
+                      "batch merge+quant");
+        if (on(BK_O)) TRY(mv(L.wo, L.so, b->x, H, qd, H, MV_ADDTO));
+        if (on(BK_POST_QUANT))
+            LAUNCHCHK(launch_quant_rows(b->x, L.post_norm, c.eps, H, B, b->xq, b->xs, st), "batch norm+quant");
+        if (on(BK_GU)) TRY(mv(L.wgu, L.sgu, b->ffn, I, H, 2 * I, MV_SWIGLU));
+        if (on(BK_FFN_QUANT)) LAUNCHCHK(launch_quant_rows(b->ffn, nullptr, 0.0f, I, B, b->xq, b->xs, st), "batch quant");
+        if (on(BK_DOWN)) TRY(mv(L.wdown, L.sdown, b->x, H, I, H, MV_ADDTO));
     }
-    LAUNCHCHK(launch_quant_rows(b->x, d->norm, c.eps, H, B, b->xq, b->xs, st), "batch final norm");
-    BatchMvArgs am{};
-    am.xq = b->xq; am.xs = b->xs; am.w = d->lm; am.ws = d->lm_s; am.K = H; am.N = c.vocab; am.B = B;
-    am.part_val = b->am_val; am.part_idx = b->am_idx;
-    LAUNCHCHK(launch_argmax_batch(am, ARGMAX_BLOCKS, b->state, b->token_log, b->max_steps, d->rc, d->rs,
-                                  b->rope_cur, (int)b->max_seq, b->gpb_table, b->gpb_dev, st),
-              "batch argmax");
+    if (on(BK_FINAL_QUANT))
+        LAUNCHCHK(launch_quant_rows(b->x, d->norm, c.eps, H, B, b->xq, b->xs, st), "batch final norm");
+    if (on(BK_LM) || on(BK_LM_FINISH)) {
+        BatchMvArgs am{};
+        am.xq = b->xq; am.xs = b->xs; am.w = d->lm; am.ws = d->lm_s; am.K = H; am.N = c.vocab; am.B = B;
+        am.part_val = b->am_val; am.part_idx = b->am_idx;
+        LAUNCHCHK(launch_argmax_batch(am, ARGMAX_BLOCKS, b->state, b->token_log, b->max_steps, d->rc, d->rs,
+                                      b->rope_cur, (int)b->max_seq, b->gpb_table, b->gpb_dev, st, on(BK_LM),
+                                      on(BK_LM_FINISH)),
+                  "batch argmax");
+    }
     return QASR_OK;
 }
 
@@ -340,5 +364,63 @@ extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_token
     for (int i = 0; i < b->B; i++)
         memcpy(tokens_out + (size_t)i * n_steps, log.data() + (size_t)i * b->max_steps, sizeof(int32_t) * n_steps);
     for (auto &l : b->len) l += n_steps;
+    return QASR_OK;
+}
+
+// HIP-event timing of each kernel kind of a step (back-to-back launches behind
+// a delay kernel, as the single-stream decoder profile): per-layer kinds over
+// the layers of one step, the others repeated once per layer; n_steps steps
+// from first_tokens at the streams' current lengths, which are restored.
+extern "C" int qasr_hip_batch_profile(qasr_batch *b, const int32_t *first_tokens, int32_t n_steps,
+                                      float *us_per_launch, int32_t *launches_per_step) {
+    if (!b || !first_tokens || !us_per_launch || n_steps <= 0)
+        return qasr_fail(QASR_ERR_INVALID, "batch_profile: bad arguments");
+    qasr_decoder *d = b->d;
+    CHECK_H(d->h);
+    const int64_t longest = *std::max_element(b->len.begin(), b->len.end());
+    if (longest + n_steps > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch_profile: KV capacity exceeded");
+    hipStream_t st = d->h->stream;
+    const int L = d->c.n_layers;
+    const int reps_once = (int)std::min<int64_t>(L, b->max_steps);
+    std::vector<int64_t> len0 = b->len;
+    std::vector<int32_t> tok(first_tokens, first_tokens + b->B), st_h((size_t)b->B * 4);
+    double tot[BK_KINDS] = {};
+    int cnt[BK_KINDS] = {};
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    HIPCHK(hipEventCreate(&e0));
+    HIPCHK(hipEventCreate(&e1));
+    int rc = QASR_OK;
+    for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
+        const int S = batch_splits(b, batch_cap(b, longest + s));
+        if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
+        if ((rc = batch_enqueue_step(b, S)) != QASR_OK) break;
+        HIPCHK(hipMemcpyAsync(st_h.data(), b->state, sizeof(int32_t) * st_h.size(), hipMemcpyDeviceToHost, st));
+        HIPCHK(hipStreamSynchronize(st));
+        for (int k = 0; k < BK_KINDS && rc == QASR_OK; k++) {
+            if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
+            LAUNCHCHK(launch_delay(400, st), "profile delay");
+            HIPCHK(hipEventRecord(e0, st));
+            const int reps = per_layer_kind(k) ? 1 : reps_once;
+            for (int r = 0; r < reps && rc == QASR_OK; r++) rc = batch_enqueue_step(b, S, k);
+            HIPCHK(hipEventRecord(e1, st));
+            HIPCHK(hipEventSynchronize(e1));
+            float ms = 0.0f;
+            HIPCHK(hipEventElapsedTime(&ms, e0, e1));
+            tot[k] += ms * 1000.0;
+            cnt[k] += per_layer_kind(k) ? L : reps_once;
+        }
+        for (int i = 0; i < b->B; i++) {
+            tok[i] = st_h[4 * i];
+            b->len[i] += 1;
+        }
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    b->len = len0;
+    if (rc != QASR_OK) return rc;
+    for (int k = 0; k < BK_KINDS; k++) {
+        us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
+        if (launches_per_step) launches_per_step[k] = per_layer_kind(k) ? L : 1;
+    }
     return QASR_OK;
 }

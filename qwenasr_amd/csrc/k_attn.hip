@@ -121,10 +121,89 @@ __device__ __forceinline__ void norm_rope16(float x[16], const float w[16], cons
     }
 }
 
+// Online-softmax state of one wave for G query heads over the positions its
+// lanes have seen: running max m, sum l, and o (16 dims per lane).
+template <int G>
+struct AttnAcc {
+    float m[G], l[G], acc[G][16];
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            m[g] = -INFINITY;
+            l[g] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc[g][k] = 0.0f;
+        }
+    }
+    // one group of 8 positions (this lane's position valid or not): scores,
+    // the group max and sum over the 8 position lanes, rescale, accumulate
+    __device__ __forceinline__ void consume(const float (&q)[G][16], const float (&kf)[16], const float (&vf)[16],
+                                            bool valid, float scale) {
+#pragma unroll
+        for (int g = 0; g < G; g++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; k++) s = fmaf(q[g][k], kf[k], s);
+            s = sum8(s);
+            s = valid ? __fmul_rn(s, scale) : -INFINITY;
+            const float mn = fmaxf(m[g], max_x8(s));           // finite: a group has a valid position
+            const float corr = m[g] == -INFINITY ? 0.0f : expf(__fsub_rn(m[g], mn));
+            const float p = valid ? expf(__fsub_rn(s, mn)) : 0.0f;
+            l[g] = fmaf(l[g], corr, sum_x8(p));
+#pragma unroll
+            for (int k = 0; k < 16; k++) acc[g][k] = fmaf(p, vf[k], __fmul_rn(acc[g][k], corr));
+            m[g] = mn;
+        }
+    }
+};
+
+// Block partial of NW waves: the lanes of each wave summed, the waves' states
+// merged through LDS (one barrier).  Threads t < G * 128 receive (m, l, o[d])
+// of query head t / 128, dim t % 128.
+template <typename KVT, int NW, int G>
+__device__ __forceinline__ void attn_block_partial(AttnAcc<G> &st, float (*wm)[G], float (*wl)[G],
+                                                   float (*wacc)[G][128], float &o_part, float &m_part,
+                                                   float &l_part) {
+    constexpr int D = 128;
+    const int t = threadIdx.x, lane = t & 63, wid = t >> 6, pj = lane >> 3, ds = lane & 7;
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int k = 0; k < 16; k++) st.acc[g][k] = sum_x8(st.acc[g][k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) { wm[wid][g] = st.m[g]; wl[wid][g] = st.l[g]; }
+    }
+    if (pj == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++)
+#pragma unroll
+            for (int k = 0; k < 16; k++) wacc[wid][g][KvSlice<KVT>::dim(k, ds)] = st.acc[g][k];
+    }
+    __syncthreads();
+    const int gq = (t >> 7) & 1, d = t & 127;
+    o_part = 0.0f;
+    m_part = -INFINITY;
+    l_part = 0.0f;
+    if (t < G * D) {
+#pragma unroll
+        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w][gq]);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = wm[w][gq] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w][gq], m_part));
+            o_part = fmaf(wacc[w][gq][d], f, o_part);
+            l_part = fmaf(wl[w][gq], f, l_part);
+        }
+    }
+}
+
 // DEC: 0 operator mode (position argument, even split of the context);
 // 1 decode step (device state, static partition, loads before the position
-// arrives); 2 multi-stream decode step (per-stream partition and position read
-// first, so that no row past a stream's context is fetched)
+// arrives); 2 multi-stream decode step: k_qk_prep_rows has already normed and
+// rotated q and written the new K/V row; the per-stream partition and
+// position are read first, so that no row past a stream's context is fetched;
+// 3 as 2 with one group in flight per wave (fewer registers, more resident
+// blocks; the groups are consumed in the same order)
 template <typename KVT, int NW, bool MERGE, int DEC>
 __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     constexpr int D = 128, G = 2;
@@ -139,7 +218,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     const int n_split = a.n_split;
     const int kvh = blockIdx.x / n_split, split = blockIdx.x % n_split;
     const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
-    constexpr bool prep = DEC != 0;                      // raw projections: norm + rope + cache write
+    constexpr bool prep = DEC == 1;                      // raw projections: norm + rope + cache write
     // stream of a multi-stream step (0 otherwise): its cache, q/k/v row,
     // position, RoPE rows and partials
     const int bs = blockIdx.y;
@@ -162,13 +241,25 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     float q[G][16];
     float cs[16], sn[16], qn[16], kn[16], vn[16], knw[16];
     int pos, g0, g1s;
-    if constexpr (DEC != 0) {
-        int max_rows = (int)(a.head_stride / D), gpb = a.gpb;
+    if constexpr (DEC >= 2) {
+        // q first: the first group's scores wait for q and that group only
+#pragma unroll
+        for (int g = 0; g < G; g++) ld16<KVT>(qkv + (kvh * G + g) * D, ds, q[g]);
+        pos = a.state[4 * bs + 1];
+        const int gpb = a.gpb_dev[bs];
+        g0 = split * gpb;
+        g1s = g0 + gpb;
+        const int max_rows = min((int)(a.head_stride / D), pos + 1);
+        const int ja = 8 * (g0 + wid) + pj, jb = ja + 8 * NW;
+        const int ra = ja < max_rows ? ja : 0, rb = jb < max_rows ? jb : 0;
+        ka.load(kc + (int64_t)ra * D, ds);
+        va.load(vc + (int64_t)ra * D, ds);
         if constexpr (DEC == 2) {
-            pos = a.state[4 * bs + 1];
-            gpb = a.gpb_dev[bs];
-            max_rows = min(max_rows, pos + 1);
+            kb.load(kc + (int64_t)rb * D, ds);
+            vb.load(vc + (int64_t)rb * D, ds);
         }
+    } else if constexpr (DEC == 1) {
+        const int max_rows = (int)(a.head_stride / D), gpb = a.gpb;
         g0 = split * gpb;
         g1s = g0 + gpb;
         const int ja = 8 * (g0 + wid) + pj, jb = ja + 8 * NW;
@@ -185,8 +276,10 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
         ld16<KVT>(qkv + Hq * D + Hkv * D + kvh * D, ds, vn);
         ld16<KVT>(a.rope_cur + 256 * bs, ds, cs);
         ld16<KVT>(a.rope_cur + 256 * bs + D, ds, sn);
-        if constexpr (DEC == 1) pos = a.state[4 * bs + 1];
+        pos = a.state[4 * bs + 1];
     } else {
+#pragma unroll
+        for (int g = 0; g < G; g++) ld16<KVT>(qkv + (kvh * G + g) * D, ds, q[g]);
         pos = a.pos;
         const int n_grp = (pos + 8) >> 3;
         const int gpb = (n_grp + n_split - 1) / n_split;
@@ -199,8 +292,6 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
         va.load(vc + (int64_t)ra * D, ds);
         kb.load(kc + (int64_t)rb * D, ds);
         vb.load(vc + (int64_t)rb * D, ds);
-#pragma unroll
-        for (int g = 0; g < G; g++) ld16<KVT>(qkv + (kvh * G + g) * D, ds, q[g]);
     }
     const int L = pos + 1;
     const int n_grp = (L + 7) >> 3;
@@ -235,84 +326,48 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     }
 
     // ---- stream this wave's groups (two in flight) -------------------------
-    float m[G], l[G], acc[G][16];
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-        m[g] = -INFINITY;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 16; k++) acc[g][k] = 0.0f;
-    }
+    AttnAcc<G> acc;
+    acc.init();
     const float scale = a.scale;
     auto consume = [&](const Sl &kt, const Sl &vt, int grp) {
         float kf[16], vf[16];
         kt.to_f32(kf);
         vt.to_f32(vf);
         const int j = 8 * grp + pj;
-        const bool valid = j < j1;
         if (j == skip) {
 #pragma unroll
             for (int k = 0; k < 16; k++) { kf[k] = kn[k]; vf[k] = vn[k]; }
         }
-#pragma unroll
-        for (int g = 0; g < G; g++) {
-            float s = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 16; k++) s = fmaf(q[g][k], kf[k], s);
-            s = sum8(s);
-            s = valid ? __fmul_rn(s, scale) : -INFINITY;
-            const float mn = fmaxf(m[g], max_x8(s));           // finite: a group has a valid position
-            const float corr = m[g] == -INFINITY ? 0.0f : expf(__fsub_rn(m[g], mn));
-            const float p = valid ? expf(__fsub_rn(s, mn)) : 0.0f;
-            l[g] = fmaf(l[g], corr, sum_x8(p));
-#pragma unroll
-            for (int k = 0; k < 16; k++) acc[g][k] = fmaf(p, vf[k], __fmul_rn(acc[g][k], corr));
-            m[g] = mn;
-        }
+        acc.consume(q, kf, vf, j < j1, scale);
     };
     auto load = [&](Sl &kt, Sl &vt, int grp) {
         const int j = row_of(grp);
         kt.load(kc + (int64_t)j * D, ds);
         vt.load(vc + (int64_t)j * D, ds);
     };
-    for (int gi = g0 + wid; gi < g1; gi += 2 * NW) {
-        consume(ka, va, gi);
-        if (gi + 2 * NW < g1) load(ka, va, gi + 2 * NW);
-        const int gb = gi + NW;
-        if (gb < g1) {
-            consume(kb, vb, gb);
-            if (gb + 2 * NW < g1) load(kb, vb, gb + 2 * NW);
+    // The refills are unconditional (past the run they read row j0 again): a
+    // load under a branch leaves the buffer's registers with two definitions,
+    // and the copy the compiler then makes at the loop edge waits for every
+    // load in flight, the other buffer's included.
+    if constexpr (DEC == 3) {
+        for (int gi = g0 + wid; gi < g1; gi += NW) {
+            consume(ka, va, gi);
+            load(ka, va, gi + NW);
+        }
+    } else {
+        for (int gi = g0 + wid; gi < g1; gi += 2 * NW) {
+            consume(ka, va, gi);
+            load(ka, va, gi + 2 * NW);
+            const int gb = gi + NW;
+            if (gb < g1) consume(kb, vb, gb);
+            load(kb, vb, gb + 2 * NW);
         }
     }
 
     // ---- merge the lanes of each wave, then the waves of the block ----------
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int k = 0; k < 16; k++) acc[g][k] = sum_x8(acc[g][k]);
-    if (lane == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++) { wm[wid][g] = m[g]; wl[wid][g] = l[g]; }
-    }
-    if (pj == 0) {
-#pragma unroll
-        for (int g = 0; g < G; g++)
-#pragma unroll
-            for (int k = 0; k < 16; k++) wacc[wid][g][Sl::dim(k, ds)] = acc[g][k];
-    }
-    __syncthreads();
     const int gq = (t >> 7) & 1, d = t & 127;    // threads t < 256: (query head, dim)
-    float o_part = 0.0f, m_part = -INFINITY, l_part = 0.0f;
-    if (t < G * D) {
-#pragma unroll
-        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w][gq]);
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float f = wm[w][gq] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w][gq], m_part));
-            o_part = fmaf(wacc[w][gq][d], f, o_part);
-            l_part = fmaf(wl[w][gq], f, l_part);
-        }
-    }
+    float o_part, m_part, l_part;
+    attn_block_partial<KVT, NW, G>(acc, wm, wl, wacc, o_part, m_part, l_part);
     if (!MERGE) {
         // the consumer (the o_proj kernel) merges; the kernel boundary publishes
         // these.  Layout, split index fastest: (m, l) of head h = G kvh + gq at
@@ -373,6 +428,52 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     if (t == 0) reset_counter(a.counters + kvh);
 }
 
+// Multi-stream decode prologue of the attention: per stream b, per-head
+// RMSNorm + RoPE of the 16 query heads (in place in the qkv row) and of the new
+// key, and the new K/V row written at the stream's position.  The lane layout,
+// norm_rope16 and the cache rounding are the decode kernel's own (lanes
+// (head, ds) as (pj, ds)), so the values are bit-identical to that kernel's
+// fused prologue.  Grid: streams; 3 waves = 24 rows (16 q heads, 8 kv heads).
+template <typename KVT>
+__global__ __launch_bounds__(192) void k_qk_prep_rows(AttnDecodeArgs a, int Hkv) {
+    constexpr int D = 128, G = 2;
+    using Sl = KvSlice<KVT>;
+    const int bs = blockIdx.x, t = threadIdx.x;
+    const int row = t >> 3, ds = t & 7, Hq = Hkv * G;
+    float *qkv = const_cast<float *>(a.qkv) + bs * a.batch_qkv_stride;
+    const bool isq = row < Hq;
+    const int kvh = isq ? 0 : row - Hq;
+    float x[16], w[16], cs[16], sn[16], v[16];
+    ld16<KVT>(isq ? qkv + row * D : qkv + Hq * D + kvh * D, ds, x);
+    ld16<KVT>(isq ? a.q_norm : a.k_norm, ds, w);
+    ld16<KVT>(a.rope_cur + 256 * bs, ds, cs);
+    ld16<KVT>(a.rope_cur + 256 * bs + D, ds, sn);
+    ld16<KVT>(qkv + Hq * D + Hkv * D + kvh * D, ds, v);
+    const int pos = a.state[4 * bs + 1];
+    norm_rope16(x, w, cs, sn, a.eps);
+    if (isq) {
+#pragma unroll
+        for (int k = 0; k < 16; k += 4)
+            reinterpret_cast<float4 *>(qkv + row * D + KvSlice<KVT>::dim(k, ds))[0] =
+                make_float4(x[k], x[k + 1], x[k + 2], x[k + 3]);
+    } else {
+        KVT *kc = reinterpret_cast<KVT *>(a.kcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
+        KVT *vc = reinterpret_cast<KVT *>(a.vcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
+        Sl::store(kc + (int64_t)pos * D, ds, x);
+        Sl::store(vc + (int64_t)pos * D, ds, v);
+    }
+}
+
+hipError_t launch_qk_prep_rows(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim, int kv_bf16,
+                               hipStream_t st) {
+    const int nb = a.batch > 1 ? a.batch : 1;
+    if (head_dim != 128 || n_kv_heads != 8 || n_heads != 16 || !a.q_norm || !a.k_norm || !a.rope_cur || !a.state)
+        return hipErrorInvalidValue;
+    if (kv_bf16) hipLaunchKernelGGL(k_qk_prep_rows<uint16_t>, dim3(nb), dim3(192), 0, st, a, n_kv_heads);
+    else hipLaunchKernelGGL(k_qk_prep_rows<float>, dim3(nb), dim3(192), 0, st, a, n_kv_heads);
+    return hipGetLastError();
+}
+
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
                               int kv_bf16, hipStream_t st, bool merge) {
     if (head_dim != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads) return hipErrorInvalidValue;
@@ -383,7 +484,7 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
     if (dec && (!a.k_norm || !a.rope_cur || !a.state || a.gpb <= 0 || a.head_stride < 128)) return hipErrorInvalidValue;
     const int nb = a.batch > 1 ? a.batch : 1;
     if (nb > 1 && (merge || !dec || !a.gpb_dev || nb > 65535)) return hipErrorInvalidValue;   // streams: separate merge
-    if (a.gpb_dev && (merge || !dec)) return hipErrorInvalidValue;
+    if (a.gpb_dev && (merge || !dec || n_kv_heads != 8)) return hipErrorInvalidValue;   // prep block: 24 rows
     const dim3 grid(n_kv_heads * a.n_split, nb);
 #define QASR_ATT(NW, DEC)                                                                           \
     if (merge) {                                                                                     \
@@ -394,8 +495,13 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
         else hipLaunchKernelGGL((k_attn_decode<float, NW, false, DEC>), grid, dim3(NW * 64), 0, st, a);           \
     }
 #define QASR_ATT_MS(NW)                                                                              \
-    if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, 2>), grid, dim3(NW * 64), 0, st, a); \
-    else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);
+    if (a.depth == 1) {                                                                              \
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, 3>), grid, dim3(NW * 64), 0, st, a); \
+        else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 3>), grid, dim3(NW * 64), 0, st, a);  \
+    } else {                                                                                         \
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, 2>), grid, dim3(NW * 64), 0, st, a); \
+        else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);  \
+    }
     if (a.gpb_dev) {
         if (a.waves == 4) { QASR_ATT_MS(4) } else { QASR_ATT_MS(8) }
     } else if (dec) {

@@ -841,6 +841,17 @@ __global__ __launch_bounds__(1024) void k_w8a8_batch(BatchMvArgs a) {
         av[s] = *reinterpret_cast<const i32x4 *>(xa + 64 * s);
         bv[s] = *reinterpret_cast<const i32x4 *>(xb + 64 * s);
     }
+    // epilogue operands of this thread's output(s), requested with the tile
+    // (threads past B read stream 0's and do not store)
+    const int t = threadIdx.x;
+    const int eb = MODE == MV_SWIGLU ? (t >> 3) & 31 : (t >> 4) & 31;
+    const int er = MODE == MV_SWIGLU ? 2 * (t & 7) : t & 15;
+    const int ebs = eb < a.B ? eb : 0;
+    const float e_xs = __builtin_nontemporal_load(a.xs + ebs);
+    const float e_w0 = __builtin_nontemporal_load(a.ws + n0 + er);
+    const float e_w1 = MODE == MV_SWIGLU ? __builtin_nontemporal_load(a.ws + n0 + er + 1) : 0.0f;
+    const float e_y = MODE == MV_ADDTO ? __builtin_nontemporal_load(a.y + (int64_t)ebs * a.ldy + n0 + er) : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
     i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
 #pragma unroll
     for (int s = 0; s < ST; s++) {
@@ -854,7 +865,6 @@ __global__ __launch_bounds__(1024) void k_w8a8_batch(BatchMvArgs a) {
         red[wid][(16 + r) * 16 + 4 * kg + j] = c1[j];
     }
     __syncthreads();
-    const int t = threadIdx.x;
     if (MODE == MV_SWIGLU) {
         // 8 outputs per stream: rows (2 p, 2 p + 1) = (gate, up) of output n0 / 2 + p
         if (t < 256) {
@@ -866,9 +876,8 @@ __global__ __launch_bounds__(1024) void k_w8a8_batch(BatchMvArgs a) {
                 u += red[w][b * 16 + 2 * p + 1];
             }
             if (b < a.B) {
-                const float xs = a.xs[b];
-                const float gf = __fmul_rn(__fmul_rn((float)g, xs), a.ws[n0 + 2 * p]);
-                const float uf = __fmul_rn(__fmul_rn((float)u, xs), a.ws[n0 + 2 * p + 1]);
+                const float gf = __fmul_rn(__fmul_rn((float)g, e_xs), e_w0);
+                const float uf = __fmul_rn(__fmul_rn((float)u, e_xs), e_w1);
                 a.y[(int64_t)b * a.ldy + n0 / 2 + p] = __fmul_rn(__fdiv_rn(gf, __fadd_rn(1.0f, expf(-gf))), uf);
             }
         }
@@ -878,10 +887,9 @@ __global__ __launch_bounds__(1024) void k_w8a8_batch(BatchMvArgs a) {
 #pragma unroll
         for (int w = 0; w < W; w++) acc += red[w][t];
         if (b < a.B) {
-            float v = __fmul_rn(__fmul_rn((float)acc, a.xs[b]), a.ws[n0 + rr]);
-            float *yp = a.y + (int64_t)b * a.ldy + n0 + rr;
-            if (MODE == MV_ADDTO) v = __fadd_rn(v, *yp);
-            *yp = v;
+            float v = __fmul_rn(__fmul_rn((float)acc, e_xs), e_w0);
+            if (MODE == MV_ADDTO) v = __fadd_rn(v, e_y);
+            a.y[(int64_t)b * a.ldy + n0 + rr] = v;
         }
     }
 }
@@ -907,107 +915,131 @@ hipError_t launch_w8a8_batch(const BatchMvArgs &a, int mode, hipStream_t st) {
 }
 
 // Batched LM-head argmax: per stream the larger value wins, lower index on
-// ties (argmax_matvec_int8, kernels/mod.rs:1832-1893).  Waves stride over
-// 16-row tiles; each lane keeps the best of its rows for its two stream
-// columns, then the 4 lanes of a column and the block's 4 waves merge; block
-// partials go to part_val / part_idx [blocks][32].
-__global__ __launch_bounds__(256) void k_argmax_batch(BatchMvArgs a) {
-    __shared__ float sv[4][32];
-    __shared__ int si[4][32];
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int K = a.K, r = lane & 15, kg = lane >> 4;
-    const int n_tiles = a.N / 16, gw = blockIdx.x * 4 + wid, n_waves = gridDim.x * 4;
+// ties (argmax_matvec_int8, kernels/mod.rs:1832-1893).  A block of 16 waves
+// stages the 32 activation rows in LDS once (32 K bytes) and each wave takes
+// one 16-row tile per pass (grid-stride), all weight loads of a tile issued up
+// front; the MFMA's activation operands come from LDS.  Each lane keeps the
+// best of its rows for its two stream columns, then the 4 lanes of a column
+// and the block's waves merge; block partials go to part_val / part_idx
+// [blocks][32].
+template <int KC>
+__global__ __launch_bounds__(1024) void k_argmax_batch(BatchMvArgs a) {
+    extern __shared__ int4 xs_lds[];                 // [32][K / 16]
+    __shared__ float sv[16][32];
+    __shared__ int si[16][32];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int K = a.K, r = lane & 15, kg = lane >> 4, kv = K >> 4;
+    for (int i = t; i < 32 * kv; i += 1024) xs_lds[i] = reinterpret_cast<const int4 *>(a.xq)[i];
+    __syncthreads();
+    const int n_tiles = a.N / 16;
     float bv[2] = {-1e30f, -1e30f};
     int bi[2] = {-1, -1};
-    for (int tile = gw; tile < n_tiles; tile += n_waves) {
+    float xsv[2];
+    xsv[0] = a.xs[r < a.B ? r : 0];
+    xsv[1] = a.xs[16 + r < a.B ? 16 + r : 0];
+    for (int tile = blockIdx.x * 16 + wid; tile < n_tiles; tile += gridDim.x * 16) {
         const int n0 = tile * 16;
+        const int8_t *wr = a.w + (int64_t)(n0 + r) * K + 16 * kg;
         i32x4 c0 = {0, 0, 0, 0}, c1 = {0, 0, 0, 0};
-        mfma_rows16(a.w + (int64_t)(n0 + r) * K + 16 * kg, a.xq + (int64_t)r * K + 16 * kg,
-                    a.xq + (int64_t)(16 + r) * K + 16 * kg, K, c0, c1);
+        for (int k0 = 0; k0 < K; k0 += 64 * KC) {
+            i32x4 wv[KC];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            const int b = 16 * t + r;
-            const float xs = a.xs[b < a.B ? b : 0];
-            const i32x4 c = t ? c1 : c0;
+            for (int s = 0; s < KC; s++) wv[s] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wr + k0 + 64 * s));
+            __builtin_amdgcn_sched_barrier(0);       // every weight load of the tile before the first MFMA
+#pragma unroll
+            for (int s = 0; s < KC; s++) {
+                const int kq = (k0 + 64 * s) / 16 + kg;
+                const int4 xa = xs_lds[r * kv + kq], xb = xs_lds[(16 + r) * kv + kq];
+                const i32x4 av = {xa.x, xa.y, xa.z, xa.w}, bvv = {xb.x, xb.y, xb.z, xb.w};
+                c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[s], av, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wv[s], bvv, c1, 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+            const i32x4 c = tt ? c1 : c0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int n = n0 + 4 * kg + j;
-                const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)c[j], xs), a.ws[n]), 0.0f);
-                if (better(v, n, bv[t], bi[t])) { bv[t] = v; bi[t] = n; }
+                const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)c[j], xsv[tt]), a.ws[n]), 0.0f);
+                if (better(v, n, bv[tt], bi[tt])) { bv[tt] = v; bi[tt] = n; }
             }
         }
     }
     // the 4 lanes (kg) of a column hold disjoint rows: merge with xor 16, 32
 #pragma unroll
-    for (int t = 0; t < 2; t++) {
+    for (int tt = 0; tt < 2; tt++) {
 #pragma unroll
         for (int o = 16; o <= 32; o <<= 1) {
-            const float ov = __shfl_xor(bv[t], o, 64);
-            const int oi = __shfl_xor(bi[t], o, 64);
-            if (better(ov, oi, bv[t], bi[t])) { bv[t] = ov; bi[t] = oi; }
+            const float ov = __shfl_xor(bv[tt], o, 64);
+            const int oi = __shfl_xor(bi[tt], o, 64);
+            if (better(ov, oi, bv[tt], bi[tt])) { bv[tt] = ov; bi[tt] = oi; }
         }
-        if (kg == 0) { sv[wid][16 * t + r] = bv[t]; si[wid][16 * t + r] = bi[t]; }
+        if (kg == 0) { sv[wid][16 * tt + r] = bv[tt]; si[wid][16 * tt + r] = bi[tt]; }
     }
     __syncthreads();
-    if (threadIdx.x < 32) {
-        const int b = threadIdx.x;
-        float v = sv[0][b];
-        int i = si[0][b];
-        for (int w = 1; w < 4; w++)
-            if (better(sv[w][b], si[w][b], v, i)) { v = sv[w][b]; i = si[w][b]; }
-        a.part_val[blockIdx.x * 32 + b] = v;
-        a.part_idx[blockIdx.x * 32 + b] = i;
+    if (t < 32) {
+        float v = sv[0][t];
+        int i = si[0][t];
+        for (int w = 1; w < 16; w++)
+            if (better(sv[w][t], si[w][t], v, i)) { v = sv[w][t]; i = si[w][t]; }
+        a.part_val[blockIdx.x * 32 + t] = v;
+        a.part_idx[blockIdx.x * 32 + t] = i;
     }
 }
 
-// merge of the block partials per stream and the per-stream step-state update
-// (token, position, token log, the next position's RoPE rows)
-__global__ __launch_bounds__(256) void k_argmax_batch_finish(BatchMvArgs a, int n_parts, int *state, int *token_log,
-                                                             int64_t log_stride, const float *rope_cos,
-                                                             const float *rope_sin, float *rope_cur, int max_pos,
-                                                             const int *gpb_table, int *gpb_dev) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    for (int b = wid; b < a.B; b += 4) {
-        float bv = -1e30f;
-        int bi = -1;
-        for (int p = lane; p < n_parts; p += 64) {
-            const float v = a.part_val[p * 32 + b];
-            const int i = a.part_idx[p * 32 + b];
-            if (better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
+// merge of the block partials per stream (one wave per stream) and the
+// per-stream step-state update (token, position, token log, the next
+// position's RoPE rows and attention partition)
+__global__ __launch_bounds__(64) void k_argmax_batch_finish(BatchMvArgs a, int n_parts, int *state, int *token_log,
+                                                            int64_t log_stride, const float *rope_cos,
+                                                            const float *rope_sin, float *rope_cur, int max_pos,
+                                                            const int *gpb_table, int *gpb_dev) {
+    const int lane = threadIdx.x, b = blockIdx.x;
+    float bv = -1e30f;
+    int bi = -1;
+    for (int p = lane; p < n_parts; p += 64) {
+        const float v = a.part_val[p * 32 + b];
+        const int i = a.part_idx[p * 32 + b];
+        if (better(v, i, bv, bi)) { bv = v; bi = i; }
+    }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    int *s = state + 4 * b;
+    const int next_pos = s[1] + 1;
+    if (next_pos < max_pos)
+        for (int i = lane; i < 128; i += 64) {
+            rope_cur[b * 256 + i] = rope_cos[(int64_t)next_pos * 128 + i];
+            rope_cur[b * 256 + 128 + i] = rope_sin[(int64_t)next_pos * 128 + i];
         }
-        int *s = state + 4 * b;
-        const int next_pos = s[1] + 1;
-        if (next_pos < max_pos)
-            for (int i = lane; i < 128; i += 64) {
-                rope_cur[b * 256 + i] = rope_cos[(int64_t)next_pos * 128 + i];
-                rope_cur[b * 256 + 128 + i] = rope_sin[(int64_t)next_pos * 128 + i];
-            }
-        if (lane == 0) {
-            const int tok = bi < 0 ? 0 : bi;
-            s[0] = tok;
-            s[1] = next_pos;
-            token_log[b * log_stride + s[2]] = tok;
-            s[2] += 1;
-            if (gpb_table && next_pos < max_pos) gpb_dev[b] = gpb_table[next_pos];
-        }
+    if (lane == 0) {
+        const int tok = bi < 0 ? 0 : bi;
+        s[0] = tok;
+        s[1] = next_pos;
+        token_log[b * log_stride + s[2]] = tok;
+        s[2] += 1;
+        if (gpb_table && next_pos < max_pos) gpb_dev[b] = gpb_table[next_pos];
     }
 }
 
 hipError_t launch_argmax_batch(const BatchMvArgs &a, int blocks, int *state, int *token_log, int64_t log_stride,
                                const float *rope_cos, const float *rope_sin, float *rope_cur, int max_pos,
-                               const int *gpb_table, int *gpb_dev, hipStream_t st) {
-    if (a.K % 64 != 0 || a.N % 16 != 0 || a.B <= 0 || a.B > 32 || blocks <= 0) return hipErrorInvalidValue;
+                               const int *gpb_table, int *gpb_dev, hipStream_t st, bool stream, bool finish) {
+    if (a.K % 1024 != 0 || a.K > 4096 || a.N % 16 != 0 || a.B <= 0 || a.B > 32 || blocks <= 0)
+        return hipErrorInvalidValue;
     if (gpb_table && !gpb_dev) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_argmax_batch, dim3(blocks), dim3(256), 0, st, a);
-    hipLaunchKernelGGL(k_argmax_batch_finish, dim3(1), dim3(256), 0, st, a, blocks, state, token_log, log_stride,
-                       rope_cos, rope_sin, rope_cur, max_pos, gpb_table, gpb_dev);
+    if (stream) {
+        const size_t lds = (size_t)32 * a.K;
+        hipLaunchKernelGGL(k_argmax_batch<16>, dim3(blocks), dim3(1024), lds, st, a);
+    }
+    if (finish)
+        hipLaunchKernelGGL(k_argmax_batch_finish, dim3(a.B), dim3(64), 0, st, a, blocks, state, token_log, log_stride,
+                           rope_cos, rope_sin, rope_cur, max_pos, gpb_table, gpb_dev);
     return hipGetLastError();
 }
 

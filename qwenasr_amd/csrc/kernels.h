@@ -80,7 +80,8 @@ hipError_t launch_w8a8_batch(const BatchMvArgs &a, int mode, hipStream_t st);
 // gpb_table[pos] (nullable): the attention partition of a step at pos, copied to gpb_dev[stream]
 hipError_t launch_argmax_batch(const BatchMvArgs &a, int blocks, int *state, int *token_log, int64_t log_stride,
                                const float *rope_cos, const float *rope_sin, float *rope_cur, int max_pos,
-                               const int *gpb_table, int *gpb_dev, hipStream_t st);
+                               const int *gpb_table, int *gpb_dev, hipStream_t st, bool stream = true,
+                               bool finish = true);
 // split merge per stream + int8 quantization of the merged row (xq [B][2048], xs [B]); att nullable
 hipError_t launch_attn_merge_rows(const float *part, int64_t part_stride, int n_split, float *att,
                                   int64_t att_stride, int8_t *xq, float *xs, int B, hipStream_t st);
@@ -107,8 +108,13 @@ struct AttnDecodeArgs {
     int batch;                // streams (0 or 1: one)
     int64_t batch_kv_stride, batch_qkv_stride, batch_part_stride;
     const int *gpb_dev;       // nullable: per-stream groups per block [batch] (overrides gpb)
+    int depth;                // multi-stream mode: groups in flight per wave (1 or 2; 0: 2)
 };
 
+// multi-stream step prologue (k_qk_prep_rows): q/k per-head norm + RoPE, the new
+// K/V row of every stream; run before launch_attn_decode with gpb_dev set
+hipError_t launch_qk_prep_rows(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim, int kv_bf16,
+                               hipStream_t st);
 // merge: the last block of each KV head merges the split partials into out;
 // otherwise the partials are left for k_oproj_merge (n_split 1, 2, 4 or 8)
 hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,

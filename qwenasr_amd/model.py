@@ -278,6 +278,19 @@ class Batch:
         check(lib().qasr_hip_batch_generate(self.b, ft.ctypes.data_as(P), int(n_steps), out.ctypes.data_as(P)))
         return out
 
+    BATCH_KINDS = ("embed", "in_norm+quant", "qkv", "qk_prep", "attention", "merge+quant", "o_proj+=",
+                   "post_norm+quant", "gate_up+swiglu", "ffn_quant", "down+=", "final_norm+quant",
+                   "lm_head_argmax", "argmax_finish")
+
+    def profile(self, first_tokens, n_steps):
+        """HIP-event us per launch of each kernel kind of a step (qasr_hip_batch_profile)."""
+        ft = np.ascontiguousarray(first_tokens, np.int32)
+        us = np.zeros(len(self.BATCH_KINDS), np.float32)
+        per = np.zeros(len(self.BATCH_KINDS), np.int32)
+        check(lib().qasr_hip_batch_profile(self.b, ft.ctypes.data_as(P), int(n_steps), us.ctypes.data_as(P),
+                                           per.ctypes.data_as(P)))
+        return [dict(kernel=k, us=float(u), per_step=int(n)) for k, u, n in zip(self.BATCH_KINDS, us, per)]
+
     def close(self):
         if self.b:
             lib().qasr_hip_batch_free(self.b)
