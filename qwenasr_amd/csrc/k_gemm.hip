@@ -14,6 +14,8 @@
 //                 per-row scale is applied in the epilogue
 // k_gemm_f32: plain f32 FMA tiles for the small GEMMs whose operands are both
 // f32 tables (mel DFT and filterbank, audio.rs:339-351).
+#include <cstdlib>
+
 #include "kernels.h"
 
 namespace qasr {
@@ -194,6 +196,195 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
 }
 
 // ---------------------------------------------------------------------------
+// k_gemm_lds: the same tile shape, MFMA and epilogues as k_gemm_mfma, fed by
+// direct global -> LDS loads (global_load_lds_dwordx4) through a ring of NS
+// stages, so NS - 1 K-steps are in flight while one is computed (the
+// register-staged kernel above keeps one, and its K loop is a chain of HBM
+// round trips at these M ~ 400 shapes).  A stage holds the block's A tile
+// (64 rows x BK, f32 or bf16, 8 KiB) and B tile (64 rows x BK, bf16 or int8,
+// 4 KiB); each wave issues 3 of the stage's 12 one-KiB loads.  A load writes
+// lane l's 16 bytes at LDS offset 16 l, so the lane -> (row, 16-byte slot)
+// map is chosen with an XOR swizzle of the slot by the row, which spreads a
+// fragment read's 16 rows over the banks.  f32 A is split into its three
+// bf16 terms when the fragment is read; int8 B is widened to bf16 (exact).
+// K-steps past the end load a zero page, so the wait count is the same in
+// every iteration.  Requires K % BK == 0 and 16-byte aligned rows.
+// ---------------------------------------------------------------------------
+__device__ __attribute__((aligned(256))) int4 g_gemm_zero16[16];
+
+// One global_load_lds_dwordx4: lane l's 16 bytes from g land at LDS byte
+// lds + 16 l.  Written as inline assembly, with the waits below, because the
+// compiler otherwise treats every LDS read as possibly aliasing any load in
+// flight and waits for all of them (vmcnt(0)) before it, which would drain
+// the ring every K-step.  The compiler does not see these loads: the kernel
+// issues no other vector-memory load until its final vmcnt(0).
+__device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
+    const uint32_t la = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// float pair -> bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+template <int ASRC, int BSRC, int EPI, int NS>
+__global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
+    constexpr bool AF = ASRC == A_F32_SPLIT;
+    constexpr int BK = AF ? 32 : 64, ASZ = 8192, BSZ = 4096, STG = ASZ + BSZ;
+    constexpr int NA = AF ? 3 : 1;
+    // wave tiling of the 64 x 64 block: the operand that needs converting is
+    // owned by one wave per fragment (f32 A: waves take 16-row strips; int8 B:
+    // waves take 16-column strips), so no fragment is converted twice
+    constexpr int WR = AF ? 1 : 4, WC = AF ? 4 : 1;
+    static_assert(BSRC == (AF ? B_BF16 : B_I8), "operand pair");
+    __shared__ __attribute__((aligned(16))) char smem[NS][STG];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int mw = AF ? 16 * wid : 0, nw = AF ? 0 : 16 * wid;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int M = g.M, N = g.N, K = g.K, nk = K / BK;
+    // this lane's rows and swizzled slots in the wave's three loads per stage
+    const int ra0 = 8 * (2 * wid) + (lane >> 3), ra1 = ra0 + 8;            // A rows of loads 2w, 2w + 1
+    const int pa0 = (lane & 7) ^ (ra0 & 7), pa1 = (lane & 7) ^ (ra1 & 7);
+    const int rb = 16 * wid + (lane >> 2), pb = (lane & 3) ^ (rb & 3);    // B row of load w
+    const int am0 = min(m0 + ra0, M - 1), am1 = min(m0 + ra1, M - 1), bnr = min(n0 + rb, N - 1);
+    const char *A = reinterpret_cast<const char *>(g.A), *B = reinterpret_cast<const char *>(g.B);
+    constexpr int AE = AF ? 4 : 2, BE = BSRC == B_BF16 ? 2 : 1;     // element bytes
+    const char *a_src0 = A + ((int64_t)am0 * g.lda) * AE + 16 * pa0;   // + k0 * AE per stage
+    const char *a_src1 = A + ((int64_t)am1 * g.lda) * AE + 16 * pa1;
+    const char *b_src = B + ((int64_t)bnr * g.ldb) * BE + 16 * pb;
+    const char *zero = reinterpret_cast<const char *>(g_gemm_zero16);
+    auto issue = [&](int buf, int kt) {
+        char *st = smem[buf];
+        const bool live = kt < nk;
+        const int64_t ka = live ? (int64_t)kt * BK * AE : 0, kb = live ? (int64_t)kt * BK * BE : 0;
+        lds_dma16(live ? a_src0 + ka : zero, st + 1024 * (2 * wid));
+        lds_dma16(live ? a_src1 + ka : zero, st + 1024 * (2 * wid + 1));
+        lds_dma16(live ? b_src + kb : zero, st + ASZ + 1024 * wid);
+    };
+
+    f32x4 acc[WR][WC];
+#pragma unroll
+    for (int i = 0; i < WR; i++)
+#pragma unroll
+        for (int j = 0; j < WC; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+#pragma unroll
+    for (int s = 0; s < NS - 1; s++) issue(s, s);
+    const int fr = lane & 15, fg = lane >> 4;
+    for (int kt = 0; kt < nk; kt++) {
+        wait_vmcnt<3 * (NS - 2)>();           // this wave's loads of stage kt have landed
+        __syncthreads();                      // ... and every wave's; stage kt - 1 is free
+        issue((kt + NS - 1) % NS, kt + NS - 1);
+        const char *st = smem[kt % NS];
+#pragma unroll
+        for (int s = 0; s < BK / 32; s++) {
+            bf16x8 bfrag[WC];
+#pragma unroll
+            for (int j = 0; j < WC; j++) {
+                const int n = nw + j * 16 + fr;
+                if (BSRC == B_BF16) {
+                    const int p = fg ^ (n & 3);
+                    bfrag[j] = *reinterpret_cast<const bf16x8 *>(st + ASZ + n * 64 + p * 16);
+                } else {
+                    // 8 int8 weights -> bf16 (exact: |q| <= 128 has 8 significant bits)
+                    const int p = (2 * s + (fg >> 1)) ^ (n & 3);
+                    const uint2 v = *reinterpret_cast<const uint2 *>(st + ASZ + n * 64 + p * 16 + (fg & 1) * 8);
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t x = e ? v.y : v.x;
+                        w[2 * e] = cvt_pk_bf16((float)(int8_t)(x & 0xFF), (float)(int8_t)((x >> 8) & 0xFF));
+                        w[2 * e + 1] = cvt_pk_bf16((float)(int8_t)((x >> 16) & 0xFF), (float)(int8_t)(x >> 24));
+                    }
+                    bfrag[j] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < WR; i++) {
+                const int r = mw + i * 16 + fr;
+                bf16x8 af[NA];
+                if (AF) {
+                    // f32 A = hi + mid + lo, each term the RNE bf16 of the remaining residual
+                    const int k4 = 2 * fg;
+                    const float4 x0 = *reinterpret_cast<const float4 *>(st + r * 128 + ((k4 ^ (r & 7)) * 16));
+                    const float4 x1 = *reinterpret_cast<const float4 *>(st + r * 128 + (((k4 + 1) ^ (r & 7)) * 16));
+                    const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                    uint32_t hi[4], mi[4], lo[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const float a0 = xv[2 * e], a1 = xv[2 * e + 1];
+                        const uint32_t h = cvt_pk_bf16(a0, a1);
+                        const float r0 = __fsub_rn(a0, __uint_as_float(h << 16));
+                        const float r1 = __fsub_rn(a1, __uint_as_float(h & 0xFFFF0000u));
+                        const uint32_t m = cvt_pk_bf16(r0, r1);
+                        const float s0 = __fsub_rn(r0, __uint_as_float(m << 16));
+                        const float s1 = __fsub_rn(r1, __uint_as_float(m & 0xFFFF0000u));
+                        hi[e] = h;
+                        mi[e] = m;
+                        lo[e] = cvt_pk_bf16(s0, s1);
+                    }
+                    af[0] = __builtin_bit_cast(bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+                    af[NA > 1 ? 1 : 0] = __builtin_bit_cast(bf16x8, make_uint4(mi[0], mi[1], mi[2], mi[3]));
+                    af[NA - 1] = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                } else {
+                    const int p = (4 * s + fg) ^ (r & 7);
+                    af[0] = *reinterpret_cast<const bf16x8 *>(st + r * 128 + p * 16);
+                }
+#pragma unroll
+                for (int a = NA - 1; a >= 0; a--)
+#pragma unroll
+                    for (int j = 0; j < WC; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[a], bfrag[j], acc[i][j], 0, 0, 0);
+            }
+        }
+    }
+    wait_vmcnt<0>();                          // no load may land in LDS after the block ends
+
+    // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile
+#pragma unroll
+    for (int i = 0; i < WR; i++)
+#pragma unroll
+        for (int j = 0; j < WC; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
+                const int n = n0 + nw + j * 16 + (lane & 15);
+                if (m >= M || n >= N) continue;
+                float v = acc[i][j][r];
+                int64_t off, gidx;
+                if (EPI & EPI_TRANS) {
+                    const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
+                    gidx = (int64_t)n * g.gelu_rows + sp;
+                    off = (int64_t)c * g.gelu_n + gidx;
+                } else {
+                    gidx = (int64_t)m * g.ldc + n;
+                    off = gidx;
+                }
+                float *cp = g.C + off;
+                if (EPI & EPI_SCALE) v = __fmul_rn(v, g.scale[n]);
+                if (EPI & EPI_ACCUM) {
+                    float c = *cp;
+                    if (g.bias) c = __fadd_rn(c, g.bias[n]);
+                    v = __fadd_rn(c, v);
+                } else if (g.bias) {
+                    v = __fadd_rn(v, g.bias[n]);
+                }
+                if (EPI & EPI_GELU) v = gelu_ref(v, gidx, g.gelu_n);
+                *cp = v;
+            }
+}
+
+// ---------------------------------------------------------------------------
 // f32 SIMT GEMM (NT), 64x64 tile, 4x4 outputs per thread, K-step 16
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_gemm_f32(GemmArgs g) {
@@ -245,14 +436,49 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
     return hipGetLastError();
 }
 
+template <int ASRC, int BSRC, int NS>
+static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
+    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64);
+    switch (epi) {
+#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS>), grid, dim3(256), 0, st, g); break;
+        QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+#undef QE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int ASRC, int BSRC>
+static hipError_t go_gemm_lds(const GemmArgs &g, int epi, hipStream_t st) {
+    // ring depth (QASR_GEMM_STAGES=3|4|6|8, tuning): 4 keeps 3 blocks per CU for large grids
+    static const int ns = [] { const char *e = getenv("QASR_GEMM_STAGES"); return e ? atoi(e) : 4; }();
+    if (ns == 3) return go_gemm_lds_ns<ASRC, BSRC, 3>(g, epi, st);
+    if (ns == 6) return go_gemm_lds_ns<ASRC, BSRC, 6>(g, epi, st);
+    if (ns == 8) return go_gemm_lds_ns<ASRC, BSRC, 8>(g, epi, st);
+    return go_gemm_lds_ns<ASRC, BSRC, 4>(g, epi, st);
+}
+
+// the LDS-ring kernel applies when every stage is whole and rows are 16-byte aligned
+static bool gemm_lds_ok(const GemmArgs &g, int asrc, int bsrc) {
+    static const bool off = [] { const char *e = getenv("QASR_GEMM_REG"); return e && e[0] == '1'; }();
+    if (off) return false;
+    const int bk = asrc == A_F32_SPLIT ? 32 : 64;
+    const int ae = asrc == A_F32_SPLIT ? 4 : 2, be = bsrc == B_BF16 ? 2 : 1;
+    return g.K % bk == 0 && (g.lda * ae) % 16 == 0 && (g.ldb * be) % 16 == 0 && (uintptr_t)g.A % 16 == 0 &&
+           (uintptr_t)g.B % 16 == 0;
+}
+
 hipError_t launch_gemm(const GemmArgs &g0, int asrc, int bsrc, int epi, hipStream_t st) {
     GemmArgs g = g0;
     if (g.M <= 0 || g.N <= 0 || g.K <= 0) return hipErrorInvalidValue;
     g.a_vec4 = (g.lda % 8 == 0) && ((uintptr_t)g.A % 16 == 0);
     g.b_vec = (g.ldb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
     if ((epi & (EPI_GELU | EPI_TRANS)) && g.gelu_rows <= 0 && (epi & EPI_TRANS)) return hipErrorInvalidValue;
-    if (asrc == A_F32_SPLIT && bsrc == B_BF16) return go_gemm<A_F32_SPLIT, B_BF16>(g, epi, st);
-    if (asrc == A_BF16 && bsrc == B_I8) return go_gemm<A_BF16, B_I8>(g, epi, st);
+    if (asrc == A_F32_SPLIT && bsrc == B_BF16)
+        return gemm_lds_ok(g, asrc, bsrc) ? go_gemm_lds<A_F32_SPLIT, B_BF16>(g, epi, st)
+                                          : go_gemm<A_F32_SPLIT, B_BF16>(g, epi, st);
+    if (asrc == A_BF16 && bsrc == B_I8)
+        return gemm_lds_ok(g, asrc, bsrc) ? go_gemm_lds<A_BF16, B_I8>(g, epi, st) : go_gemm<A_BF16, B_I8>(g, epi, st);
     if (asrc == A_BF16 && bsrc == B_BF16) return go_gemm<A_BF16, B_BF16>(g, epi, st);
     return hipErrorInvalidValue;
 }

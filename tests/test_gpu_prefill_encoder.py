@@ -19,7 +19,7 @@ def nrel(a, b):
 
 
 @pytest.mark.parametrize("M,N,K", [(404, 4096, 1024), (375, 1024, 3072), (390, 2688, 896), (100, 480, 9),
-                                   (33, 70, 100)])
+                                   (33, 70, 100), (33, 70, 128), (1, 64, 32)])
 def test_linear_bf16w(dev, orc, M, N, K):
     from qwenasr_amd import kernels as Kr
     print(f"linear_bf16w M={M} N={N} K={K}", flush=True)
