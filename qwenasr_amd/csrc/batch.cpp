@@ -32,6 +32,7 @@ using namespace qasr;
 
 namespace {
 constexpr int MAX_STREAMS = 32;
+constexpr int ATT_MAX_SPLITS = 64;
 constexpr int ARGMAX_BLOCKS = 608;      // 16 waves each: one 16-row tile per wave and pass (9496 tiles at 0.6B)
 }
 
@@ -85,11 +86,10 @@ static int64_t batch_cap(const qasr_batch *b, int64_t pos) {
     return std::min<int64_t>(std::max<int64_t>(c, 256), b->max_seq);
 }
 
-// split count of a bucket: the forced count, else the single-stream automatic
-// choice limited to the 16 splits the merge pass takes
+// split count of a bucket: the forced count, else the single-stream automatic choice
 static int batch_splits(const qasr_batch *b, int64_t cap) {
     if (b->n_split > 0) return b->n_split;
-    return std::min(16, attn_splits_auto(b->d->c, cap));
+    return attn_splits_auto(b->d->c, cap);
 }
 
 // groups of 8 positions per attention block for every position (the
@@ -133,7 +133,7 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     const int64_t I = c.intermediate, nqkv = qd + 2 * kvd;
     const int64_t kmax = std::max({H, qd, I});
     const size_t kv = (size_t)c.n_layers * n_streams * c.n_kv_heads * max_seq * hd;
-    b->part_stride = (2 * c.n_heads + c.n_heads * hd) * 16;
+    b->part_stride = (2 * c.n_heads + c.n_heads * hd) * ATT_MAX_SPLITS;
     int rc = QASR_OK;
     float *kcf = nullptr, *vcf = nullptr;
     if (rc == QASR_OK) rc = balloc(b, &kcf, kv, true);
@@ -215,8 +215,8 @@ extern "C" int qasr_hip_batch_set_options(qasr_batch *b, int attn_splits, int us
     CHECK_H(b->d->h);
     if (attn_splits < 0) b->n_split = 0;
     if (attn_splits > 0) {
-        if (attn_splits != 1 && attn_splits != 2 && attn_splits != 4 && attn_splits != 8 && attn_splits != 16)
-            return qasr_fail(QASR_ERR_INVALID, "batch_set_options: attn_splits must be 1, 2, 4, 8 or 16");
+        if (attn_splits > ATT_MAX_SPLITS)
+            return qasr_fail(QASR_ERR_INVALID, "batch_set_options: attn_splits must be 1..64 (or -1)");
         b->n_split = attn_splits;
     }
     b->use_graph = use_graph ? 1 : 0;

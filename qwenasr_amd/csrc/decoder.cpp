@@ -220,9 +220,10 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     const int64_t layer_elems = (int64_t)c.n_kv_heads * d->max_seq * hd;
     const float scale = 1.0f / sqrtf((float)hd);
     auto want = [only_kind](int kind) { return only_kind < 0 || only_kind == kind; };
-    // with few splits the o_proj kernel merges the attention partials in its
-    // prologue; otherwise the attention's last block per head merges them
-    // context bucket of this step: sizes the attention's static partition and its splits
+    // with 1, 2, 4, 8 or 16 splits the o_proj kernel merges the attention
+    // partials in its prologue; otherwise a merge kernel writes the attention
+    // row and the plain o_proj kernel quantizes it.  The context bucket of
+    // this step sizes the attention's static partition and its splits
     const int64_t cap = decoder_ctx_cap(d, d->step_pos + 1);
     const int n_split = d->n_split > 0 ? d->n_split : attn_splits_auto(c, cap);
     const bool fused_merge = oproj_merges(c, n_split);
@@ -247,14 +248,15 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = scale;
             // static partition of the step's context bucket: the first KV loads need no device state
             t.gpb = (int)((((cap + 7) / 8) + n_split - 1) / n_split);
-            LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, !fused_merge),
-                      "step attention");
+            LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, false), "step attention");
         }
         if (want(2)) {
             if (fused_merge) {
                 OprojMergeArgs om{d->part, n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
                 LAUNCHCHK(launch_oproj_merge(om, st), "step o_proj");
             } else {
+                LAUNCHCHK(launch_attn_merge_rows(d->part, 0, n_split, d->att, qd, nullptr, nullptr, 1, st),
+                          "step attention merge");
                 MvArgs o{};
                 o.x = d->att; o.K = qd;
                 o.seg[0] = {L.wo, L.so, d->x, H};

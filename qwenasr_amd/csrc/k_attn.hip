@@ -369,12 +369,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     float o_part, m_part, l_part;
     attn_block_partial<KVT, NW, G>(acc, wm, wl, wacc, o_part, m_part, l_part);
     if (!MERGE) {
-        // the consumer (the o_proj kernel) merges; the kernel boundary publishes
-        // these.  Layout, split index fastest: (m, l) of head h = G kvh + gq at
-        // [(2 h + {0,1}) S + split], o at [2 Hq S + (D h + d) S + split].
+        // the consumer (the o_proj kernel or a merge kernel) merges; the kernel
+        // boundary publishes these.  (m, l) of head h = G kvh + gq at
+        // [(2 h + {0,1}) S + split]; o as part_o_index lays it out.
         if (t < G * D) {
             const int h = kvh * G + gq;
-            partb[(int64_t)(2 * Hq + h * D + d) * n_split + split] = o_part;
+            partb[part_o_index(n_split, split, Hq, h * D + d)] = o_part;
             if (d == 0) {
                 partb[(2 * h) * n_split + split] = m_part;
                 partb[(2 * h + 1) * n_split + split] = l_part;

@@ -217,7 +217,8 @@ __device__ __attribute__((aligned(256))) int4 g_gemm_zero16[16];
 // compiler otherwise treats every LDS read as possibly aliasing any load in
 // flight and waits for all of them (vmcnt(0)) before it, which would drain
 // the ring every K-step.  The compiler does not see these loads: the kernel
-// issues no other vector-memory load until its final vmcnt(0).
+// issues no other vector-memory load until its final vmcnt(0), and it makes
+// no other use of M0 (the generated code was checked for both).
 __device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
     const uint32_t la = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory");

@@ -1095,14 +1095,91 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float *__restrict
         xq[(int64_t)b * K + (2 * j + g) * D + d] = (int8_t)round_clamp_i8(__fmul_rn(o[j], inv));
 }
 
+// The merge for the split counts the o_proj prologue does not take (any
+// other count <= 64; partials split index slowest).  Per head, one wave with
+// one split per lane: the max and sum_s l_s f_s by fixed-order wave
+// reductions, f_s = exp(m_s - max) to LDS; then per (head, dim) the o
+// partials weighted in split order.  Two kernels share these steps:
+// k_attn_merge_seq (one block per stream, all heads, with the o_proj
+// activation quantization fused) and k_attn_merge_heads (one block per
+// (head, stream), the f32 row only).
+__device__ __forceinline__ void merge_head_weights(const float *pb, int S, int h, float *fw, float *lsum) {
+    const int sp = threadIdx.x & 63;
+    const float m = sp < S ? pb[(2 * h) * S + sp] : -INFINITY;
+    const float l = sp < S ? pb[(2 * h + 1) * S + sp] : 0.0f;
+    const float M = wave_max_f32(m);
+    const float f = m == -INFINITY ? 0.0f : expf(__fsub_rn(m, M));
+    fw[sp] = f;
+    const float lt = wave_sum_f32(__fmul_rn(l, f));
+    if (sp == 0) *lsum = lt;
+}
+__device__ __forceinline__ float merge_head_dim(const float *pb, int S, int h, int d, const float *fw, float lt) {
+    constexpr int D = 128, HQ = 16;
+    const float *po = pb + 2 * HQ * S + h * D + d;
+    float ot = 0.0f;
+    for (int s = 0; s < S; s++) ot = fmaf(po[(int64_t)s * HQ * D], fw[s], ot);
+    return lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
+}
+
+__global__ __launch_bounds__(1024) void k_attn_merge_seq(const float *__restrict__ part, int64_t part_stride, int S,
+                                                        float *__restrict__ att, int64_t att_stride,
+                                                        int8_t *__restrict__ xq, float *__restrict__ xs) {
+    constexpr int D = 128, HQ = 16, K = HQ * D;
+    __shared__ float fw[HQ][64], lsum[HQ], wmax[16];
+    const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, wid = t >> 6;
+    const float *pb = part + (int64_t)b * part_stride;
+    merge_head_weights(pb, S, wid, fw[wid], &lsum[wid]);
+    __syncthreads();
+    const int hp = t >> 7, d = t & 127;
+    float o[2], am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const int h = 2 * hp + j;
+        o[j] = merge_head_dim(pb, S, h, d, fw[h], lsum[h]);
+        am = fmaxf(am, fabsf(o[j]));
+        if (att) att[(int64_t)b * att_stride + h * D + d] = o[j];
+    }
+    if (!xq) return;
+    am = wave_max_f32(am);
+    if (lane == 0) wmax[wid] = am;
+    __syncthreads();
+    am = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) am = fmaxf(am, wmax[w]);
+    float scale, inv;
+    act_scales(am, &scale, &inv);
+    if (t == 0) xs[b] = scale;
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+        xq[(int64_t)b * K + (2 * hp + j) * D + d] = (int8_t)round_clamp_i8(__fmul_rn(o[j], inv));
+}
+
+__global__ __launch_bounds__(128) void k_attn_merge_heads(const float *__restrict__ part, int64_t part_stride, int S,
+                                                         float *__restrict__ att, int64_t att_stride) {
+    constexpr int D = 128;
+    __shared__ float fw[64], lsum;
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const float *pb = part + (int64_t)b * part_stride;
+    if (t < 64) merge_head_weights(pb, S, h, fw, &lsum);
+    __syncthreads();
+    att[(int64_t)b * att_stride + h * D + t] = merge_head_dim(pb, S, h, t, fw, lsum);
+}
+
 hipError_t launch_attn_merge_rows(const float *part, int64_t part_stride, int n_split, float *att,
                                   int64_t att_stride, int8_t *xq, float *xs, int B, hipStream_t st) {
-    if (!xq || !xs || B <= 0) return hipErrorInvalidValue;
+    if ((!xq) != (!xs) || (!xq && !att) || B <= 0 || n_split <= 0 || n_split > 64) return hipErrorInvalidValue;
     switch (n_split) {
-#define AM(S) case S: hipLaunchKernelGGL(k_attn_merge_rows<S>, dim3(B), dim3(256), 0, st, part, part_stride, att, att_stride, xq, xs); break;
+#define AM(S) case S: if (!xq) return hipErrorInvalidValue; \
+        hipLaunchKernelGGL(k_attn_merge_rows<S>, dim3(B), dim3(256), 0, st, part, part_stride, att, att_stride, xq, xs); break;
         AM(1) AM(2) AM(4) AM(8) AM(16)
 #undef AM
-        default: return hipErrorInvalidValue;
+        default:
+            if (xq)
+                hipLaunchKernelGGL(k_attn_merge_seq, dim3(B), dim3(1024), 0, st, part, part_stride, n_split, att,
+                                   att_stride, xq, xs);
+            else
+                hipLaunchKernelGGL(k_attn_merge_heads, dim3(16, B), dim3(128), 0, st, part, part_stride, n_split, att,
+                                   att_stride);
     }
     return hipGetLastError();
 }

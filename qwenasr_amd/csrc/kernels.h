@@ -82,11 +82,24 @@ hipError_t launch_argmax_batch(const BatchMvArgs &a, int blocks, int *state, int
                                const float *rope_cos, const float *rope_sin, float *rope_cur, int max_pos,
                                const int *gpb_table, int *gpb_dev, hipStream_t st, bool stream = true,
                                bool finish = true);
-// split merge per stream + int8 quantization of the merged row (xq [B][2048], xs [B]); att nullable
+// split merge per stream + int8 quantization of the merged row (xq [B][2048], xs [B]);
+// att nullable.  n_split 1, 2, 4, 8, 16: the o_proj prologue's merge (xq required);
+// any other count <= 64: a sequential merge (xq nullable: att only)
 hipError_t launch_attn_merge_rows(const float *part, int64_t part_stride, int n_split, float *att,
                                   int64_t att_stride, int8_t *xq, float *xs, int B, hipStream_t st);
 
 // ---- attention / norms / rope ---------------------------------------------
+// Position of o[split][e] (e = 128 h + d) among the attention partials of one
+// step: after the 2 Hq S (max, sum) entries, split index fastest for the
+// split counts the o_proj prologue merges (1, 2, 4, 8, 16: a thread loads
+// its S values as one vector), split index slowest otherwise (the merge
+// kernel's threads read consecutive e).
+__host__ __device__ inline bool part_split_fastest(int S) { return S <= 16 && (S & (S - 1)) == 0; }
+__host__ __device__ inline int64_t part_o_index(int S, int split, int Hq, int e) {
+    return part_split_fastest(S) ? (int64_t)(2 * Hq + e) * S + split
+                                 : (int64_t)2 * Hq * S + (int64_t)split * Hq * 128 + e;
+}
+
 struct AttnDecodeArgs {
     const float *qkv;         // raw projections: q [Hq*D] | k [Hkv*D] | v [Hkv*D]
     const float *q_norm, *k_norm;   // per-head RMSNorm gains [D] (nullable: skip norm+rope)

@@ -70,8 +70,10 @@ def test_batch_matches_solo_auto(small_decoder, n_streams):
     assert len(np.unique(got)) > max(3, n_streams // 2)     # not a degenerate constant output
 
 
-@pytest.mark.parametrize("splits", [1, 8, 16])
+@pytest.mark.parametrize("splits", [1, 3, 8, 16, 40])
 def test_batch_matches_solo_forced_splits(small_decoder, splits):
+    """1, 8, 16: merged like the o_proj prologue merges; 3, 40: the
+    sequential merge kernel the single-stream decoder also uses"""
     _, dec = small_decoder
     print(f"batch vs solo, 7 streams, {splits} splits", flush=True)
     lens = [3, 250, 300, 700, 1100, 1490, 1700]
@@ -103,6 +105,35 @@ def test_batch_argument_errors(small_decoder):
         with pytest.raises(QasrError):
             b.generate([1, 2], 5)      # stream 0 would pass 64 positions
         with pytest.raises(QasrError):
-            b.set_options(attn_splits=3)
+            b.set_options(attn_splits=65)
     finally:
         b.close()
+
+
+def test_batch_matches_solo_long_contexts(dev):
+    """contexts past 2048: 36-64 automatic splits, merged by the sequential
+    merge kernel in both the batch and the single-stream decoder"""
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    print("batch vs solo, long contexts", flush=True)
+    cfg = dict(SMALL, n_layers=2, vocab=4096)
+    w = SynthDecoder(cfg, seed=1005)
+    dec = Decoder(dev, w, max_seq=4096)
+    try:
+        lens = [2100, 3000, 4000, 700]
+        r = rng(91)
+        prefixes = [r.normal(0, 1, (L, cfg["hidden"])).astype(np.float32) for L in lens]
+        first = r.integers(0, cfg["vocab"], len(lens))
+        from qwenasr_amd.model import Batch
+        b = Batch(dec, len(lens), 4096, max_steps=8)
+        try:
+            for i, p in enumerate(prefixes):
+                b.prefill(i, p)
+            got = b.generate(first, 8)
+        finally:
+            b.close()
+        for i in range(len(lens)):
+            want = solo_tokens(dec, prefixes[i], first[i], 8, -1)
+            assert (got[i] == want).all(), (i, lens[i], got[i].tolist(), want.tolist())
+    finally:
+        dec.close()
