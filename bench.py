@@ -182,7 +182,7 @@ def main():
                    "decode_stream_gbs_kernel_time": round(stream_bytes / (step_us * 1e3), 1),
                    "int8_matvec_hbm": matvec,
                    "wall_ms_per_step_pcie_inclusive": round(1000.0 * float(np.mean(wall)), 3),
-                   "matvec": "int8 W8A8 (v_dot4_i32_i8)", "gemm": "bf16 MFMA, f32 activations split in 3 bf16 terms"},
+                   "matvec": "int8 W8A8 (v_dot4_i32_i8)", "gemm": "bf16 MFMA (LDS ring fed by global_load_lds), f32 activations split in 3 bf16 terms"},
         "roofline": roof,
         "cpu_baseline": cpu,
     }
