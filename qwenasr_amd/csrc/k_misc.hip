@@ -1,5 +1,7 @@
 // Row-wise and element-wise kernels of the prefill, the audio encoder and the
 // mel front end, plus the multi-row (prefill / encoder-window) attention.
+#include <cstdlib>
+
 #include "kernels.h"
 
 namespace qasr {
@@ -337,8 +339,177 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The same multi-row attention on f32 MFMA (v_mfma_f32_16x16x4_f32, exact f32
+// products, f32 accumulation).  A block owns 16 query rows of the G query
+// heads of one KV head; its 4 waves are (head g, key split ks), G x KS = 4,
+// and wave (g, ks) takes the 16-key sub-tiles ks, ks + KS, ... of every
+// KS x 16-key chunk staged in LDS, with an online softmax of its own; the KS
+// states of a head are merged through LDS at the end.  Per sub-tile the wave
+// forms S^T = K Q^T (16 keys x 16 queries; lane l holds keys 4 (l / 16) + i
+// of query l % 16, the dot over d split as lane group l / 16 covering dims
+// [l/16 HD/4, +HD/4)), so the softmax of a query reduces over the lane's 4
+// values and two cross-group shuffles, and the probabilities already sit in
+// the A-operand layout of O += P V (query l % 16, key 4 (l / 16) + i at step
+// i).  The O rows a lane accumulates are queries 4 (l / 16) + j, whose
+// rescale factors come from the lanes owning those queries.
+// ---------------------------------------------------------------------------
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
+    constexpr int KS = NW / G, CH = 16 * KS, NST = HD / 4, NT = HD / 16, LD = HD + 4;
+    constexpr int NTH = NW * 64, SV = CH * (HD / 4) / NTH;   // float4 of K (and of V) staged per thread
+    static_assert(CH * (HD / 4) % NTH == 0, "staging");
+    // one LDS buffer: K and V chunks [CH][LD] during the loop, the waves' O rows after it
+    static_assert(2 * CH * LD >= NW * 16 * HD, "merge buffer");
+    __shared__ __attribute__((aligned(16))) float smem[2 * CH * LD];
+    float (*Ks)[LD] = reinterpret_cast<float (*)[LD]>(smem);
+    float (*Vs)[LD] = reinterpret_cast<float (*)[LD]>(smem + CH * LD);
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int g = wid / KS, ks = wid % KS;
+    const int kvh = blockIdx.x, q0 = blockIdx.y * 16;
+    const int h = kvh * G + g;
+    const int lq = lane & 15, lg = lane >> 4;
+    // key range of this lane's query (for the S^T masks) and of the block
+    const int qi = q0 + lq;
+    int lo = 0, hi = 0;
+    if (qi < a.n_q) {
+        if (a.window > 0) {
+            lo = (qi / a.window) * a.window;
+            hi = min(lo + a.window, a.n_k);
+        } else {
+            hi = min(a.q_offset + qi + 1, a.n_k);
+        }
+    }
+    const int qlast = min(q0 + 16, a.n_q) - 1;
+    int blo, bhi;
+    if (a.window > 0) {
+        blo = (q0 / a.window) * a.window;
+        bhi = min((qlast / a.window) * a.window + a.window, a.n_k);
+    } else {
+        blo = 0;
+        bhi = min(a.q_offset + qlast + 1, a.n_k);
+    }
+    // this lane's slice of q: dims [lg NST, lg NST + NST) of query qi, head h
+    float qv[NST];
+    {
+        const float *qp = a.q + (int64_t)min(qi, a.n_q - 1) * a.q_rs + h * HD + lg * NST;
+#pragma unroll
+        for (int s = 0; s < NST; s += 4) {
+            const float4 x = *reinterpret_cast<const float4 *>(qp + s);
+            qv[s] = x.x; qv[s + 1] = x.y; qv[s + 2] = x.z; qv[s + 3] = x.w;
+        }
+    }
+    f32x4 o[NT];
+#pragma unroll
+    for (int n = 0; n < NT; n++) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    float m = -INFINITY, l = 0.0f;
+    const float *kb = a.k + (int64_t)kvh * a.k_hs, *vb = a.v + (int64_t)kvh * a.k_hs;
+    for (int c0 = blo; c0 < bhi; c0 += CH) {
+        __syncthreads();
+        // stage keys [c0, c0 + CH) (rows past the range repeat row blo; their scores are masked)
+#pragma unroll
+        for (int u = 0; u < SV; u++) {
+            const int i = t + u * NTH, kk = i / (HD / 4), d4 = (i % (HD / 4)) * 4;
+            const int j = c0 + kk < bhi ? c0 + kk : blo;
+            *reinterpret_cast<float4 *>(&Ks[kk][d4]) = *reinterpret_cast<const float4 *>(kb + (int64_t)j * a.k_rs + d4);
+            *reinterpret_cast<float4 *>(&Vs[kk][d4]) = *reinterpret_cast<const float4 *>(vb + (int64_t)j * a.k_rs + d4);
+        }
+        __syncthreads();
+        const int kt = 16 * ks;                 // this wave's sub-tile of the chunk
+        if (c0 + kt >= bhi) continue;
+        // S^T[key kt + 4 lg + i][query lq]
+        f32x4 st = {0.0f, 0.0f, 0.0f, 0.0f};
+        const float *kr = &Ks[kt + lq][lg * NST];
+#pragma unroll
+        for (int s = 0; s < NST; s += 4) {
+            const float4 kx = *reinterpret_cast<const float4 *>(kr + s);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kx.x, qv[s], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kx.y, qv[s + 1], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kx.z, qv[s + 2], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kx.w, qv[s + 3], st, 0, 0, 0);
+        }
+        float sv[4], tm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int j = c0 + kt + 4 * lg + i;
+            sv[i] = (j >= lo && j < hi) ? __fmul_rn(st[i], a.scale) : -INFINITY;
+            tm = fmaxf(tm, sv[i]);
+        }
+        tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+        tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+        const float mn = fmaxf(m, tm);
+        const float corr = (m == -INFINITY) ? 0.0f : expf(__fsub_rn(m, mn));
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            sv[i] = sv[i] == -INFINITY ? 0.0f : expf(__fsub_rn(sv[i], mn));
+        }
+        ps = __fadd_rn(__fadd_rn(sv[0], sv[1]), __fadd_rn(sv[2], sv[3]));
+        ps = __fadd_rn(ps, __shfl_xor(ps, 16, 64));
+        ps = __fadd_rn(ps, __shfl_xor(ps, 32, 64));
+        l = fmaf(l, corr, ps);
+        m = mn;
+        // rescale the O rows this lane holds (queries 4 lg + j) by their owners' factors
+        float cj[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) cj[j] = __shfl(corr, 4 * lg + j, 64);
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) o[n][j] = __fmul_rn(o[n][j], cj[j]);
+        // O += P V: step i pairs key kt + 4 lg + i of P (this lane's sv[i]) with V row kt + 4 lg + i
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float *vr = &Vs[kt + 4 * lg + i][lq];
+#pragma unroll
+            for (int n = 0; n < NT; n++) o[n] = __builtin_amdgcn_mfma_f32_16x16x4f32(sv[i], vr[16 * n], o[n], 0, 0, 0);
+        }
+    }
+    // merge the KS key splits of each head: (m, l) per query, O rows through LDS
+    __syncthreads();
+    float *Om = smem;                                   // [NW waves][16 rows][HD]
+    __shared__ float Mm[NW][16], Ll[NW][16];
+    if (lg == 0) { Mm[wid][lq] = m; Ll[wid][lq] = l; }
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) Om[(wid * 16 + 4 * lg + j) * HD + 16 * n + lq] = o[n][j];
+    __syncthreads();
+    for (int i = t; i < G * 16 * HD; i += NTH) {
+        const int gg = i / (16 * HD), r = (i / HD) % 16, d = i % HD;
+        const int q = q0 + r;
+        if (q >= a.n_q) continue;
+        float M = -INFINITY;
+#pragma unroll
+        for (int k2 = 0; k2 < KS; k2++) M = fmaxf(M, Mm[gg * KS + k2][r]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int k2 = 0; k2 < KS; k2++) {
+            const int w = gg * KS + k2;
+            const float f = Mm[w][r] == -INFINITY ? 0.0f : expf(__fsub_rn(Mm[w][r], M));
+            L = fmaf(Ll[w][r], f, L);
+            O = fmaf(Om[(w * 16 + r) * HD + d], f, O);
+        }
+        a.out[(int64_t)q * a.o_rs + (kvh * G + gg) * HD + d] = L > 0.0f ? __fdiv_rn(O, L) : 0.0f;
+    }
+}
+
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st) {
     if (a.G <= 0 || 32 % a.G != 0 || a.n_q <= 0) return hipErrorInvalidValue;
+    static const bool simt = [] { const char *e = getenv("QASR_ATTN_ROWS_SIMT"); return e && e[0] == '1'; }();
+    const bool aligned = a.q_rs % 4 == 0 && a.k_rs % 4 == 0 && a.k_hs % 4 == 0 && (uintptr_t)a.q % 16 == 0 &&
+                         (uintptr_t)a.k % 16 == 0 && (uintptr_t)a.v % 16 == 0;
+    if (!simt && aligned && (a.G == 1 || a.G == 2) && (head_dim == 128 || head_dim == 64)) {
+        const dim3 grid(n_kv_heads, (a.n_q + 15) / 16);
+#define QAM(HDV, GV) hipLaunchKernelGGL((k_attn_mfma<HDV, GV, 4>), grid, dim3(256), 0, st, a);
+        if (head_dim == 128 && a.G == 2) { QAM(128, 2) }
+        else if (head_dim == 128) { QAM(128, 1) }
+        else if (a.G == 2) { QAM(64, 2) }
+        else { QAM(64, 1) }
+#undef QAM
+        return hipGetLastError();
+    }
     const dim3 grid(n_kv_heads, (a.n_q + 32 / a.G - 1) / (32 / a.G));
     if (head_dim == 128) hipLaunchKernelGGL(k_attn_rows<128>, grid, dim3(256), 0, st, a);
     else if (head_dim == 64) hipLaunchKernelGGL(k_attn_rows<64>, grid, dim3(256), 0, st, a);

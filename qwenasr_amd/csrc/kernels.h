@@ -11,6 +11,7 @@
 namespace qasr {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum { MV_PLAIN = 0, MV_ADDTO = 1, MV_SWIGLU = 2, MV_BIAS = 3 };
 
