@@ -236,40 +236,49 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
-template <int ASRC, int BSRC, int EPI, int NS>
+template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN>
 __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     constexpr bool AF = ASRC == A_F32_SPLIT;
-    constexpr int BK = AF ? 32 : 64, ASZ = 8192, BSZ = 4096, STG = ASZ + BSZ;
+    constexpr int AE = AF ? 4 : 2, BE = BSRC == B_BF16 ? 2 : 1;     // element bytes
+    constexpr int BK = AF ? 32 : 64;                                 // A rows are 128 B, B rows 64 B per stage
+    constexpr int ASZ = BM * 128, BSZ = BN * 64, STG = ASZ + BSZ;
+    constexpr int LA = BM / 32, LB = BN / 64;                        // one-KiB loads per wave per stage
     constexpr int NA = AF ? 3 : 1;
-    // wave tiling of the 64 x 64 block: the operand that needs converting is
-    // owned by one wave per fragment (f32 A: waves take 16-row strips; int8 B:
-    // waves take 16-column strips), so no fragment is converted twice
-    constexpr int WR = AF ? 1 : 4, WC = AF ? 4 : 1;
+    // wave tiling: the operand that needs converting is owned by one wave per
+    // fragment (f32 A: waves take BM/4-row strips; int8 B: BN/4-column strips),
+    // so no fragment is converted twice
+    constexpr int WR = (AF ? BM / 4 : BM) / 16, WC = (AF ? BN : BN / 4) / 16;
     static_assert(BSRC == (AF ? B_BF16 : B_I8), "operand pair");
+    static_assert(BM % 32 == 0 && BN % 64 == 0, "tile");
     __shared__ __attribute__((aligned(16))) char smem[NS][STG];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int mw = AF ? 16 * wid : 0, nw = AF ? 0 : 16 * wid;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int mw = AF ? (BM / 4) * wid : 0, nw = AF ? 0 : (BN / 4) * wid;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int M = g.M, N = g.N, K = g.K, nk = K / BK;
-    // this lane's rows and swizzled slots in the wave's three loads per stage
-    const int ra0 = 8 * (2 * wid) + (lane >> 3), ra1 = ra0 + 8;            // A rows of loads 2w, 2w + 1
-    const int pa0 = (lane & 7) ^ (ra0 & 7), pa1 = (lane & 7) ^ (ra1 & 7);
-    const int rb = 16 * wid + (lane >> 2), pb = (lane & 3) ^ (rb & 3);    // B row of load w
-    const int am0 = min(m0 + ra0, M - 1), am1 = min(m0 + ra1, M - 1), bnr = min(n0 + rb, N - 1);
+    // this lane's rows and swizzled 16-byte slots in the wave's loads: A load j
+    // covers tile rows 8 j .. 8 j + 7 (8 slots each), B load j rows 16 j .. 16 j + 15 (4 slots)
     const char *A = reinterpret_cast<const char *>(g.A), *B = reinterpret_cast<const char *>(g.B);
-    constexpr int AE = AF ? 4 : 2, BE = BSRC == B_BF16 ? 2 : 1;     // element bytes
-    const char *a_src0 = A + ((int64_t)am0 * g.lda) * AE + 16 * pa0;   // + k0 * AE per stage
-    const char *a_src1 = A + ((int64_t)am1 * g.lda) * AE + 16 * pa1;
-    const char *b_src = B + ((int64_t)bnr * g.ldb) * BE + 16 * pb;
+    const char *a_src[LA], *b_src[LB];
+#pragma unroll
+    for (int u = 0; u < LA; u++) {
+        const int r = 8 * (wid * LA + u) + (lane >> 3), p = (lane & 7) ^ (r & 7);
+        a_src[u] = A + ((int64_t)min(m0 + r, M - 1) * g.lda) * AE + 16 * p;
+    }
+#pragma unroll
+    for (int u = 0; u < LB; u++) {
+        const int r = 16 * (wid * LB + u) + (lane >> 2), p = (lane & 3) ^ (r & 3);
+        b_src[u] = B + ((int64_t)min(n0 + r, N - 1) * g.ldb) * BE + 16 * p;
+    }
     const char *zero = reinterpret_cast<const char *>(g_gemm_zero16);
     auto issue = [&](int buf, int kt) {
         char *st = smem[buf];
         const bool live = kt < nk;
         const int64_t ka = live ? (int64_t)kt * BK * AE : 0, kb = live ? (int64_t)kt * BK * BE : 0;
-        lds_dma16(live ? a_src0 + ka : zero, st + 1024 * (2 * wid));
-        lds_dma16(live ? a_src1 + ka : zero, st + 1024 * (2 * wid + 1));
-        lds_dma16(live ? b_src + kb : zero, st + ASZ + 1024 * wid);
+#pragma unroll
+        for (int u = 0; u < LA; u++) lds_dma16(live ? a_src[u] + ka : zero, st + 1024 * (wid * LA + u));
+#pragma unroll
+        for (int u = 0; u < LB; u++) lds_dma16(live ? b_src[u] + kb : zero, st + ASZ + 1024 * (wid * LB + u));
     };
 
     f32x4 acc[WR][WC];
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     for (int s = 0; s < NS - 1; s++) issue(s, s);
     const int fr = lane & 15, fg = lane >> 4;
     for (int kt = 0; kt < nk; kt++) {
-        wait_vmcnt<3 * (NS - 2)>();           // this wave's loads of stage kt have landed
+        wait_vmcnt<(LA + LB) * (NS - 2)>();   // this wave's loads of stage kt have landed
         __syncthreads();                      // ... and every wave's; stage kt - 1 is free
         issue((kt + NS - 1) % NS, kt + NS - 1);
         const char *st = smem[kt % NS];
@@ -436,11 +445,11 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
     return hipGetLastError();
 }
 
-template <int ASRC, int BSRC, int NS>
+template <int ASRC, int BSRC, int NS, int BM, int BN>
 static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
-    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64);
+    const dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
     switch (epi) {
-#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS>), grid, dim3(256), 0, st, g); break;
+#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN>), grid, dim3(256), 0, st, g); break;
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
 #undef QE
         default: return hipErrorInvalidValue;
@@ -450,12 +459,13 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
 
 template <int ASRC, int BSRC>
 static hipError_t go_gemm_lds(const GemmArgs &g, int epi, hipStream_t st) {
-    // ring depth (QASR_GEMM_STAGES=3|4|6|8, tuning): 4 keeps 3 blocks per CU for large grids
-    static const int ns = [] { const char *e = getenv("QASR_GEMM_STAGES"); return e ? atoi(e) : 4; }();
-    if (ns == 3) return go_gemm_lds_ns<ASRC, BSRC, 3>(g, epi, st);
-    if (ns == 6) return go_gemm_lds_ns<ASRC, BSRC, 6>(g, epi, st);
-    if (ns == 8) return go_gemm_lds_ns<ASRC, BSRC, 8>(g, epi, st);
-    return go_gemm_lds_ns<ASRC, BSRC, 4>(g, epi, st);
+    // 64 x 64 tiles (4 stages of 12 KiB, 3 blocks per CU) while they leave
+    // fewer than ~2 blocks per CU; beyond, 128 x 128 tiles (3 stages of 24
+    // KiB): four times the MFMA work per K-step and barrier.  QASR_GEMM_TILE=64|128 forces one.
+    static const int forced = [] { const char *e = getenv("QASR_GEMM_TILE"); return e ? atoi(e) : 0; }();
+    const int64_t small_blocks = (int64_t)((g.N + 63) / 64) * ((g.M + 63) / 64);
+    const bool big = forced ? forced == 128 : small_blocks >= 2048;
+    return big ? go_gemm_lds_ns<ASRC, BSRC, 3, 128, 128>(g, epi, st) : go_gemm_lds_ns<ASRC, BSRC, 4, 64, 64>(g, epi, st);
 }
 
 // the LDS-ring kernel applies when every stage is whole and rows are 16-byte aligned
