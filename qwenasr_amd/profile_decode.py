@@ -4,9 +4,11 @@
         --output-format csv -d <dir> -o run -- python3 -m qwenasr_amd.profile_decode [steps] [calib_mib]
 
 Loads the seeded 0.6B decoder of the headline workload (bench.py, seed 1002),
-prefills a 404-row synthetic prompt (the config-2 prompt length), runs `steps`
-greedy decode steps (kernel by kernel when QASR_DISABLE_GRAPH=1, so the
-profiler sees every dispatch) and finally one device copy of `calib_mib` MiB
+prefills a `ctx`-row synthetic prompt (494 = the context where bench.py's
+per-kernel timing starts: the 404-row config-2 prompt + 90 steps), runs `steps`
+greedy decode steps one call at a time, printing each (kernel by kernel when
+QASR_DISABLE_GRAPH=1, so the profiler sees every dispatch; a counter run
+serialises every dispatch) and finally one device copy of `calib_mib` MiB
 with the library's copy kernel, whose counter reading calibrates the others
 (``python -m qwenasr_amd.rocprof_summary --pmc``).
 """
@@ -19,16 +21,20 @@ from .model import Decoder
 from .synth import DEC_0_6B, SynthDecoder
 
 
-def main(steps=100, calib_mib=256):
+def main(steps=20, calib_mib=64, ctx=494):
     w = SynthDecoder(DEC_0_6B, seed=1002)
     dev = Device(0)
     dec = Decoder(dev, w, max_seq=1024)
+    print("[profile_decode] decoder loaded", flush=True)
     rng = np.random.default_rng(1002)
-    prompt = (rng.standard_normal((404, DEC_0_6B["hidden"])) * 0.5).astype(np.float32)
+    prompt = (rng.standard_normal((ctx, DEC_0_6B["hidden"])) * 0.5).astype(np.float32)
     dec.prefill(prompt)
-    toks = dec.generate(steps, first_embed=prompt[-1])
-    print(f"[profile_decode] {steps} steps at context {404}..{404 + steps}, last token {int(toks[-1])}",
-          flush=True)
+    print("[profile_decode] prompt prefilled", flush=True)
+    # one step per call so that a counter run (every dispatch serialised) reports progress
+    tok = int(dec.generate(1, first_embed=prompt[-1])[0])
+    for s in range(1, steps):
+        tok = int(dec.generate(1, first_token=tok)[0])
+        print(f"[profile_decode] step {s + 1}/{steps} at context {ctx + s}, token {tok}", flush=True)
     nb = calib_mib << 20
     a, b = dev.empty(nb, np.uint8), dev.empty(nb, np.uint8)
     dev.copy(b, a)
@@ -39,4 +45,5 @@ def main(steps=100, calib_mib=256):
 
 
 if __name__ == "__main__":
-    main(int(sys.argv[1]) if len(sys.argv) > 1 else 100, int(sys.argv[2]) if len(sys.argv) > 2 else 256)
+    main(int(sys.argv[1]) if len(sys.argv) > 1 else 20, int(sys.argv[2]) if len(sys.argv) > 2 else 64,
+         int(sys.argv[3]) if len(sys.argv) > 3 else 494)
