@@ -3,6 +3,7 @@
     python -m qwenasr_amd.bench_configs config1 [reps]
     python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
     python -m qwenasr_amd.bench_configs config4 [n_streams] [steps] [attn_splits]
+    python -m qwenasr_amd.bench_configs stream [seconds] [chunk_sec]
 
 config1: the prefill / audio-encoder int8 x bf16 GEMMs at M = 375 (also 390,
 404), the seven 0.6B projections and the LM head, seeded N(0,0.02) weights
@@ -27,6 +28,15 @@ by the single-stream decoder, the token identity of the two, and the
 step's algorithmic bytes (int8 weights once + every stream's KV cache) as
 GB/s.
 
+stream: the streaming driver (qasr_hip_stream_*, transcribe.rs:902-1304) on the
+config-2 model and audio (seeds 1002): the audio pushed `chunk_sec` at a time
+(each push hands over all audio so far, as stream_push_audio does), then a
+final push; per-push wall time (host clock around the synchronous push, audio
+upload included), total time and realtime factor, committed tokens and the
+driver's statistics, with the QwenCtx stream defaults and with 3-token
+bursts (rollback 1).  Token parity of the
+driver against the oracle restatement is test_gpu_stream.py's.
+
 Each configuration prints one JSON line (stdout); progress goes to stderr.
 """
 import json
@@ -37,8 +47,8 @@ import numpy as np
 
 from . import Device
 from . import kernels as K
-from .model import Batch, Decoder, profile_decoder
-from .synth import DEC_0_6B, DEC_1_7B, SynthDecoder, normal_bf16
+from .model import Batch, Decoder, Encoder, Stream, profile_decoder
+from .synth import DEC_0_6B, DEC_1_7B, ENC_0_6B, SynthDecoder, SynthEncoder, audio, normal_bf16
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
@@ -233,6 +243,56 @@ def config4(n_streams=32, steps=32, splits=-1):
     dev.close()
 
 
+def stream(seconds=30.0, chunk_sec=2.0):
+    dev = Device(0)
+    t0 = time.time()
+    wd = SynthDecoder(DEC_0_6B, seed=1002)
+    we = SynthEncoder(ENC_0_6B, seed=1002)
+    n = int(round(seconds * 16000))
+    x = audio(n, 1002)
+    dec = Decoder(dev, wd, max_seq=2048)
+    enc = Encoder(dev, we)
+    dev.sync()
+    log(f"[stream] model and {seconds:.0f} s audio ready in {time.time() - t0:.1f}s")
+    step = int(round(chunk_sec * 16000))
+    ends = list(range(step, n + 1, step))
+    res = {}
+    # the defaults (a random-init model repeats itself, so the degeneracy rule
+    # resets the stream every chunk: full prefill, 32 decode steps per push)
+    # and short bursts (no reset: prefix reuse and delta prefill every push)
+    for label, cfg in (("defaults", {}), ("bursts_of_3", {"max_new_tokens": 3, "rollback": 1})):
+        for rep in range(2):                       # the first pass warms the graphs and buffers
+            st = Stream(dec, enc, chunk_sec=chunk_sec, **cfg)
+            times, emitted = [], 0
+            for end in ends:
+                c0 = time.perf_counter()
+                emitted += len(st.push(x[:end]))
+                times.append(time.perf_counter() - c0)
+            c0 = time.perf_counter()
+            emitted += len(st.push(x[:n], finalize=True))
+            t_final = time.perf_counter() - c0
+            stats = [int(v) for v in st.stats()]
+            ntok = len(st.tokens())
+            st.close()
+        total = sum(times) + t_final
+        res[label] = {"pushes": len(ends) + 1, "push_ms_mean": round(1000 * float(np.mean(times)), 2),
+                      "push_ms_max": round(1000 * float(np.max(times)), 2),
+                      "push_ms_last_chunk": round(1000 * times[-1], 2), "final_push_ms": round(1000 * t_final, 2),
+                      "total_ms": round(1000 * total, 2), "realtime_factor": round(seconds / total, 2),
+                      "committed_tokens": ntok, "stats": stats}
+        log(f"[stream] {label}: {len(ends)} pushes of {chunk_sec} s, mean {res[label]['push_ms_mean']} ms, "
+            f"max {res[label]['push_ms_max']} ms; total {res[label]['total_ms']} ms = "
+            f"{res[label]['realtime_factor']}x realtime; {ntok} tokens; stats {stats}")
+    print(json.dumps({"config": f"streaming driver: Qwen3-ASR-0.6B (28-layer int8 decoder, 18-layer encoder), "
+                                f"{seconds:.0f} s synthetic audio pushed in {chunk_sec} s chunks",
+                      "stats_columns": ["chunk_idx", "reused_rows", "prefill_len", "delta_rows", "forwards",
+                                        "forwards_total", "encoder_windows", "raw_tokens"],
+                      "results": res}))
+    dec.close()
+    enc.close()
+    dev.close()
+
+
 if __name__ == "__main__":
     what = sys.argv[1] if len(sys.argv) > 1 else "config3"
     if what == "config1":
@@ -242,5 +302,7 @@ if __name__ == "__main__":
     elif what == "config4":
         config4(int(sys.argv[2]) if len(sys.argv) > 2 else 32, int(sys.argv[3]) if len(sys.argv) > 3 else 32,
                 int(sys.argv[4]) if len(sys.argv) > 4 else -1)
+    elif what == "stream":
+        stream(float(sys.argv[2]) if len(sys.argv) > 2 else 30.0, float(sys.argv[3]) if len(sys.argv) > 3 else 2.0)
     else:
         raise SystemExit(f"unknown configuration {what!r}")
