@@ -107,6 +107,11 @@ int qasr_hip_rmsnorm_argmax_int8(qasr_hip *h, const float *x, const float *norm_
                                  const int8_t *w, const float *ws, int64_t in_dim, int64_t out_dim,
                                  int32_t *idx);
 
+/* The aligner's per-row argmax (align.rs:312-321) over device logits
+ * x [rows][ld] (cols <= ld used): idx (device [rows]) = lowest column of the
+ * row maximum, NaN values skipped, 0 when column 0 is NaN. */
+int qasr_hip_argmax_f32_rows(qasr_hip *h, const float *x, int64_t ld, int64_t rows, int64_t cols, int32_t *idx);
+
 /* ---- A8-A12: norms, RoPE, attention (f32, device pointers) -------------- */
 /* rms_norm (kernels/mod.rs:1191-1212); hidden % 64 == 0, hidden <= 4096 */
 int qasr_hip_rms_norm(qasr_hip *h, float *out, const float *x, const float *w, int64_t seq,
@@ -183,6 +188,23 @@ int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_de
 void qasr_hip_decoder_free(qasr_decoder *d);
 /* decoder_prefill (decoder.rs:455-547): host f32 embeddings [seq_len, hidden] */
 int qasr_hip_decoder_prefill(qasr_decoder *d, const float *embeds, int64_t seq_len);
+/* decoder_prefill_logits (decoder.rs:649-681), the forced aligner's path:
+ * prefill of seq_len rows, then the final RMSNorm of every row and the bf16
+ * LM head (f32-class GEMM); logits host [seq_len][qasr_hip_decoder_logits_dim].
+ * The head is the tied embedding unless qasr_hip_decoder_set_lm_head gave a
+ * separate one (decoder.lm_head_bf16, decoder.rs:143: host bf16 [out_dim][hidden],
+ * copied; null restores the tied embedding). */
+int qasr_hip_decoder_set_lm_head(qasr_decoder *d, const uint16_t *w_bf16, int64_t out_dim);
+int64_t qasr_hip_decoder_logits_dim(const qasr_decoder *d);
+int qasr_hip_decoder_prefill_logits(qasr_decoder *d, const float *embeds, int64_t seq_len, float *logits);
+/* The forced aligner's use of those logits (align.rs:300-321): the same
+ * prefill, then the head and a per-row argmax only for the n_rows prefill rows
+ * listed in rows (host, each in [0, seq_len): the <timestamp> positions),
+ * written to idx (host [n_rows]).  The argmax is the reference's left scan:
+ * lowest column of the row maximum, NaN values skipped, 0 when column 0 is NaN.
+ * The logits stay on the device; only the indices come back. */
+int qasr_hip_decoder_prefill_argmax(qasr_decoder *d, const float *embeds, int64_t seq_len, const int32_t *rows,
+                                    int64_t n_rows, int32_t *idx);
 /* decoder_forward (decoder.rs:550-645): embed is a host f32 row, or NULL to use
  * token_in's embedding row (tok_embed_bf16_to_f32, decoder.rs:687).  Returns the
  * greedy token in *token_out. */

@@ -809,8 +809,48 @@ static void linear_bf16(or_decoder *d, float *y, const float *x, const uint16_t 
     or_linear(y, x, d->scratch, NULL, seq, in_dim, out_dim);
 }
 
-/* decoder_prefill (decoder.rs:455-547) */
-void or_decoder_prefill(or_decoder *d, const float *embeds, int64_t S) {
+/* decoder_prefill (decoder.rs:455-547); hidden_out (nullable) receives the
+ * last layer's output rows [S][H] (pref_x before the final norm) */
+static void dec_prefill(or_decoder *d, const float *embeds, int64_t S, float *hidden_out);
+void or_decoder_prefill(or_decoder *d, const float *embeds, int64_t S) { dec_prefill(d, embeds, S, NULL); }
+void or_decoder_prefill_hidden(or_decoder *d, const float *embeds, int64_t S, float *hidden) {
+    dec_prefill(d, embeds, S, hidden);
+}
+
+/* decoder_prefill_logits (decoder.rs:649-681): prefill, the final RMSNorm of
+ * every row, then the bf16 LM head (lm_bf16 [out_dim][H]; NULL: the tied
+ * embedding, out_dim = vocab) through linear_nobias_bf16 (f32 sgemm) */
+void or_decoder_prefill_logits(or_decoder *d, const float *embeds, int64_t S, const uint16_t *lm_bf16,
+                               int64_t out_dim, float *logits) {
+    const int64_t H = d->c.hidden;
+    float *x = (float *)malloc(sizeof(float) * S * H), *xn = (float *)malloc(sizeof(float) * S * H);
+    dec_prefill(d, embeds, S, x);
+    or_rms_norm(xn, x, d->w.norm, S, H, d->c.eps);
+    float *wf = (float *)malloc(sizeof(float) * out_dim * H);
+    or_bf16_to_f32(wf, lm_bf16 ? lm_bf16 : d->w.embed, out_dim * H);
+    or_linear(logits, xn, wf, NULL, S, H, out_dim);
+    free(wf);
+    free(x);
+    free(xn);
+}
+
+/* forced_align's timestamp readout (align.rs:312-321): per row, a scan from
+ * column 0 that moves on only for a strictly greater value */
+void or_argmax_f32_rows(const float *x, int64_t rows, int64_t cols, int32_t *idx) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float *row = x + r * cols;
+        int64_t best = 0;
+        float best_val = row[0];
+        for (int64_t j = 1; j < cols; j++)
+            if (row[j] > best_val) {
+                best_val = row[j];
+                best = j;
+            }
+        idx[r] = (int32_t)best;
+    }
+}
+
+static void dec_prefill(or_decoder *d, const float *embeds, int64_t S, float *hidden_out) {
     const or_dec_config *c = &d->c;
     int64_t H = c->hidden, hd = c->head_dim, qd = (int64_t)c->n_heads * hd;
     int64_t kvd = (int64_t)c->n_kv_heads * hd, I = c->intermediate;
@@ -850,6 +890,7 @@ void or_decoder_prefill(or_decoder *d, const float *embeds, int64_t S) {
         for (int64_t i = 0; i < S * H; i++) x[i] += proj[i];
     }
     d->len = start + S;
+    if (hidden_out) memcpy(hidden_out, x, sizeof(float) * S * H);
     free(x); free(xn); free(q); free(k); free(v); free(att); free(proj); free(gu); free(g);
 }
 

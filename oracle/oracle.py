@@ -58,6 +58,7 @@ _SIGS = {
     "or_linear_int8_swiglu": (None, [P, P, P, P, I64, I64]),
     "or_linear_int8_addto": (None, [P, P, P, P, I64, I64]),
     "or_argmax_int8": (I64, [P, P, P, I64, I64, P, P]),
+    "or_argmax_f32_rows": (None, [P, I64, I64, P]),
     "or_hsum8": (F32, [P]),
     "or_dot_f32": (F32, [P, P, I64]),
     "or_rms_norm": (None, [P, P, P, I64, I64, F32]),
@@ -84,6 +85,8 @@ _SIGS = {
     "or_decoder_set_len": (None, [P, I64]),
     "or_decoder_len": (I64, [P]),
     "or_decoder_prefill": (None, [P, P, I64]),
+    "or_decoder_prefill_logits": (None, [P, P, I64, P, I64, P]),
+    "or_decoder_prefill_hidden": (None, [P, P, I64, P]),
     "or_decoder_forward": (I32, [P, P, P, P, P]),
     "or_embed_token": (None, [P, I32, P]),
     "or_decoder_kv": (P, [P, C.c_int]),
@@ -193,6 +196,14 @@ def argmax_int8(x, w, ws):
     bv, sv = C.c_float(), C.c_float()
     i = lib().or_argmax_int8(_p(f32(x)), _p(w), _p(f32(ws)), k, n, C.byref(bv), C.byref(sv))
     return int(i), bv.value, sv.value
+
+
+def argmax_f32_rows(x):
+    """align.rs:312-321 per-row argmax of x [rows, cols]."""
+    x = f32(np.atleast_2d(x))
+    out = np.empty(x.shape[0], np.int32)
+    lib().or_argmax_f32_rows(_p(x), x.shape[0], x.shape[1], _p(out))
+    return out
 
 
 def rms_norm(x, w, eps):
@@ -345,6 +356,26 @@ class OracleDecoder:
     def prefill(self, embeds):
         e = f32(embeds)
         lib().or_decoder_prefill(self.d, _p(e), e.shape[0])
+
+    def prefill_hidden(self, embeds):
+        """decoder_prefill, returning the last layer's rows (pref_x) [seq, hidden]."""
+        e = f32(embeds)
+        out = np.empty((e.shape[0], self.cfg["hidden"]), np.float32)
+        lib().or_decoder_prefill_hidden(self.d, _p(e), e.shape[0], _p(out))
+        return out
+
+    def prefill_logits(self, embeds, lm_bf16=None):
+        """decoder_prefill_logits (decoder.rs:649-681): [seq, out_dim] f32."""
+        e = f32(embeds)
+        if lm_bf16 is None:
+            out_dim = self.cfg["vocab"]
+            lm = None
+        else:
+            lm = np.ascontiguousarray(lm_bf16, np.uint16)
+            out_dim = lm.shape[0]
+        out = np.empty((e.shape[0], out_dim), np.float32)
+        lib().or_decoder_prefill_logits(self.d, _p(e), e.shape[0], None if lm is None else _p(lm), out_dim, _p(out))
+        return out
 
     def forward_logits(self, embed):
         """(token, best logit, second-best logit)."""

@@ -149,6 +149,10 @@ const int8_t *or_decoder_packed(const or_decoder *d, int layer, int which, const
 void or_decoder_set_len(or_decoder *d, int64_t len);
 int64_t or_decoder_len(const or_decoder *d);
 void or_decoder_prefill(or_decoder *d, const float *embeds, int64_t seq_len);
+void or_decoder_prefill_hidden(or_decoder *d, const float *embeds, int64_t seq_len, float *hidden);
+void or_decoder_prefill_logits(or_decoder *d, const float *embeds, int64_t seq_len, const uint16_t *lm_bf16,
+                               int64_t out_dim, float *logits);
+void or_argmax_f32_rows(const float *x, int64_t rows, int64_t cols, int32_t *idx);
 int32_t or_decoder_forward(or_decoder *d, const float *embed, float *best_val, float *second_val,
                            float *hidden_out);
 void or_embed_token(const or_decoder *d, int32_t token, float *out);

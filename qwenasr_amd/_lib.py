@@ -135,6 +135,11 @@ _SIGS = {
     "qasr_hip_stream_tokens": (C.c_int, [P, P, I64, C.POINTER(I64)]),
     "qasr_hip_stream_audio_cursor": (I64, [P]),
     "qasr_hip_stream_stats": (C.c_int, [P, P]),
+    "qasr_hip_decoder_set_lm_head": (C.c_int, [P, P, I64]),
+    "qasr_hip_decoder_logits_dim": (I64, [P]),
+    "qasr_hip_decoder_prefill_logits": (C.c_int, [P, P, I64, P]),
+    "qasr_hip_decoder_prefill_argmax": (C.c_int, [P, P, I64, P, I64, P]),
+    "qasr_hip_argmax_f32_rows": (C.c_int, [P, P, I64, I64, I64, P]),
     "qasr_hip_batch_create": (C.c_int, [P, I32, I64, I64, C.POINTER(P)]),
     "qasr_hip_batch_free": (None, [P]),
     "qasr_hip_batch_prefill": (C.c_int, [P, I32, P, I64]),

@@ -35,7 +35,7 @@ final push; per-push wall time (host clock around the synchronous push, audio
 upload included), total time and realtime factor, committed tokens and the
 driver's statistics, with the QwenCtx stream defaults and with 3-token
 bursts (rollback 1).  Token parity of the
-driver against the oracle restatement is test_gpu_stream.py's.
+driver against the CPU restatement of the reference is tested in test_gpu_stream.py.
 
 Each configuration prints one JSON line (stdout); progress goes to stderr.
 """

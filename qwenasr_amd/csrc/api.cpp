@@ -5,6 +5,7 @@
 #include "model.h"
 
 #include <cmath>
+#include <climits>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -294,6 +295,15 @@ extern "C" int qasr_hip_rmsnorm_argmax_int8(qasr_hip *h, const float *x, const f
                                             int64_t in_dim, int64_t out_dim, int32_t *idx) {
     if (!norm_w) return qasr_fail(QASR_ERR_INVALID, "norm_w is null");
     return argmax_impl(h, x, norm_w, eps, w, ws, in_dim, out_dim, idx);
+}
+
+extern "C" int qasr_hip_argmax_f32_rows(qasr_hip *h, const float *x, int64_t ld, int64_t rows, int64_t cols,
+                                        int32_t *idx) {
+    CHECK_H(h);
+    if (!x || !idx || rows < 0 || cols <= 0 || ld < cols || rows > INT32_MAX)
+        return qasr_fail(QASR_ERR_INVALID, "argmax_f32_rows: bad arguments");
+    LAUNCHCHK(launch_argmax_f32_rows(x, ld, rows, cols, idx, h->stream), "argmax_f32_rows");
+    return QASR_OK;
 }
 
 extern "C" int qasr_hip_rms_norm(qasr_hip *h, float *out, const float *x, const float *w, int64_t seq,

@@ -198,6 +198,7 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
     (void)hipStreamSynchronize(d->h->stream);
     for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
     decoder_free_prefill(d);
+    if (d->lm_bf16) (void)hipFree(d->lm_bf16);
     for (void *p : d->allocs) (void)hipFree(p);
     delete d;
 }

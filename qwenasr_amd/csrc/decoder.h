@@ -28,6 +28,8 @@ struct qasr_decoder {
     uint16_t *embed = nullptr, *stage = nullptr;
     int8_t *lm = nullptr;
     float *lm_s = nullptr, *norm = nullptr;
+    uint16_t *lm_bf16 = nullptr;                // separate bf16 LM head for prefill logits (nullptr: tied embedding)
+    int64_t lm_rows = 0;
     void *kc = nullptr, *vc = nullptr;          // [layer][kv_head][max_seq][hd]
     int64_t kv_layer_stride = 0;                // prefill's cache elements between layers (0: kv_heads * max_seq * hd)
     float *rc = nullptr, *rs = nullptr;         // RoPE [max_seq][hd]

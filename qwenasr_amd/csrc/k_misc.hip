@@ -1,5 +1,6 @@
 // Row-wise and element-wise kernels of the prefill, the audio encoder and the
 // mel front end, plus the multi-row (prefill / encoder-window) attention.
+#include <climits>
 #include <cstdlib>
 
 #include "kernels.h"
@@ -217,6 +218,61 @@ __global__ __launch_bounds__(256) void k_row_diff(const float *__restrict__ a, c
 hipError_t launch_row_diff(const float *a, const float *b, int64_t rows, int64_t H, int *flags, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(k_row_diff, dim3((unsigned)rows), dim3(256), 0, st, a, b, H, flags);
+    return hipGetLastError();
+}
+
+// idx[r] = the aligner's per-row argmax of x[r] (align.rs:312-321): a left
+// scan that starts at column 0 and moves on only for a strictly greater value,
+// i.e. the lowest column holding the maximum of the non-NaN values, and 0 when
+// column 0 is NaN (nothing compares greater than it).  A lane scans a strided
+// column set in increasing order; pairs merge by value, then lowest column.
+__device__ inline void argmax_pick(float &v, int &i, float ov, int oi) {
+    if (oi == INT_MAX) return;
+    if (i == INT_MAX || ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_f32_rows(const float *__restrict__ x, int64_t ld, int64_t cols,
+                                                         int32_t *__restrict__ idx) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const float *row = x + blockIdx.x * ld;
+    float v = 0.0f;
+    int i = INT_MAX;
+    for (int64_t c = threadIdx.x; c < cols; c += 256) {
+        const float y = row[c];
+        if (y == y && (i == INT_MAX || y > v)) { v = y; i = (int)c; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) argmax_pick(v, i, __shfl_xor(v, o), __shfl_xor(i, o));
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) { sv[w] = v; si[w] = i; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int k = 1; k < 4; k++) argmax_pick(v, i, sv[k], si[k]);
+        const float c0 = row[0];
+        idx[blockIdx.x] = (c0 != c0 || i == INT_MAX) ? 0 : i;
+    }
+}
+
+hipError_t launch_argmax_f32_rows(const float *x, int64_t ld, int64_t rows, int64_t cols, int32_t *idx,
+                                  hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_argmax_f32_rows, dim3((unsigned)rows), dim3(256), 0, st, x, ld, cols, idx);
+    return hipGetLastError();
+}
+
+// dst[k] = src[rows[k]] for k < n, rows of H floats
+__global__ __launch_bounds__(256) void k_gather_rows(float *__restrict__ dst, const float *__restrict__ src,
+                                                     const int32_t *__restrict__ rows, int64_t H) {
+    const float *s = src + (int64_t)rows[blockIdx.x] * H;
+    float *d = dst + (int64_t)blockIdx.x * H;
+    for (int64_t c = threadIdx.x; c < H; c += 256) d[c] = s[c];
+}
+
+hipError_t launch_gather_rows(float *dst, const float *src, const int32_t *rows, int64_t n, int64_t H,
+                              hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_gather_rows, dim3((unsigned)n), dim3(256), 0, st, dst, src, rows, H);
     return hipGetLastError();
 }
 

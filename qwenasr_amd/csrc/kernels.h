@@ -207,6 +207,11 @@ hipError_t launch_delay(int us, hipStream_t st);
 hipError_t launch_kv_scatter(const float *qkv, int64_t qkv_rs, int k_off, int v_off, float *kc, float *vc,
                              int64_t head_stride, int start, int64_t S, int Hkv, hipStream_t st);
 hipError_t launch_row_diff(const float *a, const float *b, int64_t rows, int64_t H, int *flags, hipStream_t st);
+// idx[r] = lowest column of the maximum of row r's non-NaN values (0 when column 0 is NaN)
+hipError_t launch_argmax_f32_rows(const float *x, int64_t ld, int64_t rows, int64_t cols, int32_t *idx,
+                                  hipStream_t st);
+hipError_t launch_gather_rows(float *dst, const float *src, const int32_t *rows, int64_t n, int64_t H,
+                              hipStream_t st);
 hipError_t launch_build_prompt(float *out, const uint16_t *embed, const int *toks, int n_head, const float *mid,
                                int n_mid, int n_tail, int H, hipStream_t st);
 hipError_t launch_mel_frames(float *fr, const float *x, int64_t ns, const float *window, int nf, hipStream_t st);

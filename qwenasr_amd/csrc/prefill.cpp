@@ -120,3 +120,100 @@ int decoder_prefill_hidden(qasr_decoder *d, float *host_out, int64_t seq_len) {
     HIPCHK(hipStreamSynchronize(d->h->stream));
     return QASR_OK;
 }
+
+// The bf16 LM head decoder_prefill_logits projects onto (decoder.lm_head_bf16,
+// decoder.rs:143, 671): w [out_dim][hidden] host bf16, copied to the device;
+// null restores the tied embedding.
+extern "C" int qasr_hip_decoder_set_lm_head(qasr_decoder *d, const uint16_t *w, int64_t out_dim) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    if (d->lm_bf16) (void)hipFree(d->lm_bf16);
+    d->lm_bf16 = nullptr;
+    d->lm_rows = 0;
+    if (!w) return QASR_OK;
+    if (out_dim <= 0) return qasr_fail(QASR_ERR_INVALID, "set_lm_head: out_dim must be positive");
+    const size_t bytes = sizeof(uint16_t) * out_dim * d->c.hidden;
+    if (hipMalloc(&d->lm_bf16, bytes) != hipSuccess) {
+        d->lm_bf16 = nullptr;
+        return qasr_fail(QASR_ERR_NOMEM, "set_lm_head: device allocation failed");
+    }
+    HIPCHK(hipMemcpy(d->lm_bf16, w, bytes, hipMemcpyHostToDevice));
+    d->lm_rows = out_dim;
+    return QASR_OK;
+}
+
+extern "C" int64_t qasr_hip_decoder_logits_dim(const qasr_decoder *d) {
+    return d ? (d->lm_rows ? d->lm_rows : d->c.vocab) : -1;
+}
+
+// decoder_prefill_logits (decoder.rs:649-681) on the device: the prefill,
+// then the final RMSNorm and the bf16 LM head (f32-class MFMA GEMM, as the
+// reference's linear_nobias_bf16 f32 sgemm) over the prefill rows `rows` (host,
+// nullptr: all seq_len rows in order; each row's logits depend on that row
+// alone, so a subset computes exactly those rows).  Downloads the logits
+// [n][out_dim] when `logits` is set and the aligner's per-row argmax
+// (align.rs:312-321) when `idx` is set.
+static int prefill_head_rows(qasr_decoder *d, const float *embeds, int64_t seq_len, const int32_t *rows, int64_t n,
+                             float *logits, int32_t *idx) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (seq_len <= 0 || !embeds) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: bad arguments");
+    if (d->kv_bf16) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: needs an f32 KV cache");
+    if (d->len + seq_len > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: KV cache capacity exceeded");
+    if (rows)
+        for (int64_t k = 0; k < n; k++)
+            if (rows[k] < 0 || rows[k] >= seq_len) return qasr_fail(QASR_ERR_INVALID, "prefill_argmax: row out of range");
+    const int64_t H = d->c.hidden, out_dim = qasr_hip_decoder_logits_dim(d);
+    if (rows && 2 * (int64_t)d->c.intermediate < H)
+        return qasr_fail(QASR_ERR_INVALID, "prefill_argmax: unsupported shape (intermediate < hidden / 2)");
+    const uint16_t *w = d->lm_bf16 ? d->lm_bf16 : d->embed;
+    TRY(ensure_prefill(d, seq_len));
+    hipStream_t st = d->h->stream;
+    // one device block: logits [n][out_dim], row list [n], argmax [n]
+    const size_t y_bytes = (sizeof(float) * n * out_dim + 255) / 256 * 256;
+    char *buf = nullptr;
+    if (n > 0 && hipMalloc(&buf, y_bytes + 2 * sizeof(int32_t) * n) != hipSuccess)
+        return qasr_fail(QASR_ERR_NOMEM, "prefill_logits: device allocation failed");
+    float *y = reinterpret_cast<float *>(buf);
+    int32_t *rows_dev = reinterpret_cast<int32_t *>(buf + y_bytes), *idx_dev = rows_dev + n;
+    auto body = [&]() -> int {
+        HIPCHK(hipMemcpyAsync(d->pf.xn, embeds, sizeof(float) * seq_len * H, hipMemcpyHostToDevice, st));
+        TRY(decoder_prefill_dev(d, d->pf.xn, seq_len));
+        if (n == 0) return QASR_OK;
+        const float *src = d->pf.x;
+        if (rows) {
+            HIPCHK(hipMemcpyAsync(rows_dev, rows, sizeof(int32_t) * n, hipMemcpyHostToDevice, st));
+            LAUNCHCHK(launch_gather_rows(d->pf.gu, d->pf.x, rows_dev, n, H, st), "logits row gather");
+            src = d->pf.gu;
+        }
+        LAUNCHCHK(launch_rms_norm_rows(d->pf.xn, src, d->norm, n, (int)H, d->c.eps, st), "logits rms_norm");
+        TRY(gemm(d, d->pf.xn, H, w, H, y, out_dim, (int)n, (int)out_dim, (int)H, EPI_NONE));
+        if (logits)
+            HIPCHK(hipMemcpyAsync(logits, y, sizeof(float) * n * out_dim, hipMemcpyDeviceToHost, st));
+        if (idx) {
+            LAUNCHCHK(launch_argmax_f32_rows(y, out_dim, n, out_dim, idx_dev, st), "logits argmax");
+            HIPCHK(hipMemcpyAsync(idx, idx_dev, sizeof(int32_t) * n, hipMemcpyDeviceToHost, st));
+        }
+        return QASR_OK;
+    };
+    int rc = body();
+    const hipError_t e = hipStreamSynchronize(st);
+    if (buf) (void)hipFree(buf);
+    if (rc != QASR_OK) return rc;
+    if (e != hipSuccess) return qasr_fail(QASR_ERR_HIP, "prefill_logits: stream failed");
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_prefill_logits(qasr_decoder *d, const float *embeds, int64_t seq_len,
+                                               float *logits) {
+    if (!logits) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: logits is null");
+    return prefill_head_rows(d, embeds, seq_len, nullptr, seq_len, logits, nullptr);
+}
+
+extern "C" int qasr_hip_decoder_prefill_argmax(qasr_decoder *d, const float *embeds, int64_t seq_len,
+                                               const int32_t *rows, int64_t n_rows, int32_t *idx) {
+    if (n_rows < 0 || (n_rows > 0 && (!rows || !idx)))
+        return qasr_fail(QASR_ERR_INVALID, "prefill_argmax: bad row list");
+    return prefill_head_rows(d, embeds, seq_len, rows, n_rows, nullptr, idx);
+}

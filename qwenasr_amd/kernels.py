@@ -68,6 +68,12 @@ def argmax_matvec_int8(x, w, ws, in_dim, out_dim, out_idx, norm_w=None, eps=1e-6
     return int(out_idx.numpy().reshape(-1)[0])
 
 
+def argmax_f32_rows(x, rows, cols, out_idx, ld=None):
+    """align.rs:312-321 — per-row argmax of device logits x [rows][ld] into out_idx (int32 device [rows])."""
+    check(lib().qasr_hip_argmax_f32_rows(_h(x), x.ptr, cols if ld is None else ld, rows, cols, out_idx.ptr))
+    return out_idx.numpy().reshape(-1)[:rows].copy()
+
+
 def rms_norm(out, x, weight, seq_len, hidden, eps):
     """kernels/mod.rs:1191."""
     check(lib().qasr_hip_rms_norm(_h(x), out.ptr, x.ptr, weight.ptr, seq_len, hidden, eps))

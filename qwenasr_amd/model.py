@@ -51,6 +51,34 @@ class Decoder:
         e = np.ascontiguousarray(embeds, np.float32)
         check(lib().qasr_hip_decoder_prefill(self.d, e.ctypes.data_as(P), e.shape[0]))
 
+    def set_lm_head(self, w_bf16=None):
+        """A separate bf16 LM head [out_dim, hidden] for prefill_logits (None: the tied embedding)."""
+        if w_bf16 is None:
+            check(lib().qasr_hip_decoder_set_lm_head(self.d, None, 0))
+        else:
+            w = np.ascontiguousarray(w_bf16, np.uint16)
+            if w.ndim != 2 or w.shape[1] != self.cfg["hidden"]:
+                raise ValueError(f"LM head must be [out_dim, {self.cfg['hidden']}], got {w.shape}")
+            check(lib().qasr_hip_decoder_set_lm_head(self.d, w.ctypes.data_as(P), w.shape[0]))
+
+    def prefill_logits(self, embeds):
+        """decoder_prefill_logits (decoder.rs:649-681): [seq, out_dim] f32 logits."""
+        e = np.ascontiguousarray(embeds, np.float32)
+        out = np.empty((e.shape[0], int(lib().qasr_hip_decoder_logits_dim(self.d))), np.float32)
+        check(lib().qasr_hip_decoder_prefill_logits(self.d, e.ctypes.data_as(P), e.shape[0],
+                                                    out.ctypes.data_as(P)))
+        return out
+
+    def prefill_argmax(self, embeds, rows):
+        """The aligner's timestamp readout (align.rs:300-321): prefill, then the
+        head's per-row argmax at the prefill rows `rows`."""
+        e = np.ascontiguousarray(embeds, np.float32)
+        r = np.ascontiguousarray(rows, np.int32)
+        out = np.empty(r.shape[0], np.int32)
+        check(lib().qasr_hip_decoder_prefill_argmax(self.d, e.ctypes.data_as(P), e.shape[0], r.ctypes.data_as(P),
+                                                    r.shape[0], out.ctypes.data_as(P)))
+        return out
+
     def forward(self, embed=None, token=0):
         """decoder_forward (decoder.rs:550): returns the greedy token id."""
         out = I32()

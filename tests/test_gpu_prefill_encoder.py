@@ -135,6 +135,88 @@ def test_decoder_prefill_then_decode(dev, orc):
     cpu.close()
 
 
+def test_decoder_prefill_logits(dev, orc):
+    """decoder_prefill_logits (decoder.rs:649-681), the forced aligner's path:
+    every row's logits through the tied embedding and through a separate
+    [5000, hidden] bf16 head (ragged against the GEMM tiles), against the
+    oracle; per-row argmax agrees wherever the oracle's top-2 gap is clear."""
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    w = SynthDecoder(TINY_DEC, seed=1003)
+    r = rng(5)
+    w.norm = (1.0 + 0.5 * r.standard_normal(TINY_DEC["hidden"])).astype(np.float32)
+    gpu = Decoder(dev, w, max_seq=256)
+    S = 50
+    emb = r.normal(0, 0.02, (S, TINY_DEC["hidden"])).astype(np.float32)
+    head = bf16(r.normal(0, 0.02, (5000, TINY_DEC["hidden"])))
+    try:
+        for lm in (None, head):
+            print("prefill logits, head", "tied" if lm is None else lm.shape, flush=True)
+            gpu.set_lm_head(lm)
+            gpu.kv_len = 0
+            got = gpu.prefill_logits(emb)
+            assert gpu.kv_len == S
+            cpu = orc.OracleDecoder(w, max_seq=256)
+            want = cpu.prefill_logits(emb, lm)
+            cpu.close()
+            assert got.shape == want.shape == (S, TINY_DEC["vocab"] if lm is None else 5000)
+            assert nrel(got, want) < 2e-4
+            top2 = np.sort(want, axis=1)[:, -2:]
+            clear = (top2[:, 1] - top2[:, 0]) > 1e-3 * np.abs(top2[:, 1]).max()
+            assert clear.sum() > S // 2
+            assert (got.argmax(1)[clear] == want.argmax(1)[clear]).all()
+        # the aligner's readout: argmax at chosen rows, logits left on the device
+        rows = np.array([S - 1, 0, 7, 7, 31, 49], np.int32)
+        gpu.set_lm_head(head)
+        gpu.kv_len = 0
+        full = gpu.prefill_logits(emb)
+        gpu.kv_len = 0
+        idx = gpu.prefill_argmax(emb, rows)
+        assert gpu.kv_len == S
+        assert (idx == orc.argmax_f32_rows(full[rows])).all()      # same rows, same logits
+        gpu.kv_len = 0
+        assert gpu.prefill_argmax(emb, np.zeros(0, np.int32)).shape == (0,)
+        assert gpu.kv_len == S
+        from qwenasr_amd import QasrError
+        for bad in ([S], [-1]):
+            gpu.kv_len = 0
+            with pytest.raises(QasrError):
+                gpu.prefill_argmax(emb, np.array(bad, np.int32))
+    finally:
+        gpu.set_lm_head(None)
+        gpu.close()
+
+
+def test_argmax_f32_rows(dev, orc):
+    """per-row argmax kernel vs the oracle's restatement of the aligner's scan:
+    the hand-checked cases of the oracle's known answers, full-vocabulary rows
+    with maxima planted in different lanes and waves, and a row stride wider
+    than the columns scanned"""
+    from qwenasr_amd import kernels as Kr
+    from test_oracle_float import ARGMAX_KAT
+    for row, want in ARGMAX_KAT:
+        x = np.array([row], np.float32)
+        idx = dev.empty(1, np.int32)
+        assert Kr.argmax_f32_rows(dev.upload(x), 1, x.shape[1], idx)[0] == want, row
+    r = rng(6)
+    rows, cols = 37, 151936
+    x = r.normal(0, 1, (rows, cols)).astype(np.float32)
+    for k, cs in enumerate(([5, 70000], [257, 1, 151935], [64, 128, 192], [151935, 151934])):
+        x[k, cs] = 9.0
+    x[10, 0] = np.nan
+    x[11, 1::3] = np.nan
+    x[12] = -np.inf
+    x[13, :500] = np.nan
+    x[13, 0] = -1.0
+    want = orc.argmax_f32_rows(x)
+    idx = dev.empty(rows, np.int32)
+    got = Kr.argmax_f32_rows(dev.upload(x), rows, cols, idx)
+    assert (got == want).all(), np.nonzero(got != want)
+    assert list(want[:4]) == [5, 1, 64, 151934] and want[10] == 0 and want[12] == 0
+    got = Kr.argmax_f32_rows(dev.upload(x), rows, 5000, idx, ld=cols)
+    assert (got == orc.argmax_f32_rows(np.ascontiguousarray(x[:, :5000]))).all()
+
+
 def test_mel(dev, orc):
     from qwenasr_amd.model import Encoder
     from qwenasr_amd.synth import ENC_0_6B, SynthEncoder, audio

@@ -313,3 +313,62 @@ def test_mel_sine_peak(orc):
     fb = _slaney_mel_filters()
     peak_bin = int(np.argmax(fb[:, int(round(1000 / 40))]))
     assert (np.argmax(got[:, 5:-5], axis=0) == peak_bin).all()
+
+
+# ---- forced-aligner logits (decoder_prefill_logits, decoder.rs:649-681) ------
+def test_prefill_logits_composition(orc):
+    """prefill, then the final RMSNorm of every row and the bf16 LM head:
+    against float64 RMSNorm + matmul over the oracle's own prefill rows, for a
+    separate [5000, H] head and for the tied embedding; the prefill itself
+    leaves the same KV length either way."""
+    from qwenasr_amd.synth import SynthDecoder
+    from conftest import bf16, bf16f
+    cfg = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, intermediate=512, vocab=1024,
+               eps=1e-6, theta=1e6)
+    w = SynthDecoder(cfg, seed=77)
+    r = rng(78)
+    w.norm = (1.0 + 0.5 * r.standard_normal(cfg["hidden"])).astype(np.float32)   # a gain that matters
+    e = r.normal(0, 1, (37, cfg["hidden"])).astype(np.float32)
+    lm = bf16(r.normal(0, 0.02, (5000, cfg["hidden"])))
+    gain = np.asarray(w.norm, np.float64)
+    for head in (lm, None):
+        d1 = orc.OracleDecoder(w, max_seq=128)
+        d2 = orc.OracleDecoder(w, max_seq=128)
+        hid = d1.prefill_hidden(e).astype(np.float64)
+        got = d2.prefill_logits(e, head)
+        assert d1.kv_len == d2.kv_len == e.shape[0]
+        xn = hid / np.sqrt((hid * hid).mean(axis=1, keepdims=True) + cfg["eps"]) * gain
+        wt = bf16f(head if head is not None else w.embed).astype(np.float64)
+        ref = xn @ wt.T
+        assert got.shape == ref.shape
+        assert rel(got, ref) < 1e-5
+        d1.close()
+        d2.close()
+
+
+ARGMAX_KAT = [  # (row, index the aligner's scan picks, align.rs:312-321)
+    ([1.0, 3.0, 3.0, 2.0], 1),                       # first of equal maxima
+    ([2.0, 2.0, 2.0], 0),
+    ([np.nan, 5.0, 7.0], 0),                         # nothing compares greater than a NaN start
+    ([1.0, np.nan, 7.0, np.nan], 2),                 # later NaNs are skipped
+    ([-np.inf, -np.inf], 0),
+    ([-np.inf, np.nan, -np.inf, -1.0], 3),
+    ([0.0, -0.0], 0), ([-0.0, 0.0], 0),              # signed zeros compare equal
+    ([np.inf, np.inf, 1.0], 0),
+    ([-5.0], 0),
+]
+
+
+def test_argmax_f32_rows_kat(orc):
+    """the aligner's per-row argmax: hand-derived answers of the scan for ties,
+    NaN, infinities and signed zeros, and numpy's first-occurrence argmax on
+    NaN-free rows (ties planted across the row)"""
+    for row, want in ARGMAX_KAT:
+        assert orc.argmax_f32_rows(np.array([row], np.float32))[0] == want, row
+    r = rng(79)
+    x = r.normal(0, 1, (20, 5000)).astype(np.float32)
+    x[3, 4999] = x[3].max() + 1
+    x[4, [10, 2000, 4000]] = x[4].max() + 1
+    x[5] = 0.25
+    assert (orc.argmax_f32_rows(x) == np.argmax(x, axis=1)).all()
+    assert orc.argmax_f32_rows(x)[4] == 10 and orc.argmax_f32_rows(x)[5] == 0
