@@ -46,3 +46,27 @@ def test_synth_and_oracle_load():
     d = synth.normal_bf16((4, 1 << 21), 2, "big")
     synth._synth().qs_set_threads(8)
     assert (c == d).all()                      # block streams: thread count does not matter
+
+
+def build_c_smoke(out_dir):
+    """gcc, C99 pedantic with warnings as errors, against include/qasr_hip.h
+    and the two built libraries: the header is plain C and the library links
+    from C (the c_api.rs / jni_api.rs / Dart FFI pass-through callers)."""
+    import subprocess
+    lib_dir = os.path.join(ROOT, "qwenasr_amd")
+    exe = os.path.join(str(out_dir), "c_abi_smoke")
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+                    "-I", os.path.join(ROOT, "include"), os.path.join(ROOT, "tests", "c_abi_smoke.c"),
+                    "-L", lib_dir, "-lqasr_hip", "-lqasr_synth", "-Wl,-rpath," + lib_dir, "-o", exe],
+                   check=True, capture_output=True, text=True)
+    return exe
+
+
+def test_c_smoke_builds_and_header_is_c_and_cxx(tmp_path):
+    import subprocess
+    assert os.access(build_c_smoke(tmp_path), os.X_OK)
+    hdr = os.path.join(ROOT, "include", "qasr_hip.h")
+    for cmd in (["gcc", "-std=c99", "-pedantic", "-Werror", "-Wall", "-x", "c", "-fsyntax-only", hdr],
+                ["g++", "-std=c++17", "-pedantic", "-Werror", "-Wall", "-x", "c++", "-fsyntax-only", hdr]):
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
