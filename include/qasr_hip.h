@@ -160,6 +160,36 @@ int qasr_hip_bidirectional_attention(qasr_hip *h, float *out, const float *q, co
                                      const float *v, int64_t seq, int64_t n_heads, int64_t head_dim,
                                      float scale, int64_t window_tokens);
 
+/* ---- checkpoints: safetensors (safetensors.rs) ---------------------------
+ * A read-only mapping of one checkpoint file or of a directory's shards.
+ * Tensor data stays in the mapping (no host copy); the *_load_st loaders
+ * stream it through pinned staging buffers into HBM and pack on the GPU.
+ * Free the qasr_st after the loads that read it. */
+typedef struct qasr_st qasr_st;
+#define QASR_ST_UNKNOWN 0
+#define QASR_ST_F32 1
+#define QASR_ST_F16 2
+#define QASR_ST_BF16 3
+#define QASR_ST_I32 4
+#define QASR_ST_I64 5
+#define QASR_ST_BOOL 6
+#define QASR_ST_MAX_DIMS 8
+/* MultiSafetensors::open (safetensors.rs:212-250): <dir>/model.safetensors
+ * when it opens, else every <dir>/model-*.safetensors in byte order of names */
+int qasr_hip_st_open(const char *model_dir, qasr_st **out);
+/* SafetensorsFile::open (safetensors.rs:73-140); headers are validated (UTF-8
+ * JSON, offsets inside the data section and consistent with dtype x shape) */
+int qasr_hip_st_open_file(const char *path, qasr_st **out);
+void qasr_hip_st_free(qasr_st *st);
+int64_t qasr_hip_st_count(const qasr_st *st);           /* distinct tensor names */
+int64_t qasr_hip_st_shards(const qasr_st *st);
+const char *qasr_hip_st_name(const qasr_st *st, int64_t i);   /* shard order, then header order */
+/* MultiSafetensors::find (safetensors.rs:254-262): the first shard holding
+ * name; dtype QASR_ST_*, shape [QASR_ST_MAX_DIMS], data points into the
+ * mapping; each output pointer may be null.  QASR_ERR_INVALID when absent. */
+int qasr_hip_st_find(const qasr_st *st, const char *name, int *dtype, int *ndim, int64_t *shape,
+                     const void **data, int64_t *bytes);
+
 /* ---- model level: the Qwen3 decoder (decoder.rs) ------------------------ */
 typedef struct {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, intermediate, vocab;
@@ -185,6 +215,13 @@ typedef struct qasr_decoder qasr_decoder;
  * table (decoder.rs:301-338, computed on the host with libm and uploaded). */
 int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
                           int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
+/* Decoder::load (decoder.rs:70-167) from a checkpoint: the reference's tensor
+ * names; matrices BF16 (shapes checked against cfg), norms F32 or BF16.  A
+ * thinker.lm_head.weight with vocab rows is packed as the int8 decode head;
+ * any thinker.lm_head.weight also becomes the prefill-logits head (as
+ * qasr_hip_decoder_set_lm_head). */
+int qasr_hip_decoder_load_st(qasr_hip *h, const qasr_st *st, const qasr_dec_config *cfg, int round_mode,
+                             int64_t max_seq, int kv_bf16, qasr_decoder **out);
 void qasr_hip_decoder_free(qasr_decoder *d);
 /* decoder_prefill (decoder.rs:455-547): host f32 embeddings [seq_len, hidden] */
 int qasr_hip_decoder_prefill(qasr_decoder *d, const float *embeds, int64_t seq_len);
@@ -272,6 +309,9 @@ typedef struct qasr_encoder qasr_encoder;
 /* Encoder::load (encoder.rs:123-182) plus the mel tables (audio.rs:225-330) */
 int qasr_hip_encoder_load(qasr_hip *h, const qasr_enc_config *cfg, const qasr_enc_weights *w,
                           qasr_encoder **out);
+/* Encoder::load (encoder.rs:123-182) from a checkpoint: weight matrices (the
+ * convolutions included) BF16, biases and norms F32 or BF16 */
+int qasr_hip_encoder_load_st(qasr_hip *h, const qasr_st *st, const qasr_enc_config *cfg, qasr_encoder **out);
 void qasr_hip_encoder_free(qasr_encoder *e);
 int64_t qasr_hip_encoder_tokens(const qasr_encoder *e, int64_t mel_frames);
 /* mel_spectrogram (audio.rs:273): host samples -> host mel [128][frames]

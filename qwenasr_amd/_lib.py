@@ -106,7 +106,16 @@ _SIGS = {
     "qasr_hip_causal_attention_bf16kv": (C.c_int, [P, P, P, P, P, I64, I64, I64, I64, I64, F32, I64]),
     "qasr_hip_decoder_load": (C.c_int, [P, C.POINTER(DecConfig), C.POINTER(DecWeights), C.c_int,
                                         I64, C.c_int, C.POINTER(P)]),
+    "qasr_hip_decoder_load_st": (C.c_int, [P, P, C.POINTER(DecConfig), C.c_int, I64, C.c_int, C.POINTER(P)]),
     "qasr_hip_decoder_free": (None, [P]),
+    "qasr_hip_st_open": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+    "qasr_hip_st_open_file": (C.c_int, [C.c_char_p, C.POINTER(P)]),
+    "qasr_hip_st_free": (None, [P]),
+    "qasr_hip_st_count": (I64, [P]),
+    "qasr_hip_st_shards": (I64, [P]),
+    "qasr_hip_st_name": (C.c_char_p, [P, I64]),
+    "qasr_hip_st_find": (C.c_int, [P, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(I64),
+                                   C.POINTER(P), C.POINTER(I64)]),
     "qasr_hip_decoder_prefill": (C.c_int, [P, P, I64]),
     "qasr_hip_decoder_forward": (C.c_int, [P, P, I32, C.POINTER(I32)]),
     "qasr_hip_decoder_generate": (C.c_int, [P, P, I32, I32, P]),
@@ -122,6 +131,7 @@ _SIGS = {
     "qasr_hip_layer_norm": (C.c_int, [P, P, P, P, P, I64, I64, F32]),
     "qasr_hip_bidirectional_attention": (C.c_int, [P, P, P, P, P, I64, I64, I64, F32, I64]),
     "qasr_hip_encoder_load": (C.c_int, [P, C.POINTER(EncConfig), C.POINTER(EncWeights), C.POINTER(P)]),
+    "qasr_hip_encoder_load_st": (C.c_int, [P, P, C.POINTER(EncConfig), C.POINTER(P)]),
     "qasr_hip_encoder_free": (None, [P]),
     "qasr_hip_encoder_tokens": (I64, [P, I64]),
     "qasr_hip_mel": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),

@@ -4,6 +4,7 @@
     python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
     python -m qwenasr_amd.bench_configs config4 [n_streams] [steps] [attn_splits]
     python -m qwenasr_amd.bench_configs stream [seconds] [chunk_sec]
+    python -m qwenasr_amd.bench_configs load [reps]
 
 config1: the prefill / audio-encoder int8 x bf16 GEMMs at M = 375 (also 390,
 404), the seven 0.6B projections and the LM head, seeded N(0,0.02) weights
@@ -36,6 +37,13 @@ upload included), total time and realtime factor, committed tokens and the
 driver's statistics, with the QwenCtx stream defaults and with 3-token
 bursts (rollback 1).  Token parity of the
 driver against the CPU restatement of the reference is tested in test_gpu_stream.py.
+
+load: Decoder::load / Encoder::load of the config-2 model (0.6B, seeds 1002)
+from a 2-shard safetensors checkpoint written with the safetensors library
+under $TMPDIR (page cache warm: the files were just written), against the
+load from host arrays: wall time per load (host clock, synchronised), and
+the bf16 bytes moved per second.  Both paths upload through pinned staging
+buffers and pack int8 on the GPU.
 
 Each configuration prints one JSON line (stdout); progress goes to stderr.
 """
@@ -293,6 +301,68 @@ def stream(seconds=30.0, chunk_sec=2.0):
     dev.close()
 
 
+def load(reps=3):
+    import os
+    import shutil
+    import tempfile
+    from .model import Checkpoint
+    from .synth import decoder_tensors, encoder_tensors, write_checkpoint
+    dev = Device(0)
+    wd = SynthDecoder(DEC_0_6B, seed=1002)
+    we = SynthEncoder(ENC_0_6B, seed=1002)
+    tens = decoder_tensors(wd)
+    tens.update(encoder_tensors(we))
+    d = tempfile.mkdtemp(prefix="qasr_ckpt_")
+    try:
+        t0 = time.perf_counter()
+        write_checkpoint(d, tens, shards=2)
+        size = sum(os.path.getsize(os.path.join(d, f)) for f in os.listdir(d))
+        log(f"[load] checkpoint written: {size / 1e9:.3f} GB in {time.perf_counter() - t0:.1f}s")
+        dec_bytes = sum(a.nbytes for n, (a, _) in tens.items() if n.startswith("thinker.model."))
+        enc_bytes = sum(a.nbytes for n, (a, _) in tens.items() if n.startswith("thinker.audio_tower."))
+        rows = {"pointer": [], "checkpoint": []}
+        for rep in range(reps + 1):              # the first round warms the allocator and the page cache
+            t0 = time.perf_counter()
+            dec = Decoder(dev, wd, max_seq=2048)
+            dev.sync()
+            t1 = time.perf_counter()
+            enc = Encoder(dev, we)
+            dev.sync()
+            t2 = time.perf_counter()
+            dec.close()
+            enc.close()
+            t3 = time.perf_counter()
+            ck = Checkpoint(d)
+            t4 = time.perf_counter()
+            dec = Decoder.from_checkpoint(dev, ck, DEC_0_6B, max_seq=2048)
+            dev.sync()
+            t5 = time.perf_counter()
+            enc = Encoder.from_checkpoint(dev, ck, ENC_0_6B)
+            dev.sync()
+            t6 = time.perf_counter()
+            ck.close()
+            dec.close()
+            enc.close()
+            if rep:
+                rows["pointer"].append((t1 - t0, t2 - t1, 0.0))
+                rows["checkpoint"].append((t5 - t4, t6 - t5, t4 - t3))
+            log(f"[load] rep {rep}: host arrays decoder {1e3 * (t1 - t0):.1f} ms encoder {1e3 * (t2 - t1):.1f} ms; "
+                f"checkpoint open {1e3 * (t4 - t3):.2f} ms decoder {1e3 * (t5 - t4):.1f} ms "
+                f"encoder {1e3 * (t6 - t5):.1f} ms")
+        res = {}
+        for k, v in rows.items():
+            a = np.array(v)
+            dms, ems, oms = (1e3 * a.mean(axis=0)).tolist()
+            res[k] = {"decoder_ms": round(dms, 1), "encoder_ms": round(ems, 1), "open_ms": round(oms, 2),
+                      "decoder_GBps": round(dec_bytes / dms / 1e6, 1), "encoder_GBps": round(enc_bytes / ems / 1e6, 1)}
+        print(json.dumps({"config": "Decoder::load + Encoder::load, Qwen3-ASR-0.6B bf16 weights "
+                                    f"({dec_bytes / 1e9:.3f} + {enc_bytes / 1e9:.3f} GB), int8 packing on the GPU",
+                          "checkpoint": "2 safetensors shards, page cache warm", "reps": reps, "results": res}))
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+        dev.close()
+
+
 if __name__ == "__main__":
     what = sys.argv[1] if len(sys.argv) > 1 else "config3"
     if what == "config1":
@@ -304,5 +374,7 @@ if __name__ == "__main__":
                 int(sys.argv[4]) if len(sys.argv) > 4 else -1)
     elif what == "stream":
         stream(float(sys.argv[2]) if len(sys.argv) > 2 else 30.0, float(sys.argv[3]) if len(sys.argv) > 3 else 2.0)
+    elif what == "load":
+        load(int(sys.argv[2]) if len(sys.argv) > 2 else 3)
     else:
         raise SystemExit(f"unknown configuration {what!r}")

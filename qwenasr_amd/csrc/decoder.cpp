@@ -2,6 +2,7 @@
 // at load, an HBM-resident KV cache, and a decode step of 5 fused kernels per
 // layer plus the LM-head argmax, replayed from a captured HIP graph.
 #include "decoder.h"
+#include "upload.h"
 
 #include <cmath>
 #include <cstdlib>
@@ -35,26 +36,21 @@ static int upload(qasr_decoder *d, void *dst, const void *src, size_t bytes) {
     return QASR_OK;
 }
 
-// upload bf16 [n, k] and pack it to int8 + scales on the device
-static int upload_pack(qasr_decoder *d, const uint16_t *host, int64_t n, int64_t k, uint16_t **bf,
-                       int8_t **q, float **s, bool keep_bf16) {
-    uint16_t *tmp = nullptr;
-    if (keep_bf16) {
-        TRY(dalloc(d, bf, n * k));
-        tmp = *bf;
-    } else {
-        tmp = d->stage;
-    }
-    TRY(upload(d, tmp, host, sizeof(uint16_t) * n * k));
+// pack the device bf16 matrix bf [n, k] to int8 + scales on the device
+static int pack(qasr_decoder *d, const uint16_t *bf, int64_t n, int64_t k, int8_t **q, float **s) {
     TRY(dalloc(d, q, n * k));
     TRY(dalloc(d, s, n));
-    LAUNCHCHK(launch_pack_int8(tmp, n, (int)k, d->round_mode, *q, *s, d->h->stream), "decoder pack");
-    if (!keep_bf16) HIPCHK(hipStreamSynchronize(d->h->stream));   // the stage buffer is reused
+    LAUNCHCHK(launch_pack_int8(bf, n, (int)k, d->round_mode, *q, *s, d->h->stream), "decoder pack");
     return QASR_OK;
 }
 
 extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
                                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
+    return decoder_load_impl(h, cfg, w, nullptr, round_mode, max_seq, kv_bf16, out);
+}
+
+int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w, const uint16_t *lm_head,
+                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
     CHECK_H(h);
     if (!cfg || !w || !out || !w->embed || !w->norm || !w->layers)
         return qasr_fail(QASR_ERR_INVALID, "decoder_load: null argument");
@@ -89,7 +85,7 @@ extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, co
     // QASR_ATTN_WAVES=4|8: waves per decode-attention block (tuning)
     const char *aw = getenv("QASR_ATTN_WAVES");
     if (aw && (aw[0] == '4' || aw[0] == '8') && aw[1] == 0) d->attn_waves = aw[0] - '0';
-    int rc = decoder_build(d, w);
+    int rc = decoder_build(d, w, lm_head);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
         return rc;
@@ -98,33 +94,38 @@ extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, co
     return QASR_OK;
 }
 
-int decoder_build(qasr_decoder *d, const qasr_dec_weights *w) {
+int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head) {
     const qasr_dec_config &c = d->c;
     const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd;
     const int64_t kvd = (int64_t)c.n_kv_heads * hd, I = c.intermediate, V = c.vocab;
     const int64_t nqkv = qd + 2 * kvd;
-    size_t stage = std::max<size_t>({(size_t)nqkv * H, (size_t)2 * I * H, (size_t)H * qd, (size_t)H * I});
-    TRY(dalloc(d, &d->stage, stage));
-    std::vector<uint16_t> host((size_t)std::max<int64_t>(nqkv * H, 2 * I * H));
+    // every matrix goes host -> HBM through the pinned staging ring (the q|k|v
+    // concatenation and the gate/up interleave are assembled on the way) and
+    // is packed to int8 on the device behind its upload
+    Stager stg(d->h->stream);
+    TRY(stg.init());
+    const size_t B2 = sizeof(uint16_t);
     d->L.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; l++) {
         const qasr_dec_layer &S = w->layers[l];
         DecLayerDev &D = d->L[l];
         // q | k | v concatenated by rows (one fused projection)
-        std::memcpy(host.data(), S.wq, sizeof(uint16_t) * qd * H);
-        std::memcpy(host.data() + qd * H, S.wk, sizeof(uint16_t) * kvd * H);
-        std::memcpy(host.data() + (qd + kvd) * H, S.wv, sizeof(uint16_t) * kvd * H);
-        TRY(upload_pack(d, host.data(), nqkv, H, &D.bqkv, &D.wqkv, &D.sqkv, true));
-        HIPCHK(hipStreamSynchronize(d->h->stream));
-        TRY(upload_pack(d, S.wo, H, qd, &D.bo, &D.wo, &D.so, true));
+        TRY(dalloc(d, &D.bqkv, nqkv * H));
+        TRY(stg.upload(D.bqkv, S.wq, B2 * qd * H));
+        TRY(stg.upload(D.bqkv + qd * H, S.wk, B2 * kvd * H));
+        TRY(stg.upload(D.bqkv + (qd + kvd) * H, S.wv, B2 * kvd * H));
+        TRY(pack(d, D.bqkv, nqkv, H, &D.wqkv, &D.sqkv));
+        TRY(dalloc(d, &D.bo, H * qd));
+        TRY(stg.upload(D.bo, S.wo, B2 * H * qd));
+        TRY(pack(d, D.bo, H, qd, &D.wo, &D.so));
         // gate/up interleaved by rows (decoder.rs:91-104)
-        for (int64_t r = 0; r < I; r++) {
-            std::memcpy(host.data() + 2 * r * H, S.gate + r * H, sizeof(uint16_t) * H);
-            std::memcpy(host.data() + (2 * r + 1) * H, S.up + r * H, sizeof(uint16_t) * H);
-        }
-        TRY(upload_pack(d, host.data(), 2 * I, H, &D.bgu, &D.wgu, &D.sgu, true));
-        HIPCHK(hipStreamSynchronize(d->h->stream));
-        TRY(upload_pack(d, S.down, H, I, &D.bdown, &D.wdown, &D.sdown, true));
+        TRY(dalloc(d, &D.bgu, 2 * I * H));
+        const void *gu[2] = {S.gate, S.up};
+        TRY(stg.upload_rows(D.bgu, gu, 2, I, B2 * H));
+        TRY(pack(d, D.bgu, 2 * I, H, &D.wgu, &D.sgu));
+        TRY(dalloc(d, &D.bdown, H * I));
+        TRY(stg.upload(D.bdown, S.down, B2 * H * I));
+        TRY(pack(d, D.bdown, H, I, &D.wdown, &D.sdown));
         TRY(dalloc(d, &D.q_norm, hd));
         TRY(dalloc(d, &D.k_norm, hd));
         TRY(dalloc(d, &D.in_norm, H));
@@ -134,12 +135,27 @@ int decoder_build(qasr_decoder *d, const qasr_dec_weights *w) {
         TRY(upload(d, D.in_norm, S.input_norm, sizeof(float) * H));
         TRY(upload(d, D.post_norm, S.post_attn_norm, sizeof(float) * H));
     }
-    // embedding table (bf16, kept for lookups) and the int8 LM head packed from it
+    // embedding table (bf16, kept for lookups) and the int8 LM head packed from
+    // it, or from a separate [vocab, hidden] head (decoder.rs:145-157)
     TRY(dalloc(d, &d->embed, V * H));
-    TRY(upload(d, d->embed, w->embed, sizeof(uint16_t) * V * H));
+    TRY(stg.upload(d->embed, w->embed, B2 * V * H));
     TRY(dalloc(d, &d->lm, V * H));
     TRY(dalloc(d, &d->lm_s, V));
-    LAUNCHCHK(launch_pack_int8(d->embed, V, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream), "lm pack");
+    if (lm_head) {
+        uint16_t *tmp = nullptr;
+        if (hipMalloc(&tmp, B2 * V * H) != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "decoder: LM head staging");
+        int rc = stg.upload(tmp, lm_head, B2 * V * H);
+        if (rc == QASR_OK) {
+            hipError_t e = launch_pack_int8(tmp, V, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(d->h->stream);
+            if (e != hipSuccess) rc = qasr_fail(QASR_ERR_HIP, std::string("lm pack: ") + hipGetErrorString(e));
+        }
+        (void)hipFree(tmp);
+        if (rc != QASR_OK) return rc;
+    } else {
+        LAUNCHCHK(launch_pack_int8(d->embed, V, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream), "lm pack");
+    }
+    TRY(stg.finish());
     TRY(dalloc(d, &d->norm, H));
     TRY(upload(d, d->norm, w->norm, sizeof(float) * H));
     // KV cache [layer][kv_head][max_seq][hd]

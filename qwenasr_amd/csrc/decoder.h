@@ -25,7 +25,7 @@ struct qasr_decoder {
     int round_mode = 0, kv_bf16 = 0;
     int64_t max_seq = 0, len = 0;
     std::vector<DecLayerDev> L;
-    uint16_t *embed = nullptr, *stage = nullptr;
+    uint16_t *embed = nullptr;
     int8_t *lm = nullptr;
     float *lm_s = nullptr, *norm = nullptr;
     uint16_t *lm_bf16 = nullptr;                // separate bf16 LM head for prefill logits (nullptr: tied embedding)
@@ -51,7 +51,11 @@ struct qasr_decoder {
     std::vector<void *> allocs;
 };
 
-int decoder_build(qasr_decoder *d, const qasr_dec_weights *w);
+// lm_head (nullable): a separate bf16 [vocab, hidden] host head for the int8 LM head
+int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head);
+// qasr_hip_decoder_load with an optional separate int8 decode head (bf16 [vocab, hidden])
+int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w, const uint16_t *lm_head,
+                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
 // enqueue one decode step; only_kind >= 0 launches only the kernels of that
 // kind (0 norm+qkv, 1 attention, 2 o_proj, 3 norm+gate_up, 4 down, 5 LM head)
 // The step is enqueued for position d->step_pos (the caller advances it).

@@ -7,6 +7,7 @@
 
 #include "decoder.h"
 #include "encoder.h"
+#include "upload.h"
 
 using namespace qasr;
 
@@ -105,42 +106,43 @@ static void mel_tables(std::vector<float> &win, std::vector<float> &ct, std::vec
     }
 }
 
-static std::vector<uint16_t> concat3(const uint16_t *a, const uint16_t *b, const uint16_t *c, size_t n) {
-    std::vector<uint16_t> v(3 * n);
-    std::memcpy(v.data(), a, n * 2);
-    std::memcpy(v.data() + n, b, n * 2);
-    std::memcpy(v.data() + 2 * n, c, n * 2);
-    return v;
+// a weight matrix through the pinned staging ring
+template <typename T>
+static int eupload_big(qasr_encoder *e, Stager &stg, T **p, const T *host, size_t count) {
+    TRY(ealloc(e, p, count));
+    return stg.upload(*p, host, count * sizeof(T));
 }
 
 static int encoder_build(qasr_encoder *e, const qasr_enc_weights *w) {
     const qasr_enc_config &c = e->c;
     const int64_t D = c.d_model, F = c.ffn_dim, C = c.conv_hidden, O = c.output_dim;
     const int h3 = conv_len(conv_len(conv_len(128)));
-    TRY(eupload(e, &e->conv1_w, w->conv1_w, C * 9));
-    TRY(eupload(e, &e->conv2_w, w->conv2_w, C * C * 9));
-    TRY(eupload(e, &e->conv3_w, w->conv3_w, C * C * 9));
+    Stager stg(e->h->stream);
+    TRY(stg.init());
+    TRY(eupload_big(e, stg, &e->conv1_w, w->conv1_w, C * 9));
+    TRY(eupload_big(e, stg, &e->conv2_w, w->conv2_w, C * C * 9));
+    TRY(eupload_big(e, stg, &e->conv3_w, w->conv3_w, C * C * 9));
     TRY(eupload(e, &e->conv1_b, w->conv1_b, C));
     TRY(eupload(e, &e->conv2_b, w->conv2_b, C));
     TRY(eupload(e, &e->conv3_b, w->conv3_b, C));
-    TRY(eupload(e, &e->conv_out_w, w->conv_out_w, D * C * h3));
+    TRY(eupload_big(e, stg, &e->conv_out_w, w->conv_out_w, D * C * h3));
     e->L.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; l++) {
         const qasr_enc_layer &s = w->layers[l];
         EncLayerDev &L = e->L[l];
-        std::vector<uint16_t> qkv = concat3(s.wq, s.wk, s.wv, D * D);
-        std::vector<float> bqkv(3 * D);
-        std::memcpy(bqkv.data(), s.bq, D * 4);
-        std::memcpy(bqkv.data() + D, s.bk, D * 4);
-        std::memcpy(bqkv.data() + 2 * D, s.bv, D * 4);
-        TRY(eupload(e, &L.wqkv, qkv.data(), 3 * D * D));
-        TRY(eupload(e, &L.bqkv, bqkv.data(), 3 * D));
-        HIPCHK(hipStreamSynchronize(e->h->stream));     // host staging vectors go out of scope
-        TRY(eupload(e, &L.wo, s.wo, D * D));
+        TRY(ealloc(e, &L.wqkv, 3 * D * D));
+        TRY(stg.upload(L.wqkv, s.wq, 2 * D * D));
+        TRY(stg.upload(L.wqkv + D * D, s.wk, 2 * D * D));
+        TRY(stg.upload(L.wqkv + 2 * D * D, s.wv, 2 * D * D));
+        TRY(ealloc(e, &L.bqkv, 3 * D));
+        HIPCHK(hipMemcpyAsync(L.bqkv, s.bq, D * 4, hipMemcpyHostToDevice, e->h->stream));
+        HIPCHK(hipMemcpyAsync(L.bqkv + D, s.bk, D * 4, hipMemcpyHostToDevice, e->h->stream));
+        HIPCHK(hipMemcpyAsync(L.bqkv + 2 * D, s.bv, D * 4, hipMemcpyHostToDevice, e->h->stream));
+        TRY(eupload_big(e, stg, &L.wo, s.wo, D * D));
         TRY(eupload(e, &L.bo, s.bo, D));
-        TRY(eupload(e, &L.fc1, s.fc1, F * D));
+        TRY(eupload_big(e, stg, &L.fc1, s.fc1, F * D));
         TRY(eupload(e, &L.b1, s.b1, F));
-        TRY(eupload(e, &L.fc2, s.fc2, D * F));
+        TRY(eupload_big(e, stg, &L.fc2, s.fc2, D * F));
         TRY(eupload(e, &L.b2, s.b2, D));
         TRY(eupload(e, &L.ln1_w, s.ln1_w, D));
         TRY(eupload(e, &L.ln1_b, s.ln1_b, D));
@@ -149,9 +151,9 @@ static int encoder_build(qasr_encoder *e, const qasr_enc_weights *w) {
     }
     TRY(eupload(e, &e->ln_post_w, w->ln_post_w, D));
     TRY(eupload(e, &e->ln_post_b, w->ln_post_b, D));
-    TRY(eupload(e, &e->proj1_w, w->proj1_w, D * D));
+    TRY(eupload_big(e, stg, &e->proj1_w, w->proj1_w, D * D));
     TRY(eupload(e, &e->proj1_b, w->proj1_b, D));
-    TRY(eupload(e, &e->proj2_w, w->proj2_w, O * D));
+    TRY(eupload_big(e, stg, &e->proj2_w, w->proj2_w, O * D));
     TRY(eupload(e, &e->proj2_b, w->proj2_b, O));
     // per-chunk sinusoidal PE (sinusoidal_pe, kernels/mod.rs:1704-1717)
     e->tokens_per_chunk = conv_len(conv_len(conv_len(c.chunk_size)));
@@ -175,6 +177,7 @@ static int encoder_build(qasr_encoder *e, const qasr_enc_weights *w) {
         TRY(eupload(e, &e->filters, filt.data(), filt.size()));
         HIPCHK(hipStreamSynchronize(e->h->stream));
     }
+    TRY(stg.finish());
     return QASR_OK;
 }
 

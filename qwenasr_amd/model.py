@@ -7,6 +7,56 @@ from ._lib import (I64, QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, E
                    EncWeights, I32, P, StreamConfig, check, lib)
 
 
+ST_DTYPES = {0: None, 1: np.float32, 2: np.float16, 3: "bf16", 4: np.int32, 5: np.int64, 6: np.bool_}
+
+
+class Checkpoint:
+    """MultiSafetensors (safetensors.rs:206-272): a read-only mapping of a
+    checkpoint directory (model.safetensors or its model-*.safetensors shards)
+    or, with ``file=True``, of one file.  No GPU needed."""
+
+    def __init__(self, path, file=False):
+        st = P()
+        fn = lib().qasr_hip_st_open_file if file else lib().qasr_hip_st_open
+        check(fn(str(path).encode(), C.byref(st)))
+        self.st = st
+
+    def close(self):
+        if self.st:
+            lib().qasr_hip_st_free(self.st)
+            self.st = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def n_shards(self):
+        return int(lib().qasr_hip_st_shards(self.st))
+
+    def names(self):
+        return [lib().qasr_hip_st_name(self.st, i).decode("utf-8")
+                for i in range(int(lib().qasr_hip_st_count(self.st)))]
+
+    def find(self, name):
+        """(dtype code, shape, host address, bytes) of the first shard holding name."""
+        dt, nd, shape = C.c_int(), C.c_int(), (I64 * 8)()
+        ptr, nbytes = P(), I64()
+        check(lib().qasr_hip_st_find(self.st, name.encode("utf-8"), C.byref(dt), C.byref(nd), shape,
+                                     C.byref(ptr), C.byref(nbytes)))
+        return dt.value, tuple(shape[i] for i in range(nd.value)), ptr.value, nbytes.value
+
+    def array(self, name):
+        """A numpy copy of the tensor (bf16 as uint16)."""
+        dt, shape, ptr, nbytes = self.find(name)
+        raw = np.frombuffer((C.c_char * nbytes).from_address(ptr), np.uint8).copy() if nbytes else \
+            np.empty(0, np.uint8)
+        t = ST_DTYPES[dt]
+        return raw.view(np.uint16 if t == "bf16" else t).reshape(shape) if t is not None else raw
+
+
 class Decoder:
     """Device-resident Qwen3 decoder: Decoder::load + KvCache + decoder_prefill/forward.
 
@@ -26,6 +76,23 @@ class Decoder:
         self.max_seq = max_seq
         self.kv_bf16 = kv_bf16
         dev.adopt(self)
+
+    @classmethod
+    def from_checkpoint(cls, dev, ckpt, cfg, max_seq=2048, round_mode=QASR_ROUND_HALF_AWAY, kv_bf16=False):
+        """Decoder::load (decoder.rs:70-167) from a :class:`Checkpoint`; cfg is the config dict."""
+        self = cls.__new__(cls)
+        self.dev = dev
+        self.cfg = dict(cfg)
+        c = DecConfig(**{k: cfg[k] for k in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim",
+                                            "intermediate", "vocab", "eps", "theta")})
+        d = P()
+        check(lib().qasr_hip_decoder_load_st(dev.h, ckpt.st, C.byref(c), round_mode, max_seq,
+                                             1 if kv_bf16 else 0, C.byref(d)))
+        self.d = d
+        self.max_seq = max_seq
+        self.kv_bf16 = kv_bf16
+        dev.adopt(self)
+        return self
 
     def close(self):
         if self.d:
@@ -146,6 +213,20 @@ class Encoder:
         check(lib().qasr_hip_encoder_load(dev.h, C.byref(cfg), C.byref(w), C.byref(e)))
         self.e = e
         dev.adopt(self)
+
+    @classmethod
+    def from_checkpoint(cls, dev, ckpt, cfg):
+        """Encoder::load (encoder.rs:123-182) from a :class:`Checkpoint`; cfg is the config dict."""
+        self = cls.__new__(cls)
+        self.dev = dev
+        self.cfg = dict(cfg)
+        c = EncConfig(**{k: cfg[k] for k in ("d_model", "n_layers", "n_heads", "head_dim", "ffn_dim",
+                                            "output_dim", "chunk_size", "n_window_infer", "conv_hidden")})
+        e = P()
+        check(lib().qasr_hip_encoder_load_st(dev.h, ckpt.st, C.byref(c), C.byref(e)))
+        self.e = e
+        dev.adopt(self)
+        return self
 
     def close(self):
         if self.e:

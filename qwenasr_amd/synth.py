@@ -164,3 +164,76 @@ class SynthEncoder:
                     self.proj1_b.ctypes.data, self.proj2_b.ctypes.data)
         w._keep = arr
         return cfg, w
+
+
+def decoder_tensors(w, norm_dtype="BF16"):
+    """The checkpoint tensors of a SynthDecoder under the reference's names
+    (decoder.rs:70-167): name -> (array, "BF16" | "F32"); bf16 arrays are uint16."""
+    def norm(a):
+        a = np.asarray(a, np.float32)
+        return (f32_to_bf16(a), "BF16") if norm_dtype == "BF16" else (a, "F32")
+    t = {"thinker.model.embed_tokens.weight": (w.embed, "BF16"), "thinker.model.norm.weight": norm(w.norm)}
+    for i, L in enumerate(w.layers):
+        p = f"thinker.model.layers.{i}"
+        for k, n in (("wq", "self_attn.q_proj"), ("wk", "self_attn.k_proj"), ("wv", "self_attn.v_proj"),
+                     ("wo", "self_attn.o_proj"), ("gate", "mlp.gate_proj"), ("up", "mlp.up_proj"),
+                     ("down", "mlp.down_proj")):
+            t[f"{p}.{n}.weight"] = (L[k], "BF16")
+        for k, n in (("q_norm", "self_attn.q_norm"), ("k_norm", "self_attn.k_norm"),
+                     ("input_norm", "input_layernorm"), ("post_attn_norm", "post_attention_layernorm")):
+            t[f"{p}.{n}.weight"] = norm(L[k])
+    return t
+
+
+def encoder_tensors(w, vec_dtype="BF16"):
+    """The checkpoint tensors of a SynthEncoder under the reference's names (encoder.rs:123-182)."""
+    def vec(a):
+        a = np.asarray(a, np.float32)
+        return (f32_to_bf16(a), "BF16") if vec_dtype == "BF16" else (a, "F32")
+    p = "thinker.audio_tower."
+    t = {}
+    for k in (1, 2, 3):
+        t[f"{p}conv2d{k}.weight"] = (getattr(w, f"conv{k}_w"), "BF16")
+        t[f"{p}conv2d{k}.bias"] = vec(getattr(w, f"conv{k}_b"))
+    t[p + "conv_out.weight"] = (w.conv_out_w, "BF16")
+    for i, L in enumerate(w.layers):
+        q = f"{p}layers.{i}"
+        for wk, bk, n in (("wq", "bq", "self_attn.q_proj"), ("wk", "bk", "self_attn.k_proj"),
+                          ("wv", "bv", "self_attn.v_proj"), ("wo", "bo", "self_attn.out_proj"),
+                          ("fc1", "b1", "fc1"), ("fc2", "b2", "fc2")):
+            t[f"{q}.{n}.weight"] = (L[wk], "BF16")
+            t[f"{q}.{n}.bias"] = vec(L[bk])
+        for wk, bk, n in (("ln1_w", "ln1_b", "self_attn_layer_norm"), ("ln2_w", "ln2_b", "final_layer_norm")):
+            t[f"{q}.{n}.weight"] = vec(L[wk])
+            t[f"{q}.{n}.bias"] = vec(L[bk])
+    t[p + "ln_post.weight"] = vec(w.ln_post_w)
+    t[p + "ln_post.bias"] = vec(w.ln_post_b)
+    for k in (1, 2):
+        t[f"{p}proj{k}.weight"] = (getattr(w, f"proj{k}_w"), "BF16")
+        t[f"{p}proj{k}.bias"] = vec(getattr(w, f"proj{k}_b"))
+    return t
+
+
+def write_checkpoint(path, tensors, shards=1, metadata=None):
+    """Write tensors (name -> (array, "BF16" | "F32" | other numpy dtype name))
+    as safetensors with the safetensors library: path/model.safetensors, or
+    path/model-0000k-of-0000n.safetensors split round-robin over `shards` files."""
+    import torch
+    from safetensors.torch import save_file
+    os.makedirs(path, exist_ok=True)
+    names = sorted(tensors)
+    parts = [dict() for _ in range(shards)]
+    for i, n in enumerate(names):
+        a, dt = tensors[n]
+        a = np.ascontiguousarray(a)
+        if dt == "BF16":
+            t = torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+        else:
+            t = torch.from_numpy(a.copy())
+        parts[i % shards][n] = t
+    meta = metadata if metadata is not None else {"format": "pt"}
+    if shards == 1:
+        save_file(parts[0], os.path.join(path, "model.safetensors"), metadata=meta)
+    else:
+        for k, part in enumerate(parts):
+            save_file(part, os.path.join(path, f"model-{k + 1:05d}-of-{shards:05d}.safetensors"), metadata=meta)
