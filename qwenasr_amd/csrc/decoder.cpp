@@ -5,6 +5,7 @@
 #include "upload.h"
 
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
@@ -244,6 +245,21 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     const int64_t cap = decoder_ctx_cap(d, d->step_pos + 1);
     const int n_split = d->n_split > 0 ? d->n_split : attn_splits_auto(c, cap);
     const bool fused_merge = oproj_merges(c, n_split);
+    // rows per wave of the qkv, gate_up, down and plain o_proj matvecs: about
+    // 1024 waves per launch (rows / 1024 rounded up to 1, 2, 4 or 8; SwiGLU
+    // pairs need 2).  Measured on the 0.6B and 1.7B shapes: fewer rows per
+    // wave leave each wave's fixed prologue and reductions on too little data,
+    // more leave fewer waves to stream the matrix.  QASR_MV_ROWS="q,g,d,o"
+    // overrides them for tuning.
+    auto rows_for = [](int64_t rows, bool swiglu) {
+        int r = 1;
+        while (r < 8 && (int64_t)r * 1024 < rows) r *= 2;
+        return swiglu ? std::max(r, 2) : r;
+    };
+    std::array<int, 4> mv_rows{rows_for(qd + 2 * kvd, false), rows_for(2 * I, true), rows_for(H, false),
+                               rows_for(H, false)};
+    static const char *mv_env = getenv("QASR_MV_ROWS");
+    if (mv_env) sscanf(mv_env, "%d,%d,%d,%d", &mv_rows[0], &mv_rows[1], &mv_rows[2], &mv_rows[3]);
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
         if (want(0)) {
@@ -252,7 +268,7 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
             a.n_total = qd + 2 * kvd;
             a.resid_out = d->x;
-            LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, 4, st), "step qkv");
+            LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, mv_rows[0], st), "step qkv");
         }
         if (want(1)) {
             AttnDecodeArgs t{};
@@ -278,7 +294,7 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
                 o.x = d->att; o.K = qd;
                 o.seg[0] = {L.wo, L.so, d->x, H};
                 o.n_total = H;
-                LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, 1, st), "step o_proj");
+                LAUNCHCHK(launch_w8a8(o, MV_ADDTO, false, false, mv_rows[3], st), "step o_proj");
             }
         }
         if (want(3)) {
@@ -286,14 +302,14 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             g.x = d->x; g.norm_w = L.post_norm; g.eps = c.eps; g.K = H;
             g.seg[0] = {L.wgu, L.sgu, d->ffn, 2 * I};
             g.n_total = 2 * I;
-            LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, 4, st), "step gate_up");
+            LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, mv_rows[1], st), "step gate_up");
         }
         if (want(4)) {
             MvArgs dn{};
             dn.x = d->ffn; dn.K = I;
             dn.seg[0] = {L.wdown, L.sdown, d->x, H};
             dn.n_total = H;
-            LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, 1, st), "step down");
+            LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, mv_rows[2], st), "step down");
         }
     }
     if (want(5) || want(6)) {

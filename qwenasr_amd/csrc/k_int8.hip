@@ -694,6 +694,7 @@ hipError_t launch_w8a8(const MvArgs &a, int mode, bool norm, bool embed, int row
     if (rows_per_wave == 1 && mode != MV_SWIGLU) { QASR_MV(1) }
     if (rows_per_wave == 2) { QASR_MV(2) }
     if (rows_per_wave == 4) { QASR_MV(4) }
+    if (rows_per_wave == 8) { QASR_MV(8) }
 #undef QASR_MV
     return hipErrorInvalidValue;
 }
