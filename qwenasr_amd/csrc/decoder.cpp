@@ -256,8 +256,10 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         while (r < 8 && (int64_t)r * 1024 < rows) r *= 2;
         return swiglu ? std::max(r, 2) : r;
     };
+    // (o_proj: about 512 waves; the fused split merge that every block
+    // repeats favours fewer blocks)
     std::array<int, 4> mv_rows{rows_for(qd + 2 * kvd, false), rows_for(2 * I, true), rows_for(H, false),
-                               rows_for(H, false)};
+                               std::min(4, 2 * rows_for(H, false))};
     static const char *mv_env = getenv("QASR_MV_ROWS");
     if (mv_env) sscanf(mv_env, "%d,%d,%d,%d", &mv_rows[0], &mv_rows[1], &mv_rows[2], &mv_rows[3]);
     for (int l = 0; l < c.n_layers; l++) {
@@ -286,7 +288,7 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         if (want(2)) {
             if (fused_merge) {
                 OprojMergeArgs om{d->part, n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
-                LAUNCHCHK(launch_oproj_merge(om, st), "step o_proj");
+                LAUNCHCHK(launch_oproj_merge(om, mv_rows[3], st), "step o_proj");
             } else {
                 LAUNCHCHK(launch_attn_merge_rows(d->part, 0, n_split, d->att, qd, nullptr, nullptr, 1, st),
                           "step attention merge");

@@ -362,9 +362,9 @@ __device__ __forceinline__ float split_sum(float v) {
     return v;
 }
 
-template <int S>
+template <int S, int R>
 __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
-    constexpr int D = 128, NS = 2, R = 4, HQ = 16, K = HQ * D;
+    constexpr int D = 128, NS = 2, HQ = 16, K = HQ * D;
     __shared__ float att[K];
     __shared__ float fw[HQ][S], lsum[HQ];
     const int t = threadIdx.x, lane = t & 63;
@@ -445,18 +445,28 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     if (live) a.y[r0 + rl] = v;
 }
 
-hipError_t launch_oproj_merge(const OprojMergeArgs &a, hipStream_t st) {
-    if (a.Hkv != 8 || a.N % 4 != 0) return hipErrorInvalidValue;
-    const unsigned blocks = (unsigned)((a.N / 4 + 3) / 4);
+template <int R>
+static hipError_t go_oproj_merge(const OprojMergeArgs &a, hipStream_t st) {
+    const unsigned blocks = (unsigned)((a.N / R + 3) / 4);
     switch (a.n_split) {
-        case 1: hipLaunchKernelGGL(k_oproj_merge<1>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(k_oproj_merge<2>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(k_oproj_merge<4>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL(k_oproj_merge<8>, dim3(blocks), dim3(256), 0, st, a); break;
-        case 16: hipLaunchKernelGGL(k_oproj_merge<16>, dim3(blocks), dim3(256), 0, st, a); break;
+        case 1: hipLaunchKernelGGL((k_oproj_merge<1, R>), dim3(blocks), dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL((k_oproj_merge<2, R>), dim3(blocks), dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL((k_oproj_merge<4, R>), dim3(blocks), dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL((k_oproj_merge<8, R>), dim3(blocks), dim3(256), 0, st, a); break;
+        case 16: hipLaunchKernelGGL((k_oproj_merge<16, R>), dim3(blocks), dim3(256), 0, st, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_oproj_merge(const OprojMergeArgs &a, int rows_per_wave, hipStream_t st) {
+    if (a.Hkv != 8 || a.N % rows_per_wave != 0) return hipErrorInvalidValue;
+    switch (rows_per_wave) {
+        case 1: return go_oproj_merge<1>(a, st);
+        case 2: return go_oproj_merge<2>(a, st);
+        case 4: return go_oproj_merge<4>(a, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 // ---------------------------------------------------------------------------

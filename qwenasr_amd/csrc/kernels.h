@@ -143,7 +143,7 @@ struct OprojMergeArgs {
     float *y;                 // [N], y += W attn
     int N;
 };
-hipError_t launch_oproj_merge(const OprojMergeArgs &a, hipStream_t st);
+hipError_t launch_oproj_merge(const OprojMergeArgs &a, int rows_per_wave, hipStream_t st);
 
 hipError_t launch_rms_norm_rows(float *out, const float *x, const float *w, int64_t seq, int hidden,
                                 float eps, hipStream_t st);
