@@ -516,38 +516,85 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
 
 // ---------------------------------------------------------------------------
 // RMSNorm over rows (rms_norm, kernels/mod.rs:1191-1212, AVX order of
-// avx.rs:377-415), one wave per row, hidden % 64 == 0.
+// avx.rs:377-415), one single-wave block per row, hidden % 64 == 0: lane l
+// holds the 16-element slots s = l + 64 c in registers (float4 loads), the
+// row goes through LDS transposed (T[r][s] = x[16 s + r]) so that lanes
+// r < 16 run the reference's 16 sequential FMA chains, then the output is
+// written from the registers.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_rms_norm_rows(float *__restrict__ out, const float *__restrict__ x,
-                                                       const float *__restrict__ w, int64_t seq, int H,
-                                                       float eps) {
-    extern __shared__ float lds[];
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    const int64_t row = (int64_t)blockIdx.x * 4 + wid;
-    if (row >= seq) return;
+template <int NS>
+__global__ __launch_bounds__(64) void k_rms_norm_rows(float *__restrict__ out, const float *__restrict__ x,
+                                                      const float *__restrict__ w, int H, float eps) {
+    __shared__ float T[NS * 1024];
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
     const float *xr = x + row * H;
     float *o = out + row * H;
     const int nslot = H >> 4;
-    float *T = lds + wid * H;
-    for (int s = lane; s < nslot; s += 64)
-        for (int r = 0; r < 16; r++) T[r * nslot + s] = xr[16 * s + r];
+    float4 xv[NS][4], wv[NS][4];
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c, se = sl < nslot ? sl : 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            xv[c][i] = reinterpret_cast<const float4 *>(xr + 16 * se)[i];
+            wv[c][i] = reinterpret_cast<const float4 *>(w + 16 * se)[i];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c;
+        if (sl < nslot) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                T[(4 * i) * nslot + sl] = xv[c][i].x;
+                T[(4 * i + 1) * nslot + sl] = xv[c][i].y;
+                T[(4 * i + 2) * nslot + sl] = xv[c][i].z;
+                T[(4 * i + 3) * nslot + sl] = xv[c][i].w;
+            }
+        }
+    }
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     float acc = 0.0f;
     if (lane < 16) {
-        const float *tr = T + lane * nslot;
-        for (int i = 0; i < nslot; i++) acc = fmaf(tr[i], tr[i], acc);
+        const float4 *t = reinterpret_cast<const float4 *>(T + lane * nslot);
+        for (int i = 0; i < (nslot >> 2); i++) {
+            const float4 v = t[i];
+            acc = fmaf(v.x, v.x, acc);
+            acc = fmaf(v.y, v.y, acc);
+            acc = fmaf(v.z, v.z, acc);
+            acc = fmaf(v.w, v.w, acc);
+        }
     }
     const float ss = avx16_tree(acc);
     const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
-    for (int i = lane; i < H; i += 64) o[i] = __fmul_rn(__fmul_rn(xr[i], rinv), w[i]);
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c;
+        if (sl < nslot) {
+            float4 *op = reinterpret_cast<float4 *>(o + 16 * sl);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 a = xv[c][i], b = wv[c][i];
+                op[i] = make_float4(__fmul_rn(__fmul_rn(a.x, rinv), b.x), __fmul_rn(__fmul_rn(a.y, rinv), b.y),
+                                    __fmul_rn(__fmul_rn(a.z, rinv), b.z), __fmul_rn(__fmul_rn(a.w, rinv), b.w));
+            }
+        }
+    }
 }
 
 hipError_t launch_rms_norm_rows(float *out, const float *x, const float *w, int64_t seq, int hidden,
                                 float eps, hipStream_t st) {
     if (hidden % 64 != 0 || hidden > 4096) return hipErrorInvalidValue;
-    const unsigned blocks = (unsigned)((seq + 3) / 4);
-    hipLaunchKernelGGL(k_rms_norm_rows, dim3(blocks), dim3(256), 4 * hidden * sizeof(float), st, out, x,
-                       w, seq, hidden, eps);
+    if (seq <= 0) return hipSuccess;
+    const dim3 grid((unsigned)seq);
+    switch ((hidden + 1023) / 1024) {
+        case 1: hipLaunchKernelGGL(k_rms_norm_rows<1>, grid, dim3(64), 0, st, out, x, w, hidden, eps); break;
+        case 2: hipLaunchKernelGGL(k_rms_norm_rows<2>, grid, dim3(64), 0, st, out, x, w, hidden, eps); break;
+        case 3: hipLaunchKernelGGL(k_rms_norm_rows<3>, grid, dim3(64), 0, st, out, x, w, hidden, eps); break;
+        default: hipLaunchKernelGGL(k_rms_norm_rows<4>, grid, dim3(64), 0, st, out, x, w, hidden, eps); break;
+    }
     return hipGetLastError();
 }
 
@@ -556,6 +603,67 @@ hipError_t launch_rms_norm_rows(float *out, const float *x, const float *w, int6
 // (apply_rope_neox, mod.rs:1738-1791) over [seq][heads][hd] rows, hd = 128:
 // one wave per (row, head), two elements per lane (d and d + 64).
 // ---------------------------------------------------------------------------
+// one head's two lane elements (d = lane, lane + 64): RMSNorm then NeoX RoPE
+__device__ __forceinline__ void head_norm_rope2(float &x1, float &x2, const float *__restrict__ w,
+                                                const float *__restrict__ c, const float *__restrict__ sn,
+                                                float eps, bool do_norm, bool do_rope) {
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63;
+    if (do_norm) {
+        const float ss = wave_sum_f32(__fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2)));
+        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+        x1 = __fmul_rn(__fmul_rn(x1, r), w[lane]);
+        x2 = __fmul_rn(__fmul_rn(x2, r), w[lane + 64]);
+    }
+    if (do_rope) {
+        const float n1 = __fadd_rn(__fmul_rn(x1, c[lane]), __fmul_rn(-x2, sn[lane]));
+        const float n2 = __fadd_rn(__fmul_rn(x2, c[lane + 64]), __fmul_rn(x1, sn[lane + 64]));
+        x1 = n1; x2 = n2;
+    }
+}
+
+// The prefill's per-head work after the qkv GEMM in one launch
+// (decoder.rs:497-514): q heads normed and rotated in place; k heads normed,
+// rotated and written to the KV cache with the v heads.  One wave per
+// (row, head): waves [0, Hq) of a row take the q heads, [Hq, Hq + Hkv) the
+// k/v heads.
+__global__ __launch_bounds__(256) void k_prefill_qkv_post(PrefillPostArgs a) {
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63;
+    const int per_row = a.Hq + a.Hkv;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= a.S * per_row) return;
+    const int64_t s = item / per_row;
+    const int h = (int)(item % per_row);
+    float *row = a.qkv + s * a.row_stride;
+    const float *c = a.cos_t + s * D, *sn = a.sin_t + s * D;
+    if (h < a.Hq) {
+        float *v = row + h * D;
+        float x1 = v[lane], x2 = v[lane + 64];
+        head_norm_rope2(x1, x2, a.q_norm, c, sn, a.eps, true, true);
+        v[lane] = x1;
+        v[lane + 64] = x2;
+    } else {
+        const int kh = h - a.Hq;
+        const float *kp = row + a.Hq * D + kh * D, *vp = row + (a.Hq + a.Hkv) * D + kh * D;
+        float x1 = kp[lane], x2 = kp[lane + 64];
+        const float v1 = vp[lane], v2 = vp[lane + 64];
+        head_norm_rope2(x1, x2, a.k_norm, c, sn, a.eps, true, true);
+        const int64_t dst = kh * a.head_stride + (a.start + s) * D;
+        a.kc[dst + lane] = x1;
+        a.kc[dst + lane + 64] = x2;
+        a.vc[dst + lane] = v1;
+        a.vc[dst + lane + 64] = v2;
+    }
+}
+
+hipError_t launch_prefill_qkv_post(const PrefillPostArgs &a, hipStream_t st) {
+    const int64_t items = a.S * (a.Hq + a.Hkv);
+    if (items <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_prefill_qkv_post, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void k_head_norm_rope(float *__restrict__ x, const float *__restrict__ w,
                                                         const float *__restrict__ cos_t,
                                                         const float *__restrict__ sin_t, int64_t seq,
@@ -568,18 +676,8 @@ __global__ __launch_bounds__(256) void k_head_norm_rope(float *__restrict__ x, c
     const int64_t s = item / heads;
     float *v = x + s * row_stride + (item % heads) * D;
     float x1 = v[lane], x2 = v[lane + 64];
-    if (do_norm) {
-        const float ss = wave_sum_f32(__fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2)));
-        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
-        x1 = __fmul_rn(__fmul_rn(x1, r), w[lane]);
-        x2 = __fmul_rn(__fmul_rn(x2, r), w[lane + 64]);
-    }
-    if (do_rope) {
-        const float *c = cos_t + s * D, *sn = sin_t + s * D;
-        const float n1 = __fadd_rn(__fmul_rn(x1, c[lane]), __fmul_rn(-x2, sn[lane]));
-        const float n2 = __fadd_rn(__fmul_rn(x2, c[lane + 64]), __fmul_rn(x1, sn[lane + 64]));
-        x1 = n1; x2 = n2;
-    }
+    head_norm_rope2(x1, x2, w, do_rope ? cos_t + s * D : nullptr, do_rope ? sin_t + s * D : nullptr, eps,
+                    do_norm != 0, do_rope != 0);
     v[lane] = x1;
     v[lane + 64] = x2;
 }

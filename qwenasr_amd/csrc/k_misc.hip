@@ -10,46 +10,86 @@ namespace qasr {
 // ---------------------------------------------------------------------------
 // LayerNorm rows: avx::layer_norm_row (avx.rs:420-481) in its exact order —
 // mean over 2x8 lane accumulators, variance with FMA accumulators, both
-// through the hsum tree, then fma((x - mean) * inv, w, b).  One wave per row.
+// through the hsum tree, then fma((x - mean) * inv, w, b) (hidden % 16 == 0,
+// so every element takes the 8-wide path).  One single-wave block per row:
+// lane l holds the 16-element slots s = l + 64 c in registers, the row goes
+// through LDS transposed so that lanes r < 16 run the reference's sequential
+// accumulator chains.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_layer_norm_rows(float *__restrict__ out, const float *__restrict__ x,
-                                                         const float *__restrict__ w, const float *__restrict__ b,
-                                                         int64_t seq, int H, float eps) {
-    extern __shared__ float lds[];
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t row = (int64_t)blockIdx.x * 4 + wid;
-    if (row >= seq) return;
+template <int NS>
+__global__ __launch_bounds__(64) void k_layer_norm_rows(float *__restrict__ out, const float *__restrict__ x,
+                                                        const float *__restrict__ w, const float *__restrict__ b,
+                                                        int H, float eps) {
+    __shared__ float T[NS * 1024];
+    const int lane = threadIdx.x;
+    const int64_t row = blockIdx.x;
     const float *xr = x + row * H;
     float *o = out + row * H;
     const int nslot = H >> 4;
-    float *T = lds + wid * H;
-    for (int s = lane; s < nslot; s += 64)
-        for (int r = 0; r < 16; r++) T[r * nslot + s] = xr[16 * s + r];
+    float4 xv[NS][4];
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c, se = sl < nslot ? sl : 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[c][i] = reinterpret_cast<const float4 *>(xr + 16 * se)[i];
+    }
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c;
+        if (sl < nslot) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                T[(4 * i) * nslot + sl] = xv[c][i].x;
+                T[(4 * i + 1) * nslot + sl] = xv[c][i].y;
+                T[(4 * i + 2) * nslot + sl] = xv[c][i].z;
+                T[(4 * i + 3) * nslot + sl] = xv[c][i].w;
+            }
+        }
+    }
     __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    const float *t = T + (lane < 16 ? lane : 0) * nslot;
     float acc = 0.0f;
     if (lane < 16)
-        for (int i = 0; i < nslot; i++) acc = __fadd_rn(acc, T[lane * nslot + i]);
+        for (int i = 0; i < nslot; i++) acc = __fadd_rn(acc, t[i]);
     const float mean = __fdiv_rn(avx16_tree(acc), (float)H);
     acc = 0.0f;
     if (lane < 16)
         for (int i = 0; i < nslot; i++) {
-            const float d = __fsub_rn(T[lane * nslot + i], mean);
+            const float d = __fsub_rn(t[i], mean);
             acc = fmaf(d, d, acc);
         }
     const float var = avx16_tree(acc);
     const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(var, (float)H), eps)));
-    const int nv = H - H % 8;
-    for (int i = lane; i < H; i += 64)
-        o[i] = i < nv ? fmaf(__fmul_rn(__fsub_rn(xr[i], mean), inv), w[i], b[i])
-                      : __fadd_rn(__fmul_rn(__fmul_rn(__fsub_rn(xr[i], mean), inv), w[i]), b[i]);
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int sl = lane + 64 * c;
+        if (sl < nslot) {
+            float4 *op = reinterpret_cast<float4 *>(o + 16 * sl);
+            const float4 *wp = reinterpret_cast<const float4 *>(w + 16 * sl);
+            const float4 *bp = reinterpret_cast<const float4 *>(b + 16 * sl);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 a = xv[c][i], ww = wp[i], bb = bp[i];
+                op[i] = make_float4(fmaf(__fmul_rn(__fsub_rn(a.x, mean), inv), ww.x, bb.x),
+                                    fmaf(__fmul_rn(__fsub_rn(a.y, mean), inv), ww.y, bb.y),
+                                    fmaf(__fmul_rn(__fsub_rn(a.z, mean), inv), ww.z, bb.z),
+                                    fmaf(__fmul_rn(__fsub_rn(a.w, mean), inv), ww.w, bb.w));
+            }
+        }
+    }
 }
 
 hipError_t launch_layer_norm_rows(float *out, const float *x, const float *w, const float *b, int64_t seq,
                                   int hidden, float eps, hipStream_t st) {
     if (hidden % 16 != 0 || hidden > 4096 || seq <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_layer_norm_rows, dim3((unsigned)((seq + 3) / 4)), dim3(256), 4 * hidden * sizeof(float), st,
-                       out, x, w, b, seq, hidden, eps);
+    const dim3 grid((unsigned)seq);
+    switch ((hidden + 1023) / 1024) {
+        case 1: hipLaunchKernelGGL(k_layer_norm_rows<1>, grid, dim3(64), 0, st, out, x, w, b, hidden, eps); break;
+        case 2: hipLaunchKernelGGL(k_layer_norm_rows<2>, grid, dim3(64), 0, st, out, x, w, b, hidden, eps); break;
+        case 3: hipLaunchKernelGGL(k_layer_norm_rows<3>, grid, dim3(64), 0, st, out, x, w, b, hidden, eps); break;
+        default: hipLaunchKernelGGL(k_layer_norm_rows<4>, grid, dim3(64), 0, st, out, x, w, b, hidden, eps); break;
+    }
     return hipGetLastError();
 }
 
@@ -155,29 +195,6 @@ hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C,
     const int64_t total = (int64_t)n_chunks * C * F * T;
     const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
     hipLaunchKernelGGL(k_conv_reshape, dim3(blocks), dim3(256), 0, st, out, in, n_chunks, C, F, T);
-    return hipGetLastError();
-}
-
-// copy K (after norm + RoPE) and V rows of a prefill into the cache (decoder.rs:511-514)
-__global__ __launch_bounds__(256) void k_kv_scatter(const float *__restrict__ qkv, int64_t qkv_rs, int k_off,
-                                                    int v_off, float *__restrict__ kc, float *__restrict__ vc,
-                                                    int64_t head_stride, int start, int64_t S, int Hkv) {
-    const int64_t total = S * Hkv * 128;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= total) return;
-    const int d = (int)(i % 128);
-    const int h = (int)((i / 128) % Hkv);
-    const int64_t s = i / (128 * Hkv);
-    const int64_t dst = h * head_stride + (start + s) * 128 + d;
-    kc[dst] = qkv[s * qkv_rs + k_off + h * 128 + d];
-    vc[dst] = qkv[s * qkv_rs + v_off + h * 128 + d];
-}
-
-hipError_t launch_kv_scatter(const float *qkv, int64_t qkv_rs, int k_off, int v_off, float *kc, float *vc,
-                             int64_t head_stride, int start, int64_t S, int Hkv, hipStream_t st) {
-    const int64_t n = S * Hkv * 128;
-    hipLaunchKernelGGL(k_kv_scatter, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, qkv, qkv_rs, k_off, v_off,
-                       kc, vc, head_stride, start, S, Hkv);
     return hipGetLastError();
 }
 

@@ -204,8 +204,19 @@ hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C,
 hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C, int F, int T, hipStream_t st);
 // idle one wave for `us` microseconds (timing helper)
 hipError_t launch_delay(int us, hipStream_t st);
-hipError_t launch_kv_scatter(const float *qkv, int64_t qkv_rs, int k_off, int v_off, float *kc, float *vc,
-                             int64_t head_stride, int start, int64_t S, int Hkv, hipStream_t st);
+// the prefill's q/k per-head norm + RoPE and K/V cache write (one launch)
+struct PrefillPostArgs {
+    float *qkv;                          // [S][row_stride]: q (Hq heads) | k (Hkv) | v (Hkv), 128 dims each
+    int64_t row_stride, S;
+    int Hq, Hkv;
+    const float *q_norm, *k_norm;        // [128]
+    const float *cos_t, *sin_t;          // RoPE rows of positions start .. start + S - 1
+    float *kc, *vc;                      // [Hkv][head_stride]
+    int64_t head_stride;
+    int64_t start;
+    float eps;
+};
+hipError_t launch_prefill_qkv_post(const PrefillPostArgs &a, hipStream_t st);
 hipError_t launch_row_diff(const float *a, const float *b, int64_t rows, int64_t H, int *flags, hipStream_t st);
 // idx[r] = lowest column of the maximum of row r's non-NaN values (0 when column 0 is NaN)
 hipError_t launch_argmax_f32_rows(const float *x, int64_t ld, int64_t rows, int64_t cols, int32_t *idx,

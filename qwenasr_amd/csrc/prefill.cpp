@@ -77,13 +77,11 @@ int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S) {
         float *vc = reinterpret_cast<float *>(d->vc) + l * layer_elems;
         LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.in_norm, S, H, c.eps, st), "prefill rms_norm");
         TRY(gemm(d, p.xn, H, L.bqkv, H, p.qkv, nqkv, M, nqkv, H, EPI_NONE));
-        LAUNCHCHK(launch_head_norm_rope_strided(p.qkv, nqkv, L.q_norm, rc, rs, S, c.n_heads, c.eps, 1, 1, st),
-                  "prefill q norm/rope");
-        LAUNCHCHK(launch_head_norm_rope_strided(p.qkv + qd, nqkv, L.k_norm, rc, rs, S, c.n_kv_heads, c.eps, 1, 1, st),
-                  "prefill k norm/rope");
-        LAUNCHCHK(launch_kv_scatter(p.qkv, nqkv, qd, qd + kvd, kc, vc, d->max_seq * hd, (int)start, S, c.n_kv_heads,
-                                    st),
-                  "prefill kv write");
+        PrefillPostArgs pp{};
+        pp.qkv = p.qkv; pp.row_stride = nqkv; pp.S = S; pp.Hq = c.n_heads; pp.Hkv = c.n_kv_heads;
+        pp.q_norm = L.q_norm; pp.k_norm = L.k_norm; pp.cos_t = rc; pp.sin_t = rs;
+        pp.kc = kc; pp.vc = vc; pp.head_stride = d->max_seq * hd; pp.start = start; pp.eps = c.eps;
+        LAUNCHCHK(launch_prefill_qkv_post(pp, st), "prefill q/k norm, rope and kv write");
         AttnRowsArgs a{};
         a.q = p.qkv; a.q_rs = nqkv;
         a.k = kc; a.v = vc; a.k_hs = d->max_seq * hd; a.k_rs = hd;
