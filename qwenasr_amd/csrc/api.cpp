@@ -438,6 +438,7 @@ extern "C" int qasr_hip_linear_bf16w(qasr_hip *h, float *y, const float *x, cons
     GemmArgs g{};
     g.M = (int)seq; g.N = (int)out_dim; g.K = (int)in_dim;
     g.A = x; g.lda = in_dim; g.B = w; g.ldb = in_dim; g.C = y; g.ldc = out_dim; g.bias = bias;
+    g.ws = reinterpret_cast<float *>(h->scratch); g.ws_bytes = QASR_SCRATCH_BYTES;   // split-K partials
     LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, accumulate ? EPI_ACCUM : EPI_NONE, h->stream), "linear_bf16w");
     return QASR_OK;
 }

@@ -240,6 +240,7 @@ static int egemm(qasr_encoder *e, const float *A, int64_t lda, const uint16_t *B
     g.M = M; g.N = N; g.K = K;
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.bias = bias;
     g.gelu_n = gelu_n; g.gelu_rows = gelu_rows;
+    g.ws = reinterpret_cast<float *>(e->h->scratch); g.ws_bytes = QASR_SCRATCH_BYTES;
     LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, epi, e->h->stream), "encoder gemm");
     return QASR_OK;
 }

@@ -236,6 +236,33 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
 }
 
+// the GEMM epilogue of one output element (C row-major, or EPI_TRANS:
+// [M / gelu_rows][N][gelu_rows]): scale, then C = (C + bias) + v for
+// EPI_ACCUM or v + bias, then GELU
+template <int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, int m, int n, float v) {
+    int64_t off, gidx;
+    if (EPI & EPI_TRANS) {
+        const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
+        gidx = (int64_t)n * g.gelu_rows + sp;
+        off = (int64_t)c * g.gelu_n + gidx;
+    } else {
+        gidx = (int64_t)m * g.ldc + n;
+        off = gidx;
+    }
+    float *cp = g.C + off;
+    if (EPI & EPI_SCALE) v = __fmul_rn(v, g.scale[n]);
+    if (EPI & EPI_ACCUM) {
+        float c = *cp;
+        if (g.bias) c = __fadd_rn(c, g.bias[n]);
+        v = __fadd_rn(c, v);
+    } else if (g.bias) {
+        v = __fadd_rn(v, g.bias[n]);
+    }
+    if (EPI & EPI_GELU) v = gelu_ref(v, gidx, g.gelu_n);
+    *cp = v;
+}
+
 template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN>
 __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     constexpr bool AF = ASRC == A_F32_SPLIT;
@@ -255,7 +282,11 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int mw = AF ? (BM / 4) * wid : 0, nw = AF ? 0 : (BN / 4) * wid;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int M = g.M, N = g.N, K = g.K, nk = K / BK;
+    const int M = g.M, N = g.N, K = g.K;
+    // split K (grid z > 1): this block's K-steps [k0s, k0s + nk); its raw
+    // partial sums go to the workspace and a reduction pass runs the epilogue
+    const int nk_all = K / BK, kz = blockIdx.z, ks = gridDim.z;
+    const int k0s = (int)((int64_t)nk_all * kz / ks), nk = (int)((int64_t)nk_all * (kz + 1) / ks) - k0s;
     // this lane's rows and swizzled 16-byte slots in the wave's loads: A load j
     // covers tile rows 8 j .. 8 j + 7 (8 slots each), B load j rows 16 j .. 16 j + 15 (4 slots)
     const char *A = reinterpret_cast<const char *>(g.A), *B = reinterpret_cast<const char *>(g.B);
@@ -274,7 +305,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     auto issue = [&](int buf, int kt) {
         char *st = smem[buf];
         const bool live = kt < nk;
-        const int64_t ka = live ? (int64_t)kt * BK * AE : 0, kb = live ? (int64_t)kt * BK * BE : 0;
+        const int64_t ka = live ? (int64_t)(k0s + kt) * BK * AE : 0, kb = live ? (int64_t)(k0s + kt) * BK * BE : 0;
 #pragma unroll
         for (int u = 0; u < LA; u++) lds_dma16(live ? a_src[u] + ka : zero, st + 1024 * (wid * LA + u));
 #pragma unroll
@@ -369,28 +400,21 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
                 const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
                 const int n = n0 + nw + j * 16 + (lane & 15);
                 if (m >= M || n >= N) continue;
-                float v = acc[i][j][r];
-                int64_t off, gidx;
-                if (EPI & EPI_TRANS) {
-                    const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
-                    gidx = (int64_t)n * g.gelu_rows + sp;
-                    off = (int64_t)c * g.gelu_n + gidx;
-                } else {
-                    gidx = (int64_t)m * g.ldc + n;
-                    off = gidx;
-                }
-                float *cp = g.C + off;
-                if (EPI & EPI_SCALE) v = __fmul_rn(v, g.scale[n]);
-                if (EPI & EPI_ACCUM) {
-                    float c = *cp;
-                    if (g.bias) c = __fadd_rn(c, g.bias[n]);
-                    v = __fadd_rn(c, v);
-                } else if (g.bias) {
-                    v = __fadd_rn(v, g.bias[n]);
-                }
-                if (EPI & EPI_GELU) v = gelu_ref(v, gidx, g.gelu_n);
-                *cp = v;
+                if (ks > 1)
+                    g.ws[((int64_t)kz * M + m) * N + n] = acc[i][j][r];
+                else
+                    gemm_epilogue<EPI>(g, m, n, acc[i][j][r]);
             }
+}
+
+// split-K reduction: the partials summed in split order, then the epilogue
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int ks) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x, mn = (int64_t)g.M * g.N;
+    if (i >= mn) return;
+    float v = g.ws[i];
+    for (int z = 1; z < ks; z++) v = __fadd_rn(v, g.ws[z * mn + i]);
+    gemm_epilogue<EPI>(g, (int)(i / g.N), (int)(i % g.N), v);
 }
 
 // ---------------------------------------------------------------------------
@@ -446,13 +470,32 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
 }
 
 template <int ASRC, int BSRC, int NS, int BM, int BN>
-static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
-    const dim3 grid((g.N + BN - 1) / BN, (g.M + BM - 1) / BM);
+static hipError_t go_gemm_lds_ns(const GemmArgs &g0, int epi, hipStream_t st) {
+    GemmArgs g = g0;
+    const int gx = (g.N + BN - 1) / BN, gy = (g.M + BM - 1) / BM;
+    // split K in two when the tile grid leaves most CUs idle and the caller
+    // gave a workspace for the partials (QASR_GEMM_SPLITK=0 disables)
+    static const bool split_ok = [] { const char *e = getenv("QASR_GEMM_SPLITK"); return !(e && e[0] == '0'); }();
+    const int bk = ASRC == A_F32_SPLIT ? 32 : 64;
+    int ks = 1;
+    if (split_ok && g.ws && gx * gy <= 160 && g.K / bk >= 16 &&
+        g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float))
+        ks = 2;
+    const dim3 grid(gx, gy, ks);
     switch (epi) {
 #define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN>), grid, dim3(256), 0, st, g); break;
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
 #undef QE
         default: return hipErrorInvalidValue;
+    }
+    if (ks > 1) {
+        const dim3 rg((unsigned)(((int64_t)g.M * g.N + 255) / 256));
+        switch (epi) {
+#define QE(E) case E: hipLaunchKernelGGL((k_gemm_splitk_reduce<E>), rg, dim3(256), 0, st, g, ks); break;
+            QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+#undef QE
+            default: return hipErrorInvalidValue;
+        }
     }
     return hipGetLastError();
 }

@@ -172,6 +172,8 @@ struct GemmArgs {
     int64_t gelu_n;           // elements of the buffer gelu() sees (EPI_GELU / EPI_TRANS: per chunk)
     int gelu_rows;            // EPI_TRANS: spatial positions per chunk
     int a_vec4, b_vec;        // set by the launcher
+    float *ws;                // optional workspace for split-K partials (null: no split)
+    int64_t ws_bytes;
 };
 
 hipError_t launch_gemm(const GemmArgs &g, int asrc, int bsrc, int epi, hipStream_t st);

@@ -43,6 +43,7 @@ static int gemm(qasr_decoder *d, const float *A, int64_t lda, const uint16_t *B,
     GemmArgs g{};
     g.M = M; g.N = N; g.K = K;
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
+    g.ws = reinterpret_cast<float *>(d->h->scratch); g.ws_bytes = QASR_SCRATCH_BYTES;   // split-K partials
     LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, epi, d->h->stream), "prefill gemm");
     return QASR_OK;
 }
