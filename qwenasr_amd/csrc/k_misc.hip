@@ -168,8 +168,34 @@ __global__ __launch_bounds__(256) void k_im2col3x3s2(float *__restrict__ cols, c
     }
 }
 
+// the same patches with one block per output position (row) and the threads
+// over its C * 9 columns: the position is decoded once per block and the
+// column index needs only 32-bit divisions by constants
+__global__ __launch_bounds__(256) void k_im2col3x3s2_rows(float *__restrict__ cols, const float *__restrict__ in,
+                                                          int C, int H, int W, int64_t cs, int64_t chs, int64_t rs,
+                                                          int Ho, int Wo) {
+    const int P = C * 9;
+    const int row = blockIdx.x;
+    const int ow = row % Wo, oh = (row / Wo) % Ho, c = row / (Wo * Ho);
+    const float *src = in + c * cs;
+    float *dst = cols + (int64_t)row * P;
+    for (int p = threadIdx.x; p < P; p += 256) {
+        const int ic = p / 9, r9 = p - 9 * ic, ki = r9 / 3, kj = r9 - 3 * ki;
+        const int ih = oh * 2 + ki - 1, iw = ow * 2 + kj - 1;
+        float v = 0.0f;
+        if (ih >= 0 && ih < H && iw >= 0 && iw < W) v = src[ic * chs + (int64_t)ih * rs + iw];
+        dst[p] = v;
+    }
+}
+
 hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C, int H, int W, int64_t cs,
                               int64_t chs, int64_t rs, int Ho, int Wo, hipStream_t st) {
+    const int64_t rows = (int64_t)n_chunks * Ho * Wo;
+    if (C * 9 >= 256 && rows < (1ll << 31)) {
+        hipLaunchKernelGGL(k_im2col3x3s2_rows, dim3((unsigned)rows), dim3(256), 0, st, cols, in, C, H, W, cs, chs, rs,
+                           Ho, Wo);
+        return hipGetLastError();
+    }
     const int64_t total = (int64_t)n_chunks * Ho * Wo * C * 9;
     const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
     hipLaunchKernelGGL(k_im2col3x3s2, dim3(blocks), dim3(256), 0, st, cols, in, n_chunks, C, H, W, cs, chs, rs,
