@@ -139,12 +139,20 @@ def main():
         res = orc.transcribe_forced(od, oe, x, args.decode_steps)
         cpu_s = time.perf_counter() - c1
         match = int(np.sum(res["tokens"] == toks))
+        cpu_model = ""
+        try:
+            with open("/proc/cpuinfo") as f:
+                cpu_model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+        except OSError:
+            pass
         cpu = {"value": round(args.audio_seconds / cpu_s, 3), "unit": "x realtime", "cores": threads,
                "kind": "port",
                "sample": f"the full workload once: {args.audio_seconds:.0f} s audio, {args.decode_steps} decode "
-                         f"steps (oracle C restatement, {threads} OpenMP threads; stage ms "
+                         f"steps (oracle C restatement, {threads} OpenMP threads, its own blocked AVX2 sgemm "
+                         f"for prefill/encoder/mel since the image has no OpenBLAS; stage ms "
                          f"{[round(float(t), 1) for t in res['times_ms']]})",
-               "token_match": f"{match}/{args.decode_steps}"}
+               "token_match": f"{match}/{args.decode_steps}",
+               "host": {"cpu_model": cpu_model, "nproc": os.cpu_count()}}
         print(f"[bench] cpu: {cpu_s:.2f} s, tokens identical {match}/{args.decode_steps}", file=sys.stderr,
               flush=True)
         od.close()
