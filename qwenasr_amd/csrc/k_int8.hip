@@ -569,6 +569,16 @@ __global__ __launch_bounds__(256) void k_argmax_finish(ArgmaxArgs a, int n_parts
     __shared__ float bvals[4];
     __shared__ int bidx[4];
     const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    // the next position's RoPE rows do not depend on the token: thread t < 128
+    // copies cos[t], t >= 128 sin[t - 128], issued alongside the partial loads
+    // (every thread reads the position before the barrier below; lane 0 of
+    // wave 0 advances it after)
+    const int next_pos = a.state ? a.state[1] + 1 : 0;
+    if (a.state && a.rope_cur && next_pos < a.max_pos) {
+        const int i = threadIdx.x & 127;
+        const float *tab = threadIdx.x < 128 ? a.rope_cos : a.rope_sin;
+        a.rope_cur[threadIdx.x] = tab[(int64_t)next_pos * 128 + i];
+    }
     float bv = -1e30f;
     int bi = -1;
     for (int b = threadIdx.x; b < n_parts; b += 256) {
@@ -589,14 +599,6 @@ __global__ __launch_bounds__(256) void k_argmax_finish(ArgmaxArgs a, int n_parts
     bi = bidx[0];
     for (int w = 1; w < 4; w++)
         if (better(bvals[w], bidx[w], bv, bi)) { bv = bvals[w]; bi = bidx[w]; }
-    // the next position's RoPE rows (read by every lane before lane 0 advances the state)
-    const int next_pos = a.state ? a.state[1] + 1 : 0;
-    if (a.state && a.rope_cur && next_pos < a.max_pos) {
-        for (int i = lane; i < 128; i += 64) {
-            a.rope_cur[i] = a.rope_cos[(int64_t)next_pos * 128 + i];
-            a.rope_cur[128 + i] = a.rope_sin[(int64_t)next_pos * 128 + i];
-        }
-    }
     if (lane == 0) {
         const int tok = bi < 0 ? 0 : bi;
         a.out_idx[0] = tok;
