@@ -371,10 +371,13 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     if (!MERGE) {
         // the consumer (the o_proj kernel or a merge kernel) merges; the kernel
         // boundary publishes these.  (m, l) of head h = G kvh + gq at
-        // [(2 h + {0,1}) S + split]; o as part_o_index lays it out.
+        // [(2 h + {0,1}) S + split]; o as part_o_index lays it out (the
+        // multi-stream step: split index slowest, so the stores coalesce).
         if (t < G * D) {
             const int h = kvh * G + gq;
-            partb[part_o_index(n_split, split, Hq, h * D + d)] = o_part;
+            const int64_t oi = DEC >= 2 ? part_o_index_slow(n_split, split, Hq, h * D + d)
+                                        : part_o_index(n_split, split, Hq, h * D + d);
+            partb[oi] = o_part;
             if (d == 0) {
                 partb[(2 * h) * n_split + split] = m_part;
                 partb[(2 * h + 1) * n_split + split] = l_part;

@@ -1057,7 +1057,7 @@ hipError_t launch_argmax_batch(const BatchMvArgs &a, int blocks, int *state, int
 }
 
 // attention partial merge per stream (the o_proj prologue's merge as its own
-// pass), split-fastest layout, then the o_proj activation quantization of the
+// pass), split index slowest, then the o_proj activation quantization of the
 // merged row (absmax over the 16 heads x 128 dims, act_finish's scale and
 // rounding): xq[b][128 h + d], xs[b]; att (nullable) receives the f32 row
 template <int S>
@@ -1069,9 +1069,13 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float *__restrict
     const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const float *pb = part + (int64_t)b * part_stride;
     const int g = t >> 7, d = t & 127;
+    // o partials split index slowest (part_o_index_slow): per split, the
+    // threads' loads are contiguous
     float ov[HQ / 2][S];
 #pragma unroll
-    for (int j = 0; j < HQ / 2; j++) ld_split<S>(pb + 2 * HQ * S + ((2 * j + g) * D + d) * S, ov[j]);
+    for (int j = 0; j < HQ / 2; j++)
+#pragma unroll
+        for (int s = 0; s < S; s++) ov[j][s] = pb[part_o_index_slow(S, s, HQ, (2 * j + g) * D + d)];
     const int e = t % (HQ * S), eh = e / S, es = e % S;
     const float pm = pb[(2 * eh) * S + es], pl = pb[(2 * eh + 1) * S + es];
     {

@@ -96,9 +96,13 @@ hipError_t launch_attn_merge_rows(const float *part, int64_t part_stride, int n_
 // its S values as one vector), split index slowest otherwise (the merge
 // kernel's threads read consecutive e).
 __host__ __device__ inline bool part_split_fastest(int S) { return S <= 16 && (S & (S - 1)) == 0; }
+// o partial e (= 128 h + d) of `split`, split index slowest: every block's
+// stores are contiguous (the multi-stream step always uses this layout)
+__host__ __device__ inline int64_t part_o_index_slow(int S, int split, int Hq, int e) {
+    return (int64_t)2 * Hq * S + (int64_t)split * Hq * 128 + e;
+}
 __host__ __device__ inline int64_t part_o_index(int S, int split, int Hq, int e) {
-    return part_split_fastest(S) ? (int64_t)(2 * Hq + e) * S + split
-                                 : (int64_t)2 * Hq * S + (int64_t)split * Hq * 128 + e;
+    return part_split_fastest(S) ? (int64_t)(2 * Hq + e) * S + split : part_o_index_slow(S, split, Hq, e);
 }
 
 struct AttnDecodeArgs {
