@@ -46,6 +46,7 @@ struct qasr_batch {
     int8_t *xq = nullptr;
     int32_t *state = nullptr, *token_log = nullptr, *am_idx = nullptr;
     int32_t *gpb_dev = nullptr, *gpb_table = nullptr;   // per-stream / per-position attention partition
+    int32_t *order_dev = nullptr;                        // attention grid rows -> streams, largest units first
     std::vector<int32_t> gpb_host;
     int64_t part_stride = 0;
     std::vector<int64_t> len;          // host copy of each stream's KV length
@@ -153,7 +154,14 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     if (rc == QASR_OK) rc = balloc(b, &b->am_val, (size_t)ARGMAX_BLOCKS * 32);
     if (rc == QASR_OK) rc = balloc(b, &b->am_idx, (size_t)ARGMAX_BLOCKS * 32);
     if (rc == QASR_OK) rc = balloc(b, &b->gpb_dev, (size_t)n_streams, true);
+    if (rc == QASR_OK) rc = balloc(b, &b->order_dev, (size_t)n_streams, true);
     if (rc == QASR_OK) rc = balloc(b, &b->gpb_table, (size_t)max_seq);
+    if (rc == QASR_OK) {
+        std::vector<int32_t> ident(n_streams);
+        for (int i = 0; i < n_streams; i++) ident[i] = i;
+        if (hipMemcpy(b->order_dev, ident.data(), sizeof(int32_t) * n_streams, hipMemcpyHostToDevice) != hipSuccess)
+            rc = qasr_fail(QASR_ERR_HIP, "batch: order upload failed");
+    }
     if (rc == QASR_OK) rc = batch_partition(b);
     if (rc != QASR_OK) {
         qasr_hip_batch_free(b);
@@ -265,6 +273,7 @@ static int batch_enqueue_step(qasr_batch *b, int n_split, int kind = -1) {
         t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = 1.0f / sqrtf((float)hd);
         t.gpb = 1;                           // the per-stream gpb_dev rows are used
         t.gpb_dev = b->gpb_dev;
+        t.stream_order = b->order_dev;
         t.depth = b->attn_depth;
         t.batch = B; t.batch_kv_stride = le; t.batch_qkv_stride = nqkv; t.batch_part_stride = b->part_stride;
         if (on(BK_PREP)) LAUNCHCHK(launch_qk_prep_rows(t, c.n_heads, c.n_kv_heads, hd, 0, st), "batch q/k prep");
@@ -309,6 +318,16 @@ static int batch_set_state(qasr_batch *b, const int32_t *first_tokens) {
     std::vector<int32_t> gp(b->B);
     for (int i = 0; i < b->B; i++) gp[i] = b->gpb_host[b->len[i]];
     HIPCHK(hipMemcpyAsync(b->gpb_dev, gp.data(), sizeof(int32_t) * b->B, hipMemcpyHostToDevice, st));
+    // attention blocks of the streams with the longest units (groups per
+    // block, then context) are dispatched first, so that the short ones fill
+    // the tail; every stream grows by one position per step, so the order
+    // holds for the whole call
+    std::vector<int32_t> order(b->B);
+    for (int i = 0; i < b->B; i++) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int x, int y) {
+        return gp[x] != gp[y] ? gp[x] > gp[y] : b->len[x] > b->len[y];
+    });
+    HIPCHK(hipMemcpyAsync(b->order_dev, order.data(), sizeof(int32_t) * b->B, hipMemcpyHostToDevice, st));
     for (int i = 0; i < b->B; i++) {
         HIPCHK(hipMemcpyAsync(b->rope_cur + 256 * i, d->rc + b->len[i] * hd, sizeof(float) * hd,
                               hipMemcpyDeviceToDevice, st));

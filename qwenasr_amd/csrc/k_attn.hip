@@ -221,7 +221,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     constexpr bool prep = DEC == 1;                      // raw projections: norm + rope + cache write
     // stream of a multi-stream step (0 otherwise): its cache, q/k/v row,
     // position, RoPE rows and partials
-    const int bs = blockIdx.y;
+    const int bs = (DEC >= 2 && a.stream_order) ? a.stream_order[blockIdx.y] : (int)blockIdx.y;
     KVT *kc = reinterpret_cast<KVT *>(a.kcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
     KVT *vc = reinterpret_cast<KVT *>(a.vcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
     const float *qkv = a.qkv + bs * a.batch_qkv_stride;

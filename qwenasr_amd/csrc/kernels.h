@@ -126,6 +126,7 @@ struct AttnDecodeArgs {
     int batch;                // streams (0 or 1: one)
     int64_t batch_kv_stride, batch_qkv_stride, batch_part_stride;
     const int *gpb_dev;       // nullable: per-stream groups per block [batch] (overrides gpb)
+    const int *stream_order;  // nullable: grid row -> stream of a multi-stream step (largest units first)
     int depth;                // multi-stream mode: groups in flight per wave (1 or 2; 0: 2)
 };
 
