@@ -263,7 +263,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, int m, int n, f
     *cp = v;
 }
 
-template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN>
+template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN, int KS>
 __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     constexpr bool AF = ASRC == A_F32_SPLIT;
     constexpr int AE = AF ? 4 : 2, BE = BSRC == B_BF16 ? 2 : 1;     // element bytes
@@ -283,10 +283,12 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     const int mw = AF ? (BM / 4) * wid : 0, nw = AF ? 0 : (BN / 4) * wid;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int M = g.M, N = g.N, K = g.K;
-    // split K (grid z > 1): this block's K-steps [k0s, k0s + nk); its raw
-    // partial sums go to the workspace and a reduction pass runs the epilogue
-    const int nk_all = K / BK, kz = blockIdx.z, ks = gridDim.z;
-    const int k0s = (int)((int64_t)nk_all * kz / ks), nk = (int)((int64_t)nk_all * (kz + 1) / ks) - k0s;
+    // split K (KS > 1, grid z = KS): this block's K-steps [k0s, k0s + nk); its
+    // raw partial sums go to the workspace and a reduction pass runs the
+    // epilogue.  A compile-time count, so that the unsplit kernels keep their
+    // main loop unchanged.
+    const int nk_all = K / BK, kz = KS > 1 ? (int)blockIdx.z : 0;
+    const int k0s = KS > 1 ? nk_all * kz / KS : 0, nk = KS > 1 ? nk_all * (kz + 1) / KS - k0s : nk_all;
     // this lane's rows and swizzled 16-byte slots in the wave's loads: A load j
     // covers tile rows 8 j .. 8 j + 7 (8 slots each), B load j rows 16 j .. 16 j + 15 (4 slots)
     const char *A = reinterpret_cast<const char *>(g.A), *B = reinterpret_cast<const char *>(g.B);
@@ -400,7 +402,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
                 const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
                 const int n = n0 + nw + j * 16 + (lane & 15);
                 if (m >= M || n >= N) continue;
-                if (ks > 1)
+                if (KS > 1)
                     g.ws[((int64_t)kz * M + m) * N + n] = acc[i][j][r];
                 else
                     gemm_epilogue<EPI>(g, m, n, acc[i][j][r]);
@@ -470,32 +472,35 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
 }
 
 template <int ASRC, int BSRC, int NS, int BM, int BN>
-static hipError_t go_gemm_lds_ns(const GemmArgs &g0, int epi, hipStream_t st) {
-    GemmArgs g = g0;
+static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     const int gx = (g.N + BN - 1) / BN, gy = (g.M + BM - 1) / BM;
-    // split K in two when the tile grid leaves most CUs idle and the caller
-    // gave a workspace for the partials (QASR_GEMM_SPLITK=0 disables)
+    // split K in two (f32-class path, epilogues without a transposed store)
+    // when the tile grid leaves most CUs idle and the caller gave a workspace
+    // for the partials (QASR_GEMM_SPLITK=0 disables)
     static const bool split_ok = [] { const char *e = getenv("QASR_GEMM_SPLITK"); return !(e && e[0] == '0'); }();
-    const int bk = ASRC == A_F32_SPLIT ? 32 : 64;
-    int ks = 1;
-    if (split_ok && g.ws && gx * gy <= 160 && g.K / bk >= 16 &&
-        g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float))
-        ks = 2;
-    const dim3 grid(gx, gy, ks);
-    switch (epi) {
-#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN>), grid, dim3(256), 0, st, g); break;
-        QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
-#undef QE
-        default: return hipErrorInvalidValue;
-    }
-    if (ks > 1) {
-        const dim3 rg((unsigned)(((int64_t)g.M * g.N + 255) / 256));
+    const bool split = ASRC == A_F32_SPLIT && split_ok && g.ws && gx * gy <= 160 && g.K / 32 >= 16 &&
+                       (epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU) &&
+                       g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float);
+    if (split) {
+        const dim3 grid(gx, gy, 2), rg((unsigned)(((int64_t)g.M * g.N + 255) / 256));
         switch (epi) {
-#define QE(E) case E: hipLaunchKernelGGL((k_gemm_splitk_reduce<E>), rg, dim3(256), 0, st, g, ks); break;
-            QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+#define QE(E)                                                                                          \
+    case E:                                                                                            \
+        hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 2>), grid, dim3(256), 0, st, g);     \
+        hipLaunchKernelGGL((k_gemm_splitk_reduce<E>), rg, dim3(256), 0, st, g, 2);                     \
+        break;
+            QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_GELU)
 #undef QE
             default: return hipErrorInvalidValue;
         }
+        return hipGetLastError();
+    }
+    const dim3 grid(gx, gy);
+    switch (epi) {
+#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1>), grid, dim3(256), 0, st, g); break;
+        QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+#undef QE
+        default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
