@@ -452,6 +452,7 @@ extern "C" int qasr_hip_gemm_w8_bf16(qasr_hip *h, float *y, const uint16_t *a, c
     GemmArgs g{};
     g.M = (int)M; g.N = (int)N; g.K = (int)K;
     g.A = a; g.lda = K; g.B = w; g.ldb = K; g.C = y; g.ldc = N; g.scale = scales;
+    g.ws = reinterpret_cast<float *>(h->scratch); g.ws_bytes = QASR_SCRATCH_BYTES;   // split-K partials
     LAUNCHCHK(launch_gemm(g, A_BF16, B_I8, EPI_SCALE, h->stream), "gemm_w8_bf16");
     return QASR_OK;
 }

@@ -474,12 +474,15 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
 template <int ASRC, int BSRC, int NS, int BM, int BN>
 static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     const int gx = (g.N + BN - 1) / BN, gy = (g.M + BM - 1) / BM;
-    // split K in two (f32-class path, epilogues without a transposed store)
+    // split K in two (epilogues without a transposed store)
     // when the tile grid leaves most CUs idle and the caller gave a workspace
     // for the partials (QASR_GEMM_SPLITK=0 disables)
     static const bool split_ok = [] { const char *e = getenv("QASR_GEMM_SPLITK"); return !(e && e[0] == '0'); }();
-    const bool split = ASRC == A_F32_SPLIT && split_ok && g.ws && gx * gy <= 160 && g.K / 32 >= 16 &&
-                       (epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU) &&
+    // (K-steps: at least 16 of the f32-class path, whose steps cost three MFMA
+    // passes, 32 of the bf16 one; measured break-even points)
+    const int bk = ASRC == A_F32_SPLIT ? 32 : 64, min_steps = ASRC == A_F32_SPLIT ? 16 : 32;
+    const bool split = split_ok && g.ws && gx * gy <= 160 && g.K / bk >= min_steps &&
+                       (epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU || epi == EPI_SCALE) &&
                        g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float);
     if (split) {
         const dim3 grid(gx, gy, 2), rg((unsigned)(((int64_t)g.M * g.N + 255) / 256));
@@ -489,7 +492,7 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
         hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 2>), grid, dim3(256), 0, st, g);     \
         hipLaunchKernelGGL((k_gemm_splitk_reduce<E>), rg, dim3(256), 0, st, g, 2);                     \
         break;
-            QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_GELU)
+            QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_GELU) QE(EPI_SCALE)
 #undef QE
             default: return hipErrorInvalidValue;
         }
