@@ -1068,14 +1068,16 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float *__restrict
     __shared__ float fw[HQ][S], lsum[HQ], wmax[4];
     const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
     const float *pb = part + (int64_t)b * part_stride;
-    const int g = t >> 7, d = t & 127;
-    // o partials split index slowest (part_o_index_slow): per split, the
-    // threads' loads are contiguous
-    float ov[HQ / 2][S];
+    // o partials split index slowest (part_o_index_slow): items u = t, t + 256
+    // are (head u / 32, dims 4 (u % 32) .. + 3), one float4 per split
+    float4 ov[2][S];
 #pragma unroll
-    for (int j = 0; j < HQ / 2; j++)
+    for (int u = 0; u < 2; u++) {
+        const int it = t + 256 * u, h = it >> 5, c4 = it & 31;
 #pragma unroll
-        for (int s = 0; s < S; s++) ov[j][s] = pb[part_o_index_slow(S, s, HQ, (2 * j + g) * D + d)];
+        for (int s = 0; s < S; s++)
+            ov[u][s] = *reinterpret_cast<const float4 *>(pb + part_o_index_slow(S, s, HQ, h * D + 4 * c4));
+    }
     const int e = t % (HQ * S), eh = e / S, es = e % S;
     const float pm = pb[(2 * eh) * S + es], pl = pb[(2 * eh + 1) * S + es];
     {
@@ -1088,17 +1090,26 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float *__restrict
         }
     }
     __syncthreads();
-    float o[HQ / 2], m = 0.0f;
+    float o[2][4], m = 0.0f;
 #pragma unroll
-    for (int j = 0; j < HQ / 2; j++) {
-        const int h = 2 * j + g;
-        float ot = 0.0f;
-#pragma unroll
-        for (int s = 0; s < S; s++) ot = fmaf(ov[j][s], fw[h][s], ot);
+    for (int u = 0; u < 2; u++) {
+        const int it = t + 256 * u, h = it >> 5, c4 = it & 31;
         const float lt = lsum[h];
-        o[j] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
-        m = fmaxf(m, fabsf(o[j]));
-        if (att) att[(int64_t)b * att_stride + h * D + d] = o[j];
+        float ot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const float w = fw[h][s];
+            ot[0] = fmaf(ov[u][s].x, w, ot[0]);
+            ot[1] = fmaf(ov[u][s].y, w, ot[1]);
+            ot[2] = fmaf(ov[u][s].z, w, ot[2]);
+            ot[3] = fmaf(ov[u][s].w, w, ot[3]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            o[u][i] = lt > 0.0f ? __fdiv_rn(ot[i], lt) : 0.0f;
+            m = fmaxf(m, fabsf(o[u][i]));
+            if (att) att[(int64_t)b * att_stride + h * D + 4 * c4 + i] = o[u][i];
+        }
     }
     m = wave_max_f32(m);
     if (lane == 0) wmax[t >> 6] = m;
@@ -1108,8 +1119,12 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float *__restrict
     act_scales(m, &scale, &inv);
     if (t == 0) xs[b] = scale;
 #pragma unroll
-    for (int j = 0; j < HQ / 2; j++)
-        xq[(int64_t)b * K + (2 * j + g) * D + d] = (int8_t)round_clamp_i8(__fmul_rn(o[j], inv));
+    for (int u = 0; u < 2; u++) {
+        const int it = t + 256 * u, h = it >> 5, c4 = it & 31;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            xq[(int64_t)b * K + h * D + 4 * c4 + i] = (int8_t)round_clamp_i8(__fmul_rn(o[u][i], inv));
+    }
 }
 
 // The merge for the split counts the o_proj prologue does not take (any
