@@ -151,3 +151,52 @@ def test_header_escapes_metadata_and_unknown_fields(tmp_path):
     assert dt == 0 and shape == (3,) and nbytes == 3
     assert ck.array("dup").view(np.int32).tolist() == [-9]    # a repeated name: the last entry wins
     ck.close()
+
+
+def test_mutated_headers_never_escape_the_data(tmp_path):
+    """Seeded byte mutations of a valid header (replace, delete, insert, a
+    wrong header length, a short data region): every file is either rejected
+    with an error or opens with tensors that lie wholly inside its data region
+    (the data bytes are 128..167, so a tensor's bytes name their own offset)."""
+    import random
+    from qwenasr_amd import QasrError
+    hdr = json.dumps({"__metadata__": {"format": "pt"},
+                      "a": {"dtype": "F32", "shape": [2, 3], "data_offsets": [0, 24]},
+                      "b": {"dtype": "BF16", "shape": [4], "data_offsets": [24, 32]},
+                      "c": {"dtype": "I64", "shape": [1], "data_offsets": [32, 40]}}).encode()
+    data = bytes(range(128, 168))
+    alphabet = b'{}[]",:0123456789-+.eE \\u"tfnaFBI'
+    r = random.Random(5)
+    p = tmp_path / "m.safetensors"
+    opened = 0
+    for _ in range(1500):
+        hh = bytearray(hdr)
+        for _ in range(r.randint(1, 3)):
+            k, i = r.randrange(4), r.randrange(len(hh) + 1)
+            if k == 0 and i < len(hh):
+                hh[i] = r.choice(alphabet)
+            elif k == 1 and i < len(hh):
+                del hh[i]
+            elif k == 2:
+                hh[i:i] = bytes([r.choice(alphabet)])
+            else:
+                hh[i:i] = bytes([r.randrange(256)])
+        dd = data[:r.choice([40, 40, 40, 39, 24, 0])]
+        hl = len(hh) if r.random() < 0.9 else r.randrange(len(hh) + 16)
+        p.write_bytes(struct.pack("<Q", hl) + bytes(hh) + dd)
+        try:
+            ck = _ck()(p, file=True)
+        except QasrError:
+            continue
+        opened += 1
+        for n in ck.names():
+            dt, shape, _, nbytes = ck.find(n)
+            raw = ck.array(n).view(np.uint8).reshape(-1)
+            assert raw.size == nbytes and nbytes <= len(dd), n
+            if dt != 0:
+                assert nbytes == int(np.prod(shape, dtype=np.int64)) * ck.array(n).dtype.itemsize, n
+            if nbytes:
+                o = int(raw[0]) - 128
+                assert 0 <= o and raw.tobytes() == dd[o:o + nbytes], n
+        ck.close()
+    assert opened > 0
