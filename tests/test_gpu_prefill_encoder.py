@@ -91,15 +91,18 @@ def test_prefill_attention(dev, orc, S, start):
     assert nrel(out.numpy().reshape(-1), ref) < 1e-5
 
 
-def test_bidirectional_attention(dev, orc):
+@pytest.mark.parametrize("T,H,hd,win", [(390, 14, 64, 104), (130, 8, 128, 48), (9, 2, 128, 100), (77, 3, 64, 16)])
+def test_bidirectional_attention(dev, orc, T, H, hd, win):
+    """Windowed attention of the encoder (head_dim 64) and the 128-dim
+    single-group form, ragged windows and fewer rows than one 16-row tile."""
     from qwenasr_amd import kernels as Kr
-    r = rng(77)
-    T, H, hd, win = 390, 14, 64, 104
+    r = rng(77 + T)
     q, k, v = (r.normal(0, 1, (T, H * hd)).astype(np.float32) for _ in range(3))
     out = dev.empty((T, H * hd), np.float32)
-    Kr.bidirectional_attention(out, dev.upload(q), dev.upload(k), dev.upload(v), T, H, hd, 0.125, win)
+    scale = float(np.float32(1) / np.sqrt(np.float32(hd)))
+    Kr.bidirectional_attention(out, dev.upload(q), dev.upload(k), dev.upload(v), T, H, hd, scale, win)
     ws = list(range(0, T, win)) + [T]
-    ref = orc.bidir_attention(q, k, v, T, H, hd, 0.125, ws)
+    ref = orc.bidir_attention(q, k, v, T, H, hd, scale, ws)
     assert nrel(out.numpy().reshape(-1), ref) < 1e-5
 
 
