@@ -188,9 +188,77 @@ __global__ __launch_bounds__(256) void k_im2col3x3s2_rows(float *__restrict__ co
     }
 }
 
+// the same patches by output row strips: a block owns the Wo positions of one
+// output row (chunk c, row oh) and walks the channels 32 at a time, staging
+// the three input rows 2 oh - 1 .. 2 oh + 1 of those channels in LDS (zero
+// columns on both sides, zero rows outside the image), so the input is read
+// in contiguous rows once per strip instead of 3-float runs per position, and
+// each position's 288 columns of the channel group go out as one contiguous run
+constexpr int IM2COL_ICB = 32, IM2COL_XW = 128;
+__global__ __launch_bounds__(256) void k_im2col3x3s2_strip(float *__restrict__ cols, const float *__restrict__ in,
+                                                           int C, int H, int W, int64_t cs, int64_t chs, int64_t rs,
+                                                           int Ho, int Wo) {
+    // rows padded to an odd length so that the 9 taps of consecutive columns
+    // fall in different LDS banks
+    __shared__ float T[IM2COL_ICB][3][IM2COL_XW + 1];
+    const int P = C * 9;
+    const int c = blockIdx.x / Ho, oh = blockIdx.x % Ho;
+    const float *src = in + c * cs;
+    float *dst = cols + (int64_t)blockIdx.x * Wo * P;
+    const int XW = W + 2;
+    // the Wo x nq columns of one channel group; nq is a constant for full groups
+    auto emit = [&](int icb, int nq) {
+        for (int i = threadIdx.x; i < Wo * nq; i += 256) {
+            const int ow = i / nq, q = i - ow * nq;
+            const int icl = q / 9, r9 = q - 9 * icl, ki = r9 / 3, kj = r9 - 3 * ki;
+            dst[(int64_t)ow * P + icb * 9 + q] = T[icl][ki][2 * ow + kj];
+        }
+    };
+    // grid y splits the channel groups, so that short strips still fill the chip
+    const int ngrp = (C + IM2COL_ICB - 1) / IM2COL_ICB, gpy = (ngrp + gridDim.y - 1) / gridDim.y;
+    const int ic_end = min(C, (int)(blockIdx.y + 1) * gpy * IM2COL_ICB);
+    for (int icb = blockIdx.y * gpy * IM2COL_ICB; icb < ic_end; icb += IM2COL_ICB) {
+        const int nb = min(IM2COL_ICB, C - icb);
+        __syncthreads();
+        // eight loads in flight per thread before their LDS stores
+        const int n = nb * 3 * XW;
+        for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 256) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * 256, ie = i < n ? i : 0;
+                const int x = ie % XW, r = ie / XW, ki = r % 3, icl = r / 3;
+                const int ih = 2 * oh + ki - 1, iw = x - 1;
+                const bool ok = i < n && ih >= 0 && ih < H && iw >= 0 && iw < W;
+                v[u] = src[ok ? (int64_t)(icb + icl) * chs + (int64_t)ih * rs + iw : 0];
+                v[u] = ok ? v[u] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * 256;
+                if (i < n) {
+                    const int x = i % XW, r = i / XW;
+                    T[r / 3][r % 3][x] = v[u];
+                }
+            }
+        }
+        __syncthreads();
+        if (nb == IM2COL_ICB) emit(icb, IM2COL_ICB * 9);
+        else emit(icb, nb * 9);
+    }
+}
+
 hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C, int H, int W, int64_t cs,
                               int64_t chs, int64_t rs, int Ho, int Wo, hipStream_t st) {
     const int64_t rows = (int64_t)n_chunks * Ho * Wo;
+    if (C * 9 >= 256 && W + 2 <= IM2COL_XW && Wo == (W - 1) / 2 + 1 && (int64_t)n_chunks * Ho < (1ll << 31)) {
+        // about 4096 blocks: strips x channel splits
+        const int strips = n_chunks * Ho, ngrp = (C + IM2COL_ICB - 1) / IM2COL_ICB;
+        const int cs_split = std::max(1, std::min(ngrp, (4096 + strips - 1) / strips));
+        hipLaunchKernelGGL(k_im2col3x3s2_strip, dim3((unsigned)strips, (unsigned)cs_split), dim3(256), 0, st, cols, in, C,
+                           H, W, cs, chs, rs, Ho, Wo);
+        return hipGetLastError();
+    }
     if (C * 9 >= 256 && rows < (1ll << 31)) {
         hipLaunchKernelGGL(k_im2col3x3s2_rows, dim3((unsigned)rows), dim3(256), 0, st, cols, in, C, H, W, cs, chs, rs,
                            Ho, Wo);
