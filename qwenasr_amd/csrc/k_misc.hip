@@ -513,7 +513,9 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
 // and wave (g, ks) takes the 16-key sub-tiles ks, ks + KS, ... of every
 // KS x 16-key chunk staged in LDS, with an online softmax of its own; the KS
 // states of a head are merged through LDS at the end.  The next chunk's K/V
-// loads go out into registers before the current chunk's MFMA work.  Per sub-tile the wave
+// loads go out into registers before the current chunk's MFMA work.  With
+// kv_div = 2 (and G = 1) a block owns one query head x and reads KV head x / 2,
+// which gives the 8 waves of a 128-dim head 8 key splits.  Per sub-tile the wave
 // forms S^T = K Q^T (16 keys x 16 queries; lane l holds keys 4 (l / 16) + i
 // of query l % 16, the dot over d split as lane group l / 16 covering dims
 // [l/16 HD/4, +HD/4)), so the softmax of a query reduces over the lane's 4
@@ -535,7 +537,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = wid / KS, ks = wid % KS;
-    const int kvh = blockIdx.x, q0 = blockIdx.y * 16;
+    // causal: tiles in reverse, so that the blocks with the most keys start first
+    const int kvh = blockIdx.x, q0 = (a.window > 0 ? blockIdx.y : gridDim.y - 1 - blockIdx.y) * 16;
     const int h = kvh * G + g;
     const int lq = lane & 15, lg = lane >> 4;
     // key range of this lane's query (for the S^T masks) and of the block
@@ -572,7 +575,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
 #pragma unroll
     for (int n = 0; n < NT; n++) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     float m = -INFINITY, l = 0.0f;
-    const float *kb = a.k + (int64_t)kvh * a.k_hs, *vb = a.v + (int64_t)kvh * a.k_hs;
+    const int kv_head = a.kv_div > 1 ? kvh / a.kv_div : kvh;
+    const float *kb = a.k + (int64_t)kv_head * a.k_hs, *vb = a.v + (int64_t)kv_head * a.k_hs;
     // K/V of a chunk pass through registers: the loads of chunk c0 + CH are
     // issued before the MFMA work on chunk c0, so their latency overlaps it.
     // Rows past the range repeat row blo (their scores are masked).
@@ -688,12 +692,17 @@ hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim,
                          (uintptr_t)a.k % 16 == 0 && (uintptr_t)a.v % 16 == 0;
     if (!simt && aligned && (a.G == 1 || a.G == 2) && (head_dim == 128 || head_dim == 64)) {
         const dim3 grid(n_kv_heads, (a.n_q + 15) / 16);
-        // 8 waves (4 key splits per head pair) for the 128-dim decoder heads,
-        // 4 for the 64-dim encoder heads: measured 32.6 against 35.7 us for the
-        // 404-row prefill and 12.4 against 13.6 us for the encoder windows
+        // 128-dim decoder heads (G = 2): one query head per block, its 8 waves
+        // 8 key splits (KV head x / 2); measured 30.0 us for the 404-row prefill
+        // against 32.5 with both heads of a KV head in one 8-wave block and 35.7
+        // with 4 waves.  64-dim encoder heads: 4 waves (12.4 us against 13.6 at 8).
 #define QAM(HDV, GV, NWV) hipLaunchKernelGGL((k_attn_mfma<HDV, GV, NWV>), grid, dim3(NWV * 64), 0, st, a);
-        if (head_dim == 128 && a.G == 2) { QAM(128, 2, 8) }
-        else if (head_dim == 128) { QAM(128, 1, 8) }
+        if (head_dim == 128 && a.G == 2) {
+            AttnRowsArgs b = a;
+            b.kv_div = 2;
+            const dim3 grid1(n_kv_heads * 2, (a.n_q + 15) / 16);
+            hipLaunchKernelGGL((k_attn_mfma<128, 1, 8>), grid1, dim3(512), 0, st, b);
+        } else if (head_dim == 128) { QAM(128, 1, 8) }
         else if (a.G == 2) { QAM(64, 2, 4) }
         else { QAM(64, 1, 4) }
 #undef QAM

@@ -199,6 +199,7 @@ struct AttnRowsArgs {
     int q_offset;             // causal: query i sees keys [0, q_offset + i]
     int window;               // > 0: query i sees its window [w*window, min((w+1)*window, n_k))
     float scale;
+    int kv_div;               // set by launch_attn_rows: block x reads KV head x / kv_div (0 = 1)
 };
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st);
 hipError_t launch_layer_norm_rows(float *out, const float *x, const float *w, const float *b, int64_t seq,
