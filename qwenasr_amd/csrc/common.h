@@ -207,16 +207,8 @@ __device__ __forceinline__ float fast_exp_ref(float x) {
     return __fmul_rn(ei, p);
 }
 
-__device__ __forceinline__ float gelu_ref(float v, int64_t idx, int64_t n) {
-    bool vec = true;
-    if (n > 4096) {
-        const int64_t chunk = (n + 15) / 16;
-        const int64_t c = idx / chunk, start = c * chunk;
-        const int64_t len = min(chunk, n - start);
-        vec = (idx - start) < len - (len % 8);
-    } else {
-        vec = idx < n - (n % 8);
-    }
+// the two element paths of gelu (avx.rs:536-563): 8-wide fast_exp / scalar libm tanh
+__device__ __forceinline__ float gelu_at(float v, bool vec) {
     if (vec) {
         const float v3 = __fmul_rn(__fmul_rn(v, v), v);
         const float inner = __fmul_rn(0.7978845608028654f, fmaf(0.044715f, v3, v));
@@ -228,5 +220,38 @@ __device__ __forceinline__ float gelu_ref(float v, int64_t idx, int64_t n) {
     const float inner = __fmul_rn(0.7978845608028654f, __fadd_rn(v, __fmul_rn(0.044715f, x3)));
     return __fmul_rn(__fmul_rn(0.5f, v), __fadd_rn(1.0f, tanhf(inner)));
 }
+
+__device__ __forceinline__ float gelu_ref(float v, int64_t idx, int64_t n) {
+    bool vec = true;
+    if (n > 4096) {
+        const int64_t chunk = (n + 15) / 16;
+        const int64_t c = idx / chunk, start = c * chunk;
+        const int64_t len = min(chunk, n - start);
+        vec = (idx - start) < len - (len % 8);
+    } else {
+        vec = idx < n - (n % 8);
+    }
+    return gelu_at(v, vec);
+}
+
+// gelu_ref's path choice for indices idx in [lo, lo + span) with span no larger
+// than one per-thread chunk (so the range meets at most two chunks), computed
+// once: vec(idx) = idx < b1 ? idx < ts0 : idx < ts1
+struct GeluSpan {
+    int64_t b1, ts0, ts1;
+    __device__ __forceinline__ GeluSpan(int64_t lo, int64_t n) {
+        if (n > 4096) {
+            const int64_t chunk = (n + 15) / 16, s0 = lo / chunk * chunk;
+            const int64_t len0 = min(chunk, n - s0), s1 = s0 + chunk, len1 = max((int64_t)0, min(chunk, n - s1));
+            b1 = s1;
+            ts0 = s0 + len0 - len0 % 8;
+            ts1 = s1 + len1 - len1 % 8;
+        } else {
+            b1 = INT64_MAX;
+            ts0 = ts1 = n - n % 8;
+        }
+    }
+    __device__ __forceinline__ bool vec(int64_t idx) const { return idx < b1 ? idx < ts0 : idx < ts1; }
+};
 
 }  // namespace qasr

@@ -258,11 +258,18 @@ static int conv_stem(qasr_encoder *e, const float *mel, int64_t frames, int64_t 
     float *a2 = a1 + (int64_t)n_chunks * C * h1 * w1;
     float *a3 = a2 + (int64_t)n_chunks * C * h2 * w2;
     float *rsh = a3 + (int64_t)n_chunks * C * h3 * w3;
-    // conv1: input (chunk c, ic 0, ih, iw) = mel[ih * frames + f0 + c * chunk + iw]
-    LAUNCHCHK(launch_im2col3x3s2(cols, mel + f0, n_chunks, 1, 128, cw, e->c.chunk_size, 0, frames, h1, w1, st),
-              "im2col1");
-    TRY(egemm(e, cols, 9, e->conv1_w, 9, a1, 0, n_chunks * h1 * w1, C, 9, e->conv1_b, EPI_TRANS | EPI_GELU,
-              (int64_t)C * h1 * w1, h1 * w1));
+    // conv1: input (chunk c, ic 0, ih, iw) = mel[ih * frames + f0 + c * chunk + iw]; computed
+    // directly (9 taps) when the chunk's input plane fits the kernel's LDS, else as a GEMM
+    if (130 * (cw + 2) <= 13312 && C >= 16) {
+        LAUNCHCHK(launch_conv1_direct(a1, mel + f0, n_chunks, e->c.chunk_size, frames, 128, cw, e->conv1_w,
+                                      e->conv1_b, C, h1, w1, st),
+                  "conv1");
+    } else {
+        LAUNCHCHK(launch_im2col3x3s2(cols, mel + f0, n_chunks, 1, 128, cw, e->c.chunk_size, 0, frames, h1, w1, st),
+                  "im2col1");
+        TRY(egemm(e, cols, 9, e->conv1_w, 9, a1, 0, n_chunks * h1 * w1, C, 9, e->conv1_b, EPI_TRANS | EPI_GELU,
+                  (int64_t)C * h1 * w1, h1 * w1));
+    }
     LAUNCHCHK(launch_im2col3x3s2(cols, a1, n_chunks, C, h1, w1, (int64_t)C * h1 * w1, (int64_t)h1 * w1, w1, h2, w2,
                                  st),
               "im2col2");

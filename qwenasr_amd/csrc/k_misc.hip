@@ -271,6 +271,73 @@ hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C,
     return hipGetLastError();
 }
 
+// First convolution of the stem (one input channel, 3x3, stride 2, pad 1) +
+// bias + GELU computed directly (conv2d, mod.rs:1077-1154, then gelu): a
+// block stages one chunk's padded input plane in LDS and produces CONV1_OCB
+// output channels of it: a thread holds one position's 9 taps in registers
+// and walks the block's channels.  Each output is the f32 FMA chain over the
+// taps in im2col column order (ki, kj), plus the bias, then gelu at its index
+// in the chunk's [C][Ho][Wo] output (the path choice of gelu_ref, hoisted per
+// channel by GeluSpan).  Outputs go to out + c * C * Ho * Wo.
+constexpr int CONV1_OCB = 16, CONV1_LDS = 13312;
+__global__ __launch_bounds__(256) void k_conv1_direct(float *__restrict__ out, const float *__restrict__ in,
+                                                      int64_t cs, int64_t rs, int H, int W,
+                                                      const uint16_t *__restrict__ w, const float *__restrict__ bias,
+                                                      int C, int Ho, int Wo) {
+    __shared__ float X[CONV1_LDS];
+    const int c = blockIdx.x, XW = W + 2;
+    const float *src = in + c * cs;
+    for (int i = threadIdx.x; i < (H + 2) * XW; i += 256) {
+        const int r = i / XW, x = i - r * XW, ih = r - 1, iw = x - 1;
+        X[i] = (ih >= 0 && ih < H && iw >= 0 && iw < W) ? src[(int64_t)ih * rs + iw] : 0.0f;
+    }
+    __syncthreads();
+    const int plane = Ho * Wo;
+    const int64_t n = (int64_t)C * plane;
+    float *dst = out + (int64_t)c * n;
+    // this block's channels: weights and gelu path choices (plane <= n / 16, C >= 16)
+    const int oc0 = blockIdx.y * CONV1_OCB, noc = min(CONV1_OCB, C - oc0);
+    __shared__ float wsh[CONV1_OCB][10];
+    __shared__ int64_t gsh[CONV1_OCB][3];
+    if (threadIdx.x < noc * 9) {
+        const int o = threadIdx.x / 9, k = threadIdx.x % 9;
+        wsh[o][k] = bf16_to_f32(w[(oc0 + o) * 9 + k]);
+    } else if (threadIdx.x >= 160 && threadIdx.x < 160 + noc) {
+        const int o = threadIdx.x - 160;
+        const GeluSpan gs((int64_t)(oc0 + o) * plane, n);
+        wsh[o][9] = bias[oc0 + o];
+        gsh[o][0] = gs.b1; gsh[o][1] = gs.ts0; gsh[o][2] = gs.ts1;
+    }
+    __syncthreads();
+    // each thread: one position's 9 taps in registers, then every channel of the block
+    for (int sp = threadIdx.x; sp < plane; sp += 256) {
+        const int oh = sp / Wo, ow = sp - oh * Wo;
+        const float *xp = X + 2 * oh * XW + 2 * ow;
+        float xv[9];
+#pragma unroll
+        for (int ki = 0; ki < 3; ki++)
+#pragma unroll
+            for (int kj = 0; kj < 3; kj++) xv[ki * 3 + kj] = xp[ki * XW + kj];
+        for (int o = 0; o < noc; o++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 9; k++) acc = fmaf(xv[k], wsh[o][k], acc);
+            const int64_t gi = (int64_t)(oc0 + o) * plane + sp;
+            const bool vec = gi < gsh[o][0] ? gi < gsh[o][1] : gi < gsh[o][2];
+            dst[gi] = gelu_at(__fadd_rn(acc, wsh[o][9]), vec);
+        }
+    }
+}
+
+hipError_t launch_conv1_direct(float *out, const float *in, int n_chunks, int64_t cs, int64_t rs, int H, int W,
+                               const uint16_t *w, const float *bias, int C, int Ho, int Wo, hipStream_t st) {
+    if ((H + 2) * (W + 2) > CONV1_LDS || Ho != (H - 1) / 2 + 1 || Wo != (W - 1) / 2 + 1 || n_chunks <= 0 || C < 16)
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned)n_chunks, (unsigned)((C + CONV1_OCB - 1) / CONV1_OCB));
+    hipLaunchKernelGGL(k_conv1_direct, grid, dim3(256), 0, st, out, in, cs, rs, H, W, w, bias, C, Ho, Wo);
+    return hipGetLastError();
+}
+
 // [chunk][C][F][T] -> [chunk * T][C * F] with column ch * F + f (encoder.rs:265-277)
 __global__ __launch_bounds__(256) void k_conv_reshape(float *__restrict__ out, const float *__restrict__ in,
                                                       int n_chunks, int C, int F, int T) {

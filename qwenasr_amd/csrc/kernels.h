@@ -210,6 +210,10 @@ hipError_t launch_add_periodic(float *y, const float *table, int64_t rows, int c
 hipError_t launch_im2col3x3s2(float *cols, const float *in, int n_chunks, int C, int H, int W, int64_t cs,
                               int64_t chs, int64_t rs, int Ho, int Wo, hipStream_t st);
 hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C, int F, int T, hipStream_t st);
+// stem conv1 + bias + GELU, direct (input element (c, ih, iw) at in + c * cs + ih * rs + iw;
+// (H + 2) * (W + 2) <= 13312, Ho / Wo the stride-2 output sizes, C >= 16)
+hipError_t launch_conv1_direct(float *out, const float *in, int n_chunks, int64_t cs, int64_t rs, int H, int W,
+                               const uint16_t *w, const float *bias, int C, int Ho, int Wo, hipStream_t st);
 // idle one wave for `us` microseconds (timing helper)
 hipError_t launch_delay(int us, hipStream_t st);
 // the prefill's q/k per-head norm + RoPE and K/V cache write (one launch)
