@@ -223,7 +223,12 @@ __device__ __forceinline__ float gelu_at(float v, bool vec) {
 
 __device__ __forceinline__ float gelu_ref(float v, int64_t idx, int64_t n) {
     bool vec = true;
-    if (n > 4096) {
+    if (n > 4096 && n < (int64_t)1 << 31) {
+        // the same arithmetic in 32 bits (a 64-bit division is a long software sequence)
+        const uint32_t un = (uint32_t)n, ui = (uint32_t)idx, chunk = (un + 15) / 16;
+        const uint32_t start = ui / chunk * chunk, len = min(chunk, un - start);
+        vec = ui - start < len - len % 8;
+    } else if (n > 4096) {
         const int64_t chunk = (n + 15) / 16;
         const int64_t c = idx / chunk, start = c * chunk;
         const int64_t len = min(chunk, n - start);
