@@ -217,11 +217,16 @@ int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_de
                           int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
 /* Decoder::load (decoder.rs:70-167) from a checkpoint: the reference's tensor
  * names; matrices BF16 (shapes checked against cfg), norms F32 or BF16.  A
- * thinker.lm_head.weight with vocab rows is packed as the int8 decode head;
- * any thinker.lm_head.weight also becomes the prefill-logits head (as
- * qasr_hip_decoder_set_lm_head). */
+ * thinker.lm_head.weight [rows, hidden] of any row count (vocab, or the forced
+ * aligner's classify_num, config.rs:86-88, 145-150) is packed as the int8
+ * decode head, whose argmax then ranges over those rows, and becomes the
+ * prefill-logits head (as qasr_hip_decoder_set_lm_head) (decoder.rs:143-157);
+ * without it both heads are the tied embedding. */
 int qasr_hip_decoder_load_st(qasr_hip *h, const qasr_st *st, const qasr_dec_config *cfg, int round_mode,
                              int64_t max_seq, int kv_bf16, qasr_decoder **out);
+/* Rows of the int8 decode head (cfg.lm_head_dim(), config.rs:86-88): vocab for
+ * a tied head, the separate head's rows otherwise; -1 for a null decoder. */
+int64_t qasr_hip_decoder_head_rows(const qasr_decoder *d);
 void qasr_hip_decoder_free(qasr_decoder *d);
 /* decoder_prefill (decoder.rs:455-547): host f32 embeddings [seq_len, hidden] */
 int qasr_hip_decoder_prefill(qasr_decoder *d, const float *embeds, int64_t seq_len);

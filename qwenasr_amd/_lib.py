@@ -147,6 +147,7 @@ _SIGS = {
     "qasr_hip_stream_stats": (C.c_int, [P, P]),
     "qasr_hip_decoder_set_lm_head": (C.c_int, [P, P, I64]),
     "qasr_hip_decoder_logits_dim": (I64, [P]),
+    "qasr_hip_decoder_head_rows": (I64, [P]),
     "qasr_hip_decoder_prefill_logits": (C.c_int, [P, P, I64, P]),
     "qasr_hip_decoder_prefill_argmax": (C.c_int, [P, P, I64, P, I64, P]),
     "qasr_hip_argmax_f32_rows": (C.c_int, [P, P, I64, I64, I64, P]),

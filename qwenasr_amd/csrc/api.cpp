@@ -21,6 +21,29 @@ int qasr_fail(int code, const std::string &msg) {
 
 extern "C" const char *qasr_hip_last_error(void) { return g_err.c_str(); }
 
+int dbuf_ensure(DevBuf &b, size_t bytes) {
+    if (bytes <= b.cap) return QASR_OK;
+    if (b.p) {
+        HIPCHK(hipDeviceSynchronize());   // work queued on the old buffer has finished
+        (void)hipFree(b.p);
+    }
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t want = std::max<size_t>((bytes + 255) / 256 * 256, 4096);
+    if (hipMalloc(&b.p, want) != hipSuccess) {
+        b.p = nullptr;
+        return qasr_fail(QASR_ERR_NOMEM, "device allocation of " + std::to_string(want) + " bytes failed");
+    }
+    b.cap = want;
+    return QASR_OK;
+}
+
+void dbuf_release(DevBuf &b) {
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+}
+
 extern "C" int qasr_hip_device_count(int *n) {
     if (!n) return qasr_fail(QASR_ERR_INVALID, "n is null");
     HIPCHK(hipGetDeviceCount(n));

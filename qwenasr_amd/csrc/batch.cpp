@@ -56,6 +56,7 @@ struct qasr_batch {
     // keeps the kernel at 4 waves per SIMD, which measured faster at 32 streams
     int attn_depth = 1;
     std::map<int, hipGraphExec_t> graphs;                // by split count
+    DevBuf prefill_rows;                                 // batch_prefill's staged rows, kept between calls
     std::vector<void *> allocs;
 };
 
@@ -76,6 +77,7 @@ extern "C" void qasr_hip_batch_free(qasr_batch *b) {
     (void)hipSetDevice(b->d->h->device);
     (void)hipStreamSynchronize(b->d->h->stream);
     for (auto &g : b->graphs) (void)hipGraphExecDestroy(g.second);
+    dbuf_release(b->prefill_rows);
     for (void *p : b->allocs) (void)hipFree(p);
     delete b;
 }
@@ -119,7 +121,7 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     if (c.n_heads != 16 || c.n_kv_heads != 8 || c.head_dim != 128 || d->kv_bf16)
         return qasr_fail(QASR_ERR_INVALID, "batch_create: needs the 16/8-head, head_dim 128 decoder with an f32 KV cache");
     auto steps_ok = [](int64_t k) { return k % 1024 == 0 && (k == 1024 || k == 2048 || k == 3072 || k == 4096 || k == 6144); };
-    if (!steps_ok(c.hidden) || !steps_ok(c.intermediate) || c.hidden > 4096 || c.vocab % 16)
+    if (!steps_ok(c.hidden) || !steps_ok(c.intermediate) || c.hidden > 4096 || d->lm_i8_rows % 16)
         return qasr_fail(QASR_ERR_INVALID, "batch_create: hidden and intermediate must be 1024, 2048, 3072, 4096 or 6144");
     qasr_batch *b = new qasr_batch();
     b->d = d;
@@ -184,8 +186,9 @@ extern "C" int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float
     if (stream < 0 || stream >= b->B) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: stream out of range");
     if (b->len[stream] + seq_len > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: capacity exceeded");
     const int64_t H = d->c.hidden, le = stream_layer_elems(b);
-    float *emb = nullptr;
-    HIPCHK(hipMalloc(&emb, sizeof(float) * seq_len * H));
+    int rc0 = dbuf_ensure(b->prefill_rows, sizeof(float) * seq_len * H);
+    if (rc0 != QASR_OK) return rc0;
+    float *emb = b->prefill_rows.as<float>();
     hipError_t e = hipMemcpyAsync(emb, embeds, sizeof(float) * seq_len * H, hipMemcpyHostToDevice, d->h->stream);
     // swap in the stream's view: base, layer stride, capacity, length
     void *kc0 = d->kc, *vc0 = d->vc;
@@ -201,8 +204,8 @@ extern "C" int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float
     d->kv_layer_stride = ls0;
     d->max_seq = ms0;
     d->len = len0;
-    (void)hipStreamSynchronize(d->h->stream);
-    (void)hipFree(emb);
+    if (hipStreamSynchronize(d->h->stream) != hipSuccess && rc == QASR_OK)
+        rc = qasr_fail(QASR_ERR_HIP, "batch_prefill: stream failed");
     if (rc == QASR_OK) b->len[stream] += seq_len;
     return rc;
 }
@@ -292,7 +295,7 @@ static int batch_enqueue_step(qasr_batch *b, int n_split, int kind = -1) {
         LAUNCHCHK(launch_quant_rows(b->x, d->norm, c.eps, H, B, b->xq, b->xs, st), "batch final norm");
     if (on(BK_LM) || on(BK_LM_FINISH)) {
         BatchMvArgs am{};
-        am.xq = b->xq; am.xs = b->xs; am.w = d->lm; am.ws = d->lm_s; am.K = H; am.N = c.vocab; am.B = B;
+        am.xq = b->xq; am.xs = b->xs; am.w = d->lm; am.ws = d->lm_s; am.K = H; am.N = (int)d->lm_i8_rows; am.B = B;
         am.part_val = b->am_val; am.part_idx = b->am_idx;
         LAUNCHCHK(launch_argmax_batch(am, ARGMAX_BLOCKS, b->state, b->token_log, b->max_steps, d->rc, d->rs,
                                       b->rope_cur, (int)b->max_seq, b->gpb_table, b->gpb_dev, st, on(BK_LM),

@@ -135,14 +135,22 @@ __device__ __forceinline__ int ld_agent(const int *p) {
 }
 // wait until every memory operation this thread issued has completed
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
-// counter bump after the block's stores completed; true in the last block to arrive
+// Counter bump after the block's stores; true in the last block to arrive.
+// Ordering: every thread waits for its own stores (the barrier does not wait
+// for vector memory), thread 0 publishes them with an agent-scope release
+// fence and an acq_rel bump, and the threads of the last block acquire at
+// agent scope before they read what the other blocks wrote.
 __device__ __forceinline__ bool arrive_last(unsigned *ctr, unsigned n_blocks, int *flag_lds) {
     wait_all_mem();
     __syncthreads();
-    if (threadIdx.x == 0)
-        *flag_lds = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_blocks - 1;
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        *flag_lds = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == n_blocks - 1;
+    }
     __syncthreads();
-    return *flag_lds != 0;
+    const bool last = *flag_lds != 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return last;
 }
 __device__ __forceinline__ void reset_counter(unsigned *ctr) {
     __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -47,11 +47,11 @@ static int pack(qasr_decoder *d, const uint16_t *bf, int64_t n, int64_t k, int8_
 
 extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
                                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
-    return decoder_load_impl(h, cfg, w, nullptr, round_mode, max_seq, kv_bf16, out);
+    return decoder_load_impl(h, cfg, w, nullptr, 0, round_mode, max_seq, kv_bf16, out);
 }
 
 int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w, const uint16_t *lm_head,
-                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
+                      int64_t lm_rows, int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
     CHECK_H(h);
     if (!cfg || !w || !out || !w->embed || !w->norm || !w->layers)
         return qasr_fail(QASR_ERR_INVALID, "decoder_load: null argument");
@@ -66,6 +66,8 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
                          "hidden/intermediate multiples of 64)");
     if (round_mode != QASR_ROUND_HALF_AWAY && round_mode != QASR_TRUNC)
         return qasr_fail(QASR_ERR_INVALID, "decoder_load: unknown round_mode");
+    if (lm_head && (lm_rows <= 0 || lm_rows > (1 << 30)))
+        return qasr_fail(QASR_ERR_INVALID, "decoder_load: bad LM head row count");
     for (int l = 0; l < c.n_layers; l++) {
         const qasr_dec_layer &L = w->layers[l];
         if (!L.wq || !L.wk || !L.wv || !L.wo || !L.gate || !L.up || !L.down || !L.q_norm || !L.k_norm ||
@@ -86,7 +88,7 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
     // QASR_ATTN_WAVES=4|8: waves per decode-attention block (tuning)
     const char *aw = getenv("QASR_ATTN_WAVES");
     if (aw && (aw[0] == '4' || aw[0] == '8') && aw[1] == 0) d->attn_waves = aw[0] - '0';
-    int rc = decoder_build(d, w, lm_head);
+    int rc = decoder_build(d, w, lm_head, lm_head ? lm_rows : c.vocab);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
         return rc;
@@ -95,7 +97,7 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
     return QASR_OK;
 }
 
-int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head) {
+int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head, int64_t lm_rows) {
     const qasr_dec_config &c = d->c;
     const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd;
     const int64_t kvd = (int64_t)c.n_kv_heads * hd, I = c.intermediate, V = c.vocab;
@@ -136,23 +138,19 @@ int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm
         TRY(upload(d, D.in_norm, S.input_norm, sizeof(float) * H));
         TRY(upload(d, D.post_norm, S.post_attn_norm, sizeof(float) * H));
     }
-    // embedding table (bf16, kept for lookups) and the int8 LM head packed from
-    // it, or from a separate [vocab, hidden] head (decoder.rs:145-157)
+    // embedding table (bf16, kept for lookups) and the int8 decode head packed
+    // from it, or from a separate [lm_rows, hidden] head (decoder.rs:143-157:
+    // the forced aligner's head has classify_num rows)
     TRY(dalloc(d, &d->embed, V * H));
     TRY(stg.upload(d->embed, w->embed, B2 * V * H));
-    TRY(dalloc(d, &d->lm, V * H));
-    TRY(dalloc(d, &d->lm_s, V));
+    d->lm_i8_rows = lm_head ? lm_rows : V;
+    TRY(dalloc(d, &d->lm, d->lm_i8_rows * H));
+    TRY(dalloc(d, &d->lm_s, d->lm_i8_rows));
     if (lm_head) {
         uint16_t *tmp = nullptr;
-        if (hipMalloc(&tmp, B2 * V * H) != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "decoder: LM head staging");
-        int rc = stg.upload(tmp, lm_head, B2 * V * H);
-        if (rc == QASR_OK) {
-            hipError_t e = launch_pack_int8(tmp, V, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream);
-            if (e == hipSuccess) e = hipStreamSynchronize(d->h->stream);
-            if (e != hipSuccess) rc = qasr_fail(QASR_ERR_HIP, std::string("lm pack: ") + hipGetErrorString(e));
-        }
-        (void)hipFree(tmp);
-        if (rc != QASR_OK) return rc;
+        TRY(dalloc(d, &tmp, lm_rows * H));     // bf16 staging, freed with the decoder
+        TRY(stg.upload(tmp, lm_head, B2 * lm_rows * H));
+        LAUNCHCHK(launch_pack_int8(tmp, lm_rows, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream), "lm pack");
     } else {
         LAUNCHCHK(launch_pack_int8(d->embed, V, (int)H, d->round_mode, d->lm, d->lm_s, d->h->stream), "lm pack");
     }
@@ -215,6 +213,7 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
     (void)hipStreamSynchronize(d->h->stream);
     for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
     decoder_free_prefill(d);
+    dbuf_release(d->head_out);
     if (d->lm_bf16) (void)hipFree(d->lm_bf16);
     for (void *p : d->allocs) (void)hipFree(p);
     delete d;
@@ -316,12 +315,12 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     }
     if (want(5) || want(6)) {
         ArgmaxArgs am{};
-        am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = c.vocab;
+        am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = (int)d->lm_i8_rows;
         am.w = d->lm; am.ws = d->lm_s;
         am.part_val = d->am_val; am.part_idx = d->am_idx;
         am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
         am.rope_cos = d->rc; am.rope_sin = d->rs; am.rope_cur = d->rope_cur; am.max_pos = (int)d->max_seq;
-        LAUNCHCHK(launch_argmax(am, true, argmax_blocks(c.vocab), st, want(5), want(6)), "step argmax");
+        LAUNCHCHK(launch_argmax(am, true, argmax_blocks(d->lm_i8_rows), st, want(5), want(6)), "step argmax");
     }
     return QASR_OK;
 }
@@ -461,7 +460,7 @@ extern "C" int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, in
     const float *s = nullptr;
     int64_t rows = 0, cols = H;
     if (layer == -1) {
-        q = d->lm; s = d->lm_s; rows = c.vocab;
+        q = d->lm; s = d->lm_s; rows = d->lm_i8_rows;
     } else if (layer >= 0 && layer < c.n_layers && which >= 0 && which <= 5) {
         const DecLayerDev &L = d->L[layer];
         switch (which) {
@@ -594,7 +593,7 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
     d->len = len0;
     if (rc != QASR_OK) return rc;
     const double H = c.hidden, qd = (double)c.n_heads * c.head_dim, kvd = (double)c.n_kv_heads * c.head_dim;
-    const double I = c.intermediate, V = c.vocab, esz = d->kv_bf16 ? 2 : 4;
+    const double I = c.intermediate, V = (double)d->lm_i8_rows, esz = d->kv_bf16 ? 2 : 4;
     // algorithmic bytes: int8 weights N*K + scales 4N + activation 4K + output 4N (+4N read for += )
     const double nqkv = qd + 2 * kvd;
     const double bytes[QASR_PROFILE_KINDS] = {
@@ -604,7 +603,7 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
         2 * I * H + 8 * I + 4 * H + 4 * I,
         H * I + 4 * H + 4 * I + 8 * H,
         V * H + 4 * V + 4 * H,
-        8.0 * argmax_blocks(c.vocab)};
+        8.0 * argmax_blocks(d->lm_i8_rows)};
     for (int k = 0; k < QASR_PROFILE_KINDS; k++) {
         us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
         if (bytes_per_launch) bytes_per_launch[k] = bytes[k];

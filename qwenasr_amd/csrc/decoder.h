@@ -26,8 +26,9 @@ struct qasr_decoder {
     int64_t max_seq = 0, len = 0;
     std::vector<DecLayerDev> L;
     uint16_t *embed = nullptr;
-    int8_t *lm = nullptr;
+    int8_t *lm = nullptr;                       // int8 decode head [lm_i8_rows][hidden] + row scales
     float *lm_s = nullptr, *norm = nullptr;
+    int64_t lm_i8_rows = 0;                     // cfg.lm_head_dim(): vocab, or the aligner's classify_num
     uint16_t *lm_bf16 = nullptr;                // separate bf16 LM head for prefill logits (nullptr: tied embedding)
     int64_t lm_rows = 0;
     void *kc = nullptr, *vc = nullptr;          // [layer][kv_head][max_seq][hd]
@@ -48,14 +49,16 @@ struct qasr_decoder {
     int64_t step_pos = 0;                       // position of the next step to enqueue
     int32_t host_state[4] = {0, 0, 0, 0};
     PrefillBufs pf;
+    DevBuf head_out;                            // prefill_logits / prefill_argmax outputs, kept between calls
     std::vector<void *> allocs;
 };
 
-// lm_head (nullable): a separate bf16 [vocab, hidden] host head for the int8 LM head
-int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head);
-// qasr_hip_decoder_load with an optional separate int8 decode head (bf16 [vocab, hidden])
+// lm_head (nullable): a separate bf16 [lm_rows, hidden] host head, packed as
+// the int8 decode head instead of the tied embedding (decoder.rs:143-157)
+int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head, int64_t lm_rows);
+// qasr_hip_decoder_load with an optional separate head (bf16 [lm_rows, hidden])
 int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w, const uint16_t *lm_head,
-                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
+                      int64_t lm_rows, int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
 // enqueue one decode step; only_kind >= 0 launches only the kernels of that
 // kind (0 norm+qkv, 1 attention, 2 o_proj, 3 norm+gate_up, 4 down, 5 LM head)
 // The step is enqueued for position d->step_pos (the caller advances it).

@@ -41,6 +41,10 @@ struct qasr_encoder {
     // scratch (grown on demand)
     size_t scratch_bytes = 0;
     char *scratch = nullptr;
+    // per-call buffers of qasr_hip_mel / encoder_forward / transcribe_forced,
+    // kept between calls
+    DevBuf audio, mel, melsc, enc_out, embeds, toks;
+    hipEvent_t ev[5] = {};
     std::vector<void *> allocs;
 };
 
@@ -208,6 +212,9 @@ extern "C" void qasr_hip_encoder_free(qasr_encoder *e) {
     (void)hipSetDevice(e->h->device);
     (void)hipStreamSynchronize(e->h->stream);
     if (e->scratch) (void)hipFree(e->scratch);
+    for (DevBuf *b : {&e->audio, &e->mel, &e->melsc, &e->enc_out, &e->embeds, &e->toks}) dbuf_release(*b);
+    for (hipEvent_t v : e->ev)
+        if (v) (void)hipEventDestroy(v);
     for (void *p : e->allocs) (void)hipFree(p);
     delete e;
 }
@@ -383,10 +390,10 @@ extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, fl
     if (nf <= 0) return qasr_fail(QASR_ERR_INVALID, "mel: audio too short");
     *frames = nf;
     if (!mel_out) return QASR_OK;
-    float *dx = nullptr, *dm = nullptr, *sc = nullptr;
-    HIPCHK(hipMalloc(&dx, sizeof(float) * n));
-    HIPCHK(hipMalloc(&dm, sizeof(float) * 128 * nf));
-    HIPCHK(hipMalloc(&sc, sizeof(float) * mel_scratch_floats(nf)));
+    TRY(dbuf_ensure(e->audio, sizeof(float) * n));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf));
+    TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf)));
+    float *dx = e->audio.as<float>(), *dm = e->mel.as<float>(), *sc = e->melsc.as<float>();
     int rc = QASR_OK;
     if (hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
         rc = qasr_fail(QASR_ERR_HIP, "mel: upload failed");
@@ -394,10 +401,8 @@ extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, fl
     if (rc == QASR_OK &&
         hipMemcpyAsync(mel_out, dm, sizeof(float) * 128 * nf, hipMemcpyDeviceToHost, e->h->stream) != hipSuccess)
         rc = qasr_fail(QASR_ERR_HIP, "mel: download failed");
-    (void)hipStreamSynchronize(e->h->stream);
-    (void)hipFree(dx);
-    (void)hipFree(dm);
-    (void)hipFree(sc);
+    if (hipStreamSynchronize(e->h->stream) != hipSuccess && rc == QASR_OK)
+        rc = qasr_fail(QASR_ERR_HIP, "mel: stream failed");
     return rc;
 }
 
@@ -411,9 +416,9 @@ extern "C" int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64
     CHECK_H(e->h);
     if (!mel || frames <= 0 || !out) return qasr_fail(QASR_ERR_INVALID, "encoder_forward: bad arguments");
     const int64_t T = encoder_tokens(e, frames);
-    float *dm = nullptr, *dout = nullptr;
-    HIPCHK(hipMalloc(&dm, sizeof(float) * 128 * frames));
-    HIPCHK(hipMalloc(&dout, sizeof(float) * T * e->c.output_dim));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * frames));
+    TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * e->c.output_dim));
+    float *dm = e->mel.as<float>(), *dout = e->enc_out.as<float>();
     int rc = QASR_OK;
     if (hipMemcpyAsync(dm, mel, sizeof(float) * 128 * frames, hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
         rc = qasr_fail(QASR_ERR_HIP, "encoder_forward: upload failed");
@@ -421,9 +426,8 @@ extern "C" int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64
     if (rc == QASR_OK && hipMemcpyAsync(out, dout, sizeof(float) * T * e->c.output_dim, hipMemcpyDeviceToHost,
                                         e->h->stream) != hipSuccess)
         rc = qasr_fail(QASR_ERR_HIP, "encoder_forward: download failed");
-    (void)hipStreamSynchronize(e->h->stream);
-    (void)hipFree(dm);
-    (void)hipFree(dout);
+    if (hipStreamSynchronize(e->h->stream) != hipSuccess && rc == QASR_OK)
+        rc = qasr_fail(QASR_ERR_HIP, "encoder_forward: stream failed");
     return rc;
 }
 
@@ -434,6 +438,8 @@ static const int PREFIX_HEAD[] = {151644, 8948, 198};
 static const int PREFIX_TAIL[] = {151645, 198, 151644, 872, 198, 151669};
 static const int SUFFIX_BASE[] = {151670, 151645, 198, 151644, 77091, 198};
 
+// Every error after work has been queued leaves through one exit that waits
+// for the stream, so no kernel of this call is still running on return.
 extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
                                           int32_t n_steps, int32_t *tokens_out, double *times_ms) {
     if (!d || !e) return qasr_fail(QASR_ERR_INVALID, "transcribe: null model");
@@ -449,52 +455,43 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
     const int n_head = 9, n_tail = 6;
     const int64_t total = n_head + T + n_tail;
     if (total - 1 + n_steps > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "transcribe: KV cache capacity exceeded");
-    for (int t : PREFIX_HEAD) if (t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "transcribe: vocab too small for the prompt");
-    // device buffers for this call
-    float *dx = nullptr, *dmel = nullptr, *msc = nullptr, *enc = nullptr, *emb = nullptr;
-    int *dtok = nullptr;
-    HIPCHK(hipMalloc(&dx, sizeof(float) * n));
-    HIPCHK(hipMalloc(&dmel, sizeof(float) * 128 * nf));
-    HIPCHK(hipMalloc(&msc, sizeof(float) * mel_scratch_floats(nf)));
-    HIPCHK(hipMalloc(&enc, sizeof(float) * T * H));
-    HIPCHK(hipMalloc(&emb, sizeof(float) * total * H));
-    HIPCHK(hipMalloc(&dtok, sizeof(int) * (n_head + n_tail)));
     int toks[15];
     for (int i = 0; i < 3; i++) toks[i] = PREFIX_HEAD[i];
     for (int i = 0; i < 6; i++) toks[3 + i] = PREFIX_TAIL[i];
     for (int i = 0; i < 6; i++) toks[9 + i] = SUFFIX_BASE[i];
-    hipEvent_t ev[5];
-    for (auto &v : ev) HIPCHK(hipEventCreate(&v));
-    int rc = QASR_OK;
-    HIPCHK(hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, st));
-    HIPCHK(hipMemcpyAsync(dtok, toks, sizeof(toks), hipMemcpyHostToDevice, st));
-    HIPCHK(hipEventRecord(ev[0], st));
-    rc = mel_dev(e, dx, n, dmel, msc);
-    if (rc == QASR_OK) {
+    for (int t : toks)   // every prompt id is gathered from the embedding table on the device
+        if (t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "transcribe: vocab too small for the prompt");
+    TRY(dbuf_ensure(e->audio, sizeof(float) * n));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf));
+    TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf)));
+    TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * H));
+    TRY(dbuf_ensure(e->embeds, sizeof(float) * total * H));
+    TRY(dbuf_ensure(e->toks, sizeof(toks)));
+    for (hipEvent_t &v : e->ev)
+        if (!v) HIPCHK(hipEventCreate(&v));
+    float *dx = e->audio.as<float>(), *dmel = e->mel.as<float>(), *msc = e->melsc.as<float>();
+    float *enc = e->enc_out.as<float>(), *emb = e->embeds.as<float>();
+    int *dtok = e->toks.as<int>();
+    hipEvent_t *ev = e->ev;
+    auto body = [&]() -> int {
+        HIPCHK(hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, st));
+        HIPCHK(hipMemcpyAsync(dtok, toks, sizeof(toks), hipMemcpyHostToDevice, st));
+        HIPCHK(hipEventRecord(ev[0], st));
+        TRY(mel_dev(e, dx, n, dmel, msc));
         HIPCHK(hipEventRecord(ev[1], st));
         int64_t nt = 0;
-        rc = encoder_forward_dev(e, dmel, nf, enc, &nt);
-    }
-    if (rc == QASR_OK) {
+        TRY(encoder_forward_dev(e, dmel, nf, enc, &nt));
         HIPCHK(hipEventRecord(ev[2], st));
         LAUNCHCHK(launch_build_prompt(emb, d->embed, dtok, n_head, enc, (int)T, n_tail, H, st), "prompt");
         d->len = 0;
-        rc = decoder_prefill_dev(d, emb, total - 1);
-    }
-    if (rc == QASR_OK) {
+        TRY(decoder_prefill_dev(d, emb, total - 1));
         // first token from the last prompt row, then n_steps - 1 graph-replayed steps
-        rc = decoder_set_state(d, 0);
-        if (rc == QASR_OK) {
-            HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
-            rc = decoder_enqueue_step(d, false);
-            d->step_pos += 1;
-        }
-    }
-    if (rc == QASR_OK) {
+        TRY(decoder_set_state(d, 0));
+        HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
+        TRY(decoder_enqueue_step(d, false));
+        d->step_pos += 1;
         HIPCHK(hipEventRecord(ev[3], st));
-        for (int32_t s = 1; s < n_steps && rc == QASR_OK; s++) rc = decoder_run_embed_step(d);
-    }
-    if (rc == QASR_OK) {
+        for (int32_t s = 1; s < n_steps; s++) TRY(decoder_run_embed_step(d));
         HIPCHK(hipEventRecord(ev[4], st));
         HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
@@ -506,9 +503,9 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
                 times_ms[i] = ms;
             }
         }
-    }
-    (void)hipStreamSynchronize(st);
-    for (auto &v : ev) (void)hipEventDestroy(v);
-    for (void *p : {(void *)dx, (void *)dmel, (void *)msc, (void *)enc, (void *)emb, (void *)dtok}) (void)hipFree(p);
+        return QASR_OK;
+    };
+    const int rc = body();
+    if (rc != QASR_OK) (void)hipStreamSynchronize(st);
     return rc;
 }

@@ -25,6 +25,18 @@ struct qasr_hip {
 
 int qasr_fail(int code, const std::string &msg);
 
+// Device buffer owned by a model object and kept between calls: an entry point
+// calls hipMalloc only when it needs more bytes than any earlier call on the
+// same object (dbuf_ensure waits for the device before it frees the smaller
+// buffer), so repeated calls of one shape allocate nothing.
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    template <typename T> T *as() const { return reinterpret_cast<T *>(p); }
+};
+int dbuf_ensure(DevBuf &b, size_t bytes);
+void dbuf_release(DevBuf &b);
+
 #define CHECK_H(h)                                                                   \
     do {                                                                             \
         if (!(h)) return qasr_fail(QASR_ERR_INVALID, "handle is null");              \

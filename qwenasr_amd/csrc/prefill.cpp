@@ -153,6 +153,8 @@ extern "C" int qasr_hip_decoder_set_lm_head(qasr_decoder *d, const uint16_t *w, 
     return QASR_OK;
 }
 
+extern "C" int64_t qasr_hip_decoder_head_rows(const qasr_decoder *d) { return d ? d->lm_i8_rows : -1; }
+
 extern "C" int64_t qasr_hip_decoder_logits_dim(const qasr_decoder *d) {
     return d ? (d->lm_rows ? d->lm_rows : d->c.vocab) : -1;
 }
@@ -182,9 +184,8 @@ static int prefill_head_rows(qasr_decoder *d, const float *embeds, int64_t seq_l
     hipStream_t st = d->h->stream;
     // one device block: logits [n][out_dim], row list [n], argmax [n]
     const size_t y_bytes = (sizeof(float) * n * out_dim + 255) / 256 * 256;
-    char *buf = nullptr;
-    if (n > 0 && hipMalloc(&buf, y_bytes + 2 * sizeof(int32_t) * n) != hipSuccess)
-        return qasr_fail(QASR_ERR_NOMEM, "prefill_logits: device allocation failed");
+    if (n > 0) TRY(dbuf_ensure(d->head_out, y_bytes + 2 * sizeof(int32_t) * n));
+    char *buf = d->head_out.as<char>();
     float *y = reinterpret_cast<float *>(buf);
     int32_t *rows_dev = reinterpret_cast<int32_t *>(buf + y_bytes), *idx_dev = rows_dev + n;
     auto body = [&]() -> int {
@@ -209,7 +210,6 @@ static int prefill_head_rows(qasr_decoder *d, const float *embeds, int64_t seq_l
     };
     int rc = body();
     const hipError_t e = hipStreamSynchronize(st);
-    if (buf) (void)hipFree(buf);
     if (rc != QASR_OK) return rc;
     if (e != hipSuccess) return qasr_fail(QASR_ERR_HIP, "prefill_logits: stream failed");
     return QASR_OK;

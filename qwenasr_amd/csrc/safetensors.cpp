@@ -516,8 +516,10 @@ struct Loader {
 
 // Decoder::load (decoder.rs:70-167) from a checkpoint: names and layouts as
 // the reference reads them; matrices must be BF16, norms F32 or BF16.  A
-// "thinker.lm_head.weight" with vocab rows becomes the int8 decode head; with
-// any row count it is the prefill-logits head (the forced aligner's).
+// "thinker.lm_head.weight" of any row count (vocab, or the forced aligner's
+// classify_num: config.rs:86-88, 145-150) is both the int8 decode head and the
+// bf16 prefill-logits head (decoder.rs:143-157, 671); without it both are the
+// tied embedding.
 extern "C" int qasr_hip_decoder_load_st(qasr_hip *h, const qasr_st *st, const qasr_dec_config *cfg, int round_mode,
                                         int64_t max_seq, int kv_bf16, qasr_decoder **out) {
     CHECK_H(h);
@@ -563,7 +565,7 @@ extern "C" int qasr_hip_decoder_load_st(qasr_hip *h, const qasr_st *st, const qa
         lm_rows = t.shape[0];
     }
     qasr_decoder *d = nullptr;
-    int rc = decoder_load_impl(h, &c, &w, lm_rows == c.vocab ? lm : nullptr, round_mode, max_seq, kv_bf16, &d);
+    int rc = decoder_load_impl(h, &c, &w, lm, lm_rows, round_mode, max_seq, kv_bf16, &d);
     if (rc != QASR_OK) return rc;
     if (lm) {
         rc = qasr_hip_decoder_set_lm_head(d, lm, lm_rows);

@@ -45,28 +45,6 @@ constexpr int RESET_INTERVAL_CHUNKS = 45, RESET_CARRY_TOKENS = 24, MAX_ENC_WINDO
 constexpr int64_t SAMPLE_RATE = 16000, HOP = 160, WINDOW_FRAMES = 800;
 constexpr int DECODE_BURST = 4;
 
-// grow-only device buffer
-struct DevBuf {
-    void *p = nullptr;
-    size_t cap = 0;
-    template <typename T> T *as() { return reinterpret_cast<T *>(p); }
-};
-int ensure(DevBuf &b, size_t bytes) {
-    if (bytes <= b.cap) return QASR_OK;
-    if (b.p) (void)hipFree(b.p);
-    b.p = nullptr;
-    b.cap = 0;
-    const size_t want = std::max<size_t>(bytes, 4096);
-    if (hipMalloc(&b.p, want) != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "stream: device allocation failed");
-    b.cap = want;
-    return QASR_OK;
-}
-void release(DevBuf &b) {
-    if (b.p) (void)hipFree(b.p);
-    b.p = nullptr;
-    b.cap = 0;
-}
-
 // stream_tail_repeat_blocks (transcribe.rs:38-56): how many times a block of
 // some period <= max_period repeats at the tail; the best (reps, period)
 std::pair<int64_t, int64_t> tail_repeat_blocks(const std::vector<int32_t> &t, int64_t max_period) {
@@ -133,8 +111,12 @@ extern "C" int qasr_hip_stream_create(qasr_decoder *d, qasr_encoder *e, const qa
     *out = nullptr;
     if (encoder_output_dim(e) != d->c.hidden)
         return qasr_fail(QASR_ERR_INVALID, "stream_create: encoder output_dim != decoder hidden");
-    for (int32_t t : PREFIX)
-        if (t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream_create: vocab too small for the prompt");
+    // every prompt id is gathered from the embedding table on the device
+    int32_t top = 0;
+    for (int32_t t : PREFIX) top = std::max(top, t);
+    for (int32_t t : SUFFIX) top = std::max(top, t);
+    if (cfg && cfg->past_text_conditioning) top = std::max(top, TOKEN_ASR_TEXT);
+    if (top >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream_create: vocab too small for the prompt");
     qasr_stream *s = new qasr_stream();
     s->d = d;
     s->e = e;
@@ -149,7 +131,7 @@ extern "C" int qasr_hip_stream_create(qasr_decoder *d, qasr_encoder *e, const qa
 }
 
 static void release_windows(qasr_stream *s) {
-    for (auto &w : s->win) release(w.out);
+    for (auto &w : s->win) dbuf_release(w.out);
     s->win.clear();
 }
 
@@ -160,7 +142,7 @@ extern "C" void qasr_hip_stream_free(qasr_stream *s) {
     release_windows(s);
     for (DevBuf *b : {&s->partial, &s->embeds, &s->prev_embeds, &s->audio, &s->mel, &s->melsc, &s->enc_all,
                       &s->toks, &s->flags})
-        release(*b);
+        dbuf_release(*b);
     delete s;
 }
 
@@ -188,13 +170,13 @@ static int encode_slice(qasr_stream *s, const float *samples, int64_t ns, DevBuf
     *seq = 0;
     const int64_t nf = mel_frames_for(ns);
     if (nf <= 0) return QASR_OK;
-    TRY(ensure(s->audio, sizeof(float) * ns));
+    TRY(dbuf_ensure(s->audio, sizeof(float) * ns));
     HIPCHK(hipMemcpyAsync(s->audio.p, samples, sizeof(float) * ns, hipMemcpyHostToDevice, st));
-    TRY(ensure(s->mel, sizeof(float) * 128 * nf));
-    TRY(ensure(s->melsc, sizeof(float) * mel_scratch_floats(nf)));
+    TRY(dbuf_ensure(s->mel, sizeof(float) * 128 * nf));
+    TRY(dbuf_ensure(s->melsc, sizeof(float) * mel_scratch_floats(nf)));
     TRY(mel_dev(s->e, s->audio.as<float>(), ns, s->mel.as<float>(), s->melsc.as<float>()));
     const int64_t T = encoder_tokens(s->e, nf);
-    TRY(ensure(out, sizeof(float) * T * s->d->c.hidden));
+    TRY(dbuf_ensure(out, sizeof(float) * T * s->d->c.hidden));
     int64_t got = 0;
     TRY(encoder_forward_dev(s->e, s->mel.as<float>(), nf, out.as<float>(), &got));
     // the host copy of the audio slice must outlive the upload
@@ -306,12 +288,12 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
             int64_t seq = 0;
             TRY(encode_slice(s, samples + full_end, s->cursor - full_end, fresh, &seq));
             if (seq > 0) {
-                release(s->partial);
+                dbuf_release(s->partial);
                 s->partial = fresh;
                 s->partial_seq = partial_seq = seq;
                 s->last_partial_cursor = s->cursor;
             } else {
-                release(fresh);
+                dbuf_release(fresh);
             }
         }
     }
@@ -331,7 +313,7 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
             : 0;
     const int64_t total_seq = 9 + enc_len + 6 + n_prefix_tokens;
     const int64_t prefill_len = total_seq - 1;
-    TRY(ensure(s->enc_all, sizeof(float) * enc_len * H));
+    TRY(dbuf_ensure(s->enc_all, sizeof(float) * enc_len * H));
     int64_t off = 0;
     for (auto &w : s->win) {
         HIPCHK(hipMemcpyAsync(s->enc_all.as<float>() + off * H, w.out.p, sizeof(float) * w.seq * H,
@@ -346,9 +328,9 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
     toks.insert(toks.end(), s->raw.begin(), s->raw.begin() + n_prefix_tokens);
     for (int32_t t : toks)
         if (t < 0 || t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream: token id out of range");
-    TRY(ensure(s->toks, sizeof(int32_t) * toks.size()));
+    TRY(dbuf_ensure(s->toks, sizeof(int32_t) * toks.size()));
     HIPCHK(hipMemcpyAsync(s->toks.p, toks.data(), sizeof(int32_t) * toks.size(), hipMemcpyHostToDevice, st));
-    TRY(ensure(s->embeds, sizeof(float) * total_seq * H));
+    TRY(dbuf_ensure(s->embeds, sizeof(float) * total_seq * H));
     LAUNCHCHK(launch_build_prompt(s->embeds.as<float>(), d->embed, s->toks.as<int>(), 9, s->enc_all.as<float>(),
                                   (int)enc_len, (int)(6 + n_prefix_tokens), (int)H, st),
               "stream prompt");
@@ -357,7 +339,7 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
     int64_t reused = 0;
     if (s->prev_prefill_len > 0) {
         const int64_t cmp = std::min(prefill_len, s->prev_prefill_len);
-        TRY(ensure(s->flags, sizeof(int) * cmp));
+        TRY(dbuf_ensure(s->flags, sizeof(int) * cmp));
         LAUNCHCHK(launch_row_diff(s->embeds.as<float>(), s->prev_embeds.as<float>(), cmp, H, s->flags.as<int>(), st),
                   "stream row diff");
         std::vector<int> fl(cmp);

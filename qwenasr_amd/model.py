@@ -174,7 +174,7 @@ class Decoder:
         H, hd, I = c["hidden"], c["head_dim"], c["intermediate"]
         qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
         if layer == -1:
-            shape = (c["vocab"], H)
+            shape = (int(lib().qasr_hip_decoder_head_rows(self.d)), H)
         else:
             shape = [(qd, H), (kvd, H), (kvd, H), (H, qd), (2 * I, H), (H, I)][which]
         q = np.empty(shape, np.int8)

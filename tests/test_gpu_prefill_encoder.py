@@ -269,3 +269,28 @@ def test_transcribe_forced_tokens(dev, orc):
     assert toks_g.tolist() == res["tokens"].tolist()
     for m in (gd, ge, cd, ce):
         m.close()
+
+
+@pytest.mark.parametrize("vocab", [151650, 151670])
+def test_prompt_ids_beyond_vocab_rejected(dev, vocab):
+    """Every prompt id (transcribe.rs:13-15: up to 151670) is gathered from the
+    embedding table on the device, so a table with fewer rows is rejected with
+    QASR_ERR_INVALID before anything is launched: the offline driver at both
+    sizes, the stream at 151650 (PREFIX_TAIL's 151669) and 151670 (SUFFIX's
+    151670)."""
+    from qwenasr_amd import QasrError
+    from qwenasr_amd.model import Decoder, Encoder, Stream, transcribe_forced
+    from qwenasr_amd.synth import SynthDecoder, SynthEncoder, audio
+    wd = SynthDecoder(dict(n_layers=1, hidden=128, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=128,
+                           vocab=vocab, eps=1e-6, theta=1e6), seed=31)
+    we = SynthEncoder(dict(d_model=64, n_layers=1, n_heads=1, head_dim=64, ffn_dim=128, output_dim=128,
+                           chunk_size=100, n_window_infer=800, conv_hidden=32), seed=32)
+    d, e = Decoder(dev, wd, max_seq=256), Encoder(dev, we)
+    try:
+        with pytest.raises(QasrError, match="vocab too small"):
+            transcribe_forced(d, e, audio(16000, 33), 4)
+        with pytest.raises(QasrError, match="vocab too small"):
+            Stream(d, e)
+    finally:
+        d.close()
+        e.close()
