@@ -51,6 +51,7 @@ def main():
     ap.add_argument("--audio-seconds", type=float, default=30.0)
     ap.add_argument("--decode-steps", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-runs", type=int, default=3, help="timed CPU-baseline runs (median), after one warm-up")
     ap.add_argument("--profile-steps", type=int, default=20)
     ap.add_argument("--copy-calib-mb", type=int, default=0,
                     help="after the run, one device copy of this many MiB with the library's copy kernel "
@@ -133,11 +134,18 @@ def main():
         c0 = time.time()
         od = orc.OracleDecoder(wd, max_seq=1024)
         oe = orc.OracleEncoder(we)
-        print(f"[bench] cpu oracle model ready in {time.time() - c0:.1f}s ({threads} threads)",
-              file=sys.stderr, flush=True)
-        c1 = time.perf_counter()
-        res = orc.transcribe_forced(od, oe, x, args.decode_steps)
-        cpu_s = time.perf_counter() - c1
+        print(f"[bench] cpu oracle model ready in {time.time() - c0:.1f}s ({threads} threads, int8 dot "
+              f"{orc.int8_dot_kind()})", file=sys.stderr, flush=True)
+        # one warm-up, then the median of three full workloads
+        runs, res = [], None
+        for i in range(1 + args.cpu_runs):
+            c1 = time.perf_counter()
+            res = orc.transcribe_forced(od, oe, x, args.decode_steps)
+            dt = time.perf_counter() - c1
+            if i > 0:
+                runs.append(dt)
+            print(f"[bench] cpu {'warm-up' if i == 0 else 'run'} {i}: {dt:.2f} s", file=sys.stderr, flush=True)
+        cpu_s = float(np.median(runs))
         match = int(np.sum(res["tokens"] == toks))
         cpu_model = ""
         try:
@@ -147,13 +155,15 @@ def main():
             pass
         cpu = {"value": round(args.audio_seconds / cpu_s, 3), "unit": "x realtime", "cores": threads,
                "kind": "port",
-               "sample": f"the full workload once: {args.audio_seconds:.0f} s audio, {args.decode_steps} decode "
-                         f"steps (oracle C restatement, {threads} OpenMP threads, its own blocked AVX2 sgemm "
-                         f"for prefill/encoder/mel since the image has no OpenBLAS; stage ms "
-                         f"{[round(float(t), 1) for t in res['times_ms']]})",
+               "sample": f"the full workload ({args.audio_seconds:.0f} s audio, {args.decode_steps} decode steps), "
+                         f"median of {len(runs)} runs after one warm-up ({[round(r, 2) for r in runs]} s): the "
+                         f"oracle C restatement on {threads} OpenMP threads (the reference's MAX_THREADS cap), int8 "
+                         f"dot {orc.int8_dot_kind()}, its own blocked AVX2/FMA f32 sgemm for prefill/encoder/mel "
+                         f"(the image has no OpenBLAS); stage ms of the last run "
+                         f"{[round(float(t), 1) for t in res['times_ms']]}",
                "token_match": f"{match}/{args.decode_steps}",
                "host": {"cpu_model": cpu_model, "nproc": os.cpu_count()}}
-        print(f"[bench] cpu: {cpu_s:.2f} s, tokens identical {match}/{args.decode_steps}", file=sys.stderr,
+        print(f"[bench] cpu: median {cpu_s:.2f} s, tokens identical {match}/{args.decode_steps}", file=sys.stderr,
               flush=True)
         od.close()
         oe.close()

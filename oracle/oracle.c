@@ -94,11 +94,68 @@ float or_quantize_act(const float *x, int64_t k, int8_t *q) {
     return scale;
 }
 
-/* int32 dot of the 16-element blocks: order-free exact integer sum (neon.rs:723-749) */
+/* int32 dot of the 16-element blocks (neon.rs:723-749).  The sum is an exact
+ * integer, so any order gives the same value; x86 SIMD restates the NEON SDOT
+ * loop.  a is the quantized activation (|a| <= 127): |a| (u8) times b with a's
+ * sign moved onto it is a*b, and a pair of such products is at most
+ * 2 * 127 * 127 < 2^15, so maddubs never saturates.  AVX-512 VNNI when the
+ * host has it, else AVX2 (the build's baseline). */
+#include <immintrin.h>
+
+__attribute__((target("avx512f,avx512bw,avx512vnni")))
+static int32_t dot_i8_vnni512(const int8_t *a, const int8_t *b, int64_t k16) {
+    __m512i acc = _mm512_setzero_si512();
+    int64_t i = 0;
+    for (; i + 64 <= k16; i += 64) {
+        const __m512i va = _mm512_loadu_si512((const void *)(a + i));
+        const __m512i vb = _mm512_loadu_si512((const void *)(b + i));
+        const __mmask64 neg = _mm512_movepi8_mask(va);
+        const __m512i sb = _mm512_mask_sub_epi8(vb, neg, _mm512_setzero_si512(), vb);
+        acc = _mm512_dpbusd_epi32(acc, _mm512_abs_epi8(va), sb);
+    }
+    int32_t s = _mm512_reduce_add_epi32(acc);
+    for (; i < k16; i++) s += (int32_t)a[i] * (int32_t)b[i];
+    return s;
+}
+
+__attribute__((target("avx2")))
+static int32_t dot_i8_avx2(const int8_t *a, const int8_t *b, int64_t k16) {
+    __m256i acc = _mm256_setzero_si256();
+    const __m256i ones = _mm256_set1_epi16(1);
+    int64_t i = 0;
+    for (; i + 32 <= k16; i += 32) {
+        const __m256i va = _mm256_loadu_si256((const __m256i *)(a + i));
+        const __m256i vb = _mm256_loadu_si256((const __m256i *)(b + i));
+        const __m256i p = _mm256_maddubs_epi16(_mm256_abs_epi8(va), _mm256_sign_epi8(vb, va));
+        acc = _mm256_add_epi32(acc, _mm256_madd_epi16(p, ones));
+    }
+    __m128i h = _mm_add_epi32(_mm256_castsi256_si128(acc), _mm256_extracti128_si256(acc, 1));
+    h = _mm_add_epi32(h, _mm_shuffle_epi32(h, 0x4E));
+    h = _mm_add_epi32(h, _mm_shuffle_epi32(h, 0xB1));
+    int32_t s = _mm_cvtsi128_si32(h);
+    for (; i < k16; i++) s += (int32_t)a[i] * (int32_t)b[i];
+    return s;
+}
+
+static int g_vnni512 = -1;
+
 static inline int32_t dot_i8_blocks(const int8_t *a, const int8_t *b, int64_t k16) {
-    int32_t acc = 0;
-    for (int64_t i = 0; i < k16; i++) acc += (int32_t)a[i] * (int32_t)b[i];
-    return acc;
+    if (g_vnni512 < 0)
+        g_vnni512 = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                    __builtin_cpu_supports("avx512vnni");
+    return g_vnni512 ? dot_i8_vnni512(a, b, k16) : dot_i8_avx2(a, b, k16);
+}
+
+/* 0: AVX2, 1: AVX-512 VNNI when the host has it (tests run both) */
+void or_set_int8_dot(int vnni512) {
+    g_vnni512 = vnni512 && __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+                __builtin_cpu_supports("avx512vnni");
+}
+
+/* which int8 dot the host runs (reported with the CPU baseline) */
+const char *or_int8_dot_kind(void) {
+    dot_i8_blocks(NULL, NULL, 0);
+    return g_vnni512 ? "avx512-vnni vpdpbusd" : "avx2 vpmaddubsw";
 }
 
 /* neon::matvec_int8 (kernels/neon.rs:716-793) */
@@ -708,6 +765,7 @@ struct or_decoder {
     or_dec_packed *p;
     int8_t *lm; float *lm_s;
     int64_t max_seq, len;
+    int kv_bf16;                       /* store K/V rows rounded to bf16 (this build's config-3 cache) */
     float *k, *v;                      /* [layer][kvh][max_seq][hd] */
     float *rc, *rs;                    /* rope [max_seq][hd] */
     float *x, *xn, *q, *kk, *vv, *att, *ffn;
@@ -793,14 +851,34 @@ void or_embed_token(const or_decoder *d, int32_t token, float *out) {   /* decod
     for (int64_t i = 0; i < d->c.hidden; i++) out[i] = bf16f(row[i]);
 }
 
+/* f32 -> bf16 round-to-nearest-even -> f32 (finite values) */
+static float bf16_round(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    u &= 0xFFFF0000u;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
 static void kv_write(or_decoder *d, int layer, int64_t pos, const float *k, const float *v) {
     int64_t hd = d->c.head_dim, hs = d->max_seq * hd;   /* decoder.rs:233-253 */
     for (int h = 0; h < d->c.n_kv_heads; h++) {
         int64_t off = ((int64_t)layer * d->c.n_kv_heads + h) * hs + pos * hd;
         memcpy(d->k + off, k + h * hd, sizeof(float) * hd);
         memcpy(d->v + off, v + h * hd, sizeof(float) * hd);
+        if (d->kv_bf16)
+            for (int64_t i = 0; i < hd; i++) {
+                d->k[off + i] = bf16_round(d->k[off + i]);
+                d->v[off + i] = bf16_round(d->v[off + i]);
+            }
     }
 }
+
+/* Not in the reference (its cache is f32, decoder.rs:186-197): K/V rows
+ * stored rounded to bf16, as the GPU's bf16 cache holds them; attention then
+ * reads the rounded rows, the new position's included. */
+void or_decoder_set_kv_bf16(or_decoder *d, int on) { d->kv_bf16 = on ? 1 : 0; }
 
 /* linear_nobias_bf16_scratch (kernels/mod.rs:693-703): convert, then sgemm */
 static void linear_bf16(or_decoder *d, float *y, const float *x, const uint16_t *w, int64_t seq,

@@ -83,6 +83,7 @@ _SIGS = {
     "or_decoder_destroy": (None, [P]),
     "or_decoder_packed": (P, [P, C.c_int, C.c_int, C.POINTER(P)]),
     "or_decoder_set_len": (None, [P, I64]),
+    "or_decoder_set_kv_bf16": (None, [P, C.c_int]),
     "or_decoder_len": (I64, [P]),
     "or_decoder_prefill": (None, [P, P, I64]),
     "or_decoder_prefill_logits": (None, [P, P, I64, P, I64, P]),
@@ -103,6 +104,8 @@ _SIGS = {
     "or_stream_stats": (None, [P, P]),
     "or_tail_repeat_blocks": (I64, [P, I64, I64, P]),
     "or_set_threads": (None, [C.c_int]),
+    "or_int8_dot_kind": (C.c_char_p, []),
+    "or_set_int8_dot": (None, [C.c_int]),
     "or_get_threads": (C.c_int, []),
 }
 
@@ -133,6 +136,10 @@ def f32(a):
 
 def set_threads(n):
     lib().or_set_threads(int(n))
+
+
+def int8_dot_kind():
+    return lib().or_int8_dot_kind().decode()
 
 
 def quantize_bf16_rows(w_bf16, mode=ROUND):
@@ -313,13 +320,15 @@ def mel(samples):
 class OracleDecoder:
     """or_decoder over SynthDecoder-style numpy weights."""
 
-    def __init__(self, weights, max_seq=2048, mode=ROUND):
+    def __init__(self, weights, max_seq=2048, mode=ROUND, kv_bf16=False):
         self.w = weights
         self.cfg = weights.cfg
         cfg, w = weights.structs(DecConfig, DecLayer, DecWeights)
         self._keep = (cfg, w)
         self.d = lib().or_decoder_create(C.byref(cfg), C.byref(w), mode, max_seq)
         self.max_seq = max_seq
+        if kv_bf16:
+            lib().or_decoder_set_kv_bf16(self.d, 1)
 
     def close(self):
         if self.d:

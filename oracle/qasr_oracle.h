@@ -147,6 +147,7 @@ or_decoder *or_decoder_create(const or_dec_config *cfg, const or_dec_weights *w,
 void or_decoder_destroy(or_decoder *d);
 const int8_t *or_decoder_packed(const or_decoder *d, int layer, int which, const float **scales);
 void or_decoder_set_len(or_decoder *d, int64_t len);
+void or_decoder_set_kv_bf16(or_decoder *d, int on);
 int64_t or_decoder_len(const or_decoder *d);
 void or_decoder_prefill(or_decoder *d, const float *embeds, int64_t seq_len);
 void or_decoder_prefill_hidden(or_decoder *d, const float *embeds, int64_t seq_len, float *hidden);
@@ -188,6 +189,8 @@ void or_stream_stats(const or_stream *s, int64_t *stats);
 int64_t or_tail_repeat_blocks(const int32_t *t, int64_t n, int64_t max_period, int64_t *period);
 
 void or_set_threads(int n);
+const char *or_int8_dot_kind(void);
+void or_set_int8_dot(int vnni512);
 int or_get_threads(void);
 
 #ifdef __cplusplus

@@ -6,14 +6,19 @@ audio, mel -> encoder -> 404-row prefill -> 200 forced greedy steps
 - the 200 token ids equal the committed oracle fixture
   (tests/golden/config2_tokens.json, written by make_config2_tokens.py);
 - the random-init model settles on one token id, so the token check alone is
-  weak: the whole KV cache after the run (every layer, all 604 positions, the
-  prefill's rows and the 199 decode steps') is compared with the oracle's,
-  computed here on the host from the same seeded model and audio.  The prefill
-  rows come from f32-class MFMA GEMMs against the oracle's blocked f32 sgemm,
-  and every decode step re-quantizes its activations to int8, so small
-  prefill differences can move an int8 rounding; the bar is 1e-5 relative on
-  layer 0 and 2e-3 norm-wise on every layer (a wrong row, position or layer
-  gives errors of order 1).
+  weak: the whole KV cache after the run (every layer, all 604 positions) is
+  compared with the oracle's, computed here on the host from the same seeded
+  model and audio:
+  * the 404 prefill rows of every layer within 1e-5 (f32-class MFMA GEMMs and
+    attention against the oracle's f32 sgemm; measured 1e-6);
+  * layer 0's 200 decode rows within 1e-5 (identical token embeddings through
+    the exact int8 path);
+  * deeper decode rows within 5e-2: every decode step re-quantizes its
+    activations to int8, so an ulp-level difference can move an element
+    across a rounding boundary.  The oracle against itself with its prompt
+    rows perturbed by 1e-6 (relative) moves these rows by 0.7-2.1% at layers
+    1-27 while its prefill rows move by 1e-6 and its 200 tokens do not change;
+    a wrong row, position or layer gives errors of order 1.
 """
 import json
 import os
@@ -62,7 +67,11 @@ def test_config2_full_size(dev):
     finally:
         od.close()
         oe.close()
-    errs = [(rel(k_g[l, :, :n], k_c[l, :, :n]), rel(v_g[l, :, :n], v_c[l, :, :n])) for l in range(28)]
-    print("per-layer KV relative error (k, v):", [(round(a, 7), round(b, 7)) for a, b in errs], flush=True)
-    assert max(errs[0]) < 1e-5, errs[0]
-    assert max(max(e) for e in errs) < 2e-3, errs
+    P = golden["prompt_len"] - 1                       # prefill rows; decode rows [P, n)
+    pre = [max(rel(k_g[l, :, :P], k_c[l, :, :P]), rel(v_g[l, :, :P], v_c[l, :, :P])) for l in range(28)]
+    dec = [max(rel(k_g[l, :, P:n], k_c[l, :, P:n]), rel(v_g[l, :, P:n], v_c[l, :, P:n])) for l in range(28)]
+    print("per-layer KV relative error, prefill rows:", [f"{e:.2e}" for e in pre], flush=True)
+    print("per-layer KV relative error, decode rows:", [f"{e:.2e}" for e in dec], flush=True)
+    assert max(pre) < 1e-5, pre
+    assert dec[0] < 1e-5, dec[0]
+    assert max(dec) < 5e-2, dec

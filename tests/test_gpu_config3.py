@@ -3,8 +3,14 @@
 
 The reference's KV cache is f32 (decoder.rs:186-197); the bf16 cache is this
 build's config-3 layout.  The oracle is fed the same bf16-exact values as f32,
-so attention over the cache differs only by accumulation order (1e-5); in
-decode, the GPU rounds each new K/V row to bf16 where the oracle keeps f32.
+so attention over the cache differs only by accumulation order (1e-5).  In
+decode the GPU rounds each new K/V row to bf16; the oracle's bf16-KV mode
+(or_decoder_set_kv_bf16) rounds its rows the same way, so the two differ only
+by f32 accumulation order.  An order-of-summation difference is ~1e-6
+relative, but it can move an int8 activation across a rounding boundary, and
+one such flip moves a logit by up to max|x| * max|w_row| / 127 (about 1.5e-3
+of the best logit here); tokens must be identical wherever the oracle's top-2
+gap exceeds two such flips (3e-3 of the best logit).
 """
 import numpy as np
 import pytest
@@ -51,46 +57,88 @@ def test_kv_upload_download_bf16(dev):
     gpu.close()
 
 
+MARGIN_BOUND = 3e-3
+
+
+def teacher_forced(dev, orc, w, L0, n, max_seq, seed):
+    """n teacher-forced steps from an L0-position N(0,1) bf16 context; returns
+    (oracle tokens, GPU tokens, relative top-2 margins, GPU KV, oracle KV)."""
+    from qwenasr_amd.model import Decoder
+    gpu = Decoder(dev, w, max_seq=max_seq, kv_bf16=True)
+    cpu = orc.OracleDecoder(w, max_seq=max_seq, kv_bf16=True)
+    try:
+        r = rng(seed)
+        shape = gpu.kv_shape()
+        k = np.zeros(shape, np.float32)
+        v = np.zeros(shape, np.float32)
+        k[:, :, :L0] = bf16f(bf16(r.normal(0, 1, k[:, :, :L0].shape)))
+        v[:, :, :L0] = bf16f(bf16(r.normal(0, 1, v[:, :, :L0].shape)))
+        gpu.kv_upload(k, v)
+        cpu.set_kv(k, v)
+        gpu.kv_len = L0
+        cpu.kv_len = L0
+        tok = 17
+        tc, tg, margins = [], [], []
+        for s in range(n):
+            e = cpu.embed(tok)
+            t_c, best, second = cpu.forward_logits(e)
+            t_g = gpu.forward(token=tok) if s else gpu.forward(embed=e)
+            tc.append(t_c)
+            tg.append(t_g)
+            margins.append((best - second) / max(abs(best), 1e-30))
+            tok = t_c
+        kg, vg = gpu.kv_download()
+        kc, vc = cpu.kv()
+    finally:
+        gpu.close()
+        cpu.close()
+    print(f"L0 {L0}: oracle {tc}\n        gpu    {tg}\n        margins {np.round(margins, 4).tolist()}", flush=True)
+    return tc, tg, margins, (kg, vg), (kc, vc)
+
+
+def check_deeper_rows(kg, vg, kc, vc, L0, n):
+    """Decode rows of layers >= 1 within 5e-2 norm-wise: each step re-quantizes
+    its activations to int8, so an ulp-level difference in the attention can
+    move an element across a rounding boundary; the oracle against itself with
+    1e-6-perturbed inputs moves such rows by up to 2% (config 2), and a wrong
+    row, position or layer gives errors of order 1."""
+    for a, b in ((kg, kc), (vg, vc)):
+        rel = np.linalg.norm(a[1:, :, L0:L0 + n] - b[1:, :, L0:L0 + n]) / np.linalg.norm(b[1:, :, L0:L0 + n])
+        print("layers >= 1 decode rows relative error", rel, flush=True)
+        assert rel < 5e-2, rel
+
+
+def check_tokens(tc, tg, margins, min_clear):
+    clear = [s for s, m in enumerate(margins) if m > MARGIN_BOUND]
+    assert len(clear) >= min_clear, margins
+    for s in clear:
+        assert tc[s] == tg[s], (s, tc[s], tg[s], margins[s])
+
+
 def test_decoder_1p7b_bf16kv_teacher_forced(dev, orc):
     """24 teacher-forced steps from a 300-position N(0,1) bf16 context."""
-    from qwenasr_amd.model import Decoder
     from qwenasr_amd.synth import SynthDecoder
     w = SynthDecoder(CFG_1P7B, seed=1003)
-    max_seq, L0, n = 512, 300, 24
-    gpu = Decoder(dev, w, max_seq=max_seq, kv_bf16=True)
-    cpu = orc.OracleDecoder(w, max_seq=max_seq)
-    r = rng(1003)
-    shape = gpu.kv_shape()
-    k = np.zeros(shape, np.float32)
-    v = np.zeros(shape, np.float32)
-    k[:, :, :L0] = bf16f(bf16(r.normal(0, 1, k[:, :, :L0].shape)))
-    v[:, :, :L0] = bf16f(bf16(r.normal(0, 1, v[:, :, :L0].shape)))
-    gpu.kv_upload(k, v)
-    cpu.set_kv(k, v)
-    gpu.kv_len = L0
-    cpu.kv_len = L0
-    tok = 17
-    mism, rel_margins = [], []
-    for s in range(n):
-        e = cpu.embed(tok)
-        t_c, best, second = cpu.forward_logits(e)
-        t_g = gpu.forward(token=tok) if s else gpu.forward(embed=e)
-        rel = (best - second) / max(abs(best), 1e-30)
-        rel_margins.append(rel)
-        if t_c != t_g:
-            mism.append((s, t_c, t_g, best, second))
-        tok = t_c
-    print("relative top-2 margins", np.round(rel_margins, 4), "mismatches", mism, flush=True)
-    # the bf16 rounding of each new K/V row (relative 2^-9) may only flip near-ties
-    assert all((m[3] - m[4]) / abs(m[3]) < 5e-2 for m in mism), mism
-    assert len(mism) <= 3, mism
-    kg, vg = gpu.kv_download()
-    kc, vc = cpu.kv()
-    # layer 0's new rows come from bit-identical projections: bf16 rounding of the oracle's rows
-    np.testing.assert_allclose(kg[0, :, L0:L0 + n], bf16f(bf16(kc[0, :, L0:L0 + n])), rtol=1e-2, atol=1e-2)
-    assert (vg[0, :, L0:L0 + n] == bf16f(bf16(vc[0, :, L0:L0 + n]))).all()
-    for a, b in ((kg, kc), (vg, vc)):
-        rel = np.linalg.norm(a[:, :, L0:L0 + n] - b[:, :, L0:L0 + n]) / np.linalg.norm(b[:, :, L0:L0 + n])
-        assert rel < 2e-2, rel
-    gpu.close()
-    cpu.close()
+    L0, n = 300, 24
+    tc, tg, margins, (kg, vg), (kc, vc) = teacher_forced(dev, orc, w, L0, n, 512, 1003)
+    check_tokens(tc, tg, margins, 20)
+    # layer 0's new rows: V from bit-identical int8 projections, so equal; K
+    # after a q/k norm + RoPE whose f32 order differs, so within one bf16 step
+    assert (vg[0, :, L0:L0 + n] == vc[0, :, L0:L0 + n]).all()
+    np.testing.assert_allclose(kg[0, :, L0:L0 + n], kc[0, :, L0:L0 + n], rtol=2 ** -7, atol=1e-6)
+    check_deeper_rows(kg, vg, kc, vc, L0, n)
+
+
+@pytest.mark.parametrize("L0", [2100, 4000])
+def test_decoder_1p7b_long_context(dev, orc, L0):
+    """8 teacher-forced steps at contexts whose buckets take the automatic
+    long-context splits (2304-position bucket: 36 splits; 4096: 64) and the
+    separate merge kernel."""
+    from qwenasr_amd.synth import SynthDecoder
+    print(f"1.7B long context L0={L0}", flush=True)
+    w = SynthDecoder(CFG_1P7B, seed=1005)
+    tc, tg, margins, (kg, vg), (kc, vc) = teacher_forced(dev, orc, w, L0, 8, 4352, 1005 + L0)
+    check_tokens(tc, tg, margins, 6)
+    assert (vg[0, :, L0:L0 + 8] == vc[0, :, L0:L0 + 8]).all()
+    np.testing.assert_allclose(kg[0, :, L0:L0 + 8], kc[0, :, L0:L0 + 8], rtol=2 ** -7, atol=1e-6)
+    check_deeper_rows(kg, vg, kc, vc, L0, 8)

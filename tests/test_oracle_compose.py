@@ -308,3 +308,29 @@ def test_planted_prompt_mistake(orc, tiny_models):
         return np.concatenate([np.stack(head), rows, np.stack(tail)])
     agree = transcribe_check(orc, tiny_models, prompt=swapped_audio_markers)
     assert len(agree) >= 1 and not all(agree), agree
+
+
+def test_kv_bf16_mode(orc, dec_w):
+    """or_decoder_set_kv_bf16 (this build's config-3 cache, not the
+    reference's): the rows it stores are the f32 mode's rows rounded to bf16
+    (round to nearest even, conftest.bf16), and the rows already in the cache
+    are what attention reads."""
+    from conftest import bf16, bf16f
+    e = rng(2120).normal(0, 1, (6, DEC["hidden"])).astype(np.float32)
+    a = orc.OracleDecoder(dec_w, max_seq=16)
+    b = orc.OracleDecoder(dec_w, max_seq=16, kv_bf16=True)
+    a.prefill(e[:5])
+    b.prefill(e[:5])
+    ka, va = a.kv()
+    kb, vb = b.kv()
+    # layer 0 sees the same inputs in both modes
+    assert (kb[0, :, :5] == bf16f(bf16(ka[0, :, :5]))).all() and (vb[0, :, :5] == bf16f(bf16(va[0, :, :5]))).all()
+    assert not (kb[0, :, :5] == ka[0, :, :5]).all()
+    a.forward(e[5])
+    b.forward(e[5])
+    ka, va = a.kv()
+    kb, vb = b.kv()
+    assert (vb[0, :, 5] == bf16f(bf16(va[0, :, 5]))).all()
+    assert (kb[1, :, :6] == bf16f(bf16(kb[1, :, :6]))).all()     # every stored value is a bf16 value
+    a.close()
+    b.close()

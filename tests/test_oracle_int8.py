@@ -111,8 +111,12 @@ def np_matvec(xq, xs, w, ws, bias=None):
     return y
 
 
+@pytest.mark.parametrize("vnni", [0, 1])
 @pytest.mark.parametrize("k", [1024, 2048, 3072, 6144, 80])
-def test_matvec_bruteforce(orc, k):
+def test_matvec_bruteforce(orc, k, vnni):
+    """both SIMD int8 dots (AVX2 maddubs, AVX-512 VNNI where the host has it)
+    give the exact integer sums, extreme values included"""
+    orc.lib().or_set_int8_dot(vnni)
     r = rng(k)
     w = r.integers(-127, 128, (96, k), dtype=np.int8)
     ws = r.uniform(1e-4, 2e-3, 96).astype(np.float32)
@@ -122,6 +126,12 @@ def test_matvec_bruteforce(orc, k):
     assert (orc.matvec_w8a8(xq, xs, w, ws) == np_matvec(xq, xs, w, ws)).all()
     assert (orc.matvec_w8a8(xq, xs, w, ws, b) == np_matvec(xq, xs, w, ws, b)).all()
     assert (orc.linear_int8_addto(b, x, w, ws) == np_matvec(xq, xs, w, ws, b)).all()
+    ext = np.full((2, k), -127, np.int8)
+    ext[1] = 127
+    xe = np.where(np.arange(k) % 2, np.int8(-127), np.int8(127)).astype(np.int8)
+    assert (orc.matvec_w8a8(xe, 1.0, ext, np.ones(2, np.float32)) ==
+            np_matvec(xe, 1.0, ext, np.ones(2, np.float32))).all()
+    orc.lib().or_set_int8_dot(1)
 
 
 def test_matvec_epilogue_not_fused(orc):
