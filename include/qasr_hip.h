@@ -106,6 +106,17 @@ int qasr_hip_rmsnorm_linear_int8_swiglu(qasr_hip *h, float *ffn_out, const float
 int qasr_hip_rmsnorm_argmax_int8(qasr_hip *h, const float *x, const float *norm_w, float eps,
                                  const int8_t *w, const float *ws, int64_t in_dim, int64_t out_dim,
                                  int32_t *idx);
+/* No counterpart in the reference.  qasr_hip_argmax_int8 (norm_w null) or
+ * qasr_hip_rmsnorm_argmax_int8 (norm_w set) for callers that cannot allocate
+ * (code under HIP graph capture, serving loops that forbid hipMalloc): no
+ * handle, no device allocation.  Runs on `stream` (a hipStream_t; null: the
+ * null stream) of the current device; the block partials live in a 32 KiB
+ * device array each GPU holds until the process ends, so calls that overlap
+ * on one GPU race (order them on one stream).  in_dim a multiple of 64, at
+ * most 4096; every pointer is device memory. */
+int qasr_hip_argmax_int8_noalloc(void *stream, const float *x, const float *norm_w, float eps,
+                                 const int8_t *w, const float *ws, int64_t in_dim, int64_t out_dim,
+                                 int32_t *idx);
 
 /* The aligner's per-row argmax (align.rs:312-321) over device logits
  * x [rows][ld] (cols <= ld used): idx (device [rows]) = lowest column of the

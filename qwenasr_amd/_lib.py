@@ -98,6 +98,7 @@ _SIGS = {
                                                    I64, I64, I64]),
     "qasr_hip_rmsnorm_linear_int8_swiglu": (C.c_int, [P, P, P, P, F32, P, P, I64, I64]),
     "qasr_hip_rmsnorm_argmax_int8": (C.c_int, [P, P, P, F32, P, P, I64, I64, P]),
+    "qasr_hip_argmax_int8_noalloc": (C.c_int, [P, P, P, F32, P, P, I64, I64, P]),
     "qasr_hip_rms_norm": (C.c_int, [P, P, P, P, I64, I64, F32]),
     "qasr_hip_rms_norm_per_head": (C.c_int, [P, P, P, I64, I64, I64, F32]),
     "qasr_hip_apply_rope_neox": (C.c_int, [P, P, P, P, I64, I64, I64]),
