@@ -352,7 +352,10 @@ int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *sa
  * with the others: M = streams int8 MFMA projections, attention over every
  * stream's own cache.  Integer dots are exact, so a stream's tokens equal
  * those of the single-stream decoder run with the same attention split count
- * (e.g. 1 for both). */
+ * (e.g. 1 for both).  Creating a batch switches the decoder's own decode
+ * steps to the multi-stream attention arithmetic (the lone decoder uses a
+ * latency-optimised kernel whose f32 rounding differs), so solo runs on that
+ * decoder stay bit-identical to its streams. */
 typedef struct qasr_batch qasr_batch;
 int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t max_seq, int64_t max_steps,
                           qasr_batch **out);

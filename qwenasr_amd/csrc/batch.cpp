@@ -123,6 +123,16 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     auto steps_ok = [](int64_t k) { return k % 1024 == 0 && (k == 1024 || k == 2048 || k == 3072 || k == 4096 || k == 6144); };
     if (!steps_ok(c.hidden) || !steps_ok(c.intermediate) || c.hidden > 4096 || d->lm_i8_rows % 16)
         return qasr_fail(QASR_ERR_INVALID, "batch_create: hidden and intermediate must be 1024, 2048, 3072, 4096 or 6144");
+    // Every stream must decode bit-identically to its solo run on this decoder
+    // so the decoder's own steps switch to the attention
+    // arithmetic the multi-stream step uses (k_attn_decode; the single-stream
+    // k_attn_step is the latency-optimised form of the lone decoder).
+    if (d->attn_step) {
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        for (auto &g : d->graphs) HIPCHK(hipGraphExecDestroy(g.second));
+        d->graphs.clear();
+        d->attn_step = 0;
+    }
     qasr_batch *b = new qasr_batch();
     b->d = d;
     b->B = n_streams;

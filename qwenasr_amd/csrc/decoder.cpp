@@ -88,6 +88,13 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
     // QASR_ATTN_WAVES=4|8: waves per decode-attention block (tuning)
     const char *aw = getenv("QASR_ATTN_WAVES");
     if (aw && (aw[0] == '4' || aw[0] == '8') && aw[1] == 0) d->attn_waves = aw[0] - '0';
+    // QASR_ATTN_STEP=0: the decode-step attention (and the multi-stream
+    // step's) on k_attn_decode instead of k_attn_step (tuning).  Measured on
+    // the 0.6B decode: k_attn_step with 4 waves of up to 4 groups each 5.72 /
+    // 6.50 / 7.42 us at contexts 494 / 700 / 1000 against 6.76 / 7.24 / 7.86;
+    // 8-wave blocks were slower (5.82-7.30)
+    const char *as = getenv("QASR_ATTN_STEP");
+    if (as && as[0] == '0' && as[1] == 0) d->attn_step = 0;
     int rc = decoder_build(d, w, lm_head, lm_head ? lm_rows : c.vocab);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
@@ -282,6 +289,12 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = scale;
             // static partition of the step's context bucket: the first KV loads need no device state
             t.gpb = (int)((((cap + 7) / 8) + n_split - 1) / n_split);
+            // the 2-dims-per-lane kernel (same partials, 4 waves) when a
+            // block's run is at most 12 groups
+            if (d->attn_step && attn_step_gpw(t.gpb) > 0) {
+                t.waves = 4;
+                t.gpw = attn_step_gpw(t.gpb);
+            }
             LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, false), "step attention");
         }
         if (want(2)) {

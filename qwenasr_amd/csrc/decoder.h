@@ -43,6 +43,7 @@ struct qasr_decoder {
     int32_t *am_idx = nullptr;
     int n_split = 0, use_graph = 1;             // attention splits (0: automatic per context bucket)
     int attn_waves = 4;                         // waves per attention block (4 or 8)
+    int attn_step = 4;                          // 4: k_attn_step (4 waves per block); 0: k_attn_decode
     // one captured decode step per context bucket (the attention's static
     // partition is sized for the bucket); keyed by the bucket's capacity
     std::map<int64_t, hipGraphExec_t> graphs;

@@ -431,6 +431,272 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     if (t == 0) reset_counter(a.counters + kvh);
 }
 
+// ---------------------------------------------------------------------------
+// GQA decode attention of one decode step (the DEC = 1 case above, same
+// inputs, partial format and numerics contract), with a layout that shortens
+// each wave's dependent chain.  Lane l owns dims 2l and 2l + 1 of every
+// position: a group's 8 K rows and 8 V rows are 16 loads of 8 (f32) or 4
+// (bf16) bytes per lane, each instruction covering whole rows.  Per group a
+// lane forms 2-term partial dots for the 16 (query head, position) scores,
+// and one reduce-scatter over the wave (permlane32 / permlane16 swaps, then
+// DPP) leaves every lane one finished score: lanes are (head, position)
+// slots, replicated 4 times.  The softmax over a head's 8 x GPW positions is
+// 3 swaps; the probabilities are read back with readlane (scalar operands),
+// and since each lane already owns its dims, P V needs no cross-lane sum.
+// The RoPE pair (d, d + 64) sits in lanes l and l + 32 (one permlane32 swap).
+// Blocks: (KV head, split) with the KV head fastest, so with 8 KV heads the
+// splits of one head land on one XCD (blocks go round-robin over the 8
+// XCDs) and their partial stores merge in that L2.
+// ---------------------------------------------------------------------------
+template <typename T> struct KvPair;
+template <> struct KvPair<float> {
+    float2 v;
+    __device__ __forceinline__ void load(const float *row, int lane) { v = reinterpret_cast<const float2 *>(row)[lane]; }
+    __device__ __forceinline__ float x() const { return v.x; }
+    __device__ __forceinline__ float y() const { return v.y; }
+    __device__ __forceinline__ void set(float a, float b) { v = make_float2(a, b); }
+    static __device__ __forceinline__ void store(float *row, int lane, float a, float b) {
+        reinterpret_cast<float2 *>(row)[lane] = make_float2(a, b);
+    }
+};
+template <> struct KvPair<uint16_t> {
+    uint32_t v;
+    __device__ __forceinline__ void load(const uint16_t *row, int lane) {
+        v = reinterpret_cast<const uint32_t *>(row)[lane];
+    }
+    __device__ __forceinline__ float x() const { return __uint_as_float(v << 16); }
+    __device__ __forceinline__ float y() const { return __uint_as_float(v & 0xFFFF0000u); }
+    __device__ __forceinline__ void set(float a, float b) {
+        v = (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
+    }
+    static __device__ __forceinline__ void store(uint16_t *row, int lane, float a, float b) {
+        reinterpret_cast<uint32_t *>(row)[lane] = (uint32_t)f32_to_bf16_rne(a) | ((uint32_t)f32_to_bf16_rne(b) << 16);
+    }
+};
+
+// full-wave sum, every lane receives it
+__device__ __forceinline__ float wave_allsum(float v) { return sum_x8(sum8(v)); }
+
+// the two halves of a swap: first operand's lanes 32-63 exchanged with the
+// second's lanes 0-31 (and rows 1/3 with rows 0/2 for the 16-lane form)
+__device__ __forceinline__ float swap32_add(float keep_lo, float keep_hi) {
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(keep_lo), __float_as_uint(keep_hi), false, false);
+    return __fadd_rn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+__device__ __forceinline__ float swap16_add(float keep_even, float keep_odd) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(keep_even), __float_as_uint(keep_odd), false, false);
+    return __fadd_rn(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// per-head RMSNorm + NeoX RoPE of one 128-dim head held as dims (2l, 2l + 1)
+__device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float2 s, float eps) {
+    constexpr int D = 128;
+    const float ss = wave_allsum(fmaf(x.y, x.y, __fmul_rn(x.x, x.x)));
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+    x.x = __fmul_rn(__fmul_rn(x.x, r), w.x);
+    x.y = __fmul_rn(__fmul_rn(x.y, r), w.y);
+    // partner dims d +- 64 live in lane l ^ 32
+    const auto px = __builtin_amdgcn_permlane32_swap(__float_as_uint(x.x), __float_as_uint(x.x), false, false);
+    const auto py = __builtin_amdgcn_permlane32_swap(__float_as_uint(x.y), __float_as_uint(x.y), false, false);
+    const bool lo = (threadIdx.x & 32) == 0;
+    // one of the two results is this lane's own value, the other its partner's
+    // (whichever way round the swap returns them; equal bits mean equal values)
+    const float qx = __uint_as_float(px[0] == __float_as_uint(x.x) ? px[1] : px[0]);
+    const float qy = __uint_as_float(py[0] == __float_as_uint(x.y) ? py[1] : py[0]);
+    float2 o;
+    if (lo) {   // x1 = own, x2 = partner
+        o.x = __fadd_rn(__fmul_rn(x.x, c.x), __fmul_rn(-qx, s.x));
+        o.y = __fadd_rn(__fmul_rn(x.y, c.y), __fmul_rn(-qy, s.y));
+    } else {    // x2 = own, x1 = partner
+        o.x = __fadd_rn(__fmul_rn(x.x, c.x), __fmul_rn(qx, s.x));
+        o.y = __fadd_rn(__fmul_rn(x.y, c.y), __fmul_rn(qy, s.y));
+    }
+    return o;
+}
+
+// A wave holds its whole share of the block's run, groups g0 + wid + NW i
+// for i < GPW (the host launches it only for runs of at most NW GPW groups):
+// every group's scores, one max per head over all of them, then P V.  Rows
+// the run leaves out are masked (scores -inf, weights 0, P V terms skipped).
+template <typename KVT, int NW, int GPW>
+__global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
+    constexpr int D = 128, G = 2;
+    using Kp = KvPair<KVT>;
+    __shared__ float wm[NW][G], wl[NW][G];
+    __shared__ float wacc[NW][G][D];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int n_split = a.n_split;
+    const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
+    const int kvh = blockIdx.x % Hkv, split = blockIdx.x / Hkv;
+    KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
+    KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
+    const float *qkv = a.qkv;
+    float *part = a.part;
+    const int max_rows = (int)(a.head_stride / D);
+    const int gpb = a.gpb, g0 = split * gpb, g1s = g0 + gpb;
+
+    // ---- every load before the first wait: the block's static partition
+    // needs no device state, so the K/V rows go out before the position
+    // arrives (rows past the cache read row 0; everything past the context is
+    // masked once the position is known)
+    Kp kr[GPW][8], vr[GPW][8];
+#pragma unroll
+    for (int i = 0; i < GPW; i++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const int j = 8 * (g0 + wid + NW * i) + p;
+            const int r = j < max_rows ? j : 0;
+            kr[i][p].load(kc + (int64_t)r * D, lane);
+            vr[i][p].load(vc + (int64_t)r * D, lane);
+        }
+    float2 q[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) q[g] = reinterpret_cast<const float2 *>(qkv + (kvh * G + g) * D)[lane];
+    const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
+    const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
+    float2 kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
+    float2 vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
+    const float2 sn = reinterpret_cast<const float2 *>(a.rope_cur + D)[lane];
+    const int pos = a.state[1];
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int L = pos + 1;
+    const int g1 = min((L + 7) >> 3, g1s);
+    const int j1 = min(L, 8 * g1);
+    const bool own_pos = 8 * g0 <= pos && pos < j1;
+
+    // lane -> (head, position) slot of the reduce-scatter; the swap halves
+    // are told apart by running the same swaps on indicators
+    const float hsel = swap32_add(0.0f, 1.0f);
+    const float psel = swap16_add(0.0f, 1.0f);
+    const int bit3 = (lane >> 3) & 1, bit2 = (lane >> 2) & 1;
+    const int my_h = hsel > 1.0f ? 1 : 0;
+    const int my_p = (psel > 1.0f ? 4 : 0) + 2 * bit3 + bit2;
+    // the lane holding each (head, position) slot: any lane with those
+    // selectors (worked out while the loads are in flight)
+    int src[G][8];
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) src[g][p] = (int)__builtin_ctzll(__ballot(my_h == g && my_p == p));
+
+    // ---- q: per-head RMSNorm + RoPE; the new K/V row ------------------------
+#pragma unroll
+    for (int g = 0; g < G; g++) q[g] = norm_rope2(q[g], qn, cs, sn, a.eps);
+    if (own_pos) {
+        kn = norm_rope2(kn, knw, cs, sn, a.eps);
+        Kp kp, vp;
+        kp.set(kn.x, kn.y);      // the values the cache holds (a bf16 cache rounds)
+        vp.set(vn.x, vn.y);
+        kn = make_float2(kp.x(), kp.y());
+        vn = make_float2(vp.x(), vp.y());
+        if (wid == 0) {
+            Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
+            Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
+        }
+    }
+
+    // ---- scores: 2-term partials, one reduce-scatter per group --------------
+    float sc[GPW];
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
+        const int jb = 8 * (g0 + wid + NW * i);
+        float part2[G][8];
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            float kx = kr[i][p].x(), ky = kr[i][p].y();
+            if (own_pos && jb + p == pos) { kx = kn.x; ky = kn.y; }
+#pragma unroll
+            for (int g = 0; g < G; g++) part2[g][p] = fmaf(q[g].y, ky, __fmul_rn(q[g].x, kx));
+        }
+        float r1[8];
+#pragma unroll
+        for (int p = 0; p < 8; p++) r1[p] = swap32_add(part2[0][p], part2[1][p]);
+        float r2[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) r2[k] = swap16_add(r1[k], r1[k + 4]);
+        float r3[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const float keep = bit3 ? r2[2 + k] : r2[k], send = bit3 ? r2[k] : r2[2 + k];
+            r3[k] = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_ROR8>(send));
+        }
+        float r4;
+        {
+            const float keep = bit2 ? r3[1] : r3[0], send = bit2 ? r3[0] : r3[1];
+            r4 = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(send));
+        }
+        r4 = __fadd_rn(r4, dpp_f32<QASR_DPP_QP_1032>(r4));
+        r4 = __fadd_rn(r4, dpp_f32<QASR_DPP_QP_2301>(r4));
+        sc[i] = jb + my_p < j1 ? __fmul_rn(r4, a.scale) : -INFINITY;
+    }
+
+    // ---- softmax over this wave's positions of each head --------------------
+    float m = sc[0];
+#pragma unroll
+    for (int i = 1; i < GPW; i++) m = fmaxf(m, sc[i]);
+    m = fmaxf(m, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(m));
+    m = fmaxf(m, dpp_f32<QASR_DPP_ROW_ROR8>(m));
+    m = xrow16_max(m);
+    float pr[GPW], l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
+        pr[i] = m == -INFINITY ? 0.0f : expf(__fsub_rn(sc[i], m));
+        l = __fadd_rn(l, pr[i]);
+    }
+    l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(l));
+    l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_ROR8>(l));
+    l = xrow16_sum(l);
+
+    // ---- P V: probabilities as scalar operands; masked positions skipped ----
+    float o[G][2] = {};
+#pragma unroll
+    for (int g = 0; g < G; g++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+#pragma unroll
+            for (int i = 0; i < GPW; i++) {
+                const int j = 8 * (g0 + wid + NW * i) + p;
+                if (j >= j1) continue;                     // uniform
+                const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[i]), src[g][p]));
+                float vx = vr[i][p].x(), vy = vr[i][p].y();
+                if (own_pos && j == pos) { vx = vn.x; vy = vn.y; }
+                o[g][0] = fmaf(w, vx, o[g][0]);
+                o[g][1] = fmaf(w, vy, o[g][1]);
+            }
+        }
+
+    // ---- merge the waves of the block (LDS, one barrier) --------------------
+    if ((lane & 15) == 0 && psel < 1.0f) {   // one lane per head
+        wm[wid][my_h] = m;
+        wl[wid][my_h] = l;
+    }
+#pragma unroll
+    for (int g = 0; g < G; g++)
+        reinterpret_cast<float2 *>(&wacc[wid][g][0])[lane] = make_float2(o[g][0], o[g][1]);
+    __syncthreads();
+    const int gq = (t >> 7) & 1, d = t & 127;
+    if (t < G * D) {
+        float m_part = -INFINITY, o_part = 0.0f, l_part = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w][gq]);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = wm[w][gq] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w][gq], m_part));
+            o_part = fmaf(wacc[w][gq][d], f, o_part);
+            l_part = fmaf(wl[w][gq], f, l_part);
+        }
+        const int h = kvh * G + gq;
+        part[part_o_index(n_split, split, Hq, h * D + d)] = o_part;
+        if (d == 0) {
+            part[(2 * h) * n_split + split] = m_part;
+            part[(2 * h + 1) * n_split + split] = l_part;
+        }
+    }
+}
+
 // Multi-stream decode prologue of the attention: per stream b, per-head
 // RMSNorm + RoPE of the 16 query heads (in place in the qkv row) and of the new
 // key, and the new K/V row written at the stream's position.  The lane layout,
@@ -504,6 +770,19 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
     } else {                                                                                         \
         if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, 2>), grid, dim3(NW * 64), 0, st, a); \
         else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);  \
+    }
+    if (dec && !merge && a.gpw > 0) {
+        // k_attn_step (single-stream step): 4 waves of gpw = 1..3 groups (the
+        // whole run: gpb <= 4 gpw)
+        if (a.waves != 4 || a.gpw < 1 || a.gpw > 3 || a.gpb > 4 * a.gpw || a.gpb_dev || nb != 1 ||
+            n_kv_heads * a.n_split != (int)grid.x)
+            return hipErrorInvalidValue;
+#define QASR_ATT_STEP(GPW)                                                                            \
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_step<uint16_t, 4, GPW>), grid, dim3(256), 0, st, a);  \
+        else hipLaunchKernelGGL((k_attn_step<float, 4, GPW>), grid, dim3(256), 0, st, a);
+        if (a.gpw == 1) { QASR_ATT_STEP(1) } else if (a.gpw == 2) { QASR_ATT_STEP(2) } else { QASR_ATT_STEP(3) }
+#undef QASR_ATT_STEP
+        return hipGetLastError();
     }
     if (a.gpb_dev) {
         if (a.waves == 4) { QASR_ATT_MS(4) } else { QASR_ATT_MS(8) }

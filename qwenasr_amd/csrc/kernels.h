@@ -119,6 +119,8 @@ struct AttnDecodeArgs {
     float *out;               // [Hq * D]
     int n_split;
     int waves;                // waves per block: 4 or 8 (0: 8)
+    int gpw;                  // decode step: > 0 selects the 2-dims-per-lane kernel with up to
+                              // gpw 8-position groups per wave (gpb <= waves * gpw)
     int gpb;                  // > 0: static partition, 8-position groups per block (rows < head_stride / D)
     float eps, scale;
     // multi-stream decode: blockIdx.y = stream; per-stream strides of the cache
