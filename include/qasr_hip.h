@@ -345,6 +345,67 @@ int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *sa
                                int64_t n_samples, int32_t n_steps, int32_t *tokens_out,
                                double *times_ms);
 
+/* transcribe_segment (transcribe.rs:63-247) with its own stop rule: the same
+ * pipeline as qasr_hip_transcribe_forced, then greedy forwards until one
+ * yields a stop token (151643 endoftext, 151645 im_end) or max_tokens tokens
+ * have been produced (the reference's max_tokens is 2048).  tokens_out
+ * (capacity max_tokens) receives every token produced, the stop included;
+ * *n_out their count. */
+int qasr_hip_transcribe(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n_samples,
+                        int32_t max_tokens, int32_t *tokens_out, int64_t *n_out, double *times_ms);
+/* The ids transcribe_segment turns into text (transcribe.rs:196-214): those
+ * after the first <asr_text> (151704) and before the first stop token, in
+ * order; written to out (nullable: count only).  Returns the count (-1 for a
+ * null raw).  Host only. */
+int64_t qasr_hip_text_tokens(const int32_t *raw, int64_t n, int32_t *out);
+
+/* ---- the reference's C API (c_api.rs) at token level -------------------------
+ * Text is token ids; turning them into bytes is the caller's tokenizer
+ * (tokenizer.rs).  One engine = one handle, the checkpoint mapping, the
+ * encoder and the decoder (QwenCtx::load, context.rs:86-150). */
+typedef struct qasr_engine qasr_engine;
+typedef struct qasr_engine_stream qasr_engine_stream;
+/* QwenConfig::detect (config.rs:108-156) from tensor shapes: decoder hidden
+ * and vocab from embed_tokens, intermediate from layer 0's gate_proj, the
+ * large encoder when audio_tower layer 18 exists; layer counts are those the
+ * checkpoint holds (the reference's 28 / 24 / 18 for its checkpoints). */
+int qasr_hip_engine_detect(const qasr_st *st, qasr_dec_config *dc, qasr_enc_config *ec);
+/* qwen_asr_load_model (c_api.rs:20-46): the model directory's safetensors on
+ * GPU `device`; the KV cache holds max_seq positions (0: 8192). */
+int qasr_hip_engine_load(const char *model_dir, int device, int64_t max_seq, qasr_engine **out);
+void qasr_hip_engine_free(qasr_engine *g);                          /* qwen_asr_free */
+int qasr_hip_engine_config(const qasr_engine *g, qasr_dec_config *dc, qasr_enc_config *ec);
+/* qwen_asr_transcribe_pcm (c_api.rs:75-95), no segmentation (segment_sec 0,
+ * the default): the text token ids of the transcription (up to cap written;
+ * *n_out = their count). */
+int qasr_hip_engine_transcribe_pcm(qasr_engine *g, const float *samples, int64_t n_samples, int32_t *tokens_out,
+                                   int64_t cap, int64_t *n_out);
+/* every token of the last transcription, the stop included */
+int qasr_hip_engine_last_raw_tokens(const qasr_engine *g, int32_t *tokens_out, int64_t cap, int64_t *n);
+/* qwen_asr_stream_new / _free / _reset (c_api.rs:178-202).  Streams borrow
+ * the engine's decoder and encoder; several may be alive and interleave their
+ * pushes with each other and with transcribe_pcm (a push after another
+ * caller's work prefills every row instead of reusing the KV cache's rows,
+ * where the reference's shared cache would hold the other caller's rows).
+ * qasr_hip_engine_free releases the device state of streams still alive;
+ * they then accept only qasr_hip_engine_stream_free. */
+int qasr_hip_engine_stream_new(qasr_engine *g, qasr_engine_stream **out);
+void qasr_hip_engine_stream_free(qasr_engine_stream *s);
+int qasr_hip_engine_stream_reset(qasr_engine_stream *s);
+/* qwen_asr_stream_push (c_api.rs:204-241): append n_samples new samples (16 kHz
+ * mono f32), run stream_push_audio over the stream's audio so far; the newly
+ * committed text token ids go to tokens_out (*n_out = their count) */
+int qasr_hip_engine_stream_push(qasr_engine_stream *s, const float *samples, int64_t n_samples, int finalize,
+                                int32_t *tokens_out, int64_t cap, int64_t *n_out);
+/* qwen_asr_stream_get_result (c_api.rs:243-260): every committed text token */
+int qasr_hip_engine_stream_get_result(const qasr_engine_stream *s, int32_t *tokens_out, int64_t cap, int64_t *n);
+/* qwen_asr_stream_set_* (c_api.rs:262-297): settings of streams created
+ * afterwards; out-of-range values are ignored */
+void qasr_hip_engine_stream_set_chunk_sec(qasr_engine *g, float sec);
+void qasr_hip_engine_stream_set_rollback(qasr_engine *g, int32_t tokens);
+void qasr_hip_engine_stream_set_unfixed_chunks(qasr_engine *g, int32_t chunks);
+void qasr_hip_engine_stream_set_max_new_tokens(qasr_engine *g, int32_t tokens);
+
 /* ---- multi-stream decode (no counterpart in the reference,
  * whose streaming is batch 1 per QwenCtx) ----
  * Up to 32 independent streams share a loaded decoder's weights; each owns a

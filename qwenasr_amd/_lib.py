@@ -138,6 +138,23 @@ _SIGS = {
     "qasr_hip_mel": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),
     "qasr_hip_encoder_forward": (C.c_int, [P, P, I64, P, C.POINTER(I64)]),
     "qasr_hip_transcribe_forced": (C.c_int, [P, P, P, I64, I32, P, P]),
+    "qasr_hip_transcribe": (C.c_int, [P, P, P, I64, I32, P, C.POINTER(I64), P]),
+    "qasr_hip_text_tokens": (I64, [P, I64, P]),
+    "qasr_hip_engine_detect": (C.c_int, [P, C.POINTER(DecConfig), C.POINTER(EncConfig)]),
+    "qasr_hip_engine_load": (C.c_int, [C.c_char_p, C.c_int, I64, C.POINTER(P)]),
+    "qasr_hip_engine_free": (None, [P]),
+    "qasr_hip_engine_config": (C.c_int, [P, C.POINTER(DecConfig), C.POINTER(EncConfig)]),
+    "qasr_hip_engine_transcribe_pcm": (C.c_int, [P, P, I64, P, I64, C.POINTER(I64)]),
+    "qasr_hip_engine_last_raw_tokens": (C.c_int, [P, P, I64, C.POINTER(I64)]),
+    "qasr_hip_engine_stream_new": (C.c_int, [P, C.POINTER(P)]),
+    "qasr_hip_engine_stream_free": (None, [P]),
+    "qasr_hip_engine_stream_reset": (C.c_int, [P]),
+    "qasr_hip_engine_stream_push": (C.c_int, [P, P, I64, C.c_int, P, I64, C.POINTER(I64)]),
+    "qasr_hip_engine_stream_get_result": (C.c_int, [P, P, I64, C.POINTER(I64)]),
+    "qasr_hip_engine_stream_set_chunk_sec": (None, [P, C.c_float]),
+    "qasr_hip_engine_stream_set_rollback": (None, [P, I32]),
+    "qasr_hip_engine_stream_set_unfixed_chunks": (None, [P, I32]),
+    "qasr_hip_engine_stream_set_max_new_tokens": (None, [P, I32]),
     "qasr_hip_stream_default_config": (None, [C.POINTER(StreamConfig)]),
     "qasr_hip_stream_create": (C.c_int, [P, P, C.POINTER(StreamConfig), C.POINTER(P)]),
     "qasr_hip_stream_free": (None, [P]),

@@ -438,14 +438,16 @@ static const int PREFIX_HEAD[] = {151644, 8948, 198};
 static const int PREFIX_TAIL[] = {151645, 198, 151644, 872, 198, 151669};
 static const int SUFFIX_BASE[] = {151670, 151645, 198, 151644, 77091, 198};
 
-// Every error after work has been queued leaves through one exit that waits
-// for the stream, so no kernel of this call is still running on return.
-extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
-                                          int32_t n_steps, int32_t *tokens_out, double *times_ms) {
+// mel -> encoder -> prompt rows -> prefill of all but the last row -> the
+// first forward from the last row (transcribe.rs:71-183), queued on the
+// handle's stream; events ev[0..3] mark mel, encoder, prefill + first token.
+// Returns the prompt length in *total.
+static int transcribe_begin(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n, int64_t steps_max,
+                            int64_t *total_out) {
     if (!d || !e) return qasr_fail(QASR_ERR_INVALID, "transcribe: null model");
     CHECK_H(d->h);
     if (d->h != e->h) return qasr_fail(QASR_ERR_INVALID, "transcribe: models on different handles");
-    if (!samples || n <= 0 || n_steps <= 0 || !tokens_out) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
+    if (!samples || n <= 0 || steps_max <= 0) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
     if (e->c.output_dim != d->c.hidden) return qasr_fail(QASR_ERR_INVALID, "transcribe: encoder/decoder width mismatch");
     hipStream_t st = d->h->stream;
     const int64_t nf = mel_frames_for(n);
@@ -454,7 +456,7 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
     const int H = d->c.hidden;
     const int n_head = 9, n_tail = 6;
     const int64_t total = n_head + T + n_tail;
-    if (total - 1 + n_steps > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "transcribe: KV cache capacity exceeded");
+    if (total - 1 + steps_max > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "transcribe: KV cache capacity exceeded");
     int toks[15];
     for (int i = 0; i < 3; i++) toks[i] = PREFIX_HEAD[i];
     for (int i = 0; i < 6; i++) toks[3 + i] = PREFIX_TAIL[i];
@@ -473,39 +475,121 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
     float *enc = e->enc_out.as<float>(), *emb = e->embeds.as<float>();
     int *dtok = e->toks.as<int>();
     hipEvent_t *ev = e->ev;
+    HIPCHK(hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(dtok, toks, sizeof(toks), hipMemcpyHostToDevice, st));
+    HIPCHK(hipEventRecord(ev[0], st));
+    TRY(mel_dev(e, dx, n, dmel, msc));
+    HIPCHK(hipEventRecord(ev[1], st));
+    int64_t nt = 0;
+    TRY(encoder_forward_dev(e, dmel, nf, enc, &nt));
+    HIPCHK(hipEventRecord(ev[2], st));
+    LAUNCHCHK(launch_build_prompt(emb, d->embed, dtok, n_head, enc, (int)T, n_tail, H, st), "prompt");
+    d->len = 0;
+    TRY(decoder_prefill_dev(d, emb, total - 1));
+    TRY(decoder_set_state(d, 0));
+    HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
+    TRY(decoder_enqueue_step(d, false));
+    d->step_pos += 1;
+    HIPCHK(hipEventRecord(ev[3], st));
+    *total_out = total;
+    return QASR_OK;
+}
+
+static void stage_times(qasr_encoder *e, double *times_ms) {
+    if (!times_ms) return;
+    for (int i = 0; i < 4; i++) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, e->ev[i], e->ev[i + 1]);
+        times_ms[i] = ms;
+    }
+}
+
+// Every error after work has been queued leaves through one exit that waits
+// for the stream, so no kernel of this call is still running on return.
+extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
+                                          int32_t n_steps, int32_t *tokens_out, double *times_ms) {
+    if (n_steps <= 0 || !tokens_out) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
+    int64_t total = 0;
     auto body = [&]() -> int {
-        HIPCHK(hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, st));
-        HIPCHK(hipMemcpyAsync(dtok, toks, sizeof(toks), hipMemcpyHostToDevice, st));
-        HIPCHK(hipEventRecord(ev[0], st));
-        TRY(mel_dev(e, dx, n, dmel, msc));
-        HIPCHK(hipEventRecord(ev[1], st));
-        int64_t nt = 0;
-        TRY(encoder_forward_dev(e, dmel, nf, enc, &nt));
-        HIPCHK(hipEventRecord(ev[2], st));
-        LAUNCHCHK(launch_build_prompt(emb, d->embed, dtok, n_head, enc, (int)T, n_tail, H, st), "prompt");
-        d->len = 0;
-        TRY(decoder_prefill_dev(d, emb, total - 1));
-        // first token from the last prompt row, then n_steps - 1 graph-replayed steps
-        TRY(decoder_set_state(d, 0));
-        HIPCHK(hipMemcpyAsync(d->x, emb + (total - 1) * H, sizeof(float) * H, hipMemcpyDeviceToDevice, st));
-        TRY(decoder_enqueue_step(d, false));
-        d->step_pos += 1;
-        HIPCHK(hipEventRecord(ev[3], st));
+        TRY(transcribe_begin(d, e, samples, n, n_steps, &total));
+        hipStream_t st = d->h->stream;
         for (int32_t s = 1; s < n_steps; s++) TRY(decoder_run_embed_step(d));
-        HIPCHK(hipEventRecord(ev[4], st));
+        HIPCHK(hipEventRecord(e->ev[4], st));
         HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
         d->len += n_steps;
-        if (times_ms) {
-            for (int i = 0; i < 4; i++) {
-                float ms = 0.0f;
-                (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
-                times_ms[i] = ms;
-            }
-        }
+        stage_times(e, times_ms);
         return QASR_OK;
     };
     const int rc = body();
-    if (rc != QASR_OK) (void)hipStreamSynchronize(st);
+    if (rc != QASR_OK && d && d->h) (void)hipStreamSynchronize(d->h->stream);
     return rc;
+}
+
+// transcribe_segment's decode loop (transcribe.rs:186-230): greedy forwards
+// until one yields a stop token (151643 endoftext, 151645 im_end) or
+// max_tokens forwards have run.  The steps are graph replays in bursts of 8;
+// between bursts the host reads the token log (a burst may run past the stop:
+// those positions are discarded by setting the KV length back).
+static const int TOKEN_ENDOFTEXT = 151643, TOKEN_IM_END = 151645;
+
+extern "C" int qasr_hip_transcribe(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
+                                   int32_t max_tokens, int32_t *tokens_out, int64_t *n_out, double *times_ms) {
+    if (max_tokens <= 0 || !tokens_out || !n_out) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
+    *n_out = 0;
+    int64_t total = 0;
+    constexpr int BURST = 8;
+    auto body = [&]() -> int {
+        TRY(transcribe_begin(d, e, samples, n, max_tokens, &total));
+        hipStream_t st = d->h->stream;
+        int64_t done = 1, stop_at = -1;            // forwards queued; index of the stop token
+        std::vector<int32_t> log;
+        int64_t seen = 0;
+        while (true) {
+            // read what has been produced so far
+            log.resize((size_t)done);
+            HIPCHK(hipMemcpyAsync(log.data() + seen, d->token_log + seen, sizeof(int32_t) * (done - seen),
+                                  hipMemcpyDeviceToHost, st));
+            HIPCHK(hipStreamSynchronize(st));
+            for (int64_t i = seen; i < done; i++)
+                if (log[(size_t)i] == TOKEN_ENDOFTEXT || log[(size_t)i] == TOKEN_IM_END) {
+                    stop_at = i;
+                    break;
+                }
+            seen = done;
+            if (stop_at >= 0 || done >= max_tokens) break;
+            const int64_t b = std::min<int64_t>(BURST, max_tokens - done);
+            for (int64_t s = 0; s < b; s++) TRY(decoder_run_embed_step(d));
+            done += b;
+        }
+        HIPCHK(hipEventRecord(e->ev[4], st));
+        HIPCHK(hipStreamSynchronize(st));
+        const int64_t kept = stop_at >= 0 ? stop_at + 1 : done;
+        std::memcpy(tokens_out, log.data(), sizeof(int32_t) * kept);
+        *n_out = kept;
+        d->len += kept;                             // the KV holds the kept tokens' positions
+        stage_times(e, times_ms);
+        return QASR_OK;
+    };
+    const int rc = body();
+    if (rc != QASR_OK && d && d->h) (void)hipStreamSynchronize(d->h->stream);
+    return rc;
+}
+
+// The ids transcribe_segment turns into text (transcribe.rs:196-214): the
+// tokens after the first <asr_text> (151704) and before a stop token.
+extern "C" int64_t qasr_hip_text_tokens(const int32_t *raw, int64_t n, int32_t *out) {
+    if (!raw || n < 0) return -1;
+    int64_t k = 0;
+    bool past = false;
+    for (int64_t i = 0; i < n; i++) {
+        const int32_t t = raw[i];
+        if (t == TOKEN_ENDOFTEXT || t == TOKEN_IM_END) break;
+        if (t == 151704) past = true;
+        else if (past) {
+            if (out) out[k] = t;
+            k++;
+        }
+    }
+    return k;
 }

@@ -37,6 +37,11 @@ struct DevBuf {
 int dbuf_ensure(DevBuf &b, size_t bytes);
 void dbuf_release(DevBuf &b);
 
+// The stream's next push prefills every row instead of reusing the rows its
+// previous push left in the decoder's KV cache (another caller has written
+// that cache since).
+void stream_drop_prefix(qasr_stream *s);
+
 #define CHECK_H(h)                                                                   \
     do {                                                                             \
         if (!(h)) return qasr_fail(QASR_ERR_INVALID, "handle is null");              \

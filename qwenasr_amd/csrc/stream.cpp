@@ -146,6 +146,10 @@ extern "C" void qasr_hip_stream_free(qasr_stream *s) {
     delete s;
 }
 
+void stream_drop_prefix(qasr_stream *s) {
+    if (s) s->prev_prefill_len = 0;
+}
+
 // StreamState::reset (transcribe.rs:865-883)
 extern "C" int qasr_hip_stream_reset(qasr_stream *s) {
     if (!s) return qasr_fail(QASR_ERR_INVALID, "stream is null");

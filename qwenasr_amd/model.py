@@ -273,6 +273,125 @@ def transcribe_forced(decoder, encoder, samples, n_steps):
     return toks, times
 
 
+def transcribe(decoder, encoder, samples, max_tokens=2048):
+    """transcribe_segment (transcribe.rs:63-247): greedy to a stop token
+    (151643, 151645) or max_tokens.  Returns (every token produced, the stop
+    included; stage times in ms)."""
+    s = np.ascontiguousarray(samples, np.float32)
+    toks = np.empty(max_tokens, np.int32)
+    times = np.empty(4, np.float64)
+    n = I64()
+    check(lib().qasr_hip_transcribe(decoder.d, encoder.e, s.ctypes.data_as(P), s.size, int(max_tokens),
+                                    toks.ctypes.data_as(P), C.byref(n), times.ctypes.data_as(P)))
+    return toks[:n.value].copy(), times
+
+
+def text_tokens(raw):
+    """The ids transcribe_segment turns into text (transcribe.rs:196-214)."""
+    r = np.ascontiguousarray(raw, np.int32)
+    out = np.empty(max(1, r.size), np.int32)
+    k = lib().qasr_hip_text_tokens(r.ctypes.data_as(P), r.size, out.ctypes.data_as(P))
+    return out[:k].copy()
+
+
+def detect_config(ckpt):
+    """QwenConfig::detect (config.rs:108-156) on a Checkpoint: (decoder, encoder) config dicts."""
+    dc, ec = DecConfig(), EncConfig()
+    check(lib().qasr_hip_engine_detect(ckpt.st, C.byref(dc), C.byref(ec)))
+    return ({k: getattr(dc, k) for k, _ in DecConfig._fields_}, {k: getattr(ec, k) for k, _ in EncConfig._fields_})
+
+
+class Engine:
+    """The reference's C API (c_api.rs) at token level: qwen_asr_load_model,
+    transcribe_pcm and the streaming calls over one engine."""
+
+    def __init__(self, model_dir, device=0, max_seq=0):
+        g = P()
+        check(lib().qasr_hip_engine_load(str(model_dir).encode(), int(device), int(max_seq), C.byref(g)))
+        self.g = g
+
+    def close(self):
+        if self.g:
+            lib().qasr_hip_engine_free(self.g)
+            self.g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def config(self):
+        dc, ec = DecConfig(), EncConfig()
+        check(lib().qasr_hip_engine_config(self.g, C.byref(dc), C.byref(ec)))
+        return ({k: getattr(dc, k) for k, _ in DecConfig._fields_}, {k: getattr(ec, k) for k, _ in EncConfig._fields_})
+
+    def transcribe_pcm(self, samples):
+        s = np.ascontiguousarray(samples, np.float32)
+        out = np.empty(2048, np.int32)
+        n = I64()
+        check(lib().qasr_hip_engine_transcribe_pcm(self.g, s.ctypes.data_as(P), s.size, out.ctypes.data_as(P),
+                                                   out.size, C.byref(n)))
+        return out[:n.value].copy()
+
+    def last_raw_tokens(self):
+        out = np.empty(2048, np.int32)
+        n = I64()
+        check(lib().qasr_hip_engine_last_raw_tokens(self.g, out.ctypes.data_as(P), out.size, C.byref(n)))
+        return out[:n.value].copy()
+
+    def set_stream(self, chunk_sec=None, rollback=None, unfixed_chunks=None, max_new_tokens=None):
+        if chunk_sec is not None:
+            lib().qasr_hip_engine_stream_set_chunk_sec(self.g, float(chunk_sec))
+        if rollback is not None:
+            lib().qasr_hip_engine_stream_set_rollback(self.g, int(rollback))
+        if unfixed_chunks is not None:
+            lib().qasr_hip_engine_stream_set_unfixed_chunks(self.g, int(unfixed_chunks))
+        if max_new_tokens is not None:
+            lib().qasr_hip_engine_stream_set_max_new_tokens(self.g, int(max_new_tokens))
+
+    def stream(self):
+        return EngineStream(self)
+
+
+class EngineStream:
+    """QwenAsrStreamState (c_api.rs:167-260): push() takes the NEW samples."""
+
+    def __init__(self, engine):
+        s = P()
+        check(lib().qasr_hip_engine_stream_new(engine.g, C.byref(s)))
+        self.s = s
+        self.engine = engine
+
+    def push(self, samples, finalize=False):
+        x = np.ascontiguousarray(samples, np.float32)
+        out = np.empty(4096, np.int32)
+        n = I64()
+        check(lib().qasr_hip_engine_stream_push(self.s, x.ctypes.data_as(P) if x.size else None, x.size,
+                                                1 if finalize else 0, out.ctypes.data_as(P), out.size, C.byref(n)))
+        return out[:n.value].copy()
+
+    def result(self):
+        out = np.empty(1 << 16, np.int32)
+        n = I64()
+        check(lib().qasr_hip_engine_stream_get_result(self.s, out.ctypes.data_as(P), out.size, C.byref(n)))
+        return out[:n.value].copy()
+
+    def reset(self):
+        check(lib().qasr_hip_engine_stream_reset(self.s))
+
+    def close(self):
+        if self.s:
+            lib().qasr_hip_engine_stream_free(self.s)
+            self.s = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 KERNEL_KINDS = ("norm+qkv", "attention", "o_proj+=", "norm+gate_up+swiglu", "down+=", "norm+lm_head_argmax",
                 "argmax_merge")
 
