@@ -1,0 +1,273 @@
+// Decode-step floor probe (a standalone program, not part of the library).
+//
+// Measures on the GPU the three numbers the batch-1 decode floor rests on:
+//   1. an empty kernel replayed as a chain of dependent graph nodes: the cost
+//      of one launch boundary;
+//   2. the step's kernel sequence with every kernel reduced to a pure stream
+//      of its own HBM bytes (no activation, no arithmetic, no reduction): 28
+//      layers x (qkv, attention KV, o_proj, gate_up, down) over distinct
+//      buffers plus the LM head and its merge, one graph of 142 dependent
+//      nodes, i.e. the step time if every activation-dependent chain took
+//      zero time;
+//   3. the cheapest cross-block hand-off found for a persistent kernel: a
+//      1024-float vector published as (value, phase) 64-bit relaxed
+//      agent-scope stores and polled by one wave per block (no atomic
+//      read-modify-write); every spin is bounded and an abort flag makes
+//      every block leave.
+// Usage: probe_floor [hidden intermediate q_dim kv_dim vocab layers kv_len]
+// (default: the 0.6B decoder at the 505-position mid-decode context).
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <vector>
+
+#define CHK(x)                                                                                  \
+    do {                                                                                        \
+        hipError_t e_ = (x);                                                                    \
+        if (e_ != hipSuccess) {                                                                 \
+            std::fprintf(stderr, "%s:%d %s: %s\n", __FILE__, __LINE__, #x, hipGetErrorString(e_)); \
+            std::exit(1);                                                                       \
+        }                                                                                       \
+    } while (0)
+
+__global__ void k_empty() {}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Streams n16 16-byte words, every load issued before the first use; one
+// word per block is written so that the loads stay.
+template <int PER>
+__global__ __launch_bounds__(256) void k_stream(const int4 *__restrict__ src, int64_t n16, int *__restrict__ sink) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const i32x4 *s4 = reinterpret_cast<const i32x4 *>(src);
+    int acc = 0;
+    for (; i < n16; i += stride * PER) {
+        i32x4 v[PER];
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            const int64_t j = i + k * stride;
+            v[k] = j < n16 ? __builtin_nontemporal_load(s4 + j) : i32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int k = 0; k < PER; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    if (acc == 0x7fffffff) sink[blockIdx.x] = acc;
+}
+
+static void launch_stream(const int4 *src, int64_t bytes, int *sink, hipStream_t st) {
+    const int64_t n16 = bytes / 16;
+    // 4 loads of 16 B per thread in flight, at most 4096 blocks (the LM head loops)
+    int64_t blocks = (n16 + 256 * 4 - 1) / (256 * 4);
+    if (blocks > 4096) blocks = 4096;
+    if (blocks < 1) blocks = 1;
+    k_stream<4><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(src, n16, sink);
+}
+
+#define HV 1024
+#define SPIN_MAX 400000
+
+__device__ inline unsigned long long ld64(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void st64(unsigned long long *p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// phase p: block b publishes its HV / nb elements of phase p's vector, then
+// wave 0 polls the whole vector until every element carries phase p, copies
+// it to LDS, and the block folds it into the next phase's values.  Buffers
+// alternate by phase parity: a block can only publish phase p + 2 after every
+// block published p + 1, i.e. after every block finished reading phase p.
+__global__ __launch_bounds__(256) void k_handoff(unsigned long long *buf, int phases, int *abort_flag, int *err,
+                                                 float *out) {
+    __shared__ float vec[HV];
+    __shared__ int ok;
+    const int nb = gridDim.x, b = blockIdx.x, tid = threadIdx.x;
+    const int per = HV / nb;
+    float acc = 0.f;
+    for (int p = 1; p <= phases; p++) {
+        unsigned long long *dst = buf + (size_t)(p & 1) * HV;
+        if (tid < per) {
+            const float v = acc + (float)(b * per + tid) * 1e-3f;
+            st64(dst + b * per + tid, ((unsigned long long)(unsigned)p << 32) | __float_as_uint(v));
+        }
+        if (tid < 64) {
+            unsigned long long v[HV / 64];
+            int spins = 0;
+            bool done = false;
+            while (!done) {
+#pragma unroll
+                for (int i = 0; i < HV / 64; i++) v[i] = ld64(dst + i * 64 + tid);
+                bool mine = true;
+#pragma unroll
+                for (int i = 0; i < HV / 64; i++) mine &= (unsigned)(v[i] >> 32) == (unsigned)p;
+                done = __all(mine);
+                if (!done) {
+                    if (++spins > SPIN_MAX ||
+                        __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                        if (tid == 0) {
+                            __hip_atomic_store(abort_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            atomicAdd(err, 1);
+                        }
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < HV / 64; i++) vec[i * 64 + tid] = __uint_as_float((unsigned)v[i]);
+            if (tid == 0) ok = done;
+        }
+        __syncthreads();
+        if (!ok) break;
+        float s = 0.f;
+        for (int i = tid; i < HV; i += 256) s += vec[i];
+        acc = s * 1e-6f;
+        __syncthreads();
+    }
+    if (b == 0 && tid == 0) out[0] = acc;
+}
+
+static float graph_us(hipGraphExec_t ge, hipStream_t st, int reps, int nodes) {
+    hipEvent_t e0, e1;
+    CHK(hipEventCreate(&e0));
+    CHK(hipEventCreate(&e1));
+    for (int i = 0; i < 3; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipEventRecord(e0, st));
+    for (int i = 0; i < reps; i++) CHK(hipGraphLaunch(ge, st));
+    CHK(hipEventRecord(e1, st));
+    CHK(hipEventSynchronize(e1));
+    float ms = 0.f;
+    CHK(hipEventElapsedTime(&ms, e0, e1));
+    CHK(hipEventDestroy(e0));
+    CHK(hipEventDestroy(e1));
+    return ms * 1000.0f / reps / nodes;
+}
+
+int main(int argc, char **argv) {
+    // hidden, intermediate, q_dim, kv_dim, vocab, layers, kv_len
+    int64_t H = 1024, I = 3072, QD = 2048, KVD = 1024, V = 151936, NL = 28, L = 505;
+    if (argc == 8) {
+        H = atoll(argv[1]); I = atoll(argv[2]); QD = atoll(argv[3]); KVD = atoll(argv[4]);
+        V = atoll(argv[5]); NL = atoll(argv[6]); L = atoll(argv[7]);
+    }
+    hipStream_t st;
+    CHK(hipStreamCreate(&st));
+    int *sink;
+    CHK(hipMalloc(&sink, 4096 * sizeof(int)));
+
+    // 1. empty kernels: a chain of 142 dependent graph nodes
+    hipGraph_t g;
+    hipGraphExec_t ge;
+    const int n_empty = 142;
+    CHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < n_empty; i++) k_empty<<<dim3(256), dim3(256), 0, st>>>();
+    CHK(hipStreamEndCapture(st, &g));
+    CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    const float us_empty = graph_us(ge, st, 200, n_empty);
+    CHK(hipGraphExecDestroy(ge));
+    CHK(hipGraphDestroy(g));
+    std::printf("{\"probe\": \"empty_kernel_graph_node\", \"us_per_launch\": %.3f, \"nodes\": %d}\n", us_empty, n_empty);
+    std::fflush(stdout);
+
+    // 2. the step's kernels as pure byte streams (int8 weights + the f32 KV
+    //    of the attention), distinct buffers per layer as in the real step
+    const int64_t b_qkv = (QD + 2 * KVD) * H, b_attn = 2 * KVD * L * 4, b_o = H * QD, b_gu = 2 * I * H,
+                  b_down = H * I, b_lm = V * H;
+    const int64_t per_layer = b_qkv + b_attn + b_o + b_gu + b_down;
+    const int64_t total = per_layer * NL + b_lm;
+    const char *kinds[5] = {"qkv", "attention_kv", "o_proj", "gate_up", "down"};
+    const int64_t sizes[5] = {b_qkv, b_attn, b_o, b_gu, b_down};
+    // buffers at 256-byte aligned offsets: the layers' five, then the LM head
+    std::vector<int64_t> off(5 * NL + 1);
+    int64_t alloc = 0;
+    for (int64_t l = 0; l < NL; l++)
+        for (int k = 0; k < 5; k++) {
+            off[l * 5 + k] = alloc;
+            alloc += (sizes[k] + 255) / 256 * 256;
+        }
+    off[5 * NL] = alloc;
+    alloc += (b_lm + 255) / 256 * 256;
+    char *pool;
+    CHK(hipMalloc(&pool, (size_t)alloc));
+    CHK(hipMemset(pool, 1, (size_t)alloc));
+    std::vector<const int4 *> ptr(5 * NL);
+    for (int64_t i = 0; i < 5 * NL; i++) ptr[i] = reinterpret_cast<const int4 *>(pool + off[i]);
+    const int4 *lm = reinterpret_cast<const int4 *>(pool + off[5 * NL]);
+    // each kind alone: NL dependent launches over the NL layers' buffers
+    double floor_layer = 0.0;
+    for (int k = 0; k < 5; k++) {
+        CHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        for (int64_t l = 0; l < NL; l++) launch_stream(ptr[l * 5 + k], sizes[k], sink, st);
+        CHK(hipStreamEndCapture(st, &g));
+        CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+        const float us = graph_us(ge, st, 50, (int)NL);
+        CHK(hipGraphExecDestroy(ge));
+        CHK(hipGraphDestroy(g));
+        floor_layer += us;
+        std::printf("{\"probe\": \"stream_only\", \"kernel\": \"%s\", \"bytes\": %lld, \"us_per_launch\": %.3f, "
+                    "\"gbs\": %.1f}\n",
+                    kinds[k], (long long)sizes[k], us, sizes[k] / (us * 1e3));
+        std::fflush(stdout);
+    }
+    // the whole step: 5 NL + LM head + its merge as one chain
+    CHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    for (int64_t l = 0; l < NL; l++)
+        for (int k = 0; k < 5; k++) launch_stream(ptr[l * 5 + k], sizes[k], sink, st);
+    launch_stream(lm, b_lm, sink, st);
+    launch_stream(lm, 8192, sink, st);
+    CHK(hipStreamEndCapture(st, &g));
+    CHK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    const int nodes = (int)(5 * NL + 2);
+    const float us_node = graph_us(ge, st, 50, nodes);
+    CHK(hipGraphExecDestroy(ge));
+    CHK(hipGraphDestroy(g));
+    std::printf("{\"probe\": \"stream_only_step\", \"nodes\": %d, \"bytes\": %lld, \"us_per_step\": %.2f, "
+                "\"us_per_layer_sum_of_kinds\": %.3f}\n",
+                nodes, (long long)(total + 8192), us_node * nodes, floor_layer);
+    std::fflush(stdout);
+
+    // 3. data-plus-phase hand-off inside one cooperative launch
+    unsigned long long *buf;
+    int *abort_flag, *err;
+    float *out;
+    CHK(hipMalloc(&buf, 2 * HV * 8));
+    CHK(hipMalloc(&abort_flag, 4));
+    CHK(hipMalloc(&err, 4));
+    CHK(hipMalloc(&out, 4));
+    int phases = 2000;
+    for (int nb : {64, 128, 256}) {
+        float best = 1e30f;
+        for (int rep = 0; rep < 3; rep++) {
+            CHK(hipMemset(buf, 0, 2 * HV * 8));
+            CHK(hipMemset(abort_flag, 0, 4));
+            CHK(hipMemset(err, 0, 4));
+            CHK(hipDeviceSynchronize());
+            hipEvent_t e0, e1;
+            CHK(hipEventCreate(&e0));
+            CHK(hipEventCreate(&e1));
+            void *args[] = {&buf, &phases, &abort_flag, &err, &out};
+            CHK(hipEventRecord(e0, st));
+            CHK(hipLaunchCooperativeKernel((const void *)k_handoff, dim3(nb), dim3(256), args, 0, st));
+            CHK(hipEventRecord(e1, st));
+            CHK(hipEventSynchronize(e1));
+            float ms = 0.f;
+            CHK(hipEventElapsedTime(&ms, e0, e1));
+            int herr = 0;
+            CHK(hipMemcpy(&herr, err, 4, hipMemcpyDeviceToHost));
+            CHK(hipEventDestroy(e0));
+            CHK(hipEventDestroy(e1));
+            if (herr) {
+                std::fprintf(stderr, "hand-off: a spin reached its bound (%d blocks)\n", nb);
+                return 1;
+            }
+            const float us = ms * 1000.0f / phases;
+            if (us < best) best = us;
+        }
+        std::printf("{\"probe\": \"handoff\", \"blocks\": %d, \"us_per_phase\": %.3f}\n", nb, best);
+        std::fflush(stdout);
+    }
+    return 0;
+}
