@@ -470,6 +470,33 @@ int64_t qasr_hip_stream_audio_cursor(const qasr_stream *s);
  * prefilled, forwards, total forwards, encoder windows encoded, raw tokens */
 int qasr_hip_stream_stats(const qasr_stream *s, int64_t *stats);
 
+/* ---- many streams fed by the streaming pipeline, decoded as one batch -------
+ * BASELINE config 4 from real audio: n_streams (1..32) streaming states over
+ * one decoder and encoder; each chunk runs its encoder and prompt prefill
+ * (with common-prefix reuse) into the stream's slot of a multi-stream batch
+ * (max_seq positions each), then every stream with a chunk in that round takes
+ * its greedy steps in one batched decode (M = n_streams per projection), each
+ * stopping at its own stop token or max_new_tokens.  Per stream the sequence
+ * of stream_push_audio operations (transcribe.rs:902-1304) is that of
+ * qasr_hip_stream_push, and the decode is the lone decoder's arithmetic, so
+ * every stream commits the tokens it would commit alone.  The states belong to
+ * the batch: query them with qasr_hip_stream_tokens / _stats / _audio_cursor /
+ * _reset through qasr_hip_stream_batch_stream; qasr_hip_stream_push and
+ * qasr_hip_stream_free refuse or must not be used on them.  The decoder needs
+ * the multi-stream batch's shape (qasr_hip_batch_create). */
+typedef struct qasr_stream_batch qasr_stream_batch;
+int qasr_hip_stream_batch_create(qasr_decoder *d, qasr_encoder *e, const qasr_stream_config *cfg, int32_t n_streams,
+                                 int64_t max_seq, qasr_stream_batch **out);
+void qasr_hip_stream_batch_free(qasr_stream_batch *g);
+qasr_stream *qasr_hip_stream_batch_stream(qasr_stream_batch *g, int32_t i);
+/* samples[i] / n_samples[i]: the whole audio of stream i so far; finalize
+ * (nullable) per stream; stream i's newly committed text tokens go to
+ * tokens_out + i * cap (nullable), n_out[i] = their count.  Streams advance
+ * chunk by chunk in rounds until none has a complete chunk left (or, when
+ * finalizing, any audio). */
+int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *const *samples, const int64_t *n_samples,
+                               const int32_t *finalize, int32_t *tokens_out, int64_t cap, int64_t *n_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -163,6 +163,10 @@ _SIGS = {
     "qasr_hip_stream_tokens": (C.c_int, [P, P, I64, C.POINTER(I64)]),
     "qasr_hip_stream_audio_cursor": (I64, [P]),
     "qasr_hip_stream_stats": (C.c_int, [P, P]),
+    "qasr_hip_stream_batch_create": (C.c_int, [P, P, C.POINTER(StreamConfig), I32, I64, C.POINTER(P)]),
+    "qasr_hip_stream_batch_free": (None, [P]),
+    "qasr_hip_stream_batch_stream": (P, [P, I32]),
+    "qasr_hip_stream_batch_push": (C.c_int, [P, P, P, P, P, I64, P]),
     "qasr_hip_decoder_set_lm_head": (C.c_int, [P, P, I64]),
     "qasr_hip_decoder_logits_dim": (I64, [P]),
     "qasr_hip_decoder_head_rows": (I64, [P]),

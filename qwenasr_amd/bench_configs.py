@@ -3,6 +3,7 @@
     python -m qwenasr_amd.bench_configs config1 [reps]
     python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
     python -m qwenasr_amd.bench_configs config4 [n_streams] [steps] [attn_splits]
+    python -m qwenasr_amd.bench_configs config4_stream [n_streams] [rounds]
     python -m qwenasr_amd.bench_configs stream [seconds] [chunk_sec]
     python -m qwenasr_amd.bench_configs load [reps]
 
@@ -28,6 +29,14 @@ tokens/s (HIP events, graph replay), the same streams decoded one at a time
 by the single-stream decoder, the token identity of the two, and the
 step's algorithmic bytes (int8 weights once + every stream's KV cache) as
 GB/s.
+
+config4_stream: config 4 fed by the streaming pipeline (qasr_hip_stream_batch_*):
+32 streams of their own synthetic audio with 4-20 s histories each receive a
+2 s chunk per round; per round, every stream's encoder and prompt prefill go
+to its slot of a multi-stream batch and all their greedy steps run batched.
+Reported: wall ms per round (host clock, synchronous), seconds of audio
+processed per second, against the same streams pushed one at a time through
+lone states, and whether the committed token ids are identical.
 
 stream: the streaming driver (qasr_hip_stream_*, transcribe.rs:902-1304) on the
 config-2 model and audio (seeds 1002): the audio pushed `chunk_sec` at a time
@@ -301,6 +310,82 @@ def stream(seconds=30.0, chunk_sec=2.0):
     dev.close()
 
 
+def config4_stream(n_streams=32, rounds=3, chunk_sec=2.0):
+    """Config 4 fed by the real pipeline: n_streams streams of their own audio
+    (seeds 1004 + i) with ragged histories (stream i starts with 4-20 s
+    already pushed), then `rounds` timed rounds in which every stream receives
+    the next 2 s chunk: a StreamBatch push (per stream: encoder window(s) and
+    prompt prefill into its batch slot; one batched greedy decode for all),
+    against the same streams pushed one at a time through lone Stream states
+    on the same decoder.  Host clock around the synchronous pushes; token ids
+    must be identical."""
+    from .model import StreamBatch
+    dev = Device(0)
+    t0 = time.time()
+    wd = SynthDecoder(DEC_0_6B, seed=1004)
+    we = SynthEncoder(ENC_0_6B, seed=1004)
+    step = int(round(chunk_sec * 16000))
+    rng = np.random.default_rng(1004)
+    start_chunks = rng.integers(2, 11, n_streams)            # 4-20 s already pushed
+    total = [int(c + rounds) * step for c in start_chunks]
+    xs = [audio(n, 1004 + i) for i, n in enumerate(total)]
+    dec = Decoder(dev, wd, max_seq=1024)
+    enc = Encoder(dev, we)
+    dev.sync()
+    log(f"[config4_stream] models and audio ready in {time.time() - t0:.1f}s")
+    res = {}
+    got = {}
+    for mode in ("batched", "one_at_a_time"):
+        times, tok_rounds = [], []
+        if mode == "batched":
+            g = StreamBatch(dec, enc, n_streams, 1024)
+            g.push([x[:int(c) * step] for x, c in zip(xs, start_chunks)])          # history, untimed
+            for r in range(rounds):
+                ends = [int(c + r + 1) * step for c in start_chunks]
+                c0 = time.perf_counter()
+                out = g.push([x[:e] for x, e in zip(xs, ends)])
+                times.append(time.perf_counter() - c0)
+                tok_rounds.append([o.tolist() for o in out])
+            stats = [[int(v) for v in g.stream(i).stats()] for i in range(n_streams)]
+            g.close()
+        else:
+            # a lone state keeps its reusable prompt rows in the decoder's own
+            # KV cache, so each stream runs all its rounds before the next one;
+            # a round's time is the sum over the streams
+            times = [0.0] * rounds
+            tok_rounds = [[None] * n_streams for _ in range(rounds)]
+            stats = []
+            for i, (x, c) in enumerate(zip(xs, start_chunks)):
+                s_ = Stream(dec, enc)
+                s_.push(x[:int(c) * step])
+                for r in range(rounds):
+                    c0 = time.perf_counter()
+                    o = s_.push(x[:int(c + r + 1) * step])
+                    times[r] += time.perf_counter() - c0
+                    tok_rounds[r][i] = o.tolist()
+                stats.append([int(v) for v in s_.stats()])
+                s_.close()
+        got[mode] = tok_rounds
+        ms = 1000.0 * float(np.median(times))
+        fwd = sum(st[4] for st in stats)
+        res[mode] = {"round_ms": [round(1000 * t, 2) for t in times], "round_ms_median": round(ms, 2),
+                     "audio_s_per_wall_s": round(n_streams * chunk_sec / (ms / 1000.0), 1),
+                     "last_round_forwards_per_stream": [st[4] for st in stats],
+                     "last_round_prefill_rows": [st[2] for st in stats]}
+        log(f"[config4_stream] {mode}: rounds {res[mode]['round_ms']} ms; "
+            f"{res[mode]['audio_s_per_wall_s']} s of audio per s; last-round forwards {fwd}")
+    same = got["batched"] == got["one_at_a_time"]
+    print(json.dumps({"config": f"config 4 from the streaming pipeline: Qwen3-ASR-0.6B (28-layer int8 decoder, "
+                                f"18-layer encoder), {n_streams} streams, histories of 4-20 s, {rounds} rounds of "
+                                f"{chunk_sec} s chunks per stream, QwenCtx stream defaults",
+                      "start_seconds": [int(c) * chunk_sec for c in start_chunks], "results": res,
+                      "speedup": round(res["one_at_a_time"]["round_ms_median"] / res["batched"]["round_ms_median"], 2),
+                      "identical_tokens": same}))
+    dec.close()
+    enc.close()
+    dev.close()
+
+
 def load(reps=3):
     import os
     import shutil
@@ -372,6 +457,8 @@ if __name__ == "__main__":
     elif what == "config4":
         config4(int(sys.argv[2]) if len(sys.argv) > 2 else 32, int(sys.argv[3]) if len(sys.argv) > 3 else 32,
                 int(sys.argv[4]) if len(sys.argv) > 4 else -1)
+    elif what == "config4_stream":
+        config4_stream(int(sys.argv[2]) if len(sys.argv) > 2 else 32, int(sys.argv[3]) if len(sys.argv) > 3 else 3)
     elif what == "stream":
         stream(float(sys.argv[2]) if len(sys.argv) > 2 else 30.0, float(sys.argv[3]) if len(sys.argv) > 3 else 2.0)
     elif what == "load":

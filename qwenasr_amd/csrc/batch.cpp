@@ -220,6 +220,36 @@ extern "C" int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float
     return rc;
 }
 
+// decoder_prefill_dev of device rows [0, n) at positions [start, start + n) of
+// stream slot `stream` (the multi-stream streaming driver's chunk prefill);
+// the slot's length becomes start + n
+int batch_prefill_dev(qasr_batch *b, int32_t stream, const float *rows, int64_t start, int64_t n) {
+    if (!b || !rows || n <= 0 || start < 0) return qasr_fail(QASR_ERR_INVALID, "batch prefill: bad arguments");
+    qasr_decoder *d = b->d;
+    CHECK_H(d->h);
+    if (stream < 0 || stream >= b->B) return qasr_fail(QASR_ERR_INVALID, "batch prefill: stream out of range");
+    if (start + n > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch prefill: capacity exceeded");
+    const int64_t le = stream_layer_elems(b);
+    void *kc0 = d->kc, *vc0 = d->vc;
+    const int64_t ms0 = d->max_seq, len0 = d->len, ls0 = d->kv_layer_stride;
+    d->kc = reinterpret_cast<float *>(b->kc) + stream * le;
+    d->vc = reinterpret_cast<float *>(b->vc) + stream * le;
+    d->kv_layer_stride = (int64_t)b->B * le;
+    d->max_seq = b->max_seq;
+    d->len = start;
+    const int rc = decoder_prefill_dev(d, rows, n);
+    d->kc = kc0;
+    d->vc = vc0;
+    d->kv_layer_stride = ls0;
+    d->max_seq = ms0;
+    d->len = len0;
+    if (rc == QASR_OK) b->len[stream] = start + n;
+    return rc;
+}
+
+int64_t batch_max_seq(const qasr_batch *b) { return b ? b->max_seq : 0; }
+int32_t batch_streams(const qasr_batch *b) { return b ? b->B : 0; }
+
 extern "C" int qasr_hip_batch_set_len(qasr_batch *b, int32_t stream, int64_t len) {
     if (!b || stream < 0 || stream >= b->B || len < 0 || len > b->max_seq)
         return qasr_fail(QASR_ERR_INVALID, "batch_set_len: bad arguments");

@@ -42,6 +42,13 @@ void dbuf_release(DevBuf &b);
 // that cache since).
 void stream_drop_prefix(qasr_stream *s);
 
+// Multi-stream batch internals used by the streaming driver: a chunk prefill
+// from device rows into one stream's KV slot at positions [start, start + n),
+// the per-stream capacity and the stream count.
+int batch_prefill_dev(qasr_batch *b, int32_t stream, const float *rows, int64_t start, int64_t n);
+int64_t batch_max_seq(const qasr_batch *b);
+int32_t batch_streams(const qasr_batch *b);
+
 #define CHECK_H(h)                                                                   \
     do {                                                                             \
         if (!(h)) return qasr_fail(QASR_ERR_INVALID, "handle is null");              \

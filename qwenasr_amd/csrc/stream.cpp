@@ -92,6 +92,8 @@ struct qasr_stream {
     std::vector<int32_t> host_tok;
     // statistics of the last chunk
     int64_t st_reused = 0, st_prefill_len = 0, st_delta = 0, st_steps_total = 0, st_forwards = 0;
+    // the stream batch this state belongs to (its KV lives in a batch slot)
+    qasr_stream_batch *group = nullptr;
 };
 
 extern "C" void qasr_hip_stream_default_config(qasr_stream_config *c) {
@@ -217,16 +219,29 @@ static void carry_reset(qasr_stream *s) {
     }
 }
 
-// greedy decode of up to max_new tokens after the prefill of prefill_len rows;
-// returns the chunk's tokens (stop token excluded)
+// Where a chunk's prefill goes: the decoder's own KV cache (b == nullptr), or
+// stream slot `slot` of a multi-stream batch.
+struct PrefillTarget {
+    qasr_batch *b = nullptr;
+    int32_t slot = 0;
+};
+
+// What a prepared chunk hands to the decode and the commit.
+struct ChunkPlan {
+    bool is_final = false;
+    int64_t prefill_len = 0;       // rows prefilled; the last prompt row is decoded first
+    int64_t n_prefix_tokens = 0;   // rolled-back text tokens at the prompt's end
+    int32_t last_token = 0;        // the prompt's last row is this token's embedding
+};
+
+// greedy decode of up to max_new tokens after the prefill of prefill_len rows
+// into the decoder's own cache; returns the chunk's tokens (stop token excluded)
 static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t> &chunk) {
     qasr_decoder *d = s->d;
     hipStream_t st = d->h->stream;
     const int64_t H = d->c.hidden;
     const int max_new = s->cfg.max_new_tokens;
     chunk.clear();
-    if (prefill_len + max_new + DECODE_BURST > d->max_seq)
-        return qasr_fail(QASR_ERR_INVALID, "stream: decoder max_seq too small for this context");
     // first forward on the last prompt row
     d->len = prefill_len;
     TRY(decoder_set_state(d, 0));
@@ -258,20 +273,22 @@ static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t
     return QASR_OK;
 }
 
-// one chunk of stream_push_audio; *speech_ended stops the push loop
-static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool finalize,
-                         std::vector<int32_t> &emitted, bool *speech_ended_out, bool *abort_push) {
+// Steps 1-3 of a chunk of stream_push_audio: the encoder, the prompt rows and
+// the prefill with common-prefix reuse into `tgt`.  *skip: the chunk has no
+// encoder rows, the reference returns from the whole push with an empty delta
+// (transcribe.rs:1005-1008).
+static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool finalize, const PrefillTarget &tgt,
+                         ChunkPlan &pl, bool *skip) {
     qasr_decoder *d = s->d;
     hipStream_t st = d->h->stream;
     const int64_t H = d->c.hidden;
     const int64_t chunk_samples = (int64_t)(s->cfg.chunk_sec * (float)SAMPLE_RATE);
     const int64_t win_samples = WINDOW_FRAMES * HOP;
     const int rollback = s->cfg.rollback;
-    *speech_ended_out = false;
-    *abort_push = false;
+    *skip = false;
 
     s->cursor = std::min(s->cursor + chunk_samples, n);
-    const bool is_final = finalize && s->cursor >= n;
+    pl.is_final = finalize && s->cursor >= n;
 
     // ---- encoder: new complete windows, then the partial tail ----
     const int64_t full_end = (s->cursor / win_samples) * win_samples;
@@ -283,7 +300,7 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
         s->win.push_back(w);
     }
     const int64_t partial_age = s->cursor - s->last_partial_cursor;
-    const bool need_encode = s->last_partial_cursor == 0 || partial_age >= 2 * chunk_samples || is_final;
+    const bool need_encode = s->last_partial_cursor == 0 || partial_age >= 2 * chunk_samples || pl.is_final;
     int64_t partial_seq = 0;
     if (full_end < s->cursor) {
         partial_seq = s->partial_seq;                       // reuse unless re-encoded below
@@ -303,20 +320,21 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
     }
     const int64_t enc_len = s->enc_cached_total + partial_seq;
     if (enc_len == 0) {
-        // nothing to decode: the reference returns from the whole push with an
-        // empty delta here (transcribe.rs:1005-1008)
         s->chunk_idx += 1;
-        *abort_push = true;
+        *skip = true;
         return QASR_OK;
     }
 
     // ---- prompt rows ----
-    const int64_t n_prefix_tokens =
+    pl.n_prefix_tokens =
         (s->cfg.past_text_conditioning && s->chunk_idx >= s->cfg.unfixed_chunks && !s->raw.empty())
             ? (int64_t)std::max<int64_t>((int64_t)s->raw.size() - rollback, 0)
             : 0;
-    const int64_t total_seq = 9 + enc_len + 6 + n_prefix_tokens;
-    const int64_t prefill_len = total_seq - 1;
+    const int64_t total_seq = 9 + enc_len + 6 + pl.n_prefix_tokens;
+    pl.prefill_len = total_seq - 1;
+    const int64_t cap = tgt.b ? batch_max_seq(tgt.b) : d->max_seq;
+    if (pl.prefill_len + s->cfg.max_new_tokens + DECODE_BURST > cap)
+        return qasr_fail(QASR_ERR_INVALID, "stream: decoder max_seq too small for this context");
     TRY(dbuf_ensure(s->enc_all, sizeof(float) * enc_len * H));
     int64_t off = 0;
     for (auto &w : s->win) {
@@ -329,17 +347,19 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
                               hipMemcpyDeviceToDevice, st));
     std::vector<int32_t> toks(PREFIX, PREFIX + 9);
     toks.insert(toks.end(), SUFFIX, SUFFIX + 6);
-    toks.insert(toks.end(), s->raw.begin(), s->raw.begin() + n_prefix_tokens);
+    toks.insert(toks.end(), s->raw.begin(), s->raw.begin() + pl.n_prefix_tokens);
     for (int32_t t : toks)
         if (t < 0 || t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream: token id out of range");
+    pl.last_token = toks.back();
     TRY(dbuf_ensure(s->toks, sizeof(int32_t) * toks.size()));
     HIPCHK(hipMemcpyAsync(s->toks.p, toks.data(), sizeof(int32_t) * toks.size(), hipMemcpyHostToDevice, st));
     TRY(dbuf_ensure(s->embeds, sizeof(float) * total_seq * H));
     LAUNCHCHK(launch_build_prompt(s->embeds.as<float>(), d->embed, s->toks.as<int>(), 9, s->enc_all.as<float>(),
-                                  (int)enc_len, (int)(6 + n_prefix_tokens), (int)H, st),
+                                  (int)enc_len, (int)(6 + pl.n_prefix_tokens), (int)H, st),
               "stream prompt");
 
     // ---- prefill with common-prefix reuse ----
+    const int64_t prefill_len = pl.prefill_len;
     int64_t reused = 0;
     if (s->prev_prefill_len > 0) {
         const int64_t cmp = std::min(prefill_len, s->prev_prefill_len);
@@ -351,20 +371,28 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
         HIPCHK(hipStreamSynchronize(st));
         while (reused < cmp && !fl[reused]) reused++;
     }
-    d->len = reused;
     const int64_t delta = prefill_len - reused;
-    if (prefill_len + 1 > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "stream: decoder max_seq too small");
-    if (delta > 0) TRY(decoder_prefill_dev(d, s->embeds.as<float>() + reused * H, delta));
+    if (tgt.b) {
+        if (delta > 0) TRY(batch_prefill_dev(tgt.b, tgt.slot, s->embeds.as<float>() + reused * H, reused, delta));
+        else TRY(qasr_hip_batch_set_len(tgt.b, tgt.slot, reused));
+    } else {
+        d->len = reused;
+        if (delta > 0) TRY(decoder_prefill_dev(d, s->embeds.as<float>() + reused * H, delta));
+    }
     s->st_reused = reused;
     s->st_prefill_len = prefill_len;
     s->st_delta = delta;
+    return QASR_OK;
+}
 
-    // ---- decode ----
-    std::vector<int32_t> chunk;
-    TRY(decode_chunk(s, prefill_len, chunk));
+// Step 5 of a chunk: host bookkeeping on the chunk's tokens (transcribe.rs:
+// 1153-1292); the newly stable text tokens are appended to `emitted`.
+static void chunk_commit(qasr_stream *s, const ChunkPlan &pl, const std::vector<int32_t> &chunk,
+                         std::vector<int32_t> &emitted, bool *speech_ended_out) {
+    const int rollback = s->cfg.rollback;
     // keep this chunk's prefill rows for the next comparison
     std::swap(s->embeds, s->prev_embeds);
-    s->prev_prefill_len = prefill_len;
+    s->prev_prefill_len = pl.prefill_len;
 
     // ---- speech end: commit everything that was held back ----
     const bool speech_ended = chunk.empty() && !s->raw.empty() && s->chunk_idx >= s->cfg.unfixed_chunks;
@@ -375,7 +403,7 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
             emitted.push_back(s->raw[ts + i]);
         }
     }
-    s->raw.resize((size_t)n_prefix_tokens);
+    s->raw.resize((size_t)pl.n_prefix_tokens);
     s->raw.insert(s->raw.end(), chunk.begin(), chunk.end());
 
     if (!speech_ended) {
@@ -393,7 +421,7 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
         const size_t ts = text_start(s->raw);
         const int64_t n_text = (int64_t)s->raw.size() - (int64_t)std::min(ts, s->raw.size());
         int64_t cand = 0;
-        if (is_final) cand = n_text;
+        if (pl.is_final) cand = n_text;
         else if (s->chunk_idx >= s->cfg.unfixed_chunks) cand = std::max<int64_t>(n_text - rollback, 0);
         const int64_t from = (int64_t)s->stable.size();
         const int64_t to = std::max(cand, from);
@@ -406,7 +434,13 @@ static int process_chunk(qasr_stream *s, const float *samples, int64_t n, bool f
     }
     s->chunk_idx += 1;
     *speech_ended_out = speech_ended;
-    return QASR_OK;
+}
+
+// whether the stream has a chunk to process in a push over n_samples samples
+static bool chunk_pending(const qasr_stream *s, int64_t n_samples, bool finalize) {
+    const int64_t chunk_samples = (int64_t)(s->cfg.chunk_sec * (float)SAMPLE_RATE);
+    if (s->cursor >= n_samples) return false;
+    return n_samples - s->cursor >= chunk_samples || finalize;
 }
 
 extern "C" int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_t n_samples, int finalize,
@@ -414,26 +448,169 @@ extern "C" int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_
     if (!s) return qasr_fail(QASR_ERR_INVALID, "stream is null");
     CHECK_H(s->d->h);
     if (n_out) *n_out = 0;
+    if (s->group) return qasr_fail(QASR_ERR_INVALID, "stream_push: the stream belongs to a stream batch");
     if (n_samples < 0 || (n_samples > 0 && !samples) || n_samples < s->cursor)
         return qasr_fail(QASR_ERR_INVALID, "stream_push: samples must hold the whole stream so far");
-    const int64_t chunk_samples = (int64_t)(s->cfg.chunk_sec * (float)SAMPLE_RATE);
     std::vector<int32_t> emitted;
-    const int64_t available = n_samples - s->cursor;
-    if ((available < chunk_samples && !finalize) || available == 0) return QASR_OK;
-    while (s->cursor < n_samples) {
-        if (n_samples - s->cursor < chunk_samples && !finalize) break;
-        bool ended = false, abort_push = false;
-        TRY(process_chunk(s, samples, n_samples, finalize != 0, emitted, &ended, &abort_push));
-        if (abort_push) {
+    while (chunk_pending(s, n_samples, finalize != 0)) {
+        ChunkPlan pl;
+        bool skip = false, ended = false;
+        TRY(chunk_prepare(s, samples, n_samples, finalize != 0, PrefillTarget{}, pl, &skip));
+        if (skip) {
             emitted.clear();
             break;
         }
+        std::vector<int32_t> chunk;
+        TRY(decode_chunk(s, pl.prefill_len, chunk));
+        chunk_commit(s, pl, chunk, emitted, &ended);
         if (ended) break;
     }
     if (n_out) *n_out = (int64_t)emitted.size();
     if ((int64_t)emitted.size() > cap && tokens_out)
         return qasr_fail(QASR_ERR_INVALID, "stream_push: tokens_out too small (n_out holds the count)");
     if (tokens_out) std::copy(emitted.begin(), emitted.end(), tokens_out);
+    return QASR_OK;
+}
+
+// ---- many streams, one batched decode ---------------------------------------
+// N streaming states over one decoder and encoder whose chunks decode together
+// on a multi-stream batch (BASELINE config 4 fed by the real pipeline): per
+// round, every stream with a pending chunk runs its encoder and its prompt
+// prefill (common-prefix reuse within its own KV slot), then all of them take
+// their greedy steps together in bursts of DECODE_BURST (M = streams per
+// projection), each stopping at its own stop token or max_new_tokens, then
+// each commits its tokens.  Per stream, the sequence of operations is that of
+// qasr_hip_stream_push; the batch's decode is the lone decoder's arithmetic.
+struct qasr_stream_batch {
+    qasr_decoder *d = nullptr;
+    qasr_batch *b = nullptr;
+    std::vector<qasr_stream *> s;
+};
+
+extern "C" void qasr_hip_stream_batch_free(qasr_stream_batch *g) {
+    if (!g) return;
+    for (qasr_stream *s : g->s) {
+        s->group = nullptr;
+        qasr_hip_stream_free(s);
+    }
+    if (g->b) qasr_hip_batch_free(g->b);
+    delete g;
+}
+
+extern "C" int qasr_hip_stream_batch_create(qasr_decoder *d, qasr_encoder *e, const qasr_stream_config *cfg,
+                                            int32_t n_streams, int64_t max_seq, qasr_stream_batch **out) {
+    if (!d || !e || !out) return qasr_fail(QASR_ERR_INVALID, "stream_batch_create: null argument");
+    *out = nullptr;
+    qasr_stream_batch *g = new qasr_stream_batch();
+    g->d = d;
+    int rc = qasr_hip_batch_create(d, n_streams, max_seq, DECODE_BURST, &g->b);
+    for (int32_t i = 0; i < n_streams && rc == QASR_OK; i++) {
+        qasr_stream *s = nullptr;
+        rc = qasr_hip_stream_create(d, e, cfg, &s);
+        if (rc == QASR_OK) {
+            s->group = g;
+            g->s.push_back(s);
+        }
+    }
+    if (rc != QASR_OK) {
+        qasr_hip_stream_batch_free(g);
+        return rc;
+    }
+    *out = g;
+    return QASR_OK;
+}
+
+extern "C" qasr_stream *qasr_hip_stream_batch_stream(qasr_stream_batch *g, int32_t i) {
+    return (g && i >= 0 && i < (int32_t)g->s.size()) ? g->s[i] : nullptr;
+}
+
+// the greedy steps of the prepared streams `act` (plans pl), all slots
+// stepping together; chunks[i] gets stream i's tokens (stop excluded)
+static int group_decode(qasr_stream_batch *g, const std::vector<int> &act, const std::vector<ChunkPlan> &pl,
+                        std::vector<std::vector<int32_t>> &chunks) {
+    const int B = (int)g->s.size();
+    std::vector<int32_t> first(B, SUFFIX[5]), out((size_t)B * DECODE_BURST);
+    std::vector<char> busy(B, 0), done(B, 1);
+    for (int i : act) {
+        busy[i] = 1;
+        done[i] = 0;
+        first[i] = pl[i].last_token;
+        chunks[i].clear();
+    }
+    // the other slots step along from the end of the rows their next chunk may
+    // reuse (their last prefill), which the capacity check of that chunk covered
+    for (int j = 0; j < B; j++)
+        if (!busy[j]) TRY(qasr_hip_batch_set_len(g->b, j, g->s[j]->prev_prefill_len));
+    int64_t forwards = 0;
+    for (;;) {
+        bool open = false;
+        for (int i : act) open |= !done[i];
+        if (!open) break;
+        TRY(qasr_hip_batch_generate(g->b, first.data(), DECODE_BURST, out.data()));
+        forwards += DECODE_BURST;
+        for (int i : act) {
+            qasr_stream *s = g->s[i];
+            for (int k = 0; k < DECODE_BURST && !done[i]; k++) {
+                const int32_t t = out[(size_t)i * DECODE_BURST + k];
+                if (is_stop(s, t)) { done[i] = 1; break; }
+                chunks[i].push_back(t);
+                if ((int64_t)chunks[i].size() >= s->cfg.max_new_tokens) done[i] = 1;
+            }
+        }
+        for (int j = 0; j < B; j++) first[j] = out[(size_t)j * DECODE_BURST + DECODE_BURST - 1];
+    }
+    for (int i : act) {
+        g->s[i]->st_forwards = forwards;
+        g->s[i]->st_steps_total += forwards;
+    }
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *const *samples, const int64_t *n_samples,
+                                          const int32_t *finalize, int32_t *tokens_out, int64_t cap, int64_t *n_out) {
+    if (!g || !samples || !n_samples || !n_out) return qasr_fail(QASR_ERR_INVALID, "stream_batch_push: null argument");
+    CHECK_H(g->d->h);
+    const int B = (int)g->s.size();
+    for (int i = 0; i < B; i++) {
+        n_out[i] = 0;
+        if (n_samples[i] < 0 || (n_samples[i] > 0 && !samples[i]) || n_samples[i] < g->s[i]->cursor)
+            return qasr_fail(QASR_ERR_INVALID, "stream_batch_push: samples must hold each whole stream so far");
+    }
+    std::vector<std::vector<int32_t>> emitted(B), chunks(B);
+    std::vector<ChunkPlan> pl(B);
+    std::vector<char> open(B, 1);
+    for (;;) {
+        std::vector<int> act;
+        for (int i = 0; i < B; i++) {
+            const bool fin = finalize && finalize[i];
+            if (!open[i] || !chunk_pending(g->s[i], n_samples[i], fin)) {
+                open[i] = 0;
+                continue;
+            }
+            bool skip = false;
+            TRY(chunk_prepare(g->s[i], samples[i], n_samples[i], fin, PrefillTarget{g->b, i}, pl[i], &skip));
+            if (skip) {
+                emitted[i].clear();
+                open[i] = 0;
+                continue;
+            }
+            act.push_back(i);
+        }
+        if (act.empty()) break;
+        TRY(group_decode(g, act, pl, chunks));
+        for (int i : act) {
+            bool ended = false;
+            chunk_commit(g->s[i], pl[i], chunks[i], emitted[i], &ended);
+            if (ended) open[i] = 0;
+        }
+    }
+    for (int i = 0; i < B; i++) {
+        n_out[i] = (int64_t)emitted[i].size();
+        if (tokens_out && (int64_t)emitted[i].size() > cap)
+            return qasr_fail(QASR_ERR_INVALID, "stream_batch_push: tokens_out too small (n_out holds the counts)");
+    }
+    if (tokens_out)
+        for (int i = 0; i < B; i++) std::copy(emitted[i].begin(), emitted[i].end(), tokens_out + (size_t)i * cap);
     return QASR_OK;
 }
 

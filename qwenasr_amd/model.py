@@ -469,6 +469,71 @@ class Stream:
             pass
 
 
+class StreamBatch:
+    """Many streaming states over one decoder and encoder whose chunks decode
+    together on a multi-stream batch (qasr_hip_stream_batch_*): push() takes
+    each stream's whole audio so far and returns each stream's newly committed
+    token ids; stream(i) gives a view with tokens(), stats() and audio_cursor."""
+
+    _close_first = 2
+
+    def __init__(self, decoder, encoder, n_streams, max_seq, **cfg):
+        c = StreamConfig()
+        lib().qasr_hip_stream_default_config(C.byref(c))
+        for k, v in cfg.items():
+            if k == "stop_tokens":
+                c.stop_tokens[0], c.stop_tokens[1] = v
+            else:
+                setattr(c, k, v)
+        g = P()
+        check(lib().qasr_hip_stream_batch_create(decoder.d, encoder.e, C.byref(c), int(n_streams), int(max_seq),
+                                                 C.byref(g)))
+        self.g = g
+        self.n = int(n_streams)
+        self.decoder, self.encoder = decoder, encoder
+        decoder.dev.adopt(self)
+
+    def push(self, samples, finalize=None, cap=4096):
+        xs = [np.ascontiguousarray(x, np.float32) for x in samples]
+        assert len(xs) == self.n
+        ptrs = (P * self.n)(*[x.ctypes.data_as(P) if x.size else None for x in xs])
+        ns = np.array([x.size for x in xs], np.int64)
+        fin = np.array([1 if (finalize is not None and finalize[i]) else 0 for i in range(self.n)], np.int32)
+        out = np.empty((self.n, cap), np.int32)
+        n_out = np.zeros(self.n, np.int64)
+        check(lib().qasr_hip_stream_batch_push(self.g, C.cast(ptrs, P), ns.ctypes.data_as(P), fin.ctypes.data_as(P),
+                                               out.ctypes.data_as(P), cap, n_out.ctypes.data_as(P)))
+        return [out[i, :n_out[i]].copy() for i in range(self.n)]
+
+    def stream(self, i):
+        return _MemberStream(self, lib().qasr_hip_stream_batch_stream(self.g, int(i)))
+
+    def close(self):
+        if self.g:
+            lib().qasr_hip_stream_batch_free(self.g)
+            self.g = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _MemberStream:
+    """Read-only view of one state of a StreamBatch (owned by the batch)."""
+
+    def __init__(self, group, s):
+        if not s:
+            raise IndexError("stream index out of range")
+        self.group, self.s = group, s
+
+    tokens = Stream.tokens
+    stats = Stream.stats
+    reset = Stream.reset
+    audio_cursor = Stream.audio_cursor
+
+
 class Batch:
     """Multi-stream greedy decode: up to 32 streams with
     their own KV caches and lengths step together on one decoder's weights.
