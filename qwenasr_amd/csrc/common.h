@@ -116,11 +116,12 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 
 // ---- cross-block hand-off ------------------------------------------------
 // MI355X's L2 is private to each XCD, so a block that publishes data for a
-// block on another XCD must get it past its own L2.  Instead of a release fence
-// (which writes back the whole L2) the producer stores with agent-scope relaxed
-// atomics (write-through), waits for their acknowledgement, and only then bumps
-// the counter; the consumer reads with agent-scope atomic loads (which miss the
-// local L2).  Nothing else in the kernel needs to be made visible.
+// block on another XCD must get it past its own L2.  The producer stores with
+// agent-scope relaxed atomics (write-through) and waits for their
+// acknowledgement; arrive_last then orders them before its counter bump (an
+// agent-scope release fence and an acq_rel increment), and the consumer, after
+// the matching acquire, reads with agent-scope atomic loads (which miss its
+// local L2).
 __device__ __forceinline__ void st_agent(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

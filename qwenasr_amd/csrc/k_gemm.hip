@@ -320,6 +320,33 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < WC; j++) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // The epilogue's operands do not depend on the products: the unsplit
+    // kernels load them (column scale and bias, the old C of +=) before the
+    // ring's first stage, so that no load is left after the K loop.  Being
+    // older than every ring load, they are complete by the first wait.
+    constexpr bool PRE = KS == 1;
+    float pre_s[WC], pre_b[WC], pre_c[PRE && (EPI & EPI_ACCUM) ? WR : 1][WC][4];
+    if constexpr (PRE) {
+#pragma unroll
+        for (int j = 0; j < WC; j++) {
+            const int n = min(n0 + nw + j * 16 + (lane & 15), N - 1);
+            pre_s[j] = (EPI & EPI_SCALE) ? g.scale[n] : 1.0f;
+            pre_b[j] = g.bias ? g.bias[n] : 0.0f;
+        }
+        if constexpr ((EPI & EPI_ACCUM) != 0) {
+#pragma unroll
+            for (int i = 0; i < WR; i++)
+#pragma unroll
+                for (int j = 0; j < WC; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int m = min(m0 + mw + i * 16 + (lane >> 4) * 4 + r, M - 1);
+                        const int n = min(n0 + nw + j * 16 + (lane & 15), N - 1);
+                        pre_c[i][j][r] = g.C[(int64_t)m * g.ldc + n];
+                    }
+        }
+    }
+
 #pragma unroll
     for (int s = 0; s < NS - 1; s++) issue(s, s);
     const int fr = lane & 15, fg = lane >> 4;
@@ -393,20 +420,68 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     wait_vmcnt<0>();                          // no load may land in LDS after the block ends
 
     // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile
+    if constexpr (PRE) {
+        // every value first, then only stores under the bounds tests: an
+        // operand use inside a store's branch would make the compiler wait
+        // for all vector memory there, the previous stores included
+        float outv[WR][WC][4];
 #pragma unroll
-    for (int i = 0; i < WR; i++)
+        for (int i = 0; i < WR; i++)
 #pragma unroll
-        for (int j = 0; j < WC; j++)
+            for (int j = 0; j < WC; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
-                const int n = n0 + nw + j * 16 + (lane & 15);
-                if (m >= M || n >= N) continue;
-                if (KS > 1)
-                    g.ws[((int64_t)kz * M + m) * N + n] = acc[i][j][r];
-                else
-                    gemm_epilogue<EPI>(g, m, n, acc[i][j][r]);
-            }
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
+                    const int n = n0 + nw + j * 16 + (lane & 15);
+                    // gemm_epilogue's arithmetic on the preloaded operands
+                    int64_t gidx;              // gelu()'s element index
+                    if (EPI & EPI_TRANS) gidx = (int64_t)n * g.gelu_rows + m % g.gelu_rows;
+                    else gidx = (int64_t)m * g.ldc + n;
+                    float v = acc[i][j][r];
+                    if (EPI & EPI_SCALE) v = __fmul_rn(v, pre_s[j]);
+                    if constexpr ((EPI & EPI_ACCUM) != 0) {
+                        float c = pre_c[i][j][r];
+                        if (g.bias) c = __fadd_rn(c, pre_b[j]);
+                        v = __fadd_rn(c, v);
+                    } else {
+                        if (g.bias) v = __fadd_rn(v, pre_b[j]);
+                    }
+                    if (EPI & EPI_GELU) v = gelu_ref(v, gidx, g.gelu_n);
+                    // materialised here: otherwise the compiler sinks the
+                    // arithmetic into the store branches below
+                    asm volatile("" : "+v"(v));
+                    outv[i][j][r] = v;
+                }
+#pragma unroll
+        for (int i = 0; i < WR; i++)
+#pragma unroll
+            for (int j = 0; j < WC; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
+                    const int n = n0 + nw + j * 16 + (lane & 15);
+                    if (m >= M || n >= N) continue;
+                    int64_t off;
+                    if (EPI & EPI_TRANS) {
+                        const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
+                        off = (int64_t)c * g.gelu_n + (int64_t)n * g.gelu_rows + sp;
+                    } else {
+                        off = (int64_t)m * g.ldc + n;
+                    }
+                    g.C[off] = outv[i][j][r];
+                }
+    } else {
+#pragma unroll
+        for (int i = 0; i < WR; i++)
+#pragma unroll
+            for (int j = 0; j < WC; j++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
+                    const int n = n0 + nw + j * 16 + (lane & 15);
+                    if (m < M && n < N) g.ws[((int64_t)kz * M + m) * N + n] = acc[i][j][r];
+                }
+    }
 }
 
 // split-K reduction: the partials summed in split order, then the epilogue
@@ -479,9 +554,11 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     // for the partials (QASR_GEMM_SPLITK=0 disables)
     static const bool split_ok = [] { const char *e = getenv("QASR_GEMM_SPLITK"); return !(e && e[0] == '0'); }();
     // (K-steps: at least 16 of the f32-class path, whose steps cost three MFMA
-    // passes, 32 of the bf16 one; measured break-even points)
-    const int bk = ASRC == A_F32_SPLIT ? 32 : 64, min_steps = ASRC == A_F32_SPLIT ? 16 : 32;
-    const bool split = split_ok && g.ws && gx * gy <= 160 && g.K / bk >= min_steps &&
+    // passes; the bf16 path does not split: with its loads of the epilogue
+    // operands ahead of the K loop, the unsplit kernel measured faster at
+    // M = 375, K = 2048 (11.7 against 13.2 us) and equal at K = 3072)
+    const int bk = 32, min_steps = 16;
+    const bool split = ASRC == A_F32_SPLIT && split_ok && g.ws && gx * gy <= 160 && g.K / bk >= min_steps &&
                        (epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU || epi == EPI_SCALE) &&
                        g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float);
     if (split) {

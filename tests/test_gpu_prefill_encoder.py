@@ -41,19 +41,25 @@ def test_linear_bf16w(dev, orc, M, N, K):
     assert nrel(y.numpy(), exact + y0) < 2e-6
 
 
-@pytest.mark.parametrize("N,K", [(2048, 1024), (1024, 3072), (6144, 1024), (151936, 1024)])
-def test_gemm_w8_bf16_config1(dev, orc, N, K):
-    """Config 1: M = 375 rows of bf16 activations x int8 per-row weights."""
+@pytest.mark.parametrize("M,N,K", [(375, 2048, 1024), (375, 1024, 1024), (375, 1024, 2048), (375, 1024, 3072),
+                                   (375, 6144, 1024), (375, 151936, 1024), (1, 1024, 1024), (67, 1024, 3072),
+                                   (404, 1024, 1024)])
+def test_gemm_w8_bf16_config1(dev, orc, M, N, K):
+    """Config 1: M = 375 rows of bf16 activations x int8 per-row weights, the
+    0.6B shapes (q, k / v, o, down, gate_up, LM head) and edge row counts
+    (partial row tiles); a second call must give the same bits."""
     from qwenasr_amd import kernels as Kr
-    M = 375
     print(f"gemm_w8_bf16 M={M} N={N} K={K}", flush=True)
-    r = rng(N + K)
+    r = rng(N + K + M)
     wb = bf16(r.normal(0, 0.02, (N, K)))
     a = bf16(r.normal(0, 1, (M, K)))
     q, s = orc.quantize_bf16_rows(wb, 0)
     y = dev.empty((M, N), np.float32)
-    Kr.gemm_w8_bf16(y, dev.upload(a), dev.upload(q), dev.upload(s), M, N, K)
+    da, dq, ds = dev.upload(a), dev.upload(q), dev.upload(s)
+    Kr.gemm_w8_bf16(y, da, dq, ds, M, N, K)
     got = y.numpy()
+    Kr.gemm_w8_bf16(y, da, dq, ds, M, N, K)
+    assert (y.numpy() == got).all()
     af = bf16f(a).astype(np.float64)
     exact_int8 = (af @ q.astype(np.float64).T) * s
     assert nrel(got, exact_int8) < 1e-5
