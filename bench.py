@@ -29,18 +29,27 @@ METRIC = "realtime factor, 0.6B int8 30s audio; int8 matvec HBM GB/s (% of peak)
 
 def traffic_from_profiles(kernel):
     """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
-    scaled by a copy-kernel calibration), recorded in profiles/hbm_traffic.txt."""
+    scaled by a copy-kernel calibration), recorded in profiles/hbm_traffic.txt
+    together with a hash of the decode kernel sources it was measured on: None
+    (with the reason) when the sources have changed since."""
+    from qwenasr_amd.rocprof_summary import decode_sources_hash
     path = os.path.join(ROOT, "profiles", "hbm_traffic.txt")
     if not os.path.exists(path):
-        return None
+        return None, "profiles/hbm_traffic.txt is missing"
+    measured_on, value = None, None
     for line in open(path):
         parts = line.split()
-        if len(parts) >= 2 and parts[0] == kernel and not line.startswith("#"):
+        if line.startswith("# sources_sha256") and len(parts) >= 3:
+            measured_on = parts[2]
+        elif len(parts) >= 2 and parts[0] == kernel and not line.startswith("#"):
             try:
-                return float(parts[1])
+                value = float(parts[1])
             except ValueError:
-                return None
-    return None
+                value = None
+    current = decode_sources_hash()
+    if measured_on != current:
+        return None, f"profiles/hbm_traffic.txt was measured on kernel sources {measured_on}, these are {current}"
+    return value, f"rocprofv3 FETCH_SIZE + WRITE_SIZE per launch (profiles/hbm_traffic.txt, sources {current})"
 
 
 def main():
@@ -112,9 +121,10 @@ def main():
               f"{p['bytes'] / 1e6:9.3f} MB  {p['gbs']:8.1f} GB/s", file=sys.stderr, flush=True)
     # dominant kernel = largest time per token among the int8 matvec kernels and the attention
     dom = max(prof, key=lambda p: p["us_per_token"])
+    traffic, traffic_src = traffic_from_profiles(dom["kernel"])
     roof = {"bound": "hbm", "kernel": dom["kernel"], "achieved": round(dom["gbs"], 1), "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": round(dom["gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic_from_profiles(dom["kernel"]),
+            "traffic": traffic, "traffic_source": traffic_src,
             "us_per_launch": round(dom["us"], 3), "bytes_per_launch": dom["bytes"]}
     lm = [p for p in prof if p["kernel"].endswith("lm_head_argmax")][0]
     mv = [p for p in prof if p["kernel"] not in ("attention", "argmax_merge")]

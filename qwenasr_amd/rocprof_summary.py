@@ -2,6 +2,7 @@
 
     python -m qwenasr_amd.rocprof_summary <dir>/run_kernel_trace.csv [min_batch]
     python -m qwenasr_amd.rocprof_summary --pmc <dir>/run_counter_collection.csv <calib MiB>
+    python -m qwenasr_amd.rocprof_summary --traffic <fetch csv> <write csv> <calib MiB> > profiles/hbm_traffic.txt
 
 The second form averages each kernel's counter values (``--pmc FETCH_SIZE`` or
 ``WRITE_SIZE``, KiB per dispatch) and scales them by what the counter read for
@@ -16,9 +17,35 @@ timing batches of ``qasr_hip_decoder_profile``) and the rest (launches inside
 real decode steps, prefill, encoder, packing).
 """
 import csv
+import hashlib
+import os
+import re
 import statistics as st
 import sys
 from collections import defaultdict
+
+# the sources that decide the decode kernels' memory traffic (kernels, launch
+# shapes, split and partition choices)
+DECODE_SOURCES = ("common.h", "decoder.cpp", "k_attn.hip", "k_int8.hip", "model.h")
+
+# bench.py's decode kernel labels -> the 0.6B decoder's kernels (rocprofv3 names)
+DECODE_LABELS = (("norm+qkv", r"k_w8a8<1, 4, 0, true, false>"),
+                 ("attention", r"k_attn_step<|k_attn_decode<"),
+                 ("o_proj+=", r"k_oproj_merge<"),
+                 ("norm+gate_up+swiglu", r"k_w8a8<1, 8, 2, true, false>"),
+                 ("down+=", r"k_w8a8<3, 1, 1, false, false>"),
+                 ("norm+lm_head_argmax", r"k_argmax_w8a8<"),
+                 ("argmax_merge", r"k_argmax_finish"))
+
+
+def decode_sources_hash(root=None):
+    """sha256 (16 hex digits) over the decode kernel sources, in DECODE_SOURCES order."""
+    root = root or os.path.join(os.path.dirname(os.path.abspath(__file__)), "csrc")
+    h = hashlib.sha256()
+    for f in DECODE_SOURCES:
+        with open(os.path.join(root, f), "rb") as fh:
+            h.update(f.encode() + b"\0" + fh.read())
+    return h.hexdigest()[:16]
 
 
 def summarise(path, min_batch=20):
@@ -70,8 +97,48 @@ def summarise_pmc(path, calib_mib):
     return "\n".join(out)
 
 
+def _pmc_bytes(path, calib_mib):
+    """kernel -> per-dispatch calibrated bytes of one counter csv (values in
+    KiB, scaled so that k_copy16 moved calib_mib MiB)"""
+    per = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        per[r["Kernel_Name"].split("(")[0].replace("void ", "")].append(float(r["Counter_Value"]))
+    copy = [v for k, v in per.items() if "k_copy16" in k][0]
+    scale = calib_mib * 1024.0 / st.mean(copy)
+    return {k: [x * 1024.0 * scale for x in v] for k, v in per.items()}, scale
+
+
+def traffic(fetch_csv, write_csv, calib_mib):
+    """profiles/hbm_traffic.txt: per bench label, the mean over all its
+    dispatches of FETCH_SIZE + WRITE_SIZE bytes (calibrated)."""
+    fb, fs = _pmc_bytes(fetch_csv, calib_mib)
+    wb, ws = _pmc_bytes(write_csv, calib_mib)
+    out = ["# HBM bytes per launch of the config-2 decode kernels: rocprofv3 FETCH_SIZE + WRITE_SIZE (KiB per",
+           "# dispatch), each scaled so that the library's copy kernel (k_copy16, %g MiB) reads / writes that" % calib_mib,
+           "# much (FETCH_SIZE scale %.4f, WRITE_SIZE scale %.4f); every dispatch of the label's kernels in 20" % (fs, ws),
+           "# decode steps at contexts 495-514 (the window of bench.py's per-kernel timing).  Commands (from /tmp,",
+           "# TMPDIR=/tmp, PYTHONPATH=$R, QASR_DISABLE_GRAPH=1):",
+           "#   timeout -s KILL 150 rocprofv3 --pmc FETCH_SIZE --kernel-include-regex 'k_attn|k_w8a8|k_oproj|k_argmax|k_copy'"
+           " --output-format csv -d $R/gpurun_out/pmc_fetch -o run -- python3 -u -m qwenasr_amd.profile_decode 20 64 494",
+           "#   (the same with --pmc WRITE_SIZE -d $R/gpurun_out/pmc_write)",
+           "#   python -m qwenasr_amd.rocprof_summary --traffic $R/gpurun_out/pmc_fetch/run_counter_collection.csv"
+           " $R/gpurun_out/pmc_write/run_counter_collection.csv 64 > profiles/hbm_traffic.txt",
+           "# sources_sha256 %s  (qwenasr_amd/csrc/%s; bench.py reports the traffic only for these sources)"
+           % (decode_sources_hash(), ", ".join(DECODE_SOURCES)),
+           "# columns: bench kernel label, HBM bytes per launch (fetch + write), fetch bytes, write bytes, dispatches"]
+    for label, rx in DECODE_LABELS:
+        f = [x for k, v in fb.items() if re.search(rx, k) for x in v]
+        w = [x for k, v in wb.items() if re.search(rx, k) for x in v]
+        if not f or not w:
+            continue
+        out.append(f"{label} {st.mean(f) + st.mean(w):.0f} {st.mean(f):.0f} {st.mean(w):.0f} {len(f)}")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
-    if sys.argv[1] == "--pmc":
+    if sys.argv[1] == "--traffic":
+        print(traffic(sys.argv[2], sys.argv[3], float(sys.argv[4])))
+    elif sys.argv[1] == "--pmc":
         print(summarise_pmc(sys.argv[2], float(sys.argv[3])))
     else:
         print(summarise(sys.argv[1], int(sys.argv[2]) if len(sys.argv) > 2 else 20))
