@@ -77,7 +77,8 @@ struct qasr_stream {
     // encoder
     std::vector<EncWindow> win;
     int64_t enc_cached_total = 0, enc_base_windows = 0;
-    DevBuf partial;
+    DevBuf partial, partial_next;   // the partial tail's rows; the re-encode goes to partial_next, then they swap
+    std::vector<DevBuf> win_pool;   // buffers of released windows, reused by later ones
     int64_t partial_seq = 0, last_partial_cursor = 0;
     // tokens
     std::vector<int32_t> raw, stable, prev_tail;
@@ -132,8 +133,9 @@ extern "C" int qasr_hip_stream_create(qasr_decoder *d, qasr_encoder *e, const qa
     return QASR_OK;
 }
 
+// the windows' buffers go back to the pool (kept until the stream is freed)
 static void release_windows(qasr_stream *s) {
-    for (auto &w : s->win) dbuf_release(w.out);
+    for (auto &w : s->win) s->win_pool.push_back(w.out);
     s->win.clear();
 }
 
@@ -142,7 +144,8 @@ extern "C" void qasr_hip_stream_free(qasr_stream *s) {
     (void)hipSetDevice(s->d->h->device);
     (void)hipStreamSynchronize(s->d->h->stream);
     release_windows(s);
-    for (DevBuf *b : {&s->partial, &s->embeds, &s->prev_embeds, &s->audio, &s->mel, &s->melsc, &s->enc_all,
+    for (DevBuf &b : s->win_pool) dbuf_release(b);
+    for (DevBuf *b : {&s->partial, &s->partial_next, &s->embeds, &s->prev_embeds, &s->audio, &s->mel, &s->melsc, &s->enc_all,
                       &s->toks, &s->flags})
         dbuf_release(*b);
     delete s;
@@ -295,7 +298,15 @@ static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool f
     while ((s->enc_base_windows + (int64_t)s->win.size()) * win_samples < full_end) {
         const int64_t ws = (s->enc_base_windows + (int64_t)s->win.size()) * win_samples;
         EncWindow w;
-        TRY(encode_slice(s, samples + ws, win_samples, w.out, &w.seq));
+        if (!s->win_pool.empty()) {
+            w.out = s->win_pool.back();
+            s->win_pool.pop_back();
+        }
+        const int rc_w = encode_slice(s, samples + ws, win_samples, w.out, &w.seq);
+        if (rc_w != QASR_OK) {
+            s->win_pool.push_back(w.out);
+            return rc_w;
+        }
         s->enc_cached_total += w.seq;
         s->win.push_back(w);
     }
@@ -305,16 +316,12 @@ static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool f
     if (full_end < s->cursor) {
         partial_seq = s->partial_seq;                       // reuse unless re-encoded below
         if (need_encode) {
-            DevBuf fresh;
             int64_t seq = 0;
-            TRY(encode_slice(s, samples + full_end, s->cursor - full_end, fresh, &seq));
+            TRY(encode_slice(s, samples + full_end, s->cursor - full_end, s->partial_next, &seq));
             if (seq > 0) {
-                dbuf_release(s->partial);
-                s->partial = fresh;
+                std::swap(s->partial, s->partial_next);
                 s->partial_seq = partial_seq = seq;
                 s->last_partial_cursor = s->cursor;
-            } else {
-                dbuf_release(fresh);
             }
         }
     }

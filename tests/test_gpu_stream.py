@@ -64,3 +64,29 @@ def test_stream_stop_token(models, orc):
     """A stop token that the model emits first: empty chunks, speech end."""
     first = orc.transcribe_forced(models[2], models[3], models[4][:32000], 1)["tokens"][0]
     run_both(models, orc, [32000, 64000, 96000], 100000, max_new_tokens=4, stop_tokens=(int(first), -1))
+
+
+def test_stream_long_window_reuse(models, orc):
+    """44 s pushed 2 s at a time, max_new_tokens 4 / rollback 1: the repeated
+    tokens of the random-init model re-anchor the stream, and once 4 encoder
+    windows are cached a re-anchor releases them (their buffers are reused by
+    the windows encoded after), so the prompt shrinks at some push."""
+    from qwenasr_amd.model import Stream
+    from qwenasr_amd.synth import audio
+    gdec, genc, cdec, cenc, _ = models
+    x = audio(44 * 16000, 1044)
+    cfg = dict(max_new_tokens=4, rollback=1)
+    g = Stream(gdec, genc, **cfg)
+    c = orc.OracleStream(cdec, cenc, **cfg)
+    prefill = []
+    for end in range(32000, x.size + 1, 32000):
+        eg, ec = g.push(x[:end]), c.push(x[:end])
+        assert list(eg) == list(ec), (end, eg, ec)
+        sg, sc = g.stats(), c.stats()
+        assert list(sg[STAT_COLS]) == list(sc[STAT_COLS]), (end, sg, sc)
+        prefill.append(int(sg[2]))
+    assert list(g.tokens()) == list(c.tokens())
+    assert int(g.stats()[6]) >= 5
+    assert any(b < a for a, b in zip(prefill, prefill[1:])), prefill
+    g.close()
+    c.close()
