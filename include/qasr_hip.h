@@ -382,7 +382,7 @@ int qasr_hip_engine_transcribe_pcm(qasr_engine *g, const float *samples, int64_t
                                    int64_t cap, int64_t *n_out);
 /* every token of the last transcription, the stop included */
 int qasr_hip_engine_last_raw_tokens(const qasr_engine *g, int32_t *tokens_out, int64_t cap, int64_t *n);
-/* qwen_asr_stream_new / _free / _reset (c_api.rs:178-202).  Streams borrow
+/* qwen_asr_stream_new / _free / _reset (c_api.rs:179-202).  Streams borrow
  * the engine's decoder and encoder; several may be alive and interleave their
  * pushes with each other and with transcribe_pcm (a push after another
  * caller's work prefills every row instead of reusing the KV cache's rows,
@@ -392,15 +392,17 @@ int qasr_hip_engine_last_raw_tokens(const qasr_engine *g, int32_t *tokens_out, i
 int qasr_hip_engine_stream_new(qasr_engine *g, qasr_engine_stream **out);
 void qasr_hip_engine_stream_free(qasr_engine_stream *s);
 int qasr_hip_engine_stream_reset(qasr_engine_stream *s);
-/* qwen_asr_stream_push (c_api.rs:204-241): append n_samples new samples (16 kHz
- * mono f32), run stream_push_audio over the stream's audio so far; the newly
+/* qwen_asr_stream_push (c_api.rs:212-248): append n_samples new samples (16 kHz
+ * mono f32), run stream_push_audio over the stream's audio so far with the
+ * engine's current stream settings; the newly
  * committed text token ids go to tokens_out (*n_out = their count) */
 int qasr_hip_engine_stream_push(qasr_engine_stream *s, const float *samples, int64_t n_samples, int finalize,
                                 int32_t *tokens_out, int64_t cap, int64_t *n_out);
-/* qwen_asr_stream_get_result (c_api.rs:243-260): every committed text token */
+/* qwen_asr_stream_get_result (c_api.rs:250-267): every committed text token */
 int qasr_hip_engine_stream_get_result(const qasr_engine_stream *s, int32_t *tokens_out, int64_t cap, int64_t *n);
-/* qwen_asr_stream_set_* (c_api.rs:262-297): settings of streams created
- * afterwards; out-of-range values are ignored */
+/* qwen_asr_stream_set_* (c_api.rs:269-299): the settings every stream of the
+ * engine uses from its next push on (the reference reads them from its
+ * context on every push); out-of-range values are ignored */
 void qasr_hip_engine_stream_set_chunk_sec(qasr_engine *g, float sec);
 void qasr_hip_engine_stream_set_rollback(qasr_engine *g, int32_t tokens);
 void qasr_hip_engine_stream_set_unfixed_chunks(qasr_engine *g, int32_t chunks);

@@ -31,7 +31,7 @@ struct qasr_engine {
 struct qasr_engine_stream {
     qasr_engine *eng = nullptr;
     qasr_stream *s = nullptr;
-    std::vector<float> audio;       // QwenAsrStreamState::audio_buf (c_api.rs:173-177)
+    std::vector<float> audio;       // QwenAsrStreamState::audio_buf (c_api.rs:171-175)
 };
 
 namespace {
@@ -180,11 +180,10 @@ extern "C" int qasr_hip_engine_last_raw_tokens(const qasr_engine *g, int32_t *to
     return QASR_OK;
 }
 
-// ---- streaming (c_api.rs:167-297) ------------------------------------------
+// ---- streaming (c_api.rs:166-299) ------------------------------------------
 
-// qwen_asr_stream_new (c_api.rs:178-184); the state binds the engine's
-// decoder and encoder (one stream per engine at a time) with the engine's
-// stream settings at creation
+// qwen_asr_stream_new (c_api.rs:179-184); the state binds the engine's
+// decoder and encoder (the reference passes the engine to every push instead)
 extern "C" int qasr_hip_engine_stream_new(qasr_engine *g, qasr_engine_stream **out) {
     if (!g || !out) return qasr_fail(QASR_ERR_INVALID, "engine_stream_new: null argument");
     *out = nullptr;
@@ -219,15 +218,16 @@ int stream_live(const qasr_engine_stream *s) {
 }
 }  // namespace
 
-// qwen_asr_stream_reset (c_api.rs:195-202)
+// qwen_asr_stream_reset (c_api.rs:196-202)
 extern "C" int qasr_hip_engine_stream_reset(qasr_engine_stream *s) {
     if (int rc = stream_live(s)) return rc;
     s->audio.clear();
     return qasr_hip_stream_reset(s->s);
 }
 
-// qwen_asr_stream_push (c_api.rs:204-241): appends the new samples to the
-// stream's audio, runs stream_push_audio over all of it, and writes the newly
+// qwen_asr_stream_push (c_api.rs:212-248): appends the new samples to the
+// stream's audio, runs stream_push_audio over all of it with the engine's
+// current stream settings, and writes the newly
 // committed text token ids (capacity cap; *n_out = their count)
 extern "C" int qasr_hip_engine_stream_push(qasr_engine_stream *s, const float *samples, int64_t n_samples, int finalize,
                                        int32_t *tokens_out, int64_t cap, int64_t *n_out) {
@@ -239,18 +239,20 @@ extern "C" int qasr_hip_engine_stream_push(qasr_engine_stream *s, const float *s
     if (s->audio.empty()) return QASR_OK;
     if (s->eng->kv_owner != s) stream_drop_prefix(s->s);
     s->eng->kv_owner = s;
+    // the reference reads the stream settings from its context on every push
+    stream_set_config(s->s, s->eng->scfg);
     return qasr_hip_stream_push(s->s, s->audio.data(), (int64_t)s->audio.size(), finalize, tokens_out, cap, n_out);
 }
 
-// qwen_asr_stream_get_result (c_api.rs:243-260): every committed text token
+// qwen_asr_stream_get_result (c_api.rs:250-267): every committed text token
 extern "C" int qasr_hip_engine_stream_get_result(const qasr_engine_stream *s, int32_t *tokens_out, int64_t cap,
                                              int64_t *n) {
     if (int rc = stream_live(s)) return rc;
     return qasr_hip_stream_tokens(s->s, tokens_out, cap, n);
 }
 
-// qwen_asr_stream_set_* (c_api.rs:262-297): the settings of streams created
-// afterwards; out-of-range values are ignored as there
+// qwen_asr_stream_set_* (c_api.rs:269-299): the settings every stream of the
+// engine uses from its next push on; out-of-range values are ignored as there
 extern "C" void qasr_hip_engine_stream_set_chunk_sec(qasr_engine *g, float sec) {
     if (g && sec > 0.0f) g->scfg.chunk_sec = sec;
 }

@@ -41,6 +41,8 @@ void dbuf_release(DevBuf &b);
 // previous push left in the decoder's KV cache (another caller has written
 // that cache since).
 void stream_drop_prefix(qasr_stream *s);
+// Replaces the stream's settings (already validated by the caller).
+void stream_set_config(qasr_stream *s, const qasr_stream_config &c);
 
 // Multi-stream batch internals used by the streaming driver: a chunk prefill
 // from device rows into one stream's KV slot at positions [start, start + n),

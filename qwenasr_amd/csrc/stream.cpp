@@ -155,6 +155,10 @@ void stream_drop_prefix(qasr_stream *s) {
     if (s) s->prev_prefill_len = 0;
 }
 
+void stream_set_config(qasr_stream *s, const qasr_stream_config &c) {
+    if (s) s->cfg = c;
+}
+
 // StreamState::reset (transcribe.rs:865-883)
 extern "C" int qasr_hip_stream_reset(qasr_stream *s) {
     if (!s) return qasr_fail(QASR_ERR_INVALID, "stream is null");

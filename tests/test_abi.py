@@ -70,3 +70,18 @@ def test_c_smoke_builds_and_header_is_c_and_cxx(tmp_path):
                 ["g++", "-std=c++17", "-pedantic", "-Werror", "-Wall", "-x", "c++", "-fsyntax-only", hdr]):
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stderr
+
+
+def test_integration_ffi_block_is_current():
+    """INTEGRATION.md's Rust FFI module is the generator's output for the
+    current header: one declaration per entry point, nothing elided."""
+    import re
+    from qwenasr_amd import ffi_rust
+    header = open(os.path.join(ROOT, "include", "qasr_hip.h")).read()
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    m = re.search(r"<!-- ffi:begin -->\n```rust\n(.*?)```\n<!-- ffi:end -->", doc, re.S)
+    assert m, "INTEGRATION.md has no generated FFI block"
+    assert m.group(1) == ffi_rust.render(header)
+    n_decl = len(re.findall(r"^\s*pub fn qasr_hip_\w+\(", m.group(1), re.M))
+    n_header = len(set(re.findall(r"\b(qasr_hip_\w+)\s*\(", ffi_rust.strip_comments(header))))
+    assert n_decl == n_header

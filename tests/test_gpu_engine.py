@@ -123,8 +123,8 @@ def test_engine_stream(dev, engine_dir):
     print("reference streams", want_x, want_y, flush=True)
     g = Engine(path, device=0, max_seq=4096)
     try:
-        g.set_stream(**cfg)
         s = g.stream()
+        g.set_stream(**cfg)          # applies from the next push, as the reference reads its context per push
         for k in range(5):
             assert s.push(xs[k * 32000:(k + 1) * 32000], finalize=(k == 4)).tolist() == want_x[k], k
         assert s.result().tolist() == all_x
