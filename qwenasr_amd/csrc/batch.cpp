@@ -220,31 +220,39 @@ extern "C" int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float
     return rc;
 }
 
-// decoder_prefill_dev of device rows [0, n) at positions [start, start + n) of
-// stream slot `stream` (the multi-stream streaming driver's chunk prefill);
-// the slot's length becomes start + n
-int batch_prefill_dev(qasr_batch *b, int32_t stream, const float *rows, int64_t start, int64_t n) {
-    if (!b || !rows || n <= 0 || start < 0) return qasr_fail(QASR_ERR_INVALID, "batch prefill: bad arguments");
+// decoder_prefill of several stream slots at once (the multi-stream
+// streaming driver's chunk prefills): slot slots[i] gets counts[i] device rows
+// rows[i] at positions [starts[i], starts[i] + counts[i]) and that length;
+// each slot's rows get the bits a prefill of that slot alone gives
+int batch_prefill_segments(qasr_batch *b, int n, const int32_t *slots, const float *const *rows,
+                           const int64_t *starts, const int64_t *counts) {
+    if (!b || n < 0 || (n > 0 && (!slots || !rows || !starts || !counts)))
+        return qasr_fail(QASR_ERR_INVALID, "batch prefill: bad arguments");
     qasr_decoder *d = b->d;
     CHECK_H(d->h);
-    if (stream < 0 || stream >= b->B) return qasr_fail(QASR_ERR_INVALID, "batch prefill: stream out of range");
-    if (start + n > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch prefill: capacity exceeded");
     const int64_t le = stream_layer_elems(b);
-    void *kc0 = d->kc, *vc0 = d->vc;
-    const int64_t ms0 = d->max_seq, len0 = d->len, ls0 = d->kv_layer_stride;
-    d->kc = reinterpret_cast<float *>(b->kc) + stream * le;
-    d->vc = reinterpret_cast<float *>(b->vc) + stream * le;
-    d->kv_layer_stride = (int64_t)b->B * le;
-    d->max_seq = b->max_seq;
-    d->len = start;
-    const int rc = decoder_prefill_dev(d, rows, n);
-    d->kc = kc0;
-    d->vc = vc0;
-    d->kv_layer_stride = ls0;
-    d->max_seq = ms0;
-    d->len = len0;
-    if (rc == QASR_OK) b->len[stream] = start + n;
-    return rc;
+    std::vector<PrefillSeg> segs((size_t)n);
+    for (int i = 0; i < n; i++) {
+        if (slots[i] < 0 || slots[i] >= b->B) return qasr_fail(QASR_ERR_INVALID, "batch prefill: stream out of range");
+        if (starts[i] < 0 || counts[i] < 0 || starts[i] + counts[i] > b->max_seq)
+            return qasr_fail(QASR_ERR_INVALID, "batch prefill: capacity exceeded");
+        PrefillSeg &g = segs[(size_t)i];
+        g.rows = rows[i];
+        g.n = counts[i];
+        g.start = starts[i];
+        g.kc = reinterpret_cast<float *>(b->kc) + slots[i] * le;
+        g.vc = reinterpret_cast<float *>(b->vc) + slots[i] * le;
+        g.layer_elems = (int64_t)b->B * le;
+        g.head_stride = b->max_seq * d->c.head_dim;
+        g.cap = b->max_seq;
+    }
+    TRY(decoder_prefill_segments(d, segs.data(), n));
+    for (int i = 0; i < n; i++) b->len[slots[i]] = starts[i] + counts[i];
+    return QASR_OK;
+}
+
+int batch_prefill_dev(qasr_batch *b, int32_t stream, const float *rows, int64_t start, int64_t n) {
+    return batch_prefill_segments(b, 1, &stream, &rows, &start, &n);
 }
 
 int64_t batch_max_seq(const qasr_batch *b) { return b ? b->max_seq : 0; }

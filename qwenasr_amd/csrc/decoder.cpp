@@ -221,6 +221,7 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
     for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
     decoder_free_prefill(d);
     dbuf_release(d->head_out);
+    dbuf_release(d->gemm_ws);
     if (d->lm_bf16) (void)hipFree(d->lm_bf16);
     for (void *p : d->allocs) (void)hipFree(p);
     delete d;

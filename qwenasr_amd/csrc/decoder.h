@@ -51,6 +51,7 @@ struct qasr_decoder {
     int32_t host_state[4] = {0, 0, 0, 0};
     PrefillBufs pf;
     DevBuf head_out;                            // prefill_logits / prefill_argmax outputs, kept between calls
+    DevBuf gemm_ws;                             // the prefill GEMMs' split-K partials (2 x rows x 1024 f32)
     std::vector<void *> allocs;
 };
 
@@ -68,6 +69,22 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind = -1);
 int64_t decoder_ctx_cap(const qasr_decoder *d, int64_t L);
 void decoder_free_prefill(qasr_decoder *d);
 int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S);
+
+// One sequence of a multi-sequence prefill: n rows (device f32 [n][hidden])
+// at positions [start, start + n) of the KV view (kc, vc: layer 0's cache of
+// this sequence; layer_elems: the stride between layers; head_stride: between
+// KV heads, max_seq x head_dim).
+struct PrefillSeg {
+    const float *rows = nullptr;
+    int64_t n = 0, start = 0;
+    float *kc = nullptr, *vc = nullptr;
+    int64_t layer_elems = 0, head_stride = 0, cap = 0;
+};
+// decoder_prefill over several sequences at once: the GEMMs, RMSNorm and
+// SwiGLU run over all rows together, the q/k norm + RoPE + KV write and the
+// causal attention per sequence; every row gets the bits a prefill of its own
+// sequence alone would give.
+int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg);
 int decoder_run_embed_step(qasr_decoder *d);
 // host -> device decode state {token, pos = d->len, 0, 0} and the RoPE rows of pos
 int decoder_set_state(qasr_decoder *d, int32_t token);

@@ -558,9 +558,17 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     // operands ahead of the K loop, the unsplit kernel measured faster at
     // M = 375, K = 2048 (11.7 against 13.2 us) and equal at K = 3072)
     const int bk = 32, min_steps = 16;
-    const bool split = ASRC == A_F32_SPLIT && split_ok && g.ws && gx * gy <= 160 && g.K / bk >= min_steps &&
-                       (epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU || epi == EPI_SCALE) &&
-                       g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float);
+    const bool epi_ok = epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU || epi == EPI_SCALE;
+    const bool ws_ok = g.ws && g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float);
+    bool split;
+    if (g.split_by_shape && ASRC == A_F32_SPLIT) {
+        // (the tile-count rule's choice too for N <= 1024 up to 640 rows; that
+        // rule also splits N > 1024 when the rows are few enough)
+        split = split_ok && gx <= 16 && g.K / bk >= min_steps && epi_ok;
+        if (split && !ws_ok) return hipErrorInvalidValue;
+    } else {
+        split = ASRC == A_F32_SPLIT && split_ok && gx * gy <= 160 && g.K / bk >= min_steps && epi_ok && ws_ok;
+    }
     if (split) {
         const dim3 grid(gx, gy, 2), rg((unsigned)(((int64_t)g.M * g.N + 255) / 256));
         switch (epi) {

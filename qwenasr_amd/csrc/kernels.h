@@ -181,6 +181,10 @@ struct GemmArgs {
     int a_vec4, b_vec;        // set by the launcher
     float *ws;                // optional workspace for split-K partials (null: no split)
     int64_t ws_bytes;
+    // f32-class path: split K by the shape alone (N <= 1024 and K / 32 >= 16),
+    // whatever M, so that a row's result does not depend on how many rows
+    // share the call; the launch fails if the workspace is too small
+    int split_by_shape;
 };
 
 hipError_t launch_gemm(const GemmArgs &g, int asrc, int bsrc, int epi, hipStream_t st);

@@ -44,10 +44,12 @@ void stream_drop_prefix(qasr_stream *s);
 // Replaces the stream's settings (already validated by the caller).
 void stream_set_config(qasr_stream *s, const qasr_stream_config &c);
 
-// Multi-stream batch internals used by the streaming driver: a chunk prefill
-// from device rows into one stream's KV slot at positions [start, start + n),
-// the per-stream capacity and the stream count.
+// Multi-stream batch internals used by the streaming driver: chunk prefills
+// from device rows into stream KV slots at positions [start, start + n) (one
+// slot, or several in one call), the per-stream capacity and the stream count.
 int batch_prefill_dev(qasr_batch *b, int32_t stream, const float *rows, int64_t start, int64_t n);
+int batch_prefill_segments(qasr_batch *b, int n, const int32_t *slots, const float *const *rows,
+                           const int64_t *starts, const int64_t *counts);
 int64_t batch_max_seq(const qasr_batch *b);
 int32_t batch_streams(const qasr_batch *b);
 

@@ -38,12 +38,16 @@ static int ensure_prefill(qasr_decoder *d, int64_t S) {
     return QASR_OK;
 }
 
+// The prefill GEMMs split K by the shape alone (split_by_shape), so that a
+// row's result is the same whether its sequence is prefilled alone or with
+// others; their partials live in the decoder's grow-only workspace.
 static int gemm(qasr_decoder *d, const float *A, int64_t lda, const uint16_t *B, int64_t ldb, float *C,
                 int64_t ldc, int M, int N, int K, int epi) {
     GemmArgs g{};
     g.M = M; g.N = N; g.K = K;
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
-    g.ws = reinterpret_cast<float *>(d->h->scratch); g.ws_bytes = QASR_SCRATCH_BYTES;   // split-K partials
+    g.ws = d->gemm_ws.as<float>(); g.ws_bytes = (int64_t)d->gemm_ws.cap;   // split-K partials
+    g.split_by_shape = 1;
     LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, epi, d->h->stream), "prefill gemm");
     return QASR_OK;
 }
@@ -56,47 +60,83 @@ static int gemm(qasr_decoder *d, const float *A, int64_t lda, const uint16_t *B,
         }                       \
     } while (0)
 
-int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S) {
+int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg) {
     const qasr_dec_config &c = d->c;
-    if (S <= 0) return QASR_OK;
     if (d->kv_bf16) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: needs an f32 KV cache");
-    const int64_t start = d->len;
-    if (start + S > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: KV cache capacity exceeded");
+    int64_t S = 0;
+    for (int i = 0; i < n_seg; i++) {
+        const PrefillSeg &g = segs[i];
+        if (g.n < 0 || g.start < 0 || (g.n > 0 && (!g.rows || !g.kc || !g.vc)))
+            return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: bad sequence");
+        if (g.start + g.n > g.cap) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: KV cache capacity exceeded");
+        S += g.n;
+    }
+    if (S <= 0) return QASR_OK;
+    if (S > (1 << 30) / 8) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: too many rows");
     TRY(ensure_prefill(d, S));
+    TRY(dbuf_ensure(d->gemm_ws, sizeof(float) * 2 * (size_t)S * 1024));
     hipStream_t st = d->h->stream;
     PrefillBufs &p = d->pf;
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
     const int I = c.intermediate, nqkv = qd + 2 * kvd;
     const int M = (int)S;
-    const int64_t layer_elems = d->kv_layer_stride ? d->kv_layer_stride : (int64_t)c.n_kv_heads * d->max_seq * hd;
     const float scale = 1.0f / sqrtf((float)hd);
-    HIPCHK(hipMemcpyAsync(p.x, emb_dev, sizeof(float) * S * H, hipMemcpyDeviceToDevice, st));
-    const float *rc = d->rc + start * hd, *rs = d->rs + start * hd;
+    {
+        int64_t off = 0;
+        for (int i = 0; i < n_seg; i++) {
+            if (segs[i].n > 0)
+                HIPCHK(hipMemcpyAsync(p.x + off * H, segs[i].rows, sizeof(float) * segs[i].n * H,
+                                      hipMemcpyDeviceToDevice, st));
+            off += segs[i].n;
+        }
+    }
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
-        float *kc = reinterpret_cast<float *>(d->kc) + l * layer_elems;
-        float *vc = reinterpret_cast<float *>(d->vc) + l * layer_elems;
         LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.in_norm, S, H, c.eps, st), "prefill rms_norm");
         TRY(gemm(d, p.xn, H, L.bqkv, H, p.qkv, nqkv, M, nqkv, H, EPI_NONE));
-        PrefillPostArgs pp{};
-        pp.qkv = p.qkv; pp.row_stride = nqkv; pp.S = S; pp.Hq = c.n_heads; pp.Hkv = c.n_kv_heads;
-        pp.q_norm = L.q_norm; pp.k_norm = L.k_norm; pp.cos_t = rc; pp.sin_t = rs;
-        pp.kc = kc; pp.vc = vc; pp.head_stride = d->max_seq * hd; pp.start = start; pp.eps = c.eps;
-        LAUNCHCHK(launch_prefill_qkv_post(pp, st), "prefill q/k norm, rope and kv write");
-        AttnRowsArgs a{};
-        a.q = p.qkv; a.q_rs = nqkv;
-        a.k = kc; a.v = vc; a.k_hs = d->max_seq * hd; a.k_rs = hd;
-        a.out = p.att; a.o_rs = qd;
-        a.n_q = M; a.n_k = (int)(start + S);
-        a.G = c.n_heads / c.n_kv_heads; a.q_offset = (int)start; a.window = 0; a.scale = scale;
-        LAUNCHCHK(launch_attn_rows(a, c.n_kv_heads, hd, st), "prefill attention");
+        int64_t off = 0;
+        for (int i = 0; i < n_seg; i++) {
+            const PrefillSeg &g = segs[i];
+            if (g.n == 0) continue;
+            float *kc = g.kc + l * g.layer_elems;
+            float *vc = g.vc + l * g.layer_elems;
+            PrefillPostArgs pp{};
+            pp.qkv = p.qkv + off * nqkv; pp.row_stride = nqkv; pp.S = g.n; pp.Hq = c.n_heads; pp.Hkv = c.n_kv_heads;
+            pp.q_norm = L.q_norm; pp.k_norm = L.k_norm; pp.cos_t = d->rc + g.start * hd; pp.sin_t = d->rs + g.start * hd;
+            pp.kc = kc; pp.vc = vc; pp.head_stride = g.head_stride; pp.start = g.start; pp.eps = c.eps;
+            LAUNCHCHK(launch_prefill_qkv_post(pp, st), "prefill q/k norm, rope and kv write");
+            AttnRowsArgs a{};
+            a.q = p.qkv + off * nqkv; a.q_rs = nqkv;
+            a.k = kc; a.v = vc; a.k_hs = g.head_stride; a.k_rs = hd;
+            a.out = p.att + off * qd; a.o_rs = qd;
+            a.n_q = (int)g.n; a.n_k = (int)(g.start + g.n);
+            a.G = c.n_heads / c.n_kv_heads; a.q_offset = (int)g.start; a.window = 0; a.scale = scale;
+            LAUNCHCHK(launch_attn_rows(a, c.n_kv_heads, hd, st), "prefill attention");
+            off += g.n;
+        }
         TRY(gemm(d, p.att, qd, L.bo, qd, p.x, H, M, H, qd, EPI_ACCUM));
         LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.post_norm, S, H, c.eps, st), "prefill rms_norm");
         TRY(gemm(d, p.xn, H, L.bgu, H, p.gu, 2 * I, M, 2 * I, H, EPI_NONE));
         LAUNCHCHK(launch_swiglu_rows(p.g, p.gu, S, I, st), "prefill swiglu");
         TRY(gemm(d, p.g, I, L.bdown, I, p.x, H, M, H, I, EPI_ACCUM));
     }
-    d->len = start + S;
+    return QASR_OK;
+}
+
+int decoder_prefill_dev(qasr_decoder *d, const float *emb_dev, int64_t S) {
+    const qasr_dec_config &c = d->c;
+    if (S <= 0) return QASR_OK;
+    PrefillSeg g;
+    g.rows = emb_dev;
+    g.n = S;
+    g.start = d->len;
+    g.kc = reinterpret_cast<float *>(d->kc);
+    g.vc = reinterpret_cast<float *>(d->vc);
+    g.head_stride = d->max_seq * c.head_dim;
+    g.layer_elems = d->kv_layer_stride ? d->kv_layer_stride : (int64_t)c.n_kv_heads * g.head_stride;
+    g.cap = d->max_seq;
+    TRY(decoder_prefill_segments(d, &g, 1));
+    d->len = g.start + S;
     return QASR_OK;
 }
 

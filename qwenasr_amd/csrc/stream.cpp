@@ -231,6 +231,7 @@ static void carry_reset(qasr_stream *s) {
 struct PrefillTarget {
     qasr_batch *b = nullptr;
     int32_t slot = 0;
+    bool defer = false;   // leave the rows to the caller's multi-slot prefill (ChunkPlan rows / reused / delta)
 };
 
 // What a prepared chunk hands to the decode and the commit.
@@ -239,6 +240,8 @@ struct ChunkPlan {
     int64_t prefill_len = 0;       // rows prefilled; the last prompt row is decoded first
     int64_t n_prefix_tokens = 0;   // rolled-back text tokens at the prompt's end
     int32_t last_token = 0;        // the prompt's last row is this token's embedding
+    const float *rows = nullptr;   // a deferred prefill: delta rows at position reused
+    int64_t reused = 0, delta = 0;
 };
 
 // greedy decode of up to max_new tokens after the prefill of prefill_len rows
@@ -383,8 +386,13 @@ static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool f
         while (reused < cmp && !fl[reused]) reused++;
     }
     const int64_t delta = prefill_len - reused;
-    if (tgt.b) {
-        if (delta > 0) TRY(batch_prefill_dev(tgt.b, tgt.slot, s->embeds.as<float>() + reused * H, reused, delta));
+    pl.rows = s->embeds.as<float>() + reused * H;
+    pl.reused = reused;
+    pl.delta = delta;
+    if (tgt.b && tgt.defer) {
+        // the stream batch prefills every stream of the round in one call
+    } else if (tgt.b) {
+        if (delta > 0) TRY(batch_prefill_dev(tgt.b, tgt.slot, pl.rows, reused, delta));
         else TRY(qasr_hip_batch_set_len(tgt.b, tgt.slot, reused));
     } else {
         d->len = reused;
@@ -486,11 +494,12 @@ extern "C" int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_
 // ---- many streams, one batched decode ---------------------------------------
 // N streaming states over one decoder and encoder whose chunks decode together
 // on a multi-stream batch (BASELINE config 4 fed by the real pipeline): per
-// round, every stream with a pending chunk runs its encoder and its prompt
-// prefill (common-prefix reuse within its own KV slot), then all of them take
-// their greedy steps together in bursts of DECODE_BURST (M = streams per
-// projection), each stopping at its own stop token or max_new_tokens, then
-// each commits its tokens.  Per stream, the sequence of operations is that of
+// round, every stream with a pending chunk runs its encoder and builds its
+// prompt (common-prefix reuse within its own KV slot), one prefill of all
+// their changed rows fills the slots, then all of them take their greedy
+// steps together in bursts of DECODE_BURST (M = streams per projection), each
+// stopping at its own stop token or max_new_tokens, then each commits its
+// tokens.  Per stream, the sequence of operations is that of
 // qasr_hip_stream_push; the batch's decode is the lone decoder's arithmetic.
 struct qasr_stream_batch {
     qasr_decoder *d = nullptr;
@@ -599,7 +608,7 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
                 continue;
             }
             bool skip = false;
-            TRY(chunk_prepare(g->s[i], samples[i], n_samples[i], fin, PrefillTarget{g->b, i}, pl[i], &skip));
+            TRY(chunk_prepare(g->s[i], samples[i], n_samples[i], fin, PrefillTarget{g->b, i, true}, pl[i], &skip));
             if (skip) {
                 emitted[i].clear();
                 open[i] = 0;
@@ -608,6 +617,21 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
             act.push_back(i);
         }
         if (act.empty()) break;
+        // one prefill of every stream's changed prompt rows (GEMMs over all of
+        // them), each into its own slot
+        {
+            std::vector<int32_t> slots;
+            std::vector<const float *> rows;
+            std::vector<int64_t> starts, counts;
+            for (int i : act) {
+                slots.push_back(i);
+                rows.push_back(pl[i].rows);
+                starts.push_back(pl[i].reused);
+                counts.push_back(pl[i].delta);
+            }
+            TRY(batch_prefill_segments(g->b, (int)act.size(), slots.data(), rows.data(), starts.data(),
+                                       counts.data()));
+        }
         TRY(group_decode(g, act, pl, chunks));
         for (int i : act) {
             bool ended = false;
