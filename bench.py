@@ -46,7 +46,10 @@ def traffic_from_profiles(kernel):
                 value = float(parts[1])
             except ValueError:
                 value = None
-    current = decode_sources_hash()
+    try:
+        current = decode_sources_hash()
+    except OSError as e:
+        return None, f"the decode kernel sources are not readable here ({e}), so the recorded traffic cannot be matched"
     if measured_on != current:
         return None, f"profiles/hbm_traffic.txt was measured on kernel sources {measured_on}, these are {current}"
     return value, f"rocprofv3 FETCH_SIZE + WRITE_SIZE per launch (profiles/hbm_traffic.txt, sources {current})"

@@ -24,9 +24,9 @@ import statistics as st
 import sys
 from collections import defaultdict
 
-# the sources that decide the decode kernels' memory traffic (kernels, launch
-# shapes, split and partition choices)
-DECODE_SOURCES = ("common.h", "decoder.cpp", "k_attn.hip", "k_int8.hip", "model.h")
+# the device code of the decode kernels (a change of their launch shapes or
+# partitions in the host code also calls for a new measurement)
+DECODE_SOURCES = ("common.h", "k_attn.hip", "k_int8.hip")
 
 # bench.py's decode kernel labels -> the 0.6B decoder's kernels (rocprofv3 names)
 DECODE_LABELS = (("norm+qkv", r"k_w8a8<1, 4, 0, true, false>"),
