@@ -462,7 +462,8 @@ int qasr_hip_stream_reset(qasr_stream *s);
 /* samples: the whole audio of the stream so far (16 kHz mono f32); processes
  * every complete chunk past the cursor (and the rest when finalize != 0) and
  * writes the newly committed text token ids to tokens_out (capacity cap);
- * n_out = their count */
+ * n_out = their count.  After a failed push the stream's position is not
+ * defined: reset it before pushing again. */
 int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_t n_samples, int finalize,
                          int32_t *tokens_out, int64_t cap, int64_t *n_out);
 /* every committed text token so far (up to cap); n = the total count */
@@ -495,7 +496,8 @@ qasr_stream *qasr_hip_stream_batch_stream(qasr_stream_batch *g, int32_t i);
  * (nullable) per stream; stream i's newly committed text tokens go to
  * tokens_out + i * cap (nullable), n_out[i] = their count.  Streams advance
  * chunk by chunk in rounds until none has a complete chunk left (or, when
- * finalizing, any audio). */
+ * finalizing, any audio).  After a failed push the streams' positions are not
+ * defined: reset them before pushing again. */
 int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *const *samples, const int64_t *n_samples,
                                const int32_t *finalize, int32_t *tokens_out, int64_t cap, int64_t *n_out);
 

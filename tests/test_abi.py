@@ -85,3 +85,12 @@ def test_integration_ffi_block_is_current():
     n_decl = len(re.findall(r"^\s*pub fn qasr_hip_\w+\(", m.group(1), re.M))
     n_header = len(set(re.findall(r"\b(qasr_hip_\w+)\s*\(", ffi_rust.strip_comments(header))))
     assert n_decl == n_header
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N > 1 exits with status 2 and says why, before touching a GPU."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr

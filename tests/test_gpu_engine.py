@@ -145,3 +145,22 @@ def test_engine_stream(dev, engine_dir):
     with pytest.raises(RuntimeError, match="engine was freed"):
         s.push(xs[:1600])
     s.close()
+
+
+def test_engine_edge_cases(engine_dir):
+    """Audio shorter than one mel frame is refused before any launch; a push of
+    no new samples commits nothing; a stream's result before any push is empty."""
+    from qwenasr_amd._lib import QasrError
+    from qwenasr_amd.model import Engine
+    path, _, _ = engine_dir
+    g = Engine(path, device=0, max_seq=1024)
+    try:
+        with pytest.raises(QasrError, match="too short|bad arguments"):
+            g.transcribe_pcm(np.zeros(100, np.float32))
+        s = g.stream()
+        assert s.result().tolist() == []
+        assert s.push(np.zeros(0, np.float32)).tolist() == []
+        assert s.result().tolist() == []
+        s.close()
+    finally:
+        g.close()

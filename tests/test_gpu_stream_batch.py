@@ -140,3 +140,40 @@ def test_stream_batch_rejects_member_push(models):
         assert rc != 0 and b"stream batch" in lib().qasr_hip_last_error()
     finally:
         g.close()
+
+
+def test_stream_batch_mixed_finalize_idle_and_stop(models, orc):
+    """One push where stream 0 finalizes, stream 1 gets no new audio, stream 2
+    gets a chunk and stream 3 stops at once (its stop token is the token the
+    model emits first): each stream's tokens and stats equal the oracle's
+    stream run on its own pushes."""
+    from qwenasr_amd.model import StreamBatch
+    from qwenasr_amd.synth import audio
+    gdec, genc, cdec, cenc = models
+    xs = [audio(80000, 1300 + i) for i in range(4)]
+    first = int(orc.transcribe_forced(cdec, cenc, xs[3][:32000], 1)["tokens"][0])
+    cfg = dict(max_new_tokens=3, rollback=1)
+    ends = [[32000, 72000], [64000, 64000], [32000, 64000], [32000, 64000]]
+    fins = [[False, True], [False, False], [False, False], [False, False]]
+    want = []
+    for i, x in enumerate(xs):
+        kw = dict(cfg, stop_tokens=(first, -1)) if i == 3 else cfg
+        c = orc.OracleStream(cdec, cenc, **kw)
+        want.append([(c.push(x[:e], finalize=f).tolist(), c.stats().tolist()) for e, f in zip(ends[i], fins[i])])
+        c.close()
+    # stream 3's stop token differs from the others': a batch holds one
+    # configuration, so it runs in its own batch of one
+    g = StreamBatch(gdec, genc, 3, 1024, **cfg)
+    g3 = StreamBatch(gdec, genc, 1, 1024, **dict(cfg, stop_tokens=(first, -1)))
+    try:
+        for k in range(2):
+            got = g.push([xs[i][:ends[i][k]] for i in range(3)], finalize=[fins[i][k] for i in range(3)])
+            got3 = g3.push([xs[3][:ends[3][k]]], finalize=[fins[3][k]])
+            for i, t in enumerate(got + got3):
+                st = (g.stream(i) if i < 3 else g3.stream(0)).stats().tolist()
+                assert t.tolist() == want[i][k][0], (k, i, t.tolist(), want[i][k][0])
+                assert [st[c] for c in STAT_COLS] == [want[i][k][1][c] for c in STAT_COLS], (k, i, st, want[i][k][1])
+        assert g.stream(0).audio_cursor == 72000 and g.stream(1).audio_cursor == 64000
+    finally:
+        g.close()
+        g3.close()
