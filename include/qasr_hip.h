@@ -358,6 +358,42 @@ int qasr_hip_transcribe(qasr_decoder *d, qasr_encoder *e, const float *samples, 
  * order; written to out (nullable: count only).  Returns the count (-1 for a
  * null raw).  Host only. */
 int64_t qasr_hip_text_tokens(const int32_t *raw, int64_t n, int32_t *out);
+/* The optional ids of transcribe_segment's prompt (transcribe.rs:97-169), as
+ * QwenCtx::prepare_prompt_tokens (context.rs:197-230) leaves them:
+ *   prompt: QwenCtx::prompt_tokens, the tokenizer's ids of the text prompt,
+ *           placed between PREFIX_HEAD and PREFIX_TAIL;
+ *   force:  QwenCtx::force_prompt_tokens, the ids of "language <Name>"
+ *           followed by <asr_text> (151704), placed after SUFFIX_BASE.
+ * A null pointer with a zero count leaves that part out. */
+typedef struct {
+    const int32_t *prompt;
+    int64_t n_prompt;
+    const int32_t *force;
+    int64_t n_force;
+} qasr_prompt;
+/* transcribe_segment (transcribe.rs:63-247) with its whole prompt: PREFIX_HEAD,
+ * prompt, PREFIX_TAIL, the audio rows, SUFFIX_BASE, force, and when n_past > 0
+ * the previous segments' text ids (past) followed by <asr_text>; then the
+ * decode loop of qasr_hip_transcribe.  prompt may be null.  Every id must lie
+ * in [0, vocab). */
+int qasr_hip_transcribe_prompt(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n_samples,
+                               const qasr_prompt *prompt, const int32_t *past, int64_t n_past,
+                               int32_t max_tokens, int32_t *tokens_out, int64_t *n_out, double *times_ms);
+/* qasr_hip_text_tokens with the text region open from the first token when
+ * text_open != 0, as transcribe_segment starts when its prompt holds
+ * forced-language or past-text ids (past_asr_text, transcribe.rs:196); a
+ * later <asr_text> is skipped, not counted.  Host only. */
+int64_t qasr_hip_text_tokens_from(const int32_t *raw, int64_t n, int text_open, int32_t *out);
+/* transcribe_audio's segment starts (transcribe.rs:323-341): 0, then, while
+ * the audio after the last start is longer than segment_sec plus the search
+ * margin, the center of the quietest 100 ms window (1600 samples, hop 800,
+ * least mean square, the first of equal minima) within +-search of that start
+ * + segment_sec (find_split_point, transcribe.rs:252-277), where search =
+ * min(search_sec, segment_sec / 2); at most 127 starts.  segment_sec <= 0 or
+ * short audio: the one start 0.  Returns the count (-1 on bad arguments) and
+ * writes min(count, cap) starts.  Host only. */
+int64_t qasr_hip_segment_splits(const float *samples, int64_t n_samples, float segment_sec, float search_sec,
+                                int64_t *splits_out, int64_t cap);
 
 /* ---- the reference's C API (c_api.rs) at token level -------------------------
  * Text is token ids; turning them into bytes is the caller's tokenizer
@@ -380,8 +416,33 @@ int qasr_hip_engine_config(const qasr_engine *g, qasr_dec_config *dc, qasr_enc_c
  * *n_out = their count). */
 int qasr_hip_engine_transcribe_pcm(qasr_engine *g, const float *samples, int64_t n_samples, int32_t *tokens_out,
                                    int64_t cap, int64_t *n_out);
-/* every token of the last transcription, the stop included */
+/* every token of the last transcription, the stop included (segments one
+ * after another) */
 int qasr_hip_engine_last_raw_tokens(const qasr_engine *g, int32_t *tokens_out, int64_t cap, int64_t *n);
+/* the segments of the last transcribe_pcm, [n][4] int64: first sample, end
+ * sample, index of the segment's first text id in transcribe_pcm's output,
+ * its count of text ids (0: transcribe_audio skips the segment's empty text,
+ * transcribe.rs:382).  The caller's text step joins the segments' texts with
+ * a space where should_insert_boundary_space (transcribe.rs:279-286) asks. */
+int qasr_hip_engine_last_segments(const qasr_engine *g, int64_t *bounds, int64_t cap, int64_t *n);
+/* qwen_asr_set_segment_sec (c_api.rs:123-129): transcribe_pcm cuts audio longer
+ * than sec plus the search margin at qasr_hip_segment_splits and transcribes
+ * the segments one after another, each cut one zero-padded to 0.5 s at least
+ * (transcribe.rs:343-372); 0 (the default): one segment */
+void qasr_hip_engine_set_segment_sec(qasr_engine *g, float sec);
+/* QwenCtx::search_sec (context.rs:145; default 3.0): the split search radius */
+void qasr_hip_engine_set_search_sec(qasr_engine *g, float sec);
+/* qwen_asr_set_language (c_api.rs:131-148) at token level: ids = the caller's
+ * tokenizer encoding of "language " + the normalized language name
+ * (set_force_language, context.rs:177-195); the engine appends <asr_text> as
+ * prepare_prompt_tokens does (context.rs:215-221).  n = 0: automatic language
+ * (the reference's empty string).  Used by transcribe_pcm and by every
+ * stream's next push.  Ids outside the vocabulary: QASR_ERR_INVALID, the
+ * setting unchanged. */
+int qasr_hip_engine_set_language_tokens(qasr_engine *g, const int32_t *ids, int64_t n);
+/* QwenCtx::set_prompt (context.rs:165-175) at token level: the encoded text
+ * prompt for transcribe_pcm and every stream's next push; n = 0 clears */
+int qasr_hip_engine_set_prompt_tokens(qasr_engine *g, const int32_t *ids, int64_t n);
 /* qwen_asr_stream_new / _free / _reset (c_api.rs:179-202).  Streams borrow
  * the engine's decoder and encoder; several may be alive and interleave their
  * pushes with each other and with transcribe_pcm (a push after another
@@ -468,6 +529,11 @@ int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_t n_samples
                          int32_t *tokens_out, int64_t cap, int64_t *n_out);
 /* every committed text token so far (up to cap); n = the total count */
 int qasr_hip_stream_tokens(const qasr_stream *s, int32_t *tokens_out, int64_t cap, int64_t *n);
+/* QwenCtx::prompt_tokens / force_prompt_tokens (the qasr_prompt ids, copied)
+ * for the stream's next chunks (transcribe.rs:1037-1089); null clears both.
+ * With forced-language ids every decoded token of the tail is text
+ * (transcribe.rs:1166-1172, 1257-1263).  Also for a stream batch's members. */
+int qasr_hip_stream_set_prompt(qasr_stream *s, const qasr_prompt *prompt);
 int64_t qasr_hip_stream_audio_cursor(const qasr_stream *s);
 /* chunks processed, last chunk's reused prefill rows, prefill length, rows
  * prefilled, forwards, total forwards, encoder windows encoded, raw tokens */

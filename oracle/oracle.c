@@ -1159,8 +1159,28 @@ static double now_ms(void) {
     return ts.tv_sec * 1e3 + ts.tv_nsec * 1e-6;
 }
 
-int64_t or_transcribe_forced(or_decoder *d, or_encoder *e, const float *samples,
-                             int64_t n_samples, int32_t n_steps, int32_t *tokens,
+int64_t or_prompt_ids(const int32_t *prompt, int64_t n_prompt, const int32_t *force, int64_t n_force,
+                      const int32_t *past, int64_t n_past, int32_t *head, int64_t *n_head, int32_t *tail,
+                      int64_t *n_tail) {
+    /* transcribe.rs:97-169: PREFIX_HEAD | prompt | PREFIX_TAIL before the audio
+     * rows; SUFFIX_BASE | force | past | <asr_text> (the last two only when
+     * there are past tokens) after them */
+    int64_t h = 0, t = 0;
+    for (int i = 0; i < 3; i++) head[h++] = PREFIX_HEAD[i];
+    for (int64_t i = 0; i < n_prompt; i++) head[h++] = prompt[i];
+    for (int i = 0; i < 6; i++) head[h++] = PREFIX_TAIL[i];
+    for (int i = 0; i < 6; i++) tail[t++] = SUFFIX_BASE[i];
+    for (int64_t i = 0; i < n_force; i++) tail[t++] = force[i];
+    for (int64_t i = 0; i < n_past; i++) tail[t++] = past[i];
+    if (n_past > 0) tail[t++] = 151704;   /* TOKEN_ASR_TEXT */
+    *n_head = h;
+    *n_tail = t;
+    return h + t;
+}
+
+int64_t or_transcribe_prompt(or_decoder *d, or_encoder *e, const float *samples, int64_t n_samples,
+                             const int32_t *prompt, int64_t n_prompt, const int32_t *force, int64_t n_force,
+                             const int32_t *past, int64_t n_past, int32_t n_steps, int32_t *tokens,
                              float *margins, double *times_ms) {
     int64_t H = d->c.hidden;
     double t0 = now_ms();
@@ -1172,15 +1192,19 @@ int64_t or_transcribe_forced(or_decoder *d, or_encoder *e, const float *samples,
     float *enc = (float *)malloc(sizeof(float) * T * H);
     or_encoder_forward(e, mel, nf, enc);
     double t2 = now_ms();
-    int64_t np = 3, nt = 6, ns = 6;
-    int64_t total = np + nt + T + ns;
+    int32_t *head = (int32_t *)malloc(sizeof(int32_t) * (9 + n_prompt));
+    int32_t *tail = (int32_t *)malloc(sizeof(int32_t) * (7 + n_force + n_past));
+    int64_t nh = 0, ns = 0;
+    or_prompt_ids(prompt, n_prompt, force, n_force, past, n_past, head, &nh, tail, &ns);
+    int64_t total = nh + T + ns;
     float *emb = (float *)malloc(sizeof(float) * total * H);
     int64_t o = 0;
-    for (int i = 0; i < np; i++) or_embed_token(d, PREFIX_HEAD[i], emb + (o++) * H);
-    for (int i = 0; i < nt; i++) or_embed_token(d, PREFIX_TAIL[i], emb + (o++) * H);
+    for (int64_t i = 0; i < nh; i++) or_embed_token(d, head[i], emb + (o++) * H);
     memcpy(emb + o * H, enc, sizeof(float) * T * H);
     o += T;
-    for (int i = 0; i < ns; i++) or_embed_token(d, SUFFIX_BASE[i], emb + (o++) * H);
+    for (int64_t i = 0; i < ns; i++) or_embed_token(d, tail[i], emb + (o++) * H);
+    free(head);
+    free(tail);
     d->len = 0;
     or_decoder_prefill(d, emb, total - 1);
     float bv, sv;
@@ -1198,4 +1222,70 @@ int64_t or_transcribe_forced(or_decoder *d, or_encoder *e, const float *samples,
     if (times_ms) { times_ms[0] = t1 - t0; times_ms[1] = t2 - t1; times_ms[2] = t3 - t2; times_ms[3] = t4 - t3; }
     free(mel); free(enc); free(emb); free(te);
     return total;
+}
+
+int64_t or_transcribe_forced(or_decoder *d, or_encoder *e, const float *samples,
+                             int64_t n_samples, int32_t n_steps, int32_t *tokens,
+                             float *margins, double *times_ms) {
+    return or_transcribe_prompt(d, e, samples, n_samples, NULL, 0, NULL, 0, NULL, 0, n_steps, tokens, margins,
+                                times_ms);
+}
+
+/* ======================================================================= */
+/* segmentation of long audio (transcribe.rs:252-277, 323-341)              */
+/* ======================================================================= */
+
+/* Rust's `f32 as usize`: truncation toward zero, negative and NaN to 0 */
+static int64_t f32_to_count(float v) {
+    if (!(v > 0.0f)) return 0;
+    if (v >= 9.2e18f) return INT64_MAX;
+    return (int64_t)v;
+}
+
+/* find_split_point (transcribe.rs:252-277): the center of the 100 ms window
+ * (1600 samples, hop 800) of least mean energy inside target +- search_sec;
+ * the first of equal minima; target itself when no window fits */
+int64_t or_find_split_point(const float *x, int64_t n, int64_t target, float search_sec) {
+    const int64_t half = f32_to_count(search_sec * 16000.0f);
+    const int64_t lo = target > half ? target - half : 0;
+    const int64_t hi = target + half < n ? target + half : n;
+    const int64_t win = 1600;
+    float best = 1e30f;
+    int64_t center = target;
+    for (int64_t pos = lo; pos + win <= hi; pos += win / 2) {
+        const int64_t end = pos + win < n ? pos + win : n;
+        float energy = 0.0f;
+        for (int64_t i = pos; i < end; i++) energy += x[i] * x[i];
+        energy /= (float)(end - pos);
+        if (energy < best) {
+            best = energy;
+            center = pos + (end - pos) / 2;
+        }
+    }
+    return center;
+}
+
+/* transcribe_audio's split points (transcribe.rs:323-341): 0, then one split
+ * near every segment_sec until the rest fits in one segment plus the search
+ * margin, at most 127 in all.  Returns the count; writes min(count, cap). */
+int64_t or_segment_splits(const float *x, int64_t n, float segment_sec, float search_sec, int64_t *splits,
+                          int64_t cap) {
+    const int64_t target = f32_to_count(segment_sec * 16000.0f);
+    const float half_seg = segment_sec / 2.0f;
+    /* f32::min: a NaN operand yields the other one */
+    const float search = isnan(half_seg) ? search_sec : (search_sec < half_seg ? search_sec : half_seg);
+    const int64_t margin = f32_to_count(search * 16000.0f);
+    int64_t k = 0;
+    if (cap > 0) splits[0] = 0;
+    k = 1;
+    if (segment_sec <= 0.0f || n <= target + margin) return k;
+    int64_t pos = 0;
+    while (pos + target + margin < n) {
+        const int64_t s = or_find_split_point(x, n, pos + target, search);
+        if (k < cap) splits[k] = s;
+        k++;
+        pos = s;
+        if (k >= 127) break;
+    }
+    return k;
 }

@@ -96,6 +96,11 @@ _SIGS = {
     "or_encoder_tokens": (I64, [P, I64]),
     "or_encoder_forward": (I64, [P, P, I64, P]),
     "or_transcribe_forced": (I64, [P, P, P, I64, I32, P, P, P]),
+    "or_transcribe_prompt": (I64, [P, P, P, I64, P, I64, P, I64, P, I64, I32, P, P, P]),
+    "or_prompt_ids": (I64, [P, I64, P, I64, P, I64, P, P, P, P]),
+    "or_find_split_point": (I64, [P, I64, I64, C.c_float]),
+    "or_segment_splits": (I64, [P, I64, C.c_float, C.c_float, P, I64]),
+    "or_stream_set_prompt": (None, [P, P, I64, P, I64]),
     "or_stream_default_config": (None, [P]),
     "or_stream_create": (P, [P, P, P, I64]),
     "or_stream_destroy": (None, [P]),
@@ -442,14 +447,47 @@ class OracleEncoder:
         return out
 
 
-def transcribe_forced(dec, enc, samples, n_steps):
+def _ids(a):
+    a = np.ascontiguousarray(a if a is not None else [], np.int32)
+    return a, (_p(a) if a.size else None), a.size
+
+
+def transcribe_forced(dec, enc, samples, n_steps, prompt=None, force=None, past=None):
+    """or_transcribe_prompt: transcribe_segment (transcribe.rs:63-247) with
+    n_steps greedy forwards and the optional prompt / forced-language / past
+    text ids of its prompt layout (transcribe.rs:97-169)."""
     s = f32(samples)
     toks = np.empty(n_steps, np.int32)
     margins = np.empty(n_steps, np.float32)
     times = np.empty(4, np.float64)
-    total = lib().or_transcribe_forced(dec.d, enc.e, _p(s), s.size, n_steps, _p(toks), _p(margins),
-                                       _p(times))
+    (pa, pp, pn), (fa, fp, fn), (qa, qp, qn) = _ids(prompt), _ids(force), _ids(past)
+    total = lib().or_transcribe_prompt(dec.d, enc.e, _p(s), s.size, pp, pn, fp, fn, qp, qn, n_steps, _p(toks),
+                                       _p(margins), _p(times))
     return dict(tokens=toks, margins=margins, times_ms=times, prompt_len=int(total))
+
+
+def prompt_ids(prompt=None, force=None, past=None):
+    """The id rows before and after the audio rows (transcribe.rs:97-169)."""
+    (pa, pp, pn), (fa, fp, fn), (qa, qp, qn) = _ids(prompt), _ids(force), _ids(past)
+    head = np.empty(9 + pn, np.int32)
+    tail = np.empty(7 + fn + qn, np.int32)
+    nh, nt = I64(), I64()
+    lib().or_prompt_ids(pp, pn, fp, fn, qp, qn, _p(head), C.byref(nh), _p(tail), C.byref(nt))
+    return head[:nh.value].copy(), tail[:nt.value].copy()
+
+
+def find_split_point(samples, target, search_sec):
+    x = f32(samples)
+    return int(lib().or_find_split_point(_p(x), x.size, int(target), float(search_sec)))
+
+
+def segment_splits(samples, segment_sec, search_sec=3.0):
+    """transcribe_audio's split points (transcribe.rs:323-341)."""
+    x = f32(samples)
+    out = np.empty(128, np.int64)
+    n = lib().or_segment_splits(_p(x) if x.size else None, x.size, float(segment_sec), float(search_sec), _p(out),
+                                out.size)
+    return out[:n].copy()
 
 
 class StreamConfig(C.Structure):
@@ -483,6 +521,11 @@ class OracleStream:
         self.cfg = stream_config(**cfg)
         self.dec, self.enc = dec, enc
         self.s = lib().or_stream_create(dec.d, enc.e, C.byref(self.cfg), dec.cfg["hidden"])
+
+    def set_prompt(self, prompt=None, force=None):
+        """QwenCtx::prompt_tokens / force_prompt_tokens for the next chunks."""
+        (pa, pp, pn), (fa, fp, fn) = _ids(prompt), _ids(force)
+        lib().or_stream_set_prompt(self.s, pp, pn, fp, fn)
 
     def push(self, samples, finalize=False):
         x = f32(samples)

@@ -55,6 +55,7 @@ struct or_stream {
     float *partial;
     int64_t partial_seq, last_partial_cursor;
     ivec raw, stable, prev_tail, out;
+    ivec prompt, force;   /* QwenCtx::prompt_tokens / force_prompt_tokens */
     float *prev_embeds;
     int64_t prev_prefill_len;
     int stale;
@@ -97,6 +98,8 @@ void or_stream_destroy(or_stream *s) {
     free(s->stable.v);
     free(s->prev_tail.v);
     free(s->out.v);
+    free(s->prompt.v);
+    free(s->force.v);
     free(s);
 }
 
@@ -138,7 +141,19 @@ static float *encode(or_stream *s, const float *samples, int64_t ns, int64_t *se
 
 static int is_stop(const or_stream *s, int32_t t) { return t == s->cfg.stop_tokens[0] || t == s->cfg.stop_tokens[1]; }
 
-static int64_t text_start(const ivec *raw) {
+void or_stream_set_prompt(or_stream *s, const int32_t *prompt, int64_t n_prompt, const int32_t *force,
+                          int64_t n_force) {
+    s->prompt.n = 0;
+    for (int64_t i = 0; i < n_prompt; i++) iv_push(&s->prompt, prompt[i]);
+    s->force.n = 0;
+    for (int64_t i = 0; i < n_force; i++) iv_push(&s->force, force[i]);
+}
+
+/* the text region of raw (transcribe.rs:1166-1172, 1257-1263): after the
+ * first <asr_text>, or all of it when the language is forced (the forced ids
+ * end with <asr_text> themselves) */
+static int64_t text_start(const or_stream *s, const ivec *raw) {
+    if (s->force.n > 0) return 0;
     for (int64_t i = 0; i < raw->n; i++)
         if (raw->v[i] == TOKEN_ASR_TEXT) return i + 1;
     return 0;
@@ -214,11 +229,12 @@ static int process_chunk(or_stream *s, const float *samples, int64_t n, int fina
         (s->cfg.past_text_conditioning && s->chunk_idx >= s->cfg.unfixed_chunks && s->raw.n > 0)
             ? (s->raw.n - rollback > 0 ? s->raw.n - rollback : 0)
             : 0;
-    const int64_t prefix_len = 3 + 6, suffix_len = 6;
+    const int64_t prefix_len = 3 + s->prompt.n + 6, suffix_len = 6 + s->force.n;
     const int64_t total_seq = prefix_len + enc_len + suffix_len + n_prefix_tokens;
     float *emb = (float *)malloc(sizeof(float) * total_seq * H);
     int64_t off = 0;
     for (int i = 0; i < 3; i++) or_embed_token(s->d, PREFIX_HEAD[i], emb + (off++) * H);
+    for (int64_t i = 0; i < s->prompt.n; i++) or_embed_token(s->d, s->prompt.v[i], emb + (off++) * H);
     for (int i = 0; i < 6; i++) or_embed_token(s->d, PREFIX_TAIL[i], emb + (off++) * H);
     for (int64_t w = 0; w < s->n_win; w++) {
         memcpy(emb + off * H, s->win_out[w], sizeof(float) * s->win_seq[w] * H);
@@ -229,6 +245,7 @@ static int process_chunk(or_stream *s, const float *samples, int64_t n, int fina
         off += partial_seq;
     }
     for (int i = 0; i < 6; i++) or_embed_token(s->d, SUFFIX_BASE[i], emb + (off++) * H);
+    for (int64_t i = 0; i < s->force.n; i++) or_embed_token(s->d, s->force.v[i], emb + (off++) * H);
     for (int64_t i = 0; i < n_prefix_tokens; i++) or_embed_token(s->d, s->raw.v[i], emb + (off++) * H);
 
     /* prefill with reuse of the rows equal to the previous chunk's (float equality, :1095-1104) */
@@ -277,7 +294,7 @@ static int process_chunk(or_stream *s, const float *samples, int64_t n, int fina
 
     const int speech_ended = chunk.n == 0 && s->raw.n > 0 && s->chunk_idx >= s->cfg.unfixed_chunks;
     if (speech_ended) {
-        const int64_t ts = text_start(&s->raw);
+        const int64_t ts = text_start(s, &s->raw);
         const int64_t n_text = s->raw.n - ts;
         for (int64_t i = s->stable.n; i < n_text; i++) emit(s, s->raw.v[ts + i]);
     }
@@ -295,7 +312,7 @@ static int process_chunk(or_stream *s, const float *samples, int64_t n, int fina
         const int64_t reps = or_tail_repeat_blocks(s->raw.v, s->raw.n, DEGEN_MAX_PERIOD, NULL);
         if (s->stale >= STALE_CHUNKS || reps >= DEGEN_MIN_REPEATS) carry_reset(s);
         if (s->chunk_idx > 0 && s->chunk_idx % RESET_INTERVAL_CHUNKS == 0) carry_reset(s);
-        const int64_t ts = text_start(&s->raw);
+        const int64_t ts = text_start(s, &s->raw);
         const int64_t n_text = s->raw.n - ts;
         int64_t cand = 0;
         if (is_final) cand = n_text;

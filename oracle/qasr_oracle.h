@@ -28,9 +28,17 @@
  *   layer_norm                  : numpy float64 mean/var
  *   sgemm                       : numpy float64 matmul
  *   mel                         : numpy float64 STFT + Slaney filterbank
- *   decoder / encoder / e2e     : composition of the above; parity unpinned at
- *                                 the bit level against the real Rust binary
- *                                 (unbuildable here: no Rust toolchain).
+ *   decoder / encoder / prompt  : an independent float64 restatement of the
+ *                                 compositions (tests/ref64.py) with planted
+ *                                 mistakes that fail it; the prompt ids around
+ *                                 the audio rows likewise
+ *   segmentation                : float64 brute force and known answers
+ *   stream                      : tail-repeat KATs; one finalizing chunk equals
+ *                                 the offline driver (also with prompt ids);
+ *                                 the forced-language text-start rule alone
+ *                                 is unpinned (needs <asr_text> in the raw
+ *                                 tokens)
+ *   The Rust binary itself is unbuildable here (no Rust toolchain).
  */
 #ifndef QASR_ORACLE_H
 #define QASR_ORACLE_H
@@ -171,6 +179,23 @@ int64_t or_encoder_forward(or_encoder *e, const float *mel, int64_t frames, floa
 int64_t or_transcribe_forced(or_decoder *d, or_encoder *e, const float *samples,
                              int64_t n_samples, int32_t n_steps, int32_t *tokens,
                              float *margins, double *times_ms);
+/* The same with transcribe_segment's optional prompt ids (transcribe.rs:97-169):
+ * prompt between PREFIX_HEAD and PREFIX_TAIL, force (the language ids and
+ * <asr_text>) after SUFFIX_BASE, then past and <asr_text> when n_past > 0. */
+int64_t or_transcribe_prompt(or_decoder *d, or_encoder *e, const float *samples, int64_t n_samples,
+                             const int32_t *prompt, int64_t n_prompt, const int32_t *force, int64_t n_force,
+                             const int32_t *past, int64_t n_past, int32_t n_steps, int32_t *tokens,
+                             float *margins, double *times_ms);
+/* the id rows of that layout: head [9 + n_prompt] before the audio rows,
+ * tail [6 + n_force + n_past + (n_past > 0)] after them; returns their sum */
+int64_t or_prompt_ids(const int32_t *prompt, int64_t n_prompt, const int32_t *force, int64_t n_force,
+                      const int32_t *past, int64_t n_past, int32_t *head, int64_t *n_head, int32_t *tail,
+                      int64_t *n_tail);
+/* find_split_point (transcribe.rs:252-277) and transcribe_audio's split list
+ * (transcribe.rs:323-341; returns the count, writes min(count, cap)) */
+int64_t or_find_split_point(const float *x, int64_t n, int64_t target, float search_sec);
+int64_t or_segment_splits(const float *x, int64_t n, float segment_sec, float search_sec, int64_t *splits,
+                          int64_t cap);
 
 /* Threads used by the oracle's OpenMP loops; results do not depend on it. */
 /* streaming (stream_push_audio, transcribe.rs:902-1304), oracle_stream.c */
@@ -185,6 +210,10 @@ or_stream *or_stream_create(or_decoder *d, or_encoder *e, const or_stream_config
 void or_stream_destroy(or_stream *s);
 int64_t or_stream_push(or_stream *s, const float *samples, int64_t n, int finalize, int32_t *out, int64_t cap);
 int64_t or_stream_tokens(const or_stream *s, int32_t *out, int64_t cap);
+/* QwenCtx::prompt_tokens / force_prompt_tokens for the following chunks
+ * (transcribe.rs:1037-1089); n = 0 clears */
+void or_stream_set_prompt(or_stream *s, const int32_t *prompt, int64_t n_prompt, const int32_t *force,
+                          int64_t n_force);
 void or_stream_stats(const or_stream *s, int64_t *stats);
 int64_t or_tail_repeat_blocks(const int32_t *t, int64_t n, int64_t max_period, int64_t *period);
 

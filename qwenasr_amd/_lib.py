@@ -65,6 +65,10 @@ class EncWeights(C.Structure):
                                      "proj1_b", "proj2_b")])
 
 
+class Prompt(C.Structure):
+    _fields_ = [("prompt", P), ("n_prompt", I64), ("force", P), ("n_force", I64)]
+
+
 class StreamConfig(C.Structure):
     _fields_ = [("chunk_sec", C.c_float), ("rollback", C.c_int32), ("unfixed_chunks", C.c_int32),
                 ("max_new_tokens", C.c_int32), ("past_text_conditioning", C.c_int32),
@@ -140,6 +144,15 @@ _SIGS = {
     "qasr_hip_transcribe_forced": (C.c_int, [P, P, P, I64, I32, P, P]),
     "qasr_hip_transcribe": (C.c_int, [P, P, P, I64, I32, P, C.POINTER(I64), P]),
     "qasr_hip_text_tokens": (I64, [P, I64, P]),
+    "qasr_hip_transcribe_prompt": (C.c_int, [P, P, P, I64, C.POINTER(Prompt), P, I64, I32, P, C.POINTER(I64), P]),
+    "qasr_hip_text_tokens_from": (I64, [P, I64, C.c_int, P]),
+    "qasr_hip_segment_splits": (I64, [P, I64, C.c_float, C.c_float, P, I64]),
+    "qasr_hip_engine_last_segments": (C.c_int, [P, P, I64, C.POINTER(I64)]),
+    "qasr_hip_engine_set_segment_sec": (None, [P, C.c_float]),
+    "qasr_hip_engine_set_search_sec": (None, [P, C.c_float]),
+    "qasr_hip_engine_set_language_tokens": (C.c_int, [P, P, I64]),
+    "qasr_hip_engine_set_prompt_tokens": (C.c_int, [P, P, I64]),
+    "qasr_hip_stream_set_prompt": (C.c_int, [P, C.POINTER(Prompt)]),
     "qasr_hip_engine_detect": (C.c_int, [P, C.POINTER(DecConfig), C.POINTER(EncConfig)]),
     "qasr_hip_engine_load": (C.c_int, [C.c_char_p, C.c_int, I64, C.POINTER(P)]),
     "qasr_hip_engine_free": (None, [P]),

@@ -434,16 +434,41 @@ extern "C" int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64
 // ---------------------------------------------------------------------------
 // offline transcription with a forced number of decode steps
 // ---------------------------------------------------------------------------
-static const int PREFIX_HEAD[] = {151644, 8948, 198};
-static const int PREFIX_TAIL[] = {151645, 198, 151644, 872, 198, 151669};
-static const int SUFFIX_BASE[] = {151670, 151645, 198, 151644, 77091, 198};
+static const int32_t PREFIX_HEAD[] = {151644, 8948, 198};
+static const int32_t PREFIX_TAIL[] = {151645, 198, 151644, 872, 198, 151669};
+static const int32_t SUFFIX_BASE[] = {151670, 151645, 198, 151644, 77091, 198};
+static const int32_t TOKEN_ASR_TEXT = 151704;
+
+// The id rows of transcribe_segment's prompt (transcribe.rs:97-169): before
+// the audio rows PREFIX_HEAD | prompt | PREFIX_TAIL, after them SUFFIX_BASE |
+// force | past | <asr_text> (the last two only with past ids).  The ids are
+// gathered from the embedding table on the device, so each must index it.
+int prompt_id_rows(const qasr_prompt *p, const int32_t *past, int64_t n_past, int32_t vocab,
+                   std::vector<int32_t> &head, std::vector<int32_t> &tail) {
+    const int64_t np = p ? p->n_prompt : 0, nf = p ? p->n_force : 0;
+    if (np < 0 || nf < 0 || n_past < 0 || (np > 0 && !p->prompt) || (nf > 0 && !p->force) || (n_past > 0 && !past))
+        return qasr_fail(QASR_ERR_INVALID, "prompt ids: null ids with a nonzero count");
+    head.assign(PREFIX_HEAD, PREFIX_HEAD + 3);
+    if (np > 0) head.insert(head.end(), p->prompt, p->prompt + np);
+    head.insert(head.end(), PREFIX_TAIL, PREFIX_TAIL + 6);
+    tail.assign(SUFFIX_BASE, SUFFIX_BASE + 6);
+    if (nf > 0) tail.insert(tail.end(), p->force, p->force + nf);
+    if (n_past > 0) {
+        tail.insert(tail.end(), past, past + n_past);
+        tail.push_back(TOKEN_ASR_TEXT);
+    }
+    for (const auto *v : {&head, &tail})
+        for (int32_t t : *v)
+            if (t < 0 || t >= vocab) return qasr_fail(QASR_ERR_INVALID, "prompt ids: token id outside the vocabulary");
+    return QASR_OK;
+}
 
 // mel -> encoder -> prompt rows -> prefill of all but the last row -> the
 // first forward from the last row (transcribe.rs:71-183), queued on the
 // handle's stream; events ev[0..3] mark mel, encoder, prefill + first token.
 // Returns the prompt length in *total.
 static int transcribe_begin(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n, int64_t steps_max,
-                            int64_t *total_out) {
+                            const qasr_prompt *prompt, const int32_t *past, int64_t n_past, int64_t *total_out) {
     if (!d || !e) return qasr_fail(QASR_ERR_INVALID, "transcribe: null model");
     CHECK_H(d->h);
     if (d->h != e->h) return qasr_fail(QASR_ERR_INVALID, "transcribe: models on different handles");
@@ -454,21 +479,19 @@ static int transcribe_begin(qasr_decoder *d, qasr_encoder *e, const float *sampl
     if (nf <= 0) return qasr_fail(QASR_ERR_INVALID, "transcribe: audio too short");
     const int64_t T = encoder_tokens(e, nf);
     const int H = d->c.hidden;
-    const int n_head = 9, n_tail = 6;
+    std::vector<int32_t> head, tail;
+    TRY(prompt_id_rows(prompt, past, n_past, d->c.vocab, head, tail));
+    const int n_head = (int)head.size(), n_tail = (int)tail.size();
     const int64_t total = n_head + T + n_tail;
     if (total - 1 + steps_max > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "transcribe: KV cache capacity exceeded");
-    int toks[15];
-    for (int i = 0; i < 3; i++) toks[i] = PREFIX_HEAD[i];
-    for (int i = 0; i < 6; i++) toks[3 + i] = PREFIX_TAIL[i];
-    for (int i = 0; i < 6; i++) toks[9 + i] = SUFFIX_BASE[i];
-    for (int t : toks)   // every prompt id is gathered from the embedding table on the device
-        if (t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "transcribe: vocab too small for the prompt");
+    std::vector<int32_t> toks(head);
+    toks.insert(toks.end(), tail.begin(), tail.end());
     TRY(dbuf_ensure(e->audio, sizeof(float) * n));
     TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf));
     TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf)));
     TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * H));
     TRY(dbuf_ensure(e->embeds, sizeof(float) * total * H));
-    TRY(dbuf_ensure(e->toks, sizeof(toks)));
+    TRY(dbuf_ensure(e->toks, sizeof(int32_t) * toks.size()));
     for (hipEvent_t &v : e->ev)
         if (!v) HIPCHK(hipEventCreate(&v));
     float *dx = e->audio.as<float>(), *dmel = e->mel.as<float>(), *msc = e->melsc.as<float>();
@@ -476,7 +499,7 @@ static int transcribe_begin(qasr_decoder *d, qasr_encoder *e, const float *sampl
     int *dtok = e->toks.as<int>();
     hipEvent_t *ev = e->ev;
     HIPCHK(hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, st));
-    HIPCHK(hipMemcpyAsync(dtok, toks, sizeof(toks), hipMemcpyHostToDevice, st));
+    HIPCHK(hipMemcpyAsync(dtok, toks.data(), sizeof(int32_t) * toks.size(), hipMemcpyHostToDevice, st));
     HIPCHK(hipEventRecord(ev[0], st));
     TRY(mel_dev(e, dx, n, dmel, msc));
     HIPCHK(hipEventRecord(ev[1], st));
@@ -511,7 +534,7 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
     if (n_steps <= 0 || !tokens_out) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
     int64_t total = 0;
     auto body = [&]() -> int {
-        TRY(transcribe_begin(d, e, samples, n, n_steps, &total));
+        TRY(transcribe_begin(d, e, samples, n, n_steps, nullptr, nullptr, 0, &total));
         hipStream_t st = d->h->stream;
         for (int32_t s = 1; s < n_steps; s++) TRY(decoder_run_embed_step(d));
         HIPCHK(hipEventRecord(e->ev[4], st));
@@ -533,14 +556,15 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
 // those positions are discarded by setting the KV length back).
 static const int TOKEN_ENDOFTEXT = 151643, TOKEN_IM_END = 151645;
 
-extern "C" int qasr_hip_transcribe(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
-                                   int32_t max_tokens, int32_t *tokens_out, int64_t *n_out, double *times_ms) {
+extern "C" int qasr_hip_transcribe_prompt(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
+                                          const qasr_prompt *prompt, const int32_t *past, int64_t n_past,
+                                          int32_t max_tokens, int32_t *tokens_out, int64_t *n_out, double *times_ms) {
     if (max_tokens <= 0 || !tokens_out || !n_out) return qasr_fail(QASR_ERR_INVALID, "transcribe: bad arguments");
     *n_out = 0;
     int64_t total = 0;
     constexpr int BURST = 8;
     auto body = [&]() -> int {
-        TRY(transcribe_begin(d, e, samples, n, max_tokens, &total));
+        TRY(transcribe_begin(d, e, samples, n, max_tokens, prompt, past, n_past, &total));
         hipStream_t st = d->h->stream;
         int64_t done = 1, stop_at = -1;            // forwards queued; index of the stop token
         std::vector<int32_t> log;
@@ -576,20 +600,31 @@ extern "C" int qasr_hip_transcribe(qasr_decoder *d, qasr_encoder *e, const float
     return rc;
 }
 
+extern "C" int qasr_hip_transcribe(qasr_decoder *d, qasr_encoder *e, const float *samples, int64_t n,
+                                   int32_t max_tokens, int32_t *tokens_out, int64_t *n_out, double *times_ms) {
+    return qasr_hip_transcribe_prompt(d, e, samples, n, nullptr, nullptr, 0, max_tokens, tokens_out, n_out, times_ms);
+}
+
 // The ids transcribe_segment turns into text (transcribe.rs:196-214): the
-// tokens after the first <asr_text> (151704) and before a stop token.
-extern "C" int64_t qasr_hip_text_tokens(const int32_t *raw, int64_t n, int32_t *out) {
+// tokens after the first <asr_text> (151704) and before a stop token; with
+// text_open (forced-language or past-text ids in the prompt, transcribe.rs:
+// 196) every token before the stop except <asr_text> itself.
+extern "C" int64_t qasr_hip_text_tokens_from(const int32_t *raw, int64_t n, int text_open, int32_t *out) {
     if (!raw || n < 0) return -1;
     int64_t k = 0;
-    bool past = false;
+    bool past = text_open != 0;
     for (int64_t i = 0; i < n; i++) {
         const int32_t t = raw[i];
         if (t == TOKEN_ENDOFTEXT || t == TOKEN_IM_END) break;
-        if (t == 151704) past = true;
+        if (t == TOKEN_ASR_TEXT) past = true;
         else if (past) {
             if (out) out[k] = t;
             k++;
         }
     }
     return k;
+}
+
+extern "C" int64_t qasr_hip_text_tokens(const int32_t *raw, int64_t n, int32_t *out) {
+    return qasr_hip_text_tokens_from(raw, n, 0, out);
 }

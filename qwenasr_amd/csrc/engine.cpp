@@ -7,6 +7,8 @@
 #include "model.h"
 
 #include <algorithm>
+#include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -20,7 +22,12 @@ struct qasr_engine {
     qasr_enc_config ec{};
     qasr_stream_config scfg{};      // QwenCtx's stream_* fields (context.rs:146-150)
     int32_t max_tokens = 2048;      // transcribe_segment's max_tokens (transcribe.rs:188)
-    std::vector<int32_t> raw;       // the last transcription's tokens
+    float segment_sec = 0.0f;       // QwenCtx::segment_sec / search_sec (context.rs:144-145)
+    float search_sec = 3.0f;
+    std::vector<int32_t> prompt;    // QwenCtx::prompt_tokens
+    std::vector<int32_t> force;     // QwenCtx::force_prompt_tokens ("language X" ids + <asr_text>)
+    std::vector<int32_t> raw;       // the last transcription's tokens, segment after segment
+    std::vector<int64_t> segments;  // the last transcription's segments, 4 values each
     std::vector<qasr_engine_stream *> streams;   // live stream states, detached at engine_free
     // the last caller that wrote the decoder's KV cache (the engine itself for
     // transcribe_pcm, else a stream): a stream whose previous rows were
@@ -150,25 +157,161 @@ extern "C" int qasr_hip_engine_config(const qasr_engine *g, qasr_dec_config *dc,
     return QASR_OK;
 }
 
-// qwen_asr_transcribe_pcm (c_api.rs:75-95) without segmentation (segment_sec
-// 0, the default): transcribe_segment's greedy decode to a stop token or
-// 2048 tokens, then the text tokens (after <asr_text>, before the stop) into
-// tokens_out (capacity cap); *n_out = their count (may exceed cap: then only
-// cap were written).
+// Rust's `f32 as usize`: truncation toward zero, negative and NaN to 0
+static int64_t f32_to_count(float v) {
+    if (!(v > 0.0f)) return 0;
+    if (v >= 9.2e18f) return INT64_MAX;
+    return (int64_t)v;
+}
+
+// find_split_point (transcribe.rs:252-277): the center of the 1600-sample
+// window (hop 800) of least mean square inside target +- search_sec, the first
+// of equal minima; target when no window fits.  The energy is a sequential f32
+// sum of squares (built without contraction), as the reference adds it.
+static int64_t find_split_point(const float *x, int64_t n, int64_t target, float search_sec) {
+    const int64_t half = f32_to_count(search_sec * 16000.0f);
+    const int64_t lo = std::max<int64_t>(target - half, 0), hi = std::min(target + half, n);
+    constexpr int64_t WIN = 1600;
+    float best = 1e30f;
+    int64_t center = target;
+    for (int64_t pos = lo; pos + WIN <= hi; pos += WIN / 2) {
+        const int64_t end = std::min(pos + WIN, n);
+        float energy = 0.0f;
+        for (int64_t i = pos; i < end; i++) energy += x[i] * x[i];
+        energy /= (float)(end - pos);
+        if (energy < best) {
+            best = energy;
+            center = pos + (end - pos) / 2;
+        }
+    }
+    return center;
+}
+
+// transcribe_audio's split list (transcribe.rs:323-341)
+extern "C" int64_t qasr_hip_segment_splits(const float *samples, int64_t n, float segment_sec, float search_sec,
+                                           int64_t *splits_out, int64_t cap) {
+    if (n < 0 || (n > 0 && !samples) || cap < 0 || (cap > 0 && !splits_out)) return -1;
+    const int64_t target = f32_to_count(segment_sec * 16000.0f);
+    const float half_seg = segment_sec / 2.0f;
+    // f32::min: a NaN operand yields the other one
+    const float search = std::isnan(half_seg) ? search_sec : (search_sec < half_seg ? search_sec : half_seg);
+    const int64_t margin = f32_to_count(search * 16000.0f);
+    int64_t k = 0;
+    auto put = [&](int64_t v) {
+        if (k < cap) splits_out[k] = v;
+        k++;
+    };
+    put(0);
+    if (segment_sec <= 0.0f || n <= target + margin) return k;
+    for (int64_t pos = 0; pos + target + margin < n;) {
+        pos = find_split_point(samples, n, pos + target, search);
+        put(pos);
+        if (k >= 127) break;
+    }
+    return k;
+}
+
+// qwen_asr_transcribe_pcm (c_api.rs:75-95) -> transcribe_audio
+// (transcribe.rs:297-403): the audio in one segment, or cut at
+// qasr_hip_segment_splits when segment_sec > 0; each segment (a cut one
+// zero-padded to 0.5 s at least) runs transcribe_segment's greedy decode to a stop token or
+// 2048 tokens with the engine's prompt and language ids, and its text ids
+// (after <asr_text>, or all of them with a forced language) follow the
+// previous segments' in tokens_out (capacity cap); *n_out = their count (may
+// exceed cap: then only cap were written).  Past-text conditioning (off by
+// default, with no C-API setter) re-encodes the joined text with the
+// tokenizer and is not offered at token level.
 extern "C" int qasr_hip_engine_transcribe_pcm(qasr_engine *g, const float *samples, int64_t n_samples,
                                           int32_t *tokens_out, int64_t cap, int64_t *n_out) {
     if (!g || !samples || n_samples <= 0 || !n_out || cap < 0 || (cap > 0 && !tokens_out))
         return qasr_fail(QASR_ERR_INVALID, "engine_transcribe_pcm: bad arguments");
-    g->raw.resize((size_t)g->max_tokens);
-    int64_t n_raw = 0;
+    *n_out = 0;
+    g->raw.clear();
+    g->segments.clear();
+    std::vector<int64_t> splits(128);
+    const int64_t n_seg = qasr_hip_segment_splits(samples, n_samples, g->segment_sec, g->search_sec, splits.data(),
+                                                  (int64_t)splits.size());
+    if (n_seg < 1) return qasr_fail(QASR_ERR_INVALID, "engine_transcribe_pcm: segmentation failed");
+    const qasr_prompt ids{g->prompt.data(), (int64_t)g->prompt.size(), g->force.data(), (int64_t)g->force.size()};
+    constexpr int64_t MIN_SAMPLES = 16000 / 2;
+    std::vector<int32_t> seg_raw((size_t)g->max_tokens), text;
+    std::vector<float> padded;
     g->kv_owner = g;
-    int rc = qasr_hip_transcribe(g->d, g->e, samples, n_samples, g->max_tokens, g->raw.data(), &n_raw, nullptr);
-    g->raw.resize(rc == QASR_OK ? (size_t)n_raw : 0);
-    if (rc != QASR_OK) return rc;
-    std::vector<int32_t> text((size_t)n_raw);
-    const int64_t k = qasr_hip_text_tokens(g->raw.data(), n_raw, text.data());
+    for (int64_t k = 0; k < n_seg; k++) {
+        const int64_t a = splits[(size_t)k], b = k + 1 < n_seg ? splits[(size_t)k + 1] : n_samples;
+        const float *x = samples + a;
+        int64_t len = b - a;
+        if (n_seg > 1 && len < MIN_SAMPLES) {   // only cut segments are padded (transcribe.rs:355-366)
+            padded.assign((size_t)MIN_SAMPLES, 0.0f);
+            if (len > 0) std::memcpy(padded.data(), x, sizeof(float) * (size_t)len);
+            x = padded.data();
+            len = MIN_SAMPLES;
+        }
+        int64_t n_raw = 0;
+        const int rc = qasr_hip_transcribe_prompt(g->d, g->e, x, len, &ids, nullptr, 0, g->max_tokens,
+                                                  seg_raw.data(), &n_raw, nullptr);
+        if (rc != QASR_OK) {
+            g->raw.clear();
+            g->segments.clear();
+            return rc;
+        }
+        g->raw.insert(g->raw.end(), seg_raw.begin(), seg_raw.begin() + n_raw);
+        const size_t t0 = text.size();
+        text.resize(t0 + (size_t)n_raw);
+        const int64_t m = qasr_hip_text_tokens_from(seg_raw.data(), n_raw, g->force.empty() ? 0 : 1, text.data() + t0);
+        text.resize(t0 + (size_t)m);
+        g->segments.insert(g->segments.end(), {a, b, (int64_t)t0, m});
+    }
+    const int64_t k = (int64_t)text.size();
     if (k > 0 && cap > 0) std::memcpy(tokens_out, text.data(), sizeof(int32_t) * (size_t)std::min(k, cap));
     *n_out = k;
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_engine_last_segments(const qasr_engine *g, int64_t *bounds, int64_t cap, int64_t *n) {
+    if (!g || !n || cap < 0 || (cap > 0 && !bounds)) return qasr_fail(QASR_ERR_INVALID, "engine: bad arguments");
+    *n = (int64_t)g->segments.size() / 4;
+    if (*n > 0 && cap > 0)
+        std::memcpy(bounds, g->segments.data(), sizeof(int64_t) * 4 * (size_t)std::min<int64_t>(*n, cap));
+    return QASR_OK;
+}
+
+// qwen_asr_set_segment_sec (c_api.rs:123-129); QwenCtx::search_sec
+extern "C" void qasr_hip_engine_set_segment_sec(qasr_engine *g, float sec) {
+    if (g) g->segment_sec = sec;
+}
+extern "C" void qasr_hip_engine_set_search_sec(qasr_engine *g, float sec) {
+    if (g) g->search_sec = sec;
+}
+
+// an id list for the engine's prompt: checked against the vocabulary, then copied
+static int engine_ids(const qasr_engine *g, const int32_t *ids, int64_t n, std::vector<int32_t> &out) {
+    if (!g || n < 0 || (n > 0 && !ids)) return qasr_fail(QASR_ERR_INVALID, "engine: bad id list");
+    for (int64_t i = 0; i < n; i++)
+        if (ids[i] < 0 || ids[i] >= g->dc.vocab) return qasr_fail(QASR_ERR_INVALID, "engine: id outside the vocabulary");
+    out.assign(ids, ids + n);
+    return QASR_OK;
+}
+
+// qwen_asr_set_language (c_api.rs:131-148) with the language already encoded;
+// <asr_text> closes the forced ids as in prepare_prompt_tokens
+// (context.rs:215-221); no ids: automatic language
+extern "C" int qasr_hip_engine_set_language_tokens(qasr_engine *g, const int32_t *ids, int64_t n) {
+    std::vector<int32_t> v;
+    if (int rc = engine_ids(g, ids, n, v)) return rc;
+    if (n > 0) {
+        if (151704 >= g->dc.vocab) return qasr_fail(QASR_ERR_INVALID, "engine: vocab too small for <asr_text>");
+        v.push_back(151704);
+    }
+    g->force.swap(v);
+    return QASR_OK;
+}
+
+// QwenCtx::set_prompt (context.rs:165-175) with the prompt already encoded
+extern "C" int qasr_hip_engine_set_prompt_tokens(qasr_engine *g, const int32_t *ids, int64_t n) {
+    std::vector<int32_t> v;
+    if (int rc = engine_ids(g, ids, n, v)) return rc;
+    g->prompt.swap(v);
     return QASR_OK;
 }
 
@@ -239,8 +382,12 @@ extern "C" int qasr_hip_engine_stream_push(qasr_engine_stream *s, const float *s
     if (s->audio.empty()) return QASR_OK;
     if (s->eng->kv_owner != s) stream_drop_prefix(s->s);
     s->eng->kv_owner = s;
-    // the reference reads the stream settings from its context on every push
+    // the reference reads the stream settings and the prepared prompt ids
+    // from its context on every push
     stream_set_config(s->s, s->eng->scfg);
+    const qasr_engine *g = s->eng;
+    const qasr_prompt ids{g->prompt.data(), (int64_t)g->prompt.size(), g->force.data(), (int64_t)g->force.size()};
+    if (int rc = qasr_hip_stream_set_prompt(s->s, &ids)) return rc;
     return qasr_hip_stream_push(s->s, s->audio.data(), (int64_t)s->audio.size(), finalize, tokens_out, cap, n_out);
 }
 

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <algorithm>
 #include <string>
+#include <vector>
 #include "qasr_hip.h"
 
 // scratch area of a handle: argmax partials, attention partials
@@ -43,6 +44,11 @@ void dbuf_release(DevBuf &b);
 void stream_drop_prefix(qasr_stream *s);
 // Replaces the stream's settings (already validated by the caller).
 void stream_set_config(qasr_stream *s, const qasr_stream_config &c);
+
+// The id rows of transcribe_segment's prompt around the audio rows
+// (transcribe.rs:97-169), each checked to lie in [0, vocab).
+int prompt_id_rows(const qasr_prompt *p, const int32_t *past, int64_t n_past, int32_t vocab,
+                   std::vector<int32_t> &head, std::vector<int32_t> &tail);
 
 // Multi-stream batch internals used by the streaming driver: chunk prefills
 // from device rows into stream KV slots at positions [start, start + n) (one

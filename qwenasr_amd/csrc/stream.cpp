@@ -36,10 +36,8 @@ using namespace qasr;
 
 namespace {
 constexpr int32_t TOKEN_ASR_TEXT = 151704;
-// PREFIX_HEAD | PREFIX_TAIL and SUFFIX_BASE (transcribe.rs:13-15); no prompt or
-// language tokens (those come from the tokenizer)
-constexpr int32_t PREFIX[9] = {151644, 8948, 198, 151645, 198, 151644, 872, 198, 151669};
-constexpr int32_t SUFFIX[6] = {151670, 151645, 198, 151644, 77091, 198};
+// the last id of SUFFIX_BASE (transcribe.rs:15), the input of idle batch slots
+constexpr int32_t SUFFIX_LAST = 198;
 constexpr int DEGEN_MAX_PERIOD = 6, DEGEN_MIN_REPEATS = 4, STALE_CHUNKS = 4;
 constexpr int RESET_INTERVAL_CHUNKS = 45, RESET_CARRY_TOKENS = 24, MAX_ENC_WINDOWS = 4;
 constexpr int64_t SAMPLE_RATE = 16000, HOP = 160, WINDOW_FRAMES = 800;
@@ -82,6 +80,7 @@ struct qasr_stream {
     int64_t partial_seq = 0, last_partial_cursor = 0;
     // tokens
     std::vector<int32_t> raw, stable, prev_tail;
+    std::vector<int32_t> prompt, force;   // QwenCtx::prompt_tokens / force_prompt_tokens
     // prefill reuse
     DevBuf embeds, prev_embeds;
     int64_t prev_prefill_len = 0;
@@ -115,11 +114,10 @@ extern "C" int qasr_hip_stream_create(qasr_decoder *d, qasr_encoder *e, const qa
     if (encoder_output_dim(e) != d->c.hidden)
         return qasr_fail(QASR_ERR_INVALID, "stream_create: encoder output_dim != decoder hidden");
     // every prompt id is gathered from the embedding table on the device
-    int32_t top = 0;
-    for (int32_t t : PREFIX) top = std::max(top, t);
-    for (int32_t t : SUFFIX) top = std::max(top, t);
-    if (cfg && cfg->past_text_conditioning) top = std::max(top, TOKEN_ASR_TEXT);
-    if (top >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream_create: vocab too small for the prompt");
+    std::vector<int32_t> head, tail;
+    if (prompt_id_rows(nullptr, nullptr, 0, d->c.vocab, head, tail) != QASR_OK ||
+        (cfg && cfg->past_text_conditioning && TOKEN_ASR_TEXT >= d->c.vocab))
+        return qasr_fail(QASR_ERR_INVALID, "stream_create: vocab too small for the prompt");
     qasr_stream *s = new qasr_stream();
     s->d = d;
     s->e = e;
@@ -202,10 +200,22 @@ static bool is_stop(const qasr_stream *s, int32_t t) {
     return t == s->cfg.stop_tokens[0] || t == s->cfg.stop_tokens[1];
 }
 
-// index just past TOKEN_ASR_TEXT in raw (0 when absent): the text region
-static size_t text_start(const std::vector<int32_t> &raw) {
+// the text region of raw (transcribe.rs:1166-1172, 1257-1263): just past the
+// first TOKEN_ASR_TEXT (0 when absent), or all of raw when the language is
+// forced (the forced ids end with <asr_text> themselves)
+static size_t text_start(const qasr_stream *s, const std::vector<int32_t> &raw) {
+    if (!s->force.empty()) return 0;
     const auto it = std::find(raw.begin(), raw.end(), TOKEN_ASR_TEXT);
     return it == raw.end() ? 0 : (size_t)(it - raw.begin()) + 1;
+}
+
+extern "C" int qasr_hip_stream_set_prompt(qasr_stream *s, const qasr_prompt *p) {
+    if (!s) return qasr_fail(QASR_ERR_INVALID, "stream is null");
+    std::vector<int32_t> head, tail;
+    if (int rc = prompt_id_rows(p, nullptr, 0, s->d->c.vocab, head, tail)) return rc;
+    s->prompt.assign(head.begin() + 3, head.end() - 6);
+    s->force.assign(tail.begin() + 6, tail.end());
+    return QASR_OK;
 }
 
 static void carry_reset(qasr_stream *s) {
@@ -344,7 +354,8 @@ static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool f
         (s->cfg.past_text_conditioning && s->chunk_idx >= s->cfg.unfixed_chunks && !s->raw.empty())
             ? (int64_t)std::max<int64_t>((int64_t)s->raw.size() - rollback, 0)
             : 0;
-    const int64_t total_seq = 9 + enc_len + 6 + pl.n_prefix_tokens;
+    const int64_t n_head = 9 + (int64_t)s->prompt.size(), n_suffix = 6 + (int64_t)s->force.size();
+    const int64_t total_seq = n_head + enc_len + n_suffix + pl.n_prefix_tokens;
     pl.prefill_len = total_seq - 1;
     const int64_t cap = tgt.b ? batch_max_seq(tgt.b) : d->max_seq;
     if (pl.prefill_len + s->cfg.max_new_tokens + DECODE_BURST > cap)
@@ -359,8 +370,11 @@ static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool f
     if (partial_seq > 0)
         HIPCHK(hipMemcpyAsync(s->enc_all.as<float>() + off * H, s->partial.p, sizeof(float) * partial_seq * H,
                               hipMemcpyDeviceToDevice, st));
-    std::vector<int32_t> toks(PREFIX, PREFIX + 9);
-    toks.insert(toks.end(), SUFFIX, SUFFIX + 6);
+    // PREFIX_HEAD | prompt | PREFIX_TAIL, then SUFFIX_BASE | force | rolled-back text
+    qasr_prompt ids{s->prompt.data(), (int64_t)s->prompt.size(), s->force.data(), (int64_t)s->force.size()};
+    std::vector<int32_t> toks, tail;
+    TRY(prompt_id_rows(&ids, nullptr, 0, d->c.vocab, toks, tail));
+    toks.insert(toks.end(), tail.begin(), tail.end());
     toks.insert(toks.end(), s->raw.begin(), s->raw.begin() + pl.n_prefix_tokens);
     for (int32_t t : toks)
         if (t < 0 || t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream: token id out of range");
@@ -368,8 +382,8 @@ static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool f
     TRY(dbuf_ensure(s->toks, sizeof(int32_t) * toks.size()));
     HIPCHK(hipMemcpyAsync(s->toks.p, toks.data(), sizeof(int32_t) * toks.size(), hipMemcpyHostToDevice, st));
     TRY(dbuf_ensure(s->embeds, sizeof(float) * total_seq * H));
-    LAUNCHCHK(launch_build_prompt(s->embeds.as<float>(), d->embed, s->toks.as<int>(), 9, s->enc_all.as<float>(),
-                                  (int)enc_len, (int)(6 + pl.n_prefix_tokens), (int)H, st),
+    LAUNCHCHK(launch_build_prompt(s->embeds.as<float>(), d->embed, s->toks.as<int>(), (int)n_head,
+                                  s->enc_all.as<float>(), (int)enc_len, (int)(n_suffix + pl.n_prefix_tokens), (int)H, st),
               "stream prompt");
 
     // ---- prefill with common-prefix reuse ----
@@ -416,7 +430,7 @@ static void chunk_commit(qasr_stream *s, const ChunkPlan &pl, const std::vector<
     // ---- speech end: commit everything that was held back ----
     const bool speech_ended = chunk.empty() && !s->raw.empty() && s->chunk_idx >= s->cfg.unfixed_chunks;
     if (speech_ended) {
-        const size_t ts = text_start(s->raw);
+        const size_t ts = text_start(s, s->raw);
         for (size_t i = s->stable.size(); i + ts < s->raw.size(); i++) {
             s->stable.push_back(s->raw[ts + i]);
             emitted.push_back(s->raw[ts + i]);
@@ -437,7 +451,7 @@ static void chunk_commit(qasr_stream *s, const ChunkPlan &pl, const std::vector<
         if (s->stale >= STALE_CHUNKS || reps >= DEGEN_MIN_REPEATS) carry_reset(s);
         if (s->chunk_idx > 0 && s->chunk_idx % RESET_INTERVAL_CHUNKS == 0) carry_reset(s);
         // ---- emit the tokens that are now stable ----
-        const size_t ts = text_start(s->raw);
+        const size_t ts = text_start(s, s->raw);
         const int64_t n_text = (int64_t)s->raw.size() - (int64_t)std::min(ts, s->raw.size());
         int64_t cand = 0;
         if (pl.is_final) cand = n_text;
@@ -549,7 +563,7 @@ extern "C" qasr_stream *qasr_hip_stream_batch_stream(qasr_stream_batch *g, int32
 static int group_decode(qasr_stream_batch *g, const std::vector<int> &act, const std::vector<ChunkPlan> &pl,
                         std::vector<std::vector<int32_t>> &chunks) {
     const int B = (int)g->s.size();
-    std::vector<int32_t> first(B, SUFFIX[5]), out((size_t)B * DECODE_BURST);
+    std::vector<int32_t> first(B, SUFFIX_LAST), out((size_t)B * DECODE_BURST);
     std::vector<char> busy(B, 0), done(B, 1);
     for (int i : act) {
         busy[i] = 1;

