@@ -35,9 +35,8 @@
  *   segmentation                : float64 brute force and known answers
  *   stream                      : tail-repeat KATs; one finalizing chunk equals
  *                                 the offline driver (also with prompt ids);
- *                                 the forced-language text-start rule alone
- *                                 is unpinned (needs <asr_text> in the raw
- *                                 tokens)
+ *                                 the text-start rules on a planted model that
+ *                                 emits <asr_text> at every step
  *   The Rust binary itself is unbuildable here (no Rust toolchain).
  */
 #ifndef QASR_ORACLE_H

@@ -43,3 +43,24 @@ def bf16(a):
 
 def bf16f(a):
     return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+ASR_TEXT = 151704
+# a 2-layer decoder small enough for the oracle (the GPU kernels' head_dim
+# 128, the full vocabulary) and a 2-layer encoder of the 0.6B width
+TINY_DEC = dict(n_layers=2, hidden=128, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=256, vocab=151936,
+                eps=1e-6, theta=1e6)
+TINY_ENC = dict(d_model=896, n_layers=2, n_heads=14, head_dim=64, ffn_dim=3584, output_dim=128, chunk_size=100,
+                n_window_infer=800, conv_hidden=480)
+
+
+def plant_asr_text(w, base=10.0, top=20.0):
+    """Makes a SynthDecoder emit <asr_text> (151704) at every step: element 0
+    of every embedding row is `base` and of row 151704 `top`.  The residual of
+    every decode position (its input is a token embedding) is then dominated by
+    dimension 0, the quantized final activation is (127, ~0, ...), every row of
+    the tied int8 head has its absmax in element 0, and the head's logits
+    follow that element: 151704's is twice any other's."""
+    w.embed[:, 0] = bf16([base])[0]
+    w.embed[ASR_TEXT, 0] = bf16([top])[0]
+    return w

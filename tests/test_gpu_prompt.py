@@ -172,3 +172,40 @@ def test_stream_prompt_ids(dev, orc, tiny):
         s.close()
     finally:
         g.close()
+
+
+def test_stream_asr_text_model(dev, orc):
+    """A model that emits <asr_text> at every step (plant_asr_text): the raw
+    tokens then hold <asr_text> everywhere, so the text region's start (after
+    the first one, or 0 with a forced language) and the re-anchor that puts
+    one in front of the carried tokens decide what is committed.  Pushes of
+    2 s with past-text conditioning, with and without a forced language: the
+    GPU stream commits what the oracle's stream commits."""
+    from conftest import ASR_TEXT, TINY_DEC, TINY_ENC, plant_asr_text
+    from qwenasr_amd.model import Decoder, Encoder, Stream, transcribe
+    from qwenasr_amd.synth import SynthDecoder, SynthEncoder, audio
+    wd = plant_asr_text(SynthDecoder(TINY_DEC, seed=2401, std=0.05))
+    we = SynthEncoder(TINY_ENC, seed=2402)
+    x = audio(7 * 16000, 2404)
+    d, e = Decoder(dev, wd, max_seq=1024), Encoder(dev, we)
+    od, oe = orc.OracleDecoder(wd, max_seq=1024), orc.OracleEncoder(we)
+    try:
+        toks, _ = transcribe(d, e, x[:32000], max_tokens=4)
+        assert toks.tolist() == [ASR_TEXT] * 4
+        for ids in (dict(), dict(force=FORCE)):
+            cfg = dict(max_new_tokens=3, rollback=1, unfixed_chunks=1, past_text_conditioning=1)
+            gs, cs = Stream(d, e, **cfg), orc.OracleStream(od, oe, **cfg)
+            gs.set_prompt(**ids)
+            cs.set_prompt(**ids)
+            for end in (32000, 64000, 96000, x.size):
+                fin = end == x.size
+                print(f"force {bool(ids)}: push {end}", flush=True)
+                eg, ec = gs.push(x[:end], finalize=fin).tolist(), cs.push(x[:end], finalize=fin).tolist()
+                assert eg == ec, (ids, end, eg, ec)
+            assert gs.tokens().tolist() == cs.tokens().tolist()
+            print("committed", cs.tokens().tolist(), flush=True)
+            gs.close()
+            cs.close()
+    finally:
+        for o in (d, e, od, oe):
+            o.close()

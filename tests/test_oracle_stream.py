@@ -73,6 +73,41 @@ def test_single_chunk_with_prompt_ids_equals_offline(orc, tiny, ids):
     s.close()
 
 
+@pytest.fixture(scope="module")
+def asr_text_model(orc):
+    from conftest import TINY_DEC, TINY_ENC, plant_asr_text
+    from qwenasr_amd.synth import SynthDecoder, SynthEncoder, audio
+    wd = plant_asr_text(SynthDecoder(TINY_DEC, seed=2401, std=0.05))
+    we = SynthEncoder(TINY_ENC, seed=2402)
+    dec, enc = orc.OracleDecoder(wd, max_seq=512), orc.OracleEncoder(we)
+    yield dec, enc, audio(24000, 2403)
+    dec.close()
+    enc.close()
+
+
+def test_text_region_rules_with_asr_text_in_raw(orc, asr_text_model):
+    """A model that emits <asr_text> (A = 151704) at every step (the planted
+    embedding of plant_asr_text; the first check confirms it): one finalizing
+    chunk of 3 tokens commits raw[1:] = [A, A] without a forced language (the
+    text region starts after the first <asr_text>, transcribe.rs:1257-1263)
+    and all of raw = [A, A, A] with one (the region starts at 0); the offline
+    rule counts none of them (every <asr_text> only sets past_asr_text,
+    transcribe.rs:207-209)."""
+    from conftest import ASR_TEXT
+    from qwenasr_amd.model import text_tokens
+    dec, enc, x = asr_text_model
+    force = [11528, 6364, ASR_TEXT]
+    for ids, want in ((dict(), [ASR_TEXT] * 2), (dict(force=force), [ASR_TEXT] * 3)):
+        raw = orc.transcribe_forced(dec, enc, x, 3, **ids)["tokens"].tolist()
+        assert raw == [ASR_TEXT] * 3, raw
+        s = orc.OracleStream(dec, enc, max_new_tokens=3)
+        s.set_prompt(**ids)
+        got = s.push(x, finalize=True).tolist()
+        s.close()
+        assert got == want, (ids, got)
+        assert text_tokens(np.array(raw, np.int32), text_open=bool(ids)).tolist() == []
+
+
 def test_chunk_schedule(orc, tiny):
     """max_new_tokens 3 keeps the tail-repeat rule (>= 4 repeats) out of the
     way of a random-init model's repetitive tokens; rollback 1."""
