@@ -459,7 +459,7 @@ int prompt_id_rows(const qasr_prompt *p, const int32_t *past, int64_t n_past, in
     }
     for (const auto *v : {&head, &tail})
         for (int32_t t : *v)
-            if (t < 0 || t >= vocab) return qasr_fail(QASR_ERR_INVALID, "prompt ids: token id outside the vocabulary");
+            if (t < 0 || t >= vocab) return qasr_fail(QASR_ERR_INVALID, "prompt ids: vocab too small for the prompt (an id outside the vocabulary)");
     return QASR_OK;
 }
 

@@ -208,6 +208,14 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
 // bf16 terms when the fragment is read; int8 B is widened to bf16 (exact).
 // K-steps past the end load a zero page, so the wait count is the same in
 // every iteration.  Requires K % BK == 0 and 16-byte aligned rows.
+//
+// KP > 1 splits the K loop inside the block: 4 KP waves in KP groups of 4,
+// group p taking the K-steps p, p + KP, ... through a ring of its own; at the
+// end groups 1 .. KP - 1 leave their partial tiles in LDS and group 0 adds
+// them in group order and runs the epilogue.  At the M ~ 400 shapes of the
+// prefill and config 1 a 64 x 64 tile's K loop is a chain of K-steps that one
+// wave per SIMD walks alone (the grid holds 96-384 tiles for 256 CUs); KP
+// groups shorten the chain KP times and give each SIMD KP waves to overlap.
 // ---------------------------------------------------------------------------
 __device__ __attribute__((aligned(256))) int4 g_gemm_zero16[16];
 
@@ -263,8 +271,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, int m, int n, f
     *cp = v;
 }
 
-template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN, int KS>
-__global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
+template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN, int KS, int KP>
+__global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     constexpr bool AF = ASRC == A_F32_SPLIT;
     constexpr int AE = AF ? 4 : 2, BE = BSRC == B_BF16 ? 2 : 1;     // element bytes
     constexpr int BK = AF ? 32 : 64;                                 // A rows are 128 B, B rows 64 B per stage
@@ -277,9 +285,13 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     constexpr int WR = (AF ? BM / 4 : BM) / 16, WC = (AF ? BN : BN / 4) / 16;
     static_assert(BSRC == (AF ? B_BF16 : B_I8), "operand pair");
     static_assert(BM % 32 == 0 && BN % 64 == 0, "tile");
-    __shared__ __attribute__((aligned(16))) char smem[NS][STG];
+    static_assert(KP == 1 || KS == 1, "split K across blocks or inside them, not both");
+    static_assert((KP - 1) * 4 * WR * WC * 4 * 64 * 4 <= KP * NS * STG, "partials fit the rings");
+    __shared__ __attribute__((aligned(16))) char smem_all[KP][NS][STG];
     const int t = threadIdx.x, lane = t & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int grp = wave >> 2, wid = wave & 3;          // K group, wave within the group
+    auto &smem = smem_all[grp];
     const int mw = AF ? (BM / 4) * wid : 0, nw = AF ? 0 : (BN / 4) * wid;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int M = g.M, N = g.N, K = g.K;
@@ -289,6 +301,8 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     // main loop unchanged.
     const int nk_all = K / BK, kz = KS > 1 ? (int)blockIdx.z : 0;
     const int k0s = KS > 1 ? nk_all * kz / KS : 0, nk = KS > 1 ? nk_all * (kz + 1) / KS - k0s : nk_all;
+    // KP groups: this group's i-th K-step is k0s + grp + KP i; nit iterations each
+    const int nit = (nk + KP - 1) / KP;
     // this lane's rows and swizzled 16-byte slots in the wave's loads: A load j
     // covers tile rows 8 j .. 8 j + 7 (8 slots each), B load j rows 16 j .. 16 j + 15 (4 slots)
     const char *A = reinterpret_cast<const char *>(g.A), *B = reinterpret_cast<const char *>(g.B);
@@ -306,8 +320,9 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     const char *zero = reinterpret_cast<const char *>(g_gemm_zero16);
     auto issue = [&](int buf, int kt) {
         char *st = smem[buf];
-        const bool live = kt < nk;
-        const int64_t ka = live ? (int64_t)(k0s + kt) * BK * AE : 0, kb = live ? (int64_t)(k0s + kt) * BK * BE : 0;
+        const int kg = grp + KP * kt;       // the group's kt-th K-step
+        const bool live = kt < nit && kg < nk;
+        const int64_t ka = live ? (int64_t)(k0s + kg) * BK * AE : 0, kb = live ? (int64_t)(k0s + kg) * BK * BE : 0;
 #pragma unroll
         for (int u = 0; u < LA; u++) lds_dma16(live ? a_src[u] + ka : zero, st + 1024 * (wid * LA + u));
 #pragma unroll
@@ -326,7 +341,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
     // older than every ring load, they are complete by the first wait.
     constexpr bool PRE = KS == 1;
     float pre_s[WC], pre_b[WC], pre_c[PRE && (EPI & EPI_ACCUM) ? WR : 1][WC][4];
-    if constexpr (PRE) {
+    if (PRE && grp == 0) {
 #pragma unroll
         for (int j = 0; j < WC; j++) {
             const int n = min(n0 + nw + j * 16 + (lane & 15), N - 1);
@@ -350,7 +365,7 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
 #pragma unroll
     for (int s = 0; s < NS - 1; s++) issue(s, s);
     const int fr = lane & 15, fg = lane >> 4;
-    for (int kt = 0; kt < nk; kt++) {
+    for (int kt = 0; kt < nit; kt++) {
         wait_vmcnt<(LA + LB) * (NS - 2)>();   // this wave's loads of stage kt have landed
         __syncthreads();                      // ... and every wave's; stage kt - 1 is free
         issue((kt + NS - 1) % NS, kt + NS - 1);
@@ -418,6 +433,35 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmArgs g) {
         }
     }
     wait_vmcnt<0>();                          // no load may land in LDS after the block ends
+    if constexpr (KP > 1) {
+        // groups 1 .. KP - 1 hand their partial tiles to group 0 through the
+        // rings' LDS (every wave is past its last ring read at the barrier)
+        constexpr int EW = WR * WC * 4;      // accumulator values per lane
+        float *red = reinterpret_cast<float *>(&smem_all[0][0][0]);
+        __syncthreads();
+        if (grp > 0) {
+            float *dst = red + ((grp - 1) * 4 + wid) * EW * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < WR; i++)
+#pragma unroll
+                for (int j = 0; j < WC; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) dst[((i * WC + j) * 4 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (grp > 0) return;
+#pragma unroll
+        for (int p = 1; p < KP; p++) {
+            const float *src = red + ((p - 1) * 4 + wid) * EW * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < WR; i++)
+#pragma unroll
+                for (int j = 0; j < WC; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        acc[i][j][r] = __fadd_rn(acc[i][j][r], src[((i * WC + j) * 4 + r) * 64]);
+        }
+    }
 
     // epilogue: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile
     if constexpr (PRE) {
@@ -546,9 +590,41 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
     return hipGetLastError();
 }
 
+// the unsplit kernel with KP K groups per block
+template <int ASRC, int BSRC, int NS, int BM, int BN, int KP>
+static hipError_t go_gemm_lds_kp(const GemmArgs &g, int epi, dim3 grid, hipStream_t st) {
+    switch (epi) {
+#define QE(E)                                                                                                 \
+    case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, KP>), grid, dim3(256 * KP), 0, st, g); \
+        break;
+        QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+#undef QE
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// K groups per block of the 64 x 64 kernel: 4 while a block has at least 16
+// K-steps and the tile columns number at most 32 (QASR_GEMM_KP=1|2|4 forces
+// one).  Measured at M = 375 (config 1, us per launch, KP 1 -> 4): k / v
+// 7.7 -> 6.6, q 8.5 -> 7.5, o 12.4 -> 9.2, down 17.1 -> 11.9; gate / up (48
+// tile columns, 288 blocks of 16 waves for 256 CUs) 10.2 -> 12.2, so they
+// keep one group.  The rule reads N and K only, so a row's bits do not
+// depend on how many rows share the call.
+static int gemm_kp(const GemmArgs &g, int bk) {
+    static const int forced = [] { const char *e = getenv("QASR_GEMM_KP"); return e ? atoi(e) : 0; }();
+    if (forced == 1 || forced == 2 || forced == 4) return forced;
+    return (g.K / bk >= 16 && (g.N + 63) / 64 <= 32) ? 4 : 1;
+}
+
 template <int ASRC, int BSRC, int NS, int BM, int BN>
 static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     const int gx = (g.N + BN - 1) / BN, gy = (g.M + BM - 1) / BM;
+    if constexpr (BM == 64 && BN == 64) {
+        const int kp = gemm_kp(g, ASRC == A_F32_SPLIT ? 32 : 64);
+        if (kp == 4) return go_gemm_lds_kp<ASRC, BSRC, 3, 64, 64, 4>(g, epi, dim3(gx, gy), st);
+        if (kp == 2) return go_gemm_lds_kp<ASRC, BSRC, 4, 64, 64, 2>(g, epi, dim3(gx, gy), st);
+    }
     // split K in two (epilogues without a transposed store)
     // when the tile grid leaves most CUs idle and the caller gave a workspace
     // for the partials (QASR_GEMM_SPLITK=0 disables)
@@ -574,7 +650,7 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
         switch (epi) {
 #define QE(E)                                                                                          \
     case E:                                                                                            \
-        hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 2>), grid, dim3(256), 0, st, g);     \
+        hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 2, 1>), grid, dim3(256), 0, st, g);  \
         hipLaunchKernelGGL((k_gemm_splitk_reduce<E>), rg, dim3(256), 0, st, g, 2);                     \
         break;
             QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_GELU) QE(EPI_SCALE)
@@ -585,7 +661,7 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     }
     const dim3 grid(gx, gy);
     switch (epi) {
-#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1>), grid, dim3(256), 0, st, g); break;
+#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, 1>), grid, dim3(256), 0, st, g); break;
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
 #undef QE
         default: return hipErrorInvalidValue;
