@@ -3,6 +3,7 @@
     python -m qwenasr_amd.rocprof_summary <dir>/run_kernel_trace.csv [min_batch]
     python -m qwenasr_amd.rocprof_summary --pmc <dir>/run_counter_collection.csv <calib MiB>
     python -m qwenasr_amd.rocprof_summary --traffic <fetch csv> <write csv> <calib MiB> > profiles/hbm_traffic.txt
+    python -m qwenasr_amd.rocprof_summary --mfma-config1 <MfmaUtil csv> <MOPS csv> [reps]
 
 The second form averages each kernel's counter values (``--pmc FETCH_SIZE`` or
 ``WRITE_SIZE``, KiB per dispatch) and scales them by what the counter read for
@@ -135,8 +136,50 @@ def traffic(fetch_csv, write_csv, calib_mib):
     return "\n".join(out)
 
 
+# the shapes of bench_configs.config1, in its order (M outer)
+CONFIG1_SHAPES = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
+                  ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072), ("lm_head", 151936, 1024)]
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def _gemm_dispatches(path):
+    """k_gemm dispatches of one counter csv in dispatch order: (name, {counter: value summed
+    over the csv's per-dimension rows}, duration ns)."""
+    per = {}
+    for r in csv.DictReader(open(path)):
+        if "k_gemm" not in r["Kernel_Name"]:
+            continue
+        d = per.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"].split("(")[0].replace("void ", ""), defaultdict(float),
+                                                   int(r["End_Timestamp"]) - int(r["Start_Timestamp"])])
+        d[1][r["Counter_Name"]] += float(r["Counter_Value"])
+    return [per[k] for k in sorted(per)]
+
+
+def mfma_config1(util_csv, mops_csv, reps=3):
+    """The config-1 MFMA table from two counter runs of `bench_configs config1 <reps>`
+    (--pmc MfmaUtil; --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 GRBM_GUI_ACTIVE): per shape the
+    median over its reps timed launches (each shape's first launch is its warm-up)."""
+    util, mops = _gemm_dispatches(util_csv), _gemm_dispatches(mops_csv)
+    per = 1 + reps
+    out = ["| M | shape | N x K | kernel | MfmaUtil % | executed GFLOP | 2MNK GFLOP | us | TFLOP/s | % of peak |",
+           "|---:|---|---|---|---:|---:|---:|---:|---:|---:|"]
+    for i, M in enumerate((375, 390, 404)):
+        for j, (name, N, K) in enumerate(CONFIG1_SHAPES):
+            base = (i * len(CONFIG1_SHAPES) + j) * per
+            u = st.median(d[1]["MfmaUtil"] for d in util[base + 1:base + per])
+            ex = st.median(d[1]["SQ_INSTS_VALU_MFMA_MOPS_BF16"] for d in mops[base + 1:base + per]) * 512 / 1e9
+            us = st.median(d[2] for d in mops[base + 1:base + per]) / 1e3
+            kern = re.sub(r"qasr::k_gemm_lds<(.*)>", r"\1", mops[base + 1][0])
+            tf = ex * 1e3 / us
+            out.append(f"| {M} | {name} | {N}x{K} | `{kern}` | {u:.2f} | {ex:.3f} | {2.0 * M * N * K / 1e9:.3f} | "
+                       f"{us:.2f} | {tf:.1f} | {100 * tf / BF16_PEAK_TFLOPS:.1f} |")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
-    if sys.argv[1] == "--traffic":
+    if sys.argv[1] == "--mfma-config1":
+        print(mfma_config1(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 3))
+    elif sys.argv[1] == "--traffic":
         print(traffic(sys.argv[2], sys.argv[3], float(sys.argv[4])))
     elif sys.argv[1] == "--pmc":
         print(summarise_pmc(sys.argv[2], float(sys.argv[3])))
