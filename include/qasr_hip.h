@@ -337,6 +337,15 @@ int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n_samples, float
 /* Encoder::forward (encoder.rs:186): host mel [128][frames] -> host [tokens][output_dim] */
 int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64_t frames, float *out,
                              int64_t *n_tokens);
+/* Encoder::forward of n (1..64) mels in one pass (no counterpart in the
+ * reference, which encodes one mel per call): mels[j] host [128][frames[j]];
+ * each sequence's rows equal those of qasr_hip_encoder_forward on its own
+ * mel bit for bit (its attention windows restart at its first row), and they
+ * follow one another in out (host [sum tokens][output_dim]); tokens[j] = the
+ * row count of sequence j.  The streaming drivers' stream batch encodes all
+ * of a round's encoder windows this way. */
+int qasr_hip_encoder_forward_batch(qasr_encoder *e, int32_t n, const float *const *mels, const int64_t *frames,
+                                   float *out, int64_t *tokens);
 /* transcribe_segment (transcribe.rs:63-247) with a forced decode length and no
  * text prompt: mel -> encoder -> prompt -> prefill(total - 1) -> n_steps greedy
  * forwards, all device-resident.  times_ms (optional, 4 entries): mel, encoder,
@@ -558,6 +567,11 @@ int qasr_hip_stream_batch_create(qasr_decoder *d, qasr_encoder *e, const qasr_st
                                  int64_t max_seq, qasr_stream_batch **out);
 void qasr_hip_stream_batch_free(qasr_stream_batch *g);
 qasr_stream *qasr_hip_stream_batch_stream(qasr_stream_batch *g, int32_t i);
+/* wall time of the last push's phases on the library stream, summed over its
+ * rounds (HIP events; ms[3]): preparation (every stream's encoder windows,
+ * prompt rows and prefix comparison), the multi-stream prefill, the batched
+ * decode */
+int qasr_hip_stream_batch_times(const qasr_stream_batch *g, double *ms);
 /* samples[i] / n_samples[i]: the whole audio of stream i so far; finalize
  * (nullable) per stream; stream i's newly committed text tokens go to
  * tokens_out + i * cap (nullable), n_out[i] = their count.  Streams advance

@@ -144,6 +144,7 @@ _SIGS = {
     "qasr_hip_transcribe_forced": (C.c_int, [P, P, P, I64, I32, P, P]),
     "qasr_hip_transcribe": (C.c_int, [P, P, P, I64, I32, P, C.POINTER(I64), P]),
     "qasr_hip_text_tokens": (I64, [P, I64, P]),
+    "qasr_hip_encoder_forward_batch": (C.c_int, [P, I32, P, P, P, P]),
     "qasr_hip_transcribe_prompt": (C.c_int, [P, P, P, I64, C.POINTER(Prompt), P, I64, I32, P, C.POINTER(I64), P]),
     "qasr_hip_text_tokens_from": (I64, [P, I64, C.c_int, P]),
     "qasr_hip_segment_splits": (I64, [P, I64, C.c_float, C.c_float, P, I64]),
@@ -179,6 +180,7 @@ _SIGS = {
     "qasr_hip_stream_batch_create": (C.c_int, [P, P, C.POINTER(StreamConfig), I32, I64, C.POINTER(P)]),
     "qasr_hip_stream_batch_free": (None, [P]),
     "qasr_hip_stream_batch_stream": (P, [P, I32]),
+    "qasr_hip_stream_batch_times": (C.c_int, [P, P]),
     "qasr_hip_stream_batch_push": (C.c_int, [P, P, P, P, P, I64, P]),
     "qasr_hip_decoder_set_lm_head": (C.c_int, [P, P, I64]),
     "qasr_hip_decoder_logits_dim": (I64, [P]),

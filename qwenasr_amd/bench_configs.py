@@ -336,7 +336,7 @@ def config4_stream(n_streams=32, rounds=3, chunk_sec=2.0):
     res = {}
     got = {}
     for mode in ("batched", "one_at_a_time"):
-        times, tok_rounds = [], []
+        times, tok_rounds, phases = [], [], []
         if mode == "batched":
             g = StreamBatch(dec, enc, n_streams, 1024)
             g.push([x[:int(c) * step] for x, c in zip(xs, start_chunks)])          # history, untimed
@@ -345,6 +345,7 @@ def config4_stream(n_streams=32, rounds=3, chunk_sec=2.0):
                 c0 = time.perf_counter()
                 out = g.push([x[:e] for x, e in zip(xs, ends)])
                 times.append(time.perf_counter() - c0)
+                phases.append([round(v, 2) for v in g.times()])
                 tok_rounds.append([o.tolist() for o in out])
             stats = [[int(v) for v in g.stream(i).stats()] for i in range(n_streams)]
             g.close()
@@ -372,6 +373,11 @@ def config4_stream(n_streams=32, rounds=3, chunk_sec=2.0):
                      "audio_s_per_wall_s": round(n_streams * chunk_sec / (ms / 1000.0), 1),
                      "last_round_forwards_per_stream": [st[4] for st in stats],
                      "last_round_prefill_rows": [st[2] for st in stats]}
+        if phases:
+            # GPU-timeline phases of each round: preparation (encoder windows,
+            # prompt rows, prefix comparison), multi-stream prefill, decode
+            res[mode]["phase_ms"] = {"prepare": [p[0] for p in phases], "prefill": [p[1] for p in phases],
+                                     "decode": [p[2] for p in phases]}
         log(f"[config4_stream] {mode}: rounds {res[mode]['round_ms']} ms; "
             f"{res[mode]['audio_s_per_wall_s']} s of audio per s; last-round forwards {fwd}")
     same = got["batched"] == got["one_at_a_time"]

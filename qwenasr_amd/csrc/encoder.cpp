@@ -248,6 +248,9 @@ static int egemm(qasr_encoder *e, const float *A, int64_t lda, const uint16_t *B
     g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc; g.bias = bias;
     g.gelu_n = gelu_n; g.gelu_rows = gelu_rows;
     g.ws = reinterpret_cast<float *>(e->h->scratch); g.ws_bytes = QASR_SCRATCH_BYTES;
+    // K split chosen by the shape alone: a row's bits do not depend on how many
+    // rows (sequences) share the call
+    g.split_by_shape = 1;
     LAUNCHCHK(launch_gemm(g, A_F32_SPLIT, B_BF16, epi, e->h->stream), "encoder gemm");
     return QASR_OK;
 }
@@ -303,33 +306,67 @@ static size_t stem_bytes(const qasr_encoder *e, int n_chunks, int cw) {
     return sizeof(float) * f + 1024;
 }
 
-// Encoder::forward on a device mel [128][frames]; out [tokens][output_dim]
-int encoder_forward_dev(qasr_encoder *e, const float *mel, int64_t frames, float *out, int64_t *n_tok) {
+// Encoder::forward (encoder.rs:186-358) of n sequences in one pass, each the
+// forward of its own device mel [128][frames[j]]: the conv stem per sequence,
+// then every layer over the rows of all of them.  Sequence j's rows start at
+// row P_j, a multiple of 32 (n > 1; the rows between sequences are zeros and
+// not attended): the attention windows restart at each sequence and no block
+// of the row attention straddles two, and the GEMMs (K split by shape),
+// norms and GELU are row-wise, so each sequence's rows have the bits of a
+// call of its own.  (The GELU's vector/scalar split depends on the buffer
+// length only through tails that d_model and ffn_dim multiples of 128 never
+// have; other widths take one call per sequence.)  Sequence j's output rows
+// go to out + (T_0 + ... + T_{j-1}) * output_dim, tokens[j] = T_j.
+int encoder_forward_multi(qasr_encoder *e, int n, const float *const *mels, const int64_t *frames, float *out,
+                          int64_t *tokens) {
     const qasr_enc_config &c = e->c;
     hipStream_t st = e->h->stream;
-    const int64_t T = encoder_tokens(e, frames);
     const int D = c.d_model, F = c.ffn_dim, O = c.output_dim;
-    const int64_t n_full = frames / c.chunk_size;
-    const int tail = (int)(frames % c.chunk_size);
-    size_t stem = std::max(stem_bytes(e, (int)std::max<int64_t>(n_full, 1), c.chunk_size),
-                           tail ? stem_bytes(e, 1, tail) : (size_t)0);
-    const size_t tf = sizeof(float) * (size_t)T;
+    if (n < 1 || n > QASR_ATTN_MAX_SEG) return qasr_fail(QASR_ERR_INVALID, "encoder: 1 to 64 sequences per call");
+    if (n > 1 && (D % 128 != 0 || F % 128 != 0)) {
+        int64_t off = 0;
+        for (int j = 0; j < n; j++) {
+            TRY(encoder_forward_multi(e, 1, mels + j, frames + j, out + off * O, tokens + j));
+            off += tokens[j];
+        }
+        return QASR_OK;
+    }
+    std::vector<int64_t> T(n), P(n + 1, 0);
+    size_t stem = 0;
+    for (int j = 0; j < n; j++) {
+        T[j] = encoder_tokens(e, frames[j]);
+        P[j + 1] = P[j] + (n > 1 ? (T[j] + 31) / 32 * 32 : T[j]);
+        const int64_t n_full = frames[j] / c.chunk_size;
+        const int tail = (int)(frames[j] % c.chunk_size);
+        stem = std::max({stem, stem_bytes(e, (int)std::max<int64_t>(n_full, 1), c.chunk_size),
+                         tail ? stem_bytes(e, 1, tail) : (size_t)0});
+    }
+    const int64_t Mt = P[n];
+    const size_t tf = sizeof(float) * (size_t)Mt;
     const size_t layer_bytes = tf * (D + 3 * D + D + F) + 4096;
     const size_t x_bytes = (tf * D + 255) / 256 * 256;
     TRY(ensure_scratch(e, x_bytes + std::max(stem, layer_bytes)));
-    float *x = reinterpret_cast<float *>(e->scratch);     // residual stream [T][D]
+    float *x = reinterpret_cast<float *>(e->scratch);     // residual stream [Mt][D]
     char *buf = e->scratch + x_bytes;
-    if (n_full > 0) TRY(conv_stem(e, mel, frames, 0, (int)n_full, c.chunk_size, x, buf));
-    if (tail) TRY(conv_stem(e, mel, frames, n_full * c.chunk_size, 1, tail, x + n_full * e->tokens_per_chunk * D, buf));
+    if (n > 1) HIPCHK(hipMemsetAsync(x, 0, sizeof(float) * Mt * D, st));   // the rows between sequences
+    for (int j = 0; j < n; j++) {
+        const int64_t n_full = frames[j] / c.chunk_size;
+        const int tail = (int)(frames[j] % c.chunk_size);
+        float *xj = x + P[j] * D;
+        if (n_full > 0) TRY(conv_stem(e, mels[j], frames[j], 0, (int)n_full, c.chunk_size, xj, buf));
+        if (tail)
+            TRY(conv_stem(e, mels[j], frames[j], n_full * c.chunk_size, 1, tail, xj + n_full * e->tokens_per_chunk * D,
+                          buf));
+    }
     float *xn = reinterpret_cast<float *>(buf);
-    float *qkv = xn + T * D;
-    float *att = qkv + T * 3 * D;
-    float *mid = att + T * D;
+    float *qkv = xn + Mt * D;
+    float *att = qkv + Mt * 3 * D;
+    float *mid = att + Mt * D;
     const int wsz = e->tokens_per_chunk * (c.n_window_infer / c.chunk_size);
-    const int M = (int)T;
+    const int M = (int)Mt;
     for (int l = 0; l < c.n_layers; l++) {
         const EncLayerDev &L = e->L[l];
-        LAUNCHCHK(launch_layer_norm_rows(xn, x, L.ln1_w, L.ln1_b, T, D, 1e-5f, st), "enc ln1");
+        LAUNCHCHK(launch_layer_norm_rows(xn, x, L.ln1_w, L.ln1_b, Mt, D, 1e-5f, st), "enc ln1");
         TRY(egemm(e, xn, D, L.wqkv, D, qkv, 3 * D, M, 3 * D, D, L.bqkv, EPI_NONE));
         AttnRowsArgs a{};
         a.q = qkv; a.q_rs = 3 * D;
@@ -337,16 +374,35 @@ int encoder_forward_dev(qasr_encoder *e, const float *mel, int64_t frames, float
         a.out = att; a.o_rs = D;
         a.n_q = M; a.n_k = M; a.G = 1; a.q_offset = 0; a.window = wsz;
         a.scale = 1.0f / sqrtf((float)c.head_dim);
+        if (n > 1) {
+            a.n_seg = n;
+            for (int j = 0; j < n; j++) {
+                a.seg_lo[j] = (int)P[j];
+                a.seg_hi[j] = (int)(P[j] + T[j]);
+            }
+        }
         LAUNCHCHK(launch_attn_rows(a, c.n_heads, c.head_dim, st), "enc attention");
         TRY(egemm(e, att, D, L.wo, D, x, D, M, D, D, L.bo, EPI_ACCUM));
-        LAUNCHCHK(launch_layer_norm_rows(xn, x, L.ln2_w, L.ln2_b, T, D, 1e-5f, st), "enc ln2");
-        TRY(egemm(e, xn, D, L.fc1, D, mid, F, M, F, D, L.b1, EPI_GELU, (int64_t)T * F));
+        LAUNCHCHK(launch_layer_norm_rows(xn, x, L.ln2_w, L.ln2_b, Mt, D, 1e-5f, st), "enc ln2");
+        TRY(egemm(e, xn, D, L.fc1, D, mid, F, M, F, D, L.b1, EPI_GELU, (int64_t)Mt * F));
         TRY(egemm(e, mid, F, L.fc2, F, x, D, M, D, F, L.b2, EPI_ACCUM));
     }
-    LAUNCHCHK(launch_layer_norm_rows(xn, x, e->ln_post_w, e->ln_post_b, T, D, 1e-5f, st), "enc ln_post");
-    TRY(egemm(e, xn, D, e->proj1_w, D, att, D, M, D, D, e->proj1_b, EPI_GELU, (int64_t)T * D));
-    TRY(egemm(e, att, D, e->proj2_w, D, out, O, M, O, D, e->proj2_b, EPI_NONE));
-    if (n_tok) *n_tok = T;
+    LAUNCHCHK(launch_layer_norm_rows(xn, x, e->ln_post_w, e->ln_post_b, Mt, D, 1e-5f, st), "enc ln_post");
+    TRY(egemm(e, xn, D, e->proj1_w, D, att, D, M, D, D, e->proj1_b, EPI_GELU, (int64_t)Mt * D));
+    int64_t off = 0;
+    for (int j = 0; j < n; j++) {
+        TRY(egemm(e, att + P[j] * D, D, e->proj2_w, D, out + off * O, O, (int)T[j], O, D, e->proj2_b, EPI_NONE));
+        tokens[j] = T[j];
+        off += T[j];
+    }
+    return QASR_OK;
+}
+
+// Encoder::forward on a device mel [128][frames]; out [tokens][output_dim]
+int encoder_forward_dev(qasr_encoder *e, const float *mel, int64_t frames, float *out, int64_t *n_tok) {
+    int64_t t = 0;
+    TRY(encoder_forward_multi(e, 1, &mel, &frames, out, &t));
+    if (n_tok) *n_tok = t;
     return QASR_OK;
 }
 
@@ -403,6 +459,41 @@ extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, fl
         rc = qasr_fail(QASR_ERR_HIP, "mel: download failed");
     if (hipStreamSynchronize(e->h->stream) != hipSuccess && rc == QASR_OK)
         rc = qasr_fail(QASR_ERR_HIP, "mel: stream failed");
+    return rc;
+}
+
+// n host mels [128][frames[j]] -> their encoder rows, one after another in
+// out (host), tokens[j] each; one encoder pass over all of them
+extern "C" int qasr_hip_encoder_forward_batch(qasr_encoder *e, int32_t n, const float *const *mels,
+                                              const int64_t *frames, float *out, int64_t *tokens) {
+    if (!e) return qasr_fail(QASR_ERR_INVALID, "encoder is null");
+    CHECK_H(e->h);
+    if (n < 1 || n > QASR_ATTN_MAX_SEG || !mels || !frames || !out || !tokens)
+        return qasr_fail(QASR_ERR_INVALID, "encoder_forward_batch: bad arguments");
+    int64_t tot_f = 0, tot_t = 0;
+    for (int j = 0; j < n; j++) {
+        if (!mels[j] || frames[j] <= 0) return qasr_fail(QASR_ERR_INVALID, "encoder_forward_batch: bad sequence");
+        tot_f += frames[j];
+        tot_t += encoder_tokens(e, frames[j]);
+    }
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * tot_f));
+    TRY(dbuf_ensure(e->enc_out, sizeof(float) * tot_t * e->c.output_dim));
+    std::vector<const float *> dm(n);
+    int rc = QASR_OK;
+    int64_t f = 0;
+    for (int j = 0; j < n && rc == QASR_OK; j++) {
+        dm[j] = e->mel.as<float>() + 128 * f;
+        if (hipMemcpyAsync(const_cast<float *>(dm[j]), mels[j], sizeof(float) * 128 * frames[j],
+                           hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
+            rc = qasr_fail(QASR_ERR_HIP, "encoder_forward_batch: upload failed");
+        f += frames[j];
+    }
+    if (rc == QASR_OK) rc = encoder_forward_multi(e, n, dm.data(), frames, e->enc_out.as<float>(), tokens);
+    if (rc == QASR_OK && hipMemcpyAsync(out, e->enc_out.p, sizeof(float) * tot_t * e->c.output_dim,
+                                        hipMemcpyDeviceToHost, e->h->stream) != hipSuccess)
+        rc = qasr_fail(QASR_ERR_HIP, "encoder_forward_batch: download failed");
+    if (hipStreamSynchronize(e->h->stream) != hipSuccess && rc == QASR_OK)
+        rc = qasr_fail(QASR_ERR_HIP, "encoder_forward_batch: stream failed");
     return rc;
 }
 

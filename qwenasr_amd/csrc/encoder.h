@@ -13,6 +13,9 @@ size_t mel_scratch_floats(int64_t nf);
 int mel_dev(qasr_encoder *e, const float *x, int64_t ns, float *mel, float *scratch);
 // Encoder::forward on a device mel [128][frames]; out [tokens][output_dim]
 int encoder_forward_dev(qasr_encoder *e, const float *mel, int64_t frames, float *out, int64_t *n_tok);
+// n (<= 64) sequences in one pass; sequence j's rows at out + (T_0 + ... + T_{j-1}) rows
+int encoder_forward_multi(qasr_encoder *e, int n, const float *const *mels, const int64_t *frames, float *out,
+                          int64_t *tokens);
 int64_t encoder_tokens(const qasr_encoder *e, int64_t frames);
 int64_t encoder_output_dim(const qasr_encoder *e);
 qasr_hip *encoder_handle(const qasr_encoder *e);

@@ -470,6 +470,22 @@ hipError_t launch_build_prompt(float *out, const uint16_t *embed, const int *tok
 // A block owns 32 query rows (QT queries x G heads of one KV head) and walks key
 // tiles of 32; 8 threads per row.
 // ---------------------------------------------------------------------------
+// The rows [s0, s1) of the sequence that row q belongs to: the whole call, or
+// with n_seg > 0 the last sequence starting at or before q (compile-time
+// indices only, so the tables stay in the kernel arguments)
+__device__ __forceinline__ void attn_sequence(const AttnRowsArgs &a, int q, int &s0, int &s1) {
+    s0 = 0;
+    s1 = min(a.n_q, a.n_k);
+    if (a.n_seg > 0) {
+#pragma unroll
+        for (int j = 0; j < QASR_ATTN_MAX_SEG; j++)
+            if (j < a.n_seg && a.seg_lo[j] <= q) {
+                s0 = a.seg_lo[j];
+                s1 = a.seg_hi[j];
+            }
+    }
+}
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
     constexpr int R = 32, KT = 32, DP = HD / 8;
@@ -481,22 +497,25 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
     const int G = a.G, QT = R / G;
     const int kvh = blockIdx.x, q0 = blockIdx.y * QT;
     const int qi = q0 + r / G, h = kvh * G + r % G;
-    const bool row_ok = qi < a.n_q;
+    // the block's sequence (windowed calls; blocks never straddle two)
+    int s0 = 0, s1 = a.n_q;
+    if (a.window > 0) attn_sequence(a, q0, s0, s1);
+    const bool row_ok = qi < a.n_q && qi < s1;
     // key range of this row
     int lo = 0, hi;
     if (a.window > 0) {
-        lo = (qi / a.window) * a.window;
-        hi = min(lo + a.window, a.n_k);
+        lo = s0 + ((qi - s0) / a.window) * a.window;
+        hi = min(lo + a.window, min(a.n_k, s1));
     } else {
         hi = min(a.q_offset + qi + 1, a.n_k);
     }
     if (!row_ok) { lo = 0; hi = 0; }
     // key range of the block
-    const int qlast = min(q0 + QT, a.n_q) - 1;
+    const int qlast = min(q0 + QT, min(a.n_q, s1)) - 1;
     int blo, bhi;
     if (a.window > 0) {
-        blo = (q0 / a.window) * a.window;
-        bhi = min((qlast / a.window) * a.window + a.window, a.n_k);
+        blo = s0 + ((q0 - s0) / a.window) * a.window;
+        bhi = min(s0 + ((qlast - s0) / a.window) * a.window + a.window, min(a.n_k, s1));
     } else {
         blo = 0;
         bhi = min(a.q_offset + qlast + 1, a.n_k);
@@ -610,20 +629,24 @@ __global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
     const int lq = lane & 15, lg = lane >> 4;
     // key range of this lane's query (for the S^T masks) and of the block
     const int qi = q0 + lq;
+    // the block's sequence (windowed calls; blocks never straddle two)
+    int s0 = 0, s1 = a.n_q;
+    if (a.window > 0) attn_sequence(a, q0, s0, s1);
     int lo = 0, hi = 0;
-    if (qi < a.n_q) {
+    if (qi < a.n_q && qi < s1) {
         if (a.window > 0) {
-            lo = (qi / a.window) * a.window;
-            hi = min(lo + a.window, a.n_k);
+            lo = s0 + ((qi - s0) / a.window) * a.window;
+            hi = min(lo + a.window, min(a.n_k, s1));
         } else {
             hi = min(a.q_offset + qi + 1, a.n_k);
         }
     }
-    const int qlast = min(q0 + 16, a.n_q) - 1;
+    const int qlast = min(q0 + 16, min(a.n_q, s1)) - 1;
+    if (qlast < q0) return;                 // padding rows between two sequences
     int blo, bhi;
     if (a.window > 0) {
-        blo = (q0 / a.window) * a.window;
-        bhi = min((qlast / a.window) * a.window + a.window, a.n_k);
+        blo = s0 + ((q0 - s0) / a.window) * a.window;
+        bhi = min(s0 + ((qlast - s0) / a.window) * a.window + a.window, min(a.n_k, s1));
     } else {
         blo = 0;
         bhi = min(a.q_offset + qlast + 1, a.n_k);

@@ -193,6 +193,7 @@ hipError_t launch_gemm_f32(const GemmArgs &g, hipStream_t st);
 
 namespace qasr {
 // ---- prefill / encoder / mel ------------------------------------------------
+#define QASR_ATTN_MAX_SEG 64
 struct AttnRowsArgs {
     const float *q;           // row i, head h at q + i * q_rs + h * hd
     int64_t q_rs;
@@ -206,6 +207,13 @@ struct AttnRowsArgs {
     int window;               // > 0: query i sees its window [w*window, min((w+1)*window, n_k))
     float scale;
     int kv_div;               // set by launch_attn_rows: block x reads KV head x / kv_div (0 = 1)
+    // windowed calls over several sequences (n_seg > 0): sequence j holds rows
+    // [seg_lo[j], seg_hi[j]) and its windows start at seg_lo[j]; every seg_lo
+    // is a multiple of 32, so no block of rows straddles two sequences and a
+    // row meets the same blocks, key chunks and order as in a call of its own
+    // sequence alone; rows outside every range are not computed
+    int n_seg;
+    int seg_lo[QASR_ATTN_MAX_SEG], seg_hi[QASR_ATTN_MAX_SEG];
 };
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st);
 hipError_t launch_layer_norm_rows(float *out, const float *x, const float *w, const float *b, int64_t seq,

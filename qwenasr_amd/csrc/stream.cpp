@@ -63,6 +63,12 @@ std::pair<int64_t, int64_t> tail_repeat_blocks(const std::vector<int32_t> &t, in
 }
 }  // namespace
 
+// Device scratch of encode_requests (the audio slices, their mels, the mel
+// working area and, for several inputs, the joint output rows).
+struct EncScratch {
+    DevBuf audio, mel, melsc, out;
+};
+
 struct EncWindow {
     DevBuf out;
     int64_t seq = 0;
@@ -88,7 +94,8 @@ struct qasr_stream {
     int64_t cursor = 0;
     int32_t chunk_idx = 0;
     // scratch
-    DevBuf audio, mel, melsc, enc_all, toks, flags;
+    EncScratch enc;                 // the encoder inputs' audio, mels and joint output rows
+    DevBuf enc_all, toks, flags;
     std::vector<int32_t> host_tok;
     // statistics of the last chunk
     int64_t st_reused = 0, st_prefill_len = 0, st_delta = 0, st_steps_total = 0, st_forwards = 0;
@@ -143,7 +150,8 @@ extern "C" void qasr_hip_stream_free(qasr_stream *s) {
     (void)hipStreamSynchronize(s->d->h->stream);
     release_windows(s);
     for (DevBuf &b : s->win_pool) dbuf_release(b);
-    for (DevBuf *b : {&s->partial, &s->partial_next, &s->embeds, &s->prev_embeds, &s->audio, &s->mel, &s->melsc, &s->enc_all,
+    for (DevBuf *b : {&s->partial, &s->partial_next, &s->embeds, &s->prev_embeds, &s->enc.audio, &s->enc.mel,
+                      &s->enc.melsc, &s->enc.out, &s->enc_all,
                       &s->toks, &s->flags})
         dbuf_release(*b);
     delete s;
@@ -175,24 +183,83 @@ extern "C" int qasr_hip_stream_reset(qasr_stream *s) {
     return QASR_OK;
 }
 
-// mel + encoder of host samples[0, ns) into `out` (grown); seq = 0 when too short
-static int encode_slice(qasr_stream *s, const float *samples, int64_t ns, DevBuf &out, int64_t *seq) {
-    hipStream_t st = s->d->h->stream;
-    *seq = 0;
-    const int64_t nf = mel_frames_for(ns);
-    if (nf <= 0) return QASR_OK;
-    TRY(dbuf_ensure(s->audio, sizeof(float) * ns));
-    HIPCHK(hipMemcpyAsync(s->audio.p, samples, sizeof(float) * ns, hipMemcpyHostToDevice, st));
-    TRY(dbuf_ensure(s->mel, sizeof(float) * 128 * nf));
-    TRY(dbuf_ensure(s->melsc, sizeof(float) * mel_scratch_floats(nf)));
-    TRY(mel_dev(s->e, s->audio.as<float>(), ns, s->mel.as<float>(), s->melsc.as<float>()));
-    const int64_t T = encoder_tokens(s->e, nf);
-    TRY(dbuf_ensure(out, sizeof(float) * T * s->d->c.hidden));
-    int64_t got = 0;
-    TRY(encoder_forward_dev(s->e, s->mel.as<float>(), nf, out.as<float>(), &got));
-    // the host copy of the audio slice must outlive the upload
+// One encoder input of a chunk (transcribe.rs:959-1002): host samples[0, ns)
+// of a newly completed window (win >= 0: the stream's window win) or of the
+// partial tail (win < 0: into the stream's partial_next); seq = its rows
+// (0 when the slice has no mel frame).
+struct EncReq {
+    qasr_stream *s = nullptr;
+    const float *x = nullptr;
+    int64_t ns = 0;
+    int win = -1;
+    int64_t seq = 0;
+};
+
+static DevBuf &req_dst(EncReq &r) { return r.win >= 0 ? r.s->win[(size_t)r.win].out : r.s->partial_next; }
+
+// The mel and encoder of every request, up to 64 inputs per encoder pass
+// (qasr_hip_encoder_forward_batch's arithmetic: each input's rows are those of
+// an encoder call of its own).  The host slices are read before it returns.
+static int encode_requests(qasr_decoder *d, qasr_encoder *e, std::vector<EncReq> &reqs, EncScratch &sc) {
+    hipStream_t st = d->h->stream;
+    const int64_t H = d->c.hidden;
+    std::vector<size_t> live;
+    int64_t tot_s = 0, tot_f = 0, max_f = 0;
+    for (size_t k = 0; k < reqs.size(); k++) {
+        reqs[k].seq = 0;
+        const int64_t nf = mel_frames_for(reqs[k].ns);
+        if (nf <= 0) continue;
+        live.push_back(k);
+        tot_s += reqs[k].ns;
+        tot_f += nf;
+        max_f = std::max(max_f, nf);
+    }
+    if (live.empty()) return QASR_OK;
+    TRY(dbuf_ensure(sc.audio, sizeof(float) * tot_s));
+    TRY(dbuf_ensure(sc.mel, sizeof(float) * 128 * tot_f));
+    TRY(dbuf_ensure(sc.melsc, sizeof(float) * mel_scratch_floats(max_f)));
+    std::vector<const float *> mels;
+    std::vector<int64_t> frames;
+    int64_t so = 0, fo = 0, tot_t = 0;
+    for (size_t k : live) {
+        const EncReq &r = reqs[k];
+        float *xa = sc.audio.as<float>() + so, *m = sc.mel.as<float>() + 128 * fo;
+        HIPCHK(hipMemcpyAsync(xa, r.x, sizeof(float) * r.ns, hipMemcpyHostToDevice, st));
+        TRY(mel_dev(e, xa, r.ns, m, sc.melsc.as<float>()));
+        const int64_t nf = mel_frames_for(r.ns);
+        mels.push_back(m);
+        frames.push_back(nf);
+        tot_t += encoder_tokens(e, nf);
+        so += r.ns;
+        fo += nf;
+    }
+    std::vector<int64_t> tok(live.size());
+    if (live.size() == 1) {
+        // one input: its rows straight into its destination
+        DevBuf &dst = req_dst(reqs[live[0]]);
+        TRY(dbuf_ensure(dst, sizeof(float) * tot_t * H));
+        TRY(encoder_forward_multi(e, 1, mels.data(), frames.data(), dst.as<float>(), tok.data()));
+    } else {
+        TRY(dbuf_ensure(sc.out, sizeof(float) * tot_t * H));
+        int64_t row = 0;
+        for (size_t g0 = 0; g0 < live.size(); g0 += QASR_ATTN_MAX_SEG) {
+            const int ng = (int)std::min<size_t>(QASR_ATTN_MAX_SEG, live.size() - g0);
+            TRY(encoder_forward_multi(e, ng, mels.data() + g0, frames.data() + g0, sc.out.as<float>() + row * H,
+                                      tok.data() + g0));
+            for (int q = 0; q < ng; q++) row += tok[g0 + q];
+        }
+        row = 0;
+        for (size_t q = 0; q < live.size(); q++) {
+            DevBuf &dst = req_dst(reqs[live[q]]);
+            TRY(dbuf_ensure(dst, sizeof(float) * tok[q] * H));
+            HIPCHK(hipMemcpyAsync(dst.p, sc.out.as<float>() + row * H, sizeof(float) * tok[q] * H,
+                                  hipMemcpyDeviceToDevice, st));
+            row += tok[q];
+        }
+    }
+    for (size_t q = 0; q < live.size(); q++) reqs[live[q]].seq = tok[q];
+    // the host slices must outlive their uploads
     HIPCHK(hipStreamSynchronize(st));
-    *seq = got;
     return QASR_OK;
 }
 
@@ -252,6 +319,10 @@ struct ChunkPlan {
     int32_t last_token = 0;        // the prompt's last row is this token's embedding
     const float *rows = nullptr;   // a deferred prefill: delta rows at position reused
     int64_t reused = 0, delta = 0;
+    // the chunk's encoder inputs: reqs[req0, req0 + nreq) of the round
+    size_t req0 = 0, nreq = 0;
+    int64_t full_end = 0;          // samples covered by complete windows
+    bool tail_req = false;         // the partial tail is re-encoded (the last request)
 };
 
 // greedy decode of up to max_new tokens after the prefill of prefill_len rows
@@ -293,53 +364,73 @@ static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t
     return QASR_OK;
 }
 
-// Steps 1-3 of a chunk of stream_push_audio: the encoder, the prompt rows and
-// the prefill with common-prefix reuse into `tgt`.  *skip: the chunk has no
-// encoder rows, the reference returns from the whole push with an empty delta
-// (transcribe.rs:1005-1008).
-static int chunk_prepare(qasr_stream *s, const float *samples, int64_t n, bool finalize, const PrefillTarget &tgt,
-                         ChunkPlan &pl, bool *skip) {
-    qasr_decoder *d = s->d;
-    hipStream_t st = d->h->stream;
-    const int64_t H = d->c.hidden;
+// Step 1 of a chunk of stream_push_audio, first half: advance the cursor and
+// list the encoder inputs (transcribe.rs:959-1002): every newly completed 8 s
+// window (its buffer appended to the stream's windows, filled by
+// encode_requests) and the partial tail when it is re-encoded (the first
+// chunk, every second chunk, and when finalizing).
+static void chunk_advance(qasr_stream *s, int64_t n, bool finalize, const float *samples, ChunkPlan &pl,
+                          std::vector<EncReq> &reqs) {
     const int64_t chunk_samples = (int64_t)(s->cfg.chunk_sec * (float)SAMPLE_RATE);
     const int64_t win_samples = WINDOW_FRAMES * HOP;
-    const int rollback = s->cfg.rollback;
-    *skip = false;
-
     s->cursor = std::min(s->cursor + chunk_samples, n);
     pl.is_final = finalize && s->cursor >= n;
-
-    // ---- encoder: new complete windows, then the partial tail ----
-    const int64_t full_end = (s->cursor / win_samples) * win_samples;
-    while ((s->enc_base_windows + (int64_t)s->win.size()) * win_samples < full_end) {
+    pl.req0 = reqs.size();
+    pl.full_end = (s->cursor / win_samples) * win_samples;
+    while ((s->enc_base_windows + (int64_t)s->win.size()) * win_samples < pl.full_end) {
         const int64_t ws = (s->enc_base_windows + (int64_t)s->win.size()) * win_samples;
         EncWindow w;
         if (!s->win_pool.empty()) {
             w.out = s->win_pool.back();
             s->win_pool.pop_back();
         }
-        const int rc_w = encode_slice(s, samples + ws, win_samples, w.out, &w.seq);
-        if (rc_w != QASR_OK) {
-            s->win_pool.push_back(w.out);
-            return rc_w;
-        }
-        s->enc_cached_total += w.seq;
         s->win.push_back(w);
+        EncReq r;
+        r.s = s;
+        r.x = samples + ws;
+        r.ns = win_samples;
+        r.win = (int)s->win.size() - 1;
+        reqs.push_back(r);
     }
     const int64_t partial_age = s->cursor - s->last_partial_cursor;
     const bool need_encode = s->last_partial_cursor == 0 || partial_age >= 2 * chunk_samples || pl.is_final;
+    pl.tail_req = pl.full_end < s->cursor && need_encode;
+    if (pl.tail_req) {
+        EncReq r;
+        r.s = s;
+        r.x = samples + pl.full_end;
+        r.ns = s->cursor - pl.full_end;
+        reqs.push_back(r);
+    }
+    pl.nreq = reqs.size() - pl.req0;
+}
+
+// Steps 1 (second half) to 3 of a chunk: the encoded windows and partial tail
+// taken over, the prompt rows and the prefill with common-prefix reuse into
+// `tgt`.  *skip: the chunk has no encoder rows, the reference returns from the
+// whole push with an empty delta (transcribe.rs:1005-1008).
+static int chunk_build(qasr_stream *s, const std::vector<EncReq> &reqs, const PrefillTarget &tgt, ChunkPlan &pl,
+                       bool *skip) {
+    qasr_decoder *d = s->d;
+    hipStream_t st = d->h->stream;
+    const int64_t H = d->c.hidden;
+    const int rollback = s->cfg.rollback;
+    *skip = false;
+    for (size_t k = pl.req0; k < pl.req0 + pl.nreq; k++) {
+        const EncReq &r = reqs[k];
+        if (r.win >= 0) {
+            s->win[(size_t)r.win].seq = r.seq;
+            s->enc_cached_total += r.seq;
+        }
+    }
     int64_t partial_seq = 0;
-    if (full_end < s->cursor) {
-        partial_seq = s->partial_seq;                       // reuse unless re-encoded below
-        if (need_encode) {
-            int64_t seq = 0;
-            TRY(encode_slice(s, samples + full_end, s->cursor - full_end, s->partial_next, &seq));
-            if (seq > 0) {
-                std::swap(s->partial, s->partial_next);
-                s->partial_seq = partial_seq = seq;
-                s->last_partial_cursor = s->cursor;
-            }
+    if (pl.full_end < s->cursor) {
+        partial_seq = s->partial_seq;                       // reuse unless re-encoded
+        const int64_t seq = pl.tail_req ? reqs[pl.req0 + pl.nreq - 1].seq : 0;
+        if (seq > 0) {
+            std::swap(s->partial, s->partial_next);
+            s->partial_seq = partial_seq = seq;
+            s->last_partial_cursor = s->cursor;
         }
     }
     const int64_t enc_len = s->enc_cached_total + partial_seq;
@@ -488,7 +579,10 @@ extern "C" int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_
     while (chunk_pending(s, n_samples, finalize != 0)) {
         ChunkPlan pl;
         bool skip = false, ended = false;
-        TRY(chunk_prepare(s, samples, n_samples, finalize != 0, PrefillTarget{}, pl, &skip));
+        std::vector<EncReq> reqs;
+        chunk_advance(s, n_samples, finalize != 0, samples, pl, reqs);
+        TRY(encode_requests(s->d, s->e, reqs, s->enc));
+        TRY(chunk_build(s, reqs, PrefillTarget{}, pl, &skip));
         if (skip) {
             emitted.clear();
             break;
@@ -519,6 +613,12 @@ struct qasr_stream_batch {
     qasr_decoder *d = nullptr;
     qasr_batch *b = nullptr;
     std::vector<qasr_stream *> s;
+    // phase boundaries of each round on the library stream (prepare: encoder
+    // windows, prompt rows and prefix comparison; prefill; decode), summed
+    // over the rounds of the last push
+    hipEvent_t ev[4] = {};
+    double phase_ms[3] = {};
+    EncScratch enc;                 // one encoder pass over every stream's inputs of a round
 };
 
 extern "C" void qasr_hip_stream_batch_free(qasr_stream_batch *g) {
@@ -528,6 +628,9 @@ extern "C" void qasr_hip_stream_batch_free(qasr_stream_batch *g) {
         qasr_hip_stream_free(s);
     }
     if (g->b) qasr_hip_batch_free(g->b);
+    for (hipEvent_t &v : g->ev)
+        if (v) (void)hipEventDestroy(v);
+    for (DevBuf *b : {&g->enc.audio, &g->enc.mel, &g->enc.melsc, &g->enc.out}) dbuf_release(*b);
     delete g;
 }
 
@@ -613,16 +716,29 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
     std::vector<std::vector<int32_t>> emitted(B), chunks(B);
     std::vector<ChunkPlan> pl(B);
     std::vector<char> open(B, 1);
+    hipStream_t st = g->d->h->stream;
+    for (hipEvent_t &v : g->ev)
+        if (!v) HIPCHK(hipEventCreate(&v));
+    for (double &v : g->phase_ms) v = 0.0;
     for (;;) {
-        std::vector<int> act;
+        HIPCHK(hipEventRecord(g->ev[0], st));
+        // every stream with a pending chunk: its encoder inputs, all encoded in
+        // one pass, then its prompt rows and prefix comparison
+        std::vector<int> cand, act;
+        std::vector<EncReq> reqs;
         for (int i = 0; i < B; i++) {
             const bool fin = finalize && finalize[i];
             if (!open[i] || !chunk_pending(g->s[i], n_samples[i], fin)) {
                 open[i] = 0;
                 continue;
             }
+            chunk_advance(g->s[i], n_samples[i], fin, samples[i], pl[i], reqs);
+            cand.push_back(i);
+        }
+        TRY(encode_requests(g->d, g->s.empty() ? nullptr : g->s[0]->e, reqs, g->enc));
+        for (int i : cand) {
             bool skip = false;
-            TRY(chunk_prepare(g->s[i], samples[i], n_samples[i], fin, PrefillTarget{g->b, i, true}, pl[i], &skip));
+            TRY(chunk_build(g->s[i], reqs, PrefillTarget{g->b, i, true}, pl[i], &skip));
             if (skip) {
                 emitted[i].clear();
                 open[i] = 0;
@@ -631,6 +747,7 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
             act.push_back(i);
         }
         if (act.empty()) break;
+        HIPCHK(hipEventRecord(g->ev[1], st));
         // one prefill of every stream's changed prompt rows (GEMMs over all of
         // them), each into its own slot
         {
@@ -646,7 +763,15 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
             TRY(batch_prefill_segments(g->b, (int)act.size(), slots.data(), rows.data(), starts.data(),
                                        counts.data()));
         }
+        HIPCHK(hipEventRecord(g->ev[2], st));
         TRY(group_decode(g, act, pl, chunks));
+        HIPCHK(hipEventRecord(g->ev[3], st));
+        HIPCHK(hipEventSynchronize(g->ev[3]));
+        for (int k = 0; k < 3; k++) {
+            float ms = 0.0f;
+            HIPCHK(hipEventElapsedTime(&ms, g->ev[k], g->ev[k + 1]));
+            g->phase_ms[k] += ms;
+        }
         for (int i : act) {
             bool ended = false;
             chunk_commit(g->s[i], pl[i], chunks[i], emitted[i], &ended);
@@ -660,6 +785,12 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
     }
     if (tokens_out)
         for (int i = 0; i < B; i++) std::copy(emitted[i].begin(), emitted[i].end(), tokens_out + (size_t)i * cap);
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_stream_batch_times(const qasr_stream_batch *g, double *ms) {
+    if (!g || !ms) return qasr_fail(QASR_ERR_INVALID, "stream_batch_times: null argument");
+    std::copy(g->phase_ms, g->phase_ms + 3, ms);
     return QASR_OK;
 }
 

@@ -259,6 +259,19 @@ class Encoder:
                                              C.byref(nt)))
         return out
 
+    def forward_batch(self, mels):
+        """One encoder pass over several mels: a list of each one's rows."""
+        ms = [np.ascontiguousarray(m, np.float32) for m in mels]
+        frames = np.array([m.shape[1] for m in ms], np.int64)
+        tot = sum(self.tokens(int(f)) for f in frames)
+        out = np.empty((tot, self.cfg["output_dim"]), np.float32)
+        toks = np.zeros(len(ms), np.int64)
+        ptrs = (P * len(ms))(*[m.ctypes.data_as(P) for m in ms])
+        check(lib().qasr_hip_encoder_forward_batch(self.e, len(ms), C.cast(ptrs, P), frames.ctypes.data_as(P),
+                                                   out.ctypes.data_as(P), toks.ctypes.data_as(P)))
+        offs = np.concatenate([[0], np.cumsum(toks)])
+        return [out[offs[j]:offs[j + 1]].copy() for j in range(len(ms))]
+
 
 def transcribe_forced(decoder, encoder, samples, n_steps):
     """transcribe_segment (transcribe.rs:63-247) with a forced decode length.
@@ -570,6 +583,12 @@ class StreamBatch:
 
     def stream(self, i):
         return _MemberStream(self, lib().qasr_hip_stream_batch_stream(self.g, int(i)))
+
+    def times(self):
+        """ms of the last push's phases: (preparation, prefill, decode)."""
+        ms = np.zeros(3, np.float64)
+        check(lib().qasr_hip_stream_batch_times(self.g, ms.ctypes.data_as(P)))
+        return tuple(float(v) for v in ms)
 
     def close(self):
         if self.g:

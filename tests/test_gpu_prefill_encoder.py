@@ -258,6 +258,32 @@ def test_encoder(dev, orc):
     ore.close()
 
 
+def test_encoder_forward_batch(dev, orc):
+    """One encoder pass over several mels (the stream batch's windows and
+    partial tails): each mel's rows are bit for bit those of its own call —
+    an 8 s window (800 frames), tails of 1..99 frames after full chunks, a
+    mel shorter than one chunk — and the first also against the oracle."""
+    from qwenasr_amd.model import Encoder
+    from qwenasr_amd.synth import ENC_0_6B, SynthEncoder, audio
+    w = SynthEncoder(dict(ENC_0_6B, n_layers=2), seed=1012)
+    enc = Encoder(dev, w)
+    ore = orc.OracleEncoder(w)
+    try:
+        ns = [128000, 50000, 8000, 31840, 128000, 1600, 77777]
+        mels = [orc.mel(audio(n, 40 + i)) for i, n in enumerate(ns)]
+        print("frames", [m.shape[1] for m in mels], flush=True)
+        got = enc.forward_batch(mels)
+        for m, g in zip(mels, got):
+            one = enc.forward(m)
+            assert g.shape == one.shape and g.tobytes() == one.tobytes(), m.shape
+        assert nrel(got[0], ore.forward(mels[0])) < 2e-4
+        got2 = enc.forward_batch(mels[3:5])                 # a second call, fewer sequences
+        assert got2[0].tobytes() == got[3].tobytes() and got2[1].tobytes() == got[4].tobytes()
+    finally:
+        enc.close()
+        ore.close()
+
+
 def test_transcribe_forced_tokens(dev, orc):
     """transcribe_segment with a forced decode length: identical token ids."""
     from qwenasr_amd.model import Decoder, Encoder, transcribe_forced
