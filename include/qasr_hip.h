@@ -568,9 +568,9 @@ int qasr_hip_stream_batch_create(qasr_decoder *d, qasr_encoder *e, const qasr_st
 void qasr_hip_stream_batch_free(qasr_stream_batch *g);
 qasr_stream *qasr_hip_stream_batch_stream(qasr_stream_batch *g, int32_t i);
 /* wall time of the last push's phases on the library stream, summed over its
- * rounds (HIP events; ms[3]): preparation (every stream's encoder windows,
- * prompt rows and prefix comparison), the multi-stream prefill, the batched
- * decode */
+ * rounds (HIP events; ms[4]): the encoder pass over every stream's new windows
+ * and partial tails, the prompt rows and prefix comparison, the multi-stream
+ * prefill, the batched decode */
 int qasr_hip_stream_batch_times(const qasr_stream_batch *g, double *ms);
 /* samples[i] / n_samples[i]: the whole audio of stream i so far; finalize
  * (nullable) per stream; stream i's newly committed text tokens go to

@@ -374,10 +374,11 @@ def config4_stream(n_streams=32, rounds=3, chunk_sec=2.0):
                      "last_round_forwards_per_stream": [st[4] for st in stats],
                      "last_round_prefill_rows": [st[2] for st in stats]}
         if phases:
-            # GPU-timeline phases of each round: preparation (encoder windows,
-            # prompt rows, prefix comparison), multi-stream prefill, decode
-            res[mode]["phase_ms"] = {"prepare": [p[0] for p in phases], "prefill": [p[1] for p in phases],
-                                     "decode": [p[2] for p in phases]}
+            # GPU-timeline phases of each round: the encoder pass over every
+            # stream's new windows and tails, the prompt rows and prefix
+            # comparison, the multi-stream prefill, the batched decode
+            res[mode]["phase_ms"] = {"encoder": [p[0] for p in phases], "prompt_rows": [p[1] for p in phases],
+                                     "prefill": [p[2] for p in phases], "decode": [p[3] for p in phases]}
         log(f"[config4_stream] {mode}: rounds {res[mode]['round_ms']} ms; "
             f"{res[mode]['audio_s_per_wall_s']} s of audio per s; last-round forwards {fwd}")
     same = got["batched"] == got["one_at_a_time"]

@@ -44,6 +44,29 @@ void dbuf_release(DevBuf &b) {
     b.cap = 0;
 }
 
+int hbuf_ensure(HostBuf &b, size_t bytes) {
+    if (bytes <= b.cap) return QASR_OK;
+    if (b.p) {
+        HIPCHK(hipDeviceSynchronize());   // copies queued into the old buffer have finished
+        (void)hipHostFree(b.p);
+    }
+    b.p = nullptr;
+    b.cap = 0;
+    const size_t want = std::max<size_t>((bytes + 255) / 256 * 256, 4096);
+    if (hipHostMalloc(&b.p, want, hipHostMallocDefault) != hipSuccess) {
+        b.p = nullptr;
+        return qasr_fail(QASR_ERR_NOMEM, "pinned host allocation of " + std::to_string(want) + " bytes failed");
+    }
+    b.cap = want;
+    return QASR_OK;
+}
+
+void hbuf_release(HostBuf &b) {
+    if (b.p) (void)hipHostFree(b.p);
+    b.p = nullptr;
+    b.cap = 0;
+}
+
 extern "C" int qasr_hip_device_count(int *n) {
     if (!n) return qasr_fail(QASR_ERR_INVALID, "n is null");
     HIPCHK(hipGetDeviceCount(n));

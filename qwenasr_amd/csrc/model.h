@@ -37,6 +37,15 @@ struct DevBuf {
 };
 int dbuf_ensure(DevBuf &b, size_t bytes);
 void dbuf_release(DevBuf &b);
+// Pinned host buffer with the same grow-only rule (device-to-host copies that
+// return without waiting land here).
+struct HostBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    template <typename T> T *as() const { return reinterpret_cast<T *>(p); }
+};
+int hbuf_ensure(HostBuf &b, size_t bytes);
+void hbuf_release(HostBuf &b);
 
 // The stream's next push prefills every row instead of reusing the rows its
 // previous push left in the decoder's KV cache (another caller has written

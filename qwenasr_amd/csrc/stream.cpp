@@ -96,6 +96,7 @@ struct qasr_stream {
     // scratch
     EncScratch enc;                 // the encoder inputs' audio, mels and joint output rows
     DevBuf enc_all, toks, flags;
+    HostBuf hflags;                 // the prefix comparison's flags, read after the round's one wait
     std::vector<int32_t> host_tok;
     // statistics of the last chunk
     int64_t st_reused = 0, st_prefill_len = 0, st_delta = 0, st_steps_total = 0, st_forwards = 0;
@@ -154,6 +155,7 @@ extern "C" void qasr_hip_stream_free(qasr_stream *s) {
                       &s->enc.melsc, &s->enc.out, &s->enc_all,
                       &s->toks, &s->flags})
         dbuf_release(*b);
+    hbuf_release(s->hflags);
     delete s;
 }
 
@@ -323,6 +325,7 @@ struct ChunkPlan {
     size_t req0 = 0, nreq = 0;
     int64_t full_end = 0;          // samples covered by complete windows
     bool tail_req = false;         // the partial tail is re-encoded (the last request)
+    int64_t cmp = 0;               // prompt rows compared with the previous prefill (flags in hflags)
 };
 
 // greedy decode of up to max_new tokens after the prefill of prefill_len rows
@@ -477,19 +480,31 @@ static int chunk_build(qasr_stream *s, const std::vector<EncReq> &reqs, const Pr
                                   s->enc_all.as<float>(), (int)enc_len, (int)(n_suffix + pl.n_prefix_tokens), (int)H, st),
               "stream prompt");
 
-    // ---- prefill with common-prefix reuse ----
+    // ---- the rows equal to the previous prefill's (read back after the
+    // caller's wait, chunk_reuse) ----
+    pl.cmp = 0;
+    if (s->prev_prefill_len > 0) {
+        pl.cmp = std::min(pl.prefill_len, s->prev_prefill_len);
+        TRY(dbuf_ensure(s->flags, sizeof(int) * pl.cmp));
+        TRY(hbuf_ensure(s->hflags, sizeof(int) * pl.cmp));
+        LAUNCHCHK(launch_row_diff(s->embeds.as<float>(), s->prev_embeds.as<float>(), pl.cmp, H, s->flags.as<int>(),
+                                  st),
+                  "stream row diff");
+        HIPCHK(hipMemcpyAsync(s->hflags.p, s->flags.p, sizeof(int) * pl.cmp, hipMemcpyDeviceToHost, st));
+    }
+    return QASR_OK;
+}
+
+// Step 3 of a chunk, after the wait for chunk_build's work: the prefill with
+// common-prefix reuse (transcribe.rs:1092-1115) into `tgt`: the leading rows
+// equal to the previous prefill keep their KV entries.
+static int chunk_reuse(qasr_stream *s, const PrefillTarget &tgt, ChunkPlan &pl) {
+    qasr_decoder *d = s->d;
+    const int64_t H = d->c.hidden;
     const int64_t prefill_len = pl.prefill_len;
     int64_t reused = 0;
-    if (s->prev_prefill_len > 0) {
-        const int64_t cmp = std::min(prefill_len, s->prev_prefill_len);
-        TRY(dbuf_ensure(s->flags, sizeof(int) * cmp));
-        LAUNCHCHK(launch_row_diff(s->embeds.as<float>(), s->prev_embeds.as<float>(), cmp, H, s->flags.as<int>(), st),
-                  "stream row diff");
-        std::vector<int> fl(cmp);
-        HIPCHK(hipMemcpyAsync(fl.data(), s->flags.p, sizeof(int) * cmp, hipMemcpyDeviceToHost, st));
-        HIPCHK(hipStreamSynchronize(st));
-        while (reused < cmp && !fl[reused]) reused++;
-    }
+    const int *fl = s->hflags.as<int>();
+    while (reused < pl.cmp && !fl[reused]) reused++;
     const int64_t delta = prefill_len - reused;
     pl.rows = s->embeds.as<float>() + reused * H;
     pl.reused = reused;
@@ -583,6 +598,10 @@ extern "C" int qasr_hip_stream_push(qasr_stream *s, const float *samples, int64_
         chunk_advance(s, n_samples, finalize != 0, samples, pl, reqs);
         TRY(encode_requests(s->d, s->e, reqs, s->enc));
         TRY(chunk_build(s, reqs, PrefillTarget{}, pl, &skip));
+        if (!skip) {
+            HIPCHK(hipStreamSynchronize(s->d->h->stream));
+            TRY(chunk_reuse(s, PrefillTarget{}, pl));
+        }
         if (skip) {
             emitted.clear();
             break;
@@ -613,11 +632,11 @@ struct qasr_stream_batch {
     qasr_decoder *d = nullptr;
     qasr_batch *b = nullptr;
     std::vector<qasr_stream *> s;
-    // phase boundaries of each round on the library stream (prepare: encoder
-    // windows, prompt rows and prefix comparison; prefill; decode), summed
-    // over the rounds of the last push
-    hipEvent_t ev[4] = {};
-    double phase_ms[3] = {};
+    // phase boundaries of each round on the library stream (encoder; prompt
+    // rows and prefix comparison; prefill; decode), summed over the rounds of
+    // the last push
+    hipEvent_t ev[5] = {};
+    double phase_ms[4] = {};
     EncScratch enc;                 // one encoder pass over every stream's inputs of a round
 };
 
@@ -736,6 +755,7 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
             cand.push_back(i);
         }
         TRY(encode_requests(g->d, g->s.empty() ? nullptr : g->s[0]->e, reqs, g->enc));
+        HIPCHK(hipEventRecord(g->ev[1], st));
         for (int i : cand) {
             bool skip = false;
             TRY(chunk_build(g->s[i], reqs, PrefillTarget{g->b, i, true}, pl[i], &skip));
@@ -747,7 +767,9 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
             act.push_back(i);
         }
         if (act.empty()) break;
-        HIPCHK(hipEventRecord(g->ev[1], st));
+        HIPCHK(hipStreamSynchronize(st));      // every stream's prefix comparison
+        for (int i : act) TRY(chunk_reuse(g->s[i], PrefillTarget{g->b, i, true}, pl[i]));
+        HIPCHK(hipEventRecord(g->ev[2], st));
         // one prefill of every stream's changed prompt rows (GEMMs over all of
         // them), each into its own slot
         {
@@ -763,11 +785,11 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
             TRY(batch_prefill_segments(g->b, (int)act.size(), slots.data(), rows.data(), starts.data(),
                                        counts.data()));
         }
-        HIPCHK(hipEventRecord(g->ev[2], st));
-        TRY(group_decode(g, act, pl, chunks));
         HIPCHK(hipEventRecord(g->ev[3], st));
-        HIPCHK(hipEventSynchronize(g->ev[3]));
-        for (int k = 0; k < 3; k++) {
+        TRY(group_decode(g, act, pl, chunks));
+        HIPCHK(hipEventRecord(g->ev[4], st));
+        HIPCHK(hipEventSynchronize(g->ev[4]));
+        for (int k = 0; k < 4; k++) {
             float ms = 0.0f;
             HIPCHK(hipEventElapsedTime(&ms, g->ev[k], g->ev[k + 1]));
             g->phase_ms[k] += ms;
@@ -790,7 +812,7 @@ extern "C" int qasr_hip_stream_batch_push(qasr_stream_batch *g, const float *con
 
 extern "C" int qasr_hip_stream_batch_times(const qasr_stream_batch *g, double *ms) {
     if (!g || !ms) return qasr_fail(QASR_ERR_INVALID, "stream_batch_times: null argument");
-    std::copy(g->phase_ms, g->phase_ms + 3, ms);
+    std::copy(g->phase_ms, g->phase_ms + 4, ms);
     return QASR_OK;
 }
 

@@ -585,8 +585,8 @@ class StreamBatch:
         return _MemberStream(self, lib().qasr_hip_stream_batch_stream(self.g, int(i)))
 
     def times(self):
-        """ms of the last push's phases: (preparation, prefill, decode)."""
-        ms = np.zeros(3, np.float64)
+        """ms of the last push's phases: (encoder, prompt rows + prefix comparison, prefill, decode)."""
+        ms = np.zeros(4, np.float64)
         check(lib().qasr_hip_stream_batch_times(self.g, ms.ctypes.data_as(P)))
         return tuple(float(v) for v in ms)
 
