@@ -939,6 +939,59 @@ __global__ __launch_bounds__(256) void k_prefill_qkv_post(PrefillPostArgs a) {
     }
 }
 
+// k_prefill_qkv_post over several sequences: a wave's row picks its
+// sequence's position, KV bases and head stride (compile-time table indices).
+__global__ __launch_bounds__(256) void k_prefill_qkv_post_seqs(PrefillPostSeqArgs sa) {
+    constexpr int D = 128;
+    const PrefillPostArgs &a = sa.base;
+    const int lane = threadIdx.x & 63;
+    const int per_row = a.Hq + a.Hkv;
+    const int64_t item = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (item >= sa.row[sa.n] * per_row) return;
+    const int64_t s = item / per_row;
+    const int h = (int)(item % per_row);
+    int64_t r0 = sa.row[0], start = sa.start[0], hs = sa.head_stride[0];
+    float *kc = sa.kc[0], *vc = sa.vc[0];
+#pragma unroll
+    for (int u = 1; u < QASR_ATTN_MAX_SEQ; u++)
+        if (u < sa.n && s >= sa.row[u]) {
+            r0 = sa.row[u];
+            start = sa.start[u];
+            hs = sa.head_stride[u];
+            kc = sa.kc[u];
+            vc = sa.vc[u];
+        }
+    const int64_t pos = start + (s - r0);
+    float *row = a.qkv + s * a.row_stride;
+    const float *c = a.cos_t + pos * D, *sn = a.sin_t + pos * D;
+    if (h < a.Hq) {
+        float *v = row + h * D;
+        float x1 = v[lane], x2 = v[lane + 64];
+        head_norm_rope2(x1, x2, a.q_norm, c, sn, a.eps, true, true);
+        v[lane] = x1;
+        v[lane + 64] = x2;
+    } else {
+        const int kh = h - a.Hq;
+        const float *kp = row + a.Hq * D + kh * D, *vp = row + (a.Hq + a.Hkv) * D + kh * D;
+        float x1 = kp[lane], x2 = kp[lane + 64];
+        const float v1 = vp[lane], v2 = vp[lane + 64];
+        head_norm_rope2(x1, x2, a.k_norm, c, sn, a.eps, true, true);
+        const int64_t dst = kh * hs + pos * D;
+        kc[dst + lane] = x1;
+        kc[dst + lane + 64] = x2;
+        vc[dst + lane] = v1;
+        vc[dst + lane + 64] = v2;
+    }
+}
+
+hipError_t launch_prefill_qkv_post_seqs(const PrefillPostSeqArgs &a, hipStream_t st) {
+    if (a.n < 1 || a.n > QASR_ATTN_MAX_SEQ) return hipErrorInvalidValue;
+    const int64_t items = a.row[a.n] * (a.base.Hq + a.base.Hkv);
+    if (items <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_prefill_qkv_post_seqs, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_prefill_qkv_post(const PrefillPostArgs &a, hipStream_t st) {
     const int64_t items = a.S * (a.Hq + a.Hkv);
     if (items <= 0) return hipSuccess;

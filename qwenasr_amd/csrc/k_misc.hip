@@ -610,8 +610,9 @@ __global__ __launch_bounds__(256) void k_attn_rows(AttnRowsArgs a) {
 // i).  The O rows a lane accumulates are queries 4 (l / 16) + j, whose
 // rescale factors come from the lanes owning those queries.
 // ---------------------------------------------------------------------------
+// One block's work: query rows [q0, q0 + 16) of the KV head (pair) blockIdx.x.
 template <int HD, int G, int NW>
-__global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
+__device__ __forceinline__ void attn_mfma_block(const AttnRowsArgs &a, int q0) {
     constexpr int KS = NW / G, CH = 16 * KS, NST = HD / 4, NT = HD / 16, LD = HD + 4;
     constexpr int NTH = NW * 64, SV = CH * (HD / 4) / NTH;   // float4 of K (and of V) staged per thread
     static_assert(CH * (HD / 4) % NTH == 0, "staging");
@@ -623,8 +624,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = wid / KS, ks = wid % KS;
-    // causal: tiles in reverse, so that the blocks with the most keys start first
-    const int kvh = blockIdx.x, q0 = (a.window > 0 ? blockIdx.y : gridDim.y - 1 - blockIdx.y) * 16;
+    const int kvh = blockIdx.x;
     const int h = kvh * G + g;
     const int lq = lane & 15, lg = lane >> 4;
     // key range of this lane's query (for the S^T masks) and of the block
@@ -773,6 +773,64 @@ __global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
         }
         a.out[(int64_t)q * a.o_rs + (kvh * G + gg) * HD + d] = L > 0.0f ? __fdiv_rn(O, L) : 0.0f;
     }
+}
+
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attn_mfma(AttnRowsArgs a) {
+    // causal: tiles in reverse, so that the blocks with the most keys start first
+    attn_mfma_block<HD, G, NW>(a, (a.window > 0 ? blockIdx.y : gridDim.y - 1 - blockIdx.y) * 16);
+}
+
+// Causal attention of several sequences in one launch (the multi-sequence
+// prefill): block row y belongs to sequence j (blk[j] <= y < blk[j + 1]) and
+// is that sequence's row block of a call of its own (the same q0, in the
+// same reverse order), with the sequence's query / output rows, KV cache,
+// key count and query offset.
+template <int HD, int G, int NW>
+__global__ __launch_bounds__(NW * 64) void k_attn_mfma_seqs(AttnSeqArgs s) {
+    const int y = blockIdx.y;
+    int b1 = s.blk[1];
+    int64_t row = s.row[0];
+    const float *k = s.k[0], *v = s.v[0];
+    int nq = s.n_q[0], nk = s.n_k[0], qo = s.q_offset[0];
+#pragma unroll
+    for (int u = 1; u < QASR_ATTN_MAX_SEQ; u++)
+        if (u < s.n && y >= s.blk[u]) {
+            b1 = s.blk[u + 1];
+            row = s.row[u];
+            k = s.k[u];
+            v = s.v[u];
+            nq = s.n_q[u];
+            nk = s.n_k[u];
+            qo = s.q_offset[u];
+        }
+    AttnRowsArgs a = s.base;
+    a.q += row * a.q_rs;
+    a.out += row * a.o_rs;
+    a.k = k;
+    a.v = v;
+    a.n_q = nq;
+    a.n_k = nk;
+    a.q_offset = qo;
+    attn_mfma_block<HD, G, NW>(a, (b1 - 1 - y) * 16);
+}
+
+hipError_t launch_attn_rows_seqs(const AttnSeqArgs &s0, int n_kv_heads, int head_dim, hipStream_t st) {
+    const AttnRowsArgs &a = s0.base;
+    if (s0.n < 1 || s0.n > QASR_ATTN_MAX_SEQ || a.window > 0 || head_dim != 128 || a.G != 2)
+        return hipErrorInvalidValue;
+    AttnSeqArgs s = s0;
+    s.base.kv_div = 2;
+    s.blk[0] = 0;
+    for (int j = 0; j < s.n; j++) {
+        if (s.n_q[j] <= 0) return hipErrorInvalidValue;
+        s.blk[j + 1] = s.blk[j] + (s.n_q[j] + 15) / 16;
+    }
+    // the 128-dim decoder heads' form of launch_attn_rows: one query head per
+    // block, its 8 waves 8 key splits (KV head x / 2)
+    const dim3 grid(n_kv_heads * 2, s.blk[s.n]);
+    hipLaunchKernelGGL((k_attn_mfma_seqs<128, 1, 8>), grid, dim3(512), 0, st, s);
+    return hipGetLastError();
 }
 
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st) {

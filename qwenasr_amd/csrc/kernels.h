@@ -216,6 +216,21 @@ struct AttnRowsArgs {
     int seg_lo[QASR_ATTN_MAX_SEG], seg_hi[QASR_ATTN_MAX_SEG];
 };
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st);
+// Causal attention of n sequences (<= QASR_ATTN_MAX_SEQ) in one launch: base
+// holds the shared fields (strides, G, scale; q and out at row 0), sequence j
+// its first query / output row, KV cache bases, query rows, keys and query
+// offset.  Each sequence's rows get the bits of a launch_attn_rows call of its
+// own.  128-dim heads with G = 2 (the decoder) only.
+#define QASR_ATTN_MAX_SEQ 32
+struct AttnSeqArgs {
+    AttnRowsArgs base;
+    int n;
+    int blk[QASR_ATTN_MAX_SEQ + 1];        // set by the launcher
+    int64_t row[QASR_ATTN_MAX_SEQ];
+    const float *k[QASR_ATTN_MAX_SEQ], *v[QASR_ATTN_MAX_SEQ];
+    int n_q[QASR_ATTN_MAX_SEQ], n_k[QASR_ATTN_MAX_SEQ], q_offset[QASR_ATTN_MAX_SEQ];
+};
+hipError_t launch_attn_rows_seqs(const AttnSeqArgs &s, int n_kv_heads, int head_dim, hipStream_t st);
 hipError_t launch_layer_norm_rows(float *out, const float *x, const float *w, const float *b, int64_t seq,
                                   int hidden, float eps, hipStream_t st);
 hipError_t launch_swiglu_rows(float *out, const float *gu, int64_t seq, int inter, hipStream_t st);
@@ -243,6 +258,18 @@ struct PrefillPostArgs {
     float eps;
 };
 hipError_t launch_prefill_qkv_post(const PrefillPostArgs &a, hipStream_t st);
+// The same over n sequences of consecutive rows (<= QASR_ATTN_MAX_SEQ): base
+// holds qkv (row 0), row_stride, heads, norms, eps and cos_t / sin_t at
+// position 0; sequence j its first row, position, KV bases (this layer) and
+// head stride.
+struct PrefillPostSeqArgs {
+    PrefillPostArgs base;
+    int n;
+    int64_t row[QASR_ATTN_MAX_SEQ + 1];    // row[n] = all rows
+    int64_t start[QASR_ATTN_MAX_SEQ], head_stride[QASR_ATTN_MAX_SEQ];
+    float *kc[QASR_ATTN_MAX_SEQ], *vc[QASR_ATTN_MAX_SEQ];
+};
+hipError_t launch_prefill_qkv_post_seqs(const PrefillPostSeqArgs &a, hipStream_t st);
 hipError_t launch_row_diff(const float *a, const float *b, int64_t rows, int64_t H, int *flags, hipStream_t st);
 // idx[r] = lowest column of the maximum of row r's non-NaN values (0 when column 0 is NaN)
 hipError_t launch_argmax_f32_rows(const float *x, int64_t ld, int64_t rows, int64_t cols, int32_t *idx,

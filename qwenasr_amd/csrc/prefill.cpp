@@ -81,6 +81,23 @@ int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg)
     const int I = c.intermediate, nqkv = qd + 2 * kvd;
     const int M = (int)S;
     const float scale = 1.0f / sqrtf((float)hd);
+    // one launch for every sequence's q/k post-processing and attention when
+    // there are several (at most 32, the decoder's 128-dim heads with two
+    // query heads per KV head, one head stride: the attention reads it from
+    // the shared arguments)
+    int n_live = 0;
+    int64_t segs_head_stride = -1;
+    bool same_stride = true;
+    for (int i = 0; i < n_seg; i++)
+        if (segs[i].n > 0) {
+            n_live++;
+            if (segs_head_stride < 0) segs_head_stride = segs[i].head_stride;
+            same_stride = same_stride && segs[i].head_stride == segs_head_stride && segs[i].head_stride % 4 == 0 &&
+                          segs[i].layer_elems % 4 == 0 && (uintptr_t)segs[i].kc % 16 == 0 &&
+                          (uintptr_t)segs[i].vc % 16 == 0;   // the MFMA form's float4 K/V loads
+        }
+    const bool multi = n_live > 1 && n_live <= QASR_ATTN_MAX_SEQ && hd == 128 && c.n_heads == 2 * c.n_kv_heads &&
+                       same_stride;
     {
         int64_t off = 0;
         for (int i = 0; i < n_seg; i++) {
@@ -94,8 +111,44 @@ int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg)
         const DecLayerDev &L = d->L[l];
         LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.in_norm, S, H, c.eps, st), "prefill rms_norm");
         TRY(gemm(d, p.xn, H, L.bqkv, H, p.qkv, nqkv, M, nqkv, H, EPI_NONE));
+        if (multi) {
+            // every sequence's q/k norm, RoPE and KV write, then its causal
+            // attention, one launch each (each sequence's rows get the bits of
+            // its own launches)
+            PrefillPostSeqArgs pp{};
+            pp.base.qkv = p.qkv; pp.base.row_stride = nqkv; pp.base.Hq = c.n_heads; pp.base.Hkv = c.n_kv_heads;
+            pp.base.q_norm = L.q_norm; pp.base.k_norm = L.k_norm; pp.base.cos_t = d->rc; pp.base.sin_t = d->rs;
+            pp.base.eps = c.eps;
+            AttnSeqArgs as{};
+            as.base.q = p.qkv; as.base.q_rs = nqkv; as.base.k_hs = 0; as.base.k_rs = hd;
+            as.base.out = p.att; as.base.o_rs = qd;
+            as.base.G = c.n_heads / c.n_kv_heads; as.base.window = 0; as.base.scale = scale;
+            int64_t off = 0;
+            for (int i = 0; i < n_seg; i++) {
+                const PrefillSeg &g = segs[i];
+                if (g.n == 0) continue;
+                const int j = pp.n++;
+                pp.row[j] = off;
+                pp.start[j] = g.start;
+                pp.head_stride[j] = g.head_stride;
+                pp.kc[j] = g.kc + l * g.layer_elems;
+                pp.vc[j] = g.vc + l * g.layer_elems;
+                as.row[j] = off;
+                as.k[j] = pp.kc[j];
+                as.v[j] = pp.vc[j];
+                as.n_q[j] = (int)g.n;
+                as.n_k[j] = (int)(g.start + g.n);
+                as.q_offset[j] = (int)g.start;
+                off += g.n;
+            }
+            pp.row[pp.n] = off;
+            as.n = pp.n;
+            as.base.k_hs = segs_head_stride;
+            LAUNCHCHK(launch_prefill_qkv_post_seqs(pp, st), "prefill q/k norm, rope and kv write");
+            LAUNCHCHK(launch_attn_rows_seqs(as, c.n_kv_heads, hd, st), "prefill attention");
+        }
         int64_t off = 0;
-        for (int i = 0; i < n_seg; i++) {
+        for (int i = 0; i < n_seg && !multi; i++) {
             const PrefillSeg &g = segs[i];
             if (g.n == 0) continue;
             float *kc = g.kc + l * g.layer_elems;
