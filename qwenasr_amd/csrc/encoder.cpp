@@ -438,6 +438,48 @@ int mel_dev(qasr_encoder *e, const float *x, int64_t ns, float *mel, float *scra
 
 size_t mel_scratch_floats(int64_t nf) { return (size_t)nf * (400 + 3 * 201) + (size_t)(128 * nf / 256 + 2); }
 
+// mel_spectrogram of n device signals at once: the frames, the two DFT GEMMs,
+// the power and the filterbank GEMM over all their frames together (each f32
+// GEMM element is a sum over K in a fixed order, whatever the frame count),
+// then each mel copied out to mel[j] [128][frames_j] and log-normalised with
+// its own maximum.  scratch: mel_multi_scratch_floats(total frames, largest).
+int mel_dev_multi(qasr_encoder *e, int n, const float *const *x, const int64_t *ns, float *const *mel, float *scratch) {
+    hipStream_t st = e->h->stream;
+    int64_t tot = 0;
+    for (int j = 0; j < n; j++) tot += mel_frames_for(ns[j]);
+    float *fr = scratch, *re = fr + tot * 400, *im = re + tot * 201, *pT = im + tot * 201, *all = pT + tot * 201;
+    float *bmax = all + tot * 128;
+    int64_t off = 0;
+    for (int j = 0; j < n; j++) {
+        const int nf = (int)mel_frames_for(ns[j]);
+        LAUNCHCHK(launch_mel_frames(fr + off * 400, x[j], ns[j], e->window, nf, st), "mel frames");
+        off += nf;
+    }
+    GemmArgs g{};
+    g.M = 201; g.N = (int)tot; g.K = 400;
+    g.A = e->dft_cos; g.lda = 400; g.B = fr; g.ldb = 400; g.C = re; g.ldc = tot;
+    LAUNCHCHK(launch_gemm_f32(g, st), "mel dft");
+    g.A = e->dft_sin; g.C = im;
+    LAUNCHCHK(launch_gemm_f32(g, st), "mel dft");
+    LAUNCHCHK(launch_mel_power(pT, re, im, (int)tot, st), "mel power");
+    g.M = 128; g.N = (int)tot; g.K = 201;
+    g.A = e->filters; g.lda = 201; g.B = pT; g.ldb = 201; g.C = all; g.ldc = tot;
+    LAUNCHCHK(launch_gemm_f32(g, st), "mel filterbank");
+    off = 0;
+    for (int j = 0; j < n; j++) {
+        const int64_t nf = mel_frames_for(ns[j]);
+        HIPCHK(hipMemcpy2DAsync(mel[j], sizeof(float) * nf, all + off, sizeof(float) * tot, sizeof(float) * nf, 128,
+                                hipMemcpyDeviceToDevice, st));
+        LAUNCHCHK(launch_mel_log_norm(mel[j], 128 * nf, bmax, st), "mel log");
+        off += nf;
+    }
+    return QASR_OK;
+}
+
+size_t mel_multi_scratch_floats(int64_t total_frames, int64_t max_frames) {
+    return (size_t)total_frames * (400 + 3 * 201 + 128) + (size_t)(128 * max_frames / 256 + 2);
+}
+
 extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, float *mel_out, int64_t *frames) {
     if (!e) return qasr_fail(QASR_ERR_INVALID, "encoder is null");
     CHECK_H(e->h);

@@ -19,3 +19,7 @@ int encoder_forward_multi(qasr_encoder *e, int n, const float *const *mels, cons
 int64_t encoder_tokens(const qasr_encoder *e, int64_t frames);
 int64_t encoder_output_dim(const qasr_encoder *e);
 qasr_hip *encoder_handle(const qasr_encoder *e);
+// mel_spectrogram of n device signals with their DFT and filterbank GEMMs
+// shared; mel[j] [128][frames_j] each
+int mel_dev_multi(qasr_encoder *e, int n, const float *const *x, const int64_t *ns, float *const *mel, float *scratch);
+size_t mel_multi_scratch_floats(int64_t total_frames, int64_t max_frames);

@@ -219,22 +219,26 @@ static int encode_requests(qasr_decoder *d, qasr_encoder *e, std::vector<EncReq>
     if (live.empty()) return QASR_OK;
     TRY(dbuf_ensure(sc.audio, sizeof(float) * tot_s));
     TRY(dbuf_ensure(sc.mel, sizeof(float) * 128 * tot_f));
-    TRY(dbuf_ensure(sc.melsc, sizeof(float) * mel_scratch_floats(max_f)));
-    std::vector<const float *> mels;
-    std::vector<int64_t> frames;
+    TRY(dbuf_ensure(sc.melsc, sizeof(float) * mel_multi_scratch_floats(tot_f, max_f)));
+    std::vector<const float *> mels, xs;
+    std::vector<float *> mels_w;
+    std::vector<int64_t> frames, lens;
     int64_t so = 0, fo = 0, tot_t = 0;
     for (size_t k : live) {
         const EncReq &r = reqs[k];
         float *xa = sc.audio.as<float>() + so, *m = sc.mel.as<float>() + 128 * fo;
         HIPCHK(hipMemcpyAsync(xa, r.x, sizeof(float) * r.ns, hipMemcpyHostToDevice, st));
-        TRY(mel_dev(e, xa, r.ns, m, sc.melsc.as<float>()));
         const int64_t nf = mel_frames_for(r.ns);
+        xs.push_back(xa);
+        lens.push_back(r.ns);
         mels.push_back(m);
+        mels_w.push_back(m);
         frames.push_back(nf);
         tot_t += encoder_tokens(e, nf);
         so += r.ns;
         fo += nf;
     }
+    TRY(mel_dev_multi(e, (int)live.size(), xs.data(), lens.data(), mels_w.data(), sc.melsc.as<float>()));
     std::vector<int64_t> tok(live.size());
     if (live.size() == 1) {
         // one input: its rows straight into its destination
