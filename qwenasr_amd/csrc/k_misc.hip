@@ -820,16 +820,18 @@ hipError_t launch_attn_rows_seqs(const AttnSeqArgs &s0, int n_kv_heads, int head
     if (s0.n < 1 || s0.n > QASR_ATTN_MAX_SEQ || a.window > 0 || head_dim != 128 || a.G != 2)
         return hipErrorInvalidValue;
     AttnSeqArgs s = s0;
-    s.base.kv_div = 2;
+    s.base.kv_div = 1;
     s.blk[0] = 0;
     for (int j = 0; j < s.n; j++) {
         if (s.n_q[j] <= 0) return hipErrorInvalidValue;
         s.blk[j + 1] = s.blk[j] + (s.n_q[j] + 15) / 16;
     }
-    // the 128-dim decoder heads' form of launch_attn_rows: one query head per
-    // block, its 8 waves 8 key splits (KV head x / 2)
-    const dim3 grid(n_kv_heads * 2, s.blk[s.n]);
-    hipLaunchKernelGGL((k_attn_mfma_seqs<128, 1, 8>), grid, dim3(512), 0, st, s);
+    // both query heads of a KV head in one block of 16 waves, 8 key splits
+    // each: every head meets the key partition of launch_attn_rows' form for
+    // these heads (one head per 8-wave block, 8 splits; the same bits), and
+    // the block stages each K/V chunk once for the two heads
+    const dim3 grid(n_kv_heads, s.blk[s.n]);
+    hipLaunchKernelGGL((k_attn_mfma_seqs<128, 2, 16>), grid, dim3(1024), 0, st, s);
     return hipGetLastError();
 }
 
