@@ -433,20 +433,24 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
 
 // ---------------------------------------------------------------------------
 // GQA decode attention of one decode step (the DEC = 1 case above, same
-// inputs, partial format and numerics contract), with a layout that shortens
-// each wave's dependent chain.  Lane l owns dims 2l and 2l + 1 of every
-// position: a group's 8 K rows and 8 V rows are 16 loads of 8 (f32) or 4
-// (bf16) bytes per lane, each instruction covering whole rows.  Per group a
-// lane forms 2-term partial dots for the 16 (query head, position) scores,
-// and one reduce-scatter over the wave (permlane32 / permlane16 swaps, then
-// DPP) leaves every lane one finished score: lanes are (head, position)
-// slots, replicated 4 times.  The softmax over a head's 8 x GPW positions is
-// 3 swaps; the probabilities are read back with readlane (scalar operands),
-// and since each lane already owns its dims, P V needs no cross-lane sum.
-// The RoPE pair (d, d + 64) sits in lanes l and l + 32 (one permlane32 swap).
-// Blocks: (KV head, split) with the KV head fastest, so with 8 KV heads the
-// splits of one head land on one XCD (blocks go round-robin over the 8
-// XCDs) and their partial stores merge in that L2.
+// inputs, partial format and numerics contract), laid out for a short
+// dependent chain per wave.  A block serves ONE query head and one context
+// split: grid = Hkv x 2 x n_split with the KV head fastest, so the two query
+// heads of a KV head and all its splits go to one XCD (blocks go round-robin
+// over the 8 XCDs) and read the same K/V rows through that XCD's L2, and twice
+// as many CUs share the work as with both query heads in one block.  Lane l
+// owns dims 2l and 2l + 1 of every position: a group's 8 K rows and 8 V rows
+// are 16 loads of 8 (f32) or 4 (bf16) bytes per lane, each instruction
+// covering whole rows.  Per group a lane forms 2-term partial dots for the 8
+// positions, and one reduce-scatter over the wave (a permlane32 swap, a
+// permlane16 swap and a row_ror:8 DPP step, then three DPP sums) leaves every
+// lane one finished score: lanes are position slots, replicated 8 times.  The
+// softmax over the wave's 8 x GPW positions takes 3 cross-lane steps; the
+// probabilities go through LDS (8 floats per group, two 16-byte reads per
+// lane), and since each lane already owns its dims, P V needs no cross-lane
+// sum and no branch (positions past the context have probability 0 and their
+// V operand is replaced by 0).  The RoPE pair (d, d + 64) sits in lanes l and
+// l + 32 (one permlane32 swap).
 // ---------------------------------------------------------------------------
 template <typename T> struct KvPair;
 template <> struct KvPair<float> {
@@ -516,19 +520,24 @@ __device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float
 
 // A wave holds its whole share of the block's run, groups g0 + wid + NW i
 // for i < GPW (the host launches it only for runs of at most NW GPW groups):
-// every group's scores, one max per head over all of them, then P V.  Rows
-// the run leaves out are masked (scores -inf, weights 0, P V terms skipped).
+// every group's scores, one max over all of them, then P V.  Rows the run
+// leaves out are masked (scores -inf, probabilities 0, V operands 0).  The
+// block of query head 0 of the KV head that holds the position writes the
+// new K/V row; the other query head's block forms the same values for its
+// own score and P V term.
 template <typename KVT, int NW, int GPW>
 __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
     constexpr int D = 128, G = 2;
     using Kp = KvPair<KVT>;
-    __shared__ float wm[NW][G], wl[NW][G];
-    __shared__ float wacc[NW][G][D];
+    __shared__ float wm[NW], wl[NW];
+    __shared__ float wacc[NW][D];
+    __shared__ __attribute__((aligned(16))) float pw[NW][GPW][8];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int n_split = a.n_split;
-    const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
-    const int kvh = blockIdx.x % Hkv, split = blockIdx.x / Hkv;
+    const int Hkv = gridDim.x / (G * n_split), Hq = Hkv * G;
+    const int kvh = blockIdx.x % Hkv, gq = (blockIdx.x / Hkv) % G, split = blockIdx.x / (G * Hkv);
+    const int h = kvh * G + gq;
     KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
     KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
     const float *qkv = a.qkv;
@@ -536,30 +545,35 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
     const int max_rows = (int)(a.head_stride / D);
     const int gpb = a.gpb, g0 = split * gpb, g1s = g0 + gpb;
 
-    // ---- every load before the first wait: the block's static partition
-    // needs no device state, so the K/V rows go out before the position
-    // arrives (rows past the cache read row 0; everything past the context is
-    // masked once the position is known)
+    // ---- every load before the first wait, the previous kernel's outputs
+    // (q, the new k/v, the position) first, so that waiting for them does not
+    // wait for the K/V rows (loads complete in issue order); the static
+    // partition needs no device state, so the K rows, then the V rows, go out
+    // before the position arrives (rows past the cache read row 0; everything
+    // past the context is masked once the position is known)
+    float2 q = reinterpret_cast<const float2 *>(qkv + h * D)[lane];
+    float2 kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
+    float2 vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
+    const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
+    const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
+    const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
+    const float2 sn = reinterpret_cast<const float2 *>(a.rope_cur + D)[lane];
+    const int pos = a.state[1];
     Kp kr[GPW][8], vr[GPW][8];
 #pragma unroll
     for (int i = 0; i < GPW; i++)
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             const int j = 8 * (g0 + wid + NW * i) + p;
-            const int r = j < max_rows ? j : 0;
-            kr[i][p].load(kc + (int64_t)r * D, lane);
-            vr[i][p].load(vc + (int64_t)r * D, lane);
+            kr[i][p].load(kc + (int64_t)(j < max_rows ? j : 0) * D, lane);
         }
-    float2 q[G];
 #pragma unroll
-    for (int g = 0; g < G; g++) q[g] = reinterpret_cast<const float2 *>(qkv + (kvh * G + g) * D)[lane];
-    const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
-    const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
-    float2 kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
-    float2 vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
-    const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
-    const float2 sn = reinterpret_cast<const float2 *>(a.rope_cur + D)[lane];
-    const int pos = a.state[1];
+    for (int i = 0; i < GPW; i++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const int j = 8 * (g0 + wid + NW * i) + p;
+            vr[i][p].load(vc + (int64_t)(j < max_rows ? j : 0) * D, lane);
+        }
     __builtin_amdgcn_sched_barrier(0);
 
     const int L = pos + 1;
@@ -567,24 +581,16 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
     const int j1 = min(L, 8 * g1);
     const bool own_pos = 8 * g0 <= pos && pos < j1;
 
-    // lane -> (head, position) slot of the reduce-scatter; the swap halves
-    // are told apart by running the same swaps on indicators
-    const float hsel = swap32_add(0.0f, 1.0f);
-    const float psel = swap16_add(0.0f, 1.0f);
-    const int bit3 = (lane >> 3) & 1, bit2 = (lane >> 2) & 1;
-    const int my_h = hsel > 1.0f ? 1 : 0;
-    const int my_p = (psel > 1.0f ? 4 : 0) + 2 * bit3 + bit2;
-    // the lane holding each (head, position) slot: any lane with those
-    // selectors (worked out while the loads are in flight)
-    int src[G][8];
-#pragma unroll
-    for (int g = 0; g < G; g++)
-#pragma unroll
-        for (int p = 0; p < 8; p++) src[g][p] = (int)__builtin_ctzll(__ballot(my_h == g && my_p == p));
+    // lane -> position slot of the reduce-scatter: bit 2 from the swap32
+    // half, bit 1 from the swap16 half (told apart by running the same swaps
+    // on indicators), bit 0 = lane bit 3 (row_ror:8)
+    const float s32 = swap32_add(0.0f, 1.0f);
+    const float s16 = swap16_add(0.0f, 1.0f);
+    const int bit3 = (lane >> 3) & 1;
+    const int my_p = (s32 > 1.0f ? 4 : 0) + (s16 > 1.0f ? 2 : 0) + bit3;
 
     // ---- q: per-head RMSNorm + RoPE; the new K/V row ------------------------
-#pragma unroll
-    for (int g = 0; g < G; g++) q[g] = norm_rope2(q[g], qn, cs, sn, a.eps);
+    q = norm_rope2(q, qn, cs, sn, a.eps);
     if (own_pos) {
         kn = norm_rope2(kn, knw, cs, sn, a.eps);
         Kp kp, vp;
@@ -592,7 +598,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
         vp.set(vn.x, vn.y);
         kn = make_float2(kp.x(), kp.y());
         vn = make_float2(vp.x(), vp.y());
-        if (wid == 0) {
+        if (wid == 0 && gq == 0) {
             Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
             Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
         }
@@ -603,92 +609,91 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < GPW; i++) {
         const int jb = 8 * (g0 + wid + NW * i);
-        float part2[G][8];
+        float v8[8];
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             float kx = kr[i][p].x(), ky = kr[i][p].y();
             if (own_pos && jb + p == pos) { kx = kn.x; ky = kn.y; }
-#pragma unroll
-            for (int g = 0; g < G; g++) part2[g][p] = fmaf(q[g].y, ky, __fmul_rn(q[g].x, kx));
+            v8[p] = fmaf(q.y, ky, __fmul_rn(q.x, kx));
         }
-        float r1[8];
+        float r1[4];
 #pragma unroll
-        for (int p = 0; p < 8; p++) r1[p] = swap32_add(part2[0][p], part2[1][p]);
-        float r2[4];
+        for (int k = 0; k < 4; k++) r1[k] = swap32_add(v8[k], v8[k + 4]);
+        float r2[2];
 #pragma unroll
-        for (int k = 0; k < 4; k++) r2[k] = swap16_add(r1[k], r1[k + 4]);
-        float r3[2];
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const float keep = bit3 ? r2[2 + k] : r2[k], send = bit3 ? r2[k] : r2[2 + k];
-            r3[k] = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_ROR8>(send));
-        }
-        float r4;
+        for (int k = 0; k < 2; k++) r2[k] = swap16_add(r1[k], r1[k + 2]);
+        float r3;
         {
-            const float keep = bit2 ? r3[1] : r3[0], send = bit2 ? r3[0] : r3[1];
-            r4 = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(send));
+            const float keep = bit3 ? r2[1] : r2[0], send = bit3 ? r2[0] : r2[1];
+            r3 = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_ROR8>(send));
         }
-        r4 = __fadd_rn(r4, dpp_f32<QASR_DPP_QP_1032>(r4));
-        r4 = __fadd_rn(r4, dpp_f32<QASR_DPP_QP_2301>(r4));
-        sc[i] = jb + my_p < j1 ? __fmul_rn(r4, a.scale) : -INFINITY;
+        // the 8 lanes of a slot (lane bits 0-2) end with identical sums
+        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(r3));
+        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_1032>(r3));
+        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_2301>(r3));
+        sc[i] = jb + my_p < j1 ? __fmul_rn(r3, a.scale) : -INFINITY;
     }
 
-    // ---- softmax over this wave's positions of each head --------------------
+    // ---- softmax over this wave's positions --------------------------------
     float m = sc[0];
 #pragma unroll
     for (int i = 1; i < GPW; i++) m = fmaxf(m, sc[i]);
-    m = fmaxf(m, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(m));
     m = fmaxf(m, dpp_f32<QASR_DPP_ROW_ROR8>(m));
     m = xrow16_max(m);
+    m = xhalf_max(m);
     float pr[GPW], l = 0.0f;
 #pragma unroll
     for (int i = 0; i < GPW; i++) {
         pr[i] = m == -INFINITY ? 0.0f : expf(__fsub_rn(sc[i], m));
         l = __fadd_rn(l, pr[i]);
     }
-    l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(l));
+    if ((lane & 7) == 0) {      // one lane per position slot
+#pragma unroll
+        for (int i = 0; i < GPW; i++) pw[wid][i][my_p] = pr[i];
+    }
     l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_ROR8>(l));
     l = xrow16_sum(l);
+    l = xhalf_sum(l);
 
-    // ---- P V: probabilities as scalar operands; masked positions skipped ----
-    float o[G][2] = {};
+    // ---- P V: probabilities from LDS (the wave's own writes) ----------------
+    float ox = 0.0f, oy = 0.0f;
 #pragma unroll
-    for (int g = 0; g < G; g++)
+    for (int i = 0; i < GPW; i++) {
+        float P[8];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const float4 v4 = reinterpret_cast<const float4 *>(&pw[wid][i][0])[k];
+            P[4 * k] = v4.x; P[4 * k + 1] = v4.y; P[4 * k + 2] = v4.z; P[4 * k + 3] = v4.w;
+        }
+        const int jb = 8 * (g0 + wid + NW * i);
+        float gx = 0.0f, gy = 0.0f;
 #pragma unroll
         for (int p = 0; p < 8; p++) {
-#pragma unroll
-            for (int i = 0; i < GPW; i++) {
-                const int j = 8 * (g0 + wid + NW * i) + p;
-                if (j >= j1) continue;                     // uniform
-                const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[i]), src[g][p]));
-                float vx = vr[i][p].x(), vy = vr[i][p].y();
-                if (own_pos && j == pos) { vx = vn.x; vy = vn.y; }
-                o[g][0] = fmaf(w, vx, o[g][0]);
-                o[g][1] = fmaf(w, vy, o[g][1]);
-            }
+            const bool live = jb + p < j1;
+            float vx = live ? vr[i][p].x() : 0.0f, vy = live ? vr[i][p].y() : 0.0f;
+            if (own_pos && jb + p == pos) { vx = vn.x; vy = vn.y; }
+            gx = fmaf(P[p], vx, gx);
+            gy = fmaf(P[p], vy, gy);
         }
+        ox = __fadd_rn(ox, gx);
+        oy = __fadd_rn(oy, gy);
+    }
 
     // ---- merge the waves of the block (LDS, one barrier) --------------------
-    if ((lane & 15) == 0 && psel < 1.0f) {   // one lane per head
-        wm[wid][my_h] = m;
-        wl[wid][my_h] = l;
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++)
-        reinterpret_cast<float2 *>(&wacc[wid][g][0])[lane] = make_float2(o[g][0], o[g][1]);
+    if (lane == 0) { wm[wid] = m; wl[wid] = l; }
+    reinterpret_cast<float2 *>(&wacc[wid][0])[lane] = make_float2(ox, oy);
     __syncthreads();
-    const int gq = (t >> 7) & 1, d = t & 127;
-    if (t < G * D) {
+    if (t < D) {
+        const int d = t;
         float m_part = -INFINITY, o_part = 0.0f, l_part = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w][gq]);
+        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w]);
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float f = wm[w][gq] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w][gq], m_part));
-            o_part = fmaf(wacc[w][gq][d], f, o_part);
-            l_part = fmaf(wl[w][gq], f, l_part);
+            const float f = wm[w] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w], m_part));
+            o_part = fmaf(wacc[w][d], f, o_part);
+            l_part = fmaf(wl[w], f, l_part);
         }
-        const int h = kvh * G + gq;
         part[part_o_index(n_split, split, Hq, h * D + d)] = o_part;
         if (d == 0) {
             part[(2 * h) * n_split + split] = m_part;
@@ -772,15 +777,16 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
         else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);  \
     }
     if (dec && !merge && a.gpw > 0) {
-        // k_attn_step (single-stream step): 4 waves of gpw = 1..3 groups (the
-        // whole run: gpb <= 4 gpw)
-        if (a.waves != 4 || a.gpw < 1 || a.gpw > 3 || a.gpb > 4 * a.gpw || a.gpb_dev || nb != 1 ||
-            n_kv_heads * a.n_split != (int)grid.x)
+        // k_attn_step (single-stream step): one block per (query head, split),
+        // 4 waves of gpw = 1..4 groups (the whole run: gpb <= 4 gpw)
+        if (a.waves != 4 || a.gpw < 1 || a.gpw > 4 || a.gpb > 4 * a.gpw || a.gpb_dev || nb != 1)
             return hipErrorInvalidValue;
-#define QASR_ATT_STEP(GPW)                                                                            \
-        if (kv_bf16) hipLaunchKernelGGL((k_attn_step<uint16_t, 4, GPW>), grid, dim3(256), 0, st, a);  \
-        else hipLaunchKernelGGL((k_attn_step<float, 4, GPW>), grid, dim3(256), 0, st, a);
-        if (a.gpw == 1) { QASR_ATT_STEP(1) } else if (a.gpw == 2) { QASR_ATT_STEP(2) } else { QASR_ATT_STEP(3) }
+        const dim3 sgrid(n_kv_heads * 2 * a.n_split);
+#define QASR_ATT_STEP(GPW)                                                                             \
+        if (kv_bf16) hipLaunchKernelGGL((k_attn_step<uint16_t, 4, GPW>), sgrid, dim3(256), 0, st, a);  \
+        else hipLaunchKernelGGL((k_attn_step<float, 4, GPW>), sgrid, dim3(256), 0, st, a);
+        if (a.gpw == 1) { QASR_ATT_STEP(1) } else if (a.gpw == 2) { QASR_ATT_STEP(2) }
+        else if (a.gpw == 3) { QASR_ATT_STEP(3) } else { QASR_ATT_STEP(4) }
 #undef QASR_ATT_STEP
         return hipGetLastError();
     }
