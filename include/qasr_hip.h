@@ -288,6 +288,12 @@ int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
  * last block per KV head merges them.  use_graph: steps replay a captured HIP
  * graph, one per context bucket (default 1). */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
+/* No counterpart in the reference (the decode step's launch shape, for tuning
+ * and tests).  fuse_qkv_attention = 1 (default): each layer's RMSNorm + qkv
+ * matvec and its decode attention run as one launch, the qkv rows handed to
+ * the attention blocks as (tag, value) pairs; 0: two launches.  Tokens and
+ * KV rows are bit-identical either way. */
+int qasr_hip_decoder_set_fusion(qasr_decoder *d, int fuse_qkv_attention);
 /* per-kernel timing over n_steps real decode steps from the current KV length
  * (no graph).  After each step every kernel kind is launched once per layer
  * (the LM head n_layers times) back to back between two HIP events on the

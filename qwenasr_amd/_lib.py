@@ -130,6 +130,7 @@ _SIGS = {
     "qasr_hip_decoder_kv_upload": (C.c_int, [P, P, P]),
     "qasr_hip_decoder_kv_download": (C.c_int, [P, P, P]),
     "qasr_hip_decoder_set_options": (C.c_int, [P, C.c_int, C.c_int]),
+    "qasr_hip_decoder_set_fusion": (C.c_int, [P, C.c_int]),
     "qasr_hip_decoder_profile": (C.c_int, [P, I32, P, P, P]),
     "qasr_hip_linear_bf16w": (C.c_int, [P, P, P, P, P, I64, I64, I64, C.c_int]),
     "qasr_hip_gemm_w8_bf16": (C.c_int, [P, P, P, P, P, I64, I64, I64]),

@@ -134,6 +134,9 @@ __device__ __forceinline__ float ld_agent(const float *p) {
 __device__ __forceinline__ int ld_agent(const int *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ unsigned long long ld_agent64(const unsigned long long *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 // wait until every memory operation this thread issued has completed
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 // Counter bump after the block's stores; true in the last block to arrive.

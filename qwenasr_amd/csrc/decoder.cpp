@@ -95,6 +95,10 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
     // 8-wave blocks were slower (5.82-7.30)
     const char *as = getenv("QASR_ATTN_STEP");
     if (as && as[0] == '0' && as[1] == 0) d->attn_step = 0;
+    // QASR_ATTN_FUSE=0: the qkv matvec and the decode attention as two
+    // launches (tuning; qasr_hip_decoder_set_fusion sets it per decoder)
+    const char *af = getenv("QASR_ATTN_FUSE");
+    if (af && af[0] == '0' && af[1] == 0) d->attn_fuse = 0;
     int rc = decoder_build(d, w, lm_head, lm_head ? lm_rows : c.vocab);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
@@ -202,7 +206,14 @@ int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm
     TRY(dalloc(d, &d->qkv, nqkv));
     TRY(dalloc(d, &d->att, qd));
     TRY(dalloc(d, &d->ffn, I));
-    TRY(dalloc(d, &d->state, 4));
+    TRY(dalloc(d, &d->state, 8));
+    TRY(dalloc(d, &d->qkv_tag, nqkv));
+    HIPCHK(hipMemsetAsync(d->qkv_tag, 0, sizeof(unsigned long long) * nqkv, d->h->stream));
+    {
+        // epoch 1 (tag 0, which the cleared pairs hold, is never a live tag), no fault
+        const int32_t init[8] = {0, 0, 0, 0, 1, 0, 0, 0};
+        HIPCHK(hipMemcpy(d->state, init, sizeof(init), hipMemcpyHostToDevice));
+    }
     TRY(dalloc(d, &d->token_log, d->max_seq));
     TRY(dalloc(d, &d->out_idx, 4));
     TRY(dalloc(d, &d->counters, QASR_COUNTERS));
@@ -231,6 +242,14 @@ extern "C" void qasr_hip_decoder_free(qasr_decoder *d) {
 // one decode step: per layer [norm+qkv] [qk-norm+rope+kv-write+attention]
 // [o-proj += ] [norm+gate_up+swiglu] [down += ], then [norm+LM-head argmax]
 // ---------------------------------------------------------------------------
+// The fused qkv + attention launch applies with k_attn_step, 4 qkv rows per
+// wave, K of 1024 or 2048 and at most 32 layers (5 bits of the tag)
+static bool fused_qkv_attn(const qasr_decoder *d, bool step_kernel, int qkv_rows) {
+    const qasr_dec_config &c = d->c;
+    return d->attn_fuse && step_kernel && qkv_rows == 4 && (c.hidden == 1024 || c.hidden == 2048) &&
+           c.n_layers <= 32 && c.head_dim == 128 && c.n_heads == 2 * c.n_kv_heads;
+}
+
 int64_t decoder_ctx_cap(const qasr_decoder *d, int64_t L) {
     const int64_t c = ((L + 255) / 256) * 256;
     return std::min<int64_t>(std::max<int64_t>(c, 256), d->max_seq);
@@ -271,32 +290,41 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     if (mv_env) sscanf(mv_env, "%d,%d,%d,%d", &mv_rows[0], &mv_rows[1], &mv_rows[2], &mv_rows[3]);
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
-        if (want(0)) {
-            MvArgs a{};
-            a.x = d->x; a.embed = d->embed; a.state = d->state; a.norm_w = L.in_norm; a.eps = c.eps; a.K = H;
-            a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
-            a.n_total = qd + 2 * kvd;
-            a.resid_out = d->x;
-            LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, mv_rows[0], st), "step qkv");
+        MvArgs a{};
+        a.x = d->x; a.embed = d->embed; a.state = d->state; a.norm_w = L.in_norm; a.eps = c.eps; a.K = H;
+        a.seg[0] = {L.wqkv, L.sqkv, d->qkv, qd + 2 * kvd};
+        a.n_total = qd + 2 * kvd;
+        a.resid_out = d->x;
+        AttnDecodeArgs t{};
+        t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
+        t.rope_cos = d->rc; t.rope_sin = d->rs; t.rope_cur = d->rope_cur; t.state = d->state;
+        t.kcache = (char *)d->kc + (size_t)l * layer_elems * esz;
+        t.vcache = (char *)d->vc + (size_t)l * layer_elems * esz;
+        t.head_stride = (int64_t)d->max_seq * hd;
+        t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
+        t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = scale;
+        // static partition of the step's context bucket: the first KV loads need no device state
+        t.gpb = (int)((((cap + 7) / 8) + n_split - 1) / n_split);
+        // k_attn_step (one query head per block, same partials, 4 waves) when
+        // a block's run is at most 4 groups per wave
+        const bool step_kernel = d->attn_step && attn_step_gpw(t.gpb) > 0;
+        if (step_kernel) {
+            t.waves = 4;
+            t.gpw = attn_step_gpw(t.gpb);
         }
-        if (want(1)) {
-            AttnDecodeArgs t{};
-            t.qkv = d->qkv; t.q_norm = L.q_norm; t.k_norm = L.k_norm;
-            t.rope_cos = d->rc; t.rope_sin = d->rs; t.rope_cur = d->rope_cur; t.state = d->state;
-            t.kcache = (char *)d->kc + (size_t)l * layer_elems * esz;
-            t.vcache = (char *)d->vc + (size_t)l * layer_elems * esz;
-            t.head_stride = (int64_t)d->max_seq * hd;
-            t.part = d->part; t.counters = d->counters + QASR_CTR_ATTN; t.out = d->att;
-            t.n_split = n_split; t.waves = d->attn_waves; t.eps = c.eps; t.scale = scale;
-            // static partition of the step's context bucket: the first KV loads need no device state
-            t.gpb = (int)((((cap + 7) / 8) + n_split - 1) / n_split);
-            // the 2-dims-per-lane kernel (same partials, 4 waves) when a
-            // block's run is at most 12 groups
-            if (d->attn_step && attn_step_gpw(t.gpb) > 0) {
-                t.waves = 4;
-                t.gpw = attn_step_gpw(t.gpb);
+        // the qkv matvec and k_attn_step as one launch (kind 0; kind 1 then
+        // launches nothing): the qkv rows reach the attention as tagged pairs
+        if (fused_qkv_attn(d, step_kernel, mv_rows[0])) {
+            if (want(0)) {
+                t.qkv_tag = d->qkv_tag; t.layer = l; t.fault = d->state + 5;
+                LAUNCHCHK(launch_qkv_attn(a, t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, embed_mode && l == 0,
+                                          mv_rows[0], st),
+                          "step qkv + attention");
             }
-            LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, false), "step attention");
+        } else {
+            if (want(0)) LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, mv_rows[0], st), "step qkv");
+            if (want(1))
+                LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, st, false), "step attention");
         }
         if (want(2)) {
             if (fused_merge) {
@@ -334,13 +362,26 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         am.part_val = d->am_val; am.part_idx = d->am_idx;
         am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
         am.rope_cos = d->rc; am.rope_sin = d->rs; am.rope_cur = d->rope_cur; am.max_pos = (int)d->max_seq;
+        am.epoch = d->state + 4;
         LAUNCHCHK(launch_argmax(am, true, argmax_blocks(d->lm_i8_rows), st, want(5), want(6)), "step argmax");
+        if (want(6)) d->epochs += 1;
     }
     return QASR_OK;
 }
 
 int decoder_set_state(qasr_decoder *d, int32_t token) {
     const int64_t hd = d->c.head_dim;
+    // tags are epoch * 32 + layer in 32 bits: long before the epoch reaches
+    // 2^27 (one call runs at most max_seq steps) the pairs are cleared and the
+    // epoch restarts at 1
+    if (d->epochs >= ((int64_t)1 << 26)) {
+        const int64_t nqkv = (int64_t)(d->c.n_heads + 2 * d->c.n_kv_heads) * d->c.head_dim;
+        static const int32_t one = 1;
+        HIPCHK(hipMemsetAsync(d->qkv_tag, 0, sizeof(unsigned long long) * nqkv, d->h->stream));
+        HIPCHK(hipMemcpyAsync(d->state + 4, &one, sizeof(one), hipMemcpyHostToDevice, d->h->stream));
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        d->epochs = 0;
+    }
     d->host_state[0] = token;
     d->host_state[1] = (int32_t)d->len;
     d->host_state[2] = 0;
@@ -384,7 +425,18 @@ int decoder_run_embed_step(qasr_decoder *d) {
     }
     HIPCHK(hipGraphLaunch(it->second, d->h->stream));
     d->step_pos += 1;
+    d->epochs += 1;
     return QASR_OK;
+}
+
+int decoder_fault_check(qasr_decoder *d) {
+    int32_t f = 0;
+    HIPCHK(hipMemcpy(&f, d->state + 5, sizeof(f), hipMemcpyDeviceToHost));
+    if (f == 0) return QASR_OK;
+    const int32_t z = 0;
+    HIPCHK(hipMemcpy(d->state + 5, &z, sizeof(z), hipMemcpyHostToDevice));
+    return qasr_fail(QASR_ERR_HIP, "decode step: an attention block never observed the step's qkv rows (the fused "
+                                   "qkv + attention hand-off timed out); the tokens of this call are not valid");
 }
 
 extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int32_t token_in,
@@ -405,6 +457,7 @@ extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int
     }
     HIPCHK(hipMemcpyAsync(d->host_state, d->state, sizeof(d->host_state), hipMemcpyDeviceToHost, d->h->stream));
     HIPCHK(hipStreamSynchronize(d->h->stream));
+    TRY(decoder_fault_check(d));
     *token_out = d->host_state[0];
     d->len += 1;
     return QASR_OK;
@@ -432,6 +485,7 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
     HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost,
                           d->h->stream));
     HIPCHK(hipStreamSynchronize(d->h->stream));
+    TRY(decoder_fault_check(d));
     d->len += n_steps;
     return QASR_OK;
 }
@@ -444,6 +498,20 @@ extern "C" int qasr_hip_decoder_set_len(qasr_decoder *d, int64_t len) {
 }
 
 extern "C" int64_t qasr_hip_decoder_len(const qasr_decoder *d) { return d ? d->len : -1; }
+
+extern "C" int qasr_hip_decoder_set_fusion(qasr_decoder *d, int fuse_qkv_attention) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    if (fuse_qkv_attention != 0 && fuse_qkv_attention != 1)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_set_fusion: fuse_qkv_attention must be 0 or 1");
+    CHECK_H(d->h);
+    if (d->attn_fuse != fuse_qkv_attention) {
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
+        d->graphs.clear();
+        d->attn_fuse = fuse_qkv_attention;
+    }
+    return QASR_OK;
+}
 
 extern "C" int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
@@ -574,12 +642,28 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
     HIPCHK(hipEventCreate(&e0));
     HIPCHK(hipEventCreate(&e1));
     const int lm_reps = (int)std::min<int64_t>(c.n_layers, d->max_seq);
+    // with the fused qkv + attention launch, kind 0 is that launch and kind 1
+    // launches nothing (the split count and partition of the first step's
+    // bucket decide, as in decoder_enqueue_step)
+    auto fused_at = [d, &c](int64_t len) {
+        const int64_t cap = decoder_ctx_cap(d, len + 1);
+        const int ns = d->n_split > 0 ? d->n_split : attn_splits_auto(c, cap);
+        const int gpb = (int)((((cap + 7) / 8) + ns - 1) / ns);
+        int qr = 1;
+        while (qr < 8 && (int64_t)qr * 1024 < (int64_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim) qr *= 2;
+        static const char *mv_env = getenv("QASR_MV_ROWS");
+        if (mv_env) sscanf(mv_env, "%d", &qr);
+        return fused_qkv_attn(d, d->attn_step && attn_step_gpw(gpb) > 0, qr);
+    };
+    bool fused = fused_at(d->len), any_fused = false;
     double tot[QASR_PROFILE_KINDS] = {};
     int cnt[QASR_PROFILE_KINDS] = {};
     const int64_t len0 = d->len;
     int rc = QASR_OK;
     int32_t tok = 0;
     for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
+        fused = fused_at(d->len);
+        any_fused = any_fused || fused;
         if ((rc = set_state(d, tok)) != QASR_OK) break;
         if ((rc = decoder_enqueue_step(d, true)) != QASR_OK) break;
         HIPCHK(hipStreamSynchronize(st));
@@ -592,11 +676,14 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
             const int reps = k >= 5 ? lm_reps : 1;
             for (int r = 0; r < reps && rc == QASR_OK; r++) rc = decoder_enqueue_step(d, true, k);
             HIPCHK(hipEventRecord(e1, st));
+            // the fused qkv + attention launches above used this step's tags:
+            // advance the epoch so the next real step does not match them
+            if (k == 0 && fused) LAUNCHCHK(launch_epoch_advance(d->state + 4, st), "profile epoch");
             HIPCHK(hipEventSynchronize(e1));
             float ms = 0.0f;
             HIPCHK(hipEventElapsedTime(&ms, e0, e1));
             tot[k] += ms * 1000.0;
-            cnt[k] += k >= 5 ? lm_reps : c.n_layers;
+            if (!(k == 1 && fused)) cnt[k] += k >= 5 ? lm_reps : c.n_layers;
         }
         tok = next[0];
         d->len += 1;
@@ -606,6 +693,7 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
     const double Lavg = (double)len0 + 0.5 * (n_steps - 1) + 1.0;   // context length seen by the attention
     d->len = len0;
     if (rc != QASR_OK) return rc;
+    TRY(decoder_fault_check(d));
     const double H = c.hidden, qd = (double)c.n_heads * c.head_dim, kvd = (double)c.n_kv_heads * c.head_dim;
     const double I = c.intermediate, V = (double)d->lm_i8_rows, esz = d->kv_bf16 ? 2 : 4;
     // algorithmic bytes: int8 weights N*K + scales 4N + activation 4K + output 4N (+4N read for += )
@@ -620,8 +708,9 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
         8.0 * argmax_blocks(d->lm_i8_rows)};
     for (int k = 0; k < QASR_PROFILE_KINDS; k++) {
         us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
-        if (bytes_per_launch) bytes_per_launch[k] = bytes[k];
-        if (launches_per_step) launches_per_step[k] = k >= 5 ? 1 : c.n_layers;
+        if (bytes_per_launch)
+            bytes_per_launch[k] = any_fused && k == 0 ? bytes[0] + bytes[1] : (any_fused && k == 1 ? 0.0 : bytes[k]);
+        if (launches_per_step) launches_per_step[k] = k >= 5 ? 1 : (any_fused && k == 1 ? 0 : c.n_layers);
     }
     return QASR_OK;
 }

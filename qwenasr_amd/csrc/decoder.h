@@ -36,7 +36,8 @@ struct qasr_decoder {
     float *rc = nullptr, *rs = nullptr;         // RoPE [max_seq][hd]
     float *rope_cur = nullptr;                  // [2][hd]: cos, sin rows of the step's position
     float *x = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr;
-    int32_t *state = nullptr;                   // {token, pos, step, flag}
+    int32_t *state = nullptr;                   // {token, pos, step, flag, epoch, fault, -, -}
+    unsigned long long *qkv_tag = nullptr;      // fused qkv + attention: (tag, value) of the qkv rows
     int32_t *token_log = nullptr, *out_idx = nullptr;
     unsigned *counters = nullptr;
     float *am_val = nullptr, *part = nullptr;
@@ -44,6 +45,8 @@ struct qasr_decoder {
     int n_split = 0, use_graph = 1;             // attention splits (0: automatic per context bucket)
     int attn_waves = 4;                         // waves per attention block (4 or 8)
     int attn_step = 4;                          // 4: k_attn_step (4 waves per block); 0: k_attn_decode
+    int attn_fuse = 1;                          // 1: the qkv matvec and k_attn_step in one launch
+    int64_t epochs = 0;                         // steps since the tags were last cleared
     // one captured decode step per context bucket (the attention's static
     // partition is sized for the bucket); keyed by the bucket's capacity
     std::map<int64_t, hipGraphExec_t> graphs;
@@ -88,3 +91,7 @@ int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg)
 int decoder_run_embed_step(qasr_decoder *d);
 // host -> device decode state {token, pos = d->len, 0, 0} and the RoPE rows of pos
 int decoder_set_state(qasr_decoder *d, int32_t token);
+// after the caller's synchronisation: QASR_ERR_HIP when a fused qkv + attention
+// launch of the steps since the last check gave up waiting for its qkv values
+// (those steps' tokens are not valid); clears the flag
+int decoder_fault_check(qasr_decoder *d);

@@ -673,6 +673,7 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
         HIPCHK(hipEventRecord(e->ev[4], st));
         HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
+        TRY(decoder_fault_check(d));
         d->len += n_steps;
         stage_times(e, times_ms);
         return QASR_OK;
@@ -721,6 +722,7 @@ extern "C" int qasr_hip_transcribe_prompt(qasr_decoder *d, qasr_encoder *e, cons
         }
         HIPCHK(hipEventRecord(e->ev[4], st));
         HIPCHK(hipStreamSynchronize(st));
+        TRY(decoder_fault_check(d));
         const int64_t kept = stop_at >= 0 ? stop_at + 1 : done;
         std::memcpy(tokens_out, log.data(), sizeof(int32_t) * kept);
         *n_out = kept;

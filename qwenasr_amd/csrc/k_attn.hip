@@ -1,5 +1,6 @@
 // Decode-step attention and the small row-wise kernels around it.
 #include "kernels.h"
+#include "mv_wave.h"
 
 namespace qasr {
 
@@ -525,8 +526,17 @@ __device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float
 // block of query head 0 of the KV head that holds the position writes the
 // new K/V row; the other query head's block forms the same values for its
 // own score and P V term.
-template <typename KVT, int NW, int GPW>
-__global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
+//
+// POLL: q, the new k and the new v come from a.qkv_tag as (tag, value) pairs
+// that blocks of the same launch store (the qkv matvec role of k_qkv_attn);
+// each wave polls its 6 pairs per lane until all carry this step's tag
+// (state[4] x 32 + layer).  The pairs are issued after the K/V rows, so the
+// first poll returns when those have arrived too.  A poll that has not
+// matched after QASR_POLL_SPINS rounds sets *a.fault and goes on (the host
+// reports the step as failed), so every wave ends.
+#define QASR_POLL_SPINS (1 << 18)
+template <typename KVT, int NW, int GPW, bool POLL>
+__device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk, int nblk) {
     constexpr int D = 128, G = 2;
     using Kp = KvPair<KVT>;
     __shared__ float wm[NW], wl[NW];
@@ -535,8 +545,8 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int n_split = a.n_split;
-    const int Hkv = gridDim.x / (G * n_split), Hq = Hkv * G;
-    const int kvh = blockIdx.x % Hkv, gq = (blockIdx.x / Hkv) % G, split = blockIdx.x / (G * Hkv);
+    const int Hkv = nblk / (G * n_split), Hq = Hkv * G;
+    const int kvh = blk % Hkv, gq = (blk / Hkv) % G, split = blk / (G * Hkv);
     const int h = kvh * G + gq;
     KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
     KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
@@ -551,9 +561,12 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
     // partition needs no device state, so the K rows, then the V rows, go out
     // before the position arrives (rows past the cache read row 0; everything
     // past the context is masked once the position is known)
-    float2 q = reinterpret_cast<const float2 *>(qkv + h * D)[lane];
-    float2 kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
-    float2 vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
+    float2 q, kn, vn;
+    if (!POLL) {
+        q = reinterpret_cast<const float2 *>(qkv + h * D)[lane];
+        kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
+        vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
+    }
     const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
     const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
     const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
@@ -575,6 +588,30 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
             vr[i][p].load(vc + (int64_t)(j < max_rows ? j : 0) * D, lane);
         }
     __builtin_amdgcn_sched_barrier(0);
+    if (POLL) {
+        const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
+        const unsigned long long *tq = a.qkv_tag + h * D + 2 * lane;
+        const unsigned long long *tk = a.qkv_tag + Hq * D + kvh * D + 2 * lane;
+        const unsigned long long *tv = a.qkv_tag + Hq * D + Hkv * D + kvh * D + 2 * lane;
+        unsigned long long u[6];
+        for (int spins = 0;; spins++) {
+            u[0] = ld_agent64(tq); u[1] = ld_agent64(tq + 1);
+            u[2] = ld_agent64(tk); u[3] = ld_agent64(tk + 1);
+            u[4] = ld_agent64(tv); u[5] = ld_agent64(tv + 1);
+            bool mine = true;
+#pragma unroll
+            for (int i = 0; i < 6; i++) mine &= (unsigned)(u[i] >> 32) == tag;
+            if (__all(mine)) break;
+            if (spins >= QASR_POLL_SPINS) {
+                if (lane == 0) st_agent(a.fault, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        q = make_float2(__uint_as_float((unsigned)u[0]), __uint_as_float((unsigned)u[1]));
+        kn = make_float2(__uint_as_float((unsigned)u[2]), __uint_as_float((unsigned)u[3]));
+        vn = make_float2(__uint_as_float((unsigned)u[4]), __uint_as_float((unsigned)u[5]));
+    }
 
     const int L = pos + 1;
     const int g1 = min((L + 7) >> 3, g1s);
@@ -700,6 +737,79 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
             part[(2 * h + 1) * n_split + split] = l_part;
         }
     }
+}
+
+template <typename KVT, int NW, int GPW>
+__global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
+    attn_step_block<KVT, NW, GPW, false>(a, blockIdx.x, gridDim.x);
+}
+
+// ---------------------------------------------------------------------------
+// One launch for a layer's RMSNorm + qkv matvec and its decode attention.
+// Blocks [0, n_mv) are the qkv matvec (w8a8_wave with the layer-0 embedding
+// gather when EMBED), each row published as a (tag, value) pair in a.qkv_tag;
+// blocks [n_mv, grid) are k_attn_step's blocks, which issue their K/V loads at
+// once and then poll the pairs of their query head and KV head.  Workgroups
+// are dispatched in index order, so every matvec block has been dispatched
+// before any attention block waits: the waits end whatever the occupancy.
+// Tags are state[4] x 32 + layer: the LM-head merge advances state[4] once per
+// step, so a pair left by an earlier step or layer never matches.  The
+// values, and so the attention's outputs, are bit-identical to the two
+// separate launches'.
+// ---------------------------------------------------------------------------
+template <typename KVT, int GPW, int NS, int R, bool EMBED>
+__global__ __launch_bounds__(256) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, int n_mv) {
+    __shared__ float lds[4 * NS * 1024];
+    if ((int)blockIdx.x < n_mv) {
+        const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
+        w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, a.qkv_tag, tag);
+    } else {
+        attn_step_block<KVT, 4, GPW, true>(a, blockIdx.x - n_mv, gridDim.x - n_mv);
+    }
+}
+
+hipError_t launch_qkv_attn(const MvArgs &m, const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
+                           int kv_bf16, bool embed, int rows_per_wave, hipStream_t st) {
+    if (head_dim != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads || a.n_split <= 0 || a.n_split > ATT_MAXS)
+        return hipErrorInvalidValue;
+    if (!a.qkv_tag || !a.fault || !a.q_norm || !a.k_norm || !a.rope_cur || !a.state || a.layer < 0 || a.layer >= 32)
+        return hipErrorInvalidValue;
+    if (a.gpw < 1 || a.gpw > 4 || a.gpb <= 0 || a.gpb > 4 * a.gpw || a.head_stride < 128 || a.batch > 1)
+        return hipErrorInvalidValue;
+    if (rows_per_wave != 4 || m.n_total != (n_heads + 2 * n_kv_heads) * head_dim || m.K % 64 != 0 ||
+        m.n_total % (4 * rows_per_wave) != 0)
+        return hipErrorInvalidValue;
+    const int ns = (m.K + 1023) / 1024;
+    if (ns != 1 && ns != 2) return hipErrorInvalidValue;
+    const int n_mv = m.n_total / (4 * rows_per_wave);
+    const dim3 grid(n_mv + n_kv_heads * 2 * a.n_split);
+#define QASR_QA(KVT, GPW, NS)                                                                                     \
+    if (embed) hipLaunchKernelGGL((k_qkv_attn<KVT, GPW, NS, 4, true>), grid, dim3(256), 0, st, m, a, n_mv);     \
+    else hipLaunchKernelGGL((k_qkv_attn<KVT, GPW, NS, 4, false>), grid, dim3(256), 0, st, m, a, n_mv);
+#define QASR_QA_G(KVT, NS)                                                                                        \
+    switch (a.gpw) {                                                                                              \
+        case 1: QASR_QA(KVT, 1, NS) break;                                                                        \
+        case 2: QASR_QA(KVT, 2, NS) break;                                                                        \
+        case 3: QASR_QA(KVT, 3, NS) break;                                                                        \
+        default: QASR_QA(KVT, 4, NS) break;                                                                       \
+    }
+    if (kv_bf16) {
+        if (ns == 1) { QASR_QA_G(uint16_t, 1) } else { QASR_QA_G(uint16_t, 2) }
+    } else {
+        if (ns == 1) { QASR_QA_G(float, 1) } else { QASR_QA_G(float, 2) }
+    }
+#undef QASR_QA_G
+#undef QASR_QA
+    return hipGetLastError();
+}
+
+// advances the decode epoch by one (a step whose LM-head merge did not run)
+__global__ void k_epoch_advance(int *epoch) {
+    if (threadIdx.x == 0) epoch[0] += 1;
+}
+hipError_t launch_epoch_advance(int *epoch, hipStream_t st) {
+    hipLaunchKernelGGL(k_epoch_advance, dim3(1), dim3(64), 0, st, epoch);
+    return hipGetLastError();
 }
 
 // Multi-stream decode prologue of the attention: per stream b, per-head

@@ -3,6 +3,7 @@
 // argmax.  Integer accumulation is exact, so every output here is bit-identical
 // to the reference's NEON SDOT path for the same f32 input vector.
 #include "kernels.h"
+#include "mv_wave.h"
 
 namespace qasr {
 
@@ -40,274 +41,10 @@ __global__ __launch_bounds__(256) void k_pack_int8_rows(const uint16_t *__restri
     }
 }
 
-// ---------------------------------------------------------------------------
-// Activation prologue shared by the matvec kernels.
-//
-// Lane l owns the 16-element slots s = l + 64 c (c < NS); element e = 16 s + r.
-// The wave (a) loads its slice of x (from f32 or from a bf16 embedding row),
-// (b) optionally applies RMSNorm with the reference's exact AVX2 summation
-// order (kernels/avx.rs:377-415: 16 lanes of sequential FMAs over 16-element
-// blocks, then the hsum tree), and (c) quantizes with the absmax rule of
-// quantize_f32_to_int8 (kernels/mod.rs:1795-1802).  The result is the lane's
-// int8 dwords plus the activation scale.  No LDS barrier: each wave computes
-// the prologue redundantly (x is a few KiB and sits in L2).
-// ---------------------------------------------------------------------------
-template <int NS, bool NORM, bool EMBED>
-struct ActIn {
-    float4 xf[EMBED ? 1 : NS][4];     // raw f32 activation loads
-    uint4 xb[EMBED ? NS : 1][2];      // raw bf16 embedding-row loads
-    float4 wf[NORM ? NS : 1][4];      // raw RMSNorm gain loads
-    float xv[NS][16];
-    float wn[NORM ? NS : 1][16];
-};
-
-// Phase 1: issue the loads of the lane's activation slice (and RMSNorm gains)
-// into raw registers, nothing else.  Callers issue their weight loads right
-// after and then place a scheduling barrier, so no instruction that consumes
-// these values (and would make the wave wait for them) can be hoisted above
-// the weight loads: the weight stream is in flight before the wave first
-// waits on memory.  vmcnt retires loads in issue order, so these small
-// L2-resident reads are the first to complete.
-template <int NS, bool NORM, bool EMBED>
-__device__ __forceinline__ void act_load(const float *__restrict__ x, const uint16_t *__restrict__ xe,
-                                         const float *__restrict__ norm_w, int K, ActIn<NS, NORM, EMBED> &in) {
-    const int lane = threadIdx.x & 63;
-    const int nslot = K >> 4;
-    // out-of-range slots load slot 0; act_convert zeroes them
-#pragma unroll
-    for (int c = 0; c < NS; c++) {
-        const int s = lane + 64 * c;
-        const int se = s < nslot ? s : 0;
-        if (EMBED) {
-            const uint4 *p = reinterpret_cast<const uint4 *>(xe + 16 * se);
-            in.xb[c][0] = p[0];
-            in.xb[c][1] = p[1];
-        } else {
-            const float4 *p = reinterpret_cast<const float4 *>(x + 16 * se);
-#pragma unroll
-            for (int i = 0; i < 4; i++) in.xf[c][i] = p[i];
-        }
-        if (NORM) {
-            const float4 *wp = reinterpret_cast<const float4 *>(norm_w + 16 * se);
-#pragma unroll
-            for (int i = 0; i < 4; i++) in.wf[c][i] = wp[i];
-        }
-    }
-}
-
-// Phase 1b: raw loads -> f32 slots (zero beyond K); optionally stores the f32
-// slice to resid_out (the embedding row becomes the residual stream).
-template <int NS, bool NORM, bool EMBED>
-__device__ __forceinline__ void act_convert(ActIn<NS, NORM, EMBED> &in, int K, float *__restrict__ resid_out) {
-    const int lane = threadIdx.x & 63;
-    const int nslot = K >> 4;
-#pragma unroll
-    for (int c = 0; c < NS; c++) {
-        const int s = lane + 64 * c;
-        const bool ok = s < nslot;
-        if (EMBED) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const uint32_t wds[4] = {in.xb[c][h].x, in.xb[c][h].y, in.xb[c][h].z, in.xb[c][h].w};
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    in.xv[c][8 * h + 2 * i] = ok ? __uint_as_float(wds[i] << 16) : 0.0f;
-                    in.xv[c][8 * h + 2 * i + 1] = ok ? __uint_as_float(wds[i] & 0xFFFF0000u) : 0.0f;
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 v = in.xf[c][i];
-                in.xv[c][4 * i] = ok ? v.x : 0.0f;
-                in.xv[c][4 * i + 1] = ok ? v.y : 0.0f;
-                in.xv[c][4 * i + 2] = ok ? v.z : 0.0f;
-                in.xv[c][4 * i + 3] = ok ? v.w : 0.0f;
-            }
-        }
-        if (NORM) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float4 v = in.wf[c][i];
-                in.wn[c][4 * i] = v.x; in.wn[c][4 * i + 1] = v.y;
-                in.wn[c][4 * i + 2] = v.z; in.wn[c][4 * i + 3] = v.w;
-            }
-        }
-        if (resid_out && ok) {
-            float4 *o = reinterpret_cast<float4 *>(resid_out + 16 * s);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-                o[i] = make_float4(in.xv[c][4 * i], in.xv[c][4 * i + 1], in.xv[c][4 * i + 2], in.xv[c][4 * i + 3]);
-        }
-    }
-}
-
-// Phase 2: optional RMSNorm with the reference's exact AVX2 summation order
-// (kernels/avx.rs:377-415: 16 lanes of sequential FMAs over 16-element blocks,
-// then the hsum tree), then the absmax int8 quantization of
-// quantize_f32_to_int8 (kernels/mod.rs:1795-1802).  Lane l owns the 16-element
-// slots s = l + 64 c; the result is its int8 dwords plus the activation scale.
-// Each wave computes this redundantly — x is a few KiB and sits in L2 — so no
-// block barrier is needed.
-template <int NS, bool NORM, bool EMBED>
-__device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
-                                           int xd[NS][4], float *xs) {
-    const int lane = threadIdx.x & 63;
-    const int nslot = K >> 4;
-    if (NORM) {
-        // transpose through LDS: T[r][s] = x[16 s + r]
-#pragma unroll
-        for (int c = 0; c < NS; c++) {
-            const int s = lane + 64 * c;
-            if (s < nslot) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) lds_t[r * nslot + s] = in.xv[c][r];
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-        float acc = 0.0f;
-        if (lane < 16) {
-            const float4 *t = reinterpret_cast<const float4 *>(lds_t + lane * nslot);
-            for (int i = 0; i < (nslot >> 2); i++) {
-                float4 v = t[i];
-                acc = fmaf(v.x, v.x, acc);
-                acc = fmaf(v.y, v.y, acc);
-                acc = fmaf(v.z, v.z, acc);
-                acc = fmaf(v.w, v.w, acc);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-        const float ss = avx16_tree(acc);
-        const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
-#pragma unroll
-        for (int c = 0; c < NS; c++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) in.xv[c][r] = __fmul_rn(__fmul_rn(in.xv[c][r], rinv), in.wn[c][r]);
-    }
-    float m = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NS; c++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) m = fmaxf(m, fabsf(in.xv[c][r]));
-    m = wave_max_f32(m);
-    float scale, inv;
-    act_scales(m, &scale, &inv);
-    *xs = scale;
-#pragma unroll
-    for (int c = 0; c < NS; c++)
-#pragma unroll
-        for (int d = 0; d < 4; d++)
-            xd[c][d] = pack4_i8(round_clamp_i8(__fmul_rn(in.xv[c][4 * d], inv)),
-                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 1], inv)),
-                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 2], inv)),
-                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 3], inv)));
-}
-
-__device__ __forceinline__ int dot16(const i32x4 w, const int xd[4], int acc) {
-    acc = __builtin_amdgcn_sdot4(w.x, xd[0], acc, false);
-    acc = __builtin_amdgcn_sdot4(w.y, xd[1], acc, false);
-    acc = __builtin_amdgcn_sdot4(w.z, xd[2], acc, false);
-    acc = __builtin_amdgcn_sdot4(w.w, xd[3], acc, false);
-    return acc;
-}
-
-// ---------------------------------------------------------------------------
-// W8A8 matvec family.  Wave gw owns rows [gw R, gw R + R) of the concatenated
-// segments (q | k | v for the fused QKV projection); its weight loads are
-// issued before the activation prologue so the prologue hides under HBM
-// latency.  Epilogue ((float)acc * xs) * ws[row] as neon.rs:751-765, then:
-//   MV_PLAIN  y = v                       (linear_nobias_int8_qkv, mod.rs:884)
-//   MV_ADDTO  y = v + y                   (linear_nobias_int8_addto, mod.rs:1030)
-//   MV_SWIGLU out[j] = g/(1+expf(-g))*u   (linear_nobias_int8_swiglu, mod.rs:970)
-//   MV_BIAS   y = v + bias[row]           (matvec_int8 with bias, neon.rs:762)
-// ---------------------------------------------------------------------------
 template <int NS, int R, int MODE, bool NORM, bool EMBED>
 __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
     __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // waves past the last row compute row 0 and store nothing
-    const bool live = (blockIdx.x * 4 + wid) * R < a.n_total;
-    const int row0 = live ? (blockIdx.x * 4 + wid) * R : 0;
-    const int K = a.K, nslot = K >> 4;
-    // segment of this wave (segments are multiples of R rows); scalar selects
-    // keep the segment fields in SGPRs
-    const int n0 = a.seg[0].n, n1 = a.seg[1].n;
-    const bool in0 = row0 < n0, in1 = !in0 && row0 < n0 + n1;
-    MvSeg S;
-    S.w = in0 ? a.seg[0].w : (in1 ? a.seg[1].w : a.seg[2].w);
-    S.ws = in0 ? a.seg[0].ws : (in1 ? a.seg[1].ws : a.seg[2].ws);
-    S.y = in0 ? a.seg[0].y : (in1 ? a.seg[1].y : a.seg[2].y);
-    const int lrow0 = row0 - (in0 ? 0 : (in1 ? n0 : n0 + n1));
-    const uint16_t *xe = nullptr;
-    if (EMBED) xe = a.embed + (int64_t)a.state[0] * K;
-    float *resid = (EMBED && blockIdx.x == 0 && wid == 0) ? a.resid_out : nullptr;
-    ActIn<NS, NORM, EMBED> in;
-    act_load<NS, NORM, EMBED>(a.x, xe, a.norm_w, K, in);
-    // weight slots beyond K load slot 0; their activation bytes are zero
-    i32x4 wv[R][NS];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-#pragma unroll
-        for (int c = 0; c < NS; c++) {
-            const int s = lane + 64 * c;
-            wv[r][c] = __builtin_nontemporal_load(
-                reinterpret_cast<const i32x4 *>(S.w + (int64_t)(lrow0 + r) * K) + (s < nslot ? s : 0));
-        }
-    // epilogue operands (row scales, the old y of +=, the bias), loaded with the
-    // weights so that no load is left on the path after the dot products.
-    // SwiGLU: lane j < R/2 owns the gate/up row pair (2j, 2j+1); otherwise lane r < R owns row r.
-    // (Vector loads on purpose: as scalar loads of uniform addresses they get
-    // scheduled after the dot products.)
-    float ws0 = 0.0f, ws1 = 0.0f, yb = 0.0f;
-    if (MODE == MV_SWIGLU) {
-        const int j = lane < R / 2 ? lane : 0;
-        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * j);
-        ws1 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * j + 1);
-    } else {
-        const int r = lane < R ? lane : 0;
-        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + r);
-        if (MODE == MV_ADDTO) yb = __builtin_nontemporal_load(S.y + lrow0 + r);
-        if (MODE == MV_BIAS) yb = __builtin_nontemporal_load(a.bias + lrow0 + r);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    act_convert<NS, NORM, EMBED>(in, K, resid);
-    int xd[NS][4];
-    float xs;
-    act_finish<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
-    int acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        int t = 0;
-#pragma unroll
-        for (int c = 0; c < NS; c++) t = dot16(wv[r][c], xd[c], t);
-        acc[r] = wave_sum_i32(t);
-    }
-    // The epilogue runs in every lane with no branch: lanes past the owners
-    // recompute the first owner's value and store it to the same address.  A
-    // predicated store would let the compiler sink the operand loads above
-    // into the branch, after the dot products.
-    if (MODE == MV_SWIGLU) {
-        const int j = lane < R / 2 ? lane : 0;
-        int ag = 0, au = 0;
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            if (r == 2 * j) ag = acc[r];
-            if (r == 2 * j + 1) au = acc[r];
-        }
-        const float g = __fmul_rn(__fmul_rn((float)ag, xs), ws0);
-        const float u = __fmul_rn(__fmul_rn((float)au, xs), ws1);
-        const float o = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
-        if (live) S.y[(lrow0 >> 1) + j] = o;
-    } else {
-        const int rl = lane < R ? lane : 0;
-        int av = 0;
-#pragma unroll
-        for (int r = 0; r < R; r++) if (r == rl) av = acc[r];
-        float v = __fmul_rn(__fmul_rn((float)av, xs), ws0);
-        if (MODE == MV_ADDTO || MODE == MV_BIAS) v = __fadd_rn(v, yb);
-        if (live) S.y[lrow0 + rl] = v;
-    }
+    w8a8_wave<NS, R, MODE, NORM, EMBED>(a, blockIdx.x, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -608,6 +345,7 @@ __global__ __launch_bounds__(256) void k_argmax_finish(ArgmaxArgs a, int n_parts
             if (a.token_log) a.token_log[a.state[2]] = tok;
             a.state[2] += 1;
         }
+        if (a.epoch) a.epoch[0] += 1;
     }
 }
 

@@ -50,6 +50,7 @@ struct ArgmaxArgs {
     const float *rope_cos, *rope_sin;   // decode loop: RoPE table [max_pos][128]
     float *rope_cur;          // nullable: receives the cos, sin rows of the next position
     int max_pos;
+    int *epoch;               // nullable: advanced by one per decode step (the qkv + attention tags)
 };
 
 hipError_t launch_pack_int8(const uint16_t *w, int64_t n, int K, int mode, int8_t *q, float *s,
@@ -130,7 +131,21 @@ struct AttnDecodeArgs {
     const int *gpb_dev;       // nullable: per-stream groups per block [batch] (overrides gpb)
     const int *stream_order;  // nullable: grid row -> stream of a multi-stream step (largest units first)
     int depth;                // multi-stream mode: groups in flight per wave (1 or 2; 0: 2)
+    // qkv + attention in one launch (launch_qkv_attn): the (tag, value) pairs
+    // of the qkv rows, the layer (tag = state[4] * 32 + layer) and the flag a
+    // poll that never matched sets
+    unsigned long long *qkv_tag;
+    int layer;
+    int *fault;
 };
+
+// one launch for a layer's RMSNorm + qkv matvec (m: the MvArgs of the plain
+// qkv launch, R = 4 rows per wave) and its decode attention (a: k_attn_step's
+// arguments plus qkv_tag, layer, fault)
+hipError_t launch_qkv_attn(const MvArgs &m, const AttnDecodeArgs &a, int n_heads, int n_kv_heads, int head_dim,
+                           int kv_bf16, bool embed, int rows_per_wave, hipStream_t st);
+// epoch[0] += 1 (one thread)
+hipError_t launch_epoch_advance(int *epoch, hipStream_t st);
 
 // multi-stream step prologue (k_qk_prep_rows): q/k per-head norm + RoPE, the new
 // K/V row of every stream; run before launch_attn_decode with gpb_dev set

@@ -365,6 +365,7 @@ static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t
         for (int64_t i = 0; i < burst; i++) TRY(decoder_run_embed_step(d));
         done += burst;
     }
+    TRY(decoder_fault_check(d));
     d->len = prefill_len + done;
     s->st_forwards = done;
     s->st_steps_total += done;

@@ -201,6 +201,10 @@ class Decoder:
     def set_options(self, attn_splits=0, use_graph=True):
         check(lib().qasr_hip_decoder_set_options(self.d, int(attn_splits), 1 if use_graph else 0))
 
+    def set_fusion(self, fuse_qkv_attention=True):
+        """Each layer's qkv matvec and decode attention as one launch (True) or two."""
+        check(lib().qasr_hip_decoder_set_fusion(self.d, 1 if fuse_qkv_attention else 0))
+
 
 class Encoder:
     """Audio front end on the GPU: mel_spectrogram (audio.rs:273) + Encoder::forward (encoder.rs:186)."""

@@ -132,3 +132,46 @@ def test_kv_capacity_error(tiny_models):
     with pytest.raises(QasrError):
         gpu.forward(token=1)
     gpu.kv_len = 0
+
+
+@pytest.mark.parametrize("hidden,kv_bf16", [(1024, False), (1024, True), (2048, True)])
+def test_fused_qkv_attention_bit_identical(dev, hidden, kv_bf16):
+    """The qkv matvec and the decode attention as one launch (the qkv rows
+    handed to the attention blocks as (tag, value) pairs) against the two
+    launches: tokens and every KV row bit-identical, over a context that crosses
+    the 256- and 512-position buckets (1-3 groups per wave), with graph replay
+    and eagerly, 0.6B (K 1024) and 1.7B (K 2048) widths."""
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    cfg = dict(TINY, hidden=hidden, intermediate=3 * hidden)
+    print(f"fused qkv+attention hidden={hidden} kv_bf16={kv_bf16}", flush=True)
+    w = SynthDecoder(cfg, seed=77)
+    r = rng(78)
+    prompt = (r.standard_normal((230, hidden)) * 0.5).astype(np.float32)
+    kv = None
+    runs = []
+    for fuse, graph in ((True, True), (False, True), (True, False)):
+        g = Decoder(dev, w, max_seq=1024, kv_bf16=kv_bf16)
+        g.set_fusion(fuse)
+        g.set_options(attn_splits=-1, use_graph=graph)
+        if kv_bf16:
+            # the prefill needs an f32 cache: 229 context rows of N(0, 1) instead
+            if kv is None:
+                kv = [r.standard_normal(g.kv_shape()).astype(np.float32) for _ in range(2)]
+            g.kv_upload(*kv)
+            g.kv_len = 229
+        else:
+            g.prefill(prompt[:-1])
+        toks = g.generate(320, first_embed=prompt[-1])
+        k, v = g.kv_download()
+        runs.append((np.asarray(toks).copy(), k.copy(), v.copy()))
+        g.close()
+    n = 229 + 320
+
+    def bits(a):
+        return np.ascontiguousarray(a[:, :, :n]).view(np.uint8)
+
+    for t, k, v in runs[1:]:
+        assert (t == runs[0][0]).all()
+        assert np.array_equal(bits(k), bits(runs[0][1]))
+        assert np.array_equal(bits(v), bits(runs[0][2]))
