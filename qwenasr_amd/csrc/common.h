@@ -190,13 +190,24 @@ __device__ __forceinline__ int pack4_i8(int a, int b, int c, int d) {
 
 // hsum_ps tree of the reference (kernels/avx.rs:37-51) applied to 16 AVX-lane
 // accumulators held in lanes 0..15: t_j = A_j + A_{j+8}; result
-// ((t0+t4)+(t1+t5)) + ((t2+t6)+(t3+t7)); returned in every lane.
+// ((t0+t4)+(t1+t5)) + ((t2+t6)+(t3+t7)); returned in every lane.  Each step
+// is a DPP row shift (row_shl:N, lane i reads lane i + N of its 16-lane row)
+// and one add, so lanes 0-7, 0-3, then 0 and 2 hold the tree's partial sums
+// in the reference's order.
+#define QASR_DPP_ROW_SHL(N) (0x100 + (N))
 __device__ __forceinline__ float avx16_tree(float a) {
-    float t = __fadd_rn(a, __shfl_down(a, 8, QASR_WAVE));
-    float u = __fadd_rn(t, __shfl_down(t, 4, QASR_WAVE));
-    float v = __fadd_rn(u, __shfl_down(u, 1, QASR_WAVE));
-    float r = __fadd_rn(v, __shfl_down(v, 2, QASR_WAVE));
-    return __shfl(r, 0, QASR_WAVE);
+    const float t = __fadd_rn(a, dpp_f32<QASR_DPP_ROW_SHL(8)>(a));
+    const float u = __fadd_rn(t, dpp_f32<QASR_DPP_ROW_SHL(4)>(t));
+    const float v = __fadd_rn(u, dpp_f32<QASR_DPP_ROW_SHL(1)>(u));
+    const float r = __fadd_rn(v, dpp_f32<QASR_DPP_ROW_SHL(2)>(v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
+}
+
+// x / n rounded to nearest: for n a power of two the product with 2^-log2(n),
+// which is exact (the same value, the same single rounding), else a division
+__device__ __forceinline__ float div_by_count(float x, int n) {
+    if ((n & (n - 1)) == 0) return __fmul_rn(x, __int_as_float((127 - __builtin_ctz((unsigned)n)) << 23));
+    return __fdiv_rn(x, (float)n);
 }
 
 // gelu of the reference (avx.rs:536-563) for element `idx` of a buffer of n

@@ -111,7 +111,7 @@ __device__ __forceinline__ void norm_rope16(float x[16], const float w[16], cons
 #pragma unroll
     for (int k = 0; k < 16; k++) ss = fmaf(x[k], x[k], ss);
     ss = sum8(ss);
-    const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(div_by_count(ss, D), eps)));
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = __fmul_rn(__fmul_rn(x[k], r), w[k]);
 #pragma unroll
@@ -497,7 +497,7 @@ __device__ __forceinline__ float swap16_add(float keep_even, float keep_odd) {
 __device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float2 s, float eps) {
     constexpr int D = 128;
     const float ss = wave_allsum(fmaf(x.y, x.y, __fmul_rn(x.x, x.x)));
-    const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+    const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(div_by_count(ss, D), eps)));
     x.x = __fmul_rn(__fmul_rn(x.x, r), w.x);
     x.y = __fmul_rn(__fmul_rn(x.y, r), w.y);
     // partner dims d +- 64 live in lane l ^ 32
@@ -966,7 +966,7 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(float *__restrict__ out, c
         }
     }
     const float ss = avx16_tree(acc);
-    const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
+    const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(div_by_count(ss, H), eps)));
 #pragma unroll
     for (int c = 0; c < NS; c++) {
         const int sl = lane + 64 * c;
@@ -1009,7 +1009,7 @@ __device__ __forceinline__ void head_norm_rope2(float &x1, float &x2, const floa
     const int lane = threadIdx.x & 63;
     if (do_norm) {
         const float ss = wave_sum_f32(__fadd_rn(__fmul_rn(x1, x1), __fmul_rn(x2, x2)));
-        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)D), eps)));
+        const float r = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(div_by_count(ss, D), eps)));
         x1 = __fmul_rn(__fmul_rn(x1, r), w[lane]);
         x2 = __fmul_rn(__fmul_rn(x2, r), w[lane + 64]);
     }

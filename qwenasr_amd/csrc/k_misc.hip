@@ -52,7 +52,7 @@ __global__ __launch_bounds__(64) void k_layer_norm_rows(float *__restrict__ out,
     float acc = 0.0f;
     if (lane < 16)
         for (int i = 0; i < nslot; i++) acc = __fadd_rn(acc, t[i]);
-    const float mean = __fdiv_rn(avx16_tree(acc), (float)H);
+    const float mean = div_by_count(avx16_tree(acc), H);
     acc = 0.0f;
     if (lane < 16)
         for (int i = 0; i < nslot; i++) {
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(64) void k_layer_norm_rows(float *__restrict__ out,
             acc = fmaf(d, d, acc);
         }
     const float var = avx16_tree(acc);
-    const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(var, (float)H), eps)));
+    const float inv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(div_by_count(var, H), eps)));
 #pragma unroll
     for (int c = 0; c < NS; c++) {
         const int sl = lane + 64 * c;

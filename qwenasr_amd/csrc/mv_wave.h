@@ -145,7 +145,7 @@ __device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps
         }
         __builtin_amdgcn_wave_barrier();
         const float ss = avx16_tree(acc);
-        const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)K), eps)));
+        const float rinv = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(div_by_count(ss, K), eps)));
 #pragma unroll
         for (int c = 0; c < NS; c++)
 #pragma unroll
