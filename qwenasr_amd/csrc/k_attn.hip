@@ -760,9 +760,10 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
 template <typename KVT, int GPW, int NS, int R, bool EMBED>
 __global__ __launch_bounds__(256) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, int n_mv) {
     __shared__ float lds[4 * NS * 1024];
+    __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
     if ((int)blockIdx.x < n_mv) {
         const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
-        w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, a.qkv_tag, tag);
+        w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, qlds, a.qkv_tag, tag);
     } else {
         attn_step_block<KVT, 4, GPW, true>(a, blockIdx.x - n_mv, gridDim.x - n_mv);
     }

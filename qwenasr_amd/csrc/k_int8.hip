@@ -44,7 +44,8 @@ __global__ __launch_bounds__(256) void k_pack_int8_rows(const uint16_t *__restri
 template <int NS, int R, int MODE, bool NORM, bool EMBED>
 __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
     __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
-    w8a8_wave<NS, R, MODE, NORM, EMBED>(a, blockIdx.x, lds);
+    __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
+    w8a8_wave<NS, R, MODE, NORM, EMBED>(a, blockIdx.x, lds, qlds);
 }
 
 // ---------------------------------------------------------------------------
@@ -104,6 +105,7 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     constexpr int D = 128, NS = 2, HQ = 16, K = HQ * D;
     __shared__ float att[K];
     __shared__ float fw[HQ][S], lsum[HQ];
+    __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = t >> 7, d = t & 127;
@@ -126,9 +128,10 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
         for (int c = 0; c < NS; c++)
             wv[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(a.w + (int64_t)(r0 + r) * K) +
                                                   lane + 64 * c);
-    const int rl = lane < R ? lane : 0;
-    const float ws0 = __builtin_nontemporal_load(a.ws + r0 + rl);
-    const float yb = __builtin_nontemporal_load(a.y + r0 + rl);
+    // each lane's epilogue serves the row the reduce-scatter leaves in it
+    const int item = scatter_item<R>();
+    const float ws0 = __builtin_nontemporal_load(a.ws + r0 + item);
+    const float yb = __builtin_nontemporal_load(a.y + r0 + item);
     __builtin_amdgcn_sched_barrier(0);
     // (3) log-sum-exp weights per (head, split)
     {
@@ -152,7 +155,8 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
         att[h * D + d] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
     }
     __syncthreads();
-    // (5) quantize (each wave covers the whole vector with its lanes' slots)
+    // (5) quantize (the scale from the whole vector in every wave, the int8
+    // conversion shared by the block's waves)
     ActIn<NS, false, false> in;
 #pragma unroll
     for (int c = 0; c < NS; c++) {
@@ -165,21 +169,21 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     }
     int xd[NS][4];
     float xs;
-    act_finish<NS, false, false>(in, 0.0f, K, nullptr, xd, &xs);
-    // (6) dots and the residual-add epilogue (branch-free: extra lanes repeat lane 0's row)
-    int acc[R];
+    act_finish_block<NS, false, false>(in, 0.0f, K, nullptr, qlds, xd, &xs);
+    // (6) dots, one reduce-scatter of the R row sums and the residual-add
+    // epilogue (branch-free: lanes holding the same row store the same value)
+    int part[R][1];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         int q = 0;
 #pragma unroll
         for (int c = 0; c < NS; c++) q = dot16(wv[r][c], xd[c], q);
-        acc[r] = wave_sum_i32(q);
+        part[r][0] = q;
     }
-    int av = 0;
-#pragma unroll
-    for (int r = 0; r < R; r++) if (r == rl) av = acc[r];
-    const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)av, xs), ws0), yb);
-    if (live) a.y[r0 + rl] = v;
+    int av[1];
+    scatter_items<R, 1>(part, av);
+    const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)av[0], xs), ws0), yb);
+    if (live) a.y[r0 + item] = v;
 }
 
 template <int R>
@@ -221,6 +225,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 template <int NS, int R, bool NORM>
 __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
     __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
+    __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
     __shared__ float bvals[4];
     __shared__ int bidx[4];
     const int lane = threadIdx.x & 63;
@@ -272,7 +277,7 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
     if (gw + n_waves < n_groups) load_group(wb, sb, gw + n_waves);
     __builtin_amdgcn_sched_barrier(0);
     act_convert<NS, NORM, false>(in, K, nullptr);
-    act_finish<NS, NORM, false>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
+    act_finish_block<NS, NORM, false>(in, a.eps, K, lds + wid * NS * 1024, qlds, xd, &xs);
     for (int g = gw; g < n_groups; g += 2 * n_waves) {
         consume(wa, sa, g);
         if (g + 2 * n_waves < n_groups) load_group(wa, sa, g + 2 * n_waves);

@@ -117,8 +117,8 @@ __device__ __forceinline__ void act_convert(ActIn<NS, NORM, EMBED> &in, int K, f
 // Each wave computes this redundantly — x is a few KiB and sits in L2 — so no
 // block barrier is needed.
 template <int NS, bool NORM, bool EMBED>
-__device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
-                                           int xd[NS][4], float *xs) {
+__device__ __forceinline__ void act_norm_scale(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
+                                               float *xs, float *xinv) {
     const int lane = threadIdx.x & 63;
     const int nslot = K >> 4;
     if (NORM) {
@@ -157,17 +157,58 @@ __device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps
 #pragma unroll
         for (int r = 0; r < 16; r++) m = fmaxf(m, fabsf(in.xv[c][r]));
     m = wave_max_f32(m);
-    float scale, inv;
-    act_scales(m, &scale, &inv);
-    *xs = scale;
+    act_scales(m, xs, xinv);
+}
+
+// int8 dword d (elements 4d .. 4d + 3) of slot c
+template <int NS, bool NORM, bool EMBED>
+__device__ __forceinline__ int act_quant_dword(const ActIn<NS, NORM, EMBED> &in, int c, int d, float inv) {
+    return pack4_i8(round_clamp_i8(__fmul_rn(in.xv[c][4 * d], inv)),
+                    round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 1], inv)),
+                    round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 2], inv)),
+                    round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 3], inv)));
+}
+
+template <int NS, bool NORM, bool EMBED>
+__device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
+                                           int xd[NS][4], float *xs) {
+    float inv;
+    act_norm_scale<NS, NORM, EMBED>(in, eps, K, lds_t, xs, &inv);
 #pragma unroll
     for (int c = 0; c < NS; c++)
 #pragma unroll
-        for (int d = 0; d < 4; d++)
-            xd[c][d] = pack4_i8(round_clamp_i8(__fmul_rn(in.xv[c][4 * d], inv)),
-                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 1], inv)),
-                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 2], inv)),
-                                round_clamp_i8(__fmul_rn(in.xv[c][4 * d + 3], inv)));
+        for (int d = 0; d < 4; d++) xd[c][d] = act_quant_dword<NS, NORM, EMBED>(in, c, d, inv);
+}
+
+// act_finish for the 4 waves of a block that all need the same quantized
+// vector: each wave forms the scale itself (the absmax is over the whole
+// vector), quantizes dword wid of every slot its lanes hold (a quarter of the
+// per-lane work) into qlds, and after one block barrier every lane reads its
+// slots' 16 bytes back.  The values are act_finish's, bit for bit.  Every
+// wave of the block must call it.  qlds: NS * 64 * 4 ints.
+template <int NS, bool NORM, bool EMBED>
+__device__ __forceinline__ void act_finish_block(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
+                                                 int *qlds, int xd[NS][4], float *xs) {
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    float inv;
+    act_norm_scale<NS, NORM, EMBED>(in, eps, K, lds_t, xs, &inv);
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        int q;
+        // wid is wave-uniform: one of four static register selections
+        if (wid == 0) q = act_quant_dword<NS, NORM, EMBED>(in, c, 0, inv);
+        else if (wid == 1) q = act_quant_dword<NS, NORM, EMBED>(in, c, 1, inv);
+        else if (wid == 2) q = act_quant_dword<NS, NORM, EMBED>(in, c, 2, inv);
+        else q = act_quant_dword<NS, NORM, EMBED>(in, c, 3, inv);
+        qlds[(c * 64 + lane) * 4 + wid] = q;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < NS; c++) {
+        const int4 t = reinterpret_cast<const int4 *>(qlds)[c * 64 + lane];
+        xd[c][0] = t.x; xd[c][1] = t.y; xd[c][2] = t.z; xd[c][3] = t.w;
+    }
 }
 
 __device__ __forceinline__ int dot16(const i32x4 w, const int xd[4], int acc) {
@@ -176,6 +217,76 @@ __device__ __forceinline__ int dot16(const i32x4 w, const int xd[4], int acc) {
     acc = __builtin_amdgcn_sdot4(w.z, xd[2], acc, false);
     acc = __builtin_amdgcn_sdot4(w.w, xd[3], acc, false);
     return acc;
+}
+
+
+// ---------------------------------------------------------------------------
+// Reduce-scatter of a wave's integer partial dots.  Each lane holds W partial
+// sums for each of N items (rows, or gate/up row pairs); after
+// scatter_items<N, W> every lane holds the complete wave sums (all 64 lanes)
+// of item scatter_item<N>(), replicated over 64 / N lanes: a permlane32 swap
+// halves the items, a permlane16 swap halves them again, a row_ror:8 DPP step
+// once more, and DPP steps (row_half_mirror, quad perms) finish the sums over
+// the lanes left.  N = 8 takes 10 cross-lane steps per value where N
+// separate wave sums take 48.  Integer sums are exact in any order, so the
+// results equal the per-item wave sums bit for bit.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int swap32_sum_i(int keep_lo, int keep_hi) {
+    const auto p = __builtin_amdgcn_permlane32_swap(keep_lo, keep_hi, false, false);
+    return (int)p[0] + (int)p[1];
+}
+__device__ __forceinline__ int swap16_sum_i(int keep_even, int keep_odd) {
+    const auto p = __builtin_amdgcn_permlane16_swap(keep_even, keep_odd, false, false);
+    return (int)p[0] + (int)p[1];
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+// the item this lane holds after scatter_items<N, W> (the swap halves are
+// told apart by running the same swaps on indicators)
+template <int N>
+__device__ __forceinline__ int scatter_item() {
+    int it = 0;
+    if (N >= 2) it += swap32_sum_i(0, 1) > 1 ? N / 2 : 0;
+    if (N >= 4) it += swap16_sum_i(0, 1) > 1 ? N / 4 : 0;
+    if (N >= 8) it += (threadIdx.x >> 3) & 1;
+    return it;
+}
+template <int N, int W>
+__device__ __forceinline__ void scatter_items(int (&v)[N][W], int (&out)[W]) {
+    static_assert(N == 1 || N == 2 || N == 4 || N == 8, "1, 2, 4 or 8 items");
+    if constexpr (N >= 2) {
+#pragma unroll
+        for (int i = 0; i < N / 2; i++)
+#pragma unroll
+            for (int w = 0; w < W; w++) v[i][w] = swap32_sum_i(v[i][w], v[i + N / 2][w]);
+    }
+    if constexpr (N >= 4) {
+#pragma unroll
+        for (int i = 0; i < N / 4; i++)
+#pragma unroll
+            for (int w = 0; w < W; w++) v[i][w] = swap16_sum_i(v[i][w], v[i + N / 4][w]);
+    }
+    if constexpr (N >= 8) {
+        const int bit3 = (threadIdx.x >> 3) & 1;
+#pragma unroll
+        for (int w = 0; w < W; w++) {
+            const int keep = bit3 ? v[1][w] : v[0][w], send = bit3 ? v[0][w] : v[1][w];
+            v[0][w] = keep + dpp_i32<QASR_DPP_ROW_ROR8>(send);
+        }
+    }
+#pragma unroll
+    for (int w = 0; w < W; w++) {
+        int x = v[0][w];
+        if constexpr (N < 2) x = swap32_sum_i(x, x);
+        if constexpr (N < 4) x = swap16_sum_i(x, x);
+        if constexpr (N < 8) x += dpp_i32<QASR_DPP_ROW_ROR8>(x);
+        x += dpp_i32<QASR_DPP_ROW_HALF_MIRROR>(x);
+        x += dpp_i32<QASR_DPP_QP_1032>(x);
+        x += dpp_i32<QASR_DPP_QP_2301>(x);
+        out[w] = x;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -191,11 +302,13 @@ __device__ __forceinline__ int dot16(const i32x4 w, const int xd[4], int acc) {
 // TAG (plain rows only): row r's value goes to tag_out[r] as one 64-bit
 // (tag << 32 | f32 bits) agent-scope store instead of to the segment's y, for
 // a consumer in the same launch that polls until the tag matches.
-// lds: 4 NS 1024 floats per block when NORM.
+// lds: 4 NS 1024 floats per block when NORM; qlds: NS 256 ints per block (the
+// block's 4 waves share the quantized activation).  All 4 waves of the block
+// must call it (one block barrier).
 // ---------------------------------------------------------------------------
 template <int NS, int R, int MODE, bool NORM, bool EMBED, bool TAG = false>
-__device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, unsigned long long *tag_out = nullptr,
-                                          unsigned tag = 0) {
+__device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, int *qlds,
+                                          unsigned long long *tag_out = nullptr, unsigned tag = 0) {
     static_assert(!TAG || MODE == MV_PLAIN, "tagged outputs: plain rows only");
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -232,61 +345,68 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
     // SwiGLU: lane j < R/2 owns the gate/up row pair (2j, 2j+1); otherwise lane r < R owns row r.
     // (Vector loads on purpose: as scalar loads of uniform addresses they get
     // scheduled after the dot products.)
+    // Each lane's epilogue serves the item the reduce-scatter leaves in it:
+    // SwiGLU, the gate/up row pair (2j, 2j + 1) of item j; otherwise row r.
+    constexpr int NI = MODE == MV_SWIGLU ? (R >= 2 ? R / 2 : 1) : R;   // (SwiGLU needs R >= 2)
+    const int item = scatter_item<NI>();
     float ws0 = 0.0f, ws1 = 0.0f, yb = 0.0f;
     if (MODE == MV_SWIGLU) {
-        const int j = lane < R / 2 ? lane : 0;
-        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * j);
-        ws1 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * j + 1);
+        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * item);
+        ws1 = __builtin_nontemporal_load(S.ws + lrow0 + 2 * item + 1);
     } else {
-        const int r = lane < R ? lane : 0;
-        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + r);
-        if (MODE == MV_ADDTO) yb = __builtin_nontemporal_load(S.y + lrow0 + r);
-        if (MODE == MV_BIAS) yb = __builtin_nontemporal_load(a.bias + lrow0 + r);
+        ws0 = __builtin_nontemporal_load(S.ws + lrow0 + item);
+        if (MODE == MV_ADDTO) yb = __builtin_nontemporal_load(S.y + lrow0 + item);
+        if (MODE == MV_BIAS) yb = __builtin_nontemporal_load(a.bias + lrow0 + item);
     }
     __builtin_amdgcn_sched_barrier(0);
     act_convert<NS, NORM, EMBED>(in, K, resid);
     int xd[NS][4];
     float xs;
-    act_finish<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, xd, &xs);
-    int acc[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        int t = 0;
-#pragma unroll
-        for (int c = 0; c < NS; c++) t = dot16(wv[r][c], xd[c], t);
-        acc[r] = wave_sum_i32(t);
-    }
-    // The epilogue runs in every lane with no branch: lanes past the owners
-    // recompute the first owner's value and store it to the same address.  A
-    // predicated store would let the compiler sink the operand loads above
+    act_finish_block<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, qlds, xd, &xs);
+    // per-lane partial dots, then one reduce-scatter: every lane ends with its
+    // item's complete sums.  The epilogue runs in every lane with no branch
+    // (lanes holding the same item store the same value to the same address):
+    // a predicated store would let the compiler sink the operand loads above
     // into the branch, after the dot products.
-    if (MODE == MV_SWIGLU) {
-        const int j = lane < R / 2 ? lane : 0;
-        int ag = 0, au = 0;
+    if constexpr (MODE == MV_SWIGLU) {
+        int part[NI][2];
+#pragma unroll
+        for (int j = 0; j < NI; j++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                int t = 0;
+#pragma unroll
+                // (% R: the R = 1 SwiGLU form is never launched; this keeps it in bounds)
+                for (int c = 0; c < NS; c++) t = dot16(wv[(2 * j + h) % R][c], xd[c], t);
+                part[j][h] = t;
+            }
+        int gu[2];
+        scatter_items<NI, 2>(part, gu);
+        const float g = __fmul_rn(__fmul_rn((float)gu[0], xs), ws0);
+        const float u = __fmul_rn(__fmul_rn((float)gu[1], xs), ws1);
+        const float o = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
+        if (live) S.y[(lrow0 >> 1) + item] = o;
+    } else {
+        int part[NI][1];
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            if (r == 2 * j) ag = acc[r];
-            if (r == 2 * j + 1) au = acc[r];
-        }
-        const float g = __fmul_rn(__fmul_rn((float)ag, xs), ws0);
-        const float u = __fmul_rn(__fmul_rn((float)au, xs), ws1);
-        const float o = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
-        if (live) S.y[(lrow0 >> 1) + j] = o;
-    } else {
-        const int rl = lane < R ? lane : 0;
-        int av = 0;
+            int t = 0;
 #pragma unroll
-        for (int r = 0; r < R; r++) if (r == rl) av = acc[r];
-        float v = __fmul_rn(__fmul_rn((float)av, xs), ws0);
+            for (int c = 0; c < NS; c++) t = dot16(wv[r][c], xd[c], t);
+            part[r][0] = t;
+        }
+        int av[1];
+        scatter_items<NI, 1>(part, av);
+        float v = __fmul_rn(__fmul_rn((float)av[0], xs), ws0);
         if (MODE == MV_ADDTO || MODE == MV_BIAS) v = __fadd_rn(v, yb);
         if (TAG) {
             // (value, tag) in one 64-bit agent-scope store: a consumer in the
             // same launch polls it (row0 is the row in the concatenation)
             if (live)
-                __hip_atomic_store(tag_out + row0 + rl, ((unsigned long long)tag << 32) | __float_as_uint(v),
+                __hip_atomic_store(tag_out + row0 + item, ((unsigned long long)tag << 32) | __float_as_uint(v),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
-            if (live) S.y[lrow0 + rl] = v;
+            if (live) S.y[lrow0 + item] = v;
         }
     }
 }
