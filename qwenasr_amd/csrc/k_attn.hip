@@ -527,13 +527,15 @@ __device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float
 // new K/V row; the other query head's block forms the same values for its
 // own score and P V term.
 //
-// POLL: q, the new k and the new v come from a.qkv_tag as (tag, value) pairs
-// that blocks of the same launch store (the qkv matvec role of k_qkv_attn);
-// each wave polls its 6 pairs per lane until all carry this step's tag
-// (state[4] x 32 + layer).  The pairs are issued after the K/V rows, so the
-// first poll returns when those have arrived too.  A poll that has not
-// matched after QASR_POLL_SPINS rounds sets *a.fault and goes on (the host
-// reports the step as failed), so every wave ends.
+// POLL (the attention blocks of k_qkv_attn, NW + 1 waves): q, the new k and
+// the new v come from a.qkv_tag as (tag, value) pairs that blocks of the same
+// launch store.  Wave NW only polls: it keeps two polls of its 6 pairs per
+// lane in flight (its loads do not queue behind K/V rows, which complete in
+// issue order), and once all carry this step's tag (state[4] x 32 + layer) it
+// forms the normed, rotated q and k, writes the new K/V row and hands q, k, v
+// to the K/V waves through LDS (one barrier).  A poll that has not matched
+// after QASR_POLL_SPINS rounds sets *a.fault and goes on (the host reports
+// the step as failed), so every wave ends.
 #define QASR_POLL_SPINS (1 << 18)
 template <typename KVT, int NW, int GPW, bool POLL>
 __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk, int nblk) {
@@ -542,6 +544,7 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     __shared__ float wm[NW], wl[NW];
     __shared__ float wacc[NW][D];
     __shared__ __attribute__((aligned(16))) float pw[NW][GPW][8];
+    __shared__ float2 hq[POLL ? 64 : 1], hk[POLL ? 64 : 1], hv[POLL ? 64 : 1];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int n_split = a.n_split;
@@ -561,6 +564,78 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     // partition needs no device state, so the K rows, then the V rows, go out
     // before the position arrives (rows past the cache read row 0; everything
     // past the context is masked once the position is known)
+    if (POLL && wid == NW) {
+        // ---- the polling wave
+        const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
+        const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
+        const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
+        const float2 sn = reinterpret_cast<const float2 *>(a.rope_cur + D)[lane];
+        const int pos = a.state[1];
+        const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
+        const unsigned long long *tq = a.qkv_tag + h * D + 2 * lane;
+        const unsigned long long *tk = a.qkv_tag + Hq * D + kvh * D + 2 * lane;
+        const unsigned long long *tv = a.qkv_tag + Hq * D + Hkv * D + kvh * D + 2 * lane;
+        auto issue = [&](unsigned long long (&u)[6]) {
+            u[0] = ld_agent64(tq); u[1] = ld_agent64(tq + 1);
+            u[2] = ld_agent64(tk); u[3] = ld_agent64(tk + 1);
+            u[4] = ld_agent64(tv); u[5] = ld_agent64(tv + 1);
+        };
+        auto ready = [&](const unsigned long long (&u)[6]) {
+            bool mine = true;
+#pragma unroll
+            for (int i = 0; i < 6; i++) mine &= (unsigned)(u[i] >> 32) == tag;
+            return __all(mine) != 0;
+        };
+        // two polls in flight: the older one is checked while the newer one travels
+        unsigned long long ua[6], ub[6], u[6];
+        issue(ua);
+        for (int spins = 0;; spins += 2) {
+            __builtin_amdgcn_s_sleep(2);
+            issue(ub);
+            if (ready(ua)) {
+#pragma unroll
+                for (int i = 0; i < 6; i++) u[i] = ua[i];
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            issue(ua);
+            if (ready(ub)) {
+#pragma unroll
+                for (int i = 0; i < 6; i++) u[i] = ub[i];
+                break;
+            }
+            if (spins >= QASR_POLL_SPINS) {
+                if (lane == 0) st_agent(a.fault, 1);
+#pragma unroll
+                for (int i = 0; i < 6; i++) u[i] = ub[i];
+                break;
+            }
+        }
+        float2 q = make_float2(__uint_as_float((unsigned)u[0]), __uint_as_float((unsigned)u[1]));
+        float2 kn = make_float2(__uint_as_float((unsigned)u[2]), __uint_as_float((unsigned)u[3]));
+        float2 vn = make_float2(__uint_as_float((unsigned)u[4]), __uint_as_float((unsigned)u[5]));
+        const int g1 = min((pos + 8) >> 3, g1s);
+        const bool own_pos = 8 * g0 <= pos && pos < min(pos + 1, 8 * g1);
+        q = norm_rope2(q, qn, cs, sn, a.eps);
+        if (own_pos) {
+            kn = norm_rope2(kn, knw, cs, sn, a.eps);
+            Kp kp, vp;
+            kp.set(kn.x, kn.y);      // the values the cache holds (a bf16 cache rounds)
+            vp.set(vn.x, vn.y);
+            kn = make_float2(kp.x(), kp.y());
+            vn = make_float2(vp.x(), vp.y());
+            if (gq == 0) {
+                Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
+                Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
+            }
+        }
+        hq[lane] = q;
+        hk[lane] = kn;
+        hv[lane] = vn;
+        __syncthreads();          // q, k, v to the K/V waves
+        __syncthreads();          // their merge
+        return;
+    }
     float2 q, kn, vn;
     if (!POLL) {
         q = reinterpret_cast<const float2 *>(qkv + h * D)[lane];
@@ -589,28 +664,10 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
         }
     __builtin_amdgcn_sched_barrier(0);
     if (POLL) {
-        const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
-        const unsigned long long *tq = a.qkv_tag + h * D + 2 * lane;
-        const unsigned long long *tk = a.qkv_tag + Hq * D + kvh * D + 2 * lane;
-        const unsigned long long *tv = a.qkv_tag + Hq * D + Hkv * D + kvh * D + 2 * lane;
-        unsigned long long u[6];
-        for (int spins = 0;; spins++) {
-            u[0] = ld_agent64(tq); u[1] = ld_agent64(tq + 1);
-            u[2] = ld_agent64(tk); u[3] = ld_agent64(tk + 1);
-            u[4] = ld_agent64(tv); u[5] = ld_agent64(tv + 1);
-            bool mine = true;
-#pragma unroll
-            for (int i = 0; i < 6; i++) mine &= (unsigned)(u[i] >> 32) == tag;
-            if (__all(mine)) break;
-            if (spins >= QASR_POLL_SPINS) {
-                if (lane == 0) st_agent(a.fault, 1);
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        q = make_float2(__uint_as_float((unsigned)u[0]), __uint_as_float((unsigned)u[1]));
-        kn = make_float2(__uint_as_float((unsigned)u[2]), __uint_as_float((unsigned)u[3]));
-        vn = make_float2(__uint_as_float((unsigned)u[4]), __uint_as_float((unsigned)u[5]));
+        __syncthreads();          // q (normed, rotated), k, v from the polling wave
+        q = hq[lane];
+        kn = hk[lane];
+        vn = hv[lane];
     }
 
     const int L = pos + 1;
@@ -626,18 +683,21 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     const int bit3 = (lane >> 3) & 1;
     const int my_p = (s32 > 1.0f ? 4 : 0) + (s16 > 1.0f ? 2 : 0) + bit3;
 
-    // ---- q: per-head RMSNorm + RoPE; the new K/V row ------------------------
-    q = norm_rope2(q, qn, cs, sn, a.eps);
-    if (own_pos) {
-        kn = norm_rope2(kn, knw, cs, sn, a.eps);
-        Kp kp, vp;
-        kp.set(kn.x, kn.y);      // the values the cache holds (a bf16 cache rounds)
-        vp.set(vn.x, vn.y);
-        kn = make_float2(kp.x(), kp.y());
-        vn = make_float2(vp.x(), vp.y());
-        if (wid == 0 && gq == 0) {
-            Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
-            Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
+    // ---- q: per-head RMSNorm + RoPE; the new K/V row (POLL: done by the
+    // polling wave) -----------------------------------------------------------
+    if (!POLL) {
+        q = norm_rope2(q, qn, cs, sn, a.eps);
+        if (own_pos) {
+            kn = norm_rope2(kn, knw, cs, sn, a.eps);
+            Kp kp, vp;
+            kp.set(kn.x, kn.y);      // the values the cache holds (a bf16 cache rounds)
+            vp.set(vn.x, vn.y);
+            kn = make_float2(kp.x(), kp.y());
+            vn = make_float2(vp.x(), vp.y());
+            if (wid == 0 && gq == 0) {
+                Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
+                Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
+            }
         }
     }
 
@@ -758,10 +818,15 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
 // separate launches'.
 // ---------------------------------------------------------------------------
 template <typename KVT, int GPW, int NS, int R, bool EMBED>
-__global__ __launch_bounds__(256) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, int n_mv) {
+__global__ __launch_bounds__(320) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, int n_mv) {
     __shared__ float lds[4 * NS * 1024];
     __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
     if ((int)blockIdx.x < n_mv) {
+        // waves 0-3 run the matvec; wave 4 only joins its one block barrier
+        if ((threadIdx.x >> 6) == 4) {
+            __syncthreads();
+            return;
+        }
         const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
         w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, qlds, a.qkv_tag, tag);
     } else {
@@ -785,8 +850,8 @@ hipError_t launch_qkv_attn(const MvArgs &m, const AttnDecodeArgs &a, int n_heads
     const int n_mv = m.n_total / (4 * rows_per_wave);
     const dim3 grid(n_mv + n_kv_heads * 2 * a.n_split);
 #define QASR_QA(KVT, GPW, NS)                                                                                     \
-    if (embed) hipLaunchKernelGGL((k_qkv_attn<KVT, GPW, NS, 4, true>), grid, dim3(256), 0, st, m, a, n_mv);     \
-    else hipLaunchKernelGGL((k_qkv_attn<KVT, GPW, NS, 4, false>), grid, dim3(256), 0, st, m, a, n_mv);
+    if (embed) hipLaunchKernelGGL((k_qkv_attn<KVT, GPW, NS, 4, true>), grid, dim3(320), 0, st, m, a, n_mv);     \
+    else hipLaunchKernelGGL((k_qkv_attn<KVT, GPW, NS, 4, false>), grid, dim3(320), 0, st, m, a, n_mv);
 #define QASR_QA_G(KVT, NS)                                                                                        \
     switch (a.gpw) {                                                                                              \
         case 1: QASR_QA(KVT, 1, NS) break;                                                                        \
