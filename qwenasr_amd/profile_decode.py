@@ -1,6 +1,6 @@
 """Decode-only driver for hardware-counter runs (``rocprofv3 --pmc``).
 
-    QASR_DISABLE_GRAPH=1 rocprofv3 --pmc FETCH_SIZE --kernel-include-regex 'k_attn_decode|k_w8a8|k_oproj|k_argmax|k_copy' \\
+    QASR_DISABLE_GRAPH=1 rocprofv3 --pmc FETCH_SIZE --kernel-include-regex 'k_qkv_attn|k_attn|k_w8a8|k_oproj|k_argmax|k_copy' \\
         --output-format csv -d <dir> -o run -- python3 -m qwenasr_amd.profile_decode [steps] [calib_mib]
 
 Loads the seeded 0.6B decoder of the headline workload (bench.py, seed 1002),

@@ -27,10 +27,11 @@ from collections import defaultdict
 
 # the device code of the decode kernels (a change of their launch shapes or
 # partitions in the host code also calls for a new measurement)
-DECODE_SOURCES = ("common.h", "k_attn.hip", "k_int8.hip")
+DECODE_SOURCES = ("common.h", "mv_wave.h", "k_attn.hip", "k_int8.hip")
 
 # bench.py's decode kernel labels -> the 0.6B decoder's kernels (rocprofv3 names)
-DECODE_LABELS = (("norm+qkv", r"k_w8a8<1, 4, 0, true, false>"),
+DECODE_LABELS = (("norm+qkv+attention", r"k_qkv_attn<"),
+                 ("norm+qkv", r"k_w8a8<1, 4, 0, true, false>"),
                  ("attention", r"k_attn_step<|k_attn_decode<"),
                  ("o_proj+=", r"k_oproj_merge<"),
                  ("norm+gate_up+swiglu", r"k_w8a8<1, 8, 2, true, false>"),
@@ -119,7 +120,7 @@ def traffic(fetch_csv, write_csv, calib_mib):
            "# much (FETCH_SIZE scale %.4f, WRITE_SIZE scale %.4f); every dispatch of the label's kernels in 20" % (fs, ws),
            "# decode steps at contexts 495-514 (the window of bench.py's per-kernel timing).  Commands (from /tmp,",
            "# TMPDIR=/tmp, PYTHONPATH=$R, QASR_DISABLE_GRAPH=1):",
-           "#   timeout -s KILL 150 rocprofv3 --pmc FETCH_SIZE --kernel-include-regex 'k_attn|k_w8a8|k_oproj|k_argmax|k_copy'"
+           "#   timeout -s KILL 150 rocprofv3 --pmc FETCH_SIZE --kernel-include-regex 'k_qkv_attn|k_attn|k_w8a8|k_oproj|k_argmax|k_copy'"
            " --output-format csv -d $R/gpurun_out/pmc_fetch -o run -- python3 -u -m qwenasr_amd.profile_decode 20 64 494",
            "#   (the same with --pmc WRITE_SIZE -d $R/gpurun_out/pmc_write)",
            "#   python -m qwenasr_amd.rocprof_summary --traffic $R/gpurun_out/pmc_fetch/run_counter_collection.csv"
