@@ -198,7 +198,7 @@ def config4(n_streams=32, steps=32, splits=-1):
     # per-kernel HIP-event timing of the step at the mid-run lengths
     for i in range(n_streams):
         bat.set_len(i, int(lens[i]) + steps // 2)
-    prof = bat.profile(first, 4)
+    prof = [p for p in bat.profile(first, 4) if p["per_step"]]   # kinds the step launches
     for i in range(n_streams):
         bat.set_len(i, int(lens[i]))
     c_ = cfg

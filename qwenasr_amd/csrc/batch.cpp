@@ -55,7 +55,11 @@ struct qasr_batch {
     // groups in flight per attention wave (QASR_BATCH_ATTN_DEPTH=1|2): one
     // keeps the kernel at 4 waves per SIMD, which measured faster at 32 streams
     int attn_depth = 1;
-    std::map<int, hipGraphExec_t> graphs;                // by split count
+    // the single-stream decoder's attention form for every stream: k_attn_step
+    // (when every bucket's partition has at most 16 groups per block and the
+    // decoder uses it) or k_attn_decode
+    bool step_layout = false;
+    std::map<int, hipGraphExec_t> graphs;                // by split count x 8 + groups per wave
     DevBuf prefill_rows;                                 // batch_prefill's staged rows, kept between calls
     std::vector<void *> allocs;
 };
@@ -99,13 +103,39 @@ static int batch_splits(const qasr_batch *b, int64_t cap) {
 // single-stream decoder's static partition: ceil(ceil(cap / 8) / splits))
 static int batch_partition(qasr_batch *b) {
     b->gpb_host.resize(b->max_seq);
+    int32_t max_gpb = 0;
     for (int64_t p = 0; p < b->max_seq; p++) {
         const int64_t cap = batch_cap(b, p);
         const int S = batch_splits(b, cap);
         b->gpb_host[p] = (int32_t)((((cap + 7) / 8) + S - 1) / S);
+        max_gpb = std::max(max_gpb, b->gpb_host[p]);
     }
     HIPCHK(hipMemcpy(b->gpb_table, b->gpb_host.data(), sizeof(int32_t) * b->max_seq, hipMemcpyHostToDevice));
+    // Every stream must decode bit-identically to its solo run on this decoder
+    // so both use one attention form: k_attn_step's when
+    // every bucket's partition fits it (the decoder then uses it in every
+    // bucket too), else the decoder's own steps switch to k_attn_decode, the
+    // form the multi-stream step then uses.
+    qasr_decoder *d = b->d;
+    b->step_layout = d->attn_step && attn_step_gpw(max_gpb) > 0;
+    if (!b->step_layout && d->attn_step) {
+        HIPCHK(hipStreamSynchronize(d->h->stream));
+        for (auto &g : d->graphs) HIPCHK(hipGraphExecDestroy(g.second));
+        d->graphs.clear();
+        d->attn_step = 0;
+    }
     return QASR_OK;
+}
+
+// groups per attention wave of a multi-stream step at step s of the current
+// run (k_attn_step_batch): the most any stream's partition needs
+static int batch_step_gpw(const qasr_batch *b, int64_t s) {
+    int g = 1;
+    for (int64_t l : b->len) {
+        const int64_t p = std::min<int64_t>(l + s, b->max_seq - 1);
+        g = std::max(g, attn_step_gpw(b->gpb_host[(size_t)p]));
+    }
+    return g;
 }
 
 extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t max_seq, int64_t max_steps,
@@ -123,16 +153,6 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     auto steps_ok = [](int64_t k) { return k % 1024 == 0 && (k == 1024 || k == 2048 || k == 3072 || k == 4096 || k == 6144); };
     if (!steps_ok(c.hidden) || !steps_ok(c.intermediate) || c.hidden > 4096 || d->lm_i8_rows % 16)
         return qasr_fail(QASR_ERR_INVALID, "batch_create: hidden and intermediate must be 1024, 2048, 3072, 4096 or 6144");
-    // Every stream must decode bit-identically to its solo run on this decoder
-    // so the decoder's own steps switch to the attention
-    // arithmetic the multi-stream step uses (k_attn_decode; the single-stream
-    // k_attn_step is the latency-optimised form of the lone decoder).
-    if (d->attn_step) {
-        HIPCHK(hipStreamSynchronize(d->h->stream));
-        for (auto &g : d->graphs) HIPCHK(hipGraphExecDestroy(g.second));
-        d->graphs.clear();
-        d->attn_step = 0;
-    }
     qasr_batch *b = new qasr_batch();
     b->d = d;
     b->B = n_streams;
@@ -295,7 +315,7 @@ static bool per_layer_kind(int k) { return k >= BK_IN_QUANT && k <= BK_DOWN; }
 
 // one batched step with n_split attention splits (only kernels of one kind
 // when kind >= 0)
-static int batch_enqueue_step(qasr_batch *b, int n_split, int kind = -1) {
+static int batch_enqueue_step(qasr_batch *b, int n_split, int gpw, int kind = -1) {
     qasr_decoder *d = b->d;
     const qasr_dec_config &c = d->c;
     hipStream_t st = d->h->stream;
@@ -327,7 +347,13 @@ static int batch_enqueue_step(qasr_batch *b, int n_split, int kind = -1) {
         t.stream_order = b->order_dev;
         t.depth = b->attn_depth;
         t.batch = B; t.batch_kv_stride = le; t.batch_qkv_stride = nqkv; t.batch_part_stride = b->part_stride;
-        if (on(BK_PREP)) LAUNCHCHK(launch_qk_prep_rows(t, c.n_heads, c.n_kv_heads, hd, 0, st), "batch q/k prep");
+        // k_attn_step_batch does the q/k norm + RoPE and the K/V row write itself
+        if (b->step_layout) {
+            t.waves = 4;
+            t.gpw = gpw;
+        } else if (on(BK_PREP)) {
+            LAUNCHCHK(launch_qk_prep_rows(t, c.n_heads, c.n_kv_heads, hd, 0, st), "batch q/k prep");
+        }
         if (on(BK_ATTN)) LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
         if (on(BK_MERGE))
             LAUNCHCHK(launch_attn_merge_rows(b->part, b->part_stride, n_split, nullptr, qd, b->xq, b->xs, B, st),
@@ -402,18 +428,21 @@ extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_token
     TRY(batch_set_state(b, first_tokens));
     hipStream_t st = d->h->stream;
     for (int32_t s = 0; s < n_steps; s++) {
-        // the longest stream's bucket sets the split count (the largest of the streams')
+        // the longest stream's bucket sets the split count (the largest of the
+        // streams'), the longest partition the attention's groups per wave
         const int S = batch_splits(b, batch_cap(b, longest + s));
+        const int gpw = b->step_layout ? batch_step_gpw(b, s) : 0;
         if (!b->use_graph) {
-            TRY(batch_enqueue_step(b, S));
+            TRY(batch_enqueue_step(b, S, gpw));
             continue;
         }
-        auto it = b->graphs.find(S);
+        const int key = S * 8 + gpw;
+        auto it = b->graphs.find(key);
         if (it == b->graphs.end()) {
             hipGraph_t g = nullptr;
             hipGraphExec_t ge = nullptr;
             HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-            int rc = batch_enqueue_step(b, S);
+            int rc = batch_enqueue_step(b, S, gpw);
             hipError_t e = hipStreamEndCapture(st, &g);
             if (rc != QASR_OK) {
                 if (g) (void)hipGraphDestroy(g);
@@ -423,7 +452,7 @@ extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_token
             e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
             (void)hipGraphDestroy(g);
             HIPCHK(e);
-            it = b->graphs.emplace(S, ge).first;
+            it = b->graphs.emplace(key, ge).first;
         }
         HIPCHK(hipGraphLaunch(it->second, st));
     }
@@ -462,16 +491,18 @@ extern "C" int qasr_hip_batch_profile(qasr_batch *b, const int32_t *first_tokens
     int rc = QASR_OK;
     for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
         const int S = batch_splits(b, batch_cap(b, longest + s));
+        const int gpw = b->step_layout ? batch_step_gpw(b, 0) : 0;   // b->len advances per profiled step
         if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
-        if ((rc = batch_enqueue_step(b, S)) != QASR_OK) break;
+        if ((rc = batch_enqueue_step(b, S, gpw)) != QASR_OK) break;
         HIPCHK(hipMemcpyAsync(st_h.data(), b->state, sizeof(int32_t) * st_h.size(), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
         for (int k = 0; k < BK_KINDS && rc == QASR_OK; k++) {
+            if (k == BK_PREP && b->step_layout) continue;   // the attention does the q/k prep
             if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
             LAUNCHCHK(launch_delay(400, st), "profile delay");
             HIPCHK(hipEventRecord(e0, st));
             const int reps = per_layer_kind(k) ? 1 : reps_once;
-            for (int r = 0; r < reps && rc == QASR_OK; r++) rc = batch_enqueue_step(b, S, k);
+            for (int r = 0; r < reps && rc == QASR_OK; r++) rc = batch_enqueue_step(b, S, gpw, k);
             HIPCHK(hipEventRecord(e1, st));
             HIPCHK(hipEventSynchronize(e1));
             float ms = 0.0f;
@@ -490,7 +521,7 @@ extern "C" int qasr_hip_batch_profile(qasr_batch *b, const int32_t *first_tokens
     if (rc != QASR_OK) return rc;
     for (int k = 0; k < BK_KINDS; k++) {
         us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
-        if (launches_per_step) launches_per_step[k] = per_layer_kind(k) ? L : 1;
+        if (launches_per_step) launches_per_step[k] = cnt[k] ? (per_layer_kind(k) ? L : 1) : 0;
     }
     return QASR_OK;
 }

@@ -537,7 +537,15 @@ __device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float
 // after QASR_POLL_SPINS rounds sets *a.fault and goes on (the host reports
 // the step as failed), so every wave ends.
 #define QASR_POLL_SPINS (1 << 18)
-template <typename KVT, int NW, int GPW, bool POLL>
+//
+// BATCH (k_attn_step_batch, the multi-stream step): grid row y is stream
+// bs = stream_order[y]; each stream has its own cache slot, qkv row, position,
+// RoPE rows, partials (split index slowest) and groups per block gpb_dev[bs]
+// (its solo partition), and the waves load only their ceil(gpb / NW) groups
+// (row 0 stands in for the rest, which the partition masks: they add exact
+// zeros), so every stream gets the bits of the single-stream kernel run with
+// its own GPW.
+template <typename KVT, int NW, int GPW, bool POLL, bool BATCH = false>
 __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk, int nblk) {
     constexpr int D = 128, G = 2;
     using Kp = KvPair<KVT>;
@@ -551,12 +559,29 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     const int Hkv = nblk / (G * n_split), Hq = Hkv * G;
     const int kvh = blk % Hkv, gq = (blk / Hkv) % G, split = blk / (G * Hkv);
     const int h = kvh * G + gq;
-    KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (int64_t)kvh * a.head_stride;
-    KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (int64_t)kvh * a.head_stride;
-    const float *qkv = a.qkv;
-    float *part = a.part;
-    const int max_rows = (int)(a.head_stride / D);
-    const int gpb = a.gpb, g0 = split * gpb, g1s = g0 + gpb;
+    const int bs = BATCH ? (a.stream_order ? a.stream_order[blockIdx.y] : (int)blockIdx.y) : 0;
+    KVT *kc = reinterpret_cast<KVT *>(a.kcache) + (BATCH ? bs * a.batch_kv_stride : 0) + (int64_t)kvh * a.head_stride;
+    KVT *vc = reinterpret_cast<KVT *>(a.vcache) + (BATCH ? bs * a.batch_kv_stride : 0) + (int64_t)kvh * a.head_stride;
+    const float *qkv = a.qkv + (BATCH ? bs * a.batch_qkv_stride : 0);
+    float *part = a.part + (BATCH ? bs * a.batch_part_stride : 0);
+    const float *rope_cur = a.rope_cur + (BATCH ? 256 * bs : 0);
+    const int gpb = BATCH ? a.gpb_dev[bs] : a.gpb, g0 = split * gpb, g1s = g0 + gpb;
+    const int gpw_own = BATCH ? (gpb + NW - 1) / NW : GPW;     // groups this stream's waves hold
+    // rows loaded: the whole cache (the static partition needs no position),
+    // or in a multi-stream step the stream's context (its position is loaded
+    // with its partition anyway), so blocks and groups past it read row 0
+    const int max_rows = BATCH ? min((int)(a.head_stride / D), a.state[4 * bs + 1] + 1) : (int)(a.head_stride / D);
+    if (BATCH && 8 * g0 >= max_rows) {
+        // a block wholly past the stream's context: an empty partial
+        if (t < D) {
+            part[part_o_index_slow(n_split, split, Hq, h * D + t)] = 0.0f;
+            if (t == 0) {
+                part[(2 * h) * n_split + split] = -INFINITY;
+                part[(2 * h + 1) * n_split + split] = 0.0f;
+            }
+        }
+        return;
+    }
 
     // ---- every load before the first wait, the previous kernel's outputs
     // (q, the new k/v, the position) first, so that waiting for them does not
@@ -568,8 +593,8 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
         // ---- the polling wave
         const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
         const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
-        const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
-        const float2 sn = reinterpret_cast<const float2 *>(a.rope_cur + D)[lane];
+        const float2 cs = reinterpret_cast<const float2 *>(rope_cur)[lane];
+        const float2 sn = reinterpret_cast<const float2 *>(rope_cur + D)[lane];
         const int pos = a.state[1];
         const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
         const unsigned long long *tq = a.qkv_tag + h * D + 2 * lane;
@@ -644,23 +669,23 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     }
     const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
     const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
-    const float2 cs = reinterpret_cast<const float2 *>(a.rope_cur)[lane];
-    const float2 sn = reinterpret_cast<const float2 *>(a.rope_cur + D)[lane];
-    const int pos = a.state[1];
+    const float2 cs = reinterpret_cast<const float2 *>(rope_cur)[lane];
+    const float2 sn = reinterpret_cast<const float2 *>(rope_cur + D)[lane];
+    const int pos = a.state[BATCH ? 4 * bs + 1 : 1];
     Kp kr[GPW][8], vr[GPW][8];
 #pragma unroll
     for (int i = 0; i < GPW; i++)
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             const int j = 8 * (g0 + wid + NW * i) + p;
-            kr[i][p].load(kc + (int64_t)(j < max_rows ? j : 0) * D, lane);
+            kr[i][p].load(kc + (int64_t)(i < gpw_own && j < max_rows ? j : 0) * D, lane);
         }
 #pragma unroll
     for (int i = 0; i < GPW; i++)
 #pragma unroll
         for (int p = 0; p < 8; p++) {
             const int j = 8 * (g0 + wid + NW * i) + p;
-            vr[i][p].load(vc + (int64_t)(j < max_rows ? j : 0) * D, lane);
+            vr[i][p].load(vc + (int64_t)(i < gpw_own && j < max_rows ? j : 0) * D, lane);
         }
     __builtin_amdgcn_sched_barrier(0);
     if (POLL) {
@@ -791,7 +816,8 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
             o_part = fmaf(wacc[w][d], f, o_part);
             l_part = fmaf(wl[w], f, l_part);
         }
-        part[part_o_index(n_split, split, Hq, h * D + d)] = o_part;
+        part[BATCH ? part_o_index_slow(n_split, split, Hq, h * D + d) : part_o_index(n_split, split, Hq, h * D + d)] =
+            o_part;
         if (d == 0) {
             part[(2 * h) * n_split + split] = m_part;
             part[(2 * h + 1) * n_split + split] = l_part;
@@ -802,6 +828,204 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
 template <typename KVT, int NW, int GPW>
 __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
     attn_step_block<KVT, NW, GPW, false>(a, blockIdx.x, gridDim.x);
+}
+
+// ---------------------------------------------------------------------------
+// Multi-stream form of k_attn_step (f32 cache): the same blocks, lanes and
+// arithmetic per stream, so every stream gets the bits of the single-stream
+// kernel run alone on its context (its partition gpb_dev, its split count).
+// For throughput over many streams it holds one group of K rows, then one of
+// V rows, in flight instead of the whole run: pass 1 loads a wave's K groups
+// one after another (the next requested while the current one's scores form),
+// the softmax then takes the max over all of the wave's scores as the
+// single-stream kernel does, and pass 2 streams the V groups the same way.
+// Groups past the stream's context read row 0 (masked, adding exact zeros);
+// blocks wholly past it store an empty partial and leave.  Grid row y is
+// stream stream_order[y]; partials go split index slowest.
+// ---------------------------------------------------------------------------
+template <int NW, int GPW>
+__global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
+    constexpr int D = 128, G = 2;
+    using Kp = KvPair<float>;
+    __shared__ float wm[NW], wl[NW];
+    __shared__ float wacc[NW][D];
+    __shared__ __attribute__((aligned(16))) float pw[NW][GPW][8];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int n_split = a.n_split;
+    const int Hkv = gridDim.x / (G * n_split), Hq = Hkv * G;
+    const int blk = blockIdx.x;
+    const int kvh = blk % Hkv, gq = (blk / Hkv) % G, split = blk / (G * Hkv);
+    const int h = kvh * G + gq;
+    const int bs = a.stream_order ? a.stream_order[blockIdx.y] : (int)blockIdx.y;
+    float *kc = reinterpret_cast<float *>(a.kcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
+    float *vc = reinterpret_cast<float *>(a.vcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
+    const float *qkv = a.qkv + bs * a.batch_qkv_stride;
+    float *part = a.part + bs * a.batch_part_stride;
+    const float *rope_cur = a.rope_cur + 256 * bs;
+    const int gpb = a.gpb_dev[bs], g0 = split * gpb, g1s = g0 + gpb;
+    const int gpw_own = (gpb + NW - 1) / NW;
+    const int pos = a.state[4 * bs + 1];
+    const int max_rows = min((int)(a.head_stride / D), pos + 1);
+    if (8 * g0 >= max_rows) {
+        // a block wholly past the stream's context: an empty partial
+        if (t < D) {
+            part[part_o_index_slow(n_split, split, Hq, h * D + t)] = 0.0f;
+            if (t == 0) {
+                part[(2 * h) * n_split + split] = -INFINITY;
+                part[(2 * h + 1) * n_split + split] = 0.0f;
+            }
+        }
+        return;
+    }
+    auto row_of = [&](int i, int p) {
+        const int j = 8 * (g0 + wid + NW * i) + p;
+        return (int64_t)(i < gpw_own && j < max_rows ? j : 0) * D;
+    };
+    // q, the new k/v and the first K group
+    float2 q = reinterpret_cast<const float2 *>(qkv + h * D)[lane];
+    float2 kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
+    float2 vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
+    const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
+    const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
+    const float2 cs = reinterpret_cast<const float2 *>(rope_cur)[lane];
+    const float2 sn = reinterpret_cast<const float2 *>(rope_cur + D)[lane];
+    Kp kcur[8], knext[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++) kcur[p].load(kc + row_of(0, p), lane);
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int L = pos + 1;
+    const int g1 = min((L + 7) >> 3, g1s);
+    const int j1 = min(L, 8 * g1);
+    const bool own_pos = 8 * g0 <= pos && pos < j1;
+    const float s32 = swap32_add(0.0f, 1.0f);
+    const float s16 = swap16_add(0.0f, 1.0f);
+    const int bit3 = (lane >> 3) & 1;
+    const int my_p = (s32 > 1.0f ? 4 : 0) + (s16 > 1.0f ? 2 : 0) + bit3;
+    q = norm_rope2(q, qn, cs, sn, a.eps);
+    if (own_pos) {
+        kn = norm_rope2(kn, knw, cs, sn, a.eps);
+        if (wid == 0 && gq == 0) {
+            Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
+            Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
+        }
+    }
+
+    // ---- pass 1: scores, one K group in flight behind the one being used ----
+    float sc[GPW];
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
+        sc[i] = -INFINITY;
+        if (i >= gpw_own) continue;                   // uniform
+        if (i + 1 < gpw_own) {
+#pragma unroll
+            for (int p = 0; p < 8; p++) knext[p].load(kc + row_of(i + 1, p), lane);
+        }
+        const int jb = 8 * (g0 + wid + NW * i);
+        float v8[8];
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            float kx = kcur[p].x(), ky = kcur[p].y();
+            if (own_pos && jb + p == pos) { kx = kn.x; ky = kn.y; }
+            v8[p] = fmaf(q.y, ky, __fmul_rn(q.x, kx));
+        }
+        float r1[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) r1[k] = swap32_add(v8[k], v8[k + 4]);
+        float r2[2];
+#pragma unroll
+        for (int k = 0; k < 2; k++) r2[k] = swap16_add(r1[k], r1[k + 2]);
+        float r3;
+        {
+            const float keep = bit3 ? r2[1] : r2[0], send = bit3 ? r2[0] : r2[1];
+            r3 = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_ROR8>(send));
+        }
+        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(r3));
+        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_1032>(r3));
+        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_2301>(r3));
+        sc[i] = jb + my_p < j1 ? __fmul_rn(r3, a.scale) : -INFINITY;
+#pragma unroll
+        for (int p = 0; p < 8; p++) kcur[p] = knext[p];
+    }
+    // the first V group goes out while the softmax forms
+    Kp vcur[8], vnext[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++) vcur[p].load(vc + row_of(0, p), lane);
+
+    // ---- softmax over this wave's positions (the single-stream order) -------
+    float m = sc[0];
+#pragma unroll
+    for (int i = 1; i < GPW; i++) m = fmaxf(m, sc[i]);
+    m = fmaxf(m, dpp_f32<QASR_DPP_ROW_ROR8>(m));
+    m = xrow16_max(m);
+    m = xhalf_max(m);
+    float pr[GPW], l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
+        pr[i] = m == -INFINITY ? 0.0f : expf(__fsub_rn(sc[i], m));
+        if (i < gpw_own) l = __fadd_rn(l, pr[i]);
+    }
+    if ((lane & 7) == 0) {
+#pragma unroll
+        for (int i = 0; i < GPW; i++) pw[wid][i][my_p] = pr[i];
+    }
+    l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_ROR8>(l));
+    l = xrow16_sum(l);
+    l = xhalf_sum(l);
+
+    // ---- pass 2: P V, one V group in flight behind the one being used -------
+    float ox = 0.0f, oy = 0.0f;
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
+        if (i >= gpw_own) continue;                   // uniform
+        if (i + 1 < gpw_own) {
+#pragma unroll
+            for (int p = 0; p < 8; p++) vnext[p].load(vc + row_of(i + 1, p), lane);
+        }
+        float P[8];
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const float4 v4 = reinterpret_cast<const float4 *>(&pw[wid][i][0])[k];
+            P[4 * k] = v4.x; P[4 * k + 1] = v4.y; P[4 * k + 2] = v4.z; P[4 * k + 3] = v4.w;
+        }
+        const int jb = 8 * (g0 + wid + NW * i);
+        float gx = 0.0f, gy = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const bool live = jb + p < j1;
+            float vx = live ? vcur[p].x() : 0.0f, vy = live ? vcur[p].y() : 0.0f;
+            if (own_pos && jb + p == pos) { vx = vn.x; vy = vn.y; }
+            gx = fmaf(P[p], vx, gx);
+            gy = fmaf(P[p], vy, gy);
+        }
+        ox = __fadd_rn(ox, gx);
+        oy = __fadd_rn(oy, gy);
+#pragma unroll
+        for (int p = 0; p < 8; p++) vcur[p] = vnext[p];
+    }
+
+    // ---- merge the waves of the block (LDS, one barrier) --------------------
+    if (lane == 0) { wm[wid] = m; wl[wid] = l; }
+    reinterpret_cast<float2 *>(&wacc[wid][0])[lane] = make_float2(ox, oy);
+    __syncthreads();
+    if (t < D) {
+        const int d = t;
+        float m_part = -INFINITY, o_part = 0.0f, l_part = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w]);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = wm[w] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w], m_part));
+            o_part = fmaf(wacc[w][d], f, o_part);
+            l_part = fmaf(wl[w], f, l_part);
+        }
+        part[part_o_index_slow(n_split, split, Hq, h * D + d)] = o_part;
+        if (d == 0) {
+            part[(2 * h) * n_split + split] = m_part;
+            part[(2 * h + 1) * n_split + split] = l_part;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -951,6 +1175,17 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
     } else {                                                                                         \
         if (kv_bf16) hipLaunchKernelGGL((k_attn_decode<uint16_t, NW, false, 2>), grid, dim3(NW * 64), 0, st, a); \
         else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);  \
+    }
+    if (dec && !merge && a.gpw > 0 && a.gpb_dev) {
+        // k_attn_step_batch (multi-stream step): grid (query head x split, stream),
+        // 4 waves of up to gpw groups; each stream's gpb_dev must be <= 4 gpw
+        if (a.waves != 4 || a.gpw < 1 || a.gpw > 4 || kv_bf16 || nb > 65535) return hipErrorInvalidValue;
+        const dim3 bgrid(n_kv_heads * 2 * a.n_split, nb);
+#define QASR_ATT_BSTEP(GPW) hipLaunchKernelGGL((k_attn_step_batch<4, GPW>), bgrid, dim3(256), 0, st, a);
+        if (a.gpw == 1) { QASR_ATT_BSTEP(1) } else if (a.gpw == 2) { QASR_ATT_BSTEP(2) }
+        else if (a.gpw == 3) { QASR_ATT_BSTEP(3) } else { QASR_ATT_BSTEP(4) }
+#undef QASR_ATT_BSTEP
+        return hipGetLastError();
     }
     if (dec && !merge && a.gpw > 0) {
         // k_attn_step (single-stream step): one block per (query head, split),

@@ -119,10 +119,12 @@ static inline int attn_splits_auto(const qasr_dec_config &c, int64_t cap) {
 }
 
 // groups per wave of k_attn_step (4 waves per block, each holding its whole
-// share of the block's run): 1-3, or 0 when a block's run is longer than 12
-// groups, where k_attn_decode is faster (measured at the 1024-position
-// bucket, 16 groups: 7.86 against 9.32 us)
-static inline int attn_step_gpw(int64_t gpb) { return gpb <= 12 ? (int)std::max<int64_t>(1, (gpb + 3) / 4) : 0; }
+// share of the block's run): 1-4, or 0 when a block's run is longer than 16
+// groups (contexts past 8192 positions), where k_attn_decode takes over.
+// Measured on the 0.6B decode at contexts 780-980 (1024-position bucket, 16
+// groups per block): 666 us/token with k_attn_step (fused with the qkv
+// matvec) against 702 us with k_attn_decode.
+static inline int attn_step_gpw(int64_t gpb) { return gpb <= 16 ? (int)std::max<int64_t>(1, (gpb + 3) / 4) : 0; }
 
 // blocks of the LM-head argmax grid (4 waves of 4-row groups each): 1024
 // blocks (4 per CU) stream the 0.6B LM head in 24.6 us against 26.2 us at
