@@ -127,6 +127,11 @@ static int batch_partition(qasr_batch *b) {
     return QASR_OK;
 }
 
+// whether the multi-stream step uses k_attn_step_batch: its layout fits and
+// the decoder still runs k_attn_step (another batch on the same decoder may
+// have switched it to k_attn_decode since, and then this one follows)
+static bool batch_step_layout(const qasr_batch *b) { return b->step_layout && b->d->attn_step; }
+
 // groups per attention wave of a multi-stream step at step s of the current
 // run (k_attn_step_batch): the most any stream's partition needs
 static int batch_step_gpw(const qasr_batch *b, int64_t s) {
@@ -348,7 +353,7 @@ static int batch_enqueue_step(qasr_batch *b, int n_split, int gpw, int kind = -1
         t.depth = b->attn_depth;
         t.batch = B; t.batch_kv_stride = le; t.batch_qkv_stride = nqkv; t.batch_part_stride = b->part_stride;
         // k_attn_step_batch does the q/k norm + RoPE and the K/V row write itself
-        if (b->step_layout) {
+        if (batch_step_layout(b)) {
             t.waves = 4;
             t.gpw = gpw;
         } else if (on(BK_PREP)) {
@@ -431,7 +436,7 @@ extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_token
         // the longest stream's bucket sets the split count (the largest of the
         // streams'), the longest partition the attention's groups per wave
         const int S = batch_splits(b, batch_cap(b, longest + s));
-        const int gpw = b->step_layout ? batch_step_gpw(b, s) : 0;
+        const int gpw = batch_step_layout(b) ? batch_step_gpw(b, s) : 0;
         if (!b->use_graph) {
             TRY(batch_enqueue_step(b, S, gpw));
             continue;
@@ -491,13 +496,13 @@ extern "C" int qasr_hip_batch_profile(qasr_batch *b, const int32_t *first_tokens
     int rc = QASR_OK;
     for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
         const int S = batch_splits(b, batch_cap(b, longest + s));
-        const int gpw = b->step_layout ? batch_step_gpw(b, 0) : 0;   // b->len advances per profiled step
+        const int gpw = batch_step_layout(b) ? batch_step_gpw(b, 0) : 0;   // b->len advances per profiled step
         if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
         if ((rc = batch_enqueue_step(b, S, gpw)) != QASR_OK) break;
         HIPCHK(hipMemcpyAsync(st_h.data(), b->state, sizeof(int32_t) * st_h.size(), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
         for (int k = 0; k < BK_KINDS && rc == QASR_OK; k++) {
-            if (k == BK_PREP && b->step_layout) continue;   // the attention does the q/k prep
+            if (k == BK_PREP && batch_step_layout(b)) continue;   // the attention does the q/k prep
             if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
             LAUNCHCHK(launch_delay(400, st), "profile delay");
             HIPCHK(hipEventRecord(e0, st));
