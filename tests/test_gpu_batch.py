@@ -196,3 +196,39 @@ def test_batch_matches_oracle(small_decoder, orc):
                 assert int(got[i][s]) == want[s], (i, s, got[i].tolist(), want, margins[s])
                 compared += 1
     assert compared >= 36, compared
+
+
+def test_batch_follows_decoder_attention_form(dev):
+    """A batch made while its decoder runs the single-stream attention form
+    (k_attn_step; the batch then uses k_attn_step_batch) keeps matching solo
+    decoding after a second batch on the same decoder, with partitions longer
+    than k_attn_step takes, has switched the decoder to k_attn_decode: the
+    first batch follows the decoder's form from its next step on."""
+    from qwenasr_amd.model import Batch, Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    print("batch follows the decoder's attention form", flush=True)
+    w = SynthDecoder(SMALL, seed=1005)
+    dec = Decoder(dev, w, max_seq=2048)
+    try:
+        r = rng(1006)
+        H = SMALL["hidden"]
+        lens = [300, 700, 1100, 90]
+        prefixes = [r.normal(0, 1, (L, H)).astype(np.float32) for L in lens]
+        first = r.integers(0, SMALL["vocab"], len(lens))
+        a = Batch(dec, len(lens), 2048, max_steps=6)
+        try:
+            for i, p in enumerate(prefixes):
+                a.prefill(i, p)
+            got0 = a.generate(first, 6)                  # k_attn_step_batch
+            b2 = Batch(dec, 2, 2048, max_steps=6)
+            b2.set_options(attn_splits=1)                # runs beyond 16 groups: the decoder leaves k_attn_step
+            b2.close()
+            got1 = a.generate(got0[:, -1].astype(np.int32), 6)   # k_attn_decode, as the decoder now
+        finally:
+            a.close()
+        for i in range(len(lens)):
+            want = solo_tokens(dec, prefixes[i], first[i], 12, -1)
+            got = np.concatenate([got0[i], got1[i]])
+            assert (got == want).all(), (i, lens[i], got.tolist(), want.tolist())
+    finally:
+        dec.close()
