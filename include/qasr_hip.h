@@ -223,7 +223,11 @@ typedef struct qasr_decoder qasr_decoder;
 /* Decoder::load (decoder.rs:70-167): uploads the bf16 weights, packs every
  * projection and the LM head to int8 on the GPU, allocates a device-resident
  * KV cache of max_seq positions (f32, or bf16 when kv_bf16 != 0) and the RoPE
- * table (decoder.rs:301-338, computed on the host with libm and uploaded). */
+ * table (decoder.rs:301-338, computed on the host with libm and uploaded).
+ * max_seq is the initial capacity: a prefill, forward, generate or
+ * transcription that needs more positions doubles the cache first
+ * (KvCache::grow, decoder.rs:199-231; at least to what the call needs, in
+ * whole 256-position buckets, at most 2^20 positions), keeping every row. */
 int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
                           int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
 /* Decoder::load (decoder.rs:70-167) from a checkpoint: the reference's tensor
@@ -269,9 +273,18 @@ int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int32_t token_
  * embeds the previous token on the device.  tokens_out gets n_steps ids. */
 int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_embed, int32_t first_token,
                               int32_t n_steps, int32_t *tokens_out);
-/* kv_cache.len accessors (transcribe.rs:173, 1106) */
+/* Inspection hook with no counterpart in the reference (whose argmax_matvec_int8
+ * returns the index only): the winning logit of the last decode step's LM-head
+ * argmax (the value the returned token was chosen by), for callers and tests
+ * that check a step beyond its token id. */
+int qasr_hip_decoder_last_logit(qasr_decoder *d, float *best);
+/* kv_cache.len accessors (transcribe.rs:173, 1106); set_len stays within the
+ * current capacity */
 int qasr_hip_decoder_set_len(qasr_decoder *d, int64_t len);
 int64_t qasr_hip_decoder_len(const qasr_decoder *d);
+/* kv_cache.max_seq (decoder.rs:174-231): the positions the cache holds now
+ * (the max_seq of the kv_upload / kv_download layout); -1 for a null decoder */
+int64_t qasr_hip_decoder_capacity(const qasr_decoder *d);
 /* test hooks: the packed int8 rows / scales of layer `layer` (-1 = LM head),
  * which = 0 q, 1 k, 2 v, 3 o, 4 gate_up (interleaved), 5 down; and the KV cache
  * in the reference layout [layer][kv_head][max_seq][head_dim] as f32 (a bf16
@@ -280,6 +293,10 @@ int qasr_hip_decoder_packed(qasr_decoder *d, int layer, int which, int8_t *q_hos
                             float *scales_host);
 int qasr_hip_decoder_kv_upload(qasr_decoder *d, const float *k_host, const float *v_host);
 int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
+/* the same for positions [start, start + n) only: host [layer][kv_head][n][head_dim] */
+int qasr_hip_decoder_kv_upload_rows(qasr_decoder *d, int64_t start, int64_t n, const float *k_host,
+                                    const float *v_host);
+int qasr_hip_decoder_kv_download_rows(qasr_decoder *d, int64_t start, int64_t n, float *k_host, float *v_host);
 /* decode-step tuning: attention context splits, 1..64 (0 keeps the current
  * value, -1 restores the automatic choice per context bucket of 256
  * positions: 8 up to 1024 positions, 16 up to 2048, then about one per 64).
@@ -288,6 +305,12 @@ int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k_host, float *v_host);
  * last block per KV head merges them.  use_graph: steps replay a captured HIP
  * graph, one per context bucket (default 1). */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
+/* Profiling hook with no counterpart in the reference: in the profiling build
+ * (libqasr_hip_stamps.so, `make stamps`) the fused qkv + attention launch of
+ * every layer writes the 100 MHz real-time counter at its phase boundaries
+ * into dev ([n_layers][blocks][16] uint64, blocks = the launch's grid); null
+ * stops.  The product library returns QASR_ERR_INVALID. */
+int qasr_hip_decoder_set_stamps(qasr_decoder *d, void *dev, int64_t bytes);
 /* No counterpart in the reference (the decode step's launch shape, for tuning
  * and tests).  fuse_qkv_attention = 1 (default): each layer's RMSNorm + qkv
  * matvec and its decode attention run as one launch, the qkv rows handed to

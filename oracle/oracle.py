@@ -412,6 +412,17 @@ class OracleDecoder:
             assert a.size == self.cfg["n_layers"] * self.cfg["n_kv_heads"] * self.max_seq * self.cfg["head_dim"]
             C.memmove(lib().or_decoder_kv(self.d, which), a.ctypes.data, a.nbytes)
 
+    def kv_rows(self, start, n):
+        """Copies of positions [start, start + n): ([layer][kv_head][n][head_dim]) x 2."""
+        c = self.cfg
+        shape = (c["n_layers"], c["n_kv_heads"], self.max_seq, c["head_dim"])
+        out = []
+        for which in (0, 1):
+            p = lib().or_decoder_kv(self.d, which)
+            a = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=shape)
+            out.append(a[:, :, start:start + n].copy())
+        return out
+
     def kv(self):
         c = self.cfg
         shape = (c["n_layers"], c["n_kv_heads"], self.max_seq, c["head_dim"])

@@ -124,6 +124,11 @@ _SIGS = {
     "qasr_hip_decoder_prefill": (C.c_int, [P, P, I64]),
     "qasr_hip_decoder_forward": (C.c_int, [P, P, I32, C.POINTER(I32)]),
     "qasr_hip_decoder_generate": (C.c_int, [P, P, I32, I32, P]),
+    "qasr_hip_decoder_last_logit": (C.c_int, [P, P]),
+    "qasr_hip_decoder_capacity": (I64, [P]),
+    "qasr_hip_decoder_set_stamps": (C.c_int, [P, P, I64]),
+    "qasr_hip_decoder_kv_upload_rows": (C.c_int, [P, I64, I64, P, P]),
+    "qasr_hip_decoder_kv_download_rows": (C.c_int, [P, I64, I64, P, P]),
     "qasr_hip_decoder_set_len": (C.c_int, [P, I64]),
     "qasr_hip_decoder_len": (I64, [P]),
     "qasr_hip_decoder_packed": (C.c_int, [P, C.c_int, C.c_int, P, P]),

@@ -21,10 +21,18 @@ int qasr_fail(int code, const std::string &msg) {
 
 extern "C" const char *qasr_hip_last_error(void) { return g_err.c_str(); }
 
-int dbuf_ensure(DevBuf &b, size_t bytes) {
+// waits for the streams whose queued work may still use a buffer about to be freed
+static int sync_users(hipStream_t st, hipStream_t st2) {
+    HIPCHK(hipStreamSynchronize(st));
+    if (st2 && st2 != st) HIPCHK(hipStreamSynchronize(st2));
+    return QASR_OK;
+}
+
+int dbuf_ensure(DevBuf &b, size_t bytes, hipStream_t st, hipStream_t st2) {
     if (bytes <= b.cap) return QASR_OK;
     if (b.p) {
-        HIPCHK(hipDeviceSynchronize());   // work queued on the old buffer has finished
+        int rc = sync_users(st, st2);   // work queued on the old buffer has finished
+        if (rc != QASR_OK) return rc;
         (void)hipFree(b.p);
     }
     b.p = nullptr;
@@ -44,10 +52,11 @@ void dbuf_release(DevBuf &b) {
     b.cap = 0;
 }
 
-int hbuf_ensure(HostBuf &b, size_t bytes) {
+int hbuf_ensure(HostBuf &b, size_t bytes, hipStream_t st, hipStream_t st2) {
     if (bytes <= b.cap) return QASR_OK;
     if (b.p) {
-        HIPCHK(hipDeviceSynchronize());   // copies queued into the old buffer have finished
+        int rc = sync_users(st, st2);   // copies queued into the old buffer have finished
+        if (rc != QASR_OK) return rc;
         (void)hipHostFree(b.p);
     }
     b.p = nullptr;
@@ -92,6 +101,11 @@ extern "C" int qasr_hip_create(int device, qasr_hip **out) {
     if (e != hipSuccess) {
         qasr_hip_destroy(h);
         return qasr_fail(QASR_ERR_HIP, std::string("qasr_hip_create: ") + hipGetErrorString(e));
+    }
+    const int rc = noalloc_init_device();
+    if (rc != QASR_OK) {
+        qasr_hip_destroy(h);
+        return rc;
     }
     *out = h;
     return QASR_OK;

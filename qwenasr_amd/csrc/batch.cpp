@@ -52,14 +52,12 @@ struct qasr_batch {
     std::vector<int64_t> len;          // host copy of each stream's KV length
     int64_t steps_done = 0;            // steps since the last set of first tokens
     int n_split = 0, use_graph = 1;
-    // groups in flight per attention wave (QASR_BATCH_ATTN_DEPTH=1|2): one
-    // keeps the kernel at 4 waves per SIMD, which measured faster at 32 streams
+    // groups in flight per k_attn_decode wave: one keeps the kernel at 4 waves
+    // per SIMD, which measured faster at 32 streams than two
     int attn_depth = 1;
-    // the single-stream decoder's attention form for every stream: k_attn_step
-    // (when every bucket's partition has at most 16 groups per block and the
-    // decoder uses it) or k_attn_decode
-    bool step_layout = false;
-    std::map<int, hipGraphExec_t> graphs;                // by split count x 8 + groups per wave
+    int32_t *fault = nullptr;                            // set by an attention launch that cannot serve a stream
+    // by (split count x 8 + groups per wave) x 4 + the attention forms present
+    std::map<int, hipGraphExec_t> graphs;
     DevBuf prefill_rows;                                 // batch_prefill's staged rows, kept between calls
     std::vector<void *> allocs;
 };
@@ -103,42 +101,41 @@ static int batch_splits(const qasr_batch *b, int64_t cap) {
 // single-stream decoder's static partition: ceil(ceil(cap / 8) / splits))
 static int batch_partition(qasr_batch *b) {
     b->gpb_host.resize(b->max_seq);
-    int32_t max_gpb = 0;
     for (int64_t p = 0; p < b->max_seq; p++) {
         const int64_t cap = batch_cap(b, p);
         const int S = batch_splits(b, cap);
         b->gpb_host[p] = (int32_t)((((cap + 7) / 8) + S - 1) / S);
-        max_gpb = std::max(max_gpb, b->gpb_host[p]);
     }
     HIPCHK(hipMemcpy(b->gpb_table, b->gpb_host.data(), sizeof(int32_t) * b->max_seq, hipMemcpyHostToDevice));
-    // Every stream must decode bit-identically to its solo run on this decoder
-    // so both use one attention form: k_attn_step's when
-    // every bucket's partition fits it (the decoder then uses it in every
-    // bucket too), else the decoder's own steps switch to k_attn_decode, the
-    // form the multi-stream step then uses.
-    qasr_decoder *d = b->d;
-    b->step_layout = d->attn_step && attn_step_gpw(max_gpb) > 0;
-    if (!b->step_layout && d->attn_step) {
-        HIPCHK(hipStreamSynchronize(d->h->stream));
-        for (auto &g : d->graphs) HIPCHK(hipGraphExecDestroy(g.second));
-        d->graphs.clear();
-        d->attn_step = 0;
-    }
     return QASR_OK;
 }
 
-// whether the multi-stream step uses k_attn_step_batch: its layout fits and
-// the decoder still runs k_attn_step (another batch on the same decoder may
-// have switched it to k_attn_decode since, and then this one follows)
-static bool batch_step_layout(const qasr_batch *b) { return b->step_layout && b->d->attn_step; }
+// Every stream decodes bit-identically to its solo run on the same decoder
+// so each stream's attention takes the form the
+// single-stream decoder takes at that stream's context bucket: k_attn_step's
+// (here k_attn_step_batch) when the bucket's partition fits it, else
+// k_attn_decode's.  A step whose streams sit in buckets of both kinds runs
+// both kernels, each serving its own streams; the decoder itself is never
+// changed by a batch.
+static bool step_form(const qasr_batch *b, int64_t pos) {
+    return b->d->attn_step && attn_step_gpw(b->gpb_host[(size_t)pos]) > 0;
+}
+
+// the attention forms of step s of the current run: bit 0 some stream takes
+// the step form, bit 1 some stream takes k_attn_decode's
+static int batch_forms(const qasr_batch *b, int64_t s) {
+    int m = 0;
+    for (int64_t l : b->len) m |= step_form(b, std::min<int64_t>(l + s, b->max_seq - 1)) ? 1 : 2;
+    return m;
+}
 
 // groups per attention wave of a multi-stream step at step s of the current
-// run (k_attn_step_batch): the most any stream's partition needs
+// run (k_attn_step_batch): the most any step-form stream's partition needs
 static int batch_step_gpw(const qasr_batch *b, int64_t s) {
     int g = 1;
     for (int64_t l : b->len) {
         const int64_t p = std::min<int64_t>(l + s, b->max_seq - 1);
-        g = std::max(g, attn_step_gpw(b->gpb_host[(size_t)p]));
+        if (step_form(b, p)) g = std::max(g, attn_step_gpw(b->gpb_host[(size_t)p]));
     }
     return g;
 }
@@ -165,8 +162,6 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     b->max_steps = max_steps;
     b->len.assign(n_streams, 0);
     b->use_graph = d->use_graph;         // the decoder's setting (QASR_DISABLE_GRAPH=1 turns both off)
-    const char *ad = getenv("QASR_BATCH_ATTN_DEPTH");
-    if (ad && (ad[0] == '1' || ad[0] == '2') && ad[1] == 0) b->attn_depth = ad[0] - '0';
     const int64_t H = c.hidden, hd = c.head_dim, qd = (int64_t)c.n_heads * hd, kvd = (int64_t)c.n_kv_heads * hd;
     const int64_t I = c.intermediate, nqkv = qd + 2 * kvd;
     const int64_t kmax = std::max({H, qd, I});
@@ -193,6 +188,7 @@ extern "C" int qasr_hip_batch_create(qasr_decoder *d, int32_t n_streams, int64_t
     if (rc == QASR_OK) rc = balloc(b, &b->gpb_dev, (size_t)n_streams, true);
     if (rc == QASR_OK) rc = balloc(b, &b->order_dev, (size_t)n_streams, true);
     if (rc == QASR_OK) rc = balloc(b, &b->gpb_table, (size_t)max_seq);
+    if (rc == QASR_OK) rc = balloc(b, &b->fault, 1, true);
     if (rc == QASR_OK) {
         std::vector<int32_t> ident(n_streams);
         for (int i = 0; i < n_streams; i++) ident[i] = i;
@@ -221,7 +217,7 @@ extern "C" int qasr_hip_batch_prefill(qasr_batch *b, int32_t stream, const float
     if (stream < 0 || stream >= b->B) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: stream out of range");
     if (b->len[stream] + seq_len > b->max_seq) return qasr_fail(QASR_ERR_INVALID, "batch_prefill: capacity exceeded");
     const int64_t H = d->c.hidden, le = stream_layer_elems(b);
-    int rc0 = dbuf_ensure(b->prefill_rows, sizeof(float) * seq_len * H);
+    int rc0 = dbuf_ensure(b->prefill_rows, sizeof(float) * seq_len * H, d->h->stream);
     if (rc0 != QASR_OK) return rc0;
     float *emb = b->prefill_rows.as<float>();
     hipError_t e = hipMemcpyAsync(emb, embeds, sizeof(float) * seq_len * H, hipMemcpyHostToDevice, d->h->stream);
@@ -320,7 +316,7 @@ static bool per_layer_kind(int k) { return k >= BK_IN_QUANT && k <= BK_DOWN; }
 
 // one batched step with n_split attention splits (only kernels of one kind
 // when kind >= 0)
-static int batch_enqueue_step(qasr_batch *b, int n_split, int gpw, int kind = -1) {
+static int batch_enqueue_step(qasr_batch *b, int n_split, int gpw, int forms, int kind = -1) {
     qasr_decoder *d = b->d;
     const qasr_dec_config &c = d->c;
     hipStream_t st = d->h->stream;
@@ -351,15 +347,24 @@ static int batch_enqueue_step(qasr_batch *b, int n_split, int gpw, int kind = -1
         t.gpb_dev = b->gpb_dev;
         t.stream_order = b->order_dev;
         t.depth = b->attn_depth;
+        t.fault = b->fault;
         t.batch = B; t.batch_kv_stride = le; t.batch_qkv_stride = nqkv; t.batch_part_stride = b->part_stride;
-        // k_attn_step_batch does the q/k norm + RoPE and the K/V row write itself
-        if (batch_step_layout(b)) {
-            t.waves = 4;
-            t.gpw = gpw;
-        } else if (on(BK_PREP)) {
-            LAUNCHCHK(launch_qk_prep_rows(t, c.n_heads, c.n_kv_heads, hd, 0, st), "batch q/k prep");
+        // the step-form streams: k_attn_step_batch does their q/k norm + RoPE
+        // and K/V row write itself; the others: k_qk_prep_rows, k_attn_decode
+        const bool mixed = forms == 3;
+        if ((forms & 1) && on(BK_ATTN)) {
+            AttnDecodeArgs ts = t;
+            ts.waves = 4;
+            ts.gpw = gpw;
+            ts.select = mixed ? 1 : 0;
+            LAUNCHCHK(launch_attn_decode(ts, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
         }
-        if (on(BK_ATTN)) LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
+        if (forms & 2) {
+            t.select = mixed ? 2 : 0;
+            if (on(BK_PREP)) LAUNCHCHK(launch_qk_prep_rows(t, c.n_heads, c.n_kv_heads, hd, 0, st), "batch q/k prep");
+            if (on(BK_ATTN))
+                LAUNCHCHK(launch_attn_decode(t, c.n_heads, c.n_kv_heads, hd, 0, st, false), "batch attention");
+        }
         if (on(BK_MERGE))
             LAUNCHCHK(launch_attn_merge_rows(b->part, b->part_stride, n_split, nullptr, qd, b->xq, b->xs, B, st),
                       "batch merge+quant");
@@ -436,18 +441,19 @@ extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_token
         // the longest stream's bucket sets the split count (the largest of the
         // streams'), the longest partition the attention's groups per wave
         const int S = batch_splits(b, batch_cap(b, longest + s));
-        const int gpw = batch_step_layout(b) ? batch_step_gpw(b, s) : 0;
+        const int forms = batch_forms(b, s);
+        const int gpw = (forms & 1) ? batch_step_gpw(b, s) : 0;
         if (!b->use_graph) {
-            TRY(batch_enqueue_step(b, S, gpw));
+            TRY(batch_enqueue_step(b, S, gpw, forms));
             continue;
         }
-        const int key = S * 8 + gpw;
+        const int key = (S * 8 + gpw) * 4 + forms;
         auto it = b->graphs.find(key);
         if (it == b->graphs.end()) {
             hipGraph_t g = nullptr;
             hipGraphExec_t ge = nullptr;
             HIPCHK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-            int rc = batch_enqueue_step(b, S, gpw);
+            int rc = batch_enqueue_step(b, S, gpw, forms);
             hipError_t e = hipStreamEndCapture(st, &g);
             if (rc != QASR_OK) {
                 if (g) (void)hipGraphDestroy(g);
@@ -463,8 +469,16 @@ extern "C" int qasr_hip_batch_generate(qasr_batch *b, const int32_t *first_token
     }
     // the whole [streams][max_steps] log in one contiguous copy, then the rows
     std::vector<int32_t> log((size_t)b->B * b->max_steps);
+    int32_t fault = 0;
     HIPCHK(hipMemcpyAsync(log.data(), b->token_log, sizeof(int32_t) * log.size(), hipMemcpyDeviceToHost, st));
+    HIPCHK(hipMemcpyAsync(&fault, b->fault, sizeof(fault), hipMemcpyDeviceToHost, st));
     HIPCHK(hipStreamSynchronize(st));
+    if (fault) {
+        const int32_t z = 0;
+        HIPCHK(hipMemcpy(b->fault, &z, sizeof(z), hipMemcpyHostToDevice));
+        return qasr_fail(QASR_ERR_HIP, "batch_generate: an attention partition exceeded its launch's groups per wave; "
+                                       "the tokens of this call are not valid");
+    }
     for (int i = 0; i < b->B; i++)
         memcpy(tokens_out + (size_t)i * n_steps, log.data() + (size_t)i * b->max_steps, sizeof(int32_t) * n_steps);
     for (auto &l : b->len) l += n_steps;
@@ -496,18 +510,19 @@ extern "C" int qasr_hip_batch_profile(qasr_batch *b, const int32_t *first_tokens
     int rc = QASR_OK;
     for (int s = 0; s < n_steps && rc == QASR_OK; s++) {
         const int S = batch_splits(b, batch_cap(b, longest + s));
-        const int gpw = batch_step_layout(b) ? batch_step_gpw(b, 0) : 0;   // b->len advances per profiled step
+        const int forms = batch_forms(b, 0);                               // b->len advances per profiled step
+        const int gpw = (forms & 1) ? batch_step_gpw(b, 0) : 0;
         if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
-        if ((rc = batch_enqueue_step(b, S, gpw)) != QASR_OK) break;
+        if ((rc = batch_enqueue_step(b, S, gpw, forms)) != QASR_OK) break;
         HIPCHK(hipMemcpyAsync(st_h.data(), b->state, sizeof(int32_t) * st_h.size(), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
         for (int k = 0; k < BK_KINDS && rc == QASR_OK; k++) {
-            if (k == BK_PREP && batch_step_layout(b)) continue;   // the attention does the q/k prep
+            if (k == BK_PREP && forms == 1) continue;   // the attention does the q/k prep
             if ((rc = batch_set_state(b, tok.data())) != QASR_OK) break;
             LAUNCHCHK(launch_delay(400, st), "profile delay");
             HIPCHK(hipEventRecord(e0, st));
             const int reps = per_layer_kind(k) ? 1 : reps_once;
-            for (int r = 0; r < reps && rc == QASR_OK; r++) rc = batch_enqueue_step(b, S, gpw, k);
+            for (int r = 0; r < reps && rc == QASR_OK; r++) rc = batch_enqueue_step(b, S, gpw, forms, k);
             HIPCHK(hipEventRecord(e1, st));
             HIPCHK(hipEventSynchronize(e1));
             float ms = 0.0f;

@@ -122,6 +122,21 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 // agent-scope release fence and an acq_rel increment), and the consumer, after
 // the matching acquire, reads with agent-scope atomic loads (which miss its
 // local L2).
+// Phase stamps of the profiling build (-DQASR_STAMPS, libqasr_hip_stamps.so):
+// lane 0 of the calling wave records the 100 MHz real-time counter in
+// slot[idx].  The product build compiles them to nothing.
+#ifdef QASR_STAMPS
+#define QASR_STAMP(slot, idx)                                                         \
+    do {                                                                              \
+        if ((slot) && (threadIdx.x & 63) == 0) (slot)[idx] = __builtin_amdgcn_s_memrealtime(); \
+    } while (0)
+#else
+#define QASR_STAMP(slot, idx) \
+    do {                      \
+    } while (0)
+#endif
+#define QASR_STAMP_SLOTS 16
+
 __device__ __forceinline__ void st_agent(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

@@ -45,6 +45,95 @@ static int pack(qasr_decoder *d, const uint16_t *bf, int64_t n, int64_t k, int8_
     return QASR_OK;
 }
 
+// KV cache [layer][kv_head][cap][hd], zeroed
+static int kv_alloc(qasr_decoder *d, int64_t cap, void **kc, void **vc) {
+    const qasr_dec_config &c = d->c;
+    const size_t bytes = (size_t)c.n_layers * c.n_kv_heads * cap * c.head_dim * (d->kv_bf16 ? 2 : 4);
+    for (void **p : {kc, vc}) {
+        *p = nullptr;
+        if (hipMalloc(p, bytes) != hipSuccess) {
+            *p = nullptr;
+            return qasr_fail(QASR_ERR_NOMEM, "decoder: KV cache allocation failed");
+        }
+        d->allocs.push_back(*p);
+        HIPCHK(hipMemsetAsync(*p, 0, bytes, d->h->stream));
+    }
+    return QASR_OK;
+}
+
+// RoPE table of cap positions (RopeCache::ensure, decoder.rs:301-338) with the host libm
+static int rope_alloc(qasr_decoder *d, int64_t cap, float **rc, float **rs) {
+    const qasr_dec_config &c = d->c;
+    const int64_t hd = c.head_dim;
+    std::vector<float> cs((size_t)cap * hd), sn((size_t)cap * hd), inv(hd / 2);
+    for (int64_t i = 0; i < hd / 2; i++) inv[i] = 1.0f / powf(c.theta, (float)(2 * i) / (float)hd);
+    for (int64_t p = 0; p < cap; p++)
+        for (int64_t i = 0; i < hd / 2; i++) {
+            const float a = (float)p * inv[i];
+            const float cv = cosf(a), sv = sinf(a);
+            cs[p * hd + i] = cv; cs[p * hd + hd / 2 + i] = cv;
+            sn[p * hd + i] = sv; sn[p * hd + hd / 2 + i] = sv;
+        }
+    TRY(dalloc(d, rc, cs.size()));
+    TRY(dalloc(d, rs, sn.size()));
+    TRY(upload(d, *rc, cs.data(), sizeof(float) * cs.size()));
+    TRY(upload(d, *rs, sn.data(), sizeof(float) * sn.size()));
+    HIPCHK(hipStreamSynchronize(d->h->stream));   // the host tables go out of scope
+    return QASR_OK;
+}
+
+static void release(qasr_decoder *d, void *p) {
+    for (auto it = d->allocs.begin(); it != d->allocs.end(); ++it)
+        if (*it == p) {
+            d->allocs.erase(it);
+            (void)hipFree(p);
+            return;
+        }
+}
+
+// KvCache::grow (decoder.rs:199-231): the cache doubles (at least to `need`
+// positions, rounded up to a whole 256-position context bucket, at most 2^20)
+// when a call needs more positions than it holds.  Every position of the old
+// cache is copied to the same position of the new one, the RoPE table is
+// rebuilt for the new capacity and the captured decode steps are dropped (they
+// hold the old addresses).  The old RoPE tables stay allocated until the
+// decoder is freed: a multi-stream batch's captured steps may still read them
+// (their rows are the new table's rows).
+int decoder_reserve(qasr_decoder *d, int64_t need) {
+    if (need <= d->max_seq) return QASR_OK;
+    const int64_t limit = (int64_t)1 << 20;
+    if (need > limit) return qasr_fail(QASR_ERR_INVALID, "decoder: KV cache capacity exceeded (2^20 positions)");
+    int64_t cap = std::max<int64_t>(2 * d->max_seq, need);
+    cap = std::min<int64_t>((cap + 255) / 256 * 256, limit);
+    const qasr_dec_config &c = d->c;
+    hipStream_t st = d->h->stream;
+    HIPCHK(hipStreamSynchronize(st));
+    void *kc = nullptr, *vc = nullptr;
+    float *rc = nullptr, *rs = nullptr;
+    int32_t *log = nullptr;
+    TRY(kv_alloc(d, cap, &kc, &vc));
+    TRY(rope_alloc(d, cap, &rc, &rs));
+    TRY(dalloc(d, &log, cap));
+    const size_t esz = d->kv_bf16 ? 2 : 4, old_row = (size_t)d->max_seq * c.head_dim * esz;
+    const size_t new_row = (size_t)cap * c.head_dim * esz, heads = (size_t)c.n_layers * c.n_kv_heads;
+    HIPCHK(hipMemcpy2DAsync(kc, new_row, d->kc, old_row, old_row, heads, hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpy2DAsync(vc, new_row, d->vc, old_row, old_row, heads, hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipMemcpyAsync(log, d->token_log, sizeof(int32_t) * d->max_seq, hipMemcpyDeviceToDevice, st));
+    HIPCHK(hipStreamSynchronize(st));
+    for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
+    d->graphs.clear();
+    release(d, d->kc);
+    release(d, d->vc);
+    release(d, d->token_log);
+    d->kc = kc;
+    d->vc = vc;
+    d->rc = rc;
+    d->rs = rs;
+    d->token_log = log;
+    d->max_seq = cap;
+    return QASR_OK;
+}
+
 extern "C" int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
                                      int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out) {
     return decoder_load_impl(h, cfg, w, nullptr, 0, round_mode, max_seq, kv_bf16, out);
@@ -85,20 +174,12 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
     // do not follow graph launches)
     const char *ng = getenv("QASR_DISABLE_GRAPH");
     if (ng && ng[0] == '1') d->use_graph = 0;
-    // QASR_ATTN_WAVES=4|8: waves per decode-attention block (tuning)
-    const char *aw = getenv("QASR_ATTN_WAVES");
-    if (aw && (aw[0] == '4' || aw[0] == '8') && aw[1] == 0) d->attn_waves = aw[0] - '0';
-    // QASR_ATTN_STEP=0: the decode-step attention (and the multi-stream
-    // step's) on k_attn_decode instead of k_attn_step (tuning).  Measured on
-    // the 0.6B decode: k_attn_step with 4 waves of up to 4 groups each 5.72 /
-    // 6.50 / 7.42 us at contexts 494 / 700 / 1000 against 6.76 / 7.24 / 7.86;
-    // 8-wave blocks were slower (5.82-7.30)
-    const char *as = getenv("QASR_ATTN_STEP");
-    if (as && as[0] == '0' && as[1] == 0) d->attn_step = 0;
-    // QASR_ATTN_FUSE=0: the qkv matvec and the decode attention as two
-    // launches (tuning; qasr_hip_decoder_set_fusion sets it per decoder)
-    const char *af = getenv("QASR_ATTN_FUSE");
-    if (af && af[0] == '0' && af[1] == 0) d->attn_fuse = 0;
+    // The decode attention is k_attn_step wherever a block's run fits it (at
+    // most 16 groups of 8 positions).  Measured on the 0.6B decode: k_attn_step
+    // with 4 waves of up to 4 groups each 5.72 / 6.50 / 7.42 us at contexts
+    // 494 / 700 / 1000 against 6.76 / 7.24 / 7.86 for k_attn_decode; 8-wave
+    // blocks were slower (5.82-7.30).  qasr_hip_decoder_set_fusion selects the
+    // fused qkv + attention launch or two launches.
     int rc = decoder_build(d, w, lm_head, lm_head ? lm_rows : c.vocab);
     if (rc != QASR_OK) {
         qasr_hip_decoder_free(d);
@@ -168,40 +249,9 @@ int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm
     TRY(stg.finish());
     TRY(dalloc(d, &d->norm, H));
     TRY(upload(d, d->norm, w->norm, sizeof(float) * H));
-    // KV cache [layer][kv_head][max_seq][hd]
-    const size_t kv_elems = (size_t)c.n_layers * c.n_kv_heads * d->max_seq * hd;
-    const size_t esz = d->kv_bf16 ? 2 : 4;
-    {
-        void *p = nullptr;
-        hipError_t e = hipMalloc(&p, kv_elems * esz);
-        if (e != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "decoder: KV cache allocation failed");
-        d->allocs.push_back(p);
-        d->kc = p;
-        e = hipMalloc(&p, kv_elems * esz);
-        if (e != hipSuccess) return qasr_fail(QASR_ERR_NOMEM, "decoder: KV cache allocation failed");
-        d->allocs.push_back(p);
-        d->vc = p;
-        HIPCHK(hipMemsetAsync(d->kc, 0, kv_elems * esz, d->h->stream));
-        HIPCHK(hipMemsetAsync(d->vc, 0, kv_elems * esz, d->h->stream));
-    }
-    // RoPE table (RopeCache::ensure, decoder.rs:301-338) with the host libm
-    {
-        std::vector<float> cs((size_t)d->max_seq * hd), sn((size_t)d->max_seq * hd), inv(hd / 2);
-        for (int64_t i = 0; i < hd / 2; i++) inv[i] = 1.0f / powf(c.theta, (float)(2 * i) / (float)hd);
-        for (int64_t p = 0; p < d->max_seq; p++)
-            for (int64_t i = 0; i < hd / 2; i++) {
-                const float a = (float)p * inv[i];
-                const float cv = cosf(a), sv = sinf(a);
-                cs[p * hd + i] = cv; cs[p * hd + hd / 2 + i] = cv;
-                sn[p * hd + i] = sv; sn[p * hd + hd / 2 + i] = sv;
-            }
-        TRY(dalloc(d, &d->rc, cs.size()));
-        TRY(dalloc(d, &d->rs, sn.size()));
-        TRY(dalloc(d, &d->rope_cur, 2 * hd));
-        TRY(upload(d, d->rc, cs.data(), sizeof(float) * cs.size()));
-        TRY(upload(d, d->rs, sn.data(), sizeof(float) * sn.size()));
-        HIPCHK(hipStreamSynchronize(d->h->stream));
-    }
+    TRY(kv_alloc(d, d->max_seq, &d->kc, &d->vc));
+    TRY(rope_alloc(d, d->max_seq, &d->rc, &d->rs));
+    TRY(dalloc(d, &d->rope_cur, 2 * d->c.head_dim));
     TRY(dalloc(d, &d->x, H));
     TRY(dalloc(d, &d->qkv, nqkv));
     TRY(dalloc(d, &d->att, qd));
@@ -275,8 +325,7 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     // 1024 waves per launch (rows / 1024 rounded up to 1, 2, 4 or 8; SwiGLU
     // pairs need 2).  Measured on the 0.6B and 1.7B shapes: fewer rows per
     // wave leave each wave's fixed prologue and reductions on too little data,
-    // more leave fewer waves to stream the matrix.  QASR_MV_ROWS="q,g,d,o"
-    // overrides them for tuning.
+    // more leave fewer waves to stream the matrix.
     auto rows_for = [](int64_t rows, bool swiglu) {
         int r = 1;
         while (r < 8 && (int64_t)r * 1024 < rows) r *= 2;
@@ -286,8 +335,6 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     // repeats favours fewer blocks)
     std::array<int, 4> mv_rows{rows_for(qd + 2 * kvd, false), rows_for(2 * I, true), rows_for(H, false),
                                std::min(4, 2 * rows_for(H, false))};
-    static const char *mv_env = getenv("QASR_MV_ROWS");
-    if (mv_env) sscanf(mv_env, "%d,%d,%d,%d", &mv_rows[0], &mv_rows[1], &mv_rows[2], &mv_rows[3]);
     for (int l = 0; l < c.n_layers; l++) {
         const DecLayerDev &L = d->L[l];
         MvArgs a{};
@@ -316,7 +363,7 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         // launches nothing): the qkv rows reach the attention as tagged pairs
         if (fused_qkv_attn(d, step_kernel, mv_rows[0])) {
             if (want(0)) {
-                t.qkv_tag = d->qkv_tag; t.layer = l; t.fault = d->state + 5;
+                t.qkv_tag = d->qkv_tag; t.layer = l; t.fault = d->state + 5; t.stamps = d->stamps;
                 LAUNCHCHK(launch_qkv_attn(a, t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, embed_mode && l == 0,
                                           mv_rows[0], st),
                           "step qkv + attention");
@@ -360,7 +407,8 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         am.x = d->x; am.norm_w = d->norm; am.eps = c.eps; am.K = H; am.N = (int)d->lm_i8_rows;
         am.w = d->lm; am.ws = d->lm_s;
         am.part_val = d->am_val; am.part_idx = d->am_idx;
-        am.out_idx = d->out_idx; am.state = d->state; am.token_log = d->token_log;
+        am.out_idx = d->out_idx; am.out_val = reinterpret_cast<float *>(d->out_idx + 1);
+        am.state = d->state; am.token_log = d->token_log;
         am.rope_cos = d->rc; am.rope_sin = d->rs; am.rope_cur = d->rope_cur; am.max_pos = (int)d->max_seq;
         am.epoch = d->state + 4;
         LAUNCHCHK(launch_argmax(am, true, argmax_blocks(d->lm_i8_rows), st, want(5), want(6)), "step argmax");
@@ -444,7 +492,7 @@ extern "C" int qasr_hip_decoder_forward(qasr_decoder *d, const float *embed, int
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
     CHECK_H(d->h);
     if (!token_out) return qasr_fail(QASR_ERR_INVALID, "token_out is null");
-    if (d->len + 1 > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_forward: KV cache capacity exceeded");
+    TRY(decoder_reserve(d, d->len + 1));
     if (!embed && (token_in < 0 || token_in >= d->c.vocab))
         return qasr_fail(QASR_ERR_INVALID, "decoder_forward: token id out of range");
     TRY(set_state(d, token_in));
@@ -468,8 +516,7 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
     CHECK_H(d->h);
     if (n_steps <= 0 || !tokens_out) return qasr_fail(QASR_ERR_INVALID, "decoder_generate: bad arguments");
-    if (d->len + n_steps > d->max_seq)
-        return qasr_fail(QASR_ERR_INVALID, "decoder_generate: KV cache capacity exceeded");
+    TRY(decoder_reserve(d, d->len + n_steps));
     if (!first_embed && (first_token < 0 || first_token >= d->c.vocab))
         return qasr_fail(QASR_ERR_INVALID, "decoder_generate: token id out of range");
     TRY(set_state(d, first_token));
@@ -490,6 +537,14 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
     return QASR_OK;
 }
 
+extern "C" int qasr_hip_decoder_last_logit(qasr_decoder *d, float *best) {
+    if (!d || !best) return qasr_fail(QASR_ERR_INVALID, "decoder_last_logit: null argument");
+    CHECK_H(d->h);
+    HIPCHK(hipMemcpyAsync(best, d->out_idx + 1, sizeof(float), hipMemcpyDeviceToHost, d->h->stream));
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    return QASR_OK;
+}
+
 extern "C" int qasr_hip_decoder_set_len(qasr_decoder *d, int64_t len) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
     if (len < 0 || len > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "decoder_set_len: out of range");
@@ -498,6 +553,8 @@ extern "C" int qasr_hip_decoder_set_len(qasr_decoder *d, int64_t len) {
 }
 
 extern "C" int64_t qasr_hip_decoder_len(const qasr_decoder *d) { return d ? d->len : -1; }
+
+extern "C" int64_t qasr_hip_decoder_capacity(const qasr_decoder *d) { return d ? d->max_seq : -1; }
 
 extern "C" int qasr_hip_decoder_set_fusion(qasr_decoder *d, int fuse_qkv_attention) {
     if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
@@ -511,6 +568,30 @@ extern "C" int qasr_hip_decoder_set_fusion(qasr_decoder *d, int fuse_qkv_attenti
         d->attn_fuse = fuse_qkv_attention;
     }
     return QASR_OK;
+}
+
+// Phase stamps of the fused qkv + attention launch (the profiling build,
+// libqasr_hip_stamps.so, only): dev is a device buffer of n_layers x (the
+// launch's blocks) x QASR_STAMP_SLOTS 64-bit counters, or null to stop.
+extern "C" int qasr_hip_decoder_set_stamps(qasr_decoder *d, void *dev, int64_t bytes) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+#ifdef QASR_STAMPS
+    const qasr_dec_config &c = d->c;
+    const int64_t blocks = (int64_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim / 16 + 2 * c.n_kv_heads * 64;
+    if (dev && bytes < (int64_t)c.n_layers * blocks * QASR_STAMP_SLOTS * 8)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_set_stamps: buffer too small for every layer's blocks");
+    HIPCHK(hipStreamSynchronize(d->h->stream));
+    for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
+    d->graphs.clear();
+    d->stamps = reinterpret_cast<unsigned long long *>(dev);
+    return QASR_OK;
+#else
+    (void)dev;
+    (void)bytes;
+    return qasr_fail(QASR_ERR_INVALID, "decoder_set_stamps: this library is built without phase stamps "
+                                       "(libqasr_hip_stamps.so has them)");
+#endif
 }
 
 extern "C" int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph) {
@@ -618,6 +699,52 @@ extern "C" int qasr_hip_decoder_kv_download(qasr_decoder *d, float *k, float *v)
     return kv_copy(d, k, v, false);
 }
 
+// rows [start, start + n) of every (layer, KV head) against host [layer][kv_head][n][head_dim] f32
+static int kv_rows_copy(qasr_decoder *d, int64_t start, int64_t n, float *kh, float *vh, bool up) {
+    if (!d) return qasr_fail(QASR_ERR_INVALID, "decoder is null");
+    CHECK_H(d->h);
+    if (start < 0 || n <= 0 || start + n > d->max_seq)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_kv_rows: rows outside the cache");
+    const qasr_dec_config &c = d->c;
+    const size_t heads = (size_t)c.n_layers * c.n_kv_heads, row = (size_t)c.head_dim;
+    const size_t esz = d->kv_bf16 ? 2 : 4, width = (size_t)n * row * esz, pitch = (size_t)d->max_seq * row * esz;
+    hipStream_t st = d->h->stream;
+    std::vector<uint16_t> tmp(d->kv_bf16 ? heads * n * row : 0);
+    for (int which = 0; which < 2; which++) {
+        float *hb = which ? vh : kh;
+        char *db = reinterpret_cast<char *>(which ? d->vc : d->kc) + (size_t)start * row * esz;
+        if (!hb) continue;
+        if (!d->kv_bf16) {
+            if (up) HIPCHK(hipMemcpy2DAsync(db, pitch, hb, width, width, heads, hipMemcpyHostToDevice, st));
+            else HIPCHK(hipMemcpy2DAsync(hb, width, db, pitch, width, heads, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipStreamSynchronize(st));
+            continue;
+        }
+        if (up) {
+            for (size_t i = 0; i < tmp.size(); i++) tmp[i] = f32_to_bf16_host(hb[i]);
+            HIPCHK(hipMemcpy2DAsync(db, pitch, tmp.data(), width, width, heads, hipMemcpyHostToDevice, st));
+            HIPCHK(hipStreamSynchronize(st));
+        } else {
+            HIPCHK(hipMemcpy2DAsync(tmp.data(), width, db, pitch, width, heads, hipMemcpyDeviceToHost, st));
+            HIPCHK(hipStreamSynchronize(st));
+            for (size_t i = 0; i < tmp.size(); i++) {
+                const uint32_t u = (uint32_t)tmp[i] << 16;
+                std::memcpy(hb + i, &u, 4);
+            }
+        }
+    }
+    return QASR_OK;
+}
+
+extern "C" int qasr_hip_decoder_kv_upload_rows(qasr_decoder *d, int64_t start, int64_t n, const float *k,
+                                               const float *v) {
+    return kv_rows_copy(d, start, n, const_cast<float *>(k), const_cast<float *>(v), true);
+}
+
+extern "C" int qasr_hip_decoder_kv_download_rows(qasr_decoder *d, int64_t start, int64_t n, float *k, float *v) {
+    return kv_rows_copy(d, start, n, k, v, false);
+}
+
 // ---------------------------------------------------------------------------
 // per-kernel timing.  Each of n_steps real decode steps runs unbracketed (no
 // graph); then, from the same input state, every kernel kind is launched once
@@ -651,8 +778,6 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
         const int gpb = (int)((((cap + 7) / 8) + ns - 1) / ns);
         int qr = 1;
         while (qr < 8 && (int64_t)qr * 1024 < (int64_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim) qr *= 2;
-        static const char *mv_env = getenv("QASR_MV_ROWS");
-        if (mv_env) sscanf(mv_env, "%d", &qr);
         return fused_qkv_attn(d, d->attn_step && attn_step_gpw(gpb) > 0, qr);
     };
     bool fused = fused_at(d->len), any_fused = false;

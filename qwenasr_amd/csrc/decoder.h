@@ -47,6 +47,7 @@ struct qasr_decoder {
     int attn_step = 4;                          // 4: k_attn_step (4 waves per block); 0: k_attn_decode
     int attn_fuse = 1;                          // 1: the qkv matvec and k_attn_step in one launch
     int64_t epochs = 0;                         // steps since the tags were last cleared
+    unsigned long long *stamps = nullptr;       // profiling build: phase stamps of the fused launch
     // one captured decode step per context bucket (the attention's static
     // partition is sized for the bucket); keyed by the bucket's capacity
     std::map<int64_t, hipGraphExec_t> graphs;
@@ -58,6 +59,9 @@ struct qasr_decoder {
     std::vector<void *> allocs;
 };
 
+// Grows the KV cache (doubling, decoder.rs:199-231) so that it holds `need`
+// positions; nothing happens when it already does.
+int decoder_reserve(qasr_decoder *d, int64_t need);
 // lm_head (nullable): a separate bf16 [lm_rows, hidden] host head, packed as
 // the int8 decode head instead of the tied embedding (decoder.rs:143-157)
 int decoder_build(qasr_decoder *d, const qasr_dec_weights *w, const uint16_t *lm_head, int64_t lm_rows);

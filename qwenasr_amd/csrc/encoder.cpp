@@ -488,9 +488,9 @@ extern "C" int qasr_hip_mel(qasr_encoder *e, const float *samples, int64_t n, fl
     if (nf <= 0) return qasr_fail(QASR_ERR_INVALID, "mel: audio too short");
     *frames = nf;
     if (!mel_out) return QASR_OK;
-    TRY(dbuf_ensure(e->audio, sizeof(float) * n));
-    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf));
-    TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf)));
+    TRY(dbuf_ensure(e->audio, sizeof(float) * n, e->h->stream));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf, e->h->stream));
+    TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf), e->h->stream));
     float *dx = e->audio.as<float>(), *dm = e->mel.as<float>(), *sc = e->melsc.as<float>();
     int rc = QASR_OK;
     if (hipMemcpyAsync(dx, samples, sizeof(float) * n, hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
@@ -518,8 +518,8 @@ extern "C" int qasr_hip_encoder_forward_batch(qasr_encoder *e, int32_t n, const 
         tot_f += frames[j];
         tot_t += encoder_tokens(e, frames[j]);
     }
-    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * tot_f));
-    TRY(dbuf_ensure(e->enc_out, sizeof(float) * tot_t * e->c.output_dim));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * tot_f, e->h->stream));
+    TRY(dbuf_ensure(e->enc_out, sizeof(float) * tot_t * e->c.output_dim, e->h->stream));
     std::vector<const float *> dm(n);
     int rc = QASR_OK;
     int64_t f = 0;
@@ -549,8 +549,8 @@ extern "C" int qasr_hip_encoder_forward(qasr_encoder *e, const float *mel, int64
     CHECK_H(e->h);
     if (!mel || frames <= 0 || !out) return qasr_fail(QASR_ERR_INVALID, "encoder_forward: bad arguments");
     const int64_t T = encoder_tokens(e, frames);
-    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * frames));
-    TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * e->c.output_dim));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * frames, e->h->stream));
+    TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * e->c.output_dim, e->h->stream));
     float *dm = e->mel.as<float>(), *dout = e->enc_out.as<float>();
     int rc = QASR_OK;
     if (hipMemcpyAsync(dm, mel, sizeof(float) * 128 * frames, hipMemcpyHostToDevice, e->h->stream) != hipSuccess)
@@ -616,15 +616,15 @@ static int transcribe_begin(qasr_decoder *d, qasr_encoder *e, const float *sampl
     TRY(prompt_id_rows(prompt, past, n_past, d->c.vocab, head, tail));
     const int n_head = (int)head.size(), n_tail = (int)tail.size();
     const int64_t total = n_head + T + n_tail;
-    if (total - 1 + steps_max > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "transcribe: KV cache capacity exceeded");
+    TRY(decoder_reserve(d, total - 1 + steps_max));
     std::vector<int32_t> toks(head);
     toks.insert(toks.end(), tail.begin(), tail.end());
-    TRY(dbuf_ensure(e->audio, sizeof(float) * n));
-    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf));
-    TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf)));
-    TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * H));
-    TRY(dbuf_ensure(e->embeds, sizeof(float) * total * H));
-    TRY(dbuf_ensure(e->toks, sizeof(int32_t) * toks.size()));
+    TRY(dbuf_ensure(e->audio, sizeof(float) * n, e->h->stream, d->h->stream));
+    TRY(dbuf_ensure(e->mel, sizeof(float) * 128 * nf, e->h->stream, d->h->stream));
+    TRY(dbuf_ensure(e->melsc, sizeof(float) * mel_scratch_floats(nf), e->h->stream, d->h->stream));
+    TRY(dbuf_ensure(e->enc_out, sizeof(float) * T * H, e->h->stream, d->h->stream));
+    TRY(dbuf_ensure(e->embeds, sizeof(float) * total * H, e->h->stream, d->h->stream));
+    TRY(dbuf_ensure(e->toks, sizeof(int32_t) * toks.size(), e->h->stream, d->h->stream));
     for (hipEvent_t &v : e->ev)
         if (!v) HIPCHK(hipEventCreate(&v));
     float *dx = e->audio.as<float>(), *dmel = e->mel.as<float>(), *msc = e->melsc.as<float>();
@@ -703,12 +703,15 @@ extern "C" int qasr_hip_transcribe_prompt(qasr_decoder *d, qasr_encoder *e, cons
         int64_t done = 1, stop_at = -1;            // forwards queued; index of the stop token
         std::vector<int32_t> log;
         int64_t seen = 0;
+        int32_t fault = 0;
         while (true) {
             // read what has been produced so far
             log.resize((size_t)done);
             HIPCHK(hipMemcpyAsync(log.data() + seen, d->token_log + seen, sizeof(int32_t) * (done - seen),
                                   hipMemcpyDeviceToHost, st));
+            HIPCHK(hipMemcpyAsync(&fault, d->state + 5, sizeof(fault), hipMemcpyDeviceToHost, st));
             HIPCHK(hipStreamSynchronize(st));
+            if (fault) TRY(decoder_fault_check(d));  // a failed hand-off ends the call at once
             for (int64_t i = seen; i < done; i++)
                 if (log[(size_t)i] == TOKEN_ENDOFTEXT || log[(size_t)i] == TOKEN_IM_END) {
                     stop_at = i;

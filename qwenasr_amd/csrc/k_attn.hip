@@ -243,6 +243,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_decode(AttnDecodeArgs a) {
     float cs[16], sn[16], qn[16], kn[16], vn[16], knw[16];
     int pos, g0, g1s;
     if constexpr (DEC >= 2) {
+        if (a.select == 2 && a.gpb_dev[bs] <= QASR_STEP_MAX_GPB) return;   // k_attn_step_batch's stream
         // q first: the first group's scores wait for q and that group only
 #pragma unroll
         for (int g = 0; g < G; g++) ld16<KVT>(qkv + (kvh * G + g) * D, ds, q[g]);
@@ -546,9 +547,16 @@ __device__ __forceinline__ float2 norm_rope2(float2 x, float2 w, float2 c, float
 // zeros), so every stream gets the bits of the single-stream kernel run with
 // its own GPW.
 template <typename KVT, int NW, int GPW, bool POLL, bool BATCH = false>
-__device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk, int nblk) {
+__device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk, int nblk, int blk0 = 0) {
     constexpr int D = 128, G = 2;
     using Kp = KvPair<KVT>;
+    unsigned long long *stamp = nullptr;
+#ifdef QASR_STAMPS
+    // fused launch: slots 0-7 by wave 0, 8 by the polling wave
+    if (POLL && a.stamps) stamp = a.stamps + ((int64_t)a.layer * gridDim.x + blockIdx.x) * QASR_STAMP_SLOTS;
+    if ((threadIdx.x >> 6) == 0) QASR_STAMP(stamp, 0);
+#endif
+    (void)blk0;
     __shared__ float wm[NW], wl[NW];
     __shared__ float wacc[NW][D];
     __shared__ __attribute__((aligned(16))) float pw[NW][GPW][8];
@@ -611,10 +619,14 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
             for (int i = 0; i < 6; i++) mine &= (unsigned)(u[i] >> 32) == tag;
             return __all(mine) != 0;
         };
-        // two polls in flight: the older one is checked while the newer one travels
+        // two polls in flight: the older one is checked while the newer one travels.
+        // After a timed-out hand-off (the fault flag, cleared by the host when it
+        // reports the failure) later launches do not wait again, and a wave that
+        // has not matched its tags stores no K/V row.
         unsigned long long ua[6], ub[6], u[6];
+        bool matched = ld_agent(a.fault) == 0;
         issue(ua);
-        for (int spins = 0;; spins += 2) {
+        for (int spins = 0; matched; spins += 2) {
             __builtin_amdgcn_s_sleep(2);
             issue(ub);
             if (ready(ua)) {
@@ -631,11 +643,15 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
             }
             if (spins >= QASR_POLL_SPINS) {
                 if (lane == 0) st_agent(a.fault, 1);
-#pragma unroll
-                for (int i = 0; i < 6; i++) u[i] = ub[i];
+                matched = false;
                 break;
             }
         }
+        if (!matched) {
+#pragma unroll
+            for (int i = 0; i < 6; i++) u[i] = 0;
+        }
+        QASR_STAMP(stamp, 8);
         float2 q = make_float2(__uint_as_float((unsigned)u[0]), __uint_as_float((unsigned)u[1]));
         float2 kn = make_float2(__uint_as_float((unsigned)u[2]), __uint_as_float((unsigned)u[3]));
         float2 vn = make_float2(__uint_as_float((unsigned)u[4]), __uint_as_float((unsigned)u[5]));
@@ -649,7 +665,7 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
             vp.set(vn.x, vn.y);
             kn = make_float2(kp.x(), kp.y());
             vn = make_float2(vp.x(), vp.y());
-            if (gq == 0) {
+            if (gq == 0 && matched) {
                 Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
                 Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
             }
@@ -688,11 +704,13 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
             vr[i][p].load(vc + (int64_t)(i < gpw_own && j < max_rows ? j : 0) * D, lane);
         }
     __builtin_amdgcn_sched_barrier(0);
+    if (wid == 0) QASR_STAMP(stamp, 1);
     if (POLL) {
         __syncthreads();          // q (normed, rotated), k, v from the polling wave
         q = hq[lane];
         kn = hk[lane];
         vn = hv[lane];
+        if (wid == 0) QASR_STAMP(stamp, 2);
     }
 
     const int L = pos + 1;
@@ -755,6 +773,7 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
         r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_2301>(r3));
         sc[i] = jb + my_p < j1 ? __fmul_rn(r3, a.scale) : -INFINITY;
     }
+    if (wid == 0) QASR_STAMP(stamp, 3);
 
     // ---- softmax over this wave's positions --------------------------------
     float m = sc[0];
@@ -776,6 +795,7 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_ROR8>(l));
     l = xrow16_sum(l);
     l = xhalf_sum(l);
+    if (wid == 0) QASR_STAMP(stamp, 4);
 
     // ---- P V: probabilities from LDS (the wave's own writes) ----------------
     float ox = 0.0f, oy = 0.0f;
@@ -800,11 +820,13 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
         ox = __fadd_rn(ox, gx);
         oy = __fadd_rn(oy, gy);
     }
+    if (wid == 0) QASR_STAMP(stamp, 5);
 
     // ---- merge the waves of the block (LDS, one barrier) --------------------
     if (lane == 0) { wm[wid] = m; wl[wid] = l; }
     reinterpret_cast<float2 *>(&wacc[wid][0])[lane] = make_float2(ox, oy);
     __syncthreads();
+    if (wid == 0) QASR_STAMP(stamp, 6);
     if (t < D) {
         const int d = t;
         float m_part = -INFINITY, o_part = 0.0f, l_part = 0.0f;
@@ -822,6 +844,7 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
             part[(2 * h) * n_split + split] = m_part;
             part[(2 * h + 1) * n_split + split] = l_part;
         }
+        if (wid == 0) QASR_STAMP(stamp, 7);
     }
 }
 
@@ -864,9 +887,24 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
     float *part = a.part + bs * a.batch_part_stride;
     const float *rope_cur = a.rope_cur + 256 * bs;
     const int gpb = a.gpb_dev[bs], g0 = split * gpb, g1s = g0 + gpb;
+    if (a.select == 1 && gpb > QASR_STEP_MAX_GPB) return;     // k_attn_decode's stream this step
     const int gpw_own = (gpb + NW - 1) / NW;
     const int pos = a.state[4 * bs + 1];
     const int max_rows = min((int)(a.head_stride / D), pos + 1);
+    if (gpw_own > GPW) {
+        // a partition longer than this launch's waves hold (the host sizes GPW
+        // from its per-position table): a NaN partial and the fault flag the
+        // host checks, never a silent drop of groups
+        if (t < D) {
+            part[part_o_index_slow(n_split, split, Hq, h * D + t)] = __builtin_nanf("");
+            if (t == 0) {
+                part[(2 * h) * n_split + split] = __builtin_nanf("");
+                part[(2 * h + 1) * n_split + split] = __builtin_nanf("");
+                if (a.fault) st_agent(a.fault, 1);
+            }
+        }
+        return;
+    }
     if (8 * g0 >= max_rows) {
         // a block wholly past the stream's context: an empty partial
         if (t < D) {
@@ -1052,9 +1090,14 @@ __global__ __launch_bounds__(320) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, in
             return;
         }
         const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
-        w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, qlds, a.qkv_tag, tag);
+        unsigned long long *stamp = nullptr;
+#ifdef QASR_STAMPS
+        if (a.stamps) stamp = a.stamps + ((int64_t)a.layer * gridDim.x + blockIdx.x) * QASR_STAMP_SLOTS;
+        if ((threadIdx.x >> 6) == 0) QASR_STAMP(stamp, 0);
+#endif
+        w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, qlds, a.qkv_tag, tag, stamp);
     } else {
-        attn_step_block<KVT, 4, GPW, true>(a, blockIdx.x - n_mv, gridDim.x - n_mv);
+        attn_step_block<KVT, 4, GPW, true>(a, blockIdx.x - n_mv, gridDim.x - n_mv, n_mv);
     }
 }
 
@@ -1113,6 +1156,7 @@ __global__ __launch_bounds__(192) void k_qk_prep_rows(AttnDecodeArgs a, int Hkv)
     constexpr int D = 128, G = 2;
     using Sl = KvSlice<KVT>;
     const int bs = blockIdx.x, t = threadIdx.x;
+    if (a.select == 2 && a.gpb_dev[bs] <= QASR_STEP_MAX_GPB) return;   // prepared by k_attn_step_batch
     const int row = t >> 3, ds = t & 7, Hq = Hkv * G;
     float *qkv = const_cast<float *>(a.qkv) + bs * a.batch_qkv_stride;
     const bool isq = row < Hq;
@@ -1143,6 +1187,7 @@ hipError_t launch_qk_prep_rows(const AttnDecodeArgs &a, int n_heads, int n_kv_he
     const int nb = a.batch > 1 ? a.batch : 1;
     if (head_dim != 128 || n_kv_heads != 8 || n_heads != 16 || !a.q_norm || !a.k_norm || !a.rope_cur || !a.state)
         return hipErrorInvalidValue;
+    if (a.select != 0 && (a.select != 2 || !a.gpb_dev)) return hipErrorInvalidValue;
     if (kv_bf16) hipLaunchKernelGGL(k_qk_prep_rows<uint16_t>, dim3(nb), dim3(192), 0, st, a, n_kv_heads);
     else hipLaunchKernelGGL(k_qk_prep_rows<float>, dim3(nb), dim3(192), 0, st, a, n_kv_heads);
     return hipGetLastError();
@@ -1152,6 +1197,9 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
                               int kv_bf16, hipStream_t st, bool merge) {
     if (head_dim != 128 || n_kv_heads <= 0 || n_heads != 2 * n_kv_heads) return hipErrorInvalidValue;
     if (a.n_split <= 0 || a.n_split > ATT_MAXS) return hipErrorInvalidValue;
+    if (a.select < 0 || a.select > 2 || (a.select && !a.gpb_dev) || (a.select == 1 && a.gpw <= 0) ||
+        (a.select == 2 && a.gpw > 0))
+        return hipErrorInvalidValue;
     if (a.waves != 0 && a.waves != 4 && a.waves != 8) return hipErrorInvalidValue;
     // decode-step mode: every pointer of the fused prologue, the state and a static partition
     const bool dec = a.q_norm != nullptr;

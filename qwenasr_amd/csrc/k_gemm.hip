@@ -605,15 +605,12 @@ static hipError_t go_gemm_lds_kp(const GemmArgs &g, int epi, dim3 grid, hipStrea
 }
 
 // K groups per block of the 64 x 64 kernel: 4 while a block has at least 16
-// K-steps and the tile columns number at most 32 (QASR_GEMM_KP=1|2|4 forces
-// one).  Measured at M = 375 (config 1, us per launch, KP 1 -> 4): k / v
+// K-steps and the tile columns number at most 32.  Measured at M = 375 (config 1, us per launch, KP 1 -> 4): k / v
 // 7.7 -> 6.6, q 8.5 -> 7.5, o 12.4 -> 9.2, down 17.1 -> 11.9; gate / up (48
 // tile columns, 288 blocks of 16 waves for 256 CUs) 10.2 -> 12.2, so they
 // keep one group.  The rule reads N and K only, so a row's bits do not
 // depend on how many rows share the call.
 static int gemm_kp(const GemmArgs &g, int bk) {
-    static const int forced = [] { const char *e = getenv("QASR_GEMM_KP"); return e ? atoi(e) : 0; }();
-    if (forced == 1 || forced == 2 || forced == 4) return forced;
     return (g.K / bk >= 16 && (g.N + 63) / 64 <= 32) ? 4 : 1;
 }
 
@@ -627,8 +624,7 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     }
     // split K in two (epilogues without a transposed store)
     // when the tile grid leaves most CUs idle and the caller gave a workspace
-    // for the partials (QASR_GEMM_SPLITK=0 disables)
-    static const bool split_ok = [] { const char *e = getenv("QASR_GEMM_SPLITK"); return !(e && e[0] == '0'); }();
+    // for the partials
     // (K-steps: at least 16 of the f32-class path, whose steps cost three MFMA
     // passes; the bf16 path does not split: with its loads of the epilogue
     // operands ahead of the K loop, the unsplit kernel measured faster at
@@ -640,10 +636,10 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     if (g.split_by_shape && ASRC == A_F32_SPLIT) {
         // (the tile-count rule's choice too for N <= 1024 up to 640 rows; that
         // rule also splits N > 1024 when the rows are few enough)
-        split = split_ok && gx <= 16 && g.K / bk >= min_steps && epi_ok;
+        split = gx <= 16 && g.K / bk >= min_steps && epi_ok;
         if (split && !ws_ok) return hipErrorInvalidValue;
     } else {
-        split = ASRC == A_F32_SPLIT && split_ok && gx * gy <= 160 && g.K / bk >= min_steps && epi_ok && ws_ok;
+        split = ASRC == A_F32_SPLIT && gx * gy <= 160 && g.K / bk >= min_steps && epi_ok && ws_ok;
     }
     if (split) {
         const dim3 grid(gx, gy, 2), rg((unsigned)(((int64_t)g.M * g.N + 255) / 256));
@@ -673,17 +669,14 @@ template <int ASRC, int BSRC>
 static hipError_t go_gemm_lds(const GemmArgs &g, int epi, hipStream_t st) {
     // 64 x 64 tiles (4 stages of 12 KiB, 3 blocks per CU) while they leave
     // fewer than ~2 blocks per CU; beyond, 128 x 128 tiles (3 stages of 24
-    // KiB): four times the MFMA work per K-step and barrier.  QASR_GEMM_TILE=64|128 forces one.
-    static const int forced = [] { const char *e = getenv("QASR_GEMM_TILE"); return e ? atoi(e) : 0; }();
+    // KiB): four times the MFMA work per K-step and barrier
     const int64_t small_blocks = (int64_t)((g.N + 63) / 64) * ((g.M + 63) / 64);
-    const bool big = forced ? forced == 128 : small_blocks >= 2048;
+    const bool big = small_blocks >= 2048;
     return big ? go_gemm_lds_ns<ASRC, BSRC, 3, 128, 128>(g, epi, st) : go_gemm_lds_ns<ASRC, BSRC, 4, 64, 64>(g, epi, st);
 }
 
 // the LDS-ring kernel applies when every stage is whole and rows are 16-byte aligned
 static bool gemm_lds_ok(const GemmArgs &g, int asrc, int bsrc) {
-    static const bool off = [] { const char *e = getenv("QASR_GEMM_REG"); return e && e[0] == '1'; }();
-    if (off) return false;
     const int bk = asrc == A_F32_SPLIT ? 32 : 64;
     const int ae = asrc == A_F32_SPLIT ? 4 : 2, be = bsrc == B_BF16 ? 2 : 1;
     return g.K % bk == 0 && (g.lda * ae) % 16 == 0 && (g.ldb * be) % 16 == 0 && (uintptr_t)g.A % 16 == 0 &&

@@ -344,6 +344,7 @@ __global__ __launch_bounds__(256) void k_argmax_finish(ArgmaxArgs a, int n_parts
     if (lane == 0) {
         const int tok = bi < 0 ? 0 : bi;
         a.out_idx[0] = tok;
+        if (a.out_val) a.out_val[0] = bv;
         if (a.state) {
             a.state[0] = tok;
             a.state[1] = next_pos;

@@ -837,10 +837,9 @@ hipError_t launch_attn_rows_seqs(const AttnSeqArgs &s0, int n_kv_heads, int head
 
 hipError_t launch_attn_rows(const AttnRowsArgs &a, int n_kv_heads, int head_dim, hipStream_t st) {
     if (a.G <= 0 || 32 % a.G != 0 || a.n_q <= 0) return hipErrorInvalidValue;
-    static const bool simt = [] { const char *e = getenv("QASR_ATTN_ROWS_SIMT"); return e && e[0] == '1'; }();
     const bool aligned = a.q_rs % 4 == 0 && a.k_rs % 4 == 0 && a.k_hs % 4 == 0 && (uintptr_t)a.q % 16 == 0 &&
                          (uintptr_t)a.k % 16 == 0 && (uintptr_t)a.v % 16 == 0;
-    if (!simt && aligned && (a.G == 1 || a.G == 2) && (head_dim == 128 || head_dim == 64)) {
+    if (aligned && (a.G == 1 || a.G == 2) && (head_dim == 128 || head_dim == 64)) {
         const dim3 grid(n_kv_heads, (a.n_q + 15) / 16);
         // 128-dim decoder heads (G = 2): one query head per block, its 8 waves
         // 8 key splits (KV head x / 2); measured 30.0 us for the 404-row prefill

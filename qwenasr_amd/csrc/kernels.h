@@ -45,6 +45,7 @@ struct ArgmaxArgs {
     float *part_val;          // [gridDim.x] per-block partials, merged by k_argmax_finish
     int *part_idx;            // [gridDim.x]
     int *out_idx;             // [1]
+    float *out_val;           // nullable: [1] the winning logit
     int *state;               // nullable decode-loop state
     int *token_log;           // nullable
     const float *rope_cos, *rope_sin;   // decode loop: RoPE table [max_pos][128]
@@ -106,6 +107,10 @@ __host__ __device__ inline int64_t part_o_index(int S, int split, int Hq, int e)
     return part_split_fastest(S) ? (int64_t)(2 * Hq + e) * S + split : part_o_index_slow(S, split, Hq, e);
 }
 
+// longest run (8-position groups per block) of the single-stream step form of
+// the decode attention (k_attn_step: 4 waves of up to 4 groups)
+#define QASR_STEP_MAX_GPB 16
+
 struct AttnDecodeArgs {
     const float *qkv;         // raw projections: q [Hq*D] | k [Hkv*D] | v [Hkv*D]
     const float *q_norm, *k_norm;   // per-head RMSNorm gains [D] (nullable: skip norm+rope)
@@ -131,12 +136,22 @@ struct AttnDecodeArgs {
     const int *gpb_dev;       // nullable: per-stream groups per block [batch] (overrides gpb)
     const int *stream_order;  // nullable: grid row -> stream of a multi-stream step (largest units first)
     int depth;                // multi-stream mode: groups in flight per wave (1 or 2; 0: 2)
+    // multi-stream mode: the streams a launch serves.  A stream whose partition
+    // (gpb_dev) has at most QASR_STEP_MAX_GPB groups per block takes the
+    // single-stream step form (k_attn_step_batch), a longer one k_attn_decode's,
+    // as the single-stream decoder chooses per context bucket.  0: every stream
+    // (the step's streams all take this launch's form); 1: only the short
+    // partitions; 2: only the long ones (k_qk_prep_rows, k_attn_decode)
+    int select;
     // qkv + attention in one launch (launch_qkv_attn): the (tag, value) pairs
     // of the qkv rows, the layer (tag = state[4] * 32 + layer) and the flag a
     // poll that never matched sets
     unsigned long long *qkv_tag;
     int layer;
     int *fault;
+    // profiling build only: [layer][block][QASR_STAMP_SLOTS] phase times of the
+    // fused launch (null: none)
+    unsigned long long *stamps;
 };
 
 // one launch for a layer's RMSNorm + qkv matvec (m: the MvArgs of the plain

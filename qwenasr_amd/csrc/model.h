@@ -5,6 +5,7 @@
 #include <string>
 #include <vector>
 #include "qasr_hip.h"
+#include "kernels.h"
 
 // scratch area of a handle: argmax partials, attention partials
 #define QASR_SCRATCH_BYTES (8u << 20)
@@ -28,14 +29,15 @@ int qasr_fail(int code, const std::string &msg);
 
 // Device buffer owned by a model object and kept between calls: an entry point
 // calls hipMalloc only when it needs more bytes than any earlier call on the
-// same object (dbuf_ensure waits for the device before it frees the smaller
-// buffer), so repeated calls of one shape allocate nothing.
+// same object (dbuf_ensure waits for the streams that use the buffer, st and
+// st2 when given, before it frees the smaller one), so repeated calls of one
+// shape allocate nothing.
 struct DevBuf {
     void *p = nullptr;
     size_t cap = 0;
     template <typename T> T *as() const { return reinterpret_cast<T *>(p); }
 };
-int dbuf_ensure(DevBuf &b, size_t bytes);
+int dbuf_ensure(DevBuf &b, size_t bytes, hipStream_t st, hipStream_t st2 = nullptr);
 void dbuf_release(DevBuf &b);
 // Pinned host buffer with the same grow-only rule (device-to-host copies that
 // return without waiting land here).
@@ -44,8 +46,12 @@ struct HostBuf {
     size_t cap = 0;
     template <typename T> T *as() const { return reinterpret_cast<T *>(p); }
 };
-int hbuf_ensure(HostBuf &b, size_t bytes);
+int hbuf_ensure(HostBuf &b, size_t bytes, hipStream_t st, hipStream_t st2 = nullptr);
 void hbuf_release(HostBuf &b);
+
+// Resolves the allocation-free argmax's device scratch address on the current
+// device (qasr_hip_create calls it at set-up).
+int noalloc_init_device();
 
 // The stream's next push prefills every row instead of reusing the rows its
 // previous push left in the decoder's KV cache (another caller has written
@@ -124,7 +130,9 @@ static inline int attn_splits_auto(const qasr_dec_config &c, int64_t cap) {
 // Measured on the 0.6B decode at contexts 780-980 (1024-position bucket, 16
 // groups per block): 666 us/token with k_attn_step (fused with the qkv
 // matvec) against 702 us with k_attn_decode.
-static inline int attn_step_gpw(int64_t gpb) { return gpb <= 16 ? (int)std::max<int64_t>(1, (gpb + 3) / 4) : 0; }
+static inline int attn_step_gpw(int64_t gpb) {
+    return gpb <= QASR_STEP_MAX_GPB ? (int)std::max<int64_t>(1, (gpb + 3) / 4) : 0;
+}
 
 // blocks of the LM-head argmax grid (4 waves of 4-row groups each): 1024
 // blocks (4 per CU) stream the 0.6B LM head in 24.6 us against 26.2 us at

@@ -308,7 +308,8 @@ __device__ __forceinline__ void scatter_items(int (&v)[N][W], int (&out)[W]) {
 // ---------------------------------------------------------------------------
 template <int NS, int R, int MODE, bool NORM, bool EMBED, bool TAG = false>
 __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, int *qlds,
-                                          unsigned long long *tag_out = nullptr, unsigned tag = 0) {
+                                          unsigned long long *tag_out = nullptr, unsigned tag = 0,
+                                          unsigned long long *stamp = nullptr) {
     static_assert(!TAG || MODE == MV_PLAIN, "tagged outputs: plain rows only");
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -359,10 +360,13 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
         if (MODE == MV_BIAS) yb = __builtin_nontemporal_load(a.bias + lrow0 + item);
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (wid == 0) QASR_STAMP(stamp, 1);
     act_convert<NS, NORM, EMBED>(in, K, resid);
+    if (wid == 0) QASR_STAMP(stamp, 2);
     int xd[NS][4];
     float xs;
     act_finish_block<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, qlds, xd, &xs);
+    if (wid == 0) QASR_STAMP(stamp, 3);
     // per-lane partial dots, then one reduce-scatter: every lane ends with its
     // item's complete sums.  The epilogue runs in every lane with no branch
     // (lanes holding the same item store the same value to the same address):
@@ -397,6 +401,7 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
         }
         int av[1];
         scatter_items<NI, 1>(part, av);
+        if (wid == 0) QASR_STAMP(stamp, 4);
         float v = __fmul_rn(__fmul_rn((float)av[0], xs), ws0);
         if (MODE == MV_ADDTO || MODE == MV_BIAS) v = __fadd_rn(v, yb);
         if (TAG) {
@@ -405,6 +410,7 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
             if (live)
                 __hip_atomic_store(tag_out + row0 + item, ((unsigned long long)tag << 32) | __float_as_uint(v),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (wid == 0) QASR_STAMP(stamp, 5);
         } else {
             if (live) S.y[lrow0 + item] = v;
         }

@@ -18,7 +18,9 @@ using namespace qasr;
 static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 // device address of `scratch` per device (the host-side name is not a device
-// address), resolved once per device with that device current
+// address), resolved once per device with that device current: by
+// qasr_hip_create for its device (the library's set-up call), so that a call
+// under HIP graph capture finds it resolved, else by the first call there
 #define NOALLOC_MAX_DEVICES 64
 static void *g_scratch_dev[NOALLOC_MAX_DEVICES];
 static std::mutex g_scratch_mu;
@@ -39,6 +41,11 @@ static int scratch_for_current_device(void **ptr) {
     }
     *ptr = g_scratch_dev[dev];
     return QASR_OK;
+}
+
+int noalloc_init_device() {
+    void *p = nullptr;
+    return scratch_for_current_device(&p);
 }
 
 extern "C" int qasr_hip_argmax_int8_noalloc(void *stream, const float *x, const float *norm_w, float eps,

@@ -74,7 +74,7 @@ int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg)
     if (S <= 0) return QASR_OK;
     if (S > (1 << 30) / 8) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: too many rows");
     TRY(ensure_prefill(d, S));
-    TRY(dbuf_ensure(d->gemm_ws, sizeof(float) * 2 * (size_t)S * 1024));
+    TRY(dbuf_ensure(d->gemm_ws, sizeof(float) * 2 * (size_t)S * 1024, d->h->stream));
     hipStream_t st = d->h->stream;
     PrefillBufs &p = d->pf;
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
@@ -198,6 +198,7 @@ extern "C" int qasr_hip_decoder_prefill(qasr_decoder *d, const float *embeds, in
     CHECK_H(d->h);
     if (seq_len < 0 || (seq_len > 0 && !embeds)) return qasr_fail(QASR_ERR_INVALID, "decoder_prefill: bad arguments");
     if (seq_len == 0) return QASR_OK;
+    TRY(decoder_reserve(d, d->len + seq_len));
     TRY(ensure_prefill(d, seq_len));
     // stage the host rows in the layer-norm buffer, then run from device memory
     HIPCHK(hipMemcpyAsync(d->pf.xn, embeds, sizeof(float) * seq_len * d->c.hidden, hipMemcpyHostToDevice,
@@ -261,7 +262,7 @@ static int prefill_head_rows(qasr_decoder *d, const float *embeds, int64_t seq_l
     CHECK_H(d->h);
     if (seq_len <= 0 || !embeds) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: bad arguments");
     if (d->kv_bf16) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: needs an f32 KV cache");
-    if (d->len + seq_len > d->max_seq) return qasr_fail(QASR_ERR_INVALID, "prefill_logits: KV cache capacity exceeded");
+    TRY(decoder_reserve(d, d->len + seq_len));
     if (rows)
         for (int64_t k = 0; k < n; k++)
             if (rows[k] < 0 || rows[k] >= seq_len) return qasr_fail(QASR_ERR_INVALID, "prefill_argmax: row out of range");
@@ -273,7 +274,7 @@ static int prefill_head_rows(qasr_decoder *d, const float *embeds, int64_t seq_l
     hipStream_t st = d->h->stream;
     // one device block: logits [n][out_dim], row list [n], argmax [n]
     const size_t y_bytes = (sizeof(float) * n * out_dim + 255) / 256 * 256;
-    if (n > 0) TRY(dbuf_ensure(d->head_out, y_bytes + 2 * sizeof(int32_t) * n));
+    if (n > 0) TRY(dbuf_ensure(d->head_out, y_bytes + 2 * sizeof(int32_t) * n, d->h->stream));
     char *buf = d->head_out.as<char>();
     float *y = reinterpret_cast<float *>(buf);
     int32_t *rows_dev = reinterpret_cast<int32_t *>(buf + y_bytes), *idx_dev = rows_dev + n;

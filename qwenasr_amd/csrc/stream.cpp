@@ -202,6 +202,8 @@ static DevBuf &req_dst(EncReq &r) { return r.win >= 0 ? r.s->win[(size_t)r.win].
 // The mel and encoder of every request, up to 64 inputs per encoder pass
 // (qasr_hip_encoder_forward_batch's arithmetic: each input's rows are those of
 // an encoder call of its own).  The host slices are read before it returns.
+static hipStream_t enc_stream(qasr_decoder *d, qasr_encoder *e) { return e ? encoder_handle(e)->stream : d->h->stream; }
+
 static int encode_requests(qasr_decoder *d, qasr_encoder *e, std::vector<EncReq> &reqs, EncScratch &sc) {
     hipStream_t st = d->h->stream;
     const int64_t H = d->c.hidden;
@@ -217,9 +219,9 @@ static int encode_requests(qasr_decoder *d, qasr_encoder *e, std::vector<EncReq>
         max_f = std::max(max_f, nf);
     }
     if (live.empty()) return QASR_OK;
-    TRY(dbuf_ensure(sc.audio, sizeof(float) * tot_s));
-    TRY(dbuf_ensure(sc.mel, sizeof(float) * 128 * tot_f));
-    TRY(dbuf_ensure(sc.melsc, sizeof(float) * mel_multi_scratch_floats(tot_f, max_f)));
+    TRY(dbuf_ensure(sc.audio, sizeof(float) * tot_s, enc_stream(d, e), d->h->stream));
+    TRY(dbuf_ensure(sc.mel, sizeof(float) * 128 * tot_f, enc_stream(d, e), d->h->stream));
+    TRY(dbuf_ensure(sc.melsc, sizeof(float) * mel_multi_scratch_floats(tot_f, max_f), enc_stream(d, e), d->h->stream));
     std::vector<const float *> mels, xs;
     std::vector<float *> mels_w;
     std::vector<int64_t> frames, lens;
@@ -243,10 +245,10 @@ static int encode_requests(qasr_decoder *d, qasr_encoder *e, std::vector<EncReq>
     if (live.size() == 1) {
         // one input: its rows straight into its destination
         DevBuf &dst = req_dst(reqs[live[0]]);
-        TRY(dbuf_ensure(dst, sizeof(float) * tot_t * H));
+        TRY(dbuf_ensure(dst, sizeof(float) * tot_t * H, enc_stream(d, e), d->h->stream));
         TRY(encoder_forward_multi(e, 1, mels.data(), frames.data(), dst.as<float>(), tok.data()));
     } else {
-        TRY(dbuf_ensure(sc.out, sizeof(float) * tot_t * H));
+        TRY(dbuf_ensure(sc.out, sizeof(float) * tot_t * H, enc_stream(d, e), d->h->stream));
         int64_t row = 0;
         for (size_t g0 = 0; g0 < live.size(); g0 += QASR_ATTN_MAX_SEG) {
             const int ng = (int)std::min<size_t>(QASR_ATTN_MAX_SEG, live.size() - g0);
@@ -257,7 +259,7 @@ static int encode_requests(qasr_decoder *d, qasr_encoder *e, std::vector<EncReq>
         row = 0;
         for (size_t q = 0; q < live.size(); q++) {
             DevBuf &dst = req_dst(reqs[live[q]]);
-            TRY(dbuf_ensure(dst, sizeof(float) * tok[q] * H));
+            TRY(dbuf_ensure(dst, sizeof(float) * tok[q] * H, enc_stream(d, e), d->h->stream));
             HIPCHK(hipMemcpyAsync(dst.p, sc.out.as<float>() + row * H, sizeof(float) * tok[q] * H,
                                   hipMemcpyDeviceToDevice, st));
             row += tok[q];
@@ -349,11 +351,14 @@ static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t
     d->step_pos += 1;
     int64_t done = 1, seen = 0;
     s->host_tok.resize(max_new + DECODE_BURST + 1);
+    int32_t fault = 0;
     // tokens t_0 .. t_{max_new-1}; t_j comes from forward j + 1
     for (;;) {
         HIPCHK(hipMemcpyAsync(s->host_tok.data() + seen, d->token_log + seen, sizeof(int32_t) * (done - seen),
                               hipMemcpyDeviceToHost, st));
+        HIPCHK(hipMemcpyAsync(&fault, d->state + 5, sizeof(fault), hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
+        if (fault) TRY(decoder_fault_check(d));      // a failed hand-off ends the call at once
         bool stop = false;
         for (; seen < done && (int64_t)chunk.size() < max_new; seen++) {
             const int32_t t = s->host_tok[seen];
@@ -456,10 +461,13 @@ static int chunk_build(qasr_stream *s, const std::vector<EncReq> &reqs, const Pr
     const int64_t n_head = 9 + (int64_t)s->prompt.size(), n_suffix = 6 + (int64_t)s->force.size();
     const int64_t total_seq = n_head + enc_len + n_suffix + pl.n_prefix_tokens;
     pl.prefill_len = total_seq - 1;
-    const int64_t cap = tgt.b ? batch_max_seq(tgt.b) : d->max_seq;
-    if (pl.prefill_len + s->cfg.max_new_tokens + DECODE_BURST > cap)
-        return qasr_fail(QASR_ERR_INVALID, "stream: decoder max_seq too small for this context");
-    TRY(dbuf_ensure(s->enc_all, sizeof(float) * enc_len * H));
+    // a lone stream's decoder cache grows on demand (decoder.rs:199-231); a
+    // multi-stream slot has the batch's fixed capacity
+    const int64_t need = pl.prefill_len + s->cfg.max_new_tokens + DECODE_BURST;
+    if (!tgt.b) TRY(decoder_reserve(d, need));
+    if (need > (tgt.b ? batch_max_seq(tgt.b) : d->max_seq))
+        return qasr_fail(QASR_ERR_INVALID, "stream: the batch's max_seq is too small for this context");
+    TRY(dbuf_ensure(s->enc_all, sizeof(float) * enc_len * H, d->h->stream, s->e ? encoder_handle(s->e)->stream : nullptr));
     int64_t off = 0;
     for (auto &w : s->win) {
         HIPCHK(hipMemcpyAsync(s->enc_all.as<float>() + off * H, w.out.p, sizeof(float) * w.seq * H,
@@ -478,9 +486,9 @@ static int chunk_build(qasr_stream *s, const std::vector<EncReq> &reqs, const Pr
     for (int32_t t : toks)
         if (t < 0 || t >= d->c.vocab) return qasr_fail(QASR_ERR_INVALID, "stream: token id out of range");
     pl.last_token = toks.back();
-    TRY(dbuf_ensure(s->toks, sizeof(int32_t) * toks.size()));
+    TRY(dbuf_ensure(s->toks, sizeof(int32_t) * toks.size(), d->h->stream, s->e ? encoder_handle(s->e)->stream : nullptr));
     HIPCHK(hipMemcpyAsync(s->toks.p, toks.data(), sizeof(int32_t) * toks.size(), hipMemcpyHostToDevice, st));
-    TRY(dbuf_ensure(s->embeds, sizeof(float) * total_seq * H));
+    TRY(dbuf_ensure(s->embeds, sizeof(float) * total_seq * H, d->h->stream, s->e ? encoder_handle(s->e)->stream : nullptr));
     LAUNCHCHK(launch_build_prompt(s->embeds.as<float>(), d->embed, s->toks.as<int>(), (int)n_head,
                                   s->enc_all.as<float>(), (int)enc_len, (int)(n_suffix + pl.n_prefix_tokens), (int)H, st),
               "stream prompt");
@@ -490,8 +498,8 @@ static int chunk_build(qasr_stream *s, const std::vector<EncReq> &reqs, const Pr
     pl.cmp = 0;
     if (s->prev_prefill_len > 0) {
         pl.cmp = std::min(pl.prefill_len, s->prev_prefill_len);
-        TRY(dbuf_ensure(s->flags, sizeof(int) * pl.cmp));
-        TRY(hbuf_ensure(s->hflags, sizeof(int) * pl.cmp));
+        TRY(dbuf_ensure(s->flags, sizeof(int) * pl.cmp, d->h->stream, s->e ? encoder_handle(s->e)->stream : nullptr));
+        TRY(hbuf_ensure(s->hflags, sizeof(int) * pl.cmp, d->h->stream, s->e ? encoder_handle(s->e)->stream : nullptr));
         LAUNCHCHK(launch_row_diff(s->embeds.as<float>(), s->prev_embeds.as<float>(), pl.cmp, H, s->flags.as<int>(),
                                   st),
                   "stream row diff");

@@ -3,7 +3,7 @@ import ctypes as C
 
 import numpy as np
 
-from ._lib import (I64, QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, EncConfig, EncLayer,
+from ._lib import (F32, I64, QASR_ROUND_HALF_AWAY, DecConfig, DecLayer, DecWeights, EncConfig, EncLayer,
                    EncWeights, I32, P, Prompt, StreamConfig, check, lib)
 
 
@@ -156,6 +156,12 @@ class Decoder:
             check(lib().qasr_hip_decoder_forward(self.d, e.ctypes.data_as(P), 0, C.byref(out)))
         return int(out.value)
 
+    def last_logit(self):
+        """The winning logit of the last decode step's LM-head argmax."""
+        v = F32()
+        check(lib().qasr_hip_decoder_last_logit(self.d, C.byref(v)))
+        return float(v.value)
+
     def generate(self, n_steps, first_embed=None, first_token=0):
         """n_steps forced greedy steps with no host round trip between steps."""
         toks = np.empty(n_steps, np.int32)
@@ -183,14 +189,36 @@ class Decoder:
                                             s.ctypes.data_as(P)))
         return q, s
 
+    @property
+    def capacity(self):
+        """Positions the KV cache holds now (it doubles on demand, decoder.rs:199-231)."""
+        return int(lib().qasr_hip_decoder_capacity(self.d))
+
     def kv_shape(self):
         c = self.cfg
-        return (c["n_layers"], c["n_kv_heads"], self.max_seq, c["head_dim"])
+        return (c["n_layers"], c["n_kv_heads"], self.capacity, c["head_dim"])
 
     def kv_upload(self, k, v):
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         check(lib().qasr_hip_decoder_kv_upload(self.d, k.ctypes.data_as(P), v.ctypes.data_as(P)))
+
+    def kv_rows_upload(self, start, k, v):
+        """Overwrite positions [start, start + n) of every layer and KV head from
+        [layer][kv_head][n][head_dim] arrays."""
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        assert k.shape == v.shape and k.ndim == 4
+        check(lib().qasr_hip_decoder_kv_upload_rows(self.d, int(start), k.shape[2], k.ctypes.data_as(P),
+                                                    v.ctypes.data_as(P)))
+
+    def kv_rows_download(self, start, n):
+        c = self.cfg
+        shape = (c["n_layers"], c["n_kv_heads"], int(n), c["head_dim"])
+        k, v = np.empty(shape, np.float32), np.empty(shape, np.float32)
+        check(lib().qasr_hip_decoder_kv_download_rows(self.d, int(start), int(n), k.ctypes.data_as(P),
+                                                      v.ctypes.data_as(P)))
+        return k, v
 
     def kv_download(self):
         k = np.empty(self.kv_shape(), np.float32)

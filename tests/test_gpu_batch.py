@@ -70,10 +70,14 @@ def test_batch_matches_solo_auto(small_decoder, n_streams):
     assert len(np.unique(got)) > max(3, n_streams // 2)     # not a degenerate constant output
 
 
-@pytest.mark.parametrize("splits", [1, 3, 8, 16, 40])
+@pytest.mark.parametrize("splits", [1, 2, 3, 8, 16, 40])
 def test_batch_matches_solo_forced_splits(small_decoder, splits):
     """1, 8, 16: merged like the o_proj prologue merges; 3, 40: the
-    sequential merge kernel the single-stream decoder also uses"""
+    sequential merge kernel the single-stream decoder also uses.  Streams in
+    buckets of both attention forms share steps (short partitions on
+    k_attn_step_batch, long ones on k_attn_decode), and with 2 splits the
+    250-position stream crosses from one form to the other at position 256
+    in the middle of the call"""
     _, dec = small_decoder
     print(f"batch vs solo, 7 streams, {splits} splits", flush=True)
     lens = [3, 250, 300, 700, 1100, 1490, 1700]
@@ -198,17 +202,19 @@ def test_batch_matches_oracle(small_decoder, orc):
     assert compared >= 36, compared
 
 
-def test_batch_follows_decoder_attention_form(dev):
-    """A batch made while its decoder runs the single-stream attention form
-    (k_attn_step; the batch then uses k_attn_step_batch) keeps matching solo
-    decoding after a second batch on the same decoder, with partitions longer
-    than k_attn_step takes, has switched the decoder to k_attn_decode: the
-    first batch follows the decoder's form from its next step on."""
+def test_batch_leaves_decoder_attention_form(dev):
+    """Creating and running a batch never changes its decoder.  A second
+    batch with forced single splits (its long stream on k_attn_decode, its
+    short one on k_attn_step_batch in the same steps) runs on the decoder; an
+    earlier batch on automatic splits then keeps matching solo decoding, and
+    solo decoding on that decoder keeps the bits of a decoder that never saw
+    a batch."""
     from qwenasr_amd.model import Batch, Decoder
     from qwenasr_amd.synth import SynthDecoder
-    print("batch follows the decoder's attention form", flush=True)
+    print("batch leaves the decoder's attention form", flush=True)
     w = SynthDecoder(SMALL, seed=1005)
     dec = Decoder(dev, w, max_seq=2048)
+    ref = Decoder(dev, w, max_seq=2048)
     try:
         r = rng(1006)
         H = SMALL["hidden"]
@@ -219,16 +225,25 @@ def test_batch_follows_decoder_attention_form(dev):
         try:
             for i, p in enumerate(prefixes):
                 a.prefill(i, p)
-            got0 = a.generate(first, 6)                  # k_attn_step_batch
+            got0 = a.generate(first, 6)
             b2 = Batch(dec, 2, 2048, max_steps=6)
-            b2.set_options(attn_splits=1)                # runs beyond 16 groups: the decoder leaves k_attn_step
-            b2.close()
-            got1 = a.generate(got0[:, -1].astype(np.int32), 6)   # k_attn_decode, as the decoder now
+            try:
+                b2.set_options(attn_splits=1)        # runs past 16 groups per block: k_attn_decode
+                b2.prefill(0, prefixes[0])
+                b2.prefill(1, prefixes[3][:40])      # a 40-position run fits k_attn_step_batch
+                got_b2 = b2.generate(first[[0, 3]], 6)
+            finally:
+                b2.close()
+            got1 = a.generate(got0[:, -1].astype(np.int32), 6)
         finally:
             a.close()
         for i in range(len(lens)):
-            want = solo_tokens(dec, prefixes[i], first[i], 12, -1)
+            want = solo_tokens(ref, prefixes[i], first[i], 12, -1)
             got = np.concatenate([got0[i], got1[i]])
             assert (got == want).all(), (i, lens[i], got.tolist(), want.tolist())
+            assert (solo_tokens(dec, prefixes[i], first[i], 12, -1) == want).all(), i
+        assert (got_b2[0] == solo_tokens(ref, prefixes[0], first[0], 6, 1)).all()
+        assert (got_b2[1] == solo_tokens(ref, prefixes[3][:40], first[3], 6, 1)).all()
     finally:
         dec.close()
+        ref.close()

@@ -60,9 +60,16 @@ def test_kv_upload_download_bf16(dev):
 MARGIN_BOUND = 3e-3
 
 
-def teacher_forced(dev, orc, w, L0, n, max_seq, seed):
+def teacher_forced(dev, orc, w, L0, n, max_seq, seed, noise=None):
     """n teacher-forced steps from an L0-position N(0,1) bf16 context; returns
-    (oracle tokens, GPU tokens, relative top-2 margins, GPU KV, oracle KV)."""
+    (oracle tokens, GPU tokens, relative top-2 margins, GPU KV, oracle KV).
+    With noise (a dict), every oracle step first runs once from the same
+    state with its input embedding scaled by (1 + 1e-6 N(0, 1)); that run's
+    token, relative winning-logit change and deeper-layer new-row deviation
+    are appended to noise["tokens"], ["logit"], ["rows"], and the GPU's own
+    per-step winning-logit and new-row deviations to noise["gpu_logit"],
+    ["gpu_rows"] (the GPU's state is not synchronised: over these few steps
+    its rows stay the oracle's up to that noise)."""
     from qwenasr_amd.model import Decoder
     gpu = Decoder(dev, w, max_seq=max_seq, kv_bf16=True)
     cpu = orc.OracleDecoder(w, max_seq=max_seq, kv_bf16=True)
@@ -79,10 +86,27 @@ def teacher_forced(dev, orc, w, L0, n, max_seq, seed):
         cpu.kv_len = L0
         tok = 17
         tc, tg, margins = [], [], []
+        rn = rng(seed + 1)
         for s in range(n):
             e = cpu.embed(tok)
+            p = L0 + s
+            if noise is not None:
+                ep = (e * (1.0 + 1e-6 * rn.standard_normal(e.shape))).astype(np.float32)
+                t_n, best_n, _ = cpu.forward_logits(ep)
+                kn, vn = cpu.kv_rows(p, 1)
+                cpu.kv_len = p
             t_c, best, second = cpu.forward_logits(e)
             t_g = gpu.forward(token=tok) if s else gpu.forward(embed=e)
+            if noise is not None:
+                k1, v1 = cpu.kv_rows(p, 1)
+                kg1, vg1 = gpu.kv_rows_download(p, 1)
+                dev_rows = lambda a, b: max(float(np.linalg.norm(x[1:] - y[1:]) / np.linalg.norm(y[1:]))
+                                            for x, y in zip(a, b))
+                noise.setdefault("tokens", []).append(t_n)
+                noise.setdefault("logit", []).append(abs(best_n - best) / abs(best))
+                noise.setdefault("rows", []).append(dev_rows((kn, vn), (k1, v1)))
+                noise.setdefault("gpu_logit", []).append(abs(gpu.last_logit() - best) / abs(best))
+                noise.setdefault("gpu_rows", []).append(dev_rows((kg1, vg1), (k1, v1)))
             tc.append(t_c)
             tg.append(t_g)
             margins.append((best - second) / max(abs(best), 1e-30))
@@ -142,3 +166,34 @@ def test_decoder_1p7b_long_context(dev, orc, L0):
     assert (vg[0, :, L0:L0 + 8] == vc[0, :, L0:L0 + 8]).all()
     np.testing.assert_allclose(kg[0, :, L0:L0 + 8], kc[0, :, L0:L0 + 8], rtol=2 ** -7, atol=1e-6)
     check_deeper_rows(kg, vg, kc, vc, L0, 8)
+
+
+def test_decoder_1p7b_full_depth_2048_bucket(dev, orc):
+    """All 28 layers at 1.7B width: 8 teacher-forced steps from a 1900-position
+    N(0,1) bf16 context, so every step runs in the 2048-position bucket (16
+    attention splits merged in the o_proj prologue) through the fused qkv +
+    attention launch at hidden 2048.  28 random-init layers amplify ulp-sized
+    differences within one step (the oracle, perturbed by 1e-6 at its input,
+    moves the deeper rows and the winning logit measurably), so the GPU is
+    held to that sensitivity: argmax flips at clear-gap steps at most twice
+    the perturbed oracle's plus one, the winning logit's and the deeper new
+    rows' deviations within twice the perturbed oracle's largest (plus 1e-6),
+    layer 0's rows as in the 2-layer tests."""
+    from qwenasr_amd.synth import SynthDecoder
+    print("1.7B 28 layers, L0 1900", flush=True)
+    w = SynthDecoder(dict(CFG_1P7B, n_layers=28), seed=1007)
+    L0, n = 1900, 8
+    noise = {}
+    tc, tg, margins, (kg, vg), (kc, vc) = teacher_forced(dev, orc, w, L0, n, 2048, 1907, noise)
+    clear = [s for s, m in enumerate(margins) if m > MARGIN_BOUND]
+    flips = [s for s in clear if tc[s] != tg[s]]
+    noisy_flips = [s for s in clear if noise["tokens"][s] != tc[s]]
+    print(f"clear steps {clear}, GPU flips {flips}, perturbed-oracle flips {noisy_flips}; winning logit GPU "
+          f"{max(noise['gpu_logit']):.3g} oracle {max(noise['logit']):.3g}; rows GPU {max(noise['gpu_rows']):.3g} "
+          f"oracle {max(noise['rows']):.3g}", flush=True)
+    assert len(clear) >= 6, margins
+    assert len(flips) <= 2 * len(noisy_flips) + 1, flips
+    assert max(noise["gpu_logit"]) <= 2 * max(noise["logit"]) + 1e-6
+    assert max(noise["gpu_rows"]) <= 2 * max(noise["rows"]) + 1e-6
+    assert (vg[0, :, L0:L0 + n] == vc[0, :, L0:L0 + n]).all()
+    np.testing.assert_allclose(kg[0, :, L0:L0 + n], kc[0, :, L0:L0 + n], rtol=2 ** -7, atol=1e-6)

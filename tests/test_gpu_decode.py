@@ -125,13 +125,43 @@ def test_generate_matches_forward(tiny_models):
     gpu.set_options(use_graph=True)
 
 
-def test_kv_capacity_error(tiny_models):
+def test_kv_cache_grows(dev):
+    """KvCache::grow (decoder.rs:199-231): a decoder created with room for 256
+    positions prefills 100 rows, generates 500 tokens in one call (the cache
+    grows to 768 positions first), then decodes step by step past 768 (it
+    doubles to 1536 on the way); a decoder created with 1024 positions and
+    driven the same way gives the same tokens and, row for row, the same KV
+    cache.  Capacity beyond 2^20 positions is refused before anything is
+    allocated."""
     from qwenasr_amd import QasrError
-    _, gpu, _ = tiny_models
-    gpu.kv_len = 512
-    with pytest.raises(QasrError):
-        gpu.forward(token=1)
-    gpu.kv_len = 0
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    print("KV cache growth 256 -> 768 -> 1536", flush=True)
+    w = SynthDecoder(TINY, seed=1021)
+    prompt = (rng(1022).standard_normal((100, TINY["hidden"])) * 0.5).astype(np.float32)
+    runs = []
+    for cap0 in (256, 1024):
+        d = Decoder(dev, w, max_seq=cap0)
+        try:
+            d.prefill(prompt)
+            toks = list(d.generate(500, first_token=7))
+            caps = [d.capacity]
+            for _ in range(180):                      # positions 600..779
+                toks.append(d.forward(token=toks[-1]))
+            caps.append(d.capacity)
+            k, v = d.kv_download()
+            n = d.kv_len
+            with pytest.raises(QasrError, match="capacity"):
+                d.generate((1 << 20) + 1, first_token=1)
+        finally:
+            d.close()
+        runs.append((toks, caps, k[:, :, :n], v[:, :, :n], n))
+    (ta, ca, ka, va, na), (tb, cb, kb, vb, nb) = runs
+    assert ca == [768, 1536] and cb == [1024, 1024], (ca, cb)
+    assert na == nb == 780
+    assert ta == tb
+    assert ka.tobytes() == kb.tobytes() and va.tobytes() == vb.tobytes()
+    assert len(set(ta)) > 10
 
 
 @pytest.mark.parametrize("hidden,kv_bf16", [(1024, False), (1024, True), (2048, True)])
