@@ -118,11 +118,14 @@ def main():
     dec.kv_len = prompt + max(0, (args.decode_steps - args.profile_steps) // 2)
     prof = profile_decoder(dec, args.profile_steps)
     # the qkv matvec and the attention run as one launch (kind 0) when the
-    # attention kind launched nothing
+    # attention kind launched nothing; the qkv matvec is then also timed as its
+    # own launch (not part of the step) for the int8 matvec aggregate
     fused = prof[1]["per_step"] == 0
+    qkv_own = [p for p in prof if p["kernel"] == "norm+qkv (own launch)"][0]
+    qkv_own["gbs"] = qkv_own["bytes"] / (qkv_own["us"] * 1e3) if qkv_own["us"] > 0 else 0.0
     if fused:
         prof[0]["kernel"] = "norm+qkv+attention"
-        prof = [p for p in prof if p["per_step"] > 0]
+    prof = [p for p in prof if p["per_step"] > 0]
     for p in prof:
         p["gbs"] = p["bytes"] / (p["us"] * 1e3) if p["us"] > 0 else 0.0
         p["us_per_token"] = p["us"] * p["per_step"]
@@ -136,14 +139,17 @@ def main():
             "traffic": traffic, "traffic_source": traffic_src,
             "us_per_launch": round(dom["us"], 3), "bytes_per_launch": dom["bytes"]}
     lm = [p for p in prof if p["kernel"].endswith("lm_head_argmax")][0]
-    # pure int8 matvec launches (with the fused launch, the qkv matvec shares
-    # its launch with the attention and is not separable)
+    # every int8 matvec of a token as a pure matvec launch: q/k/v (with the
+    # fused step, timed as its own launch), o, gate/up, down and the LM head
     mv = [p for p in prof if "attention" not in p["kernel"] and p["kernel"] != "argmax_merge"]
-    mv_bytes = sum(p["bytes"] * p["per_step"] for p in mv)
-    mv_us = sum(p["us_per_token"] for p in mv)
+    mv_n = [(p, p["per_step"]) for p in mv] + ([(qkv_own, prof[0]["per_step"])] if fused else [])
+    mv_bytes = sum(p["bytes"] * n for p, n in mv_n)
+    mv_us = sum(p["us"] * n for p, n in mv_n)
     matvec = {"gbs": round(mv_bytes / (mv_us * 1e3), 1), "frac": round(mv_bytes / (mv_us * 1e3) / HBM_PEAK_GBS, 4),
-              "kernels": [p["kernel"] for p in mv],
+              "kernels": [p["kernel"] for p, _ in mv_n],
               "bytes_per_token": mv_bytes, "us_per_token": round(mv_us, 2),
+              "qkv_own_launch": {"us": round(qkv_own["us"], 3), "bytes": qkv_own["bytes"],
+                                 "gbs": round(qkv_own["gbs"], 1)},
               "lm_head_gbs": round(lm["gbs"], 1), "lm_head_frac": round(lm["gbs"] / HBM_PEAK_GBS, 4)}
     stream_bytes = sum(p["bytes"] * p["per_step"] for p in prof)
     step_us = sum(p["us_per_token"] for p in prof)

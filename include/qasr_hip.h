@@ -306,9 +306,10 @@ int qasr_hip_decoder_kv_download_rows(qasr_decoder *d, int64_t start, int64_t n,
  * graph, one per context bucket (default 1). */
 int qasr_hip_decoder_set_options(qasr_decoder *d, int attn_splits, int use_graph);
 /* Profiling hook with no counterpart in the reference: in the profiling build
- * (libqasr_hip_stamps.so, `make stamps`) the fused qkv + attention launch of
- * every layer writes the 100 MHz real-time counter at its phase boundaries
- * into dev ([n_layers][blocks][16] uint64, blocks = the launch's grid); null
+ * (libqasr_hip_stamps.so, `make stamps`) the decode step's fused qkv +
+ * attention, o_proj, gate_up and down launches of every layer write the 100 MHz
+ * real-time counter at their phase boundaries into dev ([4 kinds][n_layers]
+ * [2048 blocks][16] uint64; a launch uses its first gridDim.x blocks); null
  * stops.  The product library returns QASR_ERR_INVALID. */
 int qasr_hip_decoder_set_stamps(qasr_decoder *d, void *dev, int64_t bytes);
 /* No counterpart in the reference (the decode step's launch shape, for tuning
@@ -320,10 +321,12 @@ int qasr_hip_decoder_set_fusion(qasr_decoder *d, int fuse_qkv_attention);
 /* per-kernel timing over n_steps real decode steps from the current KV length
  * (no graph).  After each step every kernel kind is launched once per layer
  * (the LM head n_layers times) back to back between two HIP events on the
- * handle's stream, from the step's input state.  Kinds: 0 norm+qkv, 1
- * attention, 2 o_proj, 3 norm+gate_up+swiglu, 4 down, 5 norm+LM-head argmax
- * streaming pass, 6 argmax merge (+ step-state update).  Outputs average us
- * per launch, algorithmic bytes per launch and launches per step (7 entries
+ * handle's stream, from the step's input state.  Kinds: 0 norm+qkv (with the
+ * fused launch: norm+qkv+attention), 1 attention (with the fused launch:
+ * nothing), 2 o_proj, 3 norm+gate_up+swiglu, 4 down, 5 norm+LM-head argmax
+ * streaming pass, 6 argmax merge (+ step-state update), 7 norm+qkv as its own
+ * launch (not part of a fused step: launches_per_step 0).  Outputs average us
+ * per launch, algorithmic bytes per launch and launches per step (8 entries
  * each).  The KV length is restored afterwards. */
 int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float *us_per_launch,
                              double *bytes_per_launch, int32_t *launches_per_step);

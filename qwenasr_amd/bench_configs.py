@@ -1,5 +1,6 @@
 """Measurement harness for the BASELINE configs other than the headline.
 
+    python -m qwenasr_amd.bench_configs config0 [reps]
     python -m qwenasr_amd.bench_configs config1 [reps]
     python -m qwenasr_amd.bench_configs config3 [n_layers] [steps]
     python -m qwenasr_amd.bench_configs config4 [n_streams] [steps] [attn_splits]
@@ -64,6 +65,7 @@ import numpy as np
 
 from . import Device
 from . import kernels as K
+from ._lib import check
 from .model import Batch, Decoder, Encoder, Stream, profile_decoder
 from .synth import DEC_0_6B, DEC_1_7B, ENC_0_6B, SynthDecoder, SynthEncoder, audio, normal_bf16
 
@@ -73,6 +75,101 @@ BF16_PEAK_TFLOPS = 2500.0
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def config0(reps=256, mall_mib=256):
+    """one Qwen3-0.6B decoder layer's int8 matvecs at batch
+    1 through the operator entry points (the reference's kernels:: calls of
+    decoder_forward): q 1024->2048, k and v 1024->1024, o 2048->1024 (+=),
+    gate/up 1024->3072 (SwiGLU over interleaved rows), down 3072->1024 (+=),
+    and the LM-head argmax 1024->151936; the q/k/v as one fused call too.
+    Weights N(0,0.02) bf16 packed per row on the GPU; activation N(0,1) f32.
+    Each projection rotates over enough distinct device copies of its weights
+    (at least 32, and together more than twice the 256 MiB Infinity Cache) that
+    every launch streams its matrix from HBM.  Timed with HIP events over
+    `reps` back-to-back launches (kernel plus the queue's inter-dispatch gap,
+    the per-kernel method of bench.py); GB/s = algorithmic bytes (int8 W N*K +
+    scales 4N + x 4K + y 4N, +4N read for +=, +4K gains for a fused RMSNorm)
+    per launch / time."""
+    dev = Device(0)
+    H, qd, kvd, I, V = 1024, 2048, 1024, 3072, 151936
+    x = dev.upload(np.random.default_rng(1000).standard_normal(I).astype(np.float32))
+    g = dev.upload(np.random.default_rng(1001).uniform(0.5, 1.5, H).astype(np.float32))
+    y = dev.empty(V, np.float32)
+    idx = dev.zeros(1, np.int32)
+    from ._lib import lib
+    shapes = [("q", qd, H, "plain"), ("k", kvd, H, "plain"), ("v", kvd, H, "plain"), ("o", H, qd, "addto"),
+              ("gate_up", 2 * I, H, "swiglu"), ("down", H, I, "addto"), ("qkv", qd + 2 * kvd, H, "qkv"),
+              ("lm_head", V, H, "argmax")]
+    rows, layer_bytes, layer_us = [], 0.0, 0.0
+    for name, N, Kd, kind in shapes:
+        wb = dev.upload(normal_bf16((N, Kd), 1000, f"w0_{name}"))
+        q0 = dev.empty((N, Kd), np.int8)
+        s0 = dev.empty(N, np.float32)
+        K.quantize_bf16_weights_to_int8(wb, N, Kd, q0, s0)
+        wb.free()
+        per = N * Kd
+        n_copies = max(32, -(-2 * (mall_mib << 20) // per))
+        copies = []
+        for _ in range(n_copies):
+            qc, sc = dev.empty((N, Kd), np.int8), dev.empty(N, np.float32)
+            dev.copy(qc, q0)
+            dev.copy(sc, s0)
+            copies.append((qc, sc))
+        dev.sync()
+        h = dev.h
+
+        def launch(i):
+            qw, sw = copies[i % n_copies]
+            if kind == "plain":
+                check(lib().qasr_hip_linear_int8(h, y.ptr, x.ptr, qw.ptr, sw.ptr, None, Kd, N))
+            elif kind == "addto":
+                check(lib().qasr_hip_linear_int8_addto(h, y.ptr, x.ptr, qw.ptr, sw.ptr, Kd, N))
+            elif kind == "swiglu":
+                check(lib().qasr_hip_rmsnorm_linear_int8_swiglu(h, y.ptr, x.ptr, g.ptr, 1e-6, qw.ptr,
+                                                                sw.ptr, Kd, N // 2))
+            elif kind == "qkv":
+                check(lib().qasr_hip_rmsnorm_linear_int8_qkv(
+                    h, y.ptr, y.offset(qd), y.offset(qd + kvd), x.ptr, g.ptr, 1e-6, qw.ptr, sw.ptr,
+                    qw.offset(qd * H), sw.offset(qd), qw.offset((qd + kvd) * H), sw.offset(qd + kvd), H, qd, kvd))
+            else:
+                check(lib().qasr_hip_rmsnorm_argmax_int8(h, x.ptr, g.ptr, 1e-6, qw.ptr, sw.ptr, Kd, N,
+                                                         idx.ptr))
+        for i in range(n_copies):           # warm-up: every copy once
+            launch(i)
+        dev.sync()
+        dev.timer_start()
+        for i in range(reps):
+            launch(i)
+        ms = dev.timer_stop() / reps
+        byts = per + 4.0 * N + 4.0 * Kd + (4.0 * N if kind != "argmax" else 0.0)
+        if kind == "addto":
+            byts += 4.0 * N
+        if kind in ("swiglu", "qkv", "argmax"):
+            byts += 4.0 * Kd
+        if kind == "swiglu":
+            byts -= 2.0 * N                  # N/2 outputs
+        gbs = byts / (ms * 1e6)
+        r = dict(shape=name, N=N, K=Kd, copies=n_copies, us=round(ms * 1e3, 3), bytes=byts, gbs=round(gbs, 1),
+                 frac=round(gbs / HBM_PEAK_GBS, 4))
+        rows.append(r)
+        if name in ("q", "k", "v", "o", "gate_up", "down"):
+            layer_bytes += byts
+            layer_us += ms * 1e3
+        log(f"[config0] {name:8s} {N:6d}x{Kd:4d} x{n_copies:3d} copies: {r['us']:8.3f} us  {r['gbs']:8.1f} GB/s "
+            f"({100 * r['frac']:.1f}% of 8 TB/s)")
+        for qc, sc in copies:
+            qc.free()
+            sc.free()
+        q0.free()
+        s0.free()
+    layer = dict(bytes=layer_bytes, us=round(layer_us, 3), gbs=round(layer_bytes / (layer_us * 1e3), 1),
+                 frac=round(layer_bytes / (layer_us * 1e3) / HBM_PEAK_GBS, 4))
+    log(f"[config0] one layer (q, k, v, o, gate_up, down as separate launches): {layer['us']:.2f} us, "
+        f"{layer['gbs']:.1f} GB/s")
+    print(json.dumps({"config": "config 0: one 0.6B layer's int8 matvecs at batch 1 (operator entry points)",
+                      "results": rows, "layer": layer}))
+    dev.close()
 
 
 def config1(reps=20):
@@ -463,7 +560,9 @@ def load(reps=3):
 
 if __name__ == "__main__":
     what = sys.argv[1] if len(sys.argv) > 1 else "config3"
-    if what == "config1":
+    if what == "config0":
+        config0(int(sys.argv[2]) if len(sys.argv) > 2 else 256)
+    elif what == "config1":
         config1(int(sys.argv[2]) if len(sys.argv) > 2 else 20)
     elif what == "config3":
         config3(int(sys.argv[2]) if len(sys.argv) > 2 else 28, int(sys.argv[3]) if len(sys.argv) > 3 else 20)

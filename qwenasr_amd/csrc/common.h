@@ -136,6 +136,32 @@ __device__ __forceinline__ float sqrt_rn(float x) {
     } while (0)
 #endif
 #define QASR_STAMP_SLOTS 16
+#define QASR_STAMP_BLOCKS 2048
+
+// Reads one dword of every 64-byte line of the first NBYTES bytes of the
+// kernel arguments in one batch and waits once: arguments read later hit the
+// scalar cache.  For kernels whose argument reads the compiler would otherwise
+// split into several dependent batches, each a memory round trip.
+template <int NBYTES>
+__device__ __forceinline__ void kernarg_touch() {
+    static_assert(NBYTES <= 8 * 64, "at most 8 lines");
+#if defined(__HIP_DEVICE_COMPILE__)
+    typedef const uint32_t __attribute__((address_space(4))) *ka_ptr;   // the constant (kernarg) space
+    const ka_ptr ka = (ka_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+    constexpr int L = (NBYTES + 63) / 64;
+    uint32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = i < L ? ka[16 * i] : 0u;
+    // every value an operand of its own: the loads go out together, one wait
+    asm volatile("" ::"s"(v[0]), "s"(v[1]), "s"(v[2]), "s"(v[3]), "s"(v[4]), "s"(v[5]), "s"(v[6]), "s"(v[7]));
+#endif
+}
+
+// RMSNorm's LDS transpose (16 rows of the K/16 slots): rows padded by 4
+// floats so that the 16 lanes reading one row each start on different banks;
+// floats per wave for NS 1024-element slot groups
+#define QASR_NORM_PAD 4
+#define QASR_NORM_LDS(NS) (16 * (64 * (NS) + QASR_NORM_PAD))
 
 __device__ __forceinline__ void st_agent(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -305,6 +305,12 @@ int64_t decoder_ctx_cap(const qasr_decoder *d, int64_t L) {
     return std::min<int64_t>(std::max<int64_t>(c, 256), d->max_seq);
 }
 
+// profiling build: the phase stamps of kernel kind k (0 the fused qkv +
+// attention launch, 1 o_proj, 2 gate_up, 3 down), each [layer][QASR_STAMP_BLOCKS][slots]
+static unsigned long long *stamp_region(const qasr_decoder *d, int k) {
+    return d->stamps ? d->stamps + (size_t)k * d->c.n_layers * QASR_STAMP_BLOCKS * QASR_STAMP_SLOTS : nullptr;
+}
+
 int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
     const qasr_dec_config &c = d->c;
     const int H = c.hidden, hd = c.head_dim, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
@@ -361,9 +367,15 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         }
         // the qkv matvec and k_attn_step as one launch (kind 0; kind 1 then
         // launches nothing): the qkv rows reach the attention as tagged pairs
+        if (only_kind == 7) {
+            // profile only: the RMSNorm + qkv matvec as its own launch (the
+            // two-launch form's first kernel), whatever form the step uses
+            LAUNCHCHK(launch_w8a8(a, MV_PLAIN, true, embed_mode && l == 0, mv_rows[0], st), "profile qkv");
+            continue;
+        }
         if (fused_qkv_attn(d, step_kernel, mv_rows[0])) {
             if (want(0)) {
-                t.qkv_tag = d->qkv_tag; t.layer = l; t.fault = d->state + 5; t.stamps = d->stamps;
+                t.qkv_tag = d->qkv_tag; t.layer = l; t.fault = d->state + 5; t.stamps = stamp_region(d, 0);
                 LAUNCHCHK(launch_qkv_attn(a, t, c.n_heads, c.n_kv_heads, hd, d->kv_bf16, embed_mode && l == 0,
                                           mv_rows[0], st),
                           "step qkv + attention");
@@ -375,7 +387,7 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
         }
         if (want(2)) {
             if (fused_merge) {
-                OprojMergeArgs om{d->part, n_split, c.n_kv_heads, L.wo, L.so, d->x, H};
+                OprojMergeArgs om{d->part, n_split, c.n_kv_heads, L.wo, L.so, d->x, H, stamp_region(d, 1), l};
                 LAUNCHCHK(launch_oproj_merge(om, mv_rows[3], st), "step o_proj");
             } else {
                 LAUNCHCHK(launch_attn_merge_rows(d->part, 0, n_split, d->att, qd, nullptr, nullptr, 1, st),
@@ -392,6 +404,8 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             g.x = d->x; g.norm_w = L.post_norm; g.eps = c.eps; g.K = H;
             g.seg[0] = {L.wgu, L.sgu, d->ffn, 2 * I};
             g.n_total = 2 * I;
+            g.stamps = stamp_region(d, 2);
+            g.layer = l;
             LAUNCHCHK(launch_w8a8(g, MV_SWIGLU, true, false, mv_rows[1], st), "step gate_up");
         }
         if (want(4)) {
@@ -399,6 +413,8 @@ int decoder_enqueue_step(qasr_decoder *d, bool embed_mode, int only_kind) {
             dn.x = d->ffn; dn.K = I;
             dn.seg[0] = {L.wdown, L.sdown, d->x, H};
             dn.n_total = H;
+            dn.stamps = stamp_region(d, 3);
+            dn.layer = l;
             LAUNCHCHK(launch_w8a8(dn, MV_ADDTO, false, false, mv_rows[2], st), "step down");
         }
     }
@@ -579,8 +595,10 @@ extern "C" int qasr_hip_decoder_set_stamps(qasr_decoder *d, void *dev, int64_t b
 #ifdef QASR_STAMPS
     const qasr_dec_config &c = d->c;
     const int64_t blocks = (int64_t)(c.n_heads + 2 * c.n_kv_heads) * c.head_dim / 16 + 2 * c.n_kv_heads * 64;
-    if (dev && bytes < (int64_t)c.n_layers * blocks * QASR_STAMP_SLOTS * 8)
-        return qasr_fail(QASR_ERR_INVALID, "decoder_set_stamps: buffer too small for every layer's blocks");
+    if (blocks > QASR_STAMP_BLOCKS || 2 * (int64_t)c.intermediate / 16 > QASR_STAMP_BLOCKS)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_set_stamps: more blocks per launch than the stamp layout holds");
+    if (dev && bytes < 4 * (int64_t)c.n_layers * QASR_STAMP_BLOCKS * QASR_STAMP_SLOTS * 8)
+        return qasr_fail(QASR_ERR_INVALID, "decoder_set_stamps: buffer too small (4 kinds x layers x 2048 blocks)");
     HIPCHK(hipStreamSynchronize(d->h->stream));
     for (auto &g : d->graphs) (void)hipGraphExecDestroy(g.second);
     d->graphs.clear();
@@ -798,7 +816,7 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
             if ((rc = set_state(d, tok)) != QASR_OK) break;
             LAUNCHCHK(launch_delay(400, st), "profile delay");
             HIPCHK(hipEventRecord(e0, st));
-            const int reps = k >= 5 ? lm_reps : 1;
+            const int reps = k == 5 || k == 6 ? lm_reps : 1;
             for (int r = 0; r < reps && rc == QASR_OK; r++) rc = decoder_enqueue_step(d, true, k);
             HIPCHK(hipEventRecord(e1, st));
             // the fused qkv + attention launches above used this step's tags:
@@ -808,7 +826,7 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
             float ms = 0.0f;
             HIPCHK(hipEventElapsedTime(&ms, e0, e1));
             tot[k] += ms * 1000.0;
-            if (!(k == 1 && fused)) cnt[k] += k >= 5 ? lm_reps : c.n_layers;
+            if (!(k == 1 && fused)) cnt[k] += k == 5 || k == 6 ? lm_reps : c.n_layers;
         }
         tok = next[0];
         d->len += 1;
@@ -830,12 +848,14 @@ extern "C" int qasr_hip_decoder_profile(qasr_decoder *d, int32_t n_steps, float 
         2 * I * H + 8 * I + 4 * H + 4 * I,
         H * I + 4 * H + 4 * I + 8 * H,
         V * H + 4 * V + 4 * H,
-        8.0 * argmax_blocks(d->lm_i8_rows)};
+        8.0 * argmax_blocks(d->lm_i8_rows),
+        nqkv * H + 4 * nqkv + 4 * H + 4 * nqkv};
     for (int k = 0; k < QASR_PROFILE_KINDS; k++) {
         us_per_launch[k] = cnt[k] ? (float)(tot[k] / cnt[k]) : 0.0f;
         if (bytes_per_launch)
             bytes_per_launch[k] = any_fused && k == 0 ? bytes[0] + bytes[1] : (any_fused && k == 1 ? 0.0 : bytes[k]);
-        if (launches_per_step) launches_per_step[k] = k >= 5 ? 1 : (any_fused && k == 1 ? 0 : c.n_layers);
+        if (launches_per_step)
+            launches_per_step[k] = k == 7 ? 0 : (k >= 5 ? 1 : (any_fused && k == 1 ? 0 : c.n_layers));
     }
     return QASR_OK;
 }

@@ -553,7 +553,7 @@ __device__ __forceinline__ void attn_step_block(const AttnDecodeArgs &a, int blk
     unsigned long long *stamp = nullptr;
 #ifdef QASR_STAMPS
     // fused launch: slots 0-7 by wave 0, 8 by the polling wave
-    if (POLL && a.stamps) stamp = a.stamps + ((int64_t)a.layer * gridDim.x + blockIdx.x) * QASR_STAMP_SLOTS;
+    if (POLL && a.stamps) stamp = a.stamps + ((int64_t)a.layer * QASR_STAMP_BLOCKS + blockIdx.x) * QASR_STAMP_SLOTS;
     if ((threadIdx.x >> 6) == 0) QASR_STAMP(stamp, 0);
 #endif
     (void)blk0;
@@ -1081,8 +1081,10 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
 // ---------------------------------------------------------------------------
 template <typename KVT, int GPW, int NS, int R, bool EMBED>
 __global__ __launch_bounds__(320) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, int n_mv) {
-    __shared__ float lds[4 * NS * 1024];
+    __shared__ float lds[4 * QASR_NORM_LDS(NS)];
     __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
+    // both branches read arguments spread over ~7 lines: one batch of misses
+    kernarg_touch<(int)(sizeof(MvArgs) + sizeof(AttnDecodeArgs))>();
     if ((int)blockIdx.x < n_mv) {
         // waves 0-3 run the matvec; wave 4 only joins its one block barrier
         if ((threadIdx.x >> 6) == 4) {
@@ -1092,7 +1094,7 @@ __global__ __launch_bounds__(320) void k_qkv_attn(MvArgs m, AttnDecodeArgs a, in
         const unsigned tag = (unsigned)a.state[4] * 32u + (unsigned)a.layer;
         unsigned long long *stamp = nullptr;
 #ifdef QASR_STAMPS
-        if (a.stamps) stamp = a.stamps + ((int64_t)a.layer * gridDim.x + blockIdx.x) * QASR_STAMP_SLOTS;
+        if (a.stamps) stamp = a.stamps + ((int64_t)a.layer * QASR_STAMP_BLOCKS + blockIdx.x) * QASR_STAMP_SLOTS;
         if ((threadIdx.x >> 6) == 0) QASR_STAMP(stamp, 0);
 #endif
         w8a8_wave<NS, R, MV_PLAIN, true, EMBED, true>(m, blockIdx.x, lds, qlds, a.qkv_tag, tag, stamp);
@@ -1272,12 +1274,12 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
 template <int NS>
 __global__ __launch_bounds__(64) void k_rms_norm_rows(float *__restrict__ out, const float *__restrict__ x,
                                                       const float *__restrict__ w, int H, float eps) {
-    __shared__ float T[NS * 1024];
+    __shared__ float T[QASR_NORM_LDS(NS)];
     const int lane = threadIdx.x;
     const int64_t row = blockIdx.x;
     const float *xr = x + row * H;
     float *o = out + row * H;
-    const int nslot = H >> 4;
+    const int nslot = H >> 4, ts = nslot + QASR_NORM_PAD;
     float4 xv[NS][4], wv[NS][4];
 #pragma unroll
     for (int c = 0; c < NS; c++) {
@@ -1294,10 +1296,10 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(float *__restrict__ out, c
         if (sl < nslot) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                T[(4 * i) * nslot + sl] = xv[c][i].x;
-                T[(4 * i + 1) * nslot + sl] = xv[c][i].y;
-                T[(4 * i + 2) * nslot + sl] = xv[c][i].z;
-                T[(4 * i + 3) * nslot + sl] = xv[c][i].w;
+                T[(4 * i) * ts + sl] = xv[c][i].x;
+                T[(4 * i + 1) * ts + sl] = xv[c][i].y;
+                T[(4 * i + 2) * ts + sl] = xv[c][i].z;
+                T[(4 * i + 3) * ts + sl] = xv[c][i].w;
             }
         }
     }
@@ -1305,7 +1307,7 @@ __global__ __launch_bounds__(64) void k_rms_norm_rows(float *__restrict__ out, c
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     float acc = 0.0f;
     if (lane < 16) {
-        const float4 *t = reinterpret_cast<const float4 *>(T + lane * nslot);
+        const float4 *t = reinterpret_cast<const float4 *>(T + lane * ts);
         for (int i = 0; i < (nslot >> 2); i++) {
             const float4 v = t[i];
             acc = fmaf(v.x, v.x, acc);

@@ -226,6 +226,14 @@ __device__ __attribute__((aligned(256))) int4 g_gemm_zero16[16];
 // the ring every K-step.  The compiler does not see these loads: the kernel
 // issues no other vector-memory load until its final vmcnt(0), and it makes
 // no other use of M0 (the generated code was checked for both).
+// LDS placement of the ring's 16-byte slots: slot q of tile row r sits at
+// slot q ^ a_swz(r) (A rows: 128 B, 8 slots) or q ^ b_swz(r) (B rows: 64 B, 4
+// slots).  Measured and rejected: A slots by (r >> 1) & 7 (conflict-free for
+// 16-lane bank passes; the encoder's f32 GEMMs 2.9 -> 3.15 ms) and B slots by
+// (r & 3) ^ ((r >> 2) & 3) (config-1 int8 shapes 2-6% slower).
+__device__ __forceinline__ int a_swz(int r) { return r & 7; }
+__device__ __forceinline__ int b_swz(int r) { return r & 3; }
+
 __device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
     const uint32_t la = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(la) : "memory");
@@ -293,7 +301,14 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     const int grp = wave >> 2, wid = wave & 3;          // K group, wave within the group
     auto &smem = smem_all[grp];
     const int mw = AF ? (BM / 4) * wid : 0, nw = AF ? 0 : (BN / 4) * wid;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int n0 = blockIdx.x * BN;
+    // M tiles: blockIdx.y's, or with a grid of one row every tile of the
+    // column strip in turn (the strip's B rows then come from L2 after the
+    // first tile instead of HBM once per tile)
+    const int gy_all = (g.M + BM - 1) / BM;
+    for (int mt = blockIdx.y; mt < gy_all; mt += gridDim.y) {
+    const int m0 = mt * BM;
+    if (mt != (int)blockIdx.y) __syncthreads();   // every wave is past the previous tile's ring reads
     const int M = g.M, N = g.N, K = g.K;
     // split K (KS > 1, grid z = KS): this block's K-steps [k0s, k0s + nk); its
     // raw partial sums go to the workspace and a reduction pass runs the
@@ -309,12 +324,12 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     const char *a_src[LA], *b_src[LB];
 #pragma unroll
     for (int u = 0; u < LA; u++) {
-        const int r = 8 * (wid * LA + u) + (lane >> 3), p = (lane & 7) ^ (r & 7);
+        const int r = 8 * (wid * LA + u) + (lane >> 3), p = (lane & 7) ^ a_swz(r);
         a_src[u] = A + ((int64_t)min(m0 + r, M - 1) * g.lda) * AE + 16 * p;
     }
 #pragma unroll
     for (int u = 0; u < LB; u++) {
-        const int r = 16 * (wid * LB + u) + (lane >> 2), p = (lane & 3) ^ (r & 3);
+        const int r = 16 * (wid * LB + u) + (lane >> 2), p = (lane & 3) ^ b_swz(r);
         b_src[u] = B + ((int64_t)min(n0 + r, N - 1) * g.ldb) * BE + 16 * p;
     }
     const char *zero = reinterpret_cast<const char *>(g_gemm_zero16);
@@ -377,11 +392,11 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
             for (int j = 0; j < WC; j++) {
                 const int n = nw + j * 16 + fr;
                 if (BSRC == B_BF16) {
-                    const int p = fg ^ (n & 3);
+                    const int p = fg ^ b_swz(n);
                     bfrag[j] = *reinterpret_cast<const bf16x8 *>(st + ASZ + n * 64 + p * 16);
                 } else {
                     // 8 int8 weights -> bf16 (exact: |q| <= 128 has 8 significant bits)
-                    const int p = (2 * s + (fg >> 1)) ^ (n & 3);
+                    const int p = (2 * s + (fg >> 1)) ^ b_swz(n);
                     const uint2 v = *reinterpret_cast<const uint2 *>(st + ASZ + n * 64 + p * 16 + (fg & 1) * 8);
                     uint32_t w[4];
 #pragma unroll
@@ -400,8 +415,8 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                 if (AF) {
                     // f32 A = hi + mid + lo, each term the RNE bf16 of the remaining residual
                     const int k4 = 2 * fg;
-                    const float4 x0 = *reinterpret_cast<const float4 *>(st + r * 128 + ((k4 ^ (r & 7)) * 16));
-                    const float4 x1 = *reinterpret_cast<const float4 *>(st + r * 128 + (((k4 + 1) ^ (r & 7)) * 16));
+                    const float4 x0 = *reinterpret_cast<const float4 *>(st + r * 128 + ((k4 ^ a_swz(r)) * 16));
+                    const float4 x1 = *reinterpret_cast<const float4 *>(st + r * 128 + (((k4 + 1) ^ a_swz(r)) * 16));
                     const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                     uint32_t hi[4], mi[4], lo[4];
 #pragma unroll
@@ -421,7 +436,7 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                     af[NA > 1 ? 1 : 0] = __builtin_bit_cast(bf16x8, make_uint4(mi[0], mi[1], mi[2], mi[3]));
                     af[NA - 1] = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
                 } else {
-                    const int p = (4 * s + fg) ^ (r & 7);
+                    const int p = (4 * s + fg) ^ a_swz(r);
                     af[0] = *reinterpret_cast<const bf16x8 *>(st + r * 128 + p * 16);
                 }
 #pragma unroll
@@ -525,6 +540,7 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                     const int n = n0 + nw + j * 16 + (lane & 15);
                     if (m < M && n < N) g.ws[((int64_t)kz * M + m) * N + n] = acc[i][j][r];
                 }
+    }
     }
 }
 
@@ -655,6 +671,10 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
         }
         return hipGetLastError();
     }
+    // (a grid of one M row makes each block walk every M tile of its column
+    // strip, reading the strip's weights from HBM once: for the config-1 LM
+    // head, 1187 strips at M = 375, it measured 205 us against 160-184 with a
+    // block per tile, so no launch uses it)
     const dim3 grid(gx, gy);
     switch (epi) {
 #define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, 1>), grid, dim3(256), 0, st, g); break;

@@ -43,9 +43,14 @@ __global__ __launch_bounds__(256) void k_pack_int8_rows(const uint16_t *__restri
 
 template <int NS, int R, int MODE, bool NORM, bool EMBED>
 __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
-    __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
+    __shared__ float lds[NORM ? 4 * QASR_NORM_LDS(NS) : 1];
     __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
-    w8a8_wave<NS, R, MODE, NORM, EMBED>(a, blockIdx.x, lds, qlds);
+    unsigned long long *stamp = nullptr;
+#ifdef QASR_STAMPS
+    if (a.stamps) stamp = a.stamps + ((int64_t)a.layer * QASR_STAMP_BLOCKS + blockIdx.x) * QASR_STAMP_SLOTS;
+    if ((threadIdx.x >> 6) == 0) QASR_STAMP(stamp, 0);
+#endif
+    w8a8_wave<NS, R, MODE, NORM, EMBED>(a, blockIdx.x, lds, qlds, nullptr, 0, stamp);
 }
 
 // ---------------------------------------------------------------------------
@@ -54,11 +59,13 @@ __global__ __launch_bounds__(256) void k_w8a8(MvArgs a) {
 // decoder.rs:616-617).  The attention kernel leaves S partials per query head
 // h = 2 kvh + g: max m and sum l at part[(2h + {0,1}) S + s], and o[128] at
 // part[32 S + (128 h + d) S + s] (split index fastest).  Every block merges
-// all 16 heads into LDS: thread (g, d) loads its 8 heads' S partials as
-// vectors, threads t < 16 S turn (m, l) into log-sum-exp weights with 8-lane
-// DPP reductions; then each wave quantizes the merged vector (the activation
-// of a W8A8 += matvec, R = 4 rows per wave).  All loads (partials, weights,
-// epilogue operands) are issued before the first wait.
+// all 16 heads: thread (g, d) loads its 8 heads' S partials as vectors,
+// threads t < 16 S turn (m, l) into log-sum-exp weights with 8-lane DPP
+// reductions; each thread merges its 8 values in registers, the block takes
+// their absmax, and each thread writes its 8 int8 values of the quantized row
+// (the activation of the W8A8 += matvec) into LDS, which every wave reads back
+// as its 16-byte slots.  All loads (partials, weights, epilogue operands) are
+// issued before the first wait.
 // ---------------------------------------------------------------------------
 template <int S>
 __device__ __forceinline__ void ld_split(const float *p, float (&v)[S]) {
@@ -103,12 +110,16 @@ __device__ __forceinline__ float split_sum(float v) {
 template <int S, int R>
 __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     constexpr int D = 128, NS = 2, HQ = 16, K = HQ * D;
-    __shared__ float att[K];
-    __shared__ float fw[HQ][S], lsum[HQ];
-    __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
+    __shared__ __attribute__((aligned(16))) int8_t qb[K];
+    __shared__ float fw[HQ][S], lsum[HQ], wmax[4];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int g = t >> 7, d = t & 127;
+    unsigned long long *stamp = nullptr;
+#ifdef QASR_STAMPS
+    if (a.stamps) stamp = a.stamps + ((int64_t)a.layer * QASR_STAMP_BLOCKS + blockIdx.x) * QASR_STAMP_SLOTS;
+#endif
+    if (wid == 0) QASR_STAMP(stamp, 0);
     // (1) this thread's o partials: heads h = 2 j + g, dim d, all splits
     const float *po = a.part + 2 * HQ * S;
     float ov[HQ / 2][S];
@@ -133,6 +144,7 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     const float ws0 = __builtin_nontemporal_load(a.ws + r0 + item);
     const float yb = __builtin_nontemporal_load(a.y + r0 + item);
     __builtin_amdgcn_sched_barrier(0);
+    if (wid == 0) QASR_STAMP(stamp, 1);
     // (3) log-sum-exp weights per (head, split)
     {
         const float M = split_max<S>(pm);
@@ -144,7 +156,10 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
         }
     }
     __syncthreads();
-    // (4) merged attention output of heads 2 j + g, dim d
+    if (wid == 0) QASR_STAMP(stamp, 2);
+    // (4) merged attention output of heads 2 j + g, dim d, kept in registers;
+    // the block's absmax over all of them
+    float mv[HQ / 2], mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < HQ / 2; j++) {
         const int h = 2 * j + g;
@@ -152,24 +167,28 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
 #pragma unroll
         for (int s = 0; s < S; s++) ot = fmaf(ov[j][s], fw[h][s], ot);
         const float lt = lsum[h];
-        att[h * D + d] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
+        mv[j] = lt > 0.0f ? __fdiv_rn(ot, lt) : 0.0f;
+        mx = fmaxf(mx, fabsf(mv[j]));
     }
+    mx = wave_max_f32(mx);
+    if (lane == 0) wmax[wid] = mx;
     __syncthreads();
-    // (5) quantize (the scale from the whole vector in every wave, the int8
-    // conversion shared by the block's waves)
-    ActIn<NS, false, false> in;
+    if (wid == 0) QASR_STAMP(stamp, 3);
+    // (5) quantize_f32_to_int8 of the merged row: each thread converts its own
+    // 8 values with the block's scale into the int8 row in LDS (element e at
+    // byte e), then every lane reads its 16-byte slots back
+    float xs, inv;
+    act_scales(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])), &xs, &inv);
+#pragma unroll
+    for (int j = 0; j < HQ / 2; j++) qb[(2 * j + g) * D + d] = (int8_t)round_clamp_i8(__fmul_rn(mv[j], inv));
+    __syncthreads();
+    int xd[NS][4];
 #pragma unroll
     for (int c = 0; c < NS; c++) {
-        const float4 *p = reinterpret_cast<const float4 *>(att + 16 * (lane + 64 * c));
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const float4 v = p[i];
-            in.xv[c][4 * i] = v.x; in.xv[c][4 * i + 1] = v.y; in.xv[c][4 * i + 2] = v.z; in.xv[c][4 * i + 3] = v.w;
-        }
+        const int4 q4 = reinterpret_cast<const int4 *>(qb)[lane + 64 * c];
+        xd[c][0] = q4.x; xd[c][1] = q4.y; xd[c][2] = q4.z; xd[c][3] = q4.w;
     }
-    int xd[NS][4];
-    float xs;
-    act_finish_block<NS, false, false>(in, 0.0f, K, nullptr, qlds, xd, &xs);
+    if (wid == 0) QASR_STAMP(stamp, 4);
     // (6) dots, one reduce-scatter of the R row sums and the residual-add
     // epilogue (branch-free: lanes holding the same row store the same value)
     int part[R][1];
@@ -182,8 +201,10 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     }
     int av[1];
     scatter_items<R, 1>(part, av);
+    if (wid == 0) QASR_STAMP(stamp, 5);
     const float v = __fadd_rn(__fmul_rn(__fmul_rn((float)av[0], xs), ws0), yb);
     if (live) a.y[r0 + item] = v;
+    if (wid == 0) QASR_STAMP(stamp, 6);
 }
 
 template <int R>
@@ -224,7 +245,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 
 template <int NS, int R, bool NORM>
 __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
-    __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
+    __shared__ float lds[NORM ? 4 * QASR_NORM_LDS(NS) : 1];
     __shared__ __attribute__((aligned(16))) int qlds[NS * 256];
     __shared__ float bvals[4];
     __shared__ int bidx[4];
@@ -277,7 +298,7 @@ __global__ __launch_bounds__(256) void k_argmax_w8a8(ArgmaxArgs a) {
     if (gw + n_waves < n_groups) load_group(wb, sb, gw + n_waves);
     __builtin_amdgcn_sched_barrier(0);
     act_convert<NS, NORM, false>(in, K, nullptr);
-    act_finish_block<NS, NORM, false>(in, a.eps, K, lds + wid * NS * 1024, qlds, xd, &xs);
+    act_finish_block<NS, NORM, false>(in, a.eps, K, lds + wid * QASR_NORM_LDS(NS), qlds, xd, &xs);
     for (int g = gw; g < n_groups; g += 2 * n_waves) {
         consume(wa, sa, g);
         if (g + 2 * n_waves < n_groups) load_group(wa, sa, g + 2 * n_waves);
@@ -498,7 +519,7 @@ template <int NS, bool NORM>
 __global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x, const float *__restrict__ norm_w,
                                                     float eps, int K, int B, int8_t *__restrict__ xq,
                                                     float *__restrict__ xs) {
-    __shared__ float lds[NORM ? 4 * NS * 1024 : 1];
+    __shared__ float lds[NORM ? 4 * QASR_NORM_LDS(NS) : 1];
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int b = blockIdx.x * 4 + wid;
@@ -508,7 +529,7 @@ __global__ __launch_bounds__(256) void k_quant_rows(const float *__restrict__ x,
     act_convert<NS, NORM, false>(in, K, nullptr);
     int xd[NS][4];
     float s;
-    act_finish<NS, NORM, false>(in, eps, K, lds + wid * NS * 1024, xd, &s);
+    act_finish<NS, NORM, false>(in, eps, K, lds + wid * QASR_NORM_LDS(NS), xd, &s);
     const int nslot = K >> 4;
 #pragma unroll
     for (int c = 0; c < NS; c++) {

@@ -20,12 +20,12 @@ template <int NS>
 __global__ __launch_bounds__(64) void k_layer_norm_rows(float *__restrict__ out, const float *__restrict__ x,
                                                         const float *__restrict__ w, const float *__restrict__ b,
                                                         int H, float eps) {
-    __shared__ float T[NS * 1024];
+    __shared__ float T[16 * (64 * NS + 1)];   // rows one float apart beyond nslot: conflict-free reads
     const int lane = threadIdx.x;
     const int64_t row = blockIdx.x;
     const float *xr = x + row * H;
     float *o = out + row * H;
-    const int nslot = H >> 4;
+    const int nslot = H >> 4, ts = nslot + 1;
     float4 xv[NS][4];
 #pragma unroll
     for (int c = 0; c < NS; c++) {
@@ -39,16 +39,16 @@ __global__ __launch_bounds__(64) void k_layer_norm_rows(float *__restrict__ out,
         if (sl < nslot) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                T[(4 * i) * nslot + sl] = xv[c][i].x;
-                T[(4 * i + 1) * nslot + sl] = xv[c][i].y;
-                T[(4 * i + 2) * nslot + sl] = xv[c][i].z;
-                T[(4 * i + 3) * nslot + sl] = xv[c][i].w;
+                T[(4 * i) * ts + sl] = xv[c][i].x;
+                T[(4 * i + 1) * ts + sl] = xv[c][i].y;
+                T[(4 * i + 2) * ts + sl] = xv[c][i].z;
+                T[(4 * i + 3) * ts + sl] = xv[c][i].w;
             }
         }
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    const float *t = T + (lane < 16 ? lane : 0) * nslot;
+    const float *t = T + (lane < 16 ? lane : 0) * ts;
     float acc = 0.0f;
     if (lane < 16)
         for (int i = 0; i < nslot; i++) acc = __fadd_rn(acc, t[i]);

@@ -33,6 +33,8 @@ struct MvArgs {
     int n_total;
     const float *bias;        // MV_BIAS
     float *resid_out;         // EMBED mode: block 0 stores the f32 embedding here
+    unsigned long long *stamps;   // profiling build only: [layer][block][QASR_STAMP_SLOTS] (null: none)
+    int layer;
 };
 
 struct ArgmaxArgs {
@@ -179,6 +181,8 @@ struct OprojMergeArgs {
     const float *ws;          // [N]
     float *y;                 // [N], y += W attn
     int N;
+    unsigned long long *stamps;   // profiling build only: [layer][block][QASR_STAMP_SLOTS] (null: none)
+    int layer;
 };
 hipError_t launch_oproj_merge(const OprojMergeArgs &a, int rows_per_wave, hipStream_t st);
 

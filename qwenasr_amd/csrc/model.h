@@ -15,7 +15,7 @@
 #define QASR_CTR_ATTN 64
 #define QASR_CTR_ATTN_N 256
 // kernel kinds of qasr_hip_decoder_profile
-#define QASR_PROFILE_KINDS 7
+#define QASR_PROFILE_KINDS 8
 
 struct qasr_hip {
     int device = 0;

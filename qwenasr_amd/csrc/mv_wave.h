@@ -116,31 +116,47 @@ __device__ __forceinline__ void act_convert(ActIn<NS, NORM, EMBED> &in, int K, f
 // slots s = l + 64 c; the result is its int8 dwords plus the activation scale.
 // Each wave computes this redundantly — x is a few KiB and sits in L2 — so no
 // block barrier is needed.
-template <int NS, bool NORM, bool EMBED>
+template <int NS, bool NORM, bool EMBED, bool UNROLL = false>
 __device__ __forceinline__ void act_norm_scale(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
                                                float *xs, float *xinv) {
     const int lane = threadIdx.x & 63;
     const int nslot = K >> 4;
     if (NORM) {
-        // transpose through LDS: T[r][s] = x[16 s + r]
+        // transpose through LDS: T[r][s] = x[16 s + r], rows QASR_NORM_PAD
+        // floats apart beyond their nslot so that the 16 row-reading lanes
+        // start on different banks
+        const int ts = nslot + QASR_NORM_PAD;
 #pragma unroll
         for (int c = 0; c < NS; c++) {
             const int s = lane + 64 * c;
             if (s < nslot) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) lds_t[r * nslot + s] = in.xv[c][r];
+                for (int r = 0; r < 16; r++) lds_t[r * ts + s] = in.xv[c][r];
             }
         }
         __builtin_amdgcn_wave_barrier();
         float acc = 0.0f;
         if (lane < 16) {
-            const float4 *t = reinterpret_cast<const float4 *>(lds_t + lane * nslot);
-            for (int i = 0; i < (nslot >> 2); i++) {
-                float4 v = t[i];
+            const float4 *t = reinterpret_cast<const float4 *>(lds_t + lane * ts);
+            auto chain = [&acc](const float4 v) {
                 acc = fmaf(v.x, v.x, acc);
                 acc = fmaf(v.y, v.y, acc);
                 acc = fmaf(v.z, v.z, acc);
                 acc = fmaf(v.w, v.w, acc);
+            };
+            if (UNROLL && nslot == 64 * NS) {
+                // whole slots: each chunk's 16 LDS reads issued before its FMA
+                // chain (more VGPRs: for kernels whose occupancy does not bind)
+#pragma unroll
+                for (int h = 0; h < NS; h++) {
+                    float4 v[16];
+#pragma unroll
+                    for (int i = 0; i < 16; i++) v[i] = t[16 * h + i];
+#pragma unroll
+                    for (int i = 0; i < 16; i++) chain(v[i]);
+                }
+            } else {
+                for (int i = 0; i < (nslot >> 2); i++) chain(t[i]);
             }
         }
         __builtin_amdgcn_wave_barrier();
@@ -186,13 +202,13 @@ __device__ __forceinline__ void act_finish(ActIn<NS, NORM, EMBED> &in, float eps
 // per-lane work) into qlds, and after one block barrier every lane reads its
 // slots' 16 bytes back.  The values are act_finish's, bit for bit.  Every
 // wave of the block must call it.  qlds: NS * 64 * 4 ints.
-template <int NS, bool NORM, bool EMBED>
+template <int NS, bool NORM, bool EMBED, bool UNROLL = false>
 __device__ __forceinline__ void act_finish_block(ActIn<NS, NORM, EMBED> &in, float eps, int K, float *lds_t,
                                                  int *qlds, int xd[NS][4], float *xs) {
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     float inv;
-    act_norm_scale<NS, NORM, EMBED>(in, eps, K, lds_t, xs, &inv);
+    act_norm_scale<NS, NORM, EMBED, UNROLL>(in, eps, K, lds_t, xs, &inv);
 #pragma unroll
     for (int c = 0; c < NS; c++) {
         int q;
@@ -302,7 +318,7 @@ __device__ __forceinline__ void scatter_items(int (&v)[N][W], int (&out)[W]) {
 // TAG (plain rows only): row r's value goes to tag_out[r] as one 64-bit
 // (tag << 32 | f32 bits) agent-scope store instead of to the segment's y, for
 // a consumer in the same launch that polls until the tag matches.
-// lds: 4 NS 1024 floats per block when NORM; qlds: NS 256 ints per block (the
+// lds: 4 QASR_NORM_LDS(NS) floats per block when NORM; qlds: NS 256 ints per block (the
 // block's 4 waves share the quantized activation).  All 4 waves of the block
 // must call it (one block barrier).
 // ---------------------------------------------------------------------------
@@ -359,13 +375,20 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
         if (MODE == MV_ADDTO) yb = __builtin_nontemporal_load(S.y + lrow0 + item);
         if (MODE == MV_BIAS) yb = __builtin_nontemporal_load(a.bias + lrow0 + item);
     }
+    // keep every load above here: the scheduling barrier stops the machine
+    // scheduler, the empty memory-clobbering asm stops the earlier sinking
+    // passes, which otherwise move the weight loads of the kernels without the
+    // RMSNorm prologue below the activation wait (two HBM round trips in a
+    // row instead of one)
+    asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     if (wid == 0) QASR_STAMP(stamp, 1);
     act_convert<NS, NORM, EMBED>(in, K, resid);
     if (wid == 0) QASR_STAMP(stamp, 2);
     int xd[NS][4];
     float xs;
-    act_finish_block<NS, NORM, EMBED>(in, a.eps, K, lds + wid * NS * 1024, qlds, xd, &xs);
+    // (the fused qkv + attention launch, TAG, takes the unrolled RMSNorm reads)
+    act_finish_block<NS, NORM, EMBED, TAG>(in, a.eps, K, lds + wid * QASR_NORM_LDS(NS), qlds, xd, &xs);
     if (wid == 0) QASR_STAMP(stamp, 3);
     // per-lane partial dots, then one reduce-scatter: every lane ends with its
     // item's complete sums.  The epilogue runs in every lane with no branch
@@ -388,8 +411,10 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
         scatter_items<NI, 2>(part, gu);
         const float g = __fmul_rn(__fmul_rn((float)gu[0], xs), ws0);
         const float u = __fmul_rn(__fmul_rn((float)gu[1], xs), ws1);
+        if (wid == 0) QASR_STAMP(stamp, 4);
         const float o = __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), u);
         if (live) S.y[(lrow0 >> 1) + item] = o;
+        if (wid == 0) QASR_STAMP(stamp, 5);
     } else {
         int part[NI][1];
 #pragma unroll
@@ -413,6 +438,7 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
             if (wid == 0) QASR_STAMP(stamp, 5);
         } else {
             if (live) S.y[lrow0 + item] = v;
+            if (wid == 0) QASR_STAMP(stamp, 5);
         }
     }
 }

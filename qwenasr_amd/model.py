@@ -496,7 +496,7 @@ class EngineStream:
 
 
 KERNEL_KINDS = ("norm+qkv", "attention", "o_proj+=", "norm+gate_up+swiglu", "down+=", "norm+lm_head_argmax",
-                "argmax_merge")
+                "argmax_merge", "norm+qkv (own launch)")
 
 
 def profile_decoder(decoder, n_steps):
