@@ -62,6 +62,11 @@ int qasr_hip_copy(qasr_hip *h, void *dst, const void *src, size_t bytes);
 /* ---- timing on the handle's stream (HIP events) ------------------------- */
 int qasr_hip_timer_start(qasr_hip *h);
 int qasr_hip_timer_stop(qasr_hip *h, float *ms);    /* synchronises */
+/* queues a wait of `us` microseconds (0..100000) on the handle's stream:
+ * launches enqueued while it runs start back to back when it ends, so a timer
+ * started behind it measures the GPU rather than the host's launch rate (no
+ * counterpart in the reference, whose kernels run on the calling thread) */
+int qasr_hip_timer_hold(qasr_hip *h, int us);
 
 /* ---- A1: weight packer --------------------------------------------------
  * Replaces kernels::quantize_bf16_weights_to_int8 (kernels/mod.rs:1805-1829,

@@ -91,6 +91,7 @@ _SIGS = {
     "qasr_hip_copy": (C.c_int, [P, P, P, C.c_size_t]),
     "qasr_hip_timer_start": (C.c_int, [P]),
     "qasr_hip_timer_stop": (C.c_int, [P, C.POINTER(F32)]),
+    "qasr_hip_timer_hold": (C.c_int, [P, C.c_int]),
     "qasr_hip_pack_int8_rows": (C.c_int, [P, P, I64, I64, C.c_int, P, P]),
     "qasr_hip_quantize_act": (C.c_int, [P, P, I64, P, P]),
     "qasr_hip_linear_int8": (C.c_int, [P, P, P, P, P, P, I64, I64]),

@@ -71,6 +71,10 @@ from .synth import DEC_0_6B, DEC_1_7B, ENC_0_6B, SynthDecoder, SynthEncoder, aud
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+# the stream is held this long per timed launch while the host enqueues them
+# (a Python ctypes launch takes a few microseconds), so that they run back to
+# back and the events time the GPU
+HOLD_US_PER_LAUNCH = 15
 
 
 def log(msg):
@@ -87,8 +91,9 @@ def config0(reps=256, mall_mib=256):
     Each projection rotates over enough distinct device copies of its weights
     (at least 32, and together more than twice the 256 MiB Infinity Cache) that
     every launch streams its matrix from HBM.  Timed with HIP events over
-    `reps` back-to-back launches (kernel plus the queue's inter-dispatch gap,
-    the per-kernel method of bench.py); GB/s = algorithmic bytes (int8 W N*K +
+    `reps` launches queued behind a hold of the stream, so they run back to
+    back (kernel plus the queue's inter-dispatch gap, the per-kernel method of
+    bench.py); GB/s = algorithmic bytes (int8 W N*K +
     scales 4N + x 4K + y 4N, +4N read for +=, +4K gains for a fused RMSNorm)
     per launch / time."""
     dev = Device(0)
@@ -138,6 +143,7 @@ def config0(reps=256, mall_mib=256):
         for i in range(n_copies):           # warm-up: every copy once
             launch(i)
         dev.sync()
+        dev.timer_hold(HOLD_US_PER_LAUNCH * reps)
         dev.timer_start()
         for i in range(reps):
             launch(i)
@@ -187,6 +193,7 @@ def config1(reps=20):
             y = dev.empty((M, N), np.float32)
             K.gemm_w8_bf16(y, a, q, s, M, N, Kd)          # warm-up
             dev.sync()
+            dev.timer_hold(HOLD_US_PER_LAUNCH * reps)
             dev.timer_start()
             for _ in range(reps):
                 K.gemm_w8_bf16(y, a, q, s, M, N, Kd)

@@ -193,6 +193,13 @@ extern "C" int qasr_hip_timer_stop(qasr_hip *h, float *ms) {
     return QASR_OK;
 }
 
+extern "C" int qasr_hip_timer_hold(qasr_hip *h, int us) {
+    CHECK_H(h);
+    if (us < 0 || us > 100000) return qasr_fail(QASR_ERR_INVALID, "timer_hold: us must be in [0, 100000]");
+    LAUNCHCHK(launch_delay(us, h->stream), "timer_hold");
+    return QASR_OK;
+}
+
 // ---------------------------------------------------------------------------
 // op level
 // ---------------------------------------------------------------------------

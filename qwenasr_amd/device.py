@@ -57,6 +57,11 @@ class Device:
         n = src.nbytes if nbytes is None else int(nbytes)
         check(lib().qasr_hip_copy(self.h, dst.ptr, src.ptr, n))
 
+    def timer_hold(self, us):
+        """Hold the stream for `us` microseconds, so that launches enqueued
+        meanwhile run back to back (see qasr_hip_timer_hold)."""
+        check(lib().qasr_hip_timer_hold(self.h, int(us)))
+
     def timer_start(self):
         check(lib().qasr_hip_timer_start(self.h))
 
