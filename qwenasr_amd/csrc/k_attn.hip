@@ -854,32 +854,39 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Multi-stream form of k_attn_step (f32 cache): the same blocks, lanes and
-// arithmetic per stream, so every stream gets the bits of the single-stream
-// kernel run alone on its context (its partition gpb_dev, its split count).
-// For throughput over many streams it holds one group of K rows, then one of
-// V rows, in flight instead of the whole run: pass 1 loads a wave's K groups
-// one after another (the next requested while the current one's scores form),
-// the softmax then takes the max over all of the wave's scores as the
-// single-stream kernel does, and pass 2 streams the V groups the same way.
+// Multi-stream form of k_attn_step (f32 cache): the same waves, lanes and
+// arithmetic per query head, so every stream gets the bits of the
+// single-stream kernel run alone on its context (its partition gpb_dev, its
+// split count).  For throughput over many streams:
+//  * a block serves both query heads of its KV head (k_attn_step gives each
+//    its own block): it loads the K/V rows once and forms the two heads'
+//    scores, softmaxes and P V side by side, each with the single-head
+//    kernel's operations and order; the 4 waves' merge then runs one head per
+//    128 threads;
+//  * it holds one group of K rows, then one of V rows, in flight instead of
+//    the whole run: pass 1 loads a wave's K groups one after another (the
+//    next requested while the current one's scores form), the softmax then
+//    takes the max over all of the wave's scores as the single-stream kernel
+//    does, and pass 2 streams the V groups the same way.
 // Groups past the stream's context read row 0 (masked, adding exact zeros);
-// blocks wholly past it store an empty partial and leave.  Grid row y is
-// stream stream_order[y]; partials go split index slowest.
+// blocks wholly past it store empty partials and leave.  Grid row y is
+// stream stream_order[y]; grid column kvh + Hkv x split; partials go split
+// index slowest.
 // ---------------------------------------------------------------------------
 template <int NW, int GPW>
 __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
     constexpr int D = 128, G = 2;
     using Kp = KvPair<float>;
-    __shared__ float wm[NW], wl[NW];
-    __shared__ float wacc[NW][D];
-    __shared__ __attribute__((aligned(16))) float pw[NW][GPW][8];
+    __shared__ float wm[G][NW], wl[G][NW];
+    __shared__ float wacc[G][NW][D];
+    __shared__ __attribute__((aligned(16))) float pw[G][NW][GPW][8];
     const int t = threadIdx.x, lane = t & 63;
     const int wid = __builtin_amdgcn_readfirstlane(t >> 6);
     const int n_split = a.n_split;
-    const int Hkv = gridDim.x / (G * n_split), Hq = Hkv * G;
+    const int Hkv = gridDim.x / n_split, Hq = Hkv * G;
     const int blk = blockIdx.x;
-    const int kvh = blk % Hkv, gq = (blk / Hkv) % G, split = blk / (G * Hkv);
-    const int h = kvh * G + gq;
+    const int kvh = blk % Hkv, split = blk / Hkv;
+    const int h0 = kvh * G;                          // query heads h0 and h0 + 1
     const int bs = a.stream_order ? a.stream_order[blockIdx.y] : (int)blockIdx.y;
     float *kc = reinterpret_cast<float *>(a.kcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
     float *vc = reinterpret_cast<float *>(a.vcache) + bs * a.batch_kv_stride + (int64_t)kvh * a.head_stride;
@@ -891,37 +898,38 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
     const int gpw_own = (gpb + NW - 1) / NW;
     const int pos = a.state[4 * bs + 1];
     const int max_rows = min((int)(a.head_stride / D), pos + 1);
-    if (gpw_own > GPW) {
-        // a partition longer than this launch's waves hold (the host sizes GPW
-        // from its per-position table): a NaN partial and the fault flag the
-        // host checks, never a silent drop of groups
-        if (t < D) {
-            part[part_o_index_slow(n_split, split, Hq, h * D + t)] = __builtin_nanf("");
-            if (t == 0) {
-                part[(2 * h) * n_split + split] = __builtin_nanf("");
-                part[(2 * h + 1) * n_split + split] = __builtin_nanf("");
-                if (a.fault) st_agent(a.fault, 1);
+    // thread t < 2 D stores head h0 + t / D's column t % D of an early partial
+    auto early_partial = [&](float o, float m_v, float l_v) {
+        if (t < G * D) {
+            const int h = h0 + t / D, d = t % D;
+            part[part_o_index_slow(n_split, split, Hq, h * D + d)] = o;
+            if (d == 0) {
+                part[(2 * h) * n_split + split] = m_v;
+                part[(2 * h + 1) * n_split + split] = l_v;
             }
         }
+    };
+    if (gpw_own > GPW) {
+        // a partition longer than this launch's waves hold (the host sizes GPW
+        // from its per-position table): NaN partials and the fault flag the
+        // host checks, never a silent drop of groups
+        const float nan = __builtin_nanf("");
+        early_partial(nan, nan, nan);
+        if (t == 0 && a.fault) st_agent(a.fault, 1);
         return;
     }
     if (8 * g0 >= max_rows) {
-        // a block wholly past the stream's context: an empty partial
-        if (t < D) {
-            part[part_o_index_slow(n_split, split, Hq, h * D + t)] = 0.0f;
-            if (t == 0) {
-                part[(2 * h) * n_split + split] = -INFINITY;
-                part[(2 * h + 1) * n_split + split] = 0.0f;
-            }
-        }
+        early_partial(0.0f, -INFINITY, 0.0f);        // a block wholly past the stream's context
         return;
     }
     auto row_of = [&](int i, int p) {
         const int j = 8 * (g0 + wid + NW * i) + p;
         return (int64_t)(i < gpw_own && j < max_rows ? j : 0) * D;
     };
-    // q, the new k/v and the first K group
-    float2 q = reinterpret_cast<const float2 *>(qkv + h * D)[lane];
+    // q of both heads, the new k/v and the first K group
+    float2 q[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) q[g] = reinterpret_cast<const float2 *>(qkv + (h0 + g) * D)[lane];
     float2 kn = reinterpret_cast<const float2 *>(qkv + Hq * D + kvh * D)[lane];
     float2 vn = reinterpret_cast<const float2 *>(qkv + Hq * D + Hkv * D + kvh * D)[lane];
     const float2 qn = reinterpret_cast<const float2 *>(a.q_norm)[lane];
@@ -941,48 +949,53 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
     const float s16 = swap16_add(0.0f, 1.0f);
     const int bit3 = (lane >> 3) & 1;
     const int my_p = (s32 > 1.0f ? 4 : 0) + (s16 > 1.0f ? 2 : 0) + bit3;
-    q = norm_rope2(q, qn, cs, sn, a.eps);
+#pragma unroll
+    for (int g = 0; g < G; g++) q[g] = norm_rope2(q[g], qn, cs, sn, a.eps);
     if (own_pos) {
         kn = norm_rope2(kn, knw, cs, sn, a.eps);
-        if (wid == 0 && gq == 0) {
+        if (wid == 0) {
             Kp::store(kc + (int64_t)pos * D, lane, kn.x, kn.y);
             Kp::store(vc + (int64_t)pos * D, lane, vn.x, vn.y);
         }
     }
 
     // ---- pass 1: scores, one K group in flight behind the one being used ----
-    float sc[GPW];
+    float sc[G][GPW];
 #pragma unroll
     for (int i = 0; i < GPW; i++) {
-        sc[i] = -INFINITY;
+#pragma unroll
+        for (int g = 0; g < G; g++) sc[g][i] = -INFINITY;
         if (i >= gpw_own) continue;                   // uniform
         if (i + 1 < gpw_own) {
 #pragma unroll
             for (int p = 0; p < 8; p++) knext[p].load(kc + row_of(i + 1, p), lane);
         }
         const int jb = 8 * (g0 + wid + NW * i);
-        float v8[8];
 #pragma unroll
-        for (int p = 0; p < 8; p++) {
-            float kx = kcur[p].x(), ky = kcur[p].y();
-            if (own_pos && jb + p == pos) { kx = kn.x; ky = kn.y; }
-            v8[p] = fmaf(q.y, ky, __fmul_rn(q.x, kx));
+        for (int g = 0; g < G; g++) {
+            float v8[8];
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                float kx = kcur[p].x(), ky = kcur[p].y();
+                if (own_pos && jb + p == pos) { kx = kn.x; ky = kn.y; }
+                v8[p] = fmaf(q[g].y, ky, __fmul_rn(q[g].x, kx));
+            }
+            float r1[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) r1[k] = swap32_add(v8[k], v8[k + 4]);
+            float r2[2];
+#pragma unroll
+            for (int k = 0; k < 2; k++) r2[k] = swap16_add(r1[k], r1[k + 2]);
+            float r3;
+            {
+                const float keep = bit3 ? r2[1] : r2[0], send = bit3 ? r2[0] : r2[1];
+                r3 = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_ROR8>(send));
+            }
+            r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(r3));
+            r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_1032>(r3));
+            r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_2301>(r3));
+            sc[g][i] = jb + my_p < j1 ? __fmul_rn(r3, a.scale) : -INFINITY;
         }
-        float r1[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) r1[k] = swap32_add(v8[k], v8[k + 4]);
-        float r2[2];
-#pragma unroll
-        for (int k = 0; k < 2; k++) r2[k] = swap16_add(r1[k], r1[k + 2]);
-        float r3;
-        {
-            const float keep = bit3 ? r2[1] : r2[0], send = bit3 ? r2[0] : r2[1];
-            r3 = __fadd_rn(keep, dpp_f32<QASR_DPP_ROW_ROR8>(send));
-        }
-        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_ROW_HALF_MIRROR>(r3));
-        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_1032>(r3));
-        r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_2301>(r3));
-        sc[i] = jb + my_p < j1 ? __fmul_rn(r3, a.scale) : -INFINITY;
 #pragma unroll
         for (int p = 0; p < 8; p++) kcur[p] = knext[p];
     }
@@ -992,28 +1005,34 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
     for (int p = 0; p < 8; p++) vcur[p].load(vc + row_of(0, p), lane);
 
     // ---- softmax over this wave's positions (the single-stream order) -------
-    float m = sc[0];
+    float m[G], l[G];
 #pragma unroll
-    for (int i = 1; i < GPW; i++) m = fmaxf(m, sc[i]);
-    m = fmaxf(m, dpp_f32<QASR_DPP_ROW_ROR8>(m));
-    m = xrow16_max(m);
-    m = xhalf_max(m);
-    float pr[GPW], l = 0.0f;
+    for (int g = 0; g < G; g++) {
+        float mg = sc[g][0];
 #pragma unroll
-    for (int i = 0; i < GPW; i++) {
-        pr[i] = m == -INFINITY ? 0.0f : expf(__fsub_rn(sc[i], m));
-        if (i < gpw_own) l = __fadd_rn(l, pr[i]);
+        for (int i = 1; i < GPW; i++) mg = fmaxf(mg, sc[g][i]);
+        mg = fmaxf(mg, dpp_f32<QASR_DPP_ROW_ROR8>(mg));
+        mg = xrow16_max(mg);
+        mg = xhalf_max(mg);
+        float pr[GPW], lg = 0.0f;
+#pragma unroll
+        for (int i = 0; i < GPW; i++) {
+            pr[i] = mg == -INFINITY ? 0.0f : expf(__fsub_rn(sc[g][i], mg));
+            if (i < gpw_own) lg = __fadd_rn(lg, pr[i]);
+        }
+        if ((lane & 7) == 0) {
+#pragma unroll
+            for (int i = 0; i < GPW; i++) pw[g][wid][i][my_p] = pr[i];
+        }
+        lg = __fadd_rn(lg, dpp_f32<QASR_DPP_ROW_ROR8>(lg));
+        lg = xrow16_sum(lg);
+        lg = xhalf_sum(lg);
+        m[g] = mg;
+        l[g] = lg;
     }
-    if ((lane & 7) == 0) {
-#pragma unroll
-        for (int i = 0; i < GPW; i++) pw[wid][i][my_p] = pr[i];
-    }
-    l = __fadd_rn(l, dpp_f32<QASR_DPP_ROW_ROR8>(l));
-    l = xrow16_sum(l);
-    l = xhalf_sum(l);
 
     // ---- pass 2: P V, one V group in flight behind the one being used -------
-    float ox = 0.0f, oy = 0.0f;
+    float ox[G] = {0.0f, 0.0f}, oy[G] = {0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < GPW; i++) {
         if (i >= gpw_own) continue;                   // uniform
@@ -1021,42 +1040,48 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
 #pragma unroll
             for (int p = 0; p < 8; p++) vnext[p].load(vc + row_of(i + 1, p), lane);
         }
-        float P[8];
-#pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const float4 v4 = reinterpret_cast<const float4 *>(&pw[wid][i][0])[k];
-            P[4 * k] = v4.x; P[4 * k + 1] = v4.y; P[4 * k + 2] = v4.z; P[4 * k + 3] = v4.w;
-        }
         const int jb = 8 * (g0 + wid + NW * i);
-        float gx = 0.0f, gy = 0.0f;
 #pragma unroll
-        for (int p = 0; p < 8; p++) {
-            const bool live = jb + p < j1;
-            float vx = live ? vcur[p].x() : 0.0f, vy = live ? vcur[p].y() : 0.0f;
-            if (own_pos && jb + p == pos) { vx = vn.x; vy = vn.y; }
-            gx = fmaf(P[p], vx, gx);
-            gy = fmaf(P[p], vy, gy);
+        for (int g = 0; g < G; g++) {
+            float P[8];
+#pragma unroll
+            for (int k = 0; k < 2; k++) {
+                const float4 v4 = reinterpret_cast<const float4 *>(&pw[g][wid][i][0])[k];
+                P[4 * k] = v4.x; P[4 * k + 1] = v4.y; P[4 * k + 2] = v4.z; P[4 * k + 3] = v4.w;
+            }
+            float gx = 0.0f, gy = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                const bool live = jb + p < j1;
+                float vx = live ? vcur[p].x() : 0.0f, vy = live ? vcur[p].y() : 0.0f;
+                if (own_pos && jb + p == pos) { vx = vn.x; vy = vn.y; }
+                gx = fmaf(P[p], vx, gx);
+                gy = fmaf(P[p], vy, gy);
+            }
+            ox[g] = __fadd_rn(ox[g], gx);
+            oy[g] = __fadd_rn(oy[g], gy);
         }
-        ox = __fadd_rn(ox, gx);
-        oy = __fadd_rn(oy, gy);
 #pragma unroll
         for (int p = 0; p < 8; p++) vcur[p] = vnext[p];
     }
 
-    // ---- merge the waves of the block (LDS, one barrier) --------------------
-    if (lane == 0) { wm[wid] = m; wl[wid] = l; }
-    reinterpret_cast<float2 *>(&wacc[wid][0])[lane] = make_float2(ox, oy);
+    // ---- merge the waves of the block per head (LDS, one barrier) -----------
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+        if (lane == 0) { wm[g][wid] = m[g]; wl[g][wid] = l[g]; }
+        reinterpret_cast<float2 *>(&wacc[g][wid][0])[lane] = make_float2(ox[g], oy[g]);
+    }
     __syncthreads();
-    if (t < D) {
-        const int d = t;
+    if (t < G * D) {
+        const int g = t / D, d = t % D, h = h0 + g;
         float m_part = -INFINITY, o_part = 0.0f, l_part = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[w]);
+        for (int w = 0; w < NW; w++) m_part = fmaxf(m_part, wm[g][w]);
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float f = wm[w] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[w], m_part));
-            o_part = fmaf(wacc[w][d], f, o_part);
-            l_part = fmaf(wl[w], f, l_part);
+            const float f = wm[g][w] == -INFINITY ? 0.0f : expf(__fsub_rn(wm[g][w], m_part));
+            o_part = fmaf(wacc[g][w][d], f, o_part);
+            l_part = fmaf(wl[g][w], f, l_part);
         }
         part[part_o_index_slow(n_split, split, Hq, h * D + d)] = o_part;
         if (d == 0) {
@@ -1227,10 +1252,10 @@ hipError_t launch_attn_decode(const AttnDecodeArgs &a, int n_heads, int n_kv_hea
         else hipLaunchKernelGGL((k_attn_decode<float, NW, false, 2>), grid, dim3(NW * 64), 0, st, a);  \
     }
     if (dec && !merge && a.gpw > 0 && a.gpb_dev) {
-        // k_attn_step_batch (multi-stream step): grid (query head x split, stream),
+        // k_attn_step_batch (multi-stream step): grid (KV head x split, stream),
         // 4 waves of up to gpw groups; each stream's gpb_dev must be <= 4 gpw
         if (a.waves != 4 || a.gpw < 1 || a.gpw > 4 || kv_bf16 || nb > 65535) return hipErrorInvalidValue;
-        const dim3 bgrid(n_kv_heads * 2 * a.n_split, nb);
+        const dim3 bgrid(n_kv_heads * a.n_split, nb);
 #define QASR_ATT_BSTEP(GPW) hipLaunchKernelGGL((k_attn_step_batch<4, GPW>), bgrid, dim3(256), 0, st, a);
         if (a.gpw == 1) { QASR_ATT_BSTEP(1) } else if (a.gpw == 2) { QASR_ATT_BSTEP(2) }
         else if (a.gpw == 3) { QASR_ATT_BSTEP(3) } else { QASR_ATT_BSTEP(4) }

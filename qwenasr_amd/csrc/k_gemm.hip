@@ -228,11 +228,15 @@ __device__ __attribute__((aligned(256))) int4 g_gemm_zero16[16];
 // no other use of M0 (the generated code was checked for both).
 // LDS placement of the ring's 16-byte slots: slot q of tile row r sits at
 // slot q ^ a_swz(r) (A rows: 128 B, 8 slots) or q ^ b_swz(r) (B rows: 64 B, 4
-// slots).  Measured and rejected: A slots by (r >> 1) & 7 (conflict-free for
-// 16-lane bank passes; the encoder's f32 GEMMs 2.9 -> 3.15 ms) and B slots by
-// (r & 3) ^ ((r >> 2) & 3) (config-1 int8 shapes 2-6% slower).
-__device__ __forceinline__ int a_swz(int r) { return r & 7; }
-__device__ __forceinline__ int b_swz(int r) { return r & 3; }
+// slots).  The f32-split kernels keep r & 7 and r & 3 (A by (r >> 1) & 7,
+// conflict-free for 16-lane bank passes, measured 2.9 -> 3.15 ms on the
+// encoder's GEMMs).  The bf16 x int8 kernels take the conflict-free forms
+// (r >> 1) & 7 and (r & 3) ^ ((r >> 2) & 3): config-1 LM head at M = 375
+// 184 -> 178 us, the seven 64 x 64 shapes within 2%.
+template <bool AF>
+__device__ __forceinline__ int a_swz(int r) { return AF ? (r & 7) : ((r >> 1) & 7); }
+template <bool AF>
+__device__ __forceinline__ int b_swz(int r) { return AF ? (r & 3) : ((r & 3) ^ ((r >> 2) & 3)); }
 
 __device__ __forceinline__ void lds_dma16(const void *g, const void *lds) {
     const uint32_t la = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)lds;
@@ -289,7 +293,10 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     constexpr int NA = AF ? 3 : 1;
     // wave tiling: the operand that needs converting is owned by one wave per
     // fragment (f32 A: waves take BM/4-row strips; int8 B: BN/4-column strips),
-    // so no fragment is converted twice
+    // so no fragment is converted twice.  (Measured and rejected for the
+    // int8 LM head at M = 375: 2 x 2 waves of (BM/2) x (BN/2), which halve the
+    // A reads from LDS but widen every B fragment in two waves: 189 -> 209 us
+    // with 128 x 128 tiles, 248 us with 128 x 256 tiles of one block per CU.)
     constexpr int WR = (AF ? BM / 4 : BM) / 16, WC = (AF ? BN : BN / 4) / 16;
     static_assert(BSRC == (AF ? B_BF16 : B_I8), "operand pair");
     static_assert(BM % 32 == 0 && BN % 64 == 0, "tile");
@@ -324,12 +331,12 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     const char *a_src[LA], *b_src[LB];
 #pragma unroll
     for (int u = 0; u < LA; u++) {
-        const int r = 8 * (wid * LA + u) + (lane >> 3), p = (lane & 7) ^ a_swz(r);
+        const int r = 8 * (wid * LA + u) + (lane >> 3), p = (lane & 7) ^ a_swz<AF>(r);
         a_src[u] = A + ((int64_t)min(m0 + r, M - 1) * g.lda) * AE + 16 * p;
     }
 #pragma unroll
     for (int u = 0; u < LB; u++) {
-        const int r = 16 * (wid * LB + u) + (lane >> 2), p = (lane & 3) ^ b_swz(r);
+        const int r = 16 * (wid * LB + u) + (lane >> 2), p = (lane & 3) ^ b_swz<AF>(r);
         b_src[u] = B + ((int64_t)min(n0 + r, N - 1) * g.ldb) * BE + 16 * p;
     }
     const char *zero = reinterpret_cast<const char *>(g_gemm_zero16);
@@ -392,11 +399,11 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
             for (int j = 0; j < WC; j++) {
                 const int n = nw + j * 16 + fr;
                 if (BSRC == B_BF16) {
-                    const int p = fg ^ b_swz(n);
+                    const int p = fg ^ b_swz<AF>(n);
                     bfrag[j] = *reinterpret_cast<const bf16x8 *>(st + ASZ + n * 64 + p * 16);
                 } else {
                     // 8 int8 weights -> bf16 (exact: |q| <= 128 has 8 significant bits)
-                    const int p = (2 * s + (fg >> 1)) ^ b_swz(n);
+                    const int p = (2 * s + (fg >> 1)) ^ b_swz<AF>(n);
                     const uint2 v = *reinterpret_cast<const uint2 *>(st + ASZ + n * 64 + p * 16 + (fg & 1) * 8);
                     uint32_t w[4];
 #pragma unroll
@@ -415,8 +422,8 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                 if (AF) {
                     // f32 A = hi + mid + lo, each term the RNE bf16 of the remaining residual
                     const int k4 = 2 * fg;
-                    const float4 x0 = *reinterpret_cast<const float4 *>(st + r * 128 + ((k4 ^ a_swz(r)) * 16));
-                    const float4 x1 = *reinterpret_cast<const float4 *>(st + r * 128 + (((k4 + 1) ^ a_swz(r)) * 16));
+                    const float4 x0 = *reinterpret_cast<const float4 *>(st + r * 128 + ((k4 ^ a_swz<AF>(r)) * 16));
+                    const float4 x1 = *reinterpret_cast<const float4 *>(st + r * 128 + (((k4 + 1) ^ a_swz<AF>(r)) * 16));
                     const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                     uint32_t hi[4], mi[4], lo[4];
 #pragma unroll
@@ -436,7 +443,7 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                     af[NA > 1 ? 1 : 0] = __builtin_bit_cast(bf16x8, make_uint4(mi[0], mi[1], mi[2], mi[3]));
                     af[NA - 1] = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
                 } else {
-                    const int p = (4 * s + fg) ^ a_swz(r);
+                    const int p = (4 * s + fg) ^ a_swz<AF>(r);
                     af[0] = *reinterpret_cast<const bf16x8 *>(st + r * 128 + p * 16);
                 }
 #pragma unroll
