@@ -863,11 +863,14 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step(AttnDecodeArgs a) {
 //    scores, softmaxes and P V side by side, each with the single-head
 //    kernel's operations and order; the 4 waves' merge then runs one head per
 //    128 threads;
-//  * it holds one group of K rows, then one of V rows, in flight instead of
-//    the whole run: pass 1 loads a wave's K groups one after another (the
-//    next requested while the current one's scores form), the softmax then
-//    takes the max over all of the wave's scores as the single-stream kernel
-//    does, and pass 2 streams the V groups the same way.
+//  * a wave's K groups (its share of the stream's partition, not the
+//    launch's maximum) all go out at entry; its V groups go out once the
+//    scores are formed, into the same registers, and arrive while the
+//    softmax runs (101 VGPRs, 4 waves per SIMD at 4 groups per wave).
+//    Measured on config 4 (us per layer): both heads per block with one
+//    group of K, then of V, in flight 46.2; all groups in flight 43.3; one
+//    head per block, one group in flight 54.3, or the whole run of K and V
+//    in registers at once 69.9.
 // Groups past the stream's context read row 0 (masked, adding exact zeros);
 // blocks wholly past it store empty partials and leave.  Grid row y is
 // stream stream_order[y]; grid column kvh + Hkv x split; partials go split
@@ -936,9 +939,13 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
     const float2 knw = reinterpret_cast<const float2 *>(a.k_norm)[lane];
     const float2 cs = reinterpret_cast<const float2 *>(rope_cur)[lane];
     const float2 sn = reinterpret_cast<const float2 *>(rope_cur + D)[lane];
-    Kp kcur[8], knext[8];
+    Kp kr[GPW][8];
 #pragma unroll
-    for (int p = 0; p < 8; p++) kcur[p].load(kc + row_of(0, p), lane);
+    for (int i = 0; i < GPW; i++)
+        if (i < gpw_own) {                            // uniform
+#pragma unroll
+            for (int p = 0; p < 8; p++) kr[i][p].load(kc + row_of(i, p), lane);
+        }
     __builtin_amdgcn_sched_barrier(0);
 
     const int L = pos + 1;
@@ -959,24 +966,20 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
         }
     }
 
-    // ---- pass 1: scores, one K group in flight behind the one being used ----
+    // ---- pass 1: scores --------------------------------------------------------
     float sc[G][GPW];
 #pragma unroll
     for (int i = 0; i < GPW; i++) {
 #pragma unroll
         for (int g = 0; g < G; g++) sc[g][i] = -INFINITY;
         if (i >= gpw_own) continue;                   // uniform
-        if (i + 1 < gpw_own) {
-#pragma unroll
-            for (int p = 0; p < 8; p++) knext[p].load(kc + row_of(i + 1, p), lane);
-        }
         const int jb = 8 * (g0 + wid + NW * i);
 #pragma unroll
         for (int g = 0; g < G; g++) {
             float v8[8];
 #pragma unroll
             for (int p = 0; p < 8; p++) {
-                float kx = kcur[p].x(), ky = kcur[p].y();
+                float kx = kr[i][p].x(), ky = kr[i][p].y();
                 if (own_pos && jb + p == pos) { kx = kn.x; ky = kn.y; }
                 v8[p] = fmaf(q[g].y, ky, __fmul_rn(q[g].x, kx));
             }
@@ -996,13 +999,15 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
             r3 = __fadd_rn(r3, dpp_f32<QASR_DPP_QP_2301>(r3));
             sc[g][i] = jb + my_p < j1 ? __fmul_rn(r3, a.scale) : -INFINITY;
         }
-#pragma unroll
-        for (int p = 0; p < 8; p++) kcur[p] = knext[p];
     }
-    // the first V group goes out while the softmax forms
-    Kp vcur[8], vnext[8];
+    // every V group goes out while the softmax forms (into the K rows' registers)
+    Kp vr[GPW][8];
 #pragma unroll
-    for (int p = 0; p < 8; p++) vcur[p].load(vc + row_of(0, p), lane);
+    for (int i = 0; i < GPW; i++)
+        if (i < gpw_own) {                            // uniform
+#pragma unroll
+            for (int p = 0; p < 8; p++) vr[i][p].load(vc + row_of(i, p), lane);
+        }
 
     // ---- softmax over this wave's positions (the single-stream order) -------
     float m[G], l[G];
@@ -1031,15 +1036,11 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
         l[g] = lg;
     }
 
-    // ---- pass 2: P V, one V group in flight behind the one being used -------
+    // ---- pass 2: P V ------------------------------------------------------------
     float ox[G] = {0.0f, 0.0f}, oy[G] = {0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < GPW; i++) {
         if (i >= gpw_own) continue;                   // uniform
-        if (i + 1 < gpw_own) {
-#pragma unroll
-            for (int p = 0; p < 8; p++) vnext[p].load(vc + row_of(i + 1, p), lane);
-        }
         const int jb = 8 * (g0 + wid + NW * i);
 #pragma unroll
         for (int g = 0; g < G; g++) {
@@ -1053,7 +1054,7 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
 #pragma unroll
             for (int p = 0; p < 8; p++) {
                 const bool live = jb + p < j1;
-                float vx = live ? vcur[p].x() : 0.0f, vy = live ? vcur[p].y() : 0.0f;
+                float vx = live ? vr[i][p].x() : 0.0f, vy = live ? vr[i][p].y() : 0.0f;
                 if (own_pos && jb + p == pos) { vx = vn.x; vy = vn.y; }
                 gx = fmaf(P[p], vx, gx);
                 gy = fmaf(P[p], vy, gy);
@@ -1061,8 +1062,6 @@ __global__ __launch_bounds__(NW * 64) void k_attn_step_batch(AttnDecodeArgs a) {
             ox[g] = __fadd_rn(ox[g], gx);
             oy[g] = __fadd_rn(oy[g], gy);
         }
-#pragma unroll
-        for (int p = 0; p < 8; p++) vcur[p] = vnext[p];
     }
 
     // ---- merge the waves of the block per head (LDS, one barrier) -----------
