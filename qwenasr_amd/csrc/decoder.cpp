@@ -463,19 +463,26 @@ int decoder_set_state(qasr_decoder *d, int32_t token) {
 
 static int set_state(qasr_decoder *d, int32_t token) { return decoder_set_state(d, token); }
 
-int decoder_run_embed_step(qasr_decoder *d) {
-    if (!d->use_graph) {
-        TRY(decoder_enqueue_step(d, true));
-        d->step_pos += 1;
-        return QASR_OK;
-    }
-    const int64_t cap = decoder_ctx_cap(d, d->step_pos + 1);
-    auto it = d->graphs.find(cap);
+// Token-fed decode steps replay captured graphs, one per (context bucket,
+// steps per graph): runs of QASR_GRAPH_STEPS steps inside one bucket replay a
+// graph of that many steps (the device advances token, position and RoPE rows
+// between them), the rest one step at a time.  The kernels and their order are
+// those of single steps, so the results do not depend on the grouping.
+#define QASR_GRAPH_STEPS 4
+static int run_step_graph(qasr_decoder *d, int64_t cap, int n) {
+    const int64_t key = cap * 16 + n;
+    auto it = d->graphs.find(key);
     if (it == d->graphs.end()) {
         hipGraph_t g = nullptr;
         hipGraphExec_t ge = nullptr;
+        const int64_t pos0 = d->step_pos;
         HIPCHK(hipStreamBeginCapture(d->h->stream, hipStreamCaptureModeThreadLocal));
-        int rc = decoder_enqueue_step(d, true);
+        int rc = QASR_OK;
+        for (int k = 0; k < n && rc == QASR_OK; k++) {
+            rc = decoder_enqueue_step(d, true);
+            d->step_pos += 1;
+        }
+        d->step_pos = pos0;
         hipError_t e = hipStreamEndCapture(d->h->stream, &g);
         if (rc != QASR_OK) {
             if (g) (void)hipGraphDestroy(g);
@@ -485,13 +492,32 @@ int decoder_run_embed_step(qasr_decoder *d) {
         e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
         (void)hipGraphDestroy(g);
         HIPCHK(e);
-        it = d->graphs.emplace(cap, ge).first;
+        it = d->graphs.emplace(key, ge).first;
     }
     HIPCHK(hipGraphLaunch(it->second, d->h->stream));
-    d->step_pos += 1;
-    d->epochs += 1;
+    d->step_pos += n;
+    d->epochs += n;
     return QASR_OK;
 }
+
+int decoder_run_embed_steps(qasr_decoder *d, int64_t n) {
+    while (n > 0) {
+        if (!d->use_graph) {
+            TRY(decoder_enqueue_step(d, true));
+            d->step_pos += 1;
+            n -= 1;
+            continue;
+        }
+        const int64_t cap = decoder_ctx_cap(d, d->step_pos + 1);
+        const int k = n >= QASR_GRAPH_STEPS && decoder_ctx_cap(d, d->step_pos + QASR_GRAPH_STEPS) == cap
+                          ? QASR_GRAPH_STEPS : 1;
+        TRY(run_step_graph(d, cap, k));
+        n -= k;
+    }
+    return QASR_OK;
+}
+
+int decoder_run_embed_step(qasr_decoder *d) { return decoder_run_embed_steps(d, 1); }
 
 int decoder_fault_check(qasr_decoder *d) {
     int32_t f = 0;
@@ -544,7 +570,7 @@ extern "C" int qasr_hip_decoder_generate(qasr_decoder *d, const float *first_emb
     } else {
         TRY(decoder_run_embed_step(d));
     }
-    for (int32_t s = 1; s < n_steps; s++) TRY(decoder_run_embed_step(d));
+    TRY(decoder_run_embed_steps(d, n_steps - 1));
     HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost,
                           d->h->stream));
     HIPCHK(hipStreamSynchronize(d->h->stream));

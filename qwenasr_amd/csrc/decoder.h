@@ -93,6 +93,7 @@ struct PrefillSeg {
 // sequence alone would give.
 int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg);
 int decoder_run_embed_step(qasr_decoder *d);
+int decoder_run_embed_steps(qasr_decoder *d, int64_t n);
 // host -> device decode state {token, pos = d->len, 0, 0} and the RoPE rows of pos
 int decoder_set_state(qasr_decoder *d, int32_t token);
 // after the caller's synchronisation: QASR_ERR_HIP when a fused qkv + attention

@@ -669,7 +669,7 @@ extern "C" int qasr_hip_transcribe_forced(qasr_decoder *d, qasr_encoder *e, cons
     auto body = [&]() -> int {
         TRY(transcribe_begin(d, e, samples, n, n_steps, nullptr, nullptr, 0, &total));
         hipStream_t st = d->h->stream;
-        for (int32_t s = 1; s < n_steps; s++) TRY(decoder_run_embed_step(d));
+        TRY(decoder_run_embed_steps(d, n_steps - 1));
         HIPCHK(hipEventRecord(e->ev[4], st));
         HIPCHK(hipMemcpyAsync(tokens_out, d->token_log, sizeof(int32_t) * n_steps, hipMemcpyDeviceToHost, st));
         HIPCHK(hipStreamSynchronize(st));
@@ -720,7 +720,7 @@ extern "C" int qasr_hip_transcribe_prompt(qasr_decoder *d, qasr_encoder *e, cons
             seen = done;
             if (stop_at >= 0 || done >= max_tokens) break;
             const int64_t b = std::min<int64_t>(BURST, max_tokens - done);
-            for (int64_t s = 0; s < b; s++) TRY(decoder_run_embed_step(d));
+            TRY(decoder_run_embed_steps(d, b));
             done += b;
         }
         HIPCHK(hipEventRecord(e->ev[4], st));

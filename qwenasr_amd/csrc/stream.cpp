@@ -367,7 +367,7 @@ static int decode_chunk(qasr_stream *s, int64_t prefill_len, std::vector<int32_t
         }
         if (stop || (int64_t)chunk.size() >= max_new) break;
         const int64_t burst = std::min<int64_t>(DECODE_BURST, max_new - done);
-        for (int64_t i = 0; i < burst; i++) TRY(decoder_run_embed_step(d));
+        TRY(decoder_run_embed_steps(d, burst));
         done += burst;
     }
     TRY(decoder_fault_check(d));

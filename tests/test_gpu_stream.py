@@ -90,3 +90,36 @@ def test_stream_long_window_reuse(models, orc):
     assert any(b < a for a, b in zip(prefill, prefill[1:])), prefill
     g.close()
     c.close()
+
+
+def test_stream_periodic_reanchor(models, orc):
+    """48 pushes of 0.5 s chunks (chunk_sec 0.5, max_new_tokens 3, rollback 1):
+    the stream passes chunk 45, where the reference re-anchors every 45 chunks
+    whatever the tokens (transcribe.rs:1231-1252), and the GPU stream commits
+    the oracle's tokens and statistics at every push.  After that chunk the
+    raw tokens are <asr_text> and the last min(24, committed) committed tokens
+    (the carry; this random-init model commits only a few), and the next chunk
+    reuses no prefill rows."""
+    from qwenasr_amd.model import Stream
+    from qwenasr_amd.synth import audio
+    gdec, genc, cdec, cenc, _ = models
+    x = audio(24 * 16000, 1045)
+    cfg = dict(max_new_tokens=3, rollback=1, chunk_sec=0.5)
+    g = Stream(gdec, genc, **cfg)
+    c = orc.OracleStream(cdec, cenc, **cfg)
+    after = None
+    for k, end in enumerate(range(8000, x.size + 1, 8000)):
+        eg, ec = g.push(x[:end]), c.push(x[:end])
+        assert list(eg) == list(ec), (k, eg, ec)
+        sg, sc = g.stats(), c.stats()
+        assert list(sg[STAT_COLS]) == list(sc[STAT_COLS]), (k, sg, sc)
+        if int(sg[0]) == 46:                          # chunk index 45 processed
+            committed = len(g.tokens())
+            assert int(sg[7]) == (1 + min(24, committed) if committed else 0), (sg, committed)
+            after = k
+        if after is not None and k == after + 1:
+            assert int(sg[1]) == 0, sg                # no prefill reuse after a re-anchor
+    assert after is not None and int(g.stats()[0]) == 48
+    assert list(g.tokens()) == list(c.tokens())
+    g.close()
+    c.close()

@@ -157,3 +157,27 @@ def test_window_cache_and_stop_token(orc, tiny):
     s.push(x[:32000])
     assert s.stats()[7] == 0                          # the first chunk stopped at once
     s.close()
+
+
+def test_periodic_reanchor(orc, tiny):
+    """Every 45 chunks the reference re-anchors whatever the tokens
+    (transcribe.rs:1231-1252): raw becomes <asr_text> and the last
+    min(24, committed) committed tokens, prefix reuse restarts.  48 chunks of
+    0.5 s: after chunk index 45 the raw count is 1 + min(24, committed) (or 0
+    with nothing committed) and the next chunk prefills every row."""
+    from qwenasr_amd.synth import audio
+    _, _, dec, enc, _ = tiny
+    x = audio(24 * 16000, 1045)
+    s = orc.OracleStream(dec, enc, max_new_tokens=3, rollback=1, chunk_sec=0.5)
+    seen = False
+    for end in range(8000, x.size + 1, 8000):
+        s.push(x[:end])
+        st = s.stats()
+        if st[0] == 46:
+            committed = len(s.tokens())
+            assert st[7] == (1 + min(24, committed) if committed else 0), (st, committed)
+            seen = True
+        if st[0] == 47:
+            assert st[1] == 0 and st[3] == st[2], st
+    assert seen and s.stats()[0] == 48
+    s.close()
