@@ -600,7 +600,11 @@ __device__ __forceinline__ void mfma_rows16(const int8_t *__restrict__ wrow, con
 // load issued up front: the weight tile streams in one round trip); the 16
 // int32 partial tiles are summed through LDS (exact, so the order is free) and
 // the block applies the epilogue, threads over (stream, row) so that stores
-// are row-contiguous.
+// are row-contiguous.  (Measured and rejected for the 64-tile shapes, o_proj
+// and down at 0.6B: K split over 2-3 blocks per tile, each publishing its
+// int32 tile and the last to arrive (arrive_last) adding them, 5.3 -> 14.9
+// and 7.0 -> 16.6 us per launch: the agent-scope release before the counter
+// bump costs more than the CUs the 64 blocks leave idle.)
 template <int MODE, int ST>
 __global__ __launch_bounds__(1024) void k_w8a8_batch(BatchMvArgs a) {
     constexpr int W = 16;

@@ -387,8 +387,11 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
     if (wid == 0) QASR_STAMP(stamp, 2);
     int xd[NS][4];
     float xs;
-    // (the fused qkv + attention launch, TAG, takes the unrolled RMSNorm reads)
-    act_finish_block<NS, NORM, EMBED, TAG>(in, a.eps, K, lds + wid * QASR_NORM_LDS(NS), qlds, xd, &xs);
+    // (the fused qkv + attention launch, TAG, takes the unrolled RMSNorm reads
+    // at K = 1024; at K = 2048 they raised its VGPRs 120 -> 169, leaving 2
+    // waves per SIMD, one block per CU, and the 1.7B launch at L = 4096 grew
+    // 16.8 -> 22.1 us)
+    act_finish_block<NS, NORM, EMBED, TAG && NS == 1>(in, a.eps, K, lds + wid * QASR_NORM_LDS(NS), qlds, xd, &xs);
     if (wid == 0) QASR_STAMP(stamp, 3);
     // per-lane partial dots, then one reduce-scatter: every lane ends with its
     // item's complete sums.  The epilogue runs in every lane with no branch
