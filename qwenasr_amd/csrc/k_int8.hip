@@ -120,14 +120,16 @@ __global__ __launch_bounds__(256) void k_oproj_merge(OprojMergeArgs a) {
     if (a.stamps) stamp = a.stamps + ((int64_t)a.layer * QASR_STAMP_BLOCKS + blockIdx.x) * QASR_STAMP_SLOTS;
 #endif
     if (wid == 0) QASR_STAMP(stamp, 0);
-    // (1) this thread's o partials: heads h = 2 j + g, dim d, all splits
+    // (1) (m, l) of entry e = (head, split) = (e / S, e % S), first, so that
+    // the merge weights form while the o partials are still arriving (loads
+    // complete in issue order); threads past 16 S reload entry t % (16 S).
+    // Then this thread's o partials: heads h = 2 j + g, dim d, all splits
+    const int e = t % (HQ * S), eh = e / S, es = e % S;
+    const float pm = a.part[(2 * eh) * S + es], pl = a.part[(2 * eh + 1) * S + es];
     const float *po = a.part + 2 * HQ * S;
     float ov[HQ / 2][S];
 #pragma unroll
     for (int j = 0; j < HQ / 2; j++) ld_split<S>(po + ((2 * j + g) * D + d) * S, ov[j]);
-    // (m, l) of entry e = (head, split) = (e / S, e % S); threads past 16 S reload entry t % (16 S)
-    const int e = t % (HQ * S), eh = e / S, es = e % S;
-    const float pm = a.part[(2 * eh) * S + es], pl = a.part[(2 * eh + 1) * S + es];
     // (2) weights and epilogue operands of this wave's rows (rows past N read row 0 and are not stored)
     const int row0 = (blockIdx.x * 4 + wid) * R;
     const bool live = row0 < a.N;
