@@ -334,7 +334,12 @@ __device__ __forceinline__ void w8a8_wave(const MvArgs &a, int blk, float *lds, 
     const int row0 = live ? (blk * 4 + wid) * R : 0;
     const int K = a.K, nslot = K >> 4;
     // segment of this wave (segments are multiples of R rows); scalar selects
-    // keep the segment fields in SGPRs
+    // keep the segment fields in SGPRs.  (The compiler loads the selected
+    // fields from a selected argument address, a second scalar round trip
+    // after the first batch of argument loads.  Reading all nine fields in
+    // the first batch and selecting the values moved the first weight loads
+    // 0.16 us earlier inside the launch but measured slower per launch:
+    // gate_up 3.99 -> 4.33, down 3.45 -> 4.24 us.)
     const int n0 = a.seg[0].n, n1 = a.seg[1].n;
     const bool in0 = row0 < n0, in1 = !in0 && row0 < n0 + n1;
     MvSeg S;
