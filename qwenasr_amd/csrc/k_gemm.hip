@@ -308,14 +308,7 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     const int grp = wave >> 2, wid = wave & 3;          // K group, wave within the group
     auto &smem = smem_all[grp];
     const int mw = AF ? (BM / 4) * wid : 0, nw = AF ? 0 : (BN / 4) * wid;
-    const int n0 = blockIdx.x * BN;
-    // M tiles: blockIdx.y's, or with a grid of one row every tile of the
-    // column strip in turn (the strip's B rows then come from L2 after the
-    // first tile instead of HBM once per tile)
-    const int gy_all = (g.M + BM - 1) / BM;
-    for (int mt = blockIdx.y; mt < gy_all; mt += gridDim.y) {
-    const int m0 = mt * BM;
-    if (mt != (int)blockIdx.y) __syncthreads();   // every wave is past the previous tile's ring reads
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int M = g.M, N = g.N, K = g.K;
     // split K (KS > 1, grid z = KS): this block's K-steps [k0s, k0s + nk); its
     // raw partial sums go to the workspace and a reduction pass runs the
@@ -548,7 +541,6 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                     if (m < M && n < N) g.ws[((int64_t)kz * M + m) * N + n] = acc[i][j][r];
                 }
     }
-    }
 }
 
 // split-K reduction: the partials summed in split order, then the epilogue
@@ -678,10 +670,10 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
         }
         return hipGetLastError();
     }
-    // (a grid of one M row makes each block walk every M tile of its column
-    // strip, reading the strip's weights from HBM once: for the config-1 LM
-    // head, 1187 strips at M = 375, it measured 205 us against 160-184 with a
-    // block per tile, so no launch uses it)
+    // (measured and rejected: each block walking every M tile of its column
+    // strip, so that the strip's weights are read from HBM once: for the
+    // config-1 LM head, 1187 strips at M = 375, 205 us against 160-184 with a
+    // block per tile)
     const dim3 grid(gx, gy);
     switch (epi) {
 #define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, 1>), grid, dim3(256), 0, st, g); break;
