@@ -687,11 +687,20 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
 template <int ASRC, int BSRC>
 static hipError_t go_gemm_lds(const GemmArgs &g, int epi, hipStream_t st) {
     // 64 x 64 tiles (4 stages of 12 KiB, 3 blocks per CU) while they leave
-    // fewer than ~2 blocks per CU; beyond, 128 x 128 tiles (3 stages of 24
-    // KiB): four times the MFMA work per K-step and barrier
+    // fewer than ~2 blocks per CU; beyond, 128 x 128 tiles: four times the
+    // MFMA work per K-step and barrier.  Their bf16 x int8 form keeps 2
+    // stages of 24 KiB, so that 3 blocks share a CU (LM head at M = 375, 3
+    // stages -> 2: 174 -> 155 us, the same bits).  Measured and rejected
+    // there: 128 x 256 tiles (218-226 us); 2 waves of 64-column strips, which
+    // halve the A reads from LDS but need 287 registers (206 us); the M tiles
+    // of one column strip grouped on one XCD (162 us, against 155); and the
+    // activations split into three int8 planes on the int8 MFMA (273-282 us:
+    // three bytes per activation through the ring and the LDS reads).
     const int64_t small_blocks = (int64_t)((g.N + 63) / 64) * ((g.M + 63) / 64);
     const bool big = small_blocks >= 2048;
-    return big ? go_gemm_lds_ns<ASRC, BSRC, 3, 128, 128>(g, epi, st) : go_gemm_lds_ns<ASRC, BSRC, 4, 64, 64>(g, epi, st);
+    constexpr int big_ns = ASRC == A_BF16 ? 2 : 3;
+    return big ? go_gemm_lds_ns<ASRC, BSRC, big_ns, 128, 128>(g, epi, st)
+               : go_gemm_lds_ns<ASRC, BSRC, 4, 64, 64>(g, epi, st);
 }
 
 // the LDS-ring kernel applies when every stage is whole and rows are 16-byte aligned
