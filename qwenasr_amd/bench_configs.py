@@ -178,8 +178,17 @@ def config0(reps=256, mall_mib=256):
     dev.close()
 
 
-def config1(reps=20):
+def config1(reps=20, calib_mib=0):
+    """calib_mib > 0: first one device copy of that many MiB (the library's
+    copy kernel), the calibration launch of a FETCH_SIZE / WRITE_SIZE counter run."""
     dev = Device(0)
+    if calib_mib > 0:
+        src = dev.zeros(calib_mib << 20, np.uint8)
+        dst = dev.empty(calib_mib << 20, np.uint8)
+        dev.copy(dst, src)
+        dev.sync()
+        src.free()
+        dst.free()
     shapes = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
               ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072), ("lm_head", 151936, 1024)]
     rows = []
@@ -570,7 +579,7 @@ if __name__ == "__main__":
     if what == "config0":
         config0(int(sys.argv[2]) if len(sys.argv) > 2 else 256)
     elif what == "config1":
-        config1(int(sys.argv[2]) if len(sys.argv) > 2 else 20)
+        config1(int(sys.argv[2]) if len(sys.argv) > 2 else 20, int(sys.argv[3]) if len(sys.argv) > 3 else 0)
     elif what == "config3":
         config3(int(sys.argv[2]) if len(sys.argv) > 2 else 28, int(sys.argv[3]) if len(sys.argv) > 3 else 20)
     elif what == "config4":

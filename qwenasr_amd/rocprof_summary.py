@@ -3,7 +3,7 @@
     python -m qwenasr_amd.rocprof_summary <dir>/run_kernel_trace.csv [min_batch]
     python -m qwenasr_amd.rocprof_summary --pmc <dir>/run_counter_collection.csv <calib MiB>
     python -m qwenasr_amd.rocprof_summary --traffic <fetch csv> <write csv> <calib MiB> > profiles/hbm_traffic.txt
-    python -m qwenasr_amd.rocprof_summary --mfma-config1 <MfmaUtil csv> <MOPS csv> [reps]
+    python -m qwenasr_amd.rocprof_summary --mfma-config1 <MfmaUtil csv> <MOPS csv> [reps [<FETCH csv> <WRITE csv> <calib MiB>]]
 
 The second form averages each kernel's counter values (``--pmc FETCH_SIZE`` or
 ``WRITE_SIZE``, KiB per dispatch) and scales them by what the counter read for
@@ -156,14 +156,23 @@ def _gemm_dispatches(path):
     return [per[k] for k in sorted(per)]
 
 
-def mfma_config1(util_csv, mops_csv, reps=3):
+def mfma_config1(util_csv, mops_csv, reps=3, fetch_csv=None, write_csv=None, calib_mib=0.0):
     """The config-1 MFMA table from two counter runs of `bench_configs config1 <reps>`
     (--pmc MfmaUtil; --pmc SQ_INSTS_VALU_MFMA_MOPS_BF16 GRBM_GUI_ACTIVE): per shape the
-    median over its reps timed launches (each shape's first launch is its warm-up)."""
+    median over its reps timed launches (each shape's first launch is its warm-up).
+    With the FETCH_SIZE and WRITE_SIZE runs of `bench_configs config1 <reps> <calib MiB>`
+    (whose first launch copies calib MiB with k_copy16), also the HBM bytes per launch,
+    calibrated on that copy, against the algorithmic bytes (weights, scales, activations
+    and the f32 output once)."""
     util, mops = _gemm_dispatches(util_csv), _gemm_dispatches(mops_csv)
+    hbm = fetch_csv is not None
+    if hbm:
+        (_, fs), (_, ws) = _pmc_bytes(fetch_csv, calib_mib), _pmc_bytes(write_csv, calib_mib)
+        fetch, write = _gemm_dispatches(fetch_csv), _gemm_dispatches(write_csv)
     per = 1 + reps
-    out = ["| M | shape | N x K | kernel | MfmaUtil % | executed GFLOP | 2MNK GFLOP | us | TFLOP/s | % of peak |",
-           "|---:|---|---|---|---:|---:|---:|---:|---:|---:|"]
+    out = ["| M | shape | N x K | kernel | MfmaUtil % | executed GFLOP | 2MNK GFLOP | us | TFLOP/s | % of peak |" +
+           (" HBM read MB | HBM write MB | algorithmic MB |" if hbm else ""),
+           "|---:|---|---|---|---:|---:|---:|---:|---:|---:|" + ("---:|---:|---:|" if hbm else "")]
     for i, M in enumerate((375, 390, 404)):
         for j, (name, N, K) in enumerate(CONFIG1_SHAPES):
             base = (i * len(CONFIG1_SHAPES) + j) * per
@@ -172,14 +181,22 @@ def mfma_config1(util_csv, mops_csv, reps=3):
             us = st.median(d[2] for d in mops[base + 1:base + per]) / 1e3
             kern = re.sub(r"qasr::k_gemm_lds<(.*)>", r"\1", mops[base + 1][0])
             tf = ex * 1e3 / us
-            out.append(f"| {M} | {name} | {N}x{K} | `{kern}` | {u:.2f} | {ex:.3f} | {2.0 * M * N * K / 1e9:.3f} | "
-                       f"{us:.2f} | {tf:.1f} | {100 * tf / BF16_PEAK_TFLOPS:.1f} |")
+            row = (f"| {M} | {name} | {N}x{K} | `{kern}` | {u:.2f} | {ex:.3f} | {2.0 * M * N * K / 1e9:.3f} | "
+                   f"{us:.2f} | {tf:.1f} | {100 * tf / BF16_PEAK_TFLOPS:.1f} |")
+            if hbm:
+                rd = st.median(d[1]["FETCH_SIZE"] for d in fetch[base + 1:base + per]) * 1024 * fs / 1e6
+                wr = st.median(d[1]["WRITE_SIZE"] for d in write[base + 1:base + per]) * 1024 * ws / 1e6
+                alg = (N * K + 4.0 * N + 2.0 * M * K + 4.0 * M * N) / 1e6
+                row += f" {rd:.1f} | {wr:.1f} | {alg:.1f} |"
+            out.append(row)
     return "\n".join(out)
 
 
 if __name__ == "__main__":
     if sys.argv[1] == "--mfma-config1":
-        print(mfma_config1(sys.argv[2], sys.argv[3], int(sys.argv[4]) if len(sys.argv) > 4 else 3))
+        a = sys.argv
+        print(mfma_config1(a[2], a[3], int(a[4]) if len(a) > 4 else 3, *(a[5:7] if len(a) > 7 else ()),
+                           *((float(a[7]),) if len(a) > 7 else ())))
     elif sys.argv[1] == "--traffic":
         print(traffic(sys.argv[2], sys.argv[3], float(sys.argv[4])))
     elif sys.argv[1] == "--pmc":
