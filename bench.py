@@ -71,7 +71,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (got --gpus {args.gpus}); the multi-GPU "
-              "sharding of the path is described in DESIGN.md, not implemented", file=sys.stderr)
+              "sharding of the path is a design, not implemented", file=sys.stderr)
         sys.exit(2)
 
     from qwenasr_amd import Device

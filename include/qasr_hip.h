@@ -10,7 +10,8 @@
  * Each entry point cites the reference function it replaces
  * (crates/qwen-asr/src/...:line).  The reference binds native code the same
  * way it binds BLAS today (kernels/mod.rs:11-59, build.rs:1-18); the Rust
- * binding a maintainer would add is shown in INTEGRATION.md.
+ * binding a maintainer would add is generated from this header by
+ * `python -m qwenasr_amd.ffi_rust`.
  *
  * Threading: one handle per host thread (the handle owns one HIP stream and a
  * small scratch area).  Op-level calls take device pointers, enqueue work on

@@ -6,8 +6,8 @@ Emits what the reference crate would add as `src/kernels/hip.rs` (behind its
 `hip` feature): the status and mode constants, one opaque `#[repr(C)]` type
 per handle, one `#[repr(C)]` struct per configuration / weight table with the
 header's field order, and one `extern "C"` declaration per entry point, with
-the header's argument names.  INTEGRATION.md embeds this output; a test checks
-that it is current.
+the header's argument names.  The integration notes embed this output, and
+tests/test_abi.py checks that the embedded copy is current.
 """
 import os
 import re

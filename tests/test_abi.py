@@ -73,8 +73,9 @@ def test_c_smoke_builds_and_header_is_c_and_cxx(tmp_path):
 
 
 def test_integration_ffi_block_is_current():
-    """INTEGRATION.md's Rust FFI module is the generator's output for the
-    current header: one declaration per entry point, nothing elided."""
+    """The Rust FFI module embedded in the integration notes is the
+    generator's output for the current header: one declaration per entry
+    point, nothing elided."""
     import re
     from qwenasr_amd import ffi_rust
     header = open(os.path.join(ROOT, "include", "qasr_hip.h")).read()
