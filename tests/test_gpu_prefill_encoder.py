@@ -43,7 +43,8 @@ def test_linear_bf16w(dev, orc, M, N, K):
 
 @pytest.mark.parametrize("M,N,K", [(375, 2048, 1024), (375, 1024, 1024), (375, 1024, 2048), (375, 1024, 3072),
                                    (375, 6144, 1024), (375, 151936, 1024), (1, 1024, 1024), (67, 1024, 3072),
-                                   (404, 1024, 1024), (67, 151936, 1024)])
+                                   (404, 1024, 1024), (67, 151936, 1024), (1, 151936, 1024), (129, 151936, 1024),
+                                   (130, 151936, 2048)])
 def test_gemm_w8_bf16_config1(dev, orc, M, N, K):
     """Config 1: M = 375 rows of bf16 activations x int8 per-row weights, the
     0.6B shapes (q, k / v, o, down, gate_up, LM head) and edge row counts
