@@ -29,6 +29,9 @@ struct qasr_encoder {
     qasr_hip *h = nullptr;
     qasr_enc_config c{};
     uint16_t *conv1_w = nullptr, *conv2_w = nullptr, *conv3_w = nullptr, *conv_out_w = nullptr;
+    // channels-last conv stem (conv_hidden % 32 == 0): conv2 / conv3 / conv_out
+    // weights hold K in (tap, channel) order for the implicit-im2col GEMM
+    bool stem_nhwc = false;
     float *conv1_b = nullptr, *conv2_b = nullptr, *conv3_b = nullptr;
     std::vector<EncLayerDev> L;
     float *ln_post_w = nullptr, *ln_post_b = nullptr;
@@ -124,12 +127,37 @@ static int encoder_build(qasr_encoder *e, const qasr_enc_weights *w) {
     Stager stg(e->h->stream);
     TRY(stg.init());
     TRY(eupload_big(e, stg, &e->conv1_w, w->conv1_w, C * 9));
-    TRY(eupload_big(e, stg, &e->conv2_w, w->conv2_w, C * C * 9));
-    TRY(eupload_big(e, stg, &e->conv3_w, w->conv3_w, C * C * 9));
+    e->stem_nhwc = C % 32 == 0;
+    if (e->stem_nhwc) {
+        // each matrix staged as the reference holds it ([out][channel][tap]),
+        // then reordered on the device to [out][tap][channel]; the staging
+        // buffer is reused in stream order and freed once the stream drains
+        uint16_t *raw = nullptr;
+        const size_t raw_n = (size_t)std::max(C * C * 9, D * C * h3);
+        if (hipMalloc(&raw, raw_n * sizeof(uint16_t)) != hipSuccess)
+            return qasr_fail(QASR_ERR_NOMEM, "encoder: device allocation failed");
+        const struct { uint16_t **dst; const uint16_t *src; int64_t o, t; } mats[3] = {
+            {&e->conv2_w, w->conv2_w, C, 9}, {&e->conv3_w, w->conv3_w, C, 9}, {&e->conv_out_w, w->conv_out_w, D, h3}};
+        int rc = QASR_OK;
+        for (const auto &m : mats) {
+            if (rc == QASR_OK) rc = ealloc(e, m.dst, (size_t)(m.o * C * m.t));
+            if (rc == QASR_OK) rc = stg.upload(raw, m.src, sizeof(uint16_t) * m.o * C * m.t);
+            if (rc == QASR_OK && launch_taps_last(*m.dst, raw, (int)m.o, (int)C, (int)m.t, e->h->stream) != hipSuccess)
+                rc = qasr_fail(QASR_ERR_HIP, "encoder: weight reorder failed");
+        }
+        if (rc == QASR_OK) rc = stg.finish();
+        if (rc == QASR_OK && hipStreamSynchronize(e->h->stream) != hipSuccess)
+            rc = qasr_fail(QASR_ERR_HIP, "encoder: weight reorder failed");
+        (void)hipFree(raw);
+        if (rc != QASR_OK) return rc;
+    } else {
+        TRY(eupload_big(e, stg, &e->conv2_w, w->conv2_w, C * C * 9));
+        TRY(eupload_big(e, stg, &e->conv3_w, w->conv3_w, C * C * 9));
+        TRY(eupload_big(e, stg, &e->conv_out_w, w->conv_out_w, D * C * h3));
+    }
     TRY(eupload(e, &e->conv1_b, w->conv1_b, C));
     TRY(eupload(e, &e->conv2_b, w->conv2_b, C));
     TRY(eupload(e, &e->conv3_b, w->conv3_b, C));
-    TRY(eupload_big(e, stg, &e->conv_out_w, w->conv_out_w, D * C * h3));
     e->L.resize(c.n_layers);
     for (int l = 0; l < c.n_layers; l++) {
         const qasr_enc_layer &s = w->layers[l];
@@ -255,14 +283,60 @@ static int egemm(qasr_encoder *e, const float *A, int64_t lda, const uint16_t *B
     return QASR_OK;
 }
 
+// implicit-im2col GEMM of a channels-last convolution (K in (tap, channel)
+// order): out[(chunk, oy, ox)][n] with the reference's GELU index rule
+static int econv(qasr_encoder *e, const float *in, int n_chunks, int hin, int win, int cin, int hout, int wout,
+                 int kh, int kw, int sy, int sx, int py, int px, const uint16_t *w, int N, const float *bias,
+                 float *out, int64_t ldc, int epi) {
+    GemmArgs g{};
+    g.M = n_chunks * hout * wout; g.N = N; g.K = cin * kh * kw;
+    g.A = in; g.lda = cin; g.B = w; g.ldb = g.K; g.C = out; g.ldc = ldc; g.bias = bias;
+    g.gelu_n = (int64_t)N * hout * wout; g.gelu_rows = hout * wout;
+    g.conv_hin = hin; g.conv_win = win; g.conv_c = cin; g.conv_hout = hout; g.conv_wout = wout;
+    g.conv_kh = kh; g.conv_kw = kw; g.conv_sy = sy; g.conv_sx = sx; g.conv_py = py; g.conv_px = px;
+    LAUNCHCHK(launch_gemm(g, A_CONV, B_BF16, epi, e->h->stream), "encoder conv gemm");
+    return QASR_OK;
+}
+
 // conv stem for n_chunks chunks of cw frames starting at frame f0; writes the
-// projected + PE rows to x (encoder.rs:226-287)
+// projected + PE rows to x (encoder.rs:226-287).  With stem_nhwc the
+// activations stay channels-last, [chunk][h][w][C]: conv2 and conv3 are
+// implicit-im2col GEMMs over them (3 x 3 taps, stride 2, padding 1) and the
+// output projection one over conv3's (all h3 rows x 1 column: the
+// reference's [chunk][w3][C h3] rows with K in (row, channel) order); GELU
+// picks each element's path by its index in the reference's [C][h][w] chunk
+// tensor.  Otherwise the reference's layouts through im2col.
 static int conv_stem(qasr_encoder *e, const float *mel, int64_t frames, int64_t f0, int n_chunks, int cw,
                      float *x, char *buf) {
     hipStream_t st = e->h->stream;
     const int C = e->c.conv_hidden, D = e->c.d_model;
     const int h1 = conv_len(128), w1 = conv_len(cw), h2 = conv_len(h1), w2 = conv_len(w1);
     const int h3 = conv_len(h2), w3 = conv_len(w2);
+    const bool direct1 = 130 * (cw + 2) <= 13312 && C >= 16;
+    if (e->stem_nhwc) {
+        float *a1 = reinterpret_cast<float *>(buf);
+        float *a2 = a1 + (int64_t)n_chunks * C * h1 * w1;
+        float *a3 = a2 + (int64_t)n_chunks * C * h2 * w2;
+        float *cols = a3 + (int64_t)n_chunks * C * h3 * w3;           // conv1's patches (no direct form)
+        if (direct1) {
+            LAUNCHCHK(launch_conv1_direct(a1, mel + f0, n_chunks, e->c.chunk_size, frames, 128, cw, e->conv1_w,
+                                          e->conv1_b, C, h1, w1, true, st),
+                      "conv1");
+        } else {
+            LAUNCHCHK(launch_im2col3x3s2(cols, mel + f0, n_chunks, 1, 128, cw, e->c.chunk_size, 0, frames, h1, w1,
+                                         st),
+                      "im2col1");
+            TRY(egemm(e, cols, 9, e->conv1_w, 9, a1, C, n_chunks * h1 * w1, C, 9, e->conv1_b, EPI_GELU | EPI_CHW,
+                      (int64_t)C * h1 * w1, h1 * w1));
+        }
+        TRY(econv(e, a1, n_chunks, h1, w1, C, h2, w2, 3, 3, 2, 2, 1, 1, e->conv2_w, C, e->conv2_b, a2, C,
+                  EPI_GELU | EPI_CHW));
+        TRY(econv(e, a2, n_chunks, h2, w2, C, h3, w3, 3, 3, 2, 2, 1, 1, e->conv3_w, C, e->conv3_b, a3, C,
+                  EPI_GELU | EPI_CHW));
+        TRY(econv(e, a3, n_chunks, h3, w3, C, 1, w3, h3, 1, 1, 1, 0, 0, e->conv_out_w, D, nullptr, x, D, EPI_NONE));
+        LAUNCHCHK(launch_add_periodic(x, e->pe, (int64_t)n_chunks * w3, D, w3, st), "pe add");
+        return QASR_OK;
+    }
     float *cols = reinterpret_cast<float *>(buf);
     float *a1 = cols + (int64_t)n_chunks * h2 * w2 * C * 9 + (int64_t)n_chunks * h1 * w1 * 9;
     float *a2 = a1 + (int64_t)n_chunks * C * h1 * w1;
@@ -270,9 +344,9 @@ static int conv_stem(qasr_encoder *e, const float *mel, int64_t frames, int64_t 
     float *rsh = a3 + (int64_t)n_chunks * C * h3 * w3;
     // conv1: input (chunk c, ic 0, ih, iw) = mel[ih * frames + f0 + c * chunk + iw]; computed
     // directly (9 taps) when the chunk's input plane fits the kernel's LDS, else as a GEMM
-    if (130 * (cw + 2) <= 13312 && C >= 16) {
+    if (direct1) {
         LAUNCHCHK(launch_conv1_direct(a1, mel + f0, n_chunks, e->c.chunk_size, frames, 128, cw, e->conv1_w,
-                                      e->conv1_b, C, h1, w1, st),
+                                      e->conv1_b, C, h1, w1, false, st),
                   "conv1");
     } else {
         LAUNCHCHK(launch_im2col3x3s2(cols, mel + f0, n_chunks, 1, 128, cw, e->c.chunk_size, 0, frames, h1, w1, st),
@@ -301,8 +375,10 @@ static size_t stem_bytes(const qasr_encoder *e, int n_chunks, int cw) {
     const int C = e->c.conv_hidden;
     const int h1 = conv_len(128), w1 = conv_len(cw), h2 = conv_len(h1), w2 = conv_len(w1);
     const int h3 = conv_len(h2), w3 = conv_len(w2);
-    const int64_t f = (int64_t)n_chunks * h2 * w2 * C * 9 + (int64_t)n_chunks * h1 * w1 * 9 +
-                      (int64_t)n_chunks * C * (h1 * w1 + h2 * w2 + h3 * w3) + (int64_t)n_chunks * w3 * C * h3;
+    const int64_t acts = (int64_t)n_chunks * C * (h1 * w1 + h2 * w2 + h3 * w3);
+    const int64_t f = e->stem_nhwc ? acts + (int64_t)n_chunks * h1 * w1 * 9
+                                   : (int64_t)n_chunks * h2 * w2 * C * 9 + (int64_t)n_chunks * h1 * w1 * 9 + acts +
+                                         (int64_t)n_chunks * w3 * C * h3;
     return sizeof(float) * f + 1024;
 }
 

@@ -12,6 +12,11 @@
 //   B bf16        the reference's weights (exact)
 //   B int8        per-row int8 weights, dequantised exactly to bf16 in LDS; the
 //                 per-row scale is applied in the epilogue
+//   A conv       (k_gemm_lds only) f32 channels-last activations read as the
+//                 im2col matrix of a strided convolution without forming it:
+//                 each K-step is one kernel tap's run of 32 channels, loaded
+//                 straight from the activation row (zero past the borders),
+//                 then split like A f32
 // k_gemm_f32: plain f32 FMA tiles for the small GEMMs whose operands are both
 // f32 tables (mel DFT and filterbank, audio.rs:339-351).
 #include <cstdlib>
@@ -170,12 +175,16 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs g) {
                 if (m >= M || n >= N) continue;
                 float v = acc[i][j][r];
                 // EPI_TRANS: rows are (chunk, spatial) of a batched conv and the
-                // output keeps the reference layout [chunk][channel][spatial]
+                // output keeps the reference layout [chunk][channel][spatial];
+                // EPI_CHW: the same GELU index, row-major (channels-last) output
                 int64_t off, gidx;
                 if (EPI & EPI_TRANS) {
                     const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
                     gidx = (int64_t)n * g.gelu_rows + sp;
                     off = (int64_t)c * g.gelu_n + gidx;
+                } else if (EPI & EPI_CHW) {
+                    gidx = (int64_t)n * g.gelu_rows + m % g.gelu_rows;
+                    off = (int64_t)m * g.ldc + n;
                 } else {
                     gidx = (int64_t)m * g.ldc + n;
                     off = gidx;
@@ -257,8 +266,8 @@ __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
 }
 
 // the GEMM epilogue of one output element (C row-major, or EPI_TRANS:
-// [M / gelu_rows][N][gelu_rows]): scale, then C = (C + bias) + v for
-// EPI_ACCUM or v + bias, then GELU
+// [M / gelu_rows][N][gelu_rows]; EPI_CHW: row-major with EPI_TRANS's GELU
+// index): scale, then C = (C + bias) + v for EPI_ACCUM or v + bias, then GELU
 template <int EPI>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, int m, int n, float v) {
     int64_t off, gidx;
@@ -266,6 +275,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, int m, int n, f
         const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
         gidx = (int64_t)n * g.gelu_rows + sp;
         off = (int64_t)c * g.gelu_n + gidx;
+    } else if (EPI & EPI_CHW) {
+        gidx = (int64_t)n * g.gelu_rows + m % g.gelu_rows;
+        off = (int64_t)m * g.ldc + n;
     } else {
         gidx = (int64_t)m * g.ldc + n;
         off = gidx;
@@ -285,7 +297,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs &g, int m, int n, f
 
 template <int ASRC, int BSRC, int EPI, int NS, int BM, int BN, int KS, int KP>
 __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
-    constexpr bool AF = ASRC == A_F32_SPLIT;
+    constexpr bool CONV = ASRC == A_CONV;
+    constexpr bool AF = ASRC == A_F32_SPLIT || CONV;
     constexpr int AE = AF ? 4 : 2, BE = BSRC == B_BF16 ? 2 : 1;     // element bytes
     constexpr int BK = AF ? 32 : 64;                                 // A rows are 128 B, B rows 64 B per stage
     constexpr int ASZ = BM * 128, BSZ = BN * 64, STG = ASZ + BSZ;
@@ -322,10 +335,20 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
     // covers tile rows 8 j .. 8 j + 7 (8 slots each), B load j rows 16 j .. 16 j + 15 (4 slots)
     const char *A = reinterpret_cast<const char *>(g.A), *B = reinterpret_cast<const char *>(g.B);
     const char *a_src[LA], *b_src[LB];
+    int a_iy[CONV ? LA : 1], a_ix[CONV ? LA : 1];   // A_CONV: the row's input origin (may be outside)
 #pragma unroll
     for (int u = 0; u < LA; u++) {
         const int r = 8 * (wid * LA + u) + (lane >> 3), p = (lane & 7) ^ a_swz<AF>(r);
-        a_src[u] = A + ((int64_t)min(m0 + r, M - 1) * g.lda) * AE + 16 * p;
+        const int m = min(m0 + r, M - 1);
+        if constexpr (CONV) {
+            const int plane = g.conv_hout * g.conv_wout, ch = m / plane, rem = m - ch * plane;
+            const int oy = rem / g.conv_wout, ox = rem - oy * g.conv_wout;
+            a_iy[u] = oy * g.conv_sy - g.conv_py;
+            a_ix[u] = ox * g.conv_sx - g.conv_px;
+            a_src[u] = A + (int64_t)ch * g.conv_hin * g.conv_win * g.conv_c * AE + 16 * p;
+        } else {
+            a_src[u] = A + ((int64_t)m * g.lda) * AE + 16 * p;
+        }
     }
 #pragma unroll
     for (int u = 0; u < LB; u++) {
@@ -338,8 +361,26 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
         const int kg = grp + KP * kt;       // the group's kt-th K-step
         const bool live = kt < nit && kg < nk;
         const int64_t ka = live ? (int64_t)(k0s + kg) * BK * AE : 0, kb = live ? (int64_t)(k0s + kg) * BK * BE : 0;
+        if constexpr (CONV) {
+            // K-step (ky, kx, c0 .. c0 + 31): one 128-byte run of channels per
+            // row.  The quotients by reciprocal: k0 is a multiple of 32 below
+            // conv_c kh kw, so (k0 + 16) / conv_c sits at least 16 / conv_c
+            // from an integer, far beyond the float error of the product
+            // (and likewise t + 0.5 over conv_kw)
+            const int k0 = live ? (k0s + kg) * BK : 0;
+            const int t = (int)(((float)k0 + 16.0f) * g.conv_rc), c0 = k0 - t * g.conv_c;
+            const int ky = (int)(((float)t + 0.5f) * g.conv_rkw), kx = t - ky * g.conv_kw;
 #pragma unroll
-        for (int u = 0; u < LA; u++) lds_dma16(live ? a_src[u] + ka : zero, st + 1024 * (wid * LA + u));
+            for (int u = 0; u < LA; u++) {
+                const int iy = a_iy[u] + ky, ix = a_ix[u] + kx;
+                const bool in = live && iy >= 0 && iy < g.conv_hin && ix >= 0 && ix < g.conv_win;
+                const int64_t off = ((int64_t)(in ? iy : 0) * g.conv_win + (in ? ix : 0)) * g.conv_c + c0;
+                lds_dma16(in ? a_src[u] + off * AE : zero, st + 1024 * (wid * LA + u));
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < LA; u++) lds_dma16(live ? a_src[u] + ka : zero, st + 1024 * (wid * LA + u));
+        }
 #pragma unroll
         for (int u = 0; u < LB; u++) lds_dma16(live ? b_src[u] + kb : zero, st + ASZ + 1024 * (wid * LB + u));
     };
@@ -494,7 +535,7 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                     const int n = n0 + nw + j * 16 + (lane & 15);
                     // gemm_epilogue's arithmetic on the preloaded operands
                     int64_t gidx;              // gelu()'s element index
-                    if (EPI & EPI_TRANS) gidx = (int64_t)n * g.gelu_rows + m % g.gelu_rows;
+                    if (EPI & (EPI_TRANS | EPI_CHW)) gidx = (int64_t)n * g.gelu_rows + m % g.gelu_rows;
                     else gidx = (int64_t)m * g.ldc + n;
                     float v = acc[i][j][r];
                     if (EPI & EPI_SCALE) v = __fmul_rn(v, pre_s[j]);
@@ -599,20 +640,33 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
     switch (epi) {
 #define QE(E) case E: hipLaunchKernelGGL((k_gemm_mfma<ASRC, BSRC, E>), grid, dim3(256), 0, st, g); break;
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+        QE(EPI_GELU | EPI_CHW)
 #undef QE
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
+// the epilogues each operand source is launched with (the implicit-im2col
+// conv source: its plain and GELU forms, channels-last output)
+constexpr bool epi_used(int asrc, int e) {
+    return asrc == A_CONV ? (e == EPI_NONE || e == (EPI_GELU | EPI_CHW)) : (e & EPI_CHW) == 0;
+}
+
 // the unsplit kernel with KP K groups per block
 template <int ASRC, int BSRC, int NS, int BM, int BN, int KP>
 static hipError_t go_gemm_lds_kp(const GemmArgs &g, int epi, dim3 grid, hipStream_t st) {
     switch (epi) {
-#define QE(E)                                                                                                 \
-    case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, KP>), grid, dim3(256 * KP), 0, st, g); \
-        break;
+#define QE(E)                                                                                                     \
+    case E:                                                                                                       \
+        if constexpr (epi_used(ASRC, E)) {                                                                        \
+            hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, KP>), grid, dim3(256 * KP), 0, st, g); \
+            break;                                                                                                \
+        } else {                                                                                                  \
+            return hipErrorInvalidValue;                                                                          \
+        }
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+        QE(EPI_GELU | EPI_CHW)
 #undef QE
         default: return hipErrorInvalidValue;
     }
@@ -633,7 +687,7 @@ template <int ASRC, int BSRC, int NS, int BM, int BN>
 static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     const int gx = (g.N + BN - 1) / BN, gy = (g.M + BM - 1) / BM;
     if constexpr (BM == 64 && BN == 64) {
-        const int kp = gemm_kp(g, ASRC == A_F32_SPLIT ? 32 : 64);
+        const int kp = gemm_kp(g, ASRC == A_BF16 ? 64 : 32);
         if (kp == 4) return go_gemm_lds_kp<ASRC, BSRC, 3, 64, 64, 4>(g, epi, dim3(gx, gy), st);
         if (kp == 2) return go_gemm_lds_kp<ASRC, BSRC, 4, 64, 64, 2>(g, epi, dim3(gx, gy), st);
     }
@@ -644,6 +698,7 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
     // passes; the bf16 path does not split: with its loads of the epilogue
     // operands ahead of the K loop, the unsplit kernel measured faster at
     // M = 375, K = 2048 (11.7 against 13.2 us) and equal at K = 3072)
+    if constexpr (ASRC == A_F32_SPLIT) {
     const int bk = 32, min_steps = 16;
     const bool epi_ok = epi == EPI_NONE || epi == EPI_ACCUM || epi == EPI_GELU || epi == EPI_SCALE;
     const bool ws_ok = g.ws && g.ws_bytes >= (int64_t)2 * g.M * g.N * (int64_t)sizeof(float);
@@ -670,14 +725,23 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
         }
         return hipGetLastError();
     }
+    }
     // (measured and rejected: each block walking every M tile of its column
     // strip, so that the strip's weights are read from HBM once: for the
     // config-1 LM head, 1187 strips at M = 375, 205 us against 160-184 with a
     // block per tile)
     const dim3 grid(gx, gy);
     switch (epi) {
-#define QE(E) case E: hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, 1>), grid, dim3(256), 0, st, g); break;
+#define QE(E)                                                                                           \
+    case E:                                                                                             \
+        if constexpr (epi_used(ASRC, E)) {                                                              \
+            hipLaunchKernelGGL((k_gemm_lds<ASRC, BSRC, E, NS, BM, BN, 1, 1>), grid, dim3(256), 0, st, g); \
+            break;                                                                                      \
+        } else {                                                                                        \
+            return hipErrorInvalidValue;                                                                \
+        }
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
+        QE(EPI_GELU | EPI_CHW)
 #undef QE
         default: return hipErrorInvalidValue;
     }
@@ -696,9 +760,12 @@ static hipError_t go_gemm_lds(const GemmArgs &g, int epi, hipStream_t st) {
     // of one column strip grouped on one XCD (162 us, against 155); and the
     // activations split into three int8 planes on the int8 MFMA (273-282 us:
     // three bytes per activation through the ring and the LDS reads).
+    // The implicit-im2col conv GEMM keeps 2 stages as well (the encoder's
+    // conv2, M = 24000, N = 480, K = 4320: encoder 2.62-2.64 -> 2.59 ms; its
+    // 64 x 64 and 128 x 64 tiles measured 2.79 and 2.77 ms).
     const int64_t small_blocks = (int64_t)((g.N + 63) / 64) * ((g.M + 63) / 64);
     const bool big = small_blocks >= 2048;
-    constexpr int big_ns = ASRC == A_BF16 ? 2 : 3;
+    constexpr int big_ns = ASRC == A_F32_SPLIT ? 3 : 2;
     return big ? go_gemm_lds_ns<ASRC, BSRC, big_ns, 128, 128>(g, epi, st)
                : go_gemm_lds_ns<ASRC, BSRC, 4, 64, 64>(g, epi, st);
 }
@@ -716,7 +783,18 @@ hipError_t launch_gemm(const GemmArgs &g0, int asrc, int bsrc, int epi, hipStrea
     if (g.M <= 0 || g.N <= 0 || g.K <= 0) return hipErrorInvalidValue;
     g.a_vec4 = (g.lda % 8 == 0) && ((uintptr_t)g.A % 16 == 0);
     g.b_vec = (g.ldb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
-    if ((epi & (EPI_GELU | EPI_TRANS)) && g.gelu_rows <= 0 && (epi & EPI_TRANS)) return hipErrorInvalidValue;
+    if ((epi & (EPI_TRANS | EPI_CHW)) && g.gelu_rows <= 0) return hipErrorInvalidValue;
+    if (asrc == A_CONV) {
+        // implicit im2col: whole 32-channel runs, every K-step inside one tap
+        const bool ok = bsrc == B_BF16 && g.conv_c > 0 && g.conv_c % 32 == 0 && g.conv_kh > 0 && g.conv_kw > 0 &&
+                        g.K == g.conv_c * g.conv_kh * g.conv_kw && g.conv_hout > 0 && g.conv_wout > 0 &&
+                        g.conv_hin > 0 && g.conv_win > 0 && g.M % (g.conv_hout * g.conv_wout) == 0 &&
+                        (g.ldb * 2) % 16 == 0 && (uintptr_t)g.A % 16 == 0 && (uintptr_t)g.B % 16 == 0;
+        if (!ok || g.K >= (1 << 22)) return hipErrorInvalidValue;
+        g.conv_rc = 1.0f / (float)g.conv_c;
+        g.conv_rkw = 1.0f / (float)g.conv_kw;
+        return go_gemm_lds<A_CONV, B_BF16>(g, epi, st);
+    }
     if (asrc == A_F32_SPLIT && bsrc == B_BF16)
         return gemm_lds_ok(g, asrc, bsrc) ? go_gemm_lds<A_F32_SPLIT, B_BF16>(g, epi, st)
                                           : go_gemm<A_F32_SPLIT, B_BF16>(g, epi, st);

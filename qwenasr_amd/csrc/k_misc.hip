@@ -283,7 +283,7 @@ constexpr int CONV1_OCB = 16, CONV1_LDS = 13312;
 __global__ __launch_bounds__(256) void k_conv1_direct(float *__restrict__ out, const float *__restrict__ in,
                                                       int64_t cs, int64_t rs, int H, int W,
                                                       const uint16_t *__restrict__ w, const float *__restrict__ bias,
-                                                      int C, int Ho, int Wo) {
+                                                      int C, int Ho, int Wo, int nhwc) {
     __shared__ float X[CONV1_LDS];
     const int c = blockIdx.x, XW = W + 2;
     const float *src = in + c * cs;
@@ -318,23 +318,58 @@ __global__ __launch_bounds__(256) void k_conv1_direct(float *__restrict__ out, c
         for (int ki = 0; ki < 3; ki++)
 #pragma unroll
             for (int kj = 0; kj < 3; kj++) xv[ki * 3 + kj] = xp[ki * XW + kj];
-        for (int o = 0; o < noc; o++) {
+        auto value = [&](int o) {
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < 9; k++) acc = fmaf(xv[k], wsh[o][k], acc);
-            const int64_t gi = (int64_t)(oc0 + o) * plane + sp;
+            const int64_t gi = (int64_t)(oc0 + o) * plane + sp;      // the reference's (channel-major) index
             const bool vec = gi < gsh[o][0] ? gi < gsh[o][1] : gi < gsh[o][2];
-            dst[gi] = gelu_at(__fadd_rn(acc, wsh[o][9]), vec);
+            return gelu_at(__fadd_rn(acc, wsh[o][9]), vec);
+        };
+        if (nhwc) {
+            // channels last: this position's channels oc0 .. oc0 + noc - 1 are
+            // one contiguous run (float4 stores; C and oc0 are multiples of 4)
+            float *row = dst + (int64_t)sp * C + oc0;
+            for (int o = 0; o < noc; o += 4)
+                *reinterpret_cast<float4 *>(row + o) = make_float4(value(o), value(o + 1), value(o + 2), value(o + 3));
+        } else {
+            for (int o = 0; o < noc; o++) dst[(int64_t)(oc0 + o) * plane + sp] = value(o);
         }
     }
 }
 
 hipError_t launch_conv1_direct(float *out, const float *in, int n_chunks, int64_t cs, int64_t rs, int H, int W,
-                               const uint16_t *w, const float *bias, int C, int Ho, int Wo, hipStream_t st) {
+                               const uint16_t *w, const float *bias, int C, int Ho, int Wo, bool nhwc,
+                               hipStream_t st) {
     if ((H + 2) * (W + 2) > CONV1_LDS || Ho != (H - 1) / 2 + 1 || Wo != (W - 1) / 2 + 1 || n_chunks <= 0 || C < 16)
         return hipErrorInvalidValue;
+    if (nhwc && (C % 4 != 0 || (uintptr_t)out % 16 != 0)) return hipErrorInvalidValue;
     const dim3 grid((unsigned)n_chunks, (unsigned)((C + CONV1_OCB - 1) / CONV1_OCB));
-    hipLaunchKernelGGL(k_conv1_direct, grid, dim3(256), 0, st, out, in, cs, rs, H, W, w, bias, C, Ho, Wo);
+    hipLaunchKernelGGL(k_conv1_direct, grid, dim3(256), 0, st, out, in, cs, rs, H, W, w, bias, C, Ho, Wo,
+                       nhwc ? 1 : 0);
+    return hipGetLastError();
+}
+
+// w[o][c][t] -> out[o][t][c] (bf16): a convolution's weights with the K index
+// (channel, tap) reordered to (tap, channel), the order of the channels-last
+// implicit-im2col GEMM
+__global__ __launch_bounds__(256) void k_taps_last(uint16_t *__restrict__ out, const uint16_t *__restrict__ in,
+                                                   int O, int Cin, int T) {
+    const int64_t total = (int64_t)O * Cin * T;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+        const int c = (int)(i % Cin);
+        const int64_t r = i / Cin;
+        const int t = (int)(r % T);
+        const int64_t o = r / T;
+        out[i] = in[(o * Cin + c) * T + t];
+    }
+}
+
+hipError_t launch_taps_last(uint16_t *out, const uint16_t *in, int O, int Cin, int T, hipStream_t st) {
+    if (O <= 0 || Cin <= 0 || T <= 0) return hipErrorInvalidValue;
+    const int64_t total = (int64_t)O * Cin * T;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 65536);
+    hipLaunchKernelGGL(k_taps_last, dim3(blocks), dim3(256), 0, st, out, in, O, Cin, T);
     return hipGetLastError();
 }
 

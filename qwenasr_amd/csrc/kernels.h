@@ -196,9 +196,9 @@ hipError_t launch_head_norm_rope(float *x, const float *w, const float *cos_t, c
 
 namespace qasr {
 // ---- GEMM ----------------------------------------------------------------
-enum { A_F32_SPLIT = 0, A_BF16 = 1 };
+enum { A_F32_SPLIT = 0, A_BF16 = 1, A_CONV = 2 };
 enum { B_BF16 = 0, B_I8 = 1 };
-enum { EPI_NONE = 0, EPI_ACCUM = 1, EPI_SCALE = 2, EPI_GELU = 4, EPI_TRANS = 8 };
+enum { EPI_NONE = 0, EPI_ACCUM = 1, EPI_SCALE = 2, EPI_GELU = 4, EPI_TRANS = 8, EPI_CHW = 16 };
 
 struct GemmArgs {
     int M, N, K;
@@ -219,6 +219,13 @@ struct GemmArgs {
     // whatever M, so that a row's result does not depend on how many rows
     // share the call; the launch fails if the workspace is too small
     int split_by_shape;
+    // A_CONV (f32-class, implicit im2col): A is a channels-last activation
+    // [chunks][conv_hin][conv_win][conv_c]; GEMM row m is output position
+    // (chunk, oy, ox) of a conv_hout x conv_wout grid and K index (ky, kx, c)
+    // of a conv_kh x conv_kw kernel: input (oy sy - py + ky, ox sx - px + kx),
+    // zero outside the input.  conv_c % 32 == 0.
+    int conv_hin, conv_win, conv_c, conv_hout, conv_wout, conv_kh, conv_kw, conv_sy, conv_sx, conv_py, conv_px;
+    float conv_rc, conv_rkw;  // 1 / conv_c, 1 / conv_kw (set by the launcher)
 };
 
 hipError_t launch_gemm(const GemmArgs &g, int asrc, int bsrc, int epi, hipStream_t st);
@@ -276,7 +283,9 @@ hipError_t launch_conv_reshape(float *out, const float *in, int n_chunks, int C,
 // stem conv1 + bias + GELU, direct (input element (c, ih, iw) at in + c * cs + ih * rs + iw;
 // (H + 2) * (W + 2) <= 13312, Ho / Wo the stride-2 output sizes, C >= 16)
 hipError_t launch_conv1_direct(float *out, const float *in, int n_chunks, int64_t cs, int64_t rs, int H, int W,
-                               const uint16_t *w, const float *bias, int C, int Ho, int Wo, hipStream_t st);
+                               const uint16_t *w, const float *bias, int C, int Ho, int Wo, bool nhwc,
+                               hipStream_t st);
+hipError_t launch_taps_last(uint16_t *out, const uint16_t *in, int O, int Cin, int T, hipStream_t st);
 // idle one wave for `us` microseconds (timing helper)
 hipError_t launch_delay(int us, hipStream_t st);
 // the prefill's q/k per-head norm + RoPE and K/V cache write (one launch)
