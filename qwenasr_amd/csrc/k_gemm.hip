@@ -547,6 +547,15 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                         if (g.bias) v = __fadd_rn(v, pre_b[j]);
                     }
                     if (EPI & EPI_GELU) v = gelu_ref(v, gidx, g.gelu_n);
+                    if constexpr ((EPI & EPI_SWIGLU) != 0) {
+                        // (gate, up) are columns (n, n + 1), held by lanes (l, l ^ 1)
+                        // with the same rows: the even lane forms output n / 2 with
+                        // the expression and AVX / tail choice of k_swiglu_rows
+                        const float up = __shfl_xor(v, 1, 64);
+                        const int jj = n >> 1, half = N >> 1, nv = half - half % 8;
+                        const float e = jj < nv ? fast_exp_ref(__fsub_rn(0.0f, v)) : expf(-v);
+                        v = __fmul_rn(__fdiv_rn(v, __fadd_rn(1.0f, e)), up);
+                    }
                     // materialised here: otherwise the compiler sinks the
                     // arithmetic into the store branches below
                     asm volatile("" : "+v"(v));
@@ -561,10 +570,13 @@ __global__ __launch_bounds__(256 * KP) void k_gemm_lds(GemmArgs g) {
                     const int m = m0 + mw + i * 16 + (lane >> 4) * 4 + r;
                     const int n = n0 + nw + j * 16 + (lane & 15);
                     if (m >= M || n >= N) continue;
+                    if ((EPI & EPI_SWIGLU) && (n & 1)) continue;
                     int64_t off;
                     if (EPI & EPI_TRANS) {
                         const int c = m / g.gelu_rows, sp = m % g.gelu_rows;
                         off = (int64_t)c * g.gelu_n + (int64_t)n * g.gelu_rows + sp;
+                    } else if (EPI & EPI_SWIGLU) {
+                        off = (int64_t)m * g.ldc + (n >> 1);
                     } else {
                         off = (int64_t)m * g.ldc + n;
                     }
@@ -650,7 +662,9 @@ static hipError_t go_gemm(const GemmArgs &g, int epi, hipStream_t st) {
 // the epilogues each operand source is launched with (the implicit-im2col
 // conv source: its plain and GELU forms, channels-last output)
 constexpr bool epi_used(int asrc, int e) {
-    return asrc == A_CONV ? (e == EPI_NONE || e == (EPI_GELU | EPI_CHW)) : (e & EPI_CHW) == 0;
+    if (asrc == A_CONV) return e == EPI_NONE || e == (EPI_GELU | EPI_CHW);
+    if (e == EPI_SWIGLU) return asrc == A_F32_SPLIT;
+    return (e & (EPI_CHW | EPI_SWIGLU)) == 0;
 }
 
 // the unsplit kernel with KP K groups per block
@@ -666,7 +680,7 @@ static hipError_t go_gemm_lds_kp(const GemmArgs &g, int epi, dim3 grid, hipStrea
             return hipErrorInvalidValue;                                                                          \
         }
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
-        QE(EPI_GELU | EPI_CHW)
+        QE(EPI_GELU | EPI_CHW) QE(EPI_SWIGLU)
 #undef QE
         default: return hipErrorInvalidValue;
     }
@@ -741,7 +755,7 @@ static hipError_t go_gemm_lds_ns(const GemmArgs &g, int epi, hipStream_t st) {
             return hipErrorInvalidValue;                                                                \
         }
         QE(EPI_NONE) QE(EPI_ACCUM) QE(EPI_SCALE) QE(EPI_GELU) QE(EPI_TRANS) QE(EPI_TRANS | EPI_GELU)
-        QE(EPI_GELU | EPI_CHW)
+        QE(EPI_GELU | EPI_CHW) QE(EPI_SWIGLU)
 #undef QE
         default: return hipErrorInvalidValue;
     }
@@ -784,6 +798,7 @@ hipError_t launch_gemm(const GemmArgs &g0, int asrc, int bsrc, int epi, hipStrea
     g.a_vec4 = (g.lda % 8 == 0) && ((uintptr_t)g.A % 16 == 0);
     g.b_vec = (g.ldb % 8 == 0) && ((uintptr_t)g.B % 16 == 0);
     if ((epi & (EPI_TRANS | EPI_CHW)) && g.gelu_rows <= 0) return hipErrorInvalidValue;
+    if ((epi & EPI_SWIGLU) && (g.N % 2 != 0 || !gemm_lds_ok(g, asrc, bsrc))) return hipErrorInvalidValue;
     if (asrc == A_CONV) {
         // implicit im2col: whole 32-channel runs, every K-step inside one tap
         const bool ok = bsrc == B_BF16 && g.conv_c > 0 && g.conv_c % 32 == 0 && g.conv_kh > 0 && g.conv_kw > 0 &&

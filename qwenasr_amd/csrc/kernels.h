@@ -198,7 +198,9 @@ namespace qasr {
 // ---- GEMM ----------------------------------------------------------------
 enum { A_F32_SPLIT = 0, A_BF16 = 1, A_CONV = 2 };
 enum { B_BF16 = 0, B_I8 = 1 };
-enum { EPI_NONE = 0, EPI_ACCUM = 1, EPI_SCALE = 2, EPI_GELU = 4, EPI_TRANS = 8, EPI_CHW = 16 };
+// EPI_SWIGLU: B rows interleave (gate, up); C[m][n / 2] = silu(gate) up (ldc
+// in outputs, N / 2 of them), the decoder's SwiGLU with its AVX / tail paths
+enum { EPI_NONE = 0, EPI_ACCUM = 1, EPI_SCALE = 2, EPI_GELU = 4, EPI_TRANS = 8, EPI_CHW = 16, EPI_SWIGLU = 32 };
 
 struct GemmArgs {
     int M, N, K;

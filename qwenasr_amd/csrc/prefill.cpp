@@ -169,8 +169,8 @@ int decoder_prefill_segments(qasr_decoder *d, const PrefillSeg *segs, int n_seg)
         }
         TRY(gemm(d, p.att, qd, L.bo, qd, p.x, H, M, H, qd, EPI_ACCUM));
         LAUNCHCHK(launch_rms_norm_rows(p.xn, p.x, L.post_norm, S, H, c.eps, st), "prefill rms_norm");
-        TRY(gemm(d, p.xn, H, L.bgu, H, p.gu, 2 * I, M, 2 * I, H, EPI_NONE));
-        LAUNCHCHK(launch_swiglu_rows(p.g, p.gu, S, I, st), "prefill swiglu");
+        // gate_up with the SwiGLU in its epilogue (interleaved gate / up rows)
+        TRY(gemm(d, p.xn, H, L.bgu, H, p.g, I, M, 2 * I, H, EPI_SWIGLU));
         TRY(gemm(d, p.g, I, L.bdown, I, p.x, H, M, H, I, EPI_ACCUM));
     }
     return QASR_OK;
