@@ -609,14 +609,19 @@ __global__ __launch_bounds__(256) void k_gemm_splitk_reduce(GemmArgs g, int ks) 
 // ---------------------------------------------------------------------------
 // f32 SIMT GEMM (NT), 64x64 tile, 4x4 outputs per thread, K-step 16
 // ---------------------------------------------------------------------------
+// T x T output tile per block of 16 x 16 threads, (T / 16)^2 outputs per
+// thread; each output's sum runs over k in order in one thread (fmaf), so the
+// tile size does not change a bit
+template <int T>
 __global__ __launch_bounds__(256) void k_gemm_f32(GemmArgs g) {
-    __shared__ float As[16][65], Bs[16][65];
+    constexpr int R = T / 16;
+    __shared__ float As[16][T + 1], Bs[16][T + 1];
     const int t = threadIdx.x, tx = t & 15, ty = t >> 4;
-    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const int m0 = blockIdx.y * T, n0 = blockIdx.x * T;
     const float *A = reinterpret_cast<const float *>(g.A), *B = reinterpret_cast<const float *>(g.B);
-    float acc[4][4] = {};
+    float acc[R][R] = {};
     for (int k0 = 0; k0 < g.K; k0 += 16) {
-        for (int i = t; i < 64 * 16; i += 256) {
+        for (int i = t; i < T * 16; i += 256) {
             const int r = i >> 4, k = i & 15;
             const int m = m0 + r, n = n0 + r, kk = k0 + k;
             const float av = A[(int64_t)min(m, g.M - 1) * g.lda + min(kk, g.K - 1)];
@@ -627,21 +632,21 @@ __global__ __launch_bounds__(256) void k_gemm_f32(GemmArgs g) {
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            float a[4], b[4];
+            float a[R], b[R];
 #pragma unroll
-            for (int i = 0; i < 4; i++) { a[i] = As[k][ty * 4 + i]; b[i] = Bs[k][tx * 4 + i]; }
+            for (int i = 0; i < R; i++) { a[i] = As[k][ty * R + i]; b[i] = Bs[k][tx * R + i]; }
 #pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int i = 0; i < R; i++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+                for (int j = 0; j < R; j++) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
         }
         __syncthreads();
     }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < R; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+        for (int j = 0; j < R; j++) {
+            const int m = m0 + ty * R + i, n = n0 + tx * R + j;
             if (m < g.M && n < g.N) g.C[(int64_t)m * g.ldc + n] = acc[i][j];
         }
 }
@@ -821,8 +826,14 @@ hipError_t launch_gemm(const GemmArgs &g0, int asrc, int bsrc, int epi, hipStrea
 
 hipError_t launch_gemm_f32(const GemmArgs &g, hipStream_t st) {
     if (g.M <= 0 || g.N <= 0 || g.K <= 0) return hipErrorInvalidValue;
-    const dim3 grid((g.N + 63) / 64, (g.M + 63) / 64);
-    hipLaunchKernelGGL(k_gemm_f32, grid, dim3(256), 0, st, g);
+    // 32 x 32 tiles while 64 x 64 ones would leave CUs idle (the mel DFT and
+    // filterbank: 94-188 blocks of 64 x 64)
+    const int64_t tiles64 = (int64_t)((g.N + 63) / 64) * ((g.M + 63) / 64);
+    if (tiles64 < 512) {
+        hipLaunchKernelGGL(k_gemm_f32<32>, dim3((g.N + 31) / 32, (g.M + 31) / 32), dim3(256), 0, st, g);
+    } else {
+        hipLaunchKernelGGL(k_gemm_f32<64>, dim3((g.N + 63) / 64, (g.M + 63) / 64), dim3(256), 0, st, g);
+    }
     return hipGetLastError();
 }
 
