@@ -351,16 +351,21 @@ class OracleDecoder:
     def kv_len(self, n):
         lib().or_decoder_set_len(self.d, int(n))
 
-    def packed(self, layer, which):
+    def packed(self, layer, which, rows=None):
+        """(int8 rows, row scales) of a packed matrix (layer -1: the LM head);
+        rows (a list of row indices) copies only those."""
         c = self.cfg
         H, hd, I = c["hidden"], c["head_dim"], c["intermediate"]
         qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
         shape = (c["vocab"], H) if layer == -1 else [(qd, H), (kvd, H), (kvd, H), (H, qd), (2 * I, H), (H, I)][which]
         sp = P()
         qp = lib().or_decoder_packed(self.d, layer, which, C.byref(sp))
-        q = np.ctypeslib.as_array(C.cast(qp, C.POINTER(C.c_int8)), shape=shape).copy()
-        s = np.ctypeslib.as_array(C.cast(sp, C.POINTER(C.c_float)), shape=(shape[0],)).copy()
-        return q, s
+        q = np.ctypeslib.as_array(C.cast(qp, C.POINTER(C.c_int8)), shape=shape)
+        s = np.ctypeslib.as_array(C.cast(sp, C.POINTER(C.c_float)), shape=(shape[0],))
+        if rows is not None:
+            idx = np.asarray(rows, np.int64)
+            return q[idx].copy(), s[idx].copy()
+        return q.copy(), s.copy()
 
     def embed(self, token):
         out = np.empty(self.cfg["hidden"], np.float32)
@@ -391,10 +396,14 @@ class OracleDecoder:
         lib().or_decoder_prefill_logits(self.d, _p(e), e.shape[0], None if lm is None else _p(lm), out_dim, _p(out))
         return out
 
-    def forward_logits(self, embed):
-        """(token, best logit, second-best logit)."""
+    def forward_logits(self, embed, return_hidden=False):
+        """(token, best logit, second-best logit), and with return_hidden the
+        final normed hidden state the LM-head argmax scored."""
         bv, sv = C.c_float(), C.c_float()
-        t = lib().or_decoder_forward(self.d, _p(f32(embed)), C.byref(bv), C.byref(sv), None)
+        hid = np.empty(self.cfg["hidden"], np.float32) if return_hidden else None
+        t = lib().or_decoder_forward(self.d, _p(f32(embed)), C.byref(bv), C.byref(sv), _p(hid))
+        if return_hidden:
+            return int(t), bv.value, sv.value, hid
         return int(t), bv.value, sv.value
 
     def forward(self, embed, return_hidden=False):

@@ -45,6 +45,26 @@ def bf16f(a):
     return (np.asarray(a, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+def oracle_head_values(orc, hid, q_rows, s_rows):
+    """The oracle LM head's values of the given packed rows for the final
+    normed hidden state `hid`, as or_argmax_int8 forms them (oracle.c, after
+    mod.rs:1832-1893): one activation quantization, the exact int32 dot, then
+    (float)acc * xs * ws[row] in float32, left to right, no contraction."""
+    xq, xs = orc.quantize_act(hid)
+    acc = np.asarray(q_rows, np.int64).reshape(-1, xq.shape[0]) @ xq.astype(np.int64)
+    return (acc.astype(np.float32) * np.float32(xs)).astype(np.float32) * np.asarray(s_rows, np.float32)
+
+
+def gpu_token_gap(orc, od, hid, best, token):
+    """Relative distance (best - v) / |best| of the GPU's token from the
+    oracle's best logit at one step, v being the oracle's own value of that
+    token's head row on the oracle's state (0 exactly when the token is the
+    oracle's argmax)."""
+    q, s = od.packed(-1, 0, rows=[int(token)])
+    v = float(oracle_head_values(orc, hid, q, s)[0])
+    return (best - v) / max(abs(best), 1e-30)
+
+
 ASR_TEXT = 151704
 # a 2-layer decoder small enough for the oracle (the GPU kernels' head_dim
 # 128, the full vocabulary) and a 2-layer encoder of the 0.6B width

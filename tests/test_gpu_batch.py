@@ -10,7 +10,7 @@ partition of its own context bucket, so the comparison is bit-exact.
 import numpy as np
 import pytest
 
-from conftest import rng
+from conftest import gpu_token_gap, rng
 
 pytestmark = pytest.mark.gpu
 
@@ -145,17 +145,19 @@ def test_batch_matches_solo_long_contexts(dev):
 
 def oracle_forced(orc, w, prefix, first, forced, max_seq):
     """decoder_prefill, then decoder_forward steps on the oracle fed the given
-    tokens (first, then forced[:-1]): the oracle's argmax and relative top-2
-    margin at every step."""
+    tokens (first, then forced[:-1]): the oracle's argmax, relative top-2
+    margin and the relative distance of forced[s] (the GPU's token of step s)
+    from the oracle's best logit at every step."""
     od = orc.OracleDecoder(w, max_seq=max_seq)
     try:
         od.prefill(prefix)
-        toks, margins = [], []
-        for tok in [int(first)] + [int(t) for t in forced[:-1]]:
-            t, best, second = od.forward_logits(od.embed(tok))
+        toks, margins, gaps = [], [], []
+        for s, tok in enumerate([int(first)] + [int(t) for t in forced[:-1]]):
+            t, best, second, hid = od.forward_logits(od.embed(tok), return_hidden=True)
             toks.append(t)
             margins.append((best - second) / max(abs(best), 1e-30))
-        return toks, margins
+            gaps.append(gpu_token_gap(orc, od, hid, best, forced[s]))
+        return toks, margins, gaps
     finally:
         od.close()
 
@@ -174,7 +176,8 @@ def test_batch_matches_oracle(small_decoder, orc):
     show in the batch-vs-solo tests.  The oracle prefills the same rows and is
     then fed the GPU's own tokens (teacher forcing), so one near-tie does not
     end the comparison; every step whose oracle top-2 gap exceeds MARGIN_BOUND
-    must pick the GPU's token."""
+    must pick the GPU's token, and at every other step the GPU's token must
+    be one the oracle scores within MARGIN_BOUND of its best."""
     from qwenasr_amd.model import Batch
     w, dec = small_decoder
     print("batch vs oracle, 32 streams", flush=True)
@@ -192,13 +195,18 @@ def test_batch_matches_oracle(small_decoder, orc):
         b.close()
     compared = 0
     for i in (0, 9, 17, 31):
-        want, margins = oracle_forced(orc, w, prefixes[i], first[i], got[i], 2048)
+        want, margins, gaps = oracle_forced(orc, w, prefixes[i], first[i], got[i], 2048)
         print(f"stream {i} (L {lens[i]}): gpu {got[i].tolist()} oracle {want} margins "
-              f"{np.round(margins, 4).tolist()}", flush=True)
+              f"{np.round(margins, 4).tolist()} GPU token gaps {np.round(gaps, 5).tolist()}", flush=True)
         for s in range(n_steps):
             if margins[s] > MARGIN_BOUND:
                 assert int(got[i][s]) == want[s], (i, s, got[i].tolist(), want, margins[s])
                 compared += 1
+            # every step, near ties included: the GPU's token scores within the
+            # bound of the oracle's best on the oracle's state (exactly where equal)
+            assert 0.0 <= gaps[s] <= MARGIN_BOUND, (i, s, int(got[i][s]), want[s], gaps[s], margins[s])
+            if int(got[i][s]) == want[s]:
+                assert gaps[s] == 0.0, (i, s, gaps[s])
     assert compared >= 36, compared
 
 

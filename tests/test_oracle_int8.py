@@ -195,3 +195,24 @@ def test_argmax_bruteforce_and_ties(orc):
     assert (vn < 0).all()
     i3, bv3, _ = orc.argmax_int8(x, wn, ws)
     assert i3 == int(np.argmax(vn)) and bv3 == vn.max()
+
+
+def test_head_values_match_the_argmax(orc):
+    """conftest.oracle_head_values, which the GPU decode tests use for the
+    oracle's value of the GPU's chosen token, equals or_argmax_int8's best and
+    second-best values bit for bit, one row or all at once; associating the
+    two scales the other way gives different bits."""
+    from conftest import oracle_head_values
+    r = rng(71)
+    n, k = 5000, 1024
+    w = r.integers(-127, 128, (n, k), dtype=np.int8)
+    ws = r.uniform(1e-4, 2e-3, n).astype(np.float32)
+    x = r.normal(0, 1, k).astype(np.float32)
+    i, bv, sv = orc.argmax_int8(x, w, ws)
+    v = oracle_head_values(orc, x, w, ws)
+    assert v.shape == (n,) and v[i] == bv and v.max() == bv and np.sort(v)[-2] == sv
+    assert oracle_head_values(orc, x, w[i:i + 1], ws[i:i + 1])[0] == bv
+    xq, xs = orc.quantize_act(x)
+    acc = w.astype(np.int64) @ xq.astype(np.int64)
+    other = acc.astype(np.float32) * (np.float32(xs) * ws).astype(np.float32)
+    assert (other != v).any()
