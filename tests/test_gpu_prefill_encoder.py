@@ -145,6 +145,36 @@ def test_decoder_prefill_then_decode(dev, orc):
     cpu.close()
 
 
+def test_decoder_prefill_k_groups(dev, orc):
+    """A narrow decoder (hidden 512, intermediate 1024) whose prefill GEMMs
+    take the K-group form (64 x 64 tiles, 4 groups of waves splitting K: at
+    most 32 column tiles and 16+ K-steps), the gate_up GEMM with the SwiGLU in
+    its epilogue included: the prefill rows of both layers against the oracle
+    (layer 1's rows see layer 0's SwiGLU output)."""
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    cfg = dict(TINY_DEC, hidden=512, intermediate=1024)
+    w = SynthDecoder(cfg, seed=1012)
+    gpu = Decoder(dev, w, max_seq=256)
+    cpu = orc.OracleDecoder(w, max_seq=256)
+    try:
+        S = 150
+        emb = rng(41).normal(0, 0.02, (S, cfg["hidden"])).astype(np.float32)
+        print("narrow decoder prefill, K groups", flush=True)
+        gpu.prefill(emb)
+        cpu.prefill(emb)
+        kg, vg = gpu.kv_download()
+        kc, vc = cpu.kv()
+        for l in range(cfg["n_layers"]):
+            ek = nrel(kg[l, :, :S], kc[l, :, :S])
+            ev = nrel(vg[l, :, :S], vc[l, :, :S])
+            print(f"layer {l}: K {ek:.3g} V {ev:.3g}", flush=True)
+            assert ek < 1e-5 and ev < 1e-5, (l, ek, ev)
+    finally:
+        gpu.close()
+        cpu.close()
+
+
 def test_decoder_prefill_logits(dev, orc):
     """decoder_prefill_logits (decoder.rs:649-681), the forced aligner's path:
     every row's logits through the tied embedding and through a separate
