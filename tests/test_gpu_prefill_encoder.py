@@ -289,23 +289,27 @@ def test_encoder(dev, orc):
     ore.close()
 
 
-@pytest.mark.parametrize("conv_hidden", [32, 48, 96])
-def test_encoder_conv_stem_widths(dev, orc, conv_hidden):
+@pytest.mark.parametrize("conv_hidden,chunk", [(32, 100), (48, 100), (96, 100), (32, 128)])
+def test_encoder_conv_stem_widths(dev, orc, conv_hidden, chunk):
     """The conv stem at widths that are a multiple of 32 (channels-last,
     implicit-im2col GEMMs: 32, 96) and one that is not (48: the im2col form,
     whose conv2 / conv3 K of 432 also takes the fallback GEMM), each against
-    the oracle's reference-layout stem (encoder.rs:226-287)."""
+    the oracle's reference-layout stem (encoder.rs:226-287).  With 128-frame
+    chunks the full chunks' input planes exceed the direct first
+    convolution's LDS, so the channels-last stem forms conv1 as im2col and a
+    K = 9 GEMM with the channels-last GELU epilogue (the 56-frame tail chunk
+    stays direct)."""
     from qwenasr_amd.model import Encoder
     from qwenasr_amd.synth import SynthEncoder, audio
-    cfg = dict(d_model=64, n_layers=1, n_heads=1, head_dim=64, ffn_dim=128, output_dim=128, chunk_size=100,
-               n_window_infer=800, conv_hidden=conv_hidden)
+    cfg = dict(d_model=64, n_layers=1, n_heads=1, head_dim=64, ffn_dim=128, output_dim=128, chunk_size=chunk,
+               n_window_infer=8 * chunk, conv_hidden=conv_hidden)
     w = SynthEncoder(cfg, seed=60 + conv_hidden)
     enc = Encoder(dev, w)
     ore = orc.OracleEncoder(w)
     try:
-        mel = orc.mel(audio(50000, 61))             # 312 frames: 3 full chunks and a tail
+        mel = orc.mel(audio(50000, 61))             # 312 frames: full chunks and a tail
         out_g, out_c = enc.forward(mel), ore.forward(mel)
-        print(f"conv_hidden {conv_hidden}: rel {nrel(out_g, out_c):.2e}", flush=True)
+        print(f"conv_hidden {conv_hidden}, chunk {chunk}: rel {nrel(out_g, out_c):.2e}", flush=True)
         assert out_g.shape == out_c.shape and nrel(out_g, out_c) < 2e-4
     finally:
         enc.close()
