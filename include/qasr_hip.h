@@ -233,7 +233,10 @@ typedef struct qasr_decoder qasr_decoder;
  * max_seq is the initial capacity: a prefill, forward, generate or
  * transcription that needs more positions doubles the cache first
  * (KvCache::grow, decoder.rs:199-231; at least to what the call needs, in
- * whole 256-position buckets, at most 2^20 positions), keeping every row. */
+ * whole 256-position buckets, at most 2^20 positions), keeping every row.
+ * The attention shape must be that of both Qwen3-ASR decoders: 16 query
+ * heads and 8 KV heads of head_dim 128 (QASR_ERR_INVALID otherwise); hidden
+ * and intermediate multiples of 64, hidden <= 4096, intermediate <= 6144. */
 int qasr_hip_decoder_load(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_weights *w,
                           int round_mode, int64_t max_seq, int kv_bf16, qasr_decoder **out);
 /* Decoder::load (decoder.rs:70-167) from a checkpoint: the reference's tensor

@@ -146,12 +146,15 @@ int decoder_load_impl(qasr_hip *h, const qasr_dec_config *cfg, const qasr_dec_we
         return qasr_fail(QASR_ERR_INVALID, "decoder_load: null argument");
     *out = nullptr;
     const qasr_dec_config c = *cfg;
-    if (c.n_layers <= 0 || c.head_dim != 128 || c.n_kv_heads <= 0 || c.n_heads != 2 * c.n_kv_heads ||
-        c.hidden <= 0 || c.hidden % 64 != 0 || c.hidden > 4096 || c.intermediate <= 0 ||
-        (c.intermediate % 64) != 0 || c.intermediate > 6144 || c.vocab <= 0 ||
-        (int64_t)c.n_heads * c.head_dim > 6144 || max_seq <= 0 || max_seq > (1 << 20))
+    // The decode step's split merges (k_oproj_merge, k_attn_merge_rows / _seq /
+    // _heads) are laid out for the attention shape of both Qwen3-ASR decoders
+    // (config.rs: 16 query heads, 8 KV heads of 128): other head counts are
+    // refused here, before any of their partials could be merged as 16 heads.
+    if (c.n_layers <= 0 || c.head_dim != 128 || c.n_kv_heads != 8 || c.n_heads != 16 || c.hidden <= 0 ||
+        c.hidden % 64 != 0 || c.hidden > 4096 || c.intermediate <= 0 || (c.intermediate % 64) != 0 ||
+        c.intermediate > 6144 || c.vocab <= 0 || max_seq <= 0 || max_seq > (1 << 20))
         return qasr_fail(QASR_ERR_INVALID,
-                         "decoder_load: unsupported config (head_dim 128, n_heads == 2 * n_kv_heads, "
+                         "decoder_load: unsupported config (16 query heads and 8 KV heads of head_dim 128, "
                          "hidden/intermediate multiples of 64)");
     if (round_mode != QASR_ROUND_HALF_AWAY && round_mode != QASR_TRUNC)
         return qasr_fail(QASR_ERR_INVALID, "decoder_load: unknown round_mode");

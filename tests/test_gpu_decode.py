@@ -205,3 +205,18 @@ def test_fused_qkv_attention_bit_identical(dev, hidden, kv_bf16):
         assert (t == runs[0][0]).all()
         assert np.array_equal(bits(k), bits(runs[0][1]))
         assert np.array_equal(bits(v), bits(runs[0][2]))
+
+
+@pytest.mark.parametrize("n_heads,n_kv_heads", [(2, 1), (32, 16), (16, 4)])
+def test_decoder_load_rejects_other_attention_shapes(dev, n_heads, n_kv_heads):
+    """Only the attention shape of both Qwen3-ASR decoders (16 query heads, 8
+    KV heads of 128) loads: the decode step's split merges are laid out for
+    it, so another shape is refused with QASR_ERR_INVALID before anything is
+    allocated."""
+    from qwenasr_amd import QasrError
+    from qwenasr_amd.model import Decoder
+    from qwenasr_amd.synth import SynthDecoder
+    w = SynthDecoder(dict(n_layers=1, hidden=128, n_heads=n_heads, n_kv_heads=n_kv_heads, head_dim=128,
+                          intermediate=128, vocab=64, eps=1e-6, theta=1e6), seed=5)
+    with pytest.raises(QasrError, match="16 query heads"):
+        Decoder(dev, w, max_seq=64)

@@ -371,7 +371,7 @@ def test_prompt_ids_beyond_vocab_rejected(dev, vocab):
     from qwenasr_amd import QasrError
     from qwenasr_amd.model import Decoder, Encoder, Stream, transcribe_forced
     from qwenasr_amd.synth import SynthDecoder, SynthEncoder, audio
-    wd = SynthDecoder(dict(n_layers=1, hidden=128, n_heads=2, n_kv_heads=1, head_dim=128, intermediate=128,
+    wd = SynthDecoder(dict(n_layers=1, hidden=128, n_heads=16, n_kv_heads=8, head_dim=128, intermediate=128,
                            vocab=vocab, eps=1e-6, theta=1e6), seed=31)
     we = SynthEncoder(dict(d_model=64, n_layers=1, n_heads=1, head_dim=64, ffn_dim=128, output_dim=128,
                            chunk_size=100, n_window_infer=800, conv_hidden=32), seed=32)
